@@ -1,0 +1,57 @@
+"""The oracle's FP8 rule against the reference's known answers (tests/test_cache_fp8.py:47-58, 150-158) and an
+independent brute-force nearest-value search over the e4m3 codes."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8
+
+
+def test_fp32_midpoints_known_answers():
+    # reference tests/test_cache_fp8.py:150-158: 84.021 -> 88 directly (80 through an fp16 step)
+    k = torch.tensor([448., 84.021, -84.021, 1.06251, -1.06251, 1.06249, -1.06249, 0.]).reshape(1, 1, 1, 8)
+    q, scale = fp8.quantize_rows(k)
+    assert float(scale) == 1.0
+    assert q.float().flatten().tolist() == [448., 88., -88., 1.125, -1.125, 1.0, -1.0, 0.]
+    assert float(torch.tensor(84.021).half().float().to(fp8.FP8).float()) == 80.0  # the fp16 path it avoids
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_boundary_row_known_answers(dtype):
+    # reference tests/test_cache_fp8.py:47-57
+    values = torch.tensor([0., -0., 1e-15, -1e-15, .5, -.5, 1., -1., 3., -3., 448., -448.]).to(dtype)
+    q, scale = fp8.quantize_rows(values.repeat(8).reshape(1, 1, 1, 96))
+    assert float(scale) == 1.0
+    bits = q.view(torch.uint8).flatten()[:12].tolist()
+    # +0, -0, tiny -> signed zero, then exact values
+    assert bits[:4] == [0x00, 0x80, 0x00, 0x80]
+    assert q.float().flatten()[4:12].tolist() == [.5, -.5, 1., -1., 3., -3., 448., -448.]
+
+
+def test_torch_conversion_equals_brute_force_nearest():
+    vals = fp8.e4m3_values()
+    finite = np.sort(vals[np.isfinite(vals) & (vals >= 0)])
+    mids = (finite[1:] + finite[:-1]) / 2  # every tie point: must go to the even code
+    rng = np.random.default_rng(0)
+    samples = np.concatenate([
+        mids, -mids, finite, -finite,
+        rng.standard_normal(4000) * 50, rng.uniform(-470, 470, 2000), rng.uniform(-0.02, 0.02, 2000),
+        np.array([449., 463.9, 464., 464.1, 479.9, 480., 1000., -464.1]),
+    ]).astype(np.float32)
+    torch_bits = fp8.e4m3_bits(torch.from_numpy(samples)).numpy()
+    brute = fp8.e4m3_nearest(samples)
+    nan_t = np.isnan(fp8.e4m3_values()[torch_bits])
+    nan_b = np.isnan(fp8.e4m3_values()[brute])
+    assert np.array_equal(nan_t, nan_b)
+    assert np.array_equal(torch_bits[~nan_t], brute[~nan_b])
+
+
+def test_rows_scale_is_amax_over_448_and_values_reconstruct():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(5, 7, 3, 128, generator=g).to(torch.bfloat16)
+    q, s = fp8.quantize_rows(x)
+    assert torch.equal(s, (x.abs().amax(-1, keepdim=True).float() / 448))
+    assert torch.equal(q.float().abs().amax(-1), torch.full((5, 7, 3), 448.))  # the row max lands on 448
+    rel = ((q.float() * s) - x.float()).abs() / x.float().abs().clamp(min=1e-3)
+    assert float(rel[x.float().abs() > s * 2 ** -6 * 448].max()) <= 2 ** -4  # e4m3: 3 mantissa bits, half-ulp

@@ -1,0 +1,108 @@
+// Shared device helpers and the error channel of the wdl C ABI (gfx950 only).
+//
+// Every launcher in this library is `extern "C" int wdl_*(...)`: it validates its arguments on the host, launches
+// on the caller's stream, never allocates and never synchronises, and returns WDL_OK or an error code with a
+// message kept per host thread (wdl_last_error). Floating-point contraction is off for the whole library
+// (-ffp-contract=off): every fused multiply-add is written as fmaf, so the rounding of each kernel is the one its
+// source shows.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define WDL_OK 0
+#define WDL_EINVAL 1
+#define WDL_EHIP 2
+
+// element types of strided inputs
+#define WDL_F32 0
+#define WDL_F16 1
+#define WDL_BF16 2
+#define WDL_F64 3
+
+namespace wdl {
+
+int fail(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+// ---------------------------------------------------------------- bf16 / fp16 / fp8 conversions (exact, RNE)
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
+
+// round to nearest even; NaN stays a quiet NaN
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return uint16_t(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+__device__ __forceinline__ uint16_t f32_to_f16(float f) { return __half_as_ushort(__float2half_rn(f)); }
+
+// FP8 E4M3FN (OCP): bias 7, no infinities, 0x7f/0xff NaN, largest finite 448, subnormals down to 2^-9.
+// Encoding of an fp32 value, rounded to nearest even; magnitudes that round past 448 become NaN (the conversion
+// rule of torch.Tensor.to(torch.float8_e4m3fn)).
+__device__ __forceinline__ uint8_t f32_to_e4m3(float f) {
+    uint32_t u = __float_as_uint(f);
+    uint8_t sign = uint8_t((u >> 24) & 0x80u);
+    u &= 0x7fffffffu;
+    if (u >= 0x43f00000u) return uint8_t(sign | 0x7fu);  // >= 480 or NaN/inf
+    if (u < 0x3c800000u) {  // below 2^-6: subnormal, quantum 2^-9
+        // a * 512 is exact (a power-of-two scaling of a value far from overflow); rint rounds half to even; a
+        // result of 8 is the smallest normal 2^-6, whose encoding is 0x08
+        float r = __builtin_rintf(__uint_as_float(u) * 512.0f);
+        return uint8_t(sign | uint8_t(r));
+    }
+    // normal: keep 3 mantissa bits, RNE on the 20 dropped ones
+    uint32_t mant_odd = (u >> 20) & 1u;
+    u += ((uint32_t)(7 - 127) << 23) + 0x7ffffu + mant_odd;
+    return uint8_t(sign | uint8_t(u >> 20));
+}
+
+__device__ __forceinline__ float e4m3_to_f32(uint8_t b) {
+    uint32_t sign = uint32_t(b & 0x80u) << 24;
+    uint32_t e = (b >> 3) & 0xfu, m = b & 7u;
+    if (e == 0xf && m == 7) return __uint_as_float(sign | 0x7fc00000u);
+    if (e == 0) {
+        float v = float(m) * (1.0f / 512.0f);
+        return sign ? -v : v;
+    }
+    return __uint_as_float(sign | ((e + 120u) << 23) | (m << 20));
+}
+
+template <typename T>
+__device__ __forceinline__ float load_as_f32(const void* p, int64_t i);
+
+template <>
+__device__ __forceinline__ float load_as_f32<float>(const void* p, int64_t i) {
+    return static_cast<const float*>(p)[i];
+}
+template <>
+__device__ __forceinline__ float load_as_f32<uint16_t>(const void* p, int64_t i) {  // bf16
+    return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+struct half_tag {};
+template <>
+__device__ __forceinline__ float load_as_f32<half_tag>(const void* p, int64_t i) {
+    return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+// ---------------------------------------------------------------- wavefront reductions (64 lanes)
+
+template <int WIDTH>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+    for (int o = WIDTH / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WIDTH));
+    return v;
+}
+
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = WIDTH / 2; o > 0; o >>= 1) v = v + __shfl_xor(v, o, WIDTH);
+    return v;
+}
+
+}  // namespace wdl

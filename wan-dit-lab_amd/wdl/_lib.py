@@ -1,0 +1,59 @@
+"""Loads lib/libwdl.so (the C ABI of include/wdl.h) once through ctypes and raises on any non-zero status.
+
+The library is the only compute path: there is no fallback. A missing library raises FileNotFoundError naming the
+build command, as operators.library does for the reference's DLLs (src/wan_dit_lab/kernels/operators.py:12-16).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parents[1] / "lib" / "libwdl.so"
+
+c_i64 = ctypes.c_int64
+c_int = ctypes.c_int
+c_ptr = ctypes.c_void_p
+c_f32 = ctypes.c_float
+c_i64p = ctypes.POINTER(ctypes.c_int64)
+
+# name -> argtypes, in the order of include/wdl.h
+SIGNATURES: dict[str, list] = {
+    "wdl_last_error": [],
+    "wdl_abi_version": [],
+    "wdl_kv_append_fp8": [c_ptr, c_int, c_i64p, c_ptr, c_int, c_i64p, c_i64, c_i64, c_i64, c_i64,
+                          c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_ptr],
+}
+
+_LIB = None
+
+
+def library() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise FileNotFoundError(f"{LIB_PATH} is not built: python -m wdl.build (or __graft_entry__.build())")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, args in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_char_p if name == "wdl_last_error" else c_int
+        _LIB = lib
+    return _LIB
+
+
+def exported_symbols() -> list[str]:
+    return list(SIGNATURES)
+
+
+def call(name: str, *args) -> None:
+    """Calls wdl_<name>; a non-zero status raises RuntimeError with the library's message."""
+    lib = library()
+    status = getattr(lib, name)(*args)
+    if status != 0:
+        message = lib.wdl_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed ({status}): {message}")
+
+
+def i64s(values) -> ctypes.Array:
+    return (ctypes.c_int64 * len(values))(*[int(v) for v in values])
