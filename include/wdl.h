@@ -40,6 +40,32 @@ int wdl_kv_append_fp8(const void* k, int k_dtype, const int64_t* k_strides, cons
                       float* cache_ks, void* cache_v, float* cache_vs, int64_t capacity, int64_t at,
                       wdl_stream_t stream);
 
+/* W4A4 activation quantizer (+ low-rank down projection, + optional fused LayerNorm and adaLN modulation).
+ * Replaces Nunchaku's quantize_w4a4_act_fuse_lora behind live::w4a4_linear (native/ops/w4a4_ops.cpp:17-29; the
+ * quantizer itself is absent from the reference tree) and the norm/modulation of WanBlock.forward
+ * (src/wan_dit_lab/models/block.py:25,28; models/layer_norm.py:4-7).
+ * x: bf16 [M, K], row stride ldx (16-byte aligned rows); smooth: bf16 [K]; proj_down_t: bf16 [32, K] or NULL.
+ * v = x, or with ln != 0: v = bf16(LN(x)[*ln_w + ln_b] * (1 + mod_scale) + mod_shift) (fp32 vectors, NULL = absent).
+ * u = (v + qshift) / smooth; per row and 64-group: scale = bf16(max|u| / qmax) (qmax 7, or 15 if unsigned_q),
+ * q = clamp(rint(u / scale)). Outputs: q as e4m3 codes of the integers [Mp, K]; ascales bf16 [K/64, Mp];
+ * lora fp32 [Mp, 32] = v . proj_down; rows M..Mp-1 zero. Mp % 32 == 0. v_out (bf16 [M, K]) optional copy of v. */
+int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K, const void* smooth, float qshift,
+                     int unsigned_q, const void* proj_down_t, int64_t rank, void* q, void* ascales, float* lora,
+                     int64_t Mp, const float* mod_shift, const float* mod_scale, const float* ln_w,
+                     const float* ln_b, int ln, float eps, void* v_out, wdl_stream_t stream);
+
+/* W4A4 GEMM with fused dequantization, low-rank up projection and bias. Replaces Nunchaku's gemm_w4a4 behind
+ * live::w4a4_linear and live::w4a4_gelu_mlp (native/ops/w4a4_ops.cpp:36-38, 55-61).
+ * y[m][n] = sum_g ascales[g][m] wscales[g][n] I_g[m][n] + bf16(lora[m]) . proj_up[n] + bias[n], I_g the exact
+ * integer sum over the 64-group g. qa: [Mp, K] e4m3 codes (wdl_act_quant_w4); qweight: uint8 [N, K/2] (per group,
+ * byte j = k j low nibble, k j+32 high nibble); wscales bf16 [K/64, N]; lora fp32 [Mp, 32] or NULL; proj_up bf16
+ * [N, 32]; bias bf16 [N] or NULL. epilogue: 0 out bf16 [M, ldo] = y; 1 out fp32 = y; 2 out bf16 =
+ * bf16(out + bf16(y) * gate[n]) in place (gated residual; gate fp32 [N]); 3 out bf16 = GELU_tanh(y).
+ * Mp % 128 == 0, N % 128 == 0, K % 64 == 0. */
+int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* qweight, const void* wscales, const float* lora,
+                  const void* proj_up, const void* bias, int64_t M, int64_t Mp, int64_t N, int64_t K, int64_t rank,
+                  void* out, int64_t ldo, int epilogue, const float* gate, wdl_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

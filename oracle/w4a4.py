@@ -1,0 +1,168 @@
+"""SVDQuant W4A4 linear, CPU restatement of src/wan_dit_lab/quantization/w4a4.py and native/ops/w4a4_ops.cpp.
+
+y = x W^T + b computed as  y = Q(x / s) Q(R)^T  +  (x proj_down) proj_up^T  +  b      (w4a4.py:4-10)
+with W diag(s) = up down + R (rank r by SVD), R in symmetric INT4 groups of 64 input channels.
+
+Functions and what pins them:
+- int4_groups (w4a4.py:80-100): "max" rule. Pinned by the reference's own closed form
+  (tests/test_w4a4.py:175-176, round/clamp) and by brute force (the nearest grid point of every value).
+- smoothing (w4a4.py:183-186), quantize_weight (w4a4.py:140-180 without the Nunchaku packer; the shift-corrected
+  bias of 168-170). Pinned by the reference's tolerance contracts (tests/test_w4a4.py:7-59): a rank-32 weight is
+  carried by the 16-bit branch to < 1 %, smoothing beats none, the shift correction halves the GELU offset.
+- act_quant: the activation quantizer. Its reference is Nunchaku's quantize_w4a4_act_fuse_lora
+  (w4a4_ops.cpp:22-29), which is absent from the reference tree: its exact rounding is parity unpinned against
+  the reference. This oracle defines it (per token, per group of 64 of (x + shift) / smooth, IEEE fp32:
+  scale = bf16(max|v| / 7) signed or bf16(max|v| / 15) unsigned, q = round_half_even(v / scale) clamped) and the
+  HIP quantizer is pinned bit-exactly to this definition; the definition itself is checked against brute force
+  (each q is the grid point nearest to v / scale).
+- linear / gelu_mlp: exact integer group sums (float64 matmul of small integers), float64 epilogue. The integer
+  accumulators are exact by construction (integers far below 2^53); the float epilogue is a tolerance bar.
+"""
+
+from __future__ import annotations
+
+import torch
+
+GROUP = 64  # input channels per INT4 scale (w4a4.py:29)
+GELU_SHIFT = 0.171875  # w4a4.py:195
+PAD = 256  # activation rows padded to a multiple (w4a4_ops.cpp:11)
+MSE_STEPS = torch.linspace(0.5, 1.0, 26).tolist()  # w4a4.py:77
+
+
+def padded(m: int) -> int:
+    return (m + PAD - 1) // PAD * PAD
+
+
+@torch.no_grad()
+def int4_groups(R: torch.Tensor, rule: str = "max"):
+    """w4a4.py:80-100 — R [N, K] -> (q int32 [N, K] in [-8, 7], scale fp32 [N, K/64])."""
+    N, K = R.shape
+    groups = R.float().view(N, K // GROUP, GROUP)
+    top = groups.abs().amax(dim=-1).clamp(min=1e-8) / 7
+    scale = top
+    if rule == "mse":
+        best = torch.full_like(top, float("inf"))
+        for c in MSE_STEPS:
+            s = top * c
+            err = ((groups - torch.round(groups / s[..., None]).clamp(-8, 7) * s[..., None]) ** 2).sum(-1)
+            better = err < best
+            best, scale = torch.where(better, err, best), torch.where(better, s, scale)
+    elif rule != "max":
+        raise ValueError(rule)
+    q = torch.round(groups / scale[..., None]).clamp(-8, 7).to(torch.int32).view(N, K)
+    return q, scale
+
+
+def smoothing(act_amax: torch.Tensor, weight: torch.Tensor, alpha: float = 0.5) -> torch.Tensor:
+    """w4a4.py:183-186 — SmoothQuant s_j = max|x_j|^alpha / max|W_:j|^(1-alpha), clamped to [1e-2, 1e2]."""
+    w = weight.float().abs().amax(dim=0).clamp(min=1e-5)
+    return (act_amax.float().clamp(min=1e-5) ** alpha / w ** (1 - alpha)).clamp(min=1e-2, max=1e2)
+
+
+@torch.no_grad()
+def quantize_weight(weight: torch.Tensor, bias=None, smooth=None, rank: int = 32, shift: float = 0.0,
+                    rule: str = "max", R: torch.Tensor | None = None):
+    """w4a4.py:140-180 in logical (unpacked) form: dict(q int32 [N, K], wscales bf16 [N, K/64],
+    proj_down bf16 [K, r], proj_up bf16 [N, r], smooth bf16 [K], bias bf16 [N], R fp32 [N, K]).
+    R may be given (the quantizer input on which int4 parity is defined)."""
+    W = weight.float()
+    N, K = W.shape
+    s = torch.ones(K) if smooth is None else smooth.float()
+    Ws = W * s[None, :]
+    U, S, Vh = torch.linalg.svd(Ws, full_matrices=False)
+    up = U[:, :rank] * S[:rank]
+    down = Vh[:rank]
+    if R is None:
+        R = Ws - up @ down
+    q, scale = int4_groups(R, rule)
+    b = torch.zeros(N) if bias is None else bias.float()
+    if shift:
+        Rq = (q.view(N, K // GROUP, GROUP).float() * scale[..., None]).view(N, K)
+        b = b - shift * (Rq / s[None, :]).sum(dim=1)
+    return dict(q=q, wscales=scale.to(torch.bfloat16), proj_down=(down / s[None, :]).t().contiguous().to(torch.bfloat16),
+                proj_up=up.to(torch.bfloat16), smooth=s.to(torch.bfloat16), bias=b.to(torch.bfloat16), R=R)
+
+
+def act_quant(x: torch.Tensor, smooth: torch.Tensor, shift: float = 0.0, unsigned: bool = False):
+    """The activation quantizer (definition of this build; see the module docstring).
+    x [M, K] (bf16 or fp32) -> q int32 [M, K] ([-8, 7] signed / [0, 15] unsigned), scales bf16 [M, K/64]."""
+    M, K = x.shape
+    v = x.float()
+    if shift:
+        v = v + torch.tensor(shift, dtype=torch.float32)
+    v = v / smooth.float()[None, :]
+    g = v.view(M, K // GROUP, GROUP)
+    amax = g.abs().amax(-1)
+    qmax = 15.0 if unsigned else 7.0
+    scale = (amax / torch.tensor(qmax, dtype=torch.float32)).to(torch.bfloat16)
+    s = scale.float()[..., None]
+    q = torch.where(s > 0, torch.round(g / torch.where(s > 0, s, torch.ones_like(s))), torch.zeros_like(g))
+    q = q.clamp(0 if unsigned else -8, 15 if unsigned else 7).to(torch.int32).view(M, K)
+    return q, scale
+
+
+def lora_down(x: torch.Tensor, proj_down: torch.Tensor) -> torch.Tensor:
+    """lora_act = x proj_down, fp32 result of the exact (float64) sum (w4a4_ops.cpp:26-27)."""
+    return (x.double() @ proj_down.double()).float()
+
+
+def group_gemm(qa: torch.Tensor, ascales: torch.Tensor, qw: torch.Tensor, wscales: torch.Tensor) -> torch.Tensor:
+    """sum_g ascale[m,g] wscale[n,g] I_g[m,n], I_g = exact integer group sums (float64 of small integers).
+    qa [M, K], ascales [M, G], qw [N, K], wscales [N, G] -> float64 [M, N]."""
+    M, K = qa.shape
+    N = qw.shape[0]
+    G = K // GROUP
+    y = torch.zeros(M, N, dtype=torch.float64)
+    a = qa.double().view(M, G, GROUP)
+    w = qw.double().view(N, G, GROUP)
+    for g in range(G):
+        I = a[:, g] @ w[:, g].t()  # exact: |I| <= 64 * 8 * 15
+        y += I * (ascales[:, g].double()[:, None] * wscales[:, g].double()[None, :])
+    return y
+
+
+def int_gemm(qa: torch.Tensor, qw: torch.Tensor) -> torch.Tensor:
+    """Exact integer product sum_k qa[m,k] qw[n,k] (int64)."""
+    return qa.long() @ qw.long().t()
+
+
+def linear_parts(x: torch.Tensor, t: dict, shift: float = 0.0, unsigned: bool = False, lora: torch.Tensor | None = None):
+    """The pieces of w4a4_linear (w4a4_ops.cpp:31-40) for x [M, K]: act quant, lora_act, y (float64)."""
+    qa, asc = act_quant(x, t["smooth"], shift, unsigned)
+    la = lora_down(x, t["proj_down"]) if lora is None else lora
+    y = group_gemm(qa, asc.float(), t["q"], t["wscales"].float())
+    y += la.to(torch.bfloat16).double() @ t["proj_up"].double().t()
+    y += t["bias"].double()[None, :]
+    return y, qa, asc, la
+
+
+def linear(x: torch.Tensor, t: dict) -> torch.Tensor:
+    """w4a4.linear (w4a4.py:189-192) -> bf16 [M, N]."""
+    return linear_parts(x, t)[0].to(torch.bfloat16)
+
+
+def gelu_tanh(h: torch.Tensor) -> torch.Tensor:
+    return torch.nn.functional.gelu(h, approximate="tanh")
+
+
+def gelu_mlp(x: torch.Tensor, t1: dict, t2: dict) -> torch.Tensor:
+    """w4a4.gelu_mlp (w4a4.py:198-204; w4a4_ops.cpp:44-63): h = GELU(x W1^T + b1) in fp32; the second layer's INT4
+    branch quantizes (h + GELU_SHIFT) / s2 unsigned, its low-rank branch reads h; y bf16 [M, N]."""
+    h = linear_parts(x, t1)[0].float()
+    h = gelu_tanh(h)
+    y, *_ = linear_parts(h, t2, shift=GELU_SHIFT, unsigned=True)
+    return y.to(torch.bfloat16)
+
+
+def pack_nibbles(q: torch.Tensor) -> torch.Tensor:
+    """int4 values [N, K] -> uint8 [N, K/2]: byte j holds k = 2j (low nibble) and 2j+1 (high), two's complement."""
+    u = (q.to(torch.int32) & 0xF).to(torch.uint8)
+    return (u[:, 0::2] | (u[:, 1::2] << 4)).contiguous()
+
+
+def unpack_nibbles(p: torch.Tensor) -> torch.Tensor:
+    lo = (p & 0xF).to(torch.int32)
+    hi = (p >> 4).to(torch.int32)
+    lo = torch.where(lo >= 8, lo - 16, lo)
+    hi = torch.where(hi >= 8, hi - 16, hi)
+    return torch.stack([lo, hi], dim=-1).reshape(p.shape[0], -1)

@@ -1,0 +1,221 @@
+"""W4A4 on the HIP path against the oracle.
+
+Bars (written in each test): activation quantizer — bit-exact int4 values and bf16 scales (the fused LayerNorm +
+modulation variant too, with its bf16 input bit-exact to the oracle's ordered-reduction LayerNorm); GEMM integer
+accumulators — bit-exact (unit scales, fp32 output equals the exact integer product); full GEMM — within 2^-20
+relative of the float64 oracle in fp32, one bf16 rounding step in bf16; module-level — the reference's own tolerance
+contracts (tests/test_w4a4.py:7-59)."""
+
+import pytest
+import torch
+
+from oracle import norms as onorms
+from oracle import w4a4 as ow
+
+pytestmark = pytest.mark.gpu
+
+
+def codes_to_int(q):
+    return q.cpu().view(torch.float8_e4m3fn).float().to(torch.int32)
+
+
+def data(M, K, seed=0, outliers=True):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g)
+    if outliers:
+        idx = torch.randperm(K, generator=g)[: max(1, K // 100)]
+        x[:, idx] *= 20
+    return x.to(torch.bfloat16), g
+
+
+@pytest.mark.parametrize("M,K", [(7, 128), (300, 256), (464, 3072), (130, 14336)])
+@pytest.mark.parametrize("unsigned", [False, True])
+def test_act_quant_bit_exact(gpu, M, K, unsigned):
+    from wdl import ops
+
+    x, g = data(M, K, seed=M + K)
+    if unsigned:
+        x = torch.nn.functional.gelu(x.float(), approximate="tanh").to(torch.bfloat16)
+    smooth = (torch.rand(K, generator=g) + 0.5).to(torch.bfloat16)
+    pdt = (torch.randn(32, K, generator=g) / K ** 0.5).to(torch.bfloat16)
+    shift = ow.GELU_SHIFT if unsigned else 0.0
+    q, asc, lora = ops.act_quant_launch(x.cuda(), smooth.cuda(), pdt.cuda(), shift, unsigned)
+    torch.cuda.synchronize()
+    rq, rs = ow.act_quant(x, smooth, shift, unsigned)
+    Mp = q.shape[0]
+    assert Mp % 128 == 0 and Mp >= M
+    assert torch.equal(codes_to_int(q)[:M], rq)  # bar: bit-exact int4 values
+    assert torch.equal(codes_to_int(q)[M:], torch.zeros(Mp - M, K, dtype=torch.int32))
+    assert torch.equal(asc.cpu()[:, :M].t(), rs)  # bar: bit-exact bf16 scales
+    ref_lora = ow.lora_down(x, pdt.t())
+    err = (lora.cpu()[:M] - ref_lora).abs().max()
+    assert float(err) <= 1e-5 * float(ref_lora.abs().max()) + 1e-6  # fp32 sums of exact bf16 products
+    assert torch.all(lora.cpu()[M:] == 0)
+
+
+@pytest.mark.parametrize("affine", [False, True])
+def test_fused_layernorm_modulation_quant_bit_exact(gpu, affine):
+    from wdl import ops
+
+    M, K = 200, 3072
+    x, g = data(M, K, seed=11)
+    shift = torch.randn(K, generator=g) * 0.1
+    scale = torch.randn(K, generator=g) * 0.1
+    w = (torch.rand(K, generator=g) + 0.5) if affine else None
+    b = (torch.randn(K, generator=g) * 0.1) if affine else None
+    smooth = torch.ones(K, dtype=torch.bfloat16)
+    pdt = (torch.randn(32, K, generator=g) / K ** 0.5).to(torch.bfloat16)
+    v_out = torch.empty(M, K, dtype=torch.bfloat16, device="cuda")
+    ln = dict(shift=shift.cuda(), scale=scale.cuda(), weight=None if w is None else w.cuda(),
+              bias=None if b is None else b.cuda(), eps=1e-6)
+    q, asc, lora = ops.act_quant_launch(x.cuda(), smooth.cuda(), pdt.cuda(), ln=ln, v_out=v_out)
+    torch.cuda.synchronize()
+    v = onorms.ln_mod(x, shift, scale, w, b, eps=1e-6)
+    assert torch.equal(v_out.cpu(), v)  # bar: bit-exact bf16 normalized, modulated input
+    rq, rs = ow.act_quant(v, smooth)
+    assert torch.equal(codes_to_int(q)[:M], rq)
+    assert torch.equal(asc.cpu()[:, :M].t(), rs)
+
+
+def launch_gemm(qa_int, asc, qweight, wsc, lora=None, pu=None, bias=None, M=None, epi=1, out=None, gate=None):
+    from wdl import ops
+
+    Mp, K = qa_int.shape
+    codes = qa_int.float().to(torch.float8_e4m3fn).view(torch.uint8).cuda()
+    N = qweight.shape[0]
+    M = Mp if M is None else M
+    if out is None:
+        out = torch.empty(M, N, device="cuda", dtype=torch.float32 if epi == 1 else torch.bfloat16)
+    c = lambda t: None if t is None else t.cuda()
+    return ops.gemm_launch(codes, c(asc), c(lora), qweight.cuda(), c(wsc), c(pu), c(bias), M, out, epi, c(gate))
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 128, 64), (256, 384, 512), (128, 256, 3072), (128, 128, 14336),
+                                   (1408, 3072, 3072)])
+def test_gemm_integer_accumulation_is_exact(gpu, M, N, K):
+    """Unit scales, no low-rank, fp32 out: y must equal the exact integer product (bar: bit-exact)."""
+    from wdl import w4a4
+
+    g = torch.Generator().manual_seed(M + N + K)
+    qa = torch.randint(-8, 8, (M, K), generator=g, dtype=torch.int32)
+    qa[: M // 2, : K // 2] = torch.randint(0, 16, (M // 2, K // 2), generator=g)  # unsigned codes 8..15 too
+    qw = torch.randint(-8, 8, (N, K), generator=g, dtype=torch.int32)
+    ones_a = torch.ones(K // 64, M, dtype=torch.bfloat16)
+    ones_w = torch.ones(K // 64, N, dtype=torch.bfloat16)
+    y = launch_gemm(qa, ones_a, w4a4.pack_weight(qw), ones_w)
+    torch.cuda.synchronize()
+    exact = ow.int_gemm(qa, qw)
+    assert torch.equal(y.cpu().double(), exact.double())
+
+
+@pytest.mark.parametrize("M,N,K,valid", [(128, 256, 512, 100), (256, 128, 3072, 256), (1408, 384, 3072, 1392)])
+def test_gemm_scaled_lowrank_bias_matches_oracle(gpu, M, N, K, valid):
+    from wdl import w4a4
+
+    g = torch.Generator().manual_seed(7 + M)
+    qa = torch.randint(-7, 8, (M, K), generator=g, dtype=torch.int32)
+    qw = torch.randint(-8, 8, (N, K), generator=g, dtype=torch.int32)
+    asc = (torch.rand(K // 64, M, generator=g) * 0.3 + 0.01).to(torch.bfloat16)
+    wsc = (torch.rand(K // 64, N, generator=g) * 0.01 + 1e-4).to(torch.bfloat16)
+    lora = torch.randn(M, 32, generator=g)
+    pu = (torch.randn(N, 32, generator=g) * 0.05).to(torch.bfloat16)
+    bias = (torch.randn(N, generator=g) * 0.1).to(torch.bfloat16)
+    y = launch_gemm(qa, asc, w4a4.pack_weight(qw), wsc, lora, pu, bias, M=valid, epi=1)
+    yb = launch_gemm(qa, asc, w4a4.pack_weight(qw), wsc, lora, pu, bias, M=valid, epi=0)
+    torch.cuda.synchronize()
+    ref = ow.group_gemm(qa[:valid], asc.t()[:valid].float(), qw, wsc.t().float())
+    ref += lora[:valid].to(torch.bfloat16).double() @ pu.double().t() + bias.double()
+    scale = float(ref.abs().max())
+    # fp32 result: fp32 rounding of ~K/64 fused steps (bar: 2^-20 of the output scale)
+    assert float((y.cpu().double() - ref).abs().max()) <= 2 ** -20 * scale * (K // 64)
+    # bf16 result: one bf16 rounding of that
+    diff = (yb.cpu().double() - ref).abs()
+    assert torch.all(diff <= ref.abs() * 2 ** -8 + 2 ** -20 * scale * (K // 64))
+
+
+def test_gemm_residual_and_gelu_epilogues(gpu):
+    from wdl import w4a4
+
+    M, N, K = 256, 256, 512
+    g = torch.Generator().manual_seed(9)
+    qa = torch.randint(-7, 8, (M, K), generator=g, dtype=torch.int32)
+    qw = torch.randint(-8, 8, (N, K), generator=g, dtype=torch.int32)
+    asc = (torch.rand(K // 64, M, generator=g) * 0.1).to(torch.bfloat16)
+    wsc = (torch.rand(K // 64, N, generator=g) * 0.01).to(torch.bfloat16)
+    bias = (torch.randn(N, generator=g) * 0.1).to(torch.bfloat16)
+    ref = ow.group_gemm(qa, asc.t().float(), qw, wsc.t().float()) + bias.double()
+    X = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    gate = torch.randn(N, generator=g)
+    out = X.cuda().clone()
+    launch_gemm(qa, asc, w4a4.pack_weight(qw), wsc, bias=bias, epi=2, out=out, gate=gate)
+    h = launch_gemm(qa, asc, w4a4.pack_weight(qw), wsc, bias=bias, epi=3)
+    torch.cuda.synchronize()
+    expect = (X.float() + ref.float().to(torch.bfloat16).float() * gate).to(torch.bfloat16)
+    assert float((out.cpu().float() - expect.float()).abs().max()) <= 2 ** -7 * float(expect.float().abs().max())
+    hg = torch.nn.functional.gelu(ref, approximate="tanh")
+    assert float((h.cpu().double() - hg).abs().max()) <= 2 ** -7 * float(hg.abs().max()) + 1e-6
+
+
+def test_low_rank_weight_is_exact_and_smoothing_helps(gpu):
+    # reference tests/test_w4a4.py:7-29
+    from wdl import w4a4
+
+    torch.manual_seed(0)
+    M, K, N = 512, 1024, 768
+    x = torch.randn(M, K, device="cuda", dtype=torch.bfloat16)
+    x[:, :8] *= 20
+    b = torch.randn(N, device="cuda") * 0.1
+
+    def err(W, t):
+        ref = x.float() @ W.t() + b
+        return float((w4a4.linear(x, t).float() - ref).norm() / ref.norm())
+
+    low = (torch.randn(N, 32, device="cuda") @ torch.randn(32, K, device="cuda")) * 0.01
+    s = torch.rand(K, device="cuda") + 0.5
+    assert err(low, w4a4.quantize(low, b, smooth=s)) < 0.01
+    W = torch.randn(N, K, device="cuda") * 0.02
+    plain = err(W, w4a4.quantize(W, b))
+    smooth = err(W, w4a4.quantize(W, b, smooth=w4a4.smoothing(x.abs().amax(dim=0), W)))
+    assert smooth < plain < 0.25
+
+
+def test_gelu_mlp_is_the_feed_forward_and_needs_the_shift(gpu):
+    # reference tests/test_w4a4.py:32-59
+    from wdl import w4a4
+
+    torch.manual_seed(0)
+    M, K, H, N = 300, 256, 1024, 256
+    x = torch.randn(M, K, device="cuda", dtype=torch.bfloat16)
+    x[:, :4] *= 10
+    W1, b1 = torch.randn(H, K, device="cuda") * 0.08, torch.randn(H, device="cuda") * 0.1
+    W2, b2 = torch.randn(N, H, device="cuda") * 0.05, torch.randn(N, device="cuda") * 0.1
+    gelu = torch.nn.GELU(approximate="tanh")
+    h = gelu(x.float() @ W1.t() + b1)
+    ref = h @ W2.t() + b2
+    err = lambda y: float((y.float() - ref).norm() / ref.norm())
+    offset = lambda y: float((y.float() - ref).mean(dim=0).norm() / ref.mean(dim=0).norm())
+    s1 = w4a4.smoothing(x.abs().amax(dim=0), W1)
+    t1 = w4a4.quantize(W1, b1, smooth=s1)
+    s2 = w4a4.smoothing(h.abs().amax(dim=0) + w4a4.GELU_SHIFT, W2)
+    unfused = w4a4.linear(gelu(w4a4.linear(x, t1).float()).to(torch.bfloat16), w4a4.quantize(W2, b2, smooth=s2))
+    fused = w4a4.gelu_mlp(x, t1, w4a4.quantize(W2, b2, smooth=s2, shift=w4a4.GELU_SHIFT))
+    uncorrected = w4a4.gelu_mlp(x, t1, w4a4.quantize(W2, b2, smooth=s2))
+    assert err(fused) < 0.2 and err(fused) < err(unfused)
+    assert offset(fused) < 1.1 * offset(unfused) and offset(uncorrected) > 1.5 * offset(fused)
+
+
+def test_linear_end_to_end_matches_oracle(gpu):
+    from wdl import w4a4
+
+    M, K, N = 300, 512, 384
+    x, g = data(M, K, seed=21)
+    W = torch.randn(N, K, generator=g) * 0.02
+    b = torch.randn(N, generator=g) * 0.02
+    s = w4a4.smoothing(x.float().abs().amax(0), W)
+    host = w4a4.quantize(W, b, smooth=s)
+    ref_t = ow.quantize_weight(W, b, smooth=s)
+    y = w4a4.linear(x.cuda(), {k: v.cuda() for k, v in host.items()})
+    torch.cuda.synchronize()
+    ref = ow.linear_parts(x, ref_t)[0]
+    diff = (y.cpu().double() - ref).abs()
+    assert torch.all(diff <= ref.abs() * 2 ** -8 + 1e-4 * float(ref.abs().max()))

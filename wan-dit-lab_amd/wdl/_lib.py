@@ -23,6 +23,10 @@ SIGNATURES: dict[str, list] = {
     "wdl_abi_version": [],
     "wdl_kv_append_fp8": [c_ptr, c_int, c_i64p, c_ptr, c_int, c_i64p, c_i64, c_i64, c_i64, c_i64,
                           c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_ptr],
+    "wdl_act_quant_w4": [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_f32, c_int, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_i64,
+                         c_ptr, c_ptr, c_ptr, c_ptr, c_int, c_f32, c_ptr, c_ptr],
+    "wdl_w4a4_gemm": [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_ptr,
+                      c_i64, c_int, c_ptr, c_ptr],
 }
 
 _LIB = None

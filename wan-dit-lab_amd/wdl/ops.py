@@ -40,3 +40,107 @@ def store_kv_fp8_op(k: torch.Tensor, v: torch.Tensor, cache_k: torch.Tensor, cac
 @store_kv_fp8_op.register_fake
 def _(k, v, cache_k, cache_ks, cache_v, cache_vs, at):
     return None
+
+
+# ------------------------------------------------------------------------------------------------ W4A4
+
+ROWS_PAD = 128  # activation rows padded to a multiple (GEMM token tile)
+RANK = 32
+
+
+def padded_rows(m: int) -> int:
+    return (m + ROWS_PAD - 1) // ROWS_PAD * ROWS_PAD
+
+
+EPI_BF16, EPI_F32, EPI_RESIDUAL, EPI_GELU = 0, 1, 2, 3
+
+
+def act_quant_launch(x, smooth, proj_down_t, qshift=0.0, unsigned=False, *, ln=None, v_out=None):
+    """x bf16 [M, K] (rows 16-byte aligned) -> (q e4m3 codes uint8 [Mp, K], ascales bf16 [K/64, Mp],
+    lora fp32 [Mp, 32] or None). ln: dict(shift, scale, weight, bias, eps) fuses LayerNorm + modulation."""
+    M, K = x.shape
+    Mp = padded_rows(M)
+    q = torch.empty(Mp, K, device=x.device, dtype=torch.uint8)
+    ascales = torch.empty(K // 64, Mp, device=x.device, dtype=torch.bfloat16)
+    lora = None if proj_down_t is None else torch.empty(Mp, RANK, device=x.device, dtype=torch.float32)
+    ln = ln or {}
+    _lib.call("wdl_act_quant_w4", ptr(x), x.stride(0), M, K, ptr(smooth), float(qshift), int(unsigned),
+              ptr(proj_down_t), RANK, ptr(q), ptr(ascales), ptr(lora), Mp, ptr(ln.get("shift")), ptr(ln.get("scale")),
+              ptr(ln.get("weight")), ptr(ln.get("bias")), int(bool(ln)), float(ln.get("eps", 1e-6)), ptr(v_out),
+              stream_of(x))
+    return q, ascales, lora
+
+
+def gemm_launch(q, ascales, lora, qweight, wscales, proj_up, bias, M, out, epilogue=EPI_BF16, gate=None):
+    Mp, K = q.shape
+    N = qweight.shape[0]
+    _lib.call("wdl_w4a4_gemm", ptr(q), ptr(ascales), ptr(qweight), ptr(wscales), ptr(lora), ptr(proj_up), ptr(bias),
+              M, Mp, N, K, RANK, ptr(out), out.stride(0), epilogue, ptr(gate), stream_of(q))
+    return out
+
+
+@torch.library.custom_op("wdl::act_quant_w4", mutates_args=())
+def act_quant_w4(x: torch.Tensor, smooth: torch.Tensor, proj_down: torch.Tensor, qshift: float,
+                 unsigned: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    return act_quant_launch(x, smooth, proj_down, qshift, unsigned)
+
+
+@act_quant_w4.register_fake
+def _(x, smooth, proj_down, qshift, unsigned):
+    M, K = x.shape
+    Mp = padded_rows(M)
+    return (x.new_empty(Mp, K, dtype=torch.uint8), x.new_empty(K // 64, Mp, dtype=torch.bfloat16),
+            x.new_empty(Mp, RANK, dtype=torch.float32))
+
+
+@torch.library.custom_op("wdl::w4a4_gemm", mutates_args=())
+def w4a4_gemm(q: torch.Tensor, ascales: torch.Tensor, lora: torch.Tensor, qweight: torch.Tensor,
+              wscales: torch.Tensor, proj_up: torch.Tensor, bias: torch.Tensor, M: int, fp32_out: bool) -> torch.Tensor:
+    out = torch.empty(M, qweight.shape[0], device=q.device, dtype=torch.float32 if fp32_out else torch.bfloat16)
+    return gemm_launch(q, ascales, lora, qweight, wscales, proj_up, bias, M, out, EPI_F32 if fp32_out else EPI_BF16)
+
+
+@w4a4_gemm.register_fake
+def _(q, ascales, lora, qweight, wscales, proj_up, bias, M, fp32_out):
+    return q.new_empty(M, qweight.shape[0], dtype=torch.float32 if fp32_out else torch.bfloat16)
+
+
+@torch.library.custom_op("wdl::w4a4_linear", mutates_args=())
+def w4a4_linear(x: torch.Tensor, qweight: torch.Tensor, wscales: torch.Tensor, proj_down: torch.Tensor,
+                proj_up: torch.Tensor, smooth: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    """live::w4a4_linear (native/ops/w4a4_ops.cpp:31-40): activation quantizer + low-rank down projection, then
+    the W4A4 GEMM with the low-rank up projection and the bias; x bf16 [M, K] -> bf16 [M, N]."""
+    q, asc, lora = act_quant_launch(x, smooth, proj_down)
+    out = torch.empty(x.shape[0], qweight.shape[0], device=x.device, dtype=torch.bfloat16)
+    return gemm_launch(q, asc, lora, qweight, wscales, proj_up, bias, x.shape[0], out)
+
+
+@w4a4_linear.register_fake
+def _(x, qweight, wscales, proj_down, proj_up, smooth, bias):
+    return x.new_empty(x.shape[0], qweight.shape[0], dtype=torch.bfloat16)
+
+
+GELU_SHIFT = 0.171875
+
+
+@torch.library.custom_op("wdl::w4a4_gelu_mlp", mutates_args=())
+def w4a4_gelu_mlp(x: torch.Tensor, qweight1: torch.Tensor, wscales1: torch.Tensor, proj_down1: torch.Tensor,
+                  proj_up1: torch.Tensor, smooth1: torch.Tensor, bias1: torch.Tensor, qweight2: torch.Tensor,
+                  wscales2: torch.Tensor, proj_down2: torch.Tensor, proj_up2: torch.Tensor, smooth2: torch.Tensor,
+                  bias2: torch.Tensor) -> torch.Tensor:
+    """live::w4a4_gelu_mlp (native/ops/w4a4_ops.cpp:44-63): h = GELU(x W1^T + b1) in the first GEMM's epilogue
+    (bf16 h), then (h + 0.171875) / smooth2 quantized unsigned with the low-rank down projection of h, then the
+    second GEMM."""
+    M = x.shape[0]
+    q, asc, lora = act_quant_launch(x, smooth1, proj_down1)
+    h = torch.empty(M, qweight1.shape[0], device=x.device, dtype=torch.bfloat16)
+    gemm_launch(q, asc, lora, qweight1, wscales1, proj_up1, bias1, M, h, EPI_GELU)
+    q2, asc2, lora2 = act_quant_launch(h, smooth2, proj_down2, GELU_SHIFT, True)
+    out = torch.empty(M, qweight2.shape[0], device=x.device, dtype=torch.bfloat16)
+    return gemm_launch(q2, asc2, lora2, qweight2, wscales2, proj_up2, bias2, M, out)
+
+
+@w4a4_gelu_mlp.register_fake
+def _(x, qweight1, wscales1, proj_down1, proj_up1, smooth1, bias1, qweight2, wscales2, proj_down2, proj_up2,
+      smooth2, bias2):
+    return x.new_empty(x.shape[0], qweight2.shape[0], dtype=torch.bfloat16)

@@ -1,0 +1,158 @@
+"""W4A4 linears of SVDQuant on MI355X: the module API of src/wan_dit_lab/quantization/w4a4.py over the wdl::* ops.
+
+    y = x W^T + b = Q(x / s) Q(R)^T + (x proj_down) proj_up^T + b,      W diag(s) = up down + R     (w4a4.py:4-10)
+
+Weights are quantized offline (quantize, w4a4.py:140-180) into this build's own packed layout (the reference packs
+into Nunchaku's MMA tile order, which lives outside its tree):
+- qweight uint8 [N, K/2]: per 64-channel group, byte j holds k = j in the low nibble and k = j + 32 in the high
+  nibble, two's complement int4 (pack_weight / unpack_weight);
+- wscales bf16 [K/64, N] (group-major); proj_down bf16 [32, K] (the down factor divided by s, transposed);
+  proj_up bf16 [N, 32]; smooth bf16 [K]; bias bf16 [N] (shift-corrected for the second GELU-MLP layer).
+The integer values are those of int4_groups (w4a4.py:80-100) on the quantizer input R; the int4 parity of the
+build is defined on R, since the SVD is not bit-portable between LAPACK and rocSOLVER.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from wdl import ops
+from wdl.ops import GELU_SHIFT, w4a4_gelu_mlp, w4a4_linear
+
+GROUP = 64
+PARTS = ("qweight", "wscales", "proj_down", "proj_up", "smooth", "bias")  # w4a4.py:207
+MSE_STEPS = torch.linspace(0.5, 1.0, 26).tolist()
+
+__all__ = ["GROUP", "GELU_SHIFT", "PARTS", "int4_groups", "smoothing", "quantize", "pack_weight", "unpack_weight",
+           "linear", "gelu_mlp", "w4a4_linear", "w4a4_gelu_mlp", "PackedW4A4Linear", "PackedW4A4GeluMLP"]
+
+
+@torch.no_grad()
+def int4_groups(R: torch.Tensor, rule: str = "max"):
+    """R [N, K] in symmetric INT4 groups of 64 input channels (w4a4.py:80-100): the integers [N, K] and the fp32
+    scales [N, K/64]. "max": the largest |x| of a group maps to 7. "mse": of the scales MSE_STEPS times that one,
+    the one with the least squared error of the group."""
+    N, K = R.shape
+    g = R.float().reshape(N, K // GROUP, GROUP)
+    base = g.abs().amax(dim=-1).clamp(min=1e-8) / 7
+    scale = base
+    if rule == "mse":
+        best = None
+        for c in MSE_STEPS:
+            s = base * c
+            err = (g - torch.round(g / s[..., None]).clamp(-8, 7) * s[..., None]).square().sum(-1)
+            if best is None:
+                best, scale = err, s
+            else:
+                take = err < best
+                best = torch.where(take, err, best)
+                scale = torch.where(take, s, scale)
+    elif rule != "max":
+        raise ValueError(f"unknown rule {rule!r}")
+    q = torch.round(g / scale[..., None]).clamp(-8, 7).to(torch.int32).reshape(N, K)
+    return q, scale
+
+
+def smoothing(act_amax: torch.Tensor, weight: torch.Tensor, alpha: float = 0.5) -> torch.Tensor:
+    """SmoothQuant's per-input-channel s = max|x|^alpha / max|W|^(1-alpha), clamped to [1e-2, 1e2]
+    (w4a4.py:183-186)."""
+    wmax = weight.float().abs().amax(dim=0).clamp(min=1e-5)
+    amax = act_amax.float().to(wmax.device).clamp(min=1e-5)
+    return (amax ** alpha / wmax ** (1 - alpha)).clamp(min=1e-2, max=1e2)
+
+
+def pack_weight(q: torch.Tensor) -> torch.Tensor:
+    """int4 values [N, K] -> uint8 [N, K/2] in this build's layout (module docstring)."""
+    N, K = q.shape
+    u = (q.to(torch.int32) & 0xF).to(torch.uint8).reshape(N, K // GROUP, 2, GROUP // 2)
+    return (u[:, :, 0] | (u[:, :, 1] << 4)).reshape(N, K // 2).contiguous()
+
+
+def unpack_weight(p: torch.Tensor) -> torch.Tensor:
+    """uint8 [N, K/2] -> int32 [N, K] (inverse of pack_weight)."""
+    N, H = p.shape
+    b = p.reshape(N, H // 32, 32).to(torch.int32)
+    lo, hi = b & 0xF, b >> 4
+    v = torch.stack([lo, hi], dim=2).reshape(N, H * 2)
+    return torch.where(v >= 8, v - 16, v)
+
+
+@torch.no_grad()
+def quantize(weight, bias=None, smooth=None, rank: int = 32, shift: float = 0.0, rule: str = "max", R=None):
+    """The tensors of a W4A4 layer for y = x W^T + b (w4a4.py:140-180) in this build's packed layout.
+    weight [N, K]; smooth [K] (ones when None); shift: the second GELU-MLP layer quantizes x + shift unsigned, so
+    its bias takes off shift * (Q(R) / s) 1. R: the quantizer input, when given (parity tests)."""
+    W = weight.float()
+    N, K = W.shape
+    dev = W.device
+    s = torch.ones(K, device=dev) if smooth is None else smooth.float().to(dev)
+    Ws = W * s[None, :]
+    U, S, Vh = torch.linalg.svd(Ws, full_matrices=False)
+    up, down = U[:, :rank] * S[:rank], Vh[:rank]
+    if R is None:
+        R = Ws - up @ down
+    q, scale = int4_groups(R.to(dev), rule)
+    b = torch.zeros(N, device=dev) if bias is None else bias.float().to(dev)
+    if shift:
+        deq = (q.reshape(N, K // GROUP, GROUP).float() * scale[..., None]).reshape(N, K)
+        b = b - shift * (deq / s[None, :]).sum(dim=1)
+    return dict(
+        qweight=pack_weight(q),
+        wscales=scale.to(torch.bfloat16).t().contiguous(),
+        proj_down=(down / s[None, :]).to(torch.bfloat16).contiguous(),
+        proj_up=up.to(torch.bfloat16).contiguous(),
+        smooth=s.to(torch.bfloat16),
+        bias=b.to(torch.bfloat16),
+    )
+
+
+def random_parts(N: int, K: int, device, generator=None, rank: int = 32, scale: float = 0.02, unsigned_input=False):
+    """A W4A4 layer of the right shapes and value ranges without an SVD (random-init weights of the architecture,
+    for the step benchmark): int4 in [-7, 7], group scales of a N(0, scale^2) weight, small low-rank factors."""
+    g = generator
+    q = torch.randint(-7, 8, (N, K), generator=g, device="cpu", dtype=torch.int32)
+    wsc = (torch.rand(K // GROUP, N, generator=g) * 0.5 + 0.75) * (3 * scale / 7)
+    return dict(
+        qweight=pack_weight(q).to(device),
+        wscales=wsc.to(torch.bfloat16).to(device),
+        proj_down=(torch.randn(rank, K, generator=g) * (1 / K ** 0.5)).to(torch.bfloat16).to(device),
+        proj_up=(torch.randn(N, rank, generator=g) * scale).to(torch.bfloat16).to(device),
+        smooth=torch.ones(K, dtype=torch.bfloat16, device=device),
+        bias=(torch.randn(N, generator=g) * scale).to(torch.bfloat16).to(device),
+    )
+
+
+def linear(x: torch.Tensor, t: dict) -> torch.Tensor:
+    """y = x W^T + b for x [M, K] bf16 and t the tensors of quantize (w4a4.py:189-192)."""
+    return w4a4_linear(x, *(t[part] for part in PARTS))
+
+
+def gelu_mlp(x: torch.Tensor, t1: dict, t2: dict) -> torch.Tensor:
+    """GELU(x W1^T + b1) W2^T + b2, t2 made with shift=GELU_SHIFT (w4a4.py:198-204)."""
+    return w4a4_gelu_mlp(x, *(t1[p] for p in PARTS), *(t2[p] for p in PARTS))
+
+
+class PackedW4A4Linear(torch.nn.Module):
+    """A W4A4 linear layer over the parts of quantize (w4a4.py:220-231)."""
+
+    def __init__(self, **parts):
+        super().__init__()
+        self.parts = [parts[name] for name in PARTS]
+        self.out_features = parts["proj_up"].shape[0]
+
+    def forward(self, X):
+        y = w4a4_linear(X.reshape(-1, X.shape[-1]).to(torch.bfloat16).contiguous(), *self.parts)
+        return y.reshape(*X.shape[:-1], self.out_features)
+
+
+class PackedW4A4GeluMLP(torch.nn.Module):
+    """Wan's feed forward (Linear, GELU tanh, Linear) in W4A4 as one gelu_mlp (w4a4.py:234-245)."""
+
+    def __init__(self, fc1, fc2):
+        super().__init__()
+        self.parts = [fc1[name] for name in PARTS] + [fc2[name] for name in PARTS]
+        self.out_features = fc2["proj_up"].shape[0]
+
+    def forward(self, X):
+        y = w4a4_gelu_mlp(X.reshape(-1, X.shape[-1]).to(torch.bfloat16).contiguous(), *self.parts)
+        return y.reshape(*X.shape[:-1], self.out_features)
