@@ -66,6 +66,44 @@ int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* qweight, cons
                   const void* proj_up, const void* bias, int64_t M, int64_t Mp, int64_t N, int64_t K, int64_t rank,
                   void* out, int64_t ldo, int epilogue, const float* gate, wdl_stream_t stream);
 
+/* Q/K RMSNorm over all heads + 3D RoPE, fused. Replaces norm_q / norm_k (src/wan_dit_lab/models/rms_norm.py:10-13,
+ * used at src/wan_dit_lab/quantization/w4a4.py:256-257) and rope_apply / wan_dit_lab::rope3d_rotate
+ * (src/wan_dit_lab/models/rope.py:12-31; src/wan_dit_lab/kernels/rope_triton.py:66-81, 101-144).
+ * q, k: bf16 [M, heads*128] with row strides ldq, ldk; wq, wk: bf16 [heads*128]; freq: fp32 [2, positions, 64]
+ * (cos, sin; pairs split [22 time, 21 height, 21 width]); grid (f, h, w) with f*h*w <= M, time offset start_frame.
+ * Row m: n = bf16(x * rstd), y = bf16(n * w); pairs of rows m < f*h*w rotated at (start_frame + m/(h*w),
+ * (m/w)%h, m%w) in fp32, results bf16 into q_out, k_out [M, heads*128] (row stride ldo). */
+int wdl_qk_norm_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* wq, const void* wk,
+                     const float* freq, int64_t positions, int64_t M, int64_t heads, int f, int h, int w,
+                     int start_frame, float eps, void* q_out, void* k_out, int64_t ldo, wdl_stream_t stream);
+
+/* Sage per-thread int8 quantization of Q. Replaces sage_kv.quant_q (src/wan_dit_lab/kernels/sage_kv.py:112-124).
+ * x: bf16 [n, heads, 128] (token stride ldx); q: int8 [n, heads, 128]; q_scale: fp32 [heads, ceil(n/128)*32].
+ * Per 32-token block, tokens l, l+8, l+16, l+24 share scale = max|x| / 127 + 1e-7; q = trunc(x/scale +- 0.5). */
+int wdl_quant_q(const void* x, int64_t ldx, int64_t n, int64_t heads, void* q, float* q_scale, wdl_stream_t stream);
+
+/* Workspace (in floats) that wdl_sage_prep needs for `splits` token splits. */
+int64_t wdl_sage_prep_workspace_floats(int64_t heads, int splits);
+
+/* Sage preparation straight from the FP8 cache: K mean, int8 K, fp8 V. Replaces the Triton kernels _sum_max,
+ * _quant_k, _quant_v of sage_kv._attend (src/wan_dit_lab/kernels/sage_kv.py:43-105, 152-173).
+ * Tokens t < at from cache_k/cache_v (fp8 [capacity, heads, 128]) times cache_ks/cache_vs (fp32 [capacity, heads]),
+ * at <= t < at + n from k, v (bf16 [n, heads, 128], token strides ldk, ldv). Outputs: k_int8 [heads, Lpad, 128],
+ * k_scale fp32 [heads, Lpad/16], v_fp8 [heads, 128, Lpad] (within each 64-token block, token t at position
+ * 32*((t%8)/4) + 4*(t/8) + t%4), Lpad = 64*ceil(L/64); k_mean_out / v_scale_out fp32 [heads, 128] (may be NULL:
+ * then kept in the workspace). Batch 1. */
+int wdl_sage_prep(const void* cache_k, const float* cache_ks, const void* cache_v, const float* cache_vs,
+                  int64_t capacity, const void* k, int64_t ldk, const void* v, int64_t ldv, int64_t heads, int64_t at,
+                  int64_t n, int splits, float* workspace, void* k_int8, float* k_scale, void* v_fp8,
+                  float* k_mean_out, float* v_scale_out, wdl_stream_t stream);
+
+/* Sage-2 style attention (int8 QK^T, fp32 online softmax, fp8 PV, non-causal). Replaces live::sage_sm89
+ * (native/ops/sage_ops.cpp:12-19, 28-35) on the layouts of wdl_quant_q / wdl_sage_prep.
+ * out: bf16 [n, heads, 128] (row stride ldo). */
+int wdl_sage_attn(const void* q_i8, int64_t ldq, const float* q_scale, const void* k_i8, const float* k_scale,
+                  const void* v_fp8, const float* v_scale, int64_t n, int64_t L, int64_t heads, float sm_scale,
+                  void* out, int64_t ldo, wdl_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,7 +10,7 @@ ROOT = Path(__file__).resolve().parents[1]
 
 def declared():
     text = (ROOT / "include" / "wdl.h").read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(wdl_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(wdl_\w+)\(", text, re.M)))
 
 
 def test_header_declares_entry_points():

@@ -1,0 +1,208 @@
+// Q/K RMSNorm over the whole row (all heads) and 3D RoPE, fused, plus Sage's per-thread int8 quantization of Q.
+//
+// qk_norm_rope: for each token row m of q and k (bf16, row strides ldq / ldk, H heads of D = 128):
+//   n   = bf16(x * rstd),   rstd = 1 / sqrt(mean(x^2) + eps)   (fp32; ordered sum: 8 column slots per row,
+//         each summing its 8-wide chunks group by group, then an xor butterfly 4, 2, 1)
+//   w   = bf16(n * weight)                                      (RMSNorm, models/rms_norm.py:12-13)
+//   rot = bf16(x1 c - x2 s), bf16(x2 c + x1 s) on pairs (2p, 2p+1) (models/rope.py:26-31, fp32 math)
+// with pair p of a head on the time axis for p < 22, height for p < 43, width otherwise; the token's position is
+// (start_frame + m / (h w), (m / w) % h, m % w) and (c, s) = freq[0/1][position][p] (fp32 table [2, P, 64]).
+// Rows m >= f h w (padding) are normalized but not rotated. Outputs are bf16 [M, H*D] (row stride ldo).
+//
+// quant_q: Sage's per-thread int8 Q (kernels/sage_kv.py:112-124): per 32-token block and head, lane l = 0..7 owns
+// tokens l, l+8, l+16, l+24 with scale = max|x| / 127 + 1e-7, q = trunc(x / scale +- 0.5).
+#include "wdl_common.h"
+
+namespace {
+
+using namespace wdl;
+
+constexpr int ROWS = 32;
+
+struct NormRopeArgs {
+    const uint16_t* q;
+    int64_t ldq;
+    const uint16_t* k;
+    int64_t ldk;
+    const uint16_t* wq;  // bf16 [H*D]
+    const uint16_t* wk;
+    const float* freq;   // [2, P, D/2]
+    int64_t P;
+    int64_t M, C;        // rows, columns (H * D)
+    int f, h, w, start;
+    float eps;
+    uint16_t* qo;
+    uint16_t* ko;
+    int64_t ldo;
+};
+
+__device__ __forceinline__ void load8(const uint16_t* p, float* f) {
+    uint4 raw = *reinterpret_cast<const uint4*>(p);
+    const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f[2 * j] = __uint_as_float(wv[j] << 16);
+        f[2 * j + 1] = __uint_as_float(wv[j] & 0xffff0000u);
+    }
+}
+
+__device__ __forceinline__ float rowsum8(float s) {
+    s = s + __shfl_xor(s, 4, 8);
+    s = s + __shfl_xor(s, 2, 8);
+    s = s + __shfl_xor(s, 1, 8);
+    return s;
+}
+
+__device__ __forceinline__ float rms_rstd(const uint16_t* row, int G, int slot, bool live, int64_t C, float eps) {
+    float s = 0.0f;
+    for (int g = 0; g < G; ++g) {
+        float f[8];
+        if (live) load8(row + g * 64 + slot * 8, f);
+        else
+            for (int j = 0; j < 8; ++j) f[j] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s = s + f[j] * f[j];
+    }
+    s = rowsum8(s);
+    return 1.0f / sqrtf(s / float(C) + eps);
+}
+
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs a) {
+    const int t = threadIdx.x, slot = t % 8;
+    const int64_t row = int64_t(blockIdx.x) * ROWS + t / 8;
+    const bool live = row < a.M;
+    const int G = int(a.C / 64);
+    const int64_t hw = int64_t(a.h) * a.w;
+    const bool rot = live && row < int64_t(a.f) * hw;
+    const int pos_t = a.start + int(row / (hw > 0 ? hw : 1));
+    const int pos_h = hw > 0 ? int((row / a.w) % a.h) : 0;
+    const int pos_w = hw > 0 ? int(row % a.w) : 0;
+    const int half = 64;  // pairs per head (D = 128)
+    const int tpairs = half - 2 * (half / 3);  // 22
+    const int spairs = half / 3;                // 21
+    for (int which = 0; which < 2; ++which) {
+        const uint16_t* src = which == 0 ? a.q : a.k;
+        const int64_t ld = which == 0 ? a.ldq : a.ldk;
+        const uint16_t* wt = which == 0 ? a.wq : a.wk;
+        uint16_t* dst = which == 0 ? a.qo : a.ko;
+        const uint16_t* rp = src + (live ? row : 0) * ld;
+        const float rstd = rms_rstd(rp, G, slot, live, a.C, a.eps);
+        if (!live) continue;
+        for (int g = 0; g < G; ++g) {
+            const int64_t col = int64_t(g) * 64 + slot * 8;
+            float x[8];
+            load8(rp + col, x);
+            float y[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float n = bf16_to_f32(f32_to_bf16(x[j] * rstd));
+                y[j] = bf16_to_f32(f32_to_bf16(n * bf16_to_f32(wt[col + j])));
+            }
+            uint16_t o[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float x1 = y[2 * i], x2 = y[2 * i + 1];
+                if (rot) {
+                    const int p = int((col + 2 * i) % 128) / 2;
+                    const int pos = p < tpairs ? pos_t : (p < tpairs + spairs ? pos_h : pos_w);
+                    const float c = a.freq[(int64_t(pos)) * half + p];
+                    const float s = a.freq[(a.P + pos) * half + p];
+                    o[2 * i] = f32_to_bf16(x1 * c - x2 * s);
+                    o[2 * i + 1] = f32_to_bf16(x2 * c + x1 * s);
+                } else {
+                    o[2 * i] = f32_to_bf16(x1);
+                    o[2 * i + 1] = f32_to_bf16(x2);
+                }
+            }
+            *reinterpret_cast<uint4*>(dst + row * a.ldo + col) =
+                make_uint4(o[0] | (uint32_t(o[1]) << 16), o[2] | (uint32_t(o[3]) << 16), o[4] | (uint32_t(o[5]) << 16),
+                           o[6] | (uint32_t(o[7]) << 16));
+        }
+    }
+}
+
+// one wave per (32-token block, head); lane = 2 * token_in_block + (d half); values of 64 d per lane
+__global__ __launch_bounds__(256) void quant_q_kernel(const uint16_t* x, int64_t ldx, int64_t n, int64_t H,
+                                                      int64_t blocks, int8_t* q, float* q_scale) {
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int64_t item = int64_t(blockIdx.x) * 4 + wave;  // (block, head)
+    if (item >= blocks * H) return;
+    const int64_t blk = item / H, h = item % H;
+    const int tok = lane / 2, dh = lane % 2;
+    const int64_t token = blk * 32 + tok;
+    const bool live = token < n;
+    float v[64];
+    float amax = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        float f[8];
+        if (live) load8(x + token * ldx + h * 128 + dh * 64 + c * 8, f);
+        else
+            for (int j = 0; j < 8; ++j) f[j] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            v[c * 8 + j] = f[j];
+            amax = fmaxf(amax, fabsf(f[j]));
+        }
+    }
+    // group of lane l8 = tok % 8: tokens l8 + 8k -> lanes 2 * l8 + 16 k + dh: xor over lane bits 0, 4, 5
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    const float scale = amax / 127.0f + 1e-7f;
+    if (lane < 16 && (lane % 2) == 0) q_scale[h * blocks * 8 + blk * 8 + lane / 2] = scale;
+    if (!live) return;
+    int8_t* dst = q + token * (H * 128) + h * 128 + dh * 64;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        uint32_t w[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float y = v[c * 16 + b * 4 + e] / scale;
+                const float r = __builtin_truncf(y + (y >= 0.0f ? 0.5f : -0.5f));
+                word |= (uint32_t(int32_t(r)) & 0xffu) << (8 * e);
+            }
+            w[b] = word;
+        }
+        *reinterpret_cast<uint4*>(dst + c * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+}  // namespace
+
+extern "C" int wdl_qk_norm_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* wq,
+                                const void* wk, const float* freq, int64_t positions, int64_t M, int64_t heads,
+                                int f, int h, int w, int start_frame, float eps, void* q_out, void* k_out,
+                                int64_t ldo, hipStream_t stream) {
+    const int64_t C = heads * 128;
+    if (M < 0 || heads <= 0 || ldq < C || ldk < C || ldo < C || f < 0 || h <= 0 || w <= 0 || start_frame < 0)
+        return fail(WDL_EINVAL, "qk_norm_rope: bad shape");
+    if (int64_t(f) * h * w > M) return fail(WDL_EINVAL, "qk_norm_rope: grid exceeds the rows");
+    if (start_frame + f > positions || h > positions || w > positions)
+        return fail(WDL_EINVAL, "qk_norm_rope: grid or offset exceeds the frequency table");
+    if (!q || !k || !wq || !wk || !freq || !q_out || !k_out) return fail(WDL_EINVAL, "qk_norm_rope: null pointer");
+    if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(q_out) |
+         reinterpret_cast<uintptr_t>(k_out) | (ldq * 2) | (ldk * 2) | (ldo * 2)) % 16)
+        return fail(WDL_EINVAL, "qk_norm_rope: rows must be 16-byte aligned");
+    if (M == 0) return WDL_OK;
+    NormRopeArgs a{static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(k), ldk,
+                   static_cast<const uint16_t*>(wq), static_cast<const uint16_t*>(wk), freq, positions, M, C,
+                   f, h, w, start_frame, eps, static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_out), ldo};
+    qk_norm_rope_kernel<<<unsigned((M + ROWS - 1) / ROWS), 256, 0, stream>>>(a);
+    return check_launch("qk_norm_rope");
+}
+
+extern "C" int wdl_quant_q(const void* x, int64_t ldx, int64_t n, int64_t heads, void* q, float* q_scale,
+                           hipStream_t stream) {
+    if (n < 0 || heads <= 0 || ldx < heads * 128) return fail(WDL_EINVAL, "quant_q: bad shape");
+    if (!x || !q || !q_scale) return fail(WDL_EINVAL, "quant_q: null pointer");
+    if ((reinterpret_cast<uintptr_t>(x) | (ldx * 2)) % 16) return fail(WDL_EINVAL, "quant_q: unaligned rows");
+    const int64_t blocks = (n + 127) / 128 * 4;
+    if (n == 0) return WDL_OK;
+    quant_q_kernel<<<unsigned((blocks * heads + 3) / 4), 256, 0, stream>>>(
+        static_cast<const uint16_t*>(x), ldx, n, heads, blocks, static_cast<int8_t*>(q), q_scale);
+    return check_launch("quant_q");
+}

@@ -1,0 +1,216 @@
+// Sage-2 preparation read straight from the FP8 KV cache and the chunk's own bf16 K/V (kernels/sage_kv.py:28-173).
+//
+// Token t of a call: t < at comes from the cache (e4m3 value * its fp32 row scale), at <= t < L = at + n from the
+// chunk (bf16), t >= L is zero. Three launches:
+//   colstats   (grid H x S): per split s of the tokens, partial sums of K and maxima of |V| per (head, channel),
+//              each in a fixed order (16 token lanes, then the lanes in order);
+//   finalize   (grid H):     k_mean = (sum over splits, in order) / L;  v_scale = max(max |V|, 1e-8) / 2.25;
+//   quant_kv   (grid blocks x H): K - mean to int8 with one scale per group g = 0..3 of each 64-token block (tokens
+//              8i + 2g, 8i + 2g + 1): scale = max|x| / 127 + 1e-7, q = trunc(x / scale +- 0.5);
+//              V / v_scale to e4m3, stored per (head, channel) along the tokens in this build's order: within a
+//              64-token block, position 32 * ((t % 8) / 4) + 4 * (t / 8) + t % 4 holds token t (the key order one
+//              lane half of the transposed QK^T MFMA tile produces, so P feeds the PV MFMA unshuffled).
+// Layouts: k_int8 [H, Lpad, 128]; k_scale fp32 [H, Lpad / 64 * 4]; v_fp8 [H, 128, Lpad]; Lpad = 64 * ceil(L / 64);
+// padding tokens are zero in both.
+#include "wdl_common.h"
+
+namespace {
+
+using namespace wdl;
+
+constexpr int D = 128;
+
+struct Src {
+    const uint8_t* cache;   // [cap, H, D] e4m3
+    const float* cscale;    // [cap, H]
+    const uint16_t* chunk;  // bf16, token stride ld, head stride D
+    int64_t ld;
+};
+
+__device__ __forceinline__ void load_token8(const Src& s, int64_t t, int64_t h, int64_t H, int64_t at, int64_t L,
+                                            int d0, float* f) {
+    if (t < at) {
+        const uint2 raw = *reinterpret_cast<const uint2*>(s.cache + (t * H + h) * D + d0);
+        const float sc = s.cscale[t * H + h];
+        const uint32_t w[2] = {raw.x, raw.y};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] = e4m3_to_f32(uint8_t(w[j / 4] >> (8 * (j % 4)))) * sc;
+    } else if (t < L) {
+        const uint4 raw = *reinterpret_cast<const uint4*>(s.chunk + (t - at) * s.ld + h * D + d0);
+        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f[2 * j] = __uint_as_float(w[j] << 16);
+            f[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] = 0.0f;
+    }
+}
+
+__global__ __launch_bounds__(256) void colstats_kernel(Src k, Src v, int64_t H, int64_t at, int64_t L, int S,
+                                                       float* part_k, float* part_v) {
+    __shared__ float red[2][16][D];
+    const int64_t h = blockIdx.x, s = blockIdx.y;
+    const int t = threadIdx.x, lane_tok = t / 16, d0 = (t % 16) * 8;
+    const int64_t per = (L + S - 1) / S;
+    const int64_t lo = s * per, hi = min(L, lo + per);
+    float ks[8] = {}, vm[8] = {};
+    for (int64_t tok = lo + lane_tok; tok < hi; tok += 16) {
+        float f[8];
+        load_token8(k, tok, h, H, at, L, d0, f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ks[j] = ks[j] + f[j];
+        load_token8(v, tok, h, H, at, L, d0, f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) vm[j] = fmaxf(vm[j], fabsf(f[j]));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        red[0][lane_tok][d0 + j] = ks[j];
+        red[1][lane_tok][d0 + j] = vm[j];
+    }
+    __syncthreads();
+    if (t < D) {
+        float a = 0.0f, m = 0.0f;
+        for (int i = 0; i < 16; ++i) {
+            a = a + red[0][i][t];
+            m = fmaxf(m, red[1][i][t]);
+        }
+        part_k[(s * H + h) * D + t] = a;
+        part_v[(s * H + h) * D + t] = m;
+    }
+}
+
+__global__ void finalize_kernel(const float* part_k, const float* part_v, int S, int64_t H, int64_t L, float* k_mean,
+                                float* v_scale) {
+    const int64_t h = blockIdx.x;
+    const int d = threadIdx.x;
+    float a = 0.0f, m = 0.0f;
+    for (int s = 0; s < S; ++s) {
+        a = a + part_k[(s * H + h) * D + d];
+        m = fmaxf(m, part_v[(s * H + h) * D + d]);
+    }
+    k_mean[h * D + d] = a / float(L);
+    v_scale[h * D + d] = fmaxf(m, 1e-8f) / 2.25f;
+}
+
+__device__ __forceinline__ int v_position(int t) { return 32 * ((t % 8) / 4) + 4 * (t / 8) + t % 4; }
+
+__global__ __launch_bounds__(256) void quant_kv_kernel(Src k, Src v, int64_t H, int64_t at, int64_t L, int64_t Lpad,
+                                                       const float* k_mean, const float* v_scale, int8_t* k_out,
+                                                       float* k_scale, uint8_t* v_out) {
+    __shared__ float gmax[64][4];
+    __shared__ uint8_t vt[D][64 + 4];  // codes [channel][position]
+    const int64_t blk = blockIdx.x, h = blockIdx.y;
+    const int t = threadIdx.x, tt = t / 4, dq = (t % 4) * 32;
+    const int64_t tok = blk * 64 + tt;
+    // K: 32 channels of one token per thread
+    float x[32];
+    float amax = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        float f[8];
+        load_token8(k, tok, h, H, at, L, dq + c * 8, f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float y = tok < L ? f[j] - k_mean[h * D + dq + c * 8 + j] : 0.0f;
+            x[c * 8 + j] = y;
+            amax = fmaxf(amax, fabsf(y));
+        }
+    }
+    gmax[tt][t % 4] = amax;
+    // V codes into the transposed tile
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        float f[8];
+        load_token8(v, tok, h, H, at, L, dq + c * 8, f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int d = dq + c * 8 + j;
+            const float y = f[j] / v_scale[h * D + d];
+            vt[d][v_position(tt)] = tok < L ? f32_to_e4m3(y) : uint8_t(0);
+        }
+    }
+    __syncthreads();
+    const int g = (tt % 8) / 2;
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int member = 8 * i + 2 * g + p;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) m = fmaxf(m, gmax[member][q]);
+        }
+    }
+    const float scale = m / 127.0f + 1e-7f;
+    if (t % 4 == 0 && (tt % 8) == 2 * g && tt < 8) k_scale[h * (Lpad / 64 * 4) + blk * 4 + g] = scale;
+    int8_t* kd = k_out + (h * Lpad + tok) * D + dq;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        uint32_t w[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float y = x[c * 16 + b * 4 + e] / scale;
+                const float r = __builtin_truncf(y + (y >= 0.0f ? 0.5f : -0.5f));
+                word |= (uint32_t(int32_t(r)) & 0xffu) << (8 * e);
+            }
+            w[b] = word;
+        }
+        *reinterpret_cast<uint4*>(kd + c * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    // V: thread -> channel t / 2, 32 positions
+    const int d = t / 2, p0 = (t % 2) * 32;
+    uint8_t* vd = v_out + (h * D + d) * Lpad + blk * 64 + p0;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        uint32_t w[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+            w[b] = uint32_t(vt[d][p0 + c * 16 + b * 4]) | (uint32_t(vt[d][p0 + c * 16 + b * 4 + 1]) << 8) |
+                   (uint32_t(vt[d][p0 + c * 16 + b * 4 + 2]) << 16) | (uint32_t(vt[d][p0 + c * 16 + b * 4 + 3]) << 24);
+        *reinterpret_cast<uint4*>(vd + c * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+}  // namespace
+
+// workspace floats: 2 * S * H * 128 (partials) + 2 * H * 128 (k_mean, v_scale)
+extern "C" int64_t wdl_sage_prep_workspace_floats(int64_t heads, int splits) { return (2 * splits + 2) * heads * D; }
+
+extern "C" int wdl_sage_prep(const void* cache_k, const float* cache_ks, const void* cache_v, const float* cache_vs,
+                             int64_t capacity, const void* k, int64_t ldk, const void* v, int64_t ldv, int64_t heads,
+                             int64_t at, int64_t n, int splits, float* workspace, void* k_int8, float* k_scale,
+                             void* v_fp8, float* k_mean_out, float* v_scale_out, hipStream_t stream) {
+    const int64_t L = at + n;
+    if (at < 0 || n < 0 || heads <= 0 || at > capacity || splits < 1 || ldk < heads * D || ldv < heads * D)
+        return fail(WDL_EINVAL, "sage_prep: bad shape");
+    if (!cache_k || !cache_ks || !cache_v || !cache_vs || !k || !v || !workspace || !k_int8 || !k_scale || !v_fp8)
+        return fail(WDL_EINVAL, "sage_prep: null pointer");
+    if ((reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) | (ldk * 2) | (ldv * 2)) % 16)
+        return fail(WDL_EINVAL, "sage_prep: chunk rows must be 16-byte aligned");
+    if (L == 0) return WDL_OK;
+    const int64_t Lpad = (L + 63) / 64 * 64;
+    Src sk{static_cast<const uint8_t*>(cache_k), cache_ks, static_cast<const uint16_t*>(k), ldk};
+    Src sv{static_cast<const uint8_t*>(cache_v), cache_vs, static_cast<const uint16_t*>(v), ldv};
+    float* part_k = workspace;
+    float* part_v = workspace + int64_t(splits) * heads * D;
+    float* k_mean = k_mean_out ? k_mean_out : workspace + 2 * int64_t(splits) * heads * D;
+    float* v_scale = v_scale_out ? v_scale_out : k_mean + heads * D;
+    colstats_kernel<<<dim3(unsigned(heads), unsigned(splits)), 256, 0, stream>>>(sk, sv, heads, at, L, splits, part_k,
+                                                                                 part_v);
+    int rc = check_launch("sage_prep colstats");
+    if (rc) return rc;
+    finalize_kernel<<<unsigned(heads), D, 0, stream>>>(part_k, part_v, splits, heads, L, k_mean, v_scale);
+    rc = check_launch("sage_prep finalize");
+    if (rc) return rc;
+    quant_kv_kernel<<<dim3(unsigned(Lpad / 64), unsigned(heads)), 256, 0, stream>>>(
+        sk, sv, heads, at, L, Lpad, k_mean, v_scale, static_cast<int8_t*>(k_int8), k_scale,
+        static_cast<uint8_t*>(v_fp8));
+    return check_launch("sage_prep quant_kv");
+}

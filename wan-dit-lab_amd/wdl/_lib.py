@@ -27,7 +27,16 @@ SIGNATURES: dict[str, list] = {
                          c_ptr, c_ptr, c_ptr, c_ptr, c_int, c_f32, c_ptr, c_ptr],
     "wdl_w4a4_gemm": [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_ptr,
                       c_i64, c_int, c_ptr, c_ptr],
+    "wdl_qk_norm_rope": [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_int, c_int, c_int,
+                         c_int, c_f32, c_ptr, c_ptr, c_i64, c_ptr],
+    "wdl_quant_q": [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr],
+    "wdl_sage_prep_workspace_floats": [c_i64, c_int],
+    "wdl_sage_prep": [c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_i64, c_i64, c_i64, c_i64, c_int,
+                      c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr],
+    "wdl_sage_attn": [c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_f32, c_ptr, c_i64,
+                      c_ptr],
 }
+RESTYPES = {"wdl_last_error": ctypes.c_char_p, "wdl_sage_prep_workspace_floats": c_i64}
 
 _LIB = None
 
@@ -41,7 +50,7 @@ def library() -> ctypes.CDLL:
         for name, args in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = args
-            fn.restype = ctypes.c_char_p if name == "wdl_last_error" else c_int
+            fn.restype = RESTYPES.get(name, c_int)
         _LIB = lib
     return _LIB
 

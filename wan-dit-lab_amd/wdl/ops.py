@@ -144,3 +144,83 @@ def w4a4_gelu_mlp(x: torch.Tensor, qweight1: torch.Tensor, wscales1: torch.Tenso
 def _(x, qweight1, wscales1, proj_down1, proj_up1, smooth1, bias1, qweight2, wscales2, proj_down2, proj_up2,
       smooth2, bias2):
     return x.new_empty(x.shape[0], qweight2.shape[0], dtype=torch.bfloat16)
+
+
+# ------------------------------------------------------------------------------------------------ Q/K norm + RoPE
+
+def qk_norm_rope_launch(q, k, wq, wk, freq, grid, start_frame, eps=1e-6, q_out=None, k_out=None):
+    """q, k bf16 [M, H*128] (row-strided views allowed) -> RMSNorm(all heads) + 3D RoPE, bf16 [M, H*128] each."""
+    M, C = q.shape
+    f, h, w = (int(v) for v in grid)
+    q_out = torch.empty(M, C, device=q.device, dtype=torch.bfloat16) if q_out is None else q_out
+    k_out = torch.empty(M, C, device=q.device, dtype=torch.bfloat16) if k_out is None else k_out
+    _lib.call("wdl_qk_norm_rope", ptr(q), q.stride(0), ptr(k), k.stride(0), ptr(wq), ptr(wk), ptr(freq),
+              freq.shape[1], M, C // 128, f, h, w, int(start_frame), float(eps), ptr(q_out), ptr(k_out),
+              q_out.stride(0), stream_of(q))
+    return q_out, k_out
+
+
+def quant_q_launch(x, heads):
+    """x bf16 [n, heads*128] (row stride allowed) -> q int8 [n, heads, 128], q_scale fp32 [heads, blocks*8]."""
+    n = x.shape[0]
+    blocks8 = (n + 127) // 128 * 32
+    q = torch.empty(n, heads, 128, device=x.device, dtype=torch.int8)
+    qs = torch.empty(heads, blocks8, device=x.device, dtype=torch.float32)
+    _lib.call("wdl_quant_q", ptr(x), x.stride(0), n, heads, ptr(q), ptr(qs), stream_of(x))
+    return q, qs
+
+
+SPLITS = 32
+
+
+def sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, k, v, at, want_stats=False):
+    """Cache (fp8 [1, cap, H, 128] + fp32 scales [1, cap, H, 1]) tokens [0, at) and the chunk k, v
+    (bf16 [n, H*128] row-strided) -> k_int8 [H, Lpad, 128], k_scale [H, Lpad/16], v_fp8 [H, 128, Lpad],
+    v_scale [H, 128] (and k_mean when want_stats)."""
+    n = k.shape[0]
+    H = cache_k.shape[2]
+    L = at + n
+    Lp = (L + 63) // 64 * 64
+    dev = k.device
+    ws = torch.empty(_lib.library().wdl_sage_prep_workspace_floats(H, SPLITS), device=dev, dtype=torch.float32)
+    k_i8 = torch.empty(H, Lp, 128, device=dev, dtype=torch.int8)
+    k_sc = torch.empty(H, Lp // 16, device=dev, dtype=torch.float32)
+    v_f8 = torch.empty(H, 128, Lp, device=dev, dtype=torch.uint8)
+    k_mean = torch.empty(H, 128, device=dev, dtype=torch.float32)
+    v_sc = torch.empty(H, 128, device=dev, dtype=torch.float32)
+    _lib.call("wdl_sage_prep", ptr(cache_k), ptr(cache_ks), ptr(cache_v), ptr(cache_vs), cache_k.shape[1], ptr(k),
+              k.stride(0), ptr(v), v.stride(0), H, at, n, SPLITS, ptr(ws), ptr(k_i8), ptr(k_sc), ptr(v_f8),
+              ptr(k_mean), ptr(v_sc), stream_of(k))
+    out = dict(k=k_i8, k_scale=k_sc, v=v_f8, v_scale=v_sc)
+    if want_stats:
+        out["k_mean"] = k_mean
+    return out
+
+
+def sage_attn_launch(q_i8, q_scale, prep, L, sm_scale, out=None):
+    """q_i8 [n, H, 128] -> bf16 [n, H*128] (or into `out`, a row-strided [n, H*128] view)."""
+    n, H, _ = q_i8.shape
+    if out is None:
+        out = torch.empty(n, H * 128, device=q_i8.device, dtype=torch.bfloat16)
+    _lib.call("wdl_sage_attn", ptr(q_i8), H * 128, ptr(q_scale), ptr(prep["k"]), ptr(prep["k_scale"]),
+              ptr(prep["v"]), ptr(prep["v_scale"]), n, L, H, float(sm_scale), ptr(out), out.stride(0), stream_of(q_i8))
+    return out
+
+
+@torch.library.custom_op("wdl::sage_kv_attend", mutates_args=())
+def sage_kv_attend(Q: torch.Tensor, cache_k: torch.Tensor, cache_ks: torch.Tensor, cache_v: torch.Tensor,
+                   cache_vs: torch.Tensor, K: torch.Tensor, V: torch.Tensor, at: int, sm_scale: float) -> torch.Tensor:
+    """wan_dit_lab::sage_kv_attend (src/wan_dit_lab/kernels/sage_kv.py:137-176) without the head/token maps:
+    Q [1, nq, H, 128], K, V [1, n, H, 128] bf16 (row-strided token dim allowed), cache fp8 [1, cap, H, 128] with
+    fp32 scales [1, cap, H, 1] -> [1, nq, H, 128] bf16."""
+    _, nq, H, D = Q.shape
+    n = K.shape[1]
+    prep = sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, K[0].reshape(n, H * D) if K.is_contiguous() else
+                            K[0].flatten(1), V[0].flatten(1), at)
+    q_i8, q_sc = quant_q_launch(Q[0].flatten(1), H)
+    return sage_attn_launch(q_i8, q_sc, prep, at + n, sm_scale).view(1, nq, H, D)
+
+
+@sage_kv_attend.register_fake
+def _(Q, cache_k, cache_ks, cache_v, cache_vs, K, V, at, sm_scale):
+    return Q.new_empty(Q.shape, dtype=torch.bfloat16)

@@ -1,0 +1,55 @@
+"""Sage-2 style attention straight over the FP8 KV cache on MI355X — the API of src/wan_dit_lab/kernels/sage_kv.py.
+
+Tokens [0, at) come from the FP8 cache (value * per-row scale), [at, at + n) from the chunk's own bf16 K, V; the
+K mean, int8 K, fp8 V (wdl_sage_prep), int8 Q (wdl_quant_q) and the attention (wdl_sage_attn) are HIP kernels.
+The head/token maps of the reference (Forcing-KV, sage_kv.py:127-134) are not part of this hot path.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from wdl.ops import quant_q_launch, sage_attn_launch, sage_kv_attend, sage_prep_launch
+
+V_MAX = 2.25  # sage_kv.py:24
+BLKQ, WARPQ, BLKK = 128, 32, 64
+
+__all__ = ["V_MAX", "attend", "quant_q", "prep"]
+
+
+def _check(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V):
+    if Q.ndim != 4 or K.ndim != 4 or V.shape != K.shape or Q.shape[0] != 1 or Q.shape[-1] != 128:
+        raise ValueError("Q, K, V must be [1, tokens, heads, 128]")
+    if Q.shape[2] != K.shape[2] or cache_k.shape[2] != K.shape[2]:
+        raise ValueError("head counts differ")
+    if cache_k.dtype != torch.float8_e4m3fn or cache_v.dtype != torch.float8_e4m3fn:
+        raise TypeError("cache values must be FP8 E4M3FN")
+    if cache_ks.dtype != torch.float32 or cache_vs.dtype != torch.float32:
+        raise TypeError("cache scales must be FP32")
+    if Q.dtype != torch.bfloat16 or K.dtype != torch.bfloat16 or V.dtype != torch.bfloat16:
+        raise TypeError("Q, K, V must be bf16")
+    if not isinstance(at, int) or at < 0 or at > cache_k.shape[1]:
+        raise ValueError("at outside the cache")
+    if any(t.stride(-1) != 1 or t.stride(-2) != 128 for t in (Q, K, V)):
+        raise ValueError("heads must be contiguous [.., heads, 128] rows")
+
+
+def attend(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, sm_scale=None):
+    """softmax(Q K^T * sm_scale) V over the cached tokens [0, at) and the chunk (sage_kv.py:127-134);
+    [1, nq, H, 128] bf16 (sm_scale defaults to 128^-0.5)."""
+    _check(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V)
+    return sage_kv_attend(Q, cache_k.view(torch.uint8), cache_ks, cache_v.view(torch.uint8), cache_vs, K, V, at,
+                          Q.shape[-1] ** -0.5 if sm_scale is None else float(sm_scale))
+
+
+def quant_q(Q):
+    """Sage's per-thread int8 Q (sage_kv.py:112-124): Q [1, n, H, 128] -> (q int8 [1, n, H, 128],
+    q_scale fp32 [1, H, blocks * 8])."""
+    q, qs = quant_q_launch(Q[0].flatten(1), Q.shape[2])
+    return q[None], qs[None]
+
+
+def prep(cache_k, cache_ks, cache_v, cache_vs, at, K, V):
+    """The quantized K/V operands of one call in this build's layouts (see wdl_sage_prep in include/wdl.h)."""
+    return sage_prep_launch(cache_k.view(torch.uint8), cache_ks, cache_v.view(torch.uint8), cache_vs,
+                            K[0].flatten(1), V[0].flatten(1), at, want_stats=True)
