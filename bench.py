@@ -1,0 +1,288 @@
+"""DiT step benchmark on one MI355X: the Wan2.2-TI2V-5B-shaped, W4A4 + FP8-KV denoising step at 512x928.
+
+Workload: 30 blocks (dim 3072, 24 heads x 128, FFN 14336) over one 3-latent-frame chunk of 16 x 29 tokens (1392),
+with a full 21-frame rolling window (8352 cached FP8 tokens + the chunk = 9744 keys) and 512 cross-attention
+tokens, random-init W4A4 weights of that architecture (synthetic data; no checkpoint). A step is
+WanModel.forward (src/wan_dit_lab/models/model.py:32-84): patch embedding, time embedding and projection, the 30
+blocks (each writing its chunk into its FP8 cache and attending over the window), head and unpatchify. The
+timed loop replays one HIP graph of the whole step K times; the per-kernel durations (W4A4 GEMM, attention) come
+from an instrumented eager step with HIP events on the launch stream.
+
+Prints one JSON line (rank 0; one GPU).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "wan-dit-lab_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+DIM, HEADS, FFN, BLOCKS = 3072, 24, 14336, 30
+GRID = (3, 16, 29)                 # 512x928: 3 latent frames of 16 x 29 tokens
+TOKENS = GRID[0] * GRID[1] * GRID[2]  # 1392
+PER_FRAME = GRID[1] * GRID[2]        # 464
+WINDOW = 21                          # frames attention sees: 18 cached + the 3-frame chunk
+CACHED = (WINDOW - GRID[0]) * PER_FRAME  # 8352
+CONTEXT = 512
+LATENT = 48
+INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 / fp8 MFMA
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Step:
+    """One DiT step over resident weights and caches."""
+
+    def __init__(self, device, seed=0):
+        import torch
+
+        from wdl.block import random_block
+        from wdl.kvcache import KVCache
+        from wdl.rope import freqs
+
+        g = torch.Generator(device=device).manual_seed(seed)
+        self.device = device
+        self.blocks = []
+        for i in range(BLOCKS):
+            self.blocks.append(random_block(DIM, FFN, HEADS, device, g))
+        log(f"bench: {BLOCKS} blocks of random W4A4 weights ready")
+        self.caches = []
+        for i in range(BLOCKS):
+            c = KVCache(CACHED, 0, chunk=GRID[0])
+            c.allocate(torch.empty(1, TOKENS, HEADS, 128, device=device))
+            c.fill_for_benchmark(g)
+            self.caches.append(c)
+        context = torch.randn(CONTEXT, DIM, generator=g, device=device).to(torch.bfloat16)
+        self.ctx = [b.prepare_context(context) for b in self.blocks]
+        self.freq = freqs(128, 1024, device)
+        bf = torch.bfloat16
+        r = lambda *s: torch.randn(*s, generator=g, device=device)
+        patch = LATENT * 4
+        self.w_patch, self.b_patch = (r(DIM, patch) * 0.02).to(bf), (r(DIM) * 0.02).to(bf)
+        self.w_t1, self.b_t1 = (r(DIM, 256) * 0.02).to(bf), (r(DIM) * 0.02).to(bf)
+        self.w_t2, self.b_t2 = (r(DIM, DIM) * 0.02).to(bf), (r(DIM) * 0.02).to(bf)
+        self.w_proj, self.b_proj = (r(6 * DIM, DIM) * 0.02).to(bf), (r(6 * DIM) * 0.02).to(bf)
+        self.w_head, self.b_head = (r(patch, DIM) * 0.02).to(bf), (r(patch) * 0.02).to(bf)
+        self.head_mod = r(2, DIM) / DIM ** 0.5
+        self.latent = r(1, LATENT, GRID[0], 2 * GRID[1], 2 * GRID[2]).to(bf)
+        self.t = torch.tensor([750.0], device=device)
+        self.X = torch.empty(TOKENS, DIM, device=device, dtype=bf)
+        self.out = torch.empty(1, LATENT, GRID[0], 2 * GRID[1], 2 * GRID[2], device=device, dtype=bf)
+        # the chunk sits after the window's cached frames: its first frame is frame 18
+        self.start_frame = WINDOW - GRID[0]
+
+    def __call__(self):
+        import torch
+        import torch.nn.functional as F
+
+        f, h, w = GRID
+        # patch embedding: conv3d (1, 2, 2) / (1, 2, 2) as a matmul over patches (model.py:13, 37)
+        x = self.latent.view(1, LATENT, f, h, 2, w, 2).permute(0, 2, 3, 5, 1, 4, 6).reshape(TOKENS, LATENT * 4)
+        self.X.copy_(F.linear(x, self.w_patch, self.b_patch))
+        # time embedding (model.py:38-41)
+        omega = 10000 ** (-torch.arange(128, dtype=torch.float64, device=self.device) / 128)
+        theta = self.t.double()[:, None] * omega[None, :]
+        temb = torch.cat([torch.cos(theta), torch.sin(theta)], dim=1).to(torch.bfloat16)
+        temb = F.linear(F.silu(F.linear(temb, self.w_t1, self.b_t1)), self.w_t2, self.b_t2)
+        e0 = F.linear(F.silu(temb), self.w_proj, self.b_proj).float().view(6, DIM)
+        for blk, cache, ctx in zip(self.blocks, self.caches, self.ctx):
+            e = e0 + blk.p["modulation"]
+            blk.forward(self.X, e, GRID, self.freq, self.start_frame, cache, ctx)
+        # head + unpatchify (head.py:13-18; model.py:81-84)
+        shift, scale = (self.head_mod + temb.float()).chunk(2, dim=0)
+        y = F.layer_norm(self.X.float(), (DIM,), eps=1e-6) * (1 + scale) + shift
+        y = F.linear(y.to(torch.bfloat16), self.w_head, self.b_head)
+        y = y.view(1, f, h, w, 1, 2, 2, LATENT).permute(0, 7, 1, 4, 2, 5, 3, 6).reshape(self.out.shape)
+        self.out.copy_(y)
+        return self.out
+
+
+def instrumented(step):
+    """One eager step with HIP events around every W4A4 GEMM and attention launch (on the launch stream)."""
+    import torch
+
+    from wdl import ops
+
+    rec = {"gemm": [], "attn": []}
+    orig_gemm, orig_attn = ops.gemm_launch, ops.sage_attn_launch
+
+    def gemm(q, ascales, lora, qweight, *a, **k):
+        M = a[3]
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        out = orig_gemm(q, ascales, lora, qweight, *a, **k)
+        e1.record()
+        rec["gemm"].append((e0, e1, 2.0 * M * qweight.shape[0] * q.shape[1]))
+        return out
+
+    def attn(q_i8, q_scale, prep, L, sm_scale, out=None):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        r = orig_attn(q_i8, q_scale, prep, L, sm_scale, out)
+        e1.record()
+        n, H, d = q_i8.shape
+        rec["attn"].append((e0, e1, 4.0 * n * L * d * H))
+        return r
+
+    ops.gemm_launch, ops.sage_attn_launch = gemm, attn
+    import wdl.block as wblock
+    wblock.ops.gemm_launch, wblock.ops.sage_attn_launch = gemm, attn
+    try:
+        step()
+        torch.cuda.synchronize()
+    finally:
+        ops.gemm_launch, ops.sage_attn_launch = orig_gemm, orig_attn
+    out = {}
+    for name, items in rec.items():
+        ms = sum(a.elapsed_time(b) for a, b, _ in items)
+        flops = sum(f for _, _, f in items)
+        out[name] = dict(launches=len(items), ms=ms, tops=flops / (ms * 1e-3) / 1e12 if ms else 0.0)
+    return out
+
+
+def cpu_baseline():
+    """The oracle block of BASELINE config 1 (464-token frame over a 928-token FP8 cache, 512 context tokens,
+    dim 3072) timed on this host's cores; reported as latent tokens/s of a 30-block step."""
+    import torch
+
+    from oracle import block as oblock
+    from oracle import rope as orope
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(0)
+    P = oblock.random_logical_block(DIM, FFN, g)
+    grid, M, prior = (1, 16, 29), 464, 928
+    X = torch.randn(M, DIM, generator=g).to(torch.bfloat16)
+    time_in = torch.randn(6, DIM, generator=g) * 0.1
+    C = torch.randn(CONTEXT, DIM, generator=g).to(torch.bfloat16)
+    freq = orope.freqs(128, 1024, torch.float64).float()
+    ck = (torch.randn(1, prior + M, HEADS, 128, generator=g) * 100).clamp(-448, 448).to(torch.float8_e4m3fn)
+    cks = torch.rand(1, prior + M, HEADS, 1, generator=g) * 0.02
+    ctx = oblock.context_kv(C, P)
+    runs = []
+    for i in range(3):
+        cache = dict(k=ck.clone(), ks=cks.clone(), v=ck.clone(), vs=cks.clone(), at=prior)
+        t0 = time.perf_counter()
+        oblock.block_forward(X, time_in, P, grid, freq, 2, cache, ctx, HEADS)
+        runs.append(time.perf_counter() - t0)
+        log(f"bench: cpu oracle block run {i}: {runs[-1]:.2f} s")
+    t_block = sorted(runs)[len(runs) // 2]
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return dict(value=M / (BLOCKS * t_block), unit="latent tokens/s", cores=cores, kind="port",
+                sample=f"oracle block (CPU restatement, torch {torch.__version__}, fp32/fp64 CPU arithmetic) of "
+                       f"BASELINE config 1: 464-token frame over a 928-token FP8 cache + 512 context tokens, dim 3072; "
+                       f"median of 3 runs = {t_block:.2f} s per block, scaled to a 30-block step; CPU {cpu}")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="time eager launches instead of the HIP graph")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the quantized Wan block hot path runs on a single MI355X; "
+              "--gpus above 1 is not supported in this build", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from wdl import _lib
+
+    _lib.library()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    step = Step(dev)
+    with torch.no_grad():
+        for _ in range(max(1, args.warmup)):
+            step()
+        torch.cuda.synchronize()
+        log("bench: eager warmup done")
+        kernels = instrumented(step)
+        run = step
+        if not args.eager:
+            graph = torch.cuda.CUDAGraph()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                step()
+            torch.cuda.current_stream().wait_stream(s)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph):
+                step()
+            run = graph.replay
+            for _ in range(args.warmup):
+                run()
+            torch.cuda.synchronize()
+            log("bench: graph captured")
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(args.steps):
+            run()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+    log(f"bench: {ms:.3f} ms per step")
+    g = kernels["gemm"]
+    a = kernels["attn"]
+    gemm_frac = g["tops"] / INT8_PEAK_TOPS
+    result = {
+        "metric": "DiT step ms + latent tokens/s at 512x928; W4A4 GEMM TOPS (% of int8 peak)",
+        "value": TOKENS / (ms * 1e-3),
+        "unit": "latent tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4",
+        "data": "synthetic (random-init W4A4 weights of the Wan2.2-TI2V-5B block shapes, random latents, context "
+                "and FP8 cache contents)",
+        "config": {"workload": "Wan2.2-TI2V-5B-shaped DiT step at 512x928: 30 blocks, dim 3072, 24x128 heads, FFN "
+                               "14336, 3-frame chunk of 16x29 = 1392 tokens, 21-frame window = 9744 keys (FP8 KV), "
+                               "512 cross tokens, all block linears W4A4, HIP-graph replay",
+                   "tokens": TOKENS, "keys": CACHED + TOKENS, "context": CONTEXT, "blocks": BLOCKS,
+                   "graph": not args.eager},
+        "gemm_tops": g["tops"],
+        "gemm_pct_int8_peak": 100 * gemm_frac,
+        "gemm_ms_per_step": g["ms"],
+        "attention_tops": a["tops"],
+        "attention_pct_int8_peak": 100 * a["tops"] / INT8_PEAK_TOPS,
+        "attention_ms_per_step": a["ms"],
+        "roofline": {"bound": "mfma", "kernel": "w4a4_gemm_kernel", "achieved": g["tops"], "peak": INT8_PEAK_TOPS,
+                     "unit": "TFLOP/s", "frac": gemm_frac, "traffic": None,
+                     "basis": "2*M*N*K int ops per launch (M = 1392 tokens) summed over the step's "
+                              f"{g['launches']} W4A4 GEMM launches / their summed HIP-event durations"},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

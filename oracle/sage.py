@@ -189,3 +189,32 @@ def entropy_scale(keys: int, head_dim: int, ratio):
     if ratio is None:
         return None
     return math.sqrt(math.log(keys) / math.log(keys * ratio) / head_dim)
+
+
+def attention_online(p: dict, sm_scale: float, block: int = 64) -> torch.Tensor:
+    """The blockwise online-softmax restatement of the HIP kernel's arithmetic (fp32): per 64-key block, s = fp32
+    int dot * k_scale, running max m over s, P = 2^((s - m) * c) with c = q_scale * sm_scale * log2(e), P rounded
+    to e4m3 after * 448, O = O * alpha + P_fp8 . V_fp8 (fp32), l = l * alpha + sum P (unrounded); out =
+    O / (l * 448) * v_scale. Its exp2 is torch's, not the hardware's: P can differ by an ulp before rounding."""
+    q, k = p["q"].float(), p["k"].float()
+    B, n, H, D = q.shape
+    L = k.shape[1]
+    c = (expand_q_scale(p["q_scale"], n).float() * (sm_scale * 1.4426950408889634)).permute(0, 2, 1)  # [B, H, n]
+    ks = expand_k_scale(p["k_scale"], L).float().permute(0, 2, 1)  # [B, H, L]
+    vq = p["v"].float()  # fp8 codes as values [B, L, H, D]
+    m = torch.full((B, H, n), float("-inf"))
+    l = torch.zeros(B, H, n)
+    O = torch.zeros(B, H, n, D)
+    for b0 in range(0, L, block):
+        b1 = min(L, b0 + block)
+        I = torch.einsum("bnhd,blhd->bhnl", q.double(), k[:, b0:b1].double()).float()
+        s = I * ks[:, :, None, b0:b1]
+        mn = torch.maximum(m, s.amax(-1))
+        alpha = torch.exp2((m - mn) * c)
+        P = torch.exp2(s * c[..., None] - (mn * c)[..., None])
+        Pq = (P * 448.0).to(torch.float8_e4m3fn).float()
+        O = O * alpha[..., None] + torch.einsum("bhnl,blhd->bhnd", Pq.double(), vq[:, b0:b1].double()).float()
+        l = l * alpha + P.sum(-1)
+        m = mn
+    out = O / (l * 448.0)[..., None] * p["v_scale"].float()[:, :, None, :]
+    return out.permute(0, 2, 1, 3)

@@ -1,0 +1,185 @@
+"""The quantized Wan block on the HIP path against the oracle block (oracle/block.py).
+
+Bars:
+- small blocks (dim 256, SVD-quantized): bf16 output within max-rel-err 1e-2 and 2^-8 relative L2 of the oracle;
+- config 1 (dim 3072): max-rel-err 1e-2, and relative L2 within 1.5x of the oracle's own change under 50 one-ulp
+  changes of its bf16 input (a random-weight W4A4 block without smoothing is chaotic at that level: one
+  activation-int4 flip moves a whole quantization step; measured in the test);
+- stage by stage at config 1, each HIP stage fed the oracle's own input: 1e-4 relative L2 (linears), 2e-3 with
+  cosine >= 0.99999 (attention);
+- the reference's own contract (tests/test_w4a4.py:62-87): the W4A4 block's update against the float block's,
+  within 5 % of the oracle's own error there and below 0.21 (the reference's 0.2 was stated for exact SDPA; the
+  Sage attention adds about 0.003)."""
+
+import pytest
+import torch
+
+from oracle import block as oblock
+from oracle import rope as orope
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+
+
+def run_pair(dim, heads, ffn, grid, start, prior, Lc, seed, svd=False):
+    from wdl.block import build_block
+    from wdl.kvcache import KVCache
+
+    g = torch.Generator().manual_seed(seed)
+    P = (oblock.quantize_block(oblock.random_block(dim, ffn, g)) if svd
+         else oblock.random_logical_block(dim, ffn, g))
+    M = grid[0] * grid[1] * grid[2]
+    X = torch.randn(M, dim, generator=g)
+    X[:, torch.randperm(dim, generator=g)[: max(1, dim // 100)]] *= 20
+    X = X.to(BF)
+    time_in = torch.randn(6, dim, generator=g) * 0.1
+    C = torch.randn(Lc, dim, generator=g).to(BF)
+    freq = orope.freqs(128, 1024, torch.float64).float()
+    cap = prior + M
+    ck = (torch.randn(1, cap, heads, 128, generator=g) * 100).clamp(-448, 448).to(torch.float8_e4m3fn)
+    cv = (torch.randn(1, cap, heads, 128, generator=g) * 100).clamp(-448, 448).to(torch.float8_e4m3fn)
+    cks = torch.rand(1, cap, heads, 1, generator=g) * 0.02
+    cvs = torch.rand(1, cap, heads, 1, generator=g) * 0.02
+    # oracle
+    ocache = dict(k=ck.clone(), ks=cks.clone(), v=cv.clone(), vs=cvs.clone(), at=prior)
+    ctx_kv = oblock.context_kv(C, P)
+    ref = oblock.block_forward(X, time_in, P, grid, freq, start, ocache, ctx_kv, heads)
+    # HIP path
+    dev = torch.device("cuda")
+    blk = build_block(P, dim, heads, dev)
+    cache = KVCache(prior, 0, chunk=grid[0])
+    cache.allocate(torch.empty(1, M, heads, 128, device=dev))
+    cache.k.copy_(ck.to(dev))
+    cache.v.copy_(cv.to(dev))
+    cache.ks.copy_(cks.to(dev))
+    cache.vs.copy_(cvs.to(dev))
+    cache.saved = prior
+    ctx = blk.prepare_context(C.to(dev))
+    e = (time_in + P["modulation"]).float().to(dev)
+    out = blk.forward(X.to(dev).clone(), e, grid, freq.to(dev), start, cache, ctx)
+    torch.cuda.synchronize()
+    inputs = dict(P=P, time_in=time_in, ctx_kv=ctx_kv, freq=freq, grid=grid, start=start, heads=heads,
+                  cache=dict(k=ck, ks=cks, v=cv, vs=cvs, at=prior))
+    return X, out.cpu(), ref, cache, ocache, inputs
+
+
+def check(tag, out, ref):
+    err = float((out.float() - ref.float()).abs().max()) / float(ref.float().abs().max())
+    rel = float((out.float() - ref.float()).norm() / ref.float().norm())
+    print(f"{tag}: max-rel-err {err:.2e}, rel-L2 {rel:.3e}")
+    assert err <= 1e-2
+    assert rel <= 2 ** -8
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_small_block_matches_oracle(gpu, seed):
+    X, out, ref, cache, ocache, _ = run_pair(256, 2, 1024, (2, 4, 6), 2, 96, 16, seed, svd=True)
+    check(f"seed {seed}", out, ref)
+    # the chunk's K/V went into the cache rows at..at+M: fp8 bytes equal up to bf16 flips upstream
+    at, M = ocache["at"], X.shape[0]
+    same = (cache.k.cpu()[:, at:at + M].view(torch.uint8) == ocache["k"][:, at:at + M].view(torch.uint8))
+    assert float(same.float().mean()) > 0.97
+
+
+def test_baseline_config1_block_matches_oracle(gpu):
+    """dim 3072, 24 x 128 heads, FFN 14336, 464-token frame (16 x 29) at start frame 2 over a
+    928-token FP8 cache (two prior frames), 512 context tokens, random-init W4A4 weights."""
+    X, out, ref, cache, ocache, inp = run_pair(3072, 24, 14336, (1, 16, 29), 2, 928, 512, 7)
+    err = float((out.float() - ref.float()).abs().max()) / float(ref.float().abs().max())
+    rel = float((out.float() - ref.float()).norm() / ref.float().norm())
+    # the oracle against itself with 50 one-ulp input changes
+    Xp = X.clone()
+    flat = Xp.view(-1).view(torch.int16)
+    flat[torch.randperm(flat.numel(), generator=torch.Generator().manual_seed(99))[:50]] += 1
+    pert = oblock.block_forward(Xp, inp["time_in"], inp["P"], inp["grid"], inp["freq"], inp["start"],
+                                dict(inp["cache"]), inp["ctx_kv"], inp["heads"])
+    floor = float((pert.float() - ref.float()).norm() / ref.float().norm())
+    print(f"config 1: max-rel-err {err:.2e}, rel-L2 {rel:.3e} (oracle under 50 one-ulp input changes: {floor:.3e})")
+    assert err <= 1e-2
+    assert rel <= 1.5 * floor
+
+
+def test_w4a4_block_stays_close_to_the_float_block(gpu):
+    """tests/test_w4a4.py:62-87: the fused W4A4 block within 0.2 relative error of the float block, the block's
+    update compared (dim 256, 2 heads, FFN 1024, 2 x 8 x 16 tokens, X ~ N(0, 1), e ~ 0.1 N(0, 1), 16 context
+    tokens, SVD-quantized weights of rank 32, no cache). Here the attention is also quantized (Sage: int8 QK, fp8
+    PV), where the reference's test ran exact SDPA."""
+    from wdl.block import build_block
+    from wdl.kvcache import KVCache
+
+    dim, heads, ffn, grid, Lc = 256, 2, 1024, (2, 8, 16), 16
+    g = torch.Generator().manual_seed(1)
+    B = oblock.random_block(dim, ffn, g, init="torch")
+    P = oblock.quantize_block(B)
+    M = 256
+    X = torch.randn(M, dim, generator=g).to(BF)
+    time_in = torch.randn(6, dim, generator=g) * 0.1
+    C = torch.randn(Lc, dim, generator=g).to(BF)
+    none = torch.zeros(0, dim)
+    freq = orope.freqs(128, 1024, torch.float64).float()
+    ref = oblock.float_block_forward(X, time_in, B, grid, freq, 0, (none, none), C.float(), heads)
+    dev = torch.device("cuda")
+    blk = build_block(P, dim, heads, dev)
+    cache = KVCache(0, 0, chunk=grid[0])
+    out = blk.forward(X.to(dev).clone(), (time_in + P["modulation"]).float().to(dev), grid, freq.to(dev), 0, cache,
+                      blk.prepare_context(C.to(dev))).cpu()
+    upd, rupd = out.float() - X.float(), ref - X.float()
+    err = float((upd - rupd).norm() / rupd.norm())
+    z8 = torch.zeros(1, M, heads, 128, dtype=torch.float8_e4m3fn)
+    zs = torch.ones(1, M, heads, 1)
+    oq = oblock.block_forward(X, time_in, P, grid, freq, 0, dict(k=z8, ks=zs, v=z8.clone(), vs=zs.clone(), at=0),
+                              oblock.context_kv(C, P), heads)
+    oerr = float(((oq.float() - X.float()) - rupd).norm() / rupd.norm())
+    print(f"W4A4 block vs float block: update rel err {err:.3f} (oracle's own: {oerr:.3f})")
+    # the W4A4 scheme itself sits at ~0.2 here (0.195-0.203 with exact attention); the Sage attention adds ~0.003
+    assert err <= 1.05 * oerr and err < 0.21
+
+
+def test_config1_stages_given_identical_inputs(gpu):
+    """Each stage of the config-1 block on the HIP path, fed the oracle's own input for that stage."""
+    from oracle import norms as onorms
+    from oracle import sage as osage
+    from oracle import w4a4 as ow
+    from wdl import ops, sage_kv
+    from wdl.block import build_block
+
+    dev = torch.device("cuda")
+    dim, heads, ffn, M, prior, grid, start = 3072, 24, 14336, 464, 928, (1, 16, 29), 2
+    g = torch.Generator().manual_seed(7)
+    P = oblock.random_logical_block(dim, ffn, g)
+    X = torch.randn(M, dim, generator=g).to(BF)
+    e = (torch.randn(6, dim, generator=g) * 0.1 + P["modulation"]).float()
+    C = torch.randn(512, dim, generator=g).to(BF)
+    freq = orope.freqs(128, 1024, torch.float64).float()
+    ck = (torch.randn(1, prior + M, heads, 128, generator=g) * 100).clamp(-448, 448).to(torch.float8_e4m3fn)
+    cks = torch.rand(1, prior + M, heads, 1, generator=g) * 0.02
+    blk = build_block(P, dim, heads, dev)
+    rel = lambda a, b: float((a.float() - b.float()).norm() / b.float().norm())
+
+    def gpu_lin(x, name, shift=0.0, unsigned=False, epi=0):
+        t = blk.p[name]
+        qa = ops.act_quant_launch(x.to(dev).contiguous(), t["smooth"], t["proj_down"], shift, unsigned)
+        out = torch.empty(x.shape[0], t["qweight"].shape[0], device=dev, dtype=BF)
+        ops.gemm_launch(*qa, t["qweight"], t["wscales"], t["proj_up"], t["bias"], x.shape[0], out, epi)
+        return out.cpu()
+
+    x1 = onorms.ln_mod(X, e[0], e[1])
+    qkv = oblock._lin(x1, P["qkv"]).to(BF)
+    assert rel(gpu_lin(x1, "qkv"), qkv) <= 1e-4
+    D = dim
+    Q = orope.rope_apply(oblock._rms(qkv[:, :D], P["wq"]).reshape(1, -1, heads, 128), grid, freq, start)
+    K = orope.rope_apply(oblock._rms(qkv[:, D:2 * D], P["wk"]).reshape(1, -1, heads, 128), grid, freq, start)
+    V = qkv[:, 2 * D:].reshape(1, -1, heads, 128).contiguous()
+    A = oblock.attention(Q.reshape(-1, D), dict(k=ck, ks=cks, v=ck, vs=cks, at=prior), K.reshape(-1, D),
+                         V.reshape(-1, D), heads)
+    Ag = sage_kv.attend(*(t.to(dev) for t in (Q, ck, cks, ck, cks)), prior, K.to(dev), V.to(dev)).cpu()
+    assert rel(Ag.reshape(M, D), A) <= 2e-3 and osage.cosine(Ag, A) >= 0.99999
+    assert rel(gpu_lin(A, "o"), oblock._lin(A, P["o"]).to(BF)) <= 1e-4
+    xc = onorms.ln_mod(X, None, None, P["n3w"], P["n3b"])
+    assert rel(gpu_lin(xc, "cq"), oblock._lin(xc, P["cq"]).to(BF)) <= 1e-4
+    assert rel(gpu_lin(C, "ck"), oblock._lin(C, P["ck"]).to(BF)) <= 1e-4
+    x2 = onorms.ln_mod(X, e[3], e[4])
+    h = ow.gelu_tanh(oblock._lin(x2, P["ffn1"])).to(BF)
+    assert rel(gpu_lin(x2, "ffn1", epi=3), h) <= 1e-4
+    y2 = oblock._lin(h, P["ffn2"], ow.GELU_SHIFT, True).to(BF)
+    assert rel(gpu_lin(h, "ffn2", ow.GELU_SHIFT, True), y2) <= 1e-4

@@ -1,0 +1,130 @@
+"""The quantized Wan DiT block and the 30-block step on MI355X, over the wdl kernels.
+
+WanBlock.forward (src/wan_dit_lab/models/block.py:22-29) with the W4A4 layers installed as the reference's fused
+pack installs them (quantization/w4a4.py:336-352: self_attn.qkv FusedQKVAttention, ffn PackedW4A4GeluMLP, every
+other linear PackedW4A4Linear) and the FP8 KV cache attended through Sage (generation/causal.py:193-210). The
+kernel sequence of one block (about 21 launches, all on the current stream, capturable into one HIP graph):
+
+  act_quant(X; LN + (1 + scale_a), + shift_a)  -> W4A4 qkv -> norm_rope(q, k) -> kv_append(K, V @ at)
+  -> sage_prep(cache[:at] ++ K, V) -> quant_q(Q) -> sage_attn -> act_quant(A) -> W4A4 o  (X += gate_a * y, fused)
+  act_quant(X; LN3 affine) -> W4A4 cross q -> RMSNorm -> quant_q -> sage_attn(context K/V, prepared once per
+  prompt) -> act_quant -> W4A4 cross o (X += y, fused)
+  act_quant(X; LN + (1 + scale_f), + shift_f) -> W4A4 ffn.0 (GELU epilogue) -> act_quant((h + 0.171875) / s2,
+  unsigned) -> W4A4 ffn.2 (X += gate_f * y, fused)
+
+X is updated in place (a bf16 [M, dim] buffer owned by the caller).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from wdl import ops
+from wdl.kvcache import KVCache
+from wdl.ops import EPI_BF16, EPI_GELU, EPI_RESIDUAL, GELU_SHIFT
+
+LINEARS = ("qkv", "o", "cq", "ck", "cv", "co", "ffn1", "ffn2")
+
+
+class QuantizedWanBlock:
+    """parts: {linear: packed W4A4 parts (w4a4.quantize / pack_parts)} for LINEARS, plus wq, wk, cwq, cwk (bf16
+    RMSNorm weights [dim]), n3w, n3b (fp32 LayerNorm-3 affine [dim]) and modulation (fp32 [6, dim])."""
+
+    def __init__(self, parts: dict, dim: int, heads: int, eps: float = 1e-6):
+        self.p, self.dim, self.heads, self.eps = parts, dim, heads, eps
+        dev = parts["qkv"]["qweight"].device
+        self.ones = torch.ones(dim, device=dev, dtype=torch.float32)
+
+    # --------------------------------------------------------------------------------------- pieces
+    def _quant(self, x, name, ln=None, shift=0.0, unsigned=False):
+        t = self.p[name]
+        return ops.act_quant_launch(x, t["smooth"], t["proj_down"], shift, unsigned, ln=ln)
+
+    def _gemm(self, qa, name, M, out, epilogue=EPI_BF16, gate=None):
+        t = self.p[name]
+        q, asc, lora = qa
+        return ops.gemm_launch(q, asc, lora, t["qweight"], t["wscales"], t["proj_up"], t["bias"], M, out, epilogue,
+                               gate)
+
+    def linear(self, x, name):
+        out = torch.empty(x.shape[0], self.p[name]["qweight"].shape[0], device=x.device, dtype=torch.bfloat16)
+        return self._gemm(self._quant(x, name), name, x.shape[0], out)
+
+    def prepare_context(self, C: torch.Tensor) -> dict:
+        """Cross-attention keys and values of a prompt, once per prompt (multi_head_attention.py:21-26;
+        causal.Stream.cross, causal.py:557-568): K = RMSNorm(k(C)), V = v(C), then Sage's int8 K / fp8 V."""
+        Kc = self.linear(C, "ck")
+        Kn, _ = ops.qk_norm_rope_launch(Kc, Kc, self.p["cwk"], self.p["cwk"], self._nofreq(C.device), (0, 1, 1), 0,
+                                        self.eps)
+        Vc = self.linear(C, "cv")
+        H = self.heads
+        z8 = torch.zeros(1, 1, H, 128, device=C.device, dtype=torch.uint8)
+        z = torch.ones(1, 1, H, 1, device=C.device)
+        prep = ops.sage_prep_launch(z8, z, z8, z, Kn, Vc, 0)
+        prep["L"] = C.shape[0]
+        return prep
+
+    def _nofreq(self, device):
+        if not hasattr(self, "_zero_freq"):
+            self._zero_freq = torch.zeros(2, 1, 64, device=device)
+        return self._zero_freq
+
+    # --------------------------------------------------------------------------------------- forward
+    def forward(self, X: torch.Tensor, e: torch.Tensor, grid, freq, start_frame: int, cache: KVCache, ctx: dict):
+        """X bf16 [M, dim] (updated in place and returned); e fp32 [6, dim] = time_in + modulation."""
+        M, D = X.shape
+        H = self.heads
+        sh_a, sc_a, g_a, sh_f, sc_f, g_f = e
+        dev = X.device
+        # self-attention
+        qkv = torch.empty(M, 3 * D, device=dev, dtype=torch.bfloat16)
+        self._gemm(self._quant(X, "qkv", ln=dict(shift=sh_a, scale=sc_a, eps=self.eps)), "qkv", M, qkv)
+        Q, K = ops.qk_norm_rope_launch(qkv[:, :D], qkv[:, D:2 * D], self.p["wq"], self.p["wk"], freq, grid,
+                                       start_frame, self.eps)
+        V = qkv[:, 2 * D:]
+        A = cache.attend(Q.view(1, M, H, 128), K.view(1, M, H, 128), V.view(1, M, H, 128))
+        self._gemm(self._quant(A.view(M, D), "o"), "o", M, X, EPI_RESIDUAL, g_a)
+        # cross-attention over the prompt
+        qc = torch.empty(M, D, device=dev, dtype=torch.bfloat16)
+        n3 = dict(weight=self.p["n3w"], bias=self.p["n3b"], eps=self.eps)
+        self._gemm(self._quant(X, "cq", ln=n3), "cq", M, qc)
+        Qc, _ = ops.qk_norm_rope_launch(qc, qc, self.p["cwq"], self.p["cwq"], self._nofreq(dev), (0, 1, 1), 0,
+                                        self.eps)
+        q_i8, q_sc = ops.quant_q_launch(Qc, H)
+        Ac = ops.sage_attn_launch(q_i8, q_sc, ctx, ctx["L"], 128 ** -0.5)
+        self._gemm(self._quant(Ac, "co"), "co", M, X, EPI_RESIDUAL, self.ones)
+        # feed forward (W4A4 GELU MLP)
+        h = torch.empty(M, self.p["ffn1"]["qweight"].shape[0], device=dev, dtype=torch.bfloat16)
+        self._gemm(self._quant(X, "ffn1", ln=dict(shift=sh_f, scale=sc_f, eps=self.eps)), "ffn1", M, h, EPI_GELU)
+        self._gemm(self._quant(h, "ffn2", shift=GELU_SHIFT, unsigned=True), "ffn2", M, X, EPI_RESIDUAL, g_f)
+        return X
+
+
+def build_block(P_logical: dict, dim: int, heads: int, device) -> QuantizedWanBlock:
+    """A QuantizedWanBlock from the logical parts of oracle-style quantization (tests) or of quantize_block."""
+    from wdl.w4a4 import pack_parts
+
+    parts = {name: pack_parts(P_logical[name], device) for name in LINEARS}
+    for name in ("wq", "wk", "cwq", "cwk"):
+        parts[name] = P_logical[name].to(torch.bfloat16).to(device)
+    parts["n3w"] = P_logical["n3w"].float().to(device)
+    parts["n3b"] = P_logical["n3b"].float().to(device)
+    parts["modulation"] = P_logical["modulation"].float().to(device)
+    return QuantizedWanBlock(parts, dim, heads)
+
+
+def random_block(dim: int, ffn: int, heads: int, device, generator=None) -> QuantizedWanBlock:
+    """A block of random-init W4A4 weights of the Wan architecture (no SVD: random int4, group scales of an
+    N(0, 0.02^2) weight, small low-rank factors), for the step benchmark."""
+    from wdl.w4a4 import random_parts
+
+    g = generator
+    shapes = dict(qkv=(3 * dim, dim), o=(dim, dim), cq=(dim, dim), ck=(dim, dim), cv=(dim, dim), co=(dim, dim),
+                  ffn1=(ffn, dim), ffn2=(dim, ffn))
+    parts = {name: random_parts(n, k, device, g) for name, (n, k) in shapes.items()}
+    for name in ("wq", "wk", "cwq", "cwk"):
+        parts[name] = torch.ones(dim, device=device, dtype=torch.bfloat16)
+    parts["n3w"] = torch.ones(dim, device=device)
+    parts["n3b"] = torch.zeros(dim, device=device)
+    parts["modulation"] = torch.randn(6, dim, generator=g, device=device) / dim ** 0.5
+    return QuantizedWanBlock(parts, dim, heads)

@@ -109,16 +109,17 @@ def quantize(weight, bias=None, smooth=None, rank: int = 32, shift: float = 0.0,
 def random_parts(N: int, K: int, device, generator=None, rank: int = 32, scale: float = 0.02, unsigned_input=False):
     """A W4A4 layer of the right shapes and value ranges without an SVD (random-init weights of the architecture,
     for the step benchmark): int4 in [-7, 7], group scales of a N(0, scale^2) weight, small low-rank factors."""
-    g = generator
-    q = torch.randint(-7, 8, (N, K), generator=g, device="cpu", dtype=torch.int32)
-    wsc = (torch.rand(K // GROUP, N, generator=g) * 0.5 + 0.75) * (3 * scale / 7)
+    g = generator  # a generator on `device` (or None: the global one of that device)
+    kw = dict(generator=g, device=device)
+    q = torch.randint(-7, 8, (N, K), dtype=torch.int32, **kw)
+    wsc = (torch.rand(K // GROUP, N, **kw) * 0.5 + 0.75) * (3 * scale / 7)
     return dict(
-        qweight=pack_weight(q).to(device),
-        wscales=wsc.to(torch.bfloat16).to(device),
-        proj_down=(torch.randn(rank, K, generator=g) * (1 / K ** 0.5)).to(torch.bfloat16).to(device),
-        proj_up=(torch.randn(N, rank, generator=g) * scale).to(torch.bfloat16).to(device),
+        qweight=pack_weight(q),
+        wscales=wsc.to(torch.bfloat16),
+        proj_down=(torch.randn(rank, K, **kw) * (1 / K ** 0.5)).to(torch.bfloat16),
+        proj_up=(torch.randn(N, rank, **kw) * scale).to(torch.bfloat16),
         smooth=torch.ones(K, dtype=torch.bfloat16, device=device),
-        bias=(torch.randn(N, generator=g) * scale).to(torch.bfloat16).to(device),
+        bias=(torch.randn(N, **kw) * scale).to(torch.bfloat16),
     )
 
 
@@ -156,3 +157,23 @@ class PackedW4A4GeluMLP(torch.nn.Module):
     def forward(self, X):
         y = w4a4_gelu_mlp(X.reshape(-1, X.shape[-1]).to(torch.bfloat16).contiguous(), *self.parts)
         return y.reshape(*X.shape[:-1], self.out_features)
+
+
+def pack_parts(logical: dict, device=None) -> dict:
+    """Logical parts (q int [N, K], wscales [N, K/64], proj_down [K, r], proj_up [N, r], smooth [K], bias [N]) ->
+    this build's packed layout, on `device`."""
+    return dict(
+        qweight=pack_weight(logical["q"]).to(device),
+        wscales=logical["wscales"].to(torch.bfloat16).t().contiguous().to(device),
+        proj_down=logical["proj_down"].to(torch.bfloat16).t().contiguous().to(device),
+        proj_up=logical["proj_up"].to(torch.bfloat16).contiguous().to(device),
+        smooth=logical["smooth"].to(torch.bfloat16).to(device),
+        bias=logical["bias"].to(torch.bfloat16).to(device),
+    )
+
+
+def unpack_parts(parts: dict) -> dict:
+    """Inverse of pack_parts, on the CPU."""
+    return dict(q=unpack_weight(parts["qweight"].cpu()), wscales=parts["wscales"].cpu().t().contiguous(),
+                proj_down=parts["proj_down"].cpu().t().contiguous(), proj_up=parts["proj_up"].cpu(),
+                smooth=parts["smooth"].cpu(), bias=parts["bias"].cpu())
