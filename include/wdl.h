@@ -40,6 +40,9 @@ int wdl_kv_append_fp8(const void* k, int k_dtype, const int64_t* k_strides, cons
                       float* cache_ks, void* cache_v, float* cache_vs, int64_t capacity, int64_t at,
                       wdl_stream_t stream);
 
+/* Workspace (in floats) that wdl_act_quant_w4 needs for Mp padded rows of K values. */
+int64_t wdl_act_quant_workspace_floats(int64_t Mp, int64_t K);
+
 /* W4A4 activation quantizer (+ low-rank down projection, + optional fused LayerNorm and adaLN modulation).
  * Replaces Nunchaku's quantize_w4a4_act_fuse_lora behind live::w4a4_linear (native/ops/w4a4_ops.cpp:17-29; the
  * quantizer itself is absent from the reference tree) and the norm/modulation of WanBlock.forward
@@ -48,11 +51,13 @@ int wdl_kv_append_fp8(const void* k, int k_dtype, const int64_t* k_strides, cons
  * v = x, or with ln != 0: v = bf16(LN(x)[*ln_w + ln_b] * (1 + mod_scale) + mod_shift) (fp32 vectors, NULL = absent).
  * u = (v + qshift) / smooth; per row and 64-group: scale = bf16(max|u| / qmax) (qmax 7, or 15 if unsigned_q),
  * q = clamp(rint(u / scale)). Outputs: q as e4m3 codes of the integers [Mp, K]; ascales bf16 [K/64, Mp];
- * lora fp32 [Mp, 32] = v . proj_down; rows M..Mp-1 zero. Mp % 32 == 0. v_out (bf16 [M, K]) optional copy of v. */
+ * lora fp32 [Mp, 32] = v . proj_down; rows M..Mp-1 zero. Mp % 32 == 0. v_out (bf16 [M, K]) optional copy of v.
+ * LayerNorm statistics: lane l of a wave owns the 8-value chunks l, l+64, ..., summed value by value, the 64 lane
+ * sums combined by an xor butterfly 32..1 (the oracle's order). workspace: wdl_act_quant_workspace_floats(Mp, K). */
 int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K, const void* smooth, float qshift,
                      int unsigned_q, const void* proj_down_t, int64_t rank, void* q, void* ascales, float* lora,
                      int64_t Mp, const float* mod_shift, const float* mod_scale, const float* ln_w,
-                     const float* ln_b, int ln, float eps, void* v_out, wdl_stream_t stream);
+                     const float* ln_b, int ln, float eps, void* v_out, float* workspace, wdl_stream_t stream);
 
 /* W4A4 GEMM with fused dequantization, low-rank up projection and bias. Replaces Nunchaku's gemm_w4a4 behind
  * live::w4a4_linear and live::w4a4_gelu_mlp (native/ops/w4a4_ops.cpp:36-38, 55-61).

@@ -3,9 +3,10 @@ src/wan_dit_lab/models/layer_norm.py:4-7, rms_norm.py:4-13 and the modulation of
 
 The reference computes these in fp32 through torch (whose reduction order is its own); this oracle fixes one
 order so the fused HIP kernels can be pinned bit-exactly to it:
-- a row of K values is split into 8 column slots; slot c owns columns g*64 + c*8 + j (g over groups, j = 0..7)
-  and sums them sequentially, g outer, j inner, in fp32;
-- the 8 slot sums are combined by the butterfly s[i] + s[i^4], then ^2, then ^1 (fp32);
+- a row of K values is cut into chunks of 8 (chunk c = values 8c .. 8c+7); lane l of a 64-lane wave owns the
+  chunks c = l, l + 64, l + 128, ... and adds their values into one fp32 running sum, chunk by chunk, value by
+  value;
+- the 64 lane sums are combined by the butterfly s[i] + s[i^32], then ^16, ^8, ^4, ^2, ^1 (fp32);
 - mean = sum / K; var = sum((x - mean)^2) / K by the same order; rstd = 1 / sqrt(var + eps) (IEEE sqrt, IEEE div);
 - LayerNorm: (x - mean) * rstd [* w + b]; modulation: n * (1 + scale) + shift in fp32; one bf16 rounding at the end
   (the bf16 activation the reference feeds its W4A4 linear, w4a4.py:230).
@@ -13,7 +14,7 @@ order so the fused HIP kernels can be pinned bit-exactly to it:
   (rms_norm.py:12-13).
 
 Pinned by the closed form: in float64 the same functions agree with torch.nn.functional.layer_norm / the RMSNorm
-formula to fp32 rounding (tests/test_oracle_norms.py), and the reduction order is checked against an independent
+formula to fp32 rounding (tests/test_oracle_w4a4.py), and the reduction order is checked against an independent
 scalar loop.
 """
 
@@ -22,21 +23,25 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-SLOTS = 8
+LANES = 64
 VEC = 8
 
 
 def _ordered_sum(x: np.ndarray) -> np.ndarray:
-    """x float32 [M, K] -> float32 [M] in the order described above."""
+    """x float32 [M, K] (K a multiple of 8) -> float32 [M] in the order described above (a lane owning no chunk,
+    or a chunk past the row, adds +0, which leaves a running sum started at +0 unchanged)."""
     M, K = x.shape
-    G = K // (SLOTS * VEC)
-    x = x.reshape(M, G, SLOTS, VEC)
-    s = np.zeros((M, SLOTS), dtype=np.float32)
-    for g in range(G):
+    pad = (-K) % (LANES * VEC)
+    if pad:
+        x = np.concatenate([x, np.zeros((M, pad), dtype=np.float32)], axis=1)
+        K += pad
+    x = x.reshape(M, K // (LANES * VEC), LANES, VEC)
+    s = np.zeros((M, LANES), dtype=np.float32)
+    for i in range(x.shape[1]):
         for j in range(VEC):
-            s = (s + x[:, g, :, j]).astype(np.float32)
-    for o in (4, 2, 1):
-        s = (s + s[:, np.arange(SLOTS) ^ o]).astype(np.float32)
+            s = (s + x[:, i, :, j]).astype(np.float32)
+    for o in (32, 16, 8, 4, 2, 1):
+        s = (s + s[:, np.arange(LANES) ^ o]).astype(np.float32)
     return s[:, 0]
 
 

@@ -106,19 +106,19 @@ def test_int4_groups_host_equals_oracle():
 
 def test_ordered_row_sum_equals_scalar_loop():
     g = torch.Generator().manual_seed(6)
-    x = (torch.randn(3, 256, generator=g) * 10).numpy().astype(np.float32)
+    x = (torch.randn(3, 1024, generator=g) * 10).numpy().astype(np.float32)
     got = onorms._ordered_sum(x)
     for r in range(3):
-        slots = []
-        for c in range(8):
+        lanes = []
+        for lane in range(64):
             s = np.float32(0)
-            for gi in range(256 // 64):
+            for c in range(lane, 1024 // 8, 64):
                 for j in range(8):
-                    s = np.float32(s + x[r, gi * 64 + c * 8 + j])
-            slots.append(s)
-        for o in (4, 2, 1):
-            slots = [np.float32(slots[i] + slots[i ^ o]) for i in range(8)]
-        assert got[r] == slots[0]
+                    s = np.float32(s + x[r, 8 * c + j])
+            lanes.append(s)
+        for o in (32, 16, 8, 4, 2, 1):
+            lanes = [np.float32(lanes[i] + lanes[i ^ o]) for i in range(64)]
+        assert got[r] == lanes[0]
 
 
 def test_ln_mod_and_rms_close_to_torch():

@@ -1,10 +1,11 @@
 // Q/K RMSNorm over the whole row (all heads) and 3D RoPE, fused, plus Sage's per-thread int8 quantization of Q.
 //
-// qk_norm_rope: for each token row m of q and k (bf16, row strides ldq / ldk, H heads of D = 128):
-//   n   = bf16(x * rstd),   rstd = 1 / sqrt(mean(x^2) + eps)   (fp32; ordered sum: 8 column slots per row,
-//         each summing its 8-wide chunks group by group, then an xor butterfly 4, 2, 1)
-//   w   = bf16(n * weight)                                      (RMSNorm, models/rms_norm.py:12-13)
-//   rot = bf16(x1 c - x2 s), bf16(x2 c + x1 s) on pairs (2p, 2p+1) (models/rope.py:26-31, fp32 math)
+// qk_norm_rope: one wave per (row m, q or k), the row held in registers (bf16, row strides ldq / ldk, H heads of
+// D = 128, H * D <= 4096):
+//   rstd = 1 / sqrt(mean(x^2) + eps)     fp32; ordered sum: lane l owns the 8-value chunks c = l, l + 64, ... and
+//                                       adds their squares value by value, then an xor butterfly 32, 16, .., 1
+//   n   = bf16(x * rstd);  w = bf16(n * weight)                                (models/rms_norm.py:12-13)
+//   rot = bf16(w1 c - w2 s), bf16(w2 c + w1 s) on pairs (2p, 2p+1)             (models/rope.py:26-31, fp32)
 // with pair p of a head on the time axis for p < 22, height for p < 43, width otherwise; the token's position is
 // (start_frame + m / (h w), (m / w) % h, m % w) and (c, s) = freq[0/1][position][p] (fp32 table [2, P, 64]).
 // Rows m >= f h w (padding) are normalized but not rotated. Outputs are bf16 [M, H*D] (row stride ldo).
@@ -17,7 +18,7 @@ namespace {
 
 using namespace wdl;
 
-constexpr int ROWS = 32;
+constexpr int MAXCH = 8;
 
 struct NormRopeArgs {
     const uint16_t* q;
@@ -46,78 +47,70 @@ __device__ __forceinline__ void load8(const uint16_t* p, float* f) {
     }
 }
 
-__device__ __forceinline__ float rowsum8(float s) {
-    s = s + __shfl_xor(s, 4, 8);
-    s = s + __shfl_xor(s, 2, 8);
-    s = s + __shfl_xor(s, 1, 8);
-    return s;
-}
-
-__device__ __forceinline__ float rms_rstd(const uint16_t* row, int G, int slot, bool live, int64_t C, float eps) {
-    float s = 0.0f;
-    for (int g = 0; g < G; ++g) {
-        float f[8];
-        if (live) load8(row + g * 64 + slot * 8, f);
-        else
-            for (int j = 0; j < 8; ++j) f[j] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) s = s + f[j] * f[j];
-    }
-    s = rowsum8(s);
-    return 1.0f / sqrtf(s / float(C) + eps);
-}
-
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs a) {
-    const int t = threadIdx.x, slot = t % 8;
-    const int64_t row = int64_t(blockIdx.x) * ROWS + t / 8;
-    const bool live = row < a.M;
-    const int G = int(a.C / 64);
+    const int lane = threadIdx.x % 64;
+    const int64_t item = int64_t(blockIdx.x) * 4 + threadIdx.x / 64;  // (row, which)
+    if (item >= 2 * a.M) return;
+    const int64_t row = item / 2;
+    const int which = int(item % 2);
+    const uint16_t* src = (which == 0 ? a.q : a.k) + row * (which == 0 ? a.ldq : a.ldk);
+    const uint16_t* wt = which == 0 ? a.wq : a.wk;
+    uint16_t* dst = (which == 0 ? a.qo : a.ko) + row * a.ldo;
+    const int64_t chunks = a.C / 8;
+    float x[MAXCH][8];
+#pragma unroll
+    for (int i = 0; i < MAXCH; ++i) {
+        const int64_t c = lane + 64 * i;
+        if (c < chunks) load8(src + c * 8, x[i]);
+        else
+            for (int j = 0; j < 8; ++j) x[i][j] = 0.0f;
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MAXCH; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s = s + x[i][j] * x[i][j];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s = s + __shfl_xor(s, o);
+    const float rstd = 1.0f / sqrtf(s / float(a.C) + a.eps);
     const int64_t hw = int64_t(a.h) * a.w;
-    const bool rot = live && row < int64_t(a.f) * hw;
-    const int pos_t = a.start + int(row / (hw > 0 ? hw : 1));
-    const int pos_h = hw > 0 ? int((row / a.w) % a.h) : 0;
-    const int pos_w = hw > 0 ? int(row % a.w) : 0;
-    const int half = 64;  // pairs per head (D = 128)
-    const int tpairs = half - 2 * (half / 3);  // 22
-    const int spairs = half / 3;                // 21
-    for (int which = 0; which < 2; ++which) {
-        const uint16_t* src = which == 0 ? a.q : a.k;
-        const int64_t ld = which == 0 ? a.ldq : a.ldk;
-        const uint16_t* wt = which == 0 ? a.wq : a.wk;
-        uint16_t* dst = which == 0 ? a.qo : a.ko;
-        const uint16_t* rp = src + (live ? row : 0) * ld;
-        const float rstd = rms_rstd(rp, G, slot, live, a.C, a.eps);
-        if (!live) continue;
-        for (int g = 0; g < G; ++g) {
-            const int64_t col = int64_t(g) * 64 + slot * 8;
-            float x[8];
-            load8(rp + col, x);
-            float y[8];
+    const bool rot = row < int64_t(a.f) * hw;
+    const int pos_t = a.start + int(row / hw);
+    const int pos_h = int((row / a.w) % a.h);
+    const int pos_w = int(row % a.w);
+    constexpr int half = 64, tpairs = half - 2 * (half / 3), spairs = half / 3;  // 22, 21
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float n = bf16_to_f32(f32_to_bf16(x[j] * rstd));
-                y[j] = bf16_to_f32(f32_to_bf16(n * bf16_to_f32(wt[col + j])));
-            }
-            uint16_t o[8];
+    for (int i = 0; i < MAXCH; ++i) {
+        const int64_t c = lane + 64 * i;
+        if (c >= chunks) break;
+        const int64_t col = c * 8;
+        float wf[8];
+        load8(wt + col, wf);
+        float y[8];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float x1 = y[2 * i], x2 = y[2 * i + 1];
-                if (rot) {
-                    const int p = int((col + 2 * i) % 128) / 2;
-                    const int pos = p < tpairs ? pos_t : (p < tpairs + spairs ? pos_h : pos_w);
-                    const float c = a.freq[(int64_t(pos)) * half + p];
-                    const float s = a.freq[(a.P + pos) * half + p];
-                    o[2 * i] = f32_to_bf16(x1 * c - x2 * s);
-                    o[2 * i + 1] = f32_to_bf16(x2 * c + x1 * s);
-                } else {
-                    o[2 * i] = f32_to_bf16(x1);
-                    o[2 * i + 1] = f32_to_bf16(x2);
-                }
-            }
-            *reinterpret_cast<uint4*>(dst + row * a.ldo + col) =
-                make_uint4(o[0] | (uint32_t(o[1]) << 16), o[2] | (uint32_t(o[3]) << 16), o[4] | (uint32_t(o[5]) << 16),
-                           o[6] | (uint32_t(o[7]) << 16));
+        for (int j = 0; j < 8; ++j) {
+            const float n = bf16_to_f32(f32_to_bf16(x[i][j] * rstd));
+            y[j] = bf16_to_f32(f32_to_bf16(n * wf[j]));
         }
+        uint16_t o[8];
+#pragma unroll
+        for (int p2 = 0; p2 < 4; ++p2) {
+            const float x1 = y[2 * p2], x2 = y[2 * p2 + 1];
+            if (rot) {
+                const int p = int((col + 2 * p2) % 128) / 2;
+                const int pos = p < tpairs ? pos_t : (p < tpairs + spairs ? pos_h : pos_w);
+                const float cs = a.freq[int64_t(pos) * half + p];
+                const float sn = a.freq[(a.P + pos) * half + p];
+                o[2 * p2] = f32_to_bf16(x1 * cs - x2 * sn);
+                o[2 * p2 + 1] = f32_to_bf16(x2 * cs + x1 * sn);
+            } else {
+                o[2 * p2] = f32_to_bf16(x1);
+                o[2 * p2 + 1] = f32_to_bf16(x2);
+            }
+        }
+        *reinterpret_cast<uint4*>(dst + col) =
+            make_uint4(o[0] | (uint32_t(o[1]) << 16), o[2] | (uint32_t(o[3]) << 16), o[4] | (uint32_t(o[5]) << 16),
+                       o[6] | (uint32_t(o[7]) << 16));
     }
 }
 
@@ -184,6 +177,7 @@ extern "C" int wdl_qk_norm_rope(const void* q, int64_t ldq, const void* k, int64
     if (start_frame + f > positions || h > positions || w > positions)
         return fail(WDL_EINVAL, "qk_norm_rope: grid or offset exceeds the frequency table");
     if (!q || !k || !wq || !wk || !freq || !q_out || !k_out) return fail(WDL_EINVAL, "qk_norm_rope: null pointer");
+    if (C > 64 * 8 * MAXCH) return fail(WDL_EINVAL, "qk_norm_rope: rows above 4096 values");
     if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(q_out) |
          reinterpret_cast<uintptr_t>(k_out) | (ldq * 2) | (ldk * 2) | (ldo * 2)) % 16)
         return fail(WDL_EINVAL, "qk_norm_rope: rows must be 16-byte aligned");
@@ -191,7 +185,7 @@ extern "C" int wdl_qk_norm_rope(const void* q, int64_t ldq, const void* k, int64
     NormRopeArgs a{static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(k), ldk,
                    static_cast<const uint16_t*>(wq), static_cast<const uint16_t*>(wk), freq, positions, M, C,
                    f, h, w, start_frame, eps, static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_out), ldo};
-    qk_norm_rope_kernel<<<unsigned((M + ROWS - 1) / ROWS), 256, 0, stream>>>(a);
+    qk_norm_rope_kernel<<<unsigned((2 * M + 3) / 4), 256, 0, stream>>>(a);
     return check_launch("qk_norm_rope");
 }
 

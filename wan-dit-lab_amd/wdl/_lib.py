@@ -23,8 +23,9 @@ SIGNATURES: dict[str, list] = {
     "wdl_abi_version": [],
     "wdl_kv_append_fp8": [c_ptr, c_int, c_i64p, c_ptr, c_int, c_i64p, c_i64, c_i64, c_i64, c_i64,
                           c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_ptr],
+    "wdl_act_quant_workspace_floats": [c_i64, c_i64],
     "wdl_act_quant_w4": [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_f32, c_int, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_i64,
-                         c_ptr, c_ptr, c_ptr, c_ptr, c_int, c_f32, c_ptr, c_ptr],
+                         c_ptr, c_ptr, c_ptr, c_ptr, c_int, c_f32, c_ptr, c_ptr, c_ptr],
     "wdl_w4a4_gemm": [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_ptr,
                       c_i64, c_int, c_ptr, c_ptr],
     "wdl_qk_norm_rope": [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_int, c_int, c_int,
@@ -36,7 +37,8 @@ SIGNATURES: dict[str, list] = {
     "wdl_sage_attn": [c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_f32, c_ptr, c_i64,
                       c_ptr],
 }
-RESTYPES = {"wdl_last_error": ctypes.c_char_p, "wdl_sage_prep_workspace_floats": c_i64}
+RESTYPES = {"wdl_last_error": ctypes.c_char_p, "wdl_sage_prep_workspace_floats": c_i64,
+            "wdl_act_quant_workspace_floats": c_i64}
 
 _LIB = None
 

@@ -64,10 +64,11 @@ def act_quant_launch(x, smooth, proj_down_t, qshift=0.0, unsigned=False, *, ln=N
     ascales = torch.empty(K // 64, Mp, device=x.device, dtype=torch.bfloat16)
     lora = None if proj_down_t is None else torch.empty(Mp, RANK, device=x.device, dtype=torch.float32)
     ln = ln or {}
+    ws = torch.empty(_lib.library().wdl_act_quant_workspace_floats(Mp, K), device=x.device, dtype=torch.float32)
     _lib.call("wdl_act_quant_w4", ptr(x), x.stride(0), M, K, ptr(smooth), float(qshift), int(unsigned),
               ptr(proj_down_t), RANK, ptr(q), ptr(ascales), ptr(lora), Mp, ptr(ln.get("shift")), ptr(ln.get("scale")),
               ptr(ln.get("weight")), ptr(ln.get("bias")), int(bool(ln)), float(ln.get("eps", 1e-6)), ptr(v_out),
-              stream_of(x))
+              ptr(ws), stream_of(x))
     return q, ascales, lora
 
 
