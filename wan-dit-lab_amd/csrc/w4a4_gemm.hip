@@ -65,63 +65,120 @@ __device__ __forceinline__ uint32_t nib4_to_e4m3(uint32_t x) {
     return (neg & mask) | (pos & ~mask);
 }
 
-template <int BN, int BM, int WN, int WM, int EPI>
-__global__ __launch_bounds__(256) void w4a4_gemm_kernel(GemmArgs p) {
-    static_assert((BN / WN) * (BM / WM) == 4, "4 waves");
-    constexpr int TN = WN / 32, TM = WM / 32;
-    __shared__ __attribute__((aligned(16))) uint8_t sW[2][BN * PADK];
-    __shared__ __attribute__((aligned(16))) uint8_t sX[2][BM * PADK];
-    __shared__ uint16_t sWs[2][BN];
-    __shared__ uint16_t sAs[2][BM];
+// Tile BN (features) x BM (tokens), NW waves in a (BN / WN) x (BM / WM) grid. Per 64-deep group the workgroup
+// needs the activation codes [BM][64 B], the weight nibbles [BN][32 B] and the scales ws[BN], as[BM]; all three
+// stream straight from global memory into a 4-stage LDS ring with global_load_lds (lane-linear in LDS: 16 bytes
+// per lane for codes and nibbles, 4 for scales), issued 3 groups ahead, so no staging registers are involved.
+// Every wave issues the same number of these loads per group, so each wave's vmcnt names exactly the groups still
+// in flight; the loads are written as inline asm so that the compiler's own wait insertion, which cannot tell the
+// ring stages apart, does not add vmcnt(0) waits in front of every LDS read. Activation rows sit in LDS with their
+// four 16-byte quarters XOR-swizzled by (row / 4) % 4 (conflict-free operand reads). One group ahead of the
+// multiply, each thread turns its share of the raw nibbles into e4m3 codes in a double-buffered code tile.
+// Workgroup ids are remapped so that the tiles of one weight slab run on one XCD.
+constexpr int STAGES = 4;
 
-    const int t = threadIdx.x, lane = t % 64, wave = t / 64;
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return uint32_t(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
+}
+
+// 64 lanes x 16 bytes from per-lane global addresses to LDS [m0, m0 + 1024)
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds) : "memory");
+}
+// 64 lanes x 4 bytes to LDS [m0, m0 + 256)
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
+    asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds) : "memory");
+}
+
+// s_waitcnt vmcnt(n) only (expcnt and lgkmcnt left at their maxima)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int BN, int BM, int WN, int WM, int NW, int EPI>
+__global__ __launch_bounds__(NW * 64) void w4a4_gemm_kernel(GemmArgs p) {
+    static_assert((BN / WN) * (BM / WM) == NW, "wave grid");
+    static_assert(STAGES == 4, "the main loop is unrolled by 4 stages");
+    constexpr int NT = NW * 64;
+    constexpr int TN = WN / 32, TM = WM / 32;
+    constexpr int XI = BM * 4 / 64 / NW;   // 16-byte loads per wave per group: activation codes
+    constexpr int WI = BN * 2 / 64 / NW;   // and raw weight nibbles
+    constexpr int LPG = XI + WI + 1;       // + one 4-byte load of scales: loads per wave per group
+    constexpr int SB = NW * 256;           // scale bytes per stage (ws[BN], as[BM], then padding)
+    static_assert(XI >= 1 && WI >= 1 && BM * 4 == XI * 64 * NW && BN * 2 == WI * 64 * NW, "tile vs waves");
+    static_assert(2 * (BN + BM) <= SB, "scale stage");
+    __shared__ __attribute__((aligned(1024))) uint8_t sX[STAGES][BM * 64];
+    __shared__ __attribute__((aligned(1024))) uint8_t sR[STAGES][BN * 32];
+    __shared__ __attribute__((aligned(256))) uint8_t sS[STAGES][SB];
+    __shared__ __attribute__((aligned(16))) uint8_t sW[2][BN * PADK];
+
+    const int t = threadIdx.x, lane = t % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(t / 64);
     const int wn = wave % (BN / WN), wm = wave / (BN / WN);
-    const int64_t n0 = int64_t(blockIdx.x) * BN, m0 = int64_t(blockIdx.y) * BM;
+    const int64_t ntn = p.N / BN, ntm = p.Mp / BM, total = ntn * ntm;
+    const int64_t pid = blockIdx.x;
+    int64_t tile = pid;
+    if (total % 8 == 0) tile = (pid % 8) * (total / 8) + pid / 8;
+    const int64_t n0 = (tile / ntm) * BN, m0 = (tile % ntm) * BM;
     const int64_t K = p.K, G = K / 64;
 
-    // global -> register staging of one group
-    constexpr int WCH = BN * 2 / 256;  // 16-byte chunks of packed weights per thread
-    constexpr int XCH = BM * 4 / 256;  // 16-byte chunks of activation codes per thread
-    static_assert(WCH >= 1 && XCH >= 1, "tile too small for 256 threads");
-    uint4 wreg[WCH], xreg[XCH];
-    uint16_t wsreg = 0, asreg = 0;
+    // this lane's sources for group 0; group g adds g times the per-group stride
+    const uint8_t* xsrc[XI];
+#pragma unroll
+    for (int j = 0; j < XI; ++j) {
+        const int slot = (wave * XI + j) * 64 + lane;          // 16-byte slot of the stage
+        const int row = slot / 4, quarter = (slot % 4) ^ ((row >> 2) & 3);
+        xsrc[j] = p.qa + (m0 + row) * K + quarter * 16;
+    }
+    const uint8_t* wsrc[WI];
+#pragma unroll
+    for (int j = 0; j < WI; ++j) {
+        const int slot = (wave * WI + j) * 64 + lane;
+        wsrc[j] = p.qw + (n0 + slot / 2) * (K / 2) + (slot % 2) * 16;
+    }
+    const uint8_t* ssrc;   // 4 bytes: ws pair, as pair or (padding lanes) a valid dummy
+    int64_t sstride;
+    {
+        const int b = 4 * (wave * 64 + lane);
+        if (b < 2 * BN) {
+            ssrc = reinterpret_cast<const uint8_t*>(p.ws + n0) + b;
+            sstride = 2 * p.N;
+        } else if (b < 2 * (BN + BM)) {
+            ssrc = reinterpret_cast<const uint8_t*>(p.as + m0) + (b - 2 * BN);
+            sstride = 2 * p.Mp;
+        } else {
+            ssrc = reinterpret_cast<const uint8_t*>(p.ws + n0);
+            sstride = 0;
+        }
+    }
 
-    auto fetch = [&](int64_t g) {
+    // direct loads of group g (clamped to the last group) into stage st
+    auto issue = [&](int st, int64_t g) {
+        const int64_t gg = g < G ? g : G - 1;
 #pragma unroll
-        for (int c = 0; c < WCH; ++c) {
-            const int chunk = t + 256 * c, row = chunk / 2, half = chunk % 2;
-            wreg[c] = *reinterpret_cast<const uint4*>(p.qw + (n0 + row) * (K / 2) + g * 32 + half * 16);
-        }
+        for (int j = 0; j < XI; ++j) dma16(xsrc[j] + gg * 64, lds_addr(&sX[st][(wave * XI + j) * 1024]));
 #pragma unroll
-        for (int c = 0; c < XCH; ++c) {
-            const int chunk = t + 256 * c, row = chunk / 4, quarter = chunk % 4;
-            xreg[c] = *reinterpret_cast<const uint4*>(p.qa + (m0 + row) * K + g * 64 + quarter * 16);
-        }
-        if (t < BN) wsreg = p.ws[g * p.N + n0 + t];
-        if (t < BM) asreg = p.as[g * p.Mp + m0 + t];
+        for (int j = 0; j < WI; ++j) dma16(wsrc[j] + gg * 32, lds_addr(&sR[st][(wave * WI + j) * 1024]));
+        dma4(ssrc + gg * sstride, lds_addr(&sS[st][wave * 256]));
     };
-    auto stash = [&](int st) {
+    constexpr int CU = BN * 8 / NT;  // 4-byte nibble units per thread per group (8 per 32-byte weight row)
+    static_assert(CU * NT == BN * 8, "convert split");
+    auto convert = [&](int st, int cs) {  // raw nibbles of stage st -> e4m3 codes in code buffer cs
+        uint32_t w[CU];
 #pragma unroll
-        for (int c = 0; c < WCH; ++c) {
-            const int chunk = t + 256 * c, row = chunk / 2, half = chunk % 2;
-            const uint32_t w[4] = {wreg[c].x, wreg[c].y, wreg[c].z, wreg[c].w};
-            uint32_t lo[4], hi[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                lo[j] = nib4_to_e4m3(w[j] & 0x0f0f0f0fu);
-                hi[j] = nib4_to_e4m3((w[j] >> 4) & 0x0f0f0f0fu);
-            }
-            uint8_t* dst = &sW[st][row * PADK];
-            *reinterpret_cast<uint4*>(dst + half * 16) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-            *reinterpret_cast<uint4*>(dst + 32 + half * 16) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        for (int r = 0; r < CU; ++r) {
+            const int u = t + r * NT;
+            w[r] = *reinterpret_cast<const uint32_t*>(&sR[st][(u / 8) * 32 + (u % 8) * 4]);
         }
 #pragma unroll
-        for (int c = 0; c < XCH; ++c) {
-            const int chunk = t + 256 * c, row = chunk / 4, quarter = chunk % 4;
-            *reinterpret_cast<uint4*>(&sX[st][row * PADK + quarter * 16]) = xreg[c];
+        for (int r = 0; r < CU; ++r) {
+            const int u = t + r * NT;
+            uint8_t* dst = &sW[cs][(u / 8) * PADK + (u % 8) * 4];
+            *reinterpret_cast<uint32_t*>(dst) = nib4_to_e4m3(w[r] & 0x0f0f0f0fu);
+            *reinterpret_cast<uint32_t*>(dst + 32) = nib4_to_e4m3((w[r] >> 4) & 0x0f0f0f0fu);
         }
-        if (t < BN) sWs[st][t] = wsreg;
-        if (t < BM) sAs[st][t] = asreg;
     };
 
     f32x16 acc[TN][TM];
@@ -130,42 +187,76 @@ __global__ __launch_bounds__(256) void w4a4_gemm_kernel(GemmArgs p) {
 #pragma unroll
         for (int j = 0; j < TM; ++j) acc[i][j] = f32x16{};
     const f32x16 zero = {};
+    const bool low = lane < 32;
 
-    fetch(0);
-    stash(0);
-    for (int64_t g = 0; g < G; ++g) {
-        const int st = int(g & 1);
-        __syncthreads();
-        if (g + 1 < G) fetch(g + 1);
+    auto multiply = [&](int st, int cs) {
         i32x8 af[TN], bf[TM];
-        i16x4 sa[TN], sb[TM];
+        short sa[TN], sb[TM];
+        const uint16_t* sc = reinterpret_cast<const uint16_t*>(sS[st]);
 #pragma unroll
         for (int i = 0; i < TN; ++i) {
-            const int row = wn * WN + i * 32 + lane % 32;
-            const uint8_t* src = &sW[st][row * PADK + 32 * (lane / 32)];
+            const uint8_t* src = &sW[cs][(wn * WN + i * 32 + lane % 32) * PADK + 32 * (lane / 32)];
             const uint4 a0 = *reinterpret_cast<const uint4*>(src), a1 = *reinterpret_cast<const uint4*>(src + 16);
             af[i] = i32x8{int(a0.x), int(a0.y), int(a0.z), int(a0.w), int(a1.x), int(a1.y), int(a1.z), int(a1.w)};
-            sa[i] = i16x4{short(lane < 32 ? sWs[st][row] : 0), 0, 0, 0};
+            sa[i] = low ? short(sc[wn * WN + i * 32 + lane % 32]) : short(0);
         }
 #pragma unroll
         for (int j = 0; j < TM; ++j) {
             const int row = wm * WM + j * 32 + lane % 32;
-            const uint8_t* src = &sX[st][row * PADK + 32 * (lane / 32)];
-            const uint4 b0 = *reinterpret_cast<const uint4*>(src), b1 = *reinterpret_cast<const uint4*>(src + 16);
+            const int sw = (row >> 2) & 3;
+            const uint8_t* base = &sX[st][row * 64];
+            const uint4 b0 = *reinterpret_cast<const uint4*>(base + ((2 * (lane / 32)) ^ sw) * 16);
+            const uint4 b1 = *reinterpret_cast<const uint4*>(base + ((2 * (lane / 32) + 1) ^ sw) * 16);
             bf[j] = i32x8{int(b0.x), int(b0.y), int(b0.z), int(b0.w), int(b1.x), int(b1.y), int(b1.z), int(b1.w)};
-            sb[j] = i16x4{short(lane < 32 ? sAs[st][row] : 0), 0, 0, 0};
+            sb[j] = low ? short(sc[BN + row]) : short(0);
         }
 #pragma unroll
         for (int i = 0; i < TN; ++i)
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
+                const i16x4 oa = {sa[i], 0, 0, 0}, ob = {sb[j], 0, 0, 0};
                 const f32x16 I = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[i], bf[j], zero, 0, 0, 0, 0, 0, 0);
-                const f32x16 P = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(sa[i], sb[j], zero, 0, 0, 0);
+                const f32x16 P = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(oa, ob, zero, 0, 0, 0);
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[i][j][e] = fmaf(I[e], P[e], acc[i][j][e]);
             }
-        if (g + 1 < G) stash(st ^ 1);
+    };
+
+    // Ring step for group g on stage g % 4: wait until this wave's loads of groups <= g + 1 have landed (only
+    // group g + 2's are still in flight) and for every wave (barrier); the stage of group g - 1 is free again:
+    // issue group g + 3 into it; convert group g + 1's nibbles into the code buffer multiply(g - 1) used; multiply g.
+    issue(0, 0);
+    issue(1, 1);
+    issue(2, 2);
+    wait_vmcnt<2 * LPG>();
+    __syncthreads();
+    convert(0, 0);
+    for (int64_t g = 0; g < G; g += 4) {
+        wait_vmcnt<LPG>();
+        __syncthreads();
+        issue(3, g + 3);
+        convert(1, 1);
+        multiply(0, 0);
+        if (g + 1 >= G) break;
+        wait_vmcnt<LPG>();
+        __syncthreads();
+        issue(0, g + 4);
+        convert(2, 0);
+        multiply(1, 1);
+        if (g + 2 >= G) break;
+        wait_vmcnt<LPG>();
+        __syncthreads();
+        issue(1, g + 5);
+        convert(3, 1);
+        multiply(2, 0);
+        if (g + 3 >= G) break;
+        wait_vmcnt<LPG>();
+        __syncthreads();
+        issue(2, g + 6);
+        convert(0, 0);
+        multiply(3, 1);
     }
+    wait_vmcnt<0>();  // the clamped tail loads land before the workgroup can end
 
     // low-rank branch: acc += pu[n] . bf16(lora[m]) over r = 0..31, two 32x32x16 bf16 MFMAs per subtile
     if (p.lora) {
@@ -232,17 +323,27 @@ __global__ __launch_bounds__(256) void w4a4_gemm_kernel(GemmArgs p) {
         }
 }
 
-template <int BN, int BM, int WN, int WM>
+template <int BN, int BM, int WN, int WM, int NW>
 int launch(const GemmArgs& a, int epi, hipStream_t stream) {
-    dim3 grid(unsigned(a.N / BN), unsigned(a.Mp / BM));
+    if (a.N % BN || a.Mp % BM) return fail(WDL_EINVAL, "w4a4_gemm: tile %dx%d does not divide N=%lld Mp=%lld", BN, BM,
+                                           (long long)a.N, (long long)a.Mp);
+    const unsigned grid = unsigned((a.N / BN) * (a.Mp / BM));
     switch (epi) {
-        case EPI_BF16: w4a4_gemm_kernel<BN, BM, WN, WM, EPI_BF16><<<grid, 256, 0, stream>>>(a); break;
-        case EPI_F32: w4a4_gemm_kernel<BN, BM, WN, WM, EPI_F32><<<grid, 256, 0, stream>>>(a); break;
-        case EPI_RESIDUAL: w4a4_gemm_kernel<BN, BM, WN, WM, EPI_RESIDUAL><<<grid, 256, 0, stream>>>(a); break;
-        case EPI_GELU: w4a4_gemm_kernel<BN, BM, WN, WM, EPI_GELU><<<grid, 256, 0, stream>>>(a); break;
+        case EPI_BF16: w4a4_gemm_kernel<BN, BM, WN, WM, NW, EPI_BF16><<<grid, NW * 64, 0, stream>>>(a); break;
+        case EPI_F32: w4a4_gemm_kernel<BN, BM, WN, WM, NW, EPI_F32><<<grid, NW * 64, 0, stream>>>(a); break;
+        case EPI_RESIDUAL: w4a4_gemm_kernel<BN, BM, WN, WM, NW, EPI_RESIDUAL><<<grid, NW * 64, 0, stream>>>(a); break;
+        case EPI_GELU: w4a4_gemm_kernel<BN, BM, WN, WM, NW, EPI_GELU><<<grid, NW * 64, 0, stream>>>(a); break;
         default: return fail(WDL_EINVAL, "w4a4_gemm: bad epilogue %d", epi);
     }
     return check_launch("w4a4_gemm");
+}
+
+// tile configurations (BN x BM, waves): 0 = 128x128 (4 waves of 64x64), 1 = 256x128 (8 waves of 64x64)
+int dispatch(const GemmArgs& a, int epi, int config, hipStream_t stream) {
+    switch (config) {
+        case 1: return launch<256, 128, 64, 64, 8>(a, epi, stream);
+        default: return launch<128, 128, 64, 64, 4>(a, epi, stream);
+    }
 }
 
 }  // namespace
@@ -258,11 +359,14 @@ extern "C" int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* qw
                     (long long)Mp, (long long)N, (long long)K, (long long)ldo);
     if (lora && (rank != 32 || !proj_up)) return fail(WDL_EINVAL, "w4a4_gemm: low-rank branch needs rank 32");
     if (!qa || !ascales || !qweight || !wscales || !out) return fail(WDL_EINVAL, "w4a4_gemm: null pointer");
+    if ((reinterpret_cast<uintptr_t>(qa) | reinterpret_cast<uintptr_t>(qweight)) % 16 ||
+        (reinterpret_cast<uintptr_t>(ascales) | reinterpret_cast<uintptr_t>(wscales)) % 4)
+        return fail(WDL_EINVAL, "w4a4_gemm: operands must be 16-byte (codes) / 4-byte (scales) aligned");
     if (epilogue == EPI_RESIDUAL && !gate) return fail(WDL_EINVAL, "w4a4_gemm: residual epilogue needs gate");
     if (Mp == 0) return WDL_OK;
     GemmArgs a{static_cast<const uint8_t*>(qa), static_cast<const uint16_t*>(ascales),
                static_cast<const uint8_t*>(qweight), static_cast<const uint16_t*>(wscales), lora,
                static_cast<const uint16_t*>(proj_up), static_cast<const uint16_t*>(bias), M, Mp, N, K, out, ldo,
                gate};
-    return launch<128, 128, 64, 64>(a, epilogue, stream);
+    return dispatch(a, epilogue, 0, stream);  // 128x128 measured ahead of 256x128 on every block shape
 }

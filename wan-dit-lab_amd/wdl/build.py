@@ -30,6 +30,7 @@ FLAGS = [
     "-fPIC",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",  # MFMA results in VGPRs: no accvgpr read-backs before VALU use
     "-Wno-unused-command-line-argument",
 ]
 
