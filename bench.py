@@ -140,7 +140,17 @@ def instrumented(step):
     ops.gemm_launch, ops.sage_attn_launch = gemm, attn
     import wdl.block as wblock
     wblock.ops.gemm_launch, wblock.ops.sage_attn_launch = gemm, attn
+    # Keep the GPU behind the host while the step is enqueued, so that each start event is followed at once by its
+    # (already queued) kernel and no host launch latency falls between the events: a spin kernel of ~0.5 s first.
+    probe = 10_000_000
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s0.record()
+    torch.cuda._sleep(probe)
+    s1.record()
+    torch.cuda.synchronize()
+    cycles_per_ms = probe / max(s0.elapsed_time(s1), 1e-3)
     try:
+        torch.cuda._sleep(int(500 * cycles_per_ms))
         step()
         torch.cuda.synchronize()
     finally:
@@ -151,6 +161,20 @@ def instrumented(step):
         flops = sum(f for _, _, f in items)
         out[name] = dict(launches=len(items), ms=ms, tops=flops / (ms * 1e-3) / 1e12 if ms else 0.0)
     return out
+
+
+COUNTERS = ROOT / "profiles" / "w4a4_gemm_kernel_dit_step_512x928_counters.md"
+
+
+def gemm_traffic():
+    """HBM bytes per W4A4 GEMM launch over the step: FETCH_SIZE and WRITE_SIZE averages of two rocprofv3 --pmc runs
+    of this benchmark, each scaled by its reading for a copy of known size (the committed counter summary)."""
+    import re
+
+    if not COUNTERS.exists():
+        return None
+    m = re.search(r"w4a4_gemm_kernel, all launches: HBM bytes per launch \(calibrated\): (\d+)", COUNTERS.read_text())
+    return int(m.group(1)) if m else None
 
 
 def cpu_baseline():
@@ -202,6 +226,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of the HIP graph")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="first run a plain elementwise copy of MIB MiB (bitwise_not, uint8) three times: the "
+                         "known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the quantized Wan block hot path runs on a single MI355X; "
@@ -214,6 +241,14 @@ def main():
     _lib.library()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_probe:
+        src = torch.randint(0, 256, (args.copy_probe << 20,), dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.bitwise_not(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
+        log(f"bench: copy probe of {args.copy_probe} MiB done")
     step = Step(dev)
     with torch.no_grad():
         for _ in range(max(1, args.warmup)):
@@ -275,9 +310,10 @@ def main():
         "attention_pct_int8_peak": 100 * a["tops"] / INT8_PEAK_TOPS,
         "attention_ms_per_step": a["ms"],
         "roofline": {"bound": "mfma", "kernel": "w4a4_gemm_kernel", "achieved": g["tops"], "peak": INT8_PEAK_TOPS,
-                     "unit": "TFLOP/s", "frac": gemm_frac, "traffic": None,
+                     "unit": "TFLOP/s", "frac": gemm_frac, "traffic": gemm_traffic(),
                      "basis": "2*M*N*K int ops per launch (M = 1392 tokens) summed over the step's "
-                              f"{g['launches']} W4A4 GEMM launches / their summed HIP-event durations"},
+                              f"{g['launches']} W4A4 GEMM launches / their summed HIP-event durations; traffic = "
+                              "calibrated HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE"},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()

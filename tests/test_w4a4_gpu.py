@@ -87,7 +87,19 @@ def launch_gemm(qa_int, asc, qweight, wsc, lora=None, pu=None, bias=None, M=None
     if out is None:
         out = torch.empty(M, N, device="cuda", dtype=torch.float32 if epi == 1 else torch.bfloat16)
     c = lambda t: None if t is None else t.cuda()
-    return ops.gemm_launch(codes, c(asc), c(lora), qweight.cuda(), c(wsc), c(pu), c(bias), M, out, epi, c(gate))
+    return ops.gemm_launch(codes, c(asc), c(lora), ops.as_codes(qweight.cuda(), K), c(wsc), c(pu), c(bias), M, out,
+                           epi, c(gate))
+
+
+@pytest.mark.parametrize("N,K", [(128, 64), (384, 3072), (256, 14336)])
+def test_weight_codes_are_the_e4m3_values_of_the_packed_integers(gpu, N, K):
+    """wdl_w4a4_weight_codes: packed nibbles [N, K/2] -> e4m3 codes [N, K], bit-exact against torch's e4m3 of the
+    unpacked integers (every int4 value is exactly representable)."""
+    from wdl import ops, w4a4
+
+    q = torch.randint(-8, 8, (N, K), generator=torch.Generator().manual_seed(N + K), dtype=torch.int32)
+    codes = ops.weight_codes(w4a4.pack_weight(q).cuda()).cpu()
+    assert torch.equal(codes, q.float().to(torch.float8_e4m3fn).view(torch.uint8))
 
 
 @pytest.mark.parametrize("M,N,K", [(128, 128, 64), (256, 384, 512), (128, 256, 3072), (128, 128, 14336),

@@ -3,9 +3,9 @@
 //   y[m][n] = sum_g as[g][m] * ws[g][n] * I_g[m][n]  +  bf16(lora[m]) . pu[n]  +  bias[n]
 //   I_g[m][n] = sum_{k in group g} qa[m][k] * qw[n][k]          (exact integers)
 //
-// Operands: qa — activation int4 values as e4m3 codes, one byte each, [Mp, K] (wdl_act_quant_w4);
-// qw — weight int4 nibbles [N, K/2], in each 64-group byte j holds k = j (low nibble) and k = j + 32 (high),
-// two's complement; as [K/64, Mp], ws [K/64, N] bf16; lora fp32 [Mp, 32]; pu bf16 [N, 32]; bias bf16 [N].
+// Operands: qa — activation int4 values as e4m3 codes, one byte each, [Mp, K] (wdl_act_quant_w4); wc — weight
+// int4 values as e4m3 codes [N, K] (wdl_w4a4_weight_codes, expanded once from the packed [N, K/2] nibbles);
+// as [K/64, Mp], ws [K/64, N] bf16; lora fp32 [Mp, 32]; pu bf16 [N, 32]; bias bf16 [N].
 //
 // Arithmetic: every int4 value is exactly an e4m3 value, so v_mfma_f32_32x32x64_f8f6f4 (one 64-deep group per
 // instruction, the int8 rate) returns I_g exactly as an fp32 integer (|I_g| <= 64 * 8 * 15 < 2^24). The per-group
@@ -15,7 +15,8 @@
 //
 // Orientation: the tile is computed transposed, C^T[n][m] (rows = output features, columns = tokens), so a lane
 // holds one token and 16 features: row n = 8*(i/4) + 4*(lane/32) + i%4, column m = lane%32 of each 32x32 subtile.
-// Weights are unpacked once per workgroup per group into LDS as e4m3 codes (two v_perm lookups per 4 values).
+// Both operands arrive as codes, so the main loop issues no conversion work: per MFMA pair its vector ALU work is
+// the 16 fmaf of the scale fold.
 #include "wdl_common.h"
 
 namespace {
@@ -39,7 +40,7 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 struct GemmArgs {
     const uint8_t* qa;        // [Mp, K] e4m3 codes
     const uint16_t* as;       // [G, Mp]
-    const uint8_t* qw;        // [N, K/2]
+    const uint8_t* wc;        // [N, K] e4m3 codes
     const uint16_t* ws;       // [G, N]
     const float* lora;        // [Mp, 32] or null
     const uint16_t* pu;       // [N, 32] or null
@@ -50,30 +51,15 @@ struct GemmArgs {
     const float* gate;        // [N] fp32 (EPI_RESIDUAL: out += gate * bf16(y))
 };
 
-constexpr int PADK = 80;  // LDS row stride (bytes) of 64-byte k rows
-
-// e4m3 codes of the two's complement nibbles 0..7 (values 0..7) and 8..15 (values -8..-1)
-constexpr uint32_t LUT0 = 0x44403800u, LUT1 = 0x4E4C4A48u, LUT2 = 0xCACCCED0u, LUT3 = 0xB8C0C4C8u;
-
-// four nibbles in the low 4 bits of each byte of x -> four e4m3 codes
-__device__ __forceinline__ uint32_t nib4_to_e4m3(uint32_t x) {
-    const uint32_t sel = x & 0x07070707u;
-    const uint32_t pos = __builtin_amdgcn_perm(LUT1, LUT0, sel);
-    const uint32_t neg = __builtin_amdgcn_perm(LUT3, LUT2, sel);
-    const uint32_t t = (x >> 3) & 0x01010101u;
-    const uint32_t mask = (t << 8) - t;  // 0xff in every byte whose nibble is negative
-    return (neg & mask) | (pos & ~mask);
-}
-
 // Tile BN (features) x BM (tokens), NW waves in a (BN / WN) x (BM / WM) grid. Per 64-deep group the workgroup
-// needs the activation codes [BM][64 B], the weight nibbles [BN][32 B] and the scales ws[BN], as[BM]; all three
+// needs the activation codes [BM][64 B], the weight codes [BN][64 B] and the scales ws[BN], as[BM]; all three
 // stream straight from global memory into a 4-stage LDS ring with global_load_lds (lane-linear in LDS: 16 bytes
-// per lane for codes and nibbles, 4 for scales), issued 3 groups ahead, so no staging registers are involved.
-// Every wave issues the same number of these loads per group, so each wave's vmcnt names exactly the groups still
-// in flight; the loads are written as inline asm so that the compiler's own wait insertion, which cannot tell the
-// ring stages apart, does not add vmcnt(0) waits in front of every LDS read. Activation rows sit in LDS with their
-// four 16-byte quarters XOR-swizzled by (row / 4) % 4 (conflict-free operand reads). One group ahead of the
-// multiply, each thread turns its share of the raw nibbles into e4m3 codes in a double-buffered code tile.
+// per lane for codes, 4 for scales), issued 3 groups ahead, so no staging registers are involved. Every wave
+// issues the same number of these loads per group, so each wave's vmcnt names exactly the groups still in flight;
+// the loads are written as inline asm so that the compiler's own wait insertion, which cannot tell the ring
+// stages apart, does not add vmcnt(0) waits in front of every LDS read. Code rows sit in LDS with their four
+// 16-byte quarters XOR-swizzled by (row / 4) % 4 (conflict-free operand reads). Each scale stage ends in 64 zero
+// bytes that lanes 32..63 read, which zeroes their half of the outer-product operands without a select.
 // Workgroup ids are remapped so that the tiles of one weight slab run on one XCD.
 constexpr int STAGES = 4;
 
@@ -101,18 +87,17 @@ template <int BN, int BM, int WN, int WM, int NW, int EPI>
 __global__ __launch_bounds__(NW * 64) void w4a4_gemm_kernel(GemmArgs p) {
     static_assert((BN / WN) * (BM / WM) == NW, "wave grid");
     static_assert(STAGES == 4, "the main loop is unrolled by 4 stages");
-    constexpr int NT = NW * 64;
     constexpr int TN = WN / 32, TM = WM / 32;
     constexpr int XI = BM * 4 / 64 / NW;   // 16-byte loads per wave per group: activation codes
-    constexpr int WI = BN * 2 / 64 / NW;   // and raw weight nibbles
+    constexpr int WI = BN * 4 / 64 / NW;   // and weight codes
     constexpr int LPG = XI + WI + 1;       // + one 4-byte load of scales: loads per wave per group
-    constexpr int SB = NW * 256;           // scale bytes per stage (ws[BN], as[BM], then padding)
-    static_assert(XI >= 1 && WI >= 1 && BM * 4 == XI * 64 * NW && BN * 2 == WI * 64 * NW, "tile vs waves");
-    static_assert(2 * (BN + BM) <= SB, "scale stage");
+    constexpr int SD = NW * 256;           // scale bytes loaded per stage (ws[BN], as[BM], then padding)
+    constexpr int SB = SD + 256;           // + 64 zero bytes (rounded up) read by lanes 32..63
+    static_assert(XI >= 1 && WI >= 1 && BM * 4 == XI * 64 * NW && BN * 4 == WI * 64 * NW, "tile vs waves");
+    static_assert(2 * (BN + BM) <= SD, "scale stage");
     __shared__ __attribute__((aligned(1024))) uint8_t sX[STAGES][BM * 64];
-    __shared__ __attribute__((aligned(1024))) uint8_t sR[STAGES][BN * 32];
+    __shared__ __attribute__((aligned(1024))) uint8_t sW[STAGES][BN * 64];
     __shared__ __attribute__((aligned(256))) uint8_t sS[STAGES][SB];
-    __shared__ __attribute__((aligned(16))) uint8_t sW[2][BN * PADK];
 
     const int t = threadIdx.x, lane = t % 64;
     const int wave = __builtin_amdgcn_readfirstlane(t / 64);
@@ -124,7 +109,10 @@ __global__ __launch_bounds__(NW * 64) void w4a4_gemm_kernel(GemmArgs p) {
     const int64_t n0 = (tile / ntm) * BN, m0 = (tile % ntm) * BM;
     const int64_t K = p.K, G = K / 64;
 
-    // this lane's sources for group 0; group g adds g times the per-group stride
+    // zero tails of the scale stages (written once; the loads never touch them)
+    if (t < STAGES * 16) *reinterpret_cast<uint32_t*>(&sS[t / 16][SD + (t % 16) * 4]) = 0u;
+
+    // this lane's sources for group 0; group g adds 64 g bytes (codes) or g times the scale row stride
     const uint8_t* xsrc[XI];
 #pragma unroll
     for (int j = 0; j < XI; ++j) {
@@ -136,7 +124,8 @@ __global__ __launch_bounds__(NW * 64) void w4a4_gemm_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < WI; ++j) {
         const int slot = (wave * WI + j) * 64 + lane;
-        wsrc[j] = p.qw + (n0 + slot / 2) * (K / 2) + (slot % 2) * 16;
+        const int row = slot / 4, quarter = (slot % 4) ^ ((row >> 2) & 3);
+        wsrc[j] = p.wc + (n0 + row) * K + quarter * 16;
     }
     const uint8_t* ssrc;   // 4 bytes: ws pair, as pair or (padding lanes) a valid dummy
     int64_t sstride;
@@ -160,26 +149,33 @@ __global__ __launch_bounds__(NW * 64) void w4a4_gemm_kernel(GemmArgs p) {
 #pragma unroll
         for (int j = 0; j < XI; ++j) dma16(xsrc[j] + gg * 64, lds_addr(&sX[st][(wave * XI + j) * 1024]));
 #pragma unroll
-        for (int j = 0; j < WI; ++j) dma16(wsrc[j] + gg * 32, lds_addr(&sR[st][(wave * WI + j) * 1024]));
+        for (int j = 0; j < WI; ++j) dma16(wsrc[j] + gg * 64, lds_addr(&sW[st][(wave * WI + j) * 1024]));
         dma4(ssrc + gg * sstride, lds_addr(&sS[st][wave * 256]));
     };
-    constexpr int CU = BN * 8 / NT;  // 4-byte nibble units per thread per group (8 per 32-byte weight row)
-    static_assert(CU * NT == BN * 8, "convert split");
-    auto convert = [&](int st, int cs) {  // raw nibbles of stage st -> e4m3 codes in code buffer cs
-        uint32_t w[CU];
+
+    // per-lane LDS offsets (stage-independent): operand rows with their swizzled quarters, scale entries
+    const bool low = lane < 32;
+    int aoff[TN], soa[TN], boff[TM], sob[TM];
+    int q0, q1;
 #pragma unroll
-        for (int r = 0; r < CU; ++r) {
-            const int u = t + r * NT;
-            w[r] = *reinterpret_cast<const uint32_t*>(&sR[st][(u / 8) * 32 + (u % 8) * 4]);
-        }
+    for (int i = 0; i < TN; ++i) {
+        const int row = wn * WN + i * 32 + lane % 32;
+        aoff[i] = row * 64;
+        soa[i] = low ? 2 * row : SD + 2 * (lane % 32);
+    }
 #pragma unroll
-        for (int r = 0; r < CU; ++r) {
-            const int u = t + r * NT;
-            uint8_t* dst = &sW[cs][(u / 8) * PADK + (u % 8) * 4];
-            *reinterpret_cast<uint32_t*>(dst) = nib4_to_e4m3(w[r] & 0x0f0f0f0fu);
-            *reinterpret_cast<uint32_t*>(dst + 32) = nib4_to_e4m3((w[r] >> 4) & 0x0f0f0f0fu);
-        }
-    };
+    for (int j = 0; j < TM; ++j) {
+        const int row = wm * WM + j * 32 + lane % 32;
+        boff[j] = row * 64;
+        sob[j] = low ? 2 * BN + 2 * row : SD + 2 * (lane % 32);
+    }
+    {
+        // every operand row index here is 32-aligned plus lane % 32, so (row / 4) % 4 = (lane % 32 / 4) % 4
+        const int sw = ((lane % 32) >> 2) & 3;
+        q0 = ((2 * (lane / 32)) ^ sw) * 16;
+        q1 = ((2 * (lane / 32) + 1) ^ sw) * 16;
+    }
+    static_assert(WN % 32 == 0 && WM % 32 == 0, "32-aligned subtiles");
 
     f32x16 acc[TN][TM];
 #pragma unroll
@@ -187,28 +183,23 @@ __global__ __launch_bounds__(NW * 64) void w4a4_gemm_kernel(GemmArgs p) {
 #pragma unroll
         for (int j = 0; j < TM; ++j) acc[i][j] = f32x16{};
     const f32x16 zero = {};
-    const bool low = lane < 32;
 
-    auto multiply = [&](int st, int cs) {
+    auto multiply = [&](int st) {
         i32x8 af[TN], bf[TM];
         short sa[TN], sb[TM];
-        const uint16_t* sc = reinterpret_cast<const uint16_t*>(sS[st]);
 #pragma unroll
         for (int i = 0; i < TN; ++i) {
-            const uint8_t* src = &sW[cs][(wn * WN + i * 32 + lane % 32) * PADK + 32 * (lane / 32)];
-            const uint4 a0 = *reinterpret_cast<const uint4*>(src), a1 = *reinterpret_cast<const uint4*>(src + 16);
+            const uint8_t* r = &sW[st][aoff[i]];
+            const uint4 a0 = *reinterpret_cast<const uint4*>(r + q0), a1 = *reinterpret_cast<const uint4*>(r + q1);
             af[i] = i32x8{int(a0.x), int(a0.y), int(a0.z), int(a0.w), int(a1.x), int(a1.y), int(a1.z), int(a1.w)};
-            sa[i] = low ? short(sc[wn * WN + i * 32 + lane % 32]) : short(0);
+            sa[i] = *reinterpret_cast<const short*>(&sS[st][soa[i]]);
         }
 #pragma unroll
         for (int j = 0; j < TM; ++j) {
-            const int row = wm * WM + j * 32 + lane % 32;
-            const int sw = (row >> 2) & 3;
-            const uint8_t* base = &sX[st][row * 64];
-            const uint4 b0 = *reinterpret_cast<const uint4*>(base + ((2 * (lane / 32)) ^ sw) * 16);
-            const uint4 b1 = *reinterpret_cast<const uint4*>(base + ((2 * (lane / 32) + 1) ^ sw) * 16);
+            const uint8_t* r = &sX[st][boff[j]];
+            const uint4 b0 = *reinterpret_cast<const uint4*>(r + q0), b1 = *reinterpret_cast<const uint4*>(r + q1);
             bf[j] = i32x8{int(b0.x), int(b0.y), int(b0.z), int(b0.w), int(b1.x), int(b1.y), int(b1.z), int(b1.w)};
-            sb[j] = low ? short(sc[BN + row]) : short(0);
+            sb[j] = *reinterpret_cast<const short*>(&sS[st][sob[j]]);
         }
 #pragma unroll
         for (int i = 0; i < TN; ++i)
@@ -222,39 +213,32 @@ __global__ __launch_bounds__(NW * 64) void w4a4_gemm_kernel(GemmArgs p) {
             }
     };
 
-    // Ring step for group g on stage g % 4: wait until this wave's loads of groups <= g + 1 have landed (only
-    // group g + 2's are still in flight) and for every wave (barrier); the stage of group g - 1 is free again:
-    // issue group g + 3 into it; convert group g + 1's nibbles into the code buffer multiply(g - 1) used; multiply g.
+    // Ring step for group g on stage g % 4: wait until this wave's loads of groups <= g have landed (groups g + 1
+    // and g + 2 may still be in flight) and for every wave (barrier); the stage of group g - 1 is free again:
+    // issue group g + 3 into it; multiply group g.
     issue(0, 0);
     issue(1, 1);
     issue(2, 2);
-    wait_vmcnt<2 * LPG>();
-    __syncthreads();
-    convert(0, 0);
     for (int64_t g = 0; g < G; g += 4) {
-        wait_vmcnt<LPG>();
+        wait_vmcnt<2 * LPG>();
         __syncthreads();
         issue(3, g + 3);
-        convert(1, 1);
-        multiply(0, 0);
+        multiply(0);
         if (g + 1 >= G) break;
-        wait_vmcnt<LPG>();
+        wait_vmcnt<2 * LPG>();
         __syncthreads();
         issue(0, g + 4);
-        convert(2, 0);
-        multiply(1, 1);
+        multiply(1);
         if (g + 2 >= G) break;
-        wait_vmcnt<LPG>();
+        wait_vmcnt<2 * LPG>();
         __syncthreads();
         issue(1, g + 5);
-        convert(3, 1);
-        multiply(2, 0);
+        multiply(2);
         if (g + 3 >= G) break;
-        wait_vmcnt<LPG>();
+        wait_vmcnt<2 * LPG>();
         __syncthreads();
         issue(2, g + 6);
-        convert(0, 0);
-        multiply(3, 1);
+        multiply(3);
     }
     wait_vmcnt<0>();  // the clamped tail loads land before the workgroup can end
 
@@ -346,11 +330,38 @@ int dispatch(const GemmArgs& a, int epi, int config, hipStream_t stream) {
     }
 }
 
+// e4m3 codes of the two's complement nibbles 0..7 (values 0..7) and 8..15 (values -8..-1)
+constexpr uint32_t LUT0 = 0x44403800u, LUT1 = 0x4E4C4A48u, LUT2 = 0xCACCCED0u, LUT3 = 0xB8C0C4C8u;
+
+// four nibbles in the low 4 bits of each byte of x -> four e4m3 codes
+__device__ __forceinline__ uint32_t nib4_to_e4m3(uint32_t x) {
+    const uint32_t sel = x & 0x07070707u;
+    const uint32_t pos = __builtin_amdgcn_perm(LUT1, LUT0, sel);
+    const uint32_t neg = __builtin_amdgcn_perm(LUT3, LUT2, sel);
+    const uint32_t t = (x >> 3) & 0x01010101u;
+    const uint32_t mask = (t << 8) - t;  // 0xff in every byte whose nibble is negative
+    return (neg & mask) | (pos & ~mask);
+}
+
+// packed nibbles [N, K/2] -> e4m3 codes [N, K]: one thread per 4 packed bytes (8 values)
+__global__ __launch_bounds__(256) void weight_codes_kernel(const uint32_t* qw, int64_t words, int64_t K,
+                                                         uint32_t* codes) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= words) return;
+    // word i covers packed bytes 4i..4i+3 of row n = 4i / (K/2): group g, byte offset j0 = (4i) % 32 in the group
+    const int64_t byte = 4 * i, row = byte / (K / 2), in_row = byte % (K / 2);
+    const int64_t g = in_row / 32, j0 = in_row % 32;
+    const uint32_t w = qw[i];
+    uint32_t* dst = codes + (row * K + g * 64 + j0) / 4;
+    dst[0] = nib4_to_e4m3(w & 0x0f0f0f0fu);              // k = j0..j0+3
+    dst[8] = nib4_to_e4m3((w >> 4) & 0x0f0f0f0fu);       // k = 32 + j0..j0+3
+}
+
 }  // namespace
 
 // epilogue: 0 = bf16 out, 1 = fp32 out, 2 = out(bf16) = bf16(out + bf16(y) * gate) (gated residual in place),
 // 3 = bf16(GELU_tanh(y)) out
-extern "C" int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* qweight, const void* wscales,
+extern "C" int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wcodes, const void* wscales,
                              const float* lora, const void* proj_up, const void* bias, int64_t M, int64_t Mp,
                              int64_t N, int64_t K, int64_t rank, void* out, int64_t ldo, int epilogue,
                              const float* gate, hipStream_t stream) {
@@ -358,15 +369,28 @@ extern "C" int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* qw
         return fail(WDL_EINVAL, "w4a4_gemm: bad shape M=%lld Mp=%lld N=%lld K=%lld ldo=%lld", (long long)M,
                     (long long)Mp, (long long)N, (long long)K, (long long)ldo);
     if (lora && (rank != 32 || !proj_up)) return fail(WDL_EINVAL, "w4a4_gemm: low-rank branch needs rank 32");
-    if (!qa || !ascales || !qweight || !wscales || !out) return fail(WDL_EINVAL, "w4a4_gemm: null pointer");
-    if ((reinterpret_cast<uintptr_t>(qa) | reinterpret_cast<uintptr_t>(qweight)) % 16 ||
+    if (!qa || !ascales || !wcodes || !wscales || !out) return fail(WDL_EINVAL, "w4a4_gemm: null pointer");
+    if ((reinterpret_cast<uintptr_t>(qa) | reinterpret_cast<uintptr_t>(wcodes)) % 16 ||
         (reinterpret_cast<uintptr_t>(ascales) | reinterpret_cast<uintptr_t>(wscales)) % 4)
         return fail(WDL_EINVAL, "w4a4_gemm: operands must be 16-byte (codes) / 4-byte (scales) aligned");
     if (epilogue == EPI_RESIDUAL && !gate) return fail(WDL_EINVAL, "w4a4_gemm: residual epilogue needs gate");
     if (Mp == 0) return WDL_OK;
     GemmArgs a{static_cast<const uint8_t*>(qa), static_cast<const uint16_t*>(ascales),
-               static_cast<const uint8_t*>(qweight), static_cast<const uint16_t*>(wscales), lora,
+               static_cast<const uint8_t*>(wcodes), static_cast<const uint16_t*>(wscales), lora,
                static_cast<const uint16_t*>(proj_up), static_cast<const uint16_t*>(bias), M, Mp, N, K, out, ldo,
                gate};
     return dispatch(a, epilogue, 0, stream);  // 128x128 measured ahead of 256x128 on every block shape
+}
+
+extern "C" int wdl_w4a4_weight_codes(const void* qweight, int64_t N, int64_t K, void* codes, hipStream_t stream) {
+    if (N < 0 || K <= 0 || K % 64) return fail(WDL_EINVAL, "w4a4_weight_codes: bad shape N=%lld K=%lld",
+                                               (long long)N, (long long)K);
+    if (!qweight || !codes) return fail(WDL_EINVAL, "w4a4_weight_codes: null pointer");
+    if ((reinterpret_cast<uintptr_t>(qweight) | reinterpret_cast<uintptr_t>(codes)) % 16)
+        return fail(WDL_EINVAL, "w4a4_weight_codes: buffers must be 16-byte aligned");
+    const int64_t words = N * K / 8;
+    if (words == 0) return WDL_OK;
+    weight_codes_kernel<<<unsigned((words + 255) / 256), 256, 0, stream>>>(static_cast<const uint32_t*>(qweight),
+                                                                          words, K, static_cast<uint32_t*>(codes));
+    return check_launch("w4a4_weight_codes");
 }

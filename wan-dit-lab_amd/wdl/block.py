@@ -33,6 +33,8 @@ class QuantizedWanBlock:
     def __init__(self, parts: dict, dim: int, heads: int, eps: float = 1e-6):
         self.p, self.dim, self.heads, self.eps = parts, dim, heads, eps
         dev = parts["qkv"]["qweight"].device
+        for name in LINEARS:  # the GEMM operand: e4m3 codes [N, K], expanded once from the packed nibbles
+            parts[name]["wcodes"] = ops.weight_codes(parts[name]["qweight"])
         self.ones = torch.ones(dim, device=dev, dtype=torch.float32)
 
     # --------------------------------------------------------------------------------------- pieces
@@ -43,11 +45,11 @@ class QuantizedWanBlock:
     def _gemm(self, qa, name, M, out, epilogue=EPI_BF16, gate=None):
         t = self.p[name]
         q, asc, lora = qa
-        return ops.gemm_launch(q, asc, lora, t["qweight"], t["wscales"], t["proj_up"], t["bias"], M, out, epilogue,
+        return ops.gemm_launch(q, asc, lora, t["wcodes"], t["wscales"], t["proj_up"], t["bias"], M, out, epilogue,
                                gate)
 
     def linear(self, x, name):
-        out = torch.empty(x.shape[0], self.p[name]["qweight"].shape[0], device=x.device, dtype=torch.bfloat16)
+        out = torch.empty(x.shape[0], self.p[name]["wcodes"].shape[0], device=x.device, dtype=torch.bfloat16)
         return self._gemm(self._quant(x, name), name, x.shape[0], out)
 
     def prepare_context(self, C: torch.Tensor) -> dict:
@@ -94,7 +96,7 @@ class QuantizedWanBlock:
         Ac = ops.sage_attn_launch(q_i8, q_sc, ctx, ctx["L"], 128 ** -0.5)
         self._gemm(self._quant(Ac, "co"), "co", M, X, EPI_RESIDUAL, self.ones)
         # feed forward (W4A4 GELU MLP)
-        h = torch.empty(M, self.p["ffn1"]["qweight"].shape[0], device=dev, dtype=torch.bfloat16)
+        h = torch.empty(M, self.p["ffn1"]["wcodes"].shape[0], device=dev, dtype=torch.bfloat16)
         self._gemm(self._quant(X, "ffn1", ln=dict(shift=sh_f, scale=sc_f, eps=self.eps)), "ffn1", M, h, EPI_GELU)
         self._gemm(self._quant(h, "ffn2", shift=GELU_SHIFT, unsigned=True), "ffn2", M, X, EPI_RESIDUAL, g_f)
         return X

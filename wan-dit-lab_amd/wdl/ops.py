@@ -72,10 +72,33 @@ def act_quant_launch(x, smooth, proj_down_t, qshift=0.0, unsigned=False, *, ln=N
     return q, ascales, lora
 
 
-def gemm_launch(q, ascales, lora, qweight, wscales, proj_up, bias, M, out, epilogue=EPI_BF16, gate=None):
+def weight_codes(qweight: torch.Tensor) -> torch.Tensor:
+    """Packed int4 weights uint8 [N, K/2] -> the GEMM's operand, e4m3 codes of the same integers, uint8 [N, K]."""
+    N, half = qweight.shape
+    codes = torch.empty(N, 2 * half, device=qweight.device, dtype=torch.uint8)
+    _lib.call("wdl_w4a4_weight_codes", ptr(qweight.contiguous()), N, 2 * half, ptr(codes), stream_of(qweight))
+    return codes
+
+
+def as_codes(qweight: torch.Tensor, K: int) -> torch.Tensor:
+    """The weight operand for input width K: uint8 [N, K] codes pass through, packed [N, K/2] nibbles are
+    expanded (once per call)."""
+    if qweight.dtype not in (torch.uint8, torch.int8) or qweight.dim() != 2:
+        raise TypeError(f"qweight must be a 2-d uint8 tensor, got {qweight.dtype} {tuple(qweight.shape)}")
+    if qweight.shape[1] == K:
+        return qweight.view(torch.uint8)
+    if 2 * qweight.shape[1] == K:
+        return weight_codes(qweight.view(torch.uint8))
+    raise ValueError(f"qweight {tuple(qweight.shape)} fits neither [N, {K}] codes nor [N, {K // 2}] nibbles")
+
+
+def gemm_launch(q, ascales, lora, wcodes, wscales, proj_up, bias, M, out, epilogue=EPI_BF16, gate=None):
+    """W4A4 GEMM on the quantizer's outputs (q, ascales, lora) and e4m3 weight codes [N, K] (weight_codes)."""
     Mp, K = q.shape
-    N = qweight.shape[0]
-    _lib.call("wdl_w4a4_gemm", ptr(q), ptr(ascales), ptr(qweight), ptr(wscales), ptr(lora), ptr(proj_up), ptr(bias),
+    N = wcodes.shape[0]
+    if wcodes.shape[1] != K:
+        raise ValueError(f"weight codes {tuple(wcodes.shape)} do not match activations of width {K}")
+    _lib.call("wdl_w4a4_gemm", ptr(q), ptr(ascales), ptr(wcodes), ptr(wscales), ptr(lora), ptr(proj_up), ptr(bias),
               M, Mp, N, K, RANK, ptr(out), out.stride(0), epilogue, ptr(gate), stream_of(q))
     return out
 
@@ -98,7 +121,8 @@ def _(x, smooth, proj_down, qshift, unsigned):
 def w4a4_gemm(q: torch.Tensor, ascales: torch.Tensor, lora: torch.Tensor, qweight: torch.Tensor,
               wscales: torch.Tensor, proj_up: torch.Tensor, bias: torch.Tensor, M: int, fp32_out: bool) -> torch.Tensor:
     out = torch.empty(M, qweight.shape[0], device=q.device, dtype=torch.float32 if fp32_out else torch.bfloat16)
-    return gemm_launch(q, ascales, lora, qweight, wscales, proj_up, bias, M, out, EPI_F32 if fp32_out else EPI_BF16)
+    return gemm_launch(q, ascales, lora, as_codes(qweight, q.shape[1]), wscales, proj_up, bias, M, out,
+                       EPI_F32 if fp32_out else EPI_BF16)
 
 
 @w4a4_gemm.register_fake
@@ -113,7 +137,7 @@ def w4a4_linear(x: torch.Tensor, qweight: torch.Tensor, wscales: torch.Tensor, p
     the W4A4 GEMM with the low-rank up projection and the bias; x bf16 [M, K] -> bf16 [M, N]."""
     q, asc, lora = act_quant_launch(x, smooth, proj_down)
     out = torch.empty(x.shape[0], qweight.shape[0], device=x.device, dtype=torch.bfloat16)
-    return gemm_launch(q, asc, lora, qweight, wscales, proj_up, bias, x.shape[0], out)
+    return gemm_launch(q, asc, lora, as_codes(qweight, x.shape[1]), wscales, proj_up, bias, x.shape[0], out)
 
 
 @w4a4_linear.register_fake
@@ -135,10 +159,10 @@ def w4a4_gelu_mlp(x: torch.Tensor, qweight1: torch.Tensor, wscales1: torch.Tenso
     M = x.shape[0]
     q, asc, lora = act_quant_launch(x, smooth1, proj_down1)
     h = torch.empty(M, qweight1.shape[0], device=x.device, dtype=torch.bfloat16)
-    gemm_launch(q, asc, lora, qweight1, wscales1, proj_up1, bias1, M, h, EPI_GELU)
+    gemm_launch(q, asc, lora, as_codes(qweight1, x.shape[1]), wscales1, proj_up1, bias1, M, h, EPI_GELU)
     q2, asc2, lora2 = act_quant_launch(h, smooth2, proj_down2, GELU_SHIFT, True)
     out = torch.empty(M, qweight2.shape[0], device=x.device, dtype=torch.bfloat16)
-    return gemm_launch(q2, asc2, lora2, qweight2, wscales2, proj_up2, bias2, M, out)
+    return gemm_launch(q2, asc2, lora2, as_codes(qweight2, h.shape[1]), wscales2, proj_up2, bias2, M, out)
 
 
 @w4a4_gelu_mlp.register_fake

@@ -133,12 +133,18 @@ def gelu_mlp(x: torch.Tensor, t1: dict, t2: dict) -> torch.Tensor:
     return w4a4_gelu_mlp(x, *(t1[p] for p in PARTS), *(t2[p] for p in PARTS))
 
 
+def _operand(parts: dict, name: str):
+    """Module operands: packed weights on the GPU are expanded once to the GEMM's e4m3 codes [N, K]."""
+    t = parts[name]
+    return ops.weight_codes(t) if name == "qweight" and t.is_cuda else t
+
+
 class PackedW4A4Linear(torch.nn.Module):
     """A W4A4 linear layer over the parts of quantize (w4a4.py:220-231)."""
 
     def __init__(self, **parts):
         super().__init__()
-        self.parts = [parts[name] for name in PARTS]
+        self.parts = [_operand(parts, name) for name in PARTS]
         self.out_features = parts["proj_up"].shape[0]
 
     def forward(self, X):
@@ -151,7 +157,7 @@ class PackedW4A4GeluMLP(torch.nn.Module):
 
     def __init__(self, fc1, fc2):
         super().__init__()
-        self.parts = [fc1[name] for name in PARTS] + [fc2[name] for name in PARTS]
+        self.parts = [_operand(fc1, name) for name in PARTS] + [_operand(fc2, name) for name in PARTS]
         self.out_features = fc2["proj_up"].shape[0]
 
     def forward(self, X):
