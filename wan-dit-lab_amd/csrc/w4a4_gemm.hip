@@ -61,8 +61,6 @@ struct GemmArgs {
 // 16-byte quarters XOR-swizzled by (row / 4) % 4 (conflict-free operand reads). Each scale stage ends in 64 zero
 // bytes that lanes 32..63 read, which zeroes their half of the outer-product operands without a select.
 // Workgroup ids are remapped so that the tiles of one weight slab run on one XCD.
-constexpr int STAGES = 4;
-
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return uint32_t(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
 }
@@ -83,10 +81,82 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-template <int BN, int BM, int WN, int WM, int NW, int EPI>
+// Low-rank branch, bias and epilogue of one wave's TN x TM subtiles (rows nb0 + 32 i + .., tokens mb0 + 32 j + ..);
+// only >= 0 restricts the work to the subtile row i == only.
+template <int TN, int TM, int EPI>
+__device__ __forceinline__ void finish_tile(const GemmArgs& p, f32x16 (&acc)[TN][TM], int64_t nb0, int64_t mb0,
+                                            int lane, int only) {
+    // low-rank branch: acc += pu[n] . bf16(lora[m]) over r = 0..31, two 32x32x16 bf16 MFMAs per subtile
+    if (p.lora) {
+#pragma unroll
+        for (int i = 0; i < TN; ++i) {
+            if (only >= 0 && i != only) continue;
+            const int64_t n = nb0 + i * 32 + lane % 32;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const bf16x8 pa = *reinterpret_cast<const bf16x8*>(p.pu + n * 32 + h * 16 + 8 * (lane / 32));
+#pragma unroll
+                for (int j = 0; j < TM; ++j) {
+                    const int64_t m = mb0 + j * 32 + lane % 32;
+                    const float* lr = p.lora + m * 32 + h * 16 + 8 * (lane / 32);
+                    bf16x8 lb;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) lb[e] = __builtin_bit_cast(__bf16, f32_to_bf16(lr[e]));
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa, lb, acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    // epilogue
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int j = 0; j < TM; ++j) {
+            if (only >= 0 && i != only) continue;
+            const int64_t m = mb0 + j * 32 + lane % 32;
+            if (m >= p.M) continue;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int64_t nb = nb0 + i * 32 + 8 * q + 4 * (lane / 32);
+                float y[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    y[e] = acc[i][j][4 * q + e];
+                    if (p.bias) y[e] = y[e] + bf16_to_f32(p.bias[nb + e]);
+                }
+                if (EPI == EPI_F32) {
+                    float* o = static_cast<float*>(p.out) + m * p.ldo + nb;
+                    *reinterpret_cast<float4*>(o) = make_float4(y[0], y[1], y[2], y[3]);
+                } else {
+                    uint16_t* o = static_cast<uint16_t*>(p.out) + m * p.ldo + nb;
+                    uint16_t r[4];
+                    if (EPI == EPI_RESIDUAL) {
+                        const uint2 old = *reinterpret_cast<const uint2*>(o);
+                        const uint16_t ov[4] = {uint16_t(old.x), uint16_t(old.x >> 16), uint16_t(old.y),
+                                                uint16_t(old.y >> 16)};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float yb = bf16_to_f32(f32_to_bf16(y[e]));
+                            r[e] = f32_to_bf16(bf16_to_f32(ov[e]) + yb * p.gate[nb + e]);
+                        }
+                    } else if (EPI == EPI_GELU) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) r[e] = f32_to_bf16(gelu_tanh(y[e]));
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) r[e] = f32_to_bf16(y[e]);
+                    }
+                    *reinterpret_cast<uint2*>(o) = make_uint2(r[0] | (uint32_t(r[1]) << 16), r[2] | (uint32_t(r[3]) << 16));
+                }
+            }
+        }
+}
+
+template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES>
 __global__ __launch_bounds__(NW * 64) void w4a4_gemm_kernel(GemmArgs p) {
     static_assert((BN / WN) * (BM / WM) == NW, "wave grid");
-    static_assert(STAGES == 4, "the main loop is unrolled by 4 stages");
+    static_assert(STAGES >= 3 && STAGES <= 8, "ring depth");
     constexpr int TN = WN / 32, TM = WM / 32;
     constexpr int XI = BM * 4 / 64 / NW;   // 16-byte loads per wave per group: activation codes
     constexpr int WI = BN * 4 / 64 / NW;   // and weight codes
@@ -213,122 +283,45 @@ __global__ __launch_bounds__(NW * 64) void w4a4_gemm_kernel(GemmArgs p) {
             }
     };
 
-    // Ring step for group g on stage g % 4: wait until this wave's loads of groups <= g have landed (groups g + 1
-    // and g + 2 may still be in flight) and for every wave (barrier); the stage of group g - 1 is free again:
-    // issue group g + 3 into it; multiply group g.
-    issue(0, 0);
-    issue(1, 1);
-    issue(2, 2);
-    for (int64_t g = 0; g < G; g += 4) {
-        wait_vmcnt<2 * LPG>();
-        __syncthreads();
-        issue(3, g + 3);
-        multiply(0);
-        if (g + 1 >= G) break;
-        wait_vmcnt<2 * LPG>();
-        __syncthreads();
-        issue(0, g + 4);
-        multiply(1);
-        if (g + 2 >= G) break;
-        wait_vmcnt<2 * LPG>();
-        __syncthreads();
-        issue(1, g + 5);
-        multiply(2);
-        if (g + 3 >= G) break;
-        wait_vmcnt<2 * LPG>();
-        __syncthreads();
-        issue(2, g + 6);
-        multiply(3);
+    // Ring step for group g on stage g % STAGES: wait until this wave's loads of groups <= g have landed (the
+    // STAGES - 2 groups after it may still be in flight) and for every wave (barrier); the stage of group g - 1 is
+    // free again: issue group g + STAGES - 1 into it; multiply group g. Unrolled by STAGES (constant stages).
+#pragma unroll
+    for (int k = 0; k < STAGES - 1; ++k) issue(k, k);
+    for (int64_t g = 0; g < G; g += STAGES) {
+#pragma unroll
+        for (int k = 0; k < STAGES; ++k) {
+            if (g + k >= G) break;
+            wait_vmcnt<(STAGES - 2) * LPG>();
+            __syncthreads();
+            issue((k + STAGES - 1) % STAGES, g + k + STAGES - 1);
+            multiply(k);
+        }
     }
     wait_vmcnt<0>();  // the clamped tail loads land before the workgroup can end
 
-    // low-rank branch: acc += pu[n] . bf16(lora[m]) over r = 0..31, two 32x32x16 bf16 MFMAs per subtile
-    if (p.lora) {
-#pragma unroll
-        for (int i = 0; i < TN; ++i) {
-            const int64_t n = n0 + wn * WN + i * 32 + lane % 32;
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const bf16x8 pa = *reinterpret_cast<const bf16x8*>(p.pu + n * 32 + h * 16 + 8 * (lane / 32));
-#pragma unroll
-                for (int j = 0; j < TM; ++j) {
-                    const int64_t m = m0 + wm * WM + j * 32 + lane % 32;
-                    const float* lr = p.lora + m * 32 + h * 16 + 8 * (lane / 32);
-                    bf16x8 lb;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) lb[e] = __builtin_bit_cast(__bf16, f32_to_bf16(lr[e]));
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa, lb, acc[i][j], 0, 0, 0);
-                }
-            }
-        }
-    }
-
-    // epilogue
-#pragma unroll
-    for (int i = 0; i < TN; ++i)
-#pragma unroll
-        for (int j = 0; j < TM; ++j) {
-            const int64_t m = m0 + wm * WM + j * 32 + lane % 32;
-            if (m >= p.M) continue;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int64_t nb = n0 + wn * WN + i * 32 + 8 * q + 4 * (lane / 32);
-                float y[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    y[e] = acc[i][j][4 * q + e];
-                    if (p.bias) y[e] = y[e] + bf16_to_f32(p.bias[nb + e]);
-                }
-                if (EPI == EPI_F32) {
-                    float* o = static_cast<float*>(p.out) + m * p.ldo + nb;
-                    *reinterpret_cast<float4*>(o) = make_float4(y[0], y[1], y[2], y[3]);
-                } else {
-                    uint16_t* o = static_cast<uint16_t*>(p.out) + m * p.ldo + nb;
-                    uint16_t r[4];
-                    if (EPI == EPI_RESIDUAL) {
-                        const uint2 old = *reinterpret_cast<const uint2*>(o);
-                        const uint16_t ov[4] = {uint16_t(old.x), uint16_t(old.x >> 16), uint16_t(old.y),
-                                                uint16_t(old.y >> 16)};
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const float yb = bf16_to_f32(f32_to_bf16(y[e]));
-                            r[e] = f32_to_bf16(bf16_to_f32(ov[e]) + yb * p.gate[nb + e]);
-                        }
-                    } else if (EPI == EPI_GELU) {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) r[e] = f32_to_bf16(gelu_tanh(y[e]));
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) r[e] = f32_to_bf16(y[e]);
-                    }
-                    *reinterpret_cast<uint2*>(o) = make_uint2(r[0] | (uint32_t(r[1]) << 16), r[2] | (uint32_t(r[3]) << 16));
-                }
-            }
-        }
+    finish_tile<TN, TM, EPI>(p, acc, n0 + wn * WN, m0 + wm * WM, lane, -1);
 }
 
-template <int BN, int BM, int WN, int WM, int NW>
+template <int BN, int BM, int WN, int WM, int NW, int ST>
 int launch(const GemmArgs& a, int epi, hipStream_t stream) {
     if (a.N % BN || a.Mp % BM) return fail(WDL_EINVAL, "w4a4_gemm: tile %dx%d does not divide N=%lld Mp=%lld", BN, BM,
                                            (long long)a.N, (long long)a.Mp);
     const unsigned grid = unsigned((a.N / BN) * (a.Mp / BM));
     switch (epi) {
-        case EPI_BF16: w4a4_gemm_kernel<BN, BM, WN, WM, NW, EPI_BF16><<<grid, NW * 64, 0, stream>>>(a); break;
-        case EPI_F32: w4a4_gemm_kernel<BN, BM, WN, WM, NW, EPI_F32><<<grid, NW * 64, 0, stream>>>(a); break;
-        case EPI_RESIDUAL: w4a4_gemm_kernel<BN, BM, WN, WM, NW, EPI_RESIDUAL><<<grid, NW * 64, 0, stream>>>(a); break;
-        case EPI_GELU: w4a4_gemm_kernel<BN, BM, WN, WM, NW, EPI_GELU><<<grid, NW * 64, 0, stream>>>(a); break;
+        case EPI_BF16: w4a4_gemm_kernel<BN, BM, WN, WM, NW, EPI_BF16, ST><<<grid, NW * 64, 0, stream>>>(a); break;
+        case EPI_F32: w4a4_gemm_kernel<BN, BM, WN, WM, NW, EPI_F32, ST><<<grid, NW * 64, 0, stream>>>(a); break;
+        case EPI_RESIDUAL: w4a4_gemm_kernel<BN, BM, WN, WM, NW, EPI_RESIDUAL, ST><<<grid, NW * 64, 0, stream>>>(a); break;
+        case EPI_GELU: w4a4_gemm_kernel<BN, BM, WN, WM, NW, EPI_GELU, ST><<<grid, NW * 64, 0, stream>>>(a); break;
         default: return fail(WDL_EINVAL, "w4a4_gemm: bad epilogue %d", epi);
     }
     return check_launch("w4a4_gemm");
 }
 
-// tile configurations (BN x BM, waves): 0 = 128x128 (4 waves of 64x64), 1 = 256x128 (8 waves of 64x64)
-int dispatch(const GemmArgs& a, int epi, int config, hipStream_t stream) {
-    switch (config) {
-        case 1: return launch<256, 128, 64, 64, 8>(a, epi, stream);
-        default: return launch<128, 128, 64, 64, 4>(a, epi, stream);
-    }
-}
+// Tile configuration: 128 x 128 per workgroup, 4 waves of 64 x 64, a 4-stage ring (69 KB of LDS: two workgroups
+// per CU). Measured on the block shapes at 1392 and 2640 tokens against 6- and 8-stage rings (one workgroup per CU)
+// and an 8-wave even/odd split of the groups: this one is fastest on all of them.
+int dispatch(const GemmArgs& a, int epi, hipStream_t stream) { return launch<128, 128, 64, 64, 4, 4>(a, epi, stream); }
 
 // e4m3 codes of the two's complement nibbles 0..7 (values 0..7) and 8..15 (values -8..-1)
 constexpr uint32_t LUT0 = 0x44403800u, LUT1 = 0x4E4C4A48u, LUT2 = 0xCACCCED0u, LUT3 = 0xB8C0C4C8u;
@@ -379,7 +372,7 @@ extern "C" int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wc
                static_cast<const uint8_t*>(wcodes), static_cast<const uint16_t*>(wscales), lora,
                static_cast<const uint16_t*>(proj_up), static_cast<const uint16_t*>(bias), M, Mp, N, K, out, ldo,
                gate};
-    return dispatch(a, epilogue, 0, stream);  // 128x128 measured ahead of 256x128 on every block shape
+    return dispatch(a, epilogue, stream);
 }
 
 extern "C" int wdl_w4a4_weight_codes(const void* qweight, int64_t N, int64_t K, void* codes, hipStream_t stream) {
