@@ -191,11 +191,13 @@ def entropy_scale(keys: int, head_dim: int, ratio):
     return math.sqrt(math.log(keys) / math.log(keys * ratio) / head_dim)
 
 
-def attention_online(p: dict, sm_scale: float, block: int = 64) -> torch.Tensor:
+def attention_online(p: dict, sm_scale: float, block: int = 64, round_p: bool = True) -> torch.Tensor:
     """The blockwise online-softmax restatement of the HIP kernel's arithmetic (fp32): per 64-key block, s = fp32
     int dot * k_scale, running max m over s, P = 2^((s - m) * c) with c = q_scale * sm_scale * log2(e), P rounded
     to e4m3 after * 448, O = O * alpha + P_fp8 . V_fp8 (fp32), l = l * alpha + sum P (unrounded); out =
-    O / (l * 448) * v_scale. Its exp2 is torch's, not the hardware's: P can differ by an ulp before rounding."""
+    O / (l * 448) * v_scale. Its exp2 is torch's, not the hardware's: P can differ by an ulp before rounding.
+    round_p=False keeps P in fp32: then the result is the exact softmax of attention_quantized up to fp32 rounding
+    (the check that pins the online rescaling)."""
     q, k = p["q"].float(), p["k"].float()
     B, n, H, D = q.shape
     L = k.shape[1]
@@ -212,7 +214,7 @@ def attention_online(p: dict, sm_scale: float, block: int = 64) -> torch.Tensor:
         mn = torch.maximum(m, s.amax(-1))
         alpha = torch.exp2((m - mn) * c)
         P = torch.exp2(s * c[..., None] - (mn * c)[..., None])
-        Pq = (P * 448.0).to(torch.float8_e4m3fn).float()
+        Pq = (P * 448.0).to(torch.float8_e4m3fn).float() if round_p else P * 448.0
         O = O * alpha[..., None] + torch.einsum("bhnl,blhd->bhnd", Pq.double(), vq[:, b0:b1].double()).float()
         l = l * alpha + P.sum(-1)
         m = mn

@@ -51,3 +51,20 @@ def test_attention_emulation_close_to_exact():
     exact = osage.attention_exact(Q, p["K"], p["V"])
     assert osage.rel_err(osage.attention_quantized(p, 128 ** -0.5), exact) < 0.05
     assert osage.rel_err(osage.attention_quantized(p, 128 ** -0.5, p_fp8=True), exact) < 0.06
+
+
+def test_online_softmax_restatement_equals_exact_softmax():
+    """attention_online (the kernel's blockwise arithmetic) with P kept in fp32 equals the float64 softmax of the
+    same quantized operands (fp32 rounding only), for a key count that is not a multiple of the 64-key block; with
+    P rounded to e4m3 it sits at the fp8-P emulation's error against exact attention."""
+    g = torch.Generator().manual_seed(3)
+    Q = torch.randn(1, 48, 2, 128, generator=g).to(torch.bfloat16)
+    cache = (torch.randn(1, 150, 2, 128, generator=g) * 2).to(torch.float8_e4m3fn)
+    V = torch.randn(1, 48, 2, 128, generator=g).to(torch.bfloat16)
+    one = torch.ones(1, 150, 2, 1) * 0.5
+    p = osage.prep(Q, cache, one, cache, one, 102, Q * 0.7, V)
+    ref = osage.attention_quantized(p, 128 ** -0.5)
+    assert osage.rel_err(osage.attention_online(p, 128 ** -0.5, round_p=False), ref) < 1e-5
+    exact = osage.attention_exact(Q, p["K"], p["V"])
+    e_fp8 = osage.rel_err(osage.attention_quantized(p, 128 ** -0.5, p_fp8=True), exact)
+    assert osage.rel_err(osage.attention_online(p, 128 ** -0.5), exact) <= 1.2 * e_fp8 + 1e-3
