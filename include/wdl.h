@@ -80,13 +80,15 @@ int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wcodes, const
 /* Q/K RMSNorm over all heads + 3D RoPE, fused. Replaces norm_q / norm_k (src/wan_dit_lab/models/rms_norm.py:10-13,
  * used at src/wan_dit_lab/quantization/w4a4.py:256-257) and rope_apply / wan_dit_lab::rope3d_rotate
  * (src/wan_dit_lab/models/rope.py:12-31; src/wan_dit_lab/kernels/rope_triton.py:66-81, 101-144).
- * q, k: bf16 [M, heads*128] with row strides ldq, ldk; wq, wk: bf16 [heads*128]; freq: fp32 [2, positions, 64]
- * (cos, sin; pairs split [22 time, 21 height, 21 width]); grid (f, h, w) with f*h*w <= M, time offset start_frame.
- * Row m: n = bf16(x * rstd), y = bf16(n * w); pairs of rows m < f*h*w rotated at (start_frame + m/(h*w),
- * (m/w)%h, m%w) in fp32, results bf16 into q_out, k_out [M, heads*128] (row stride ldo). */
+ * q, k: bf16 [M, heads*128] with row strides ldq, ldk; wq, wk: bf16 [heads*128] or NULL (then that input is only
+ * rotated: rope_apply alone); k may be NULL (q only). freq: [2, positions, 64] (cos, sin; pairs split [22 time,
+ * 21 height, 21 width]) of type freq_dtype (0 fp32, 3 fp64); grid (f, h, w) with f*h*w <= M, time offset
+ * start_frame. Row m: n = bf16(x * rstd), y = bf16(n * w); pairs of rows m < f*h*w rotated at (start_frame +
+ * m/(h*w), (m/w)%h, m%w) in the table's precision (fp64 results rounded to fp32, then bf16), results bf16 into
+ * q_out, k_out [M, heads*128] (row stride ldo). */
 int wdl_qk_norm_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* wq, const void* wk,
-                     const float* freq, int64_t positions, int64_t M, int64_t heads, int f, int h, int w,
-                     int start_frame, float eps, void* q_out, void* k_out, int64_t ldo, wdl_stream_t stream);
+                     const void* freq, int freq_dtype, int64_t positions, int64_t M, int64_t heads, int f, int h,
+                     int w, int start_frame, float eps, void* q_out, void* k_out, int64_t ldo, wdl_stream_t stream);
 
 /* Sage per-thread int8 quantization of Q. Replaces sage_kv.quant_q (src/wan_dit_lab/kernels/sage_kv.py:112-124).
  * x: bf16 [n, heads, 128] (token stride ldx); q: int8 [n, heads, 128]; q_scale: fp32 [heads, ceil(n/128)*32].

@@ -25,7 +25,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     for name in declared():
         assert hasattr(lib, name), name
     assert set(declared()) == set(_lib.SIGNATURES)
-    assert lib.wdl_abi_version() == 1
+    assert lib.wdl_abi_version() == 2
     assert lib.wdl_last_error() == b""
 
 
@@ -38,3 +38,37 @@ def test_invalid_call_reports_error_without_launch():
     rc = lib.wdl_kv_append_fp8(None, 2, strides, None, 2, strides, 1, 4, 1, 8, None, None, None, None, 3, 0, None)
     assert rc == 1
     assert b"exceeds capacity" in lib.wdl_last_error()
+
+
+def test_live_operator_names_carry_the_reference_schemas():
+    """wdl.live registers live::w4a4_linear / live::w4a4_gelu_mlp with the argument lists of
+    native/ops/w4a4_ops.cpp:79-85, and their fake kernels give the reference's output shapes."""
+    import torch
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    import wdl.live  # noqa: F401
+
+    lin = str(torch.ops.live.w4a4_linear.default._schema)
+    assert "x, Tensor qweight, Tensor wscales, Tensor proj_down, Tensor proj_up, Tensor smooth, Tensor bias" in lin
+    mlp = str(torch.ops.live.w4a4_gelu_mlp.default._schema)
+    assert "qweight1" in mlp and "bias2" in mlp
+    with FakeTensorMode():
+        x = torch.empty(10, 128, dtype=torch.bfloat16)
+        q = torch.empty(64, 64, dtype=torch.uint8)
+        y = torch.ops.live.w4a4_linear(x, q, torch.empty(2, 64), torch.empty(32, 128), torch.empty(64, 32),
+                                       torch.empty(128), torch.empty(64))
+        assert y.shape == (10, 64) and y.dtype == torch.bfloat16
+
+
+def test_weight_operand_shapes_are_checked_before_any_launch():
+    import pytest
+    import torch
+
+    from wdl import ops
+
+    with pytest.raises(ValueError):
+        ops.as_codes(torch.zeros(4, 48, dtype=torch.uint8), 128)
+    with pytest.raises(TypeError):
+        ops.as_codes(torch.zeros(4, 64, dtype=torch.float32), 128)
+    codes = torch.zeros(4, 128, dtype=torch.uint8)
+    assert ops.as_codes(codes, 128) is not None

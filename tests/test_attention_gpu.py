@@ -155,3 +155,100 @@ def test_rope_identities_on_gpu(gpu):
     a = whole.float().reshape(M, H, 64, 2).square().sum(-1)
     b = plain.float().reshape(M, H, 64, 2).square().sum(-1)
     assert torch.allclose(a, b, rtol=2 ** -6, atol=1e-3)
+
+
+@pytest.mark.parametrize("table", ["fp32", "fp64"])
+def test_rope_apply_bit_exact_with_padding_and_batch(gpu, table):
+    """wdl.rope.rope_apply (rope.py:12-31 / rope3d_rotate) against the oracle's rope_apply: bf16 X [2, L, H, 128]
+    with L past the grid (padding rows copied), a chunk offset, an fp32 or an fp64 table (the fp64 products are
+    rounded to fp32, then bf16, as torch converts double to bfloat16)."""
+    from wdl import rope
+
+    g = torch.Generator().manual_seed(21)
+    grid, start, L, H = (2, 3, 5), 7, 34, 3
+    X = (torch.randn(2, L, H, 128, generator=g) * 3).to(torch.bfloat16)
+    freq = orope.freqs(128, 64, torch.float64)
+    if table == "fp32":
+        freq = freq.float()
+    got = rope.rope_apply(X.cuda(), [grid], freq.cuda(), start).cpu()
+    for b in range(2):
+        want = orope.rope_apply(X[b:b + 1], grid, freq, start)
+        assert torch.equal(got[b:b + 1], want)
+    assert torch.equal(got[:, 30:], X[:, 30:])
+    with pytest.raises(ValueError):
+        rope.rope_apply(X.cuda(), [(3, 3, 5)], freq.cuda(), start)
+
+
+@pytest.mark.parametrize("cached", [False, True])
+def test_fused_qkv_attention_module_matches_oracle(gpu, cached):
+    """FusedQKVAttention (w4a4.py:246-262) on the HIP path, dim 256, 2 heads, grid (2, 4, 6), with and without an
+    FP8 cache of 96 prior tokens:
+    - wiring: bit-equal to the forward of the reference written out with the same wdl ops;
+    - the attention stage, fed the oracle's own Q, K, V: cosine >= 0.99999 and relative L2 <= 2e-3 against the
+      oracle's blockwise attention (the config-1 stage bar);
+    - end to end against the oracle composition: relative L2 <= 2e-2 (the W4A4 o projection re-quantizes the
+      attention output to int4, so its ~1e-3 differences flip codes: measured ~7e-3)."""
+    from oracle import block as oblock
+    from wdl import rope, sage_kv, w4a4
+    from wdl.kvcache import KVCache
+
+    g = torch.Generator().manual_seed(5)
+    dim, H, grid, start, prior = 256, 2, (2, 4, 6), 3, 96
+    P = oblock.quantize_block(oblock.random_block(dim, 512, g))
+    M = grid[0] * grid[1] * grid[2]
+    X = torch.randn(1, M, dim, generator=g).to(torch.bfloat16)
+    freq = orope.freqs(128, 64, torch.float64).float()
+    dev = torch.device("cuda")
+    m = w4a4.FusedQKVAttention(dim, H)
+    m.qkv = w4a4.PackedW4A4Linear(**w4a4.pack_parts(P["qkv"], dev))
+    m.o = w4a4.PackedW4A4Linear(**w4a4.pack_parts(P["o"], dev))
+    m.norm_q, m.norm_k = P["wq"].to(torch.bfloat16).to(dev), P["wk"].to(torch.bfloat16).to(dev)
+    ck = (torch.randn(1, prior + M, H, 128, generator=g) * 50).clamp(-448, 448).to(torch.float8_e4m3fn)
+    cks = torch.rand(1, prior + M, H, 1, generator=g) * 0.02
+
+    def new_cache():
+        if not cached:
+            return None
+        c = KVCache(prior, 0, chunk=grid[0])
+        c.allocate(torch.empty(1, M, H, 128, device=dev))
+        c.k.copy_(ck.to(dev)), c.v.copy_(ck.to(dev)), c.ks.copy_(cks.to(dev)), c.vs.copy_(cks.to(dev))
+        c.saved = prior
+        return c
+
+    got = m(X.to(dev), [grid], freq.to(dev), start_frame=start, cache=new_cache())
+    # the reference's forward, written out with the same ops
+    Xd = X.to(dev)
+    q, k, v = m.qkv(Xd).split(dim, dim=-1)
+    Qw, Kw = rope.norm_rope(q[0], k[0], m.norm_q, m.norm_k, freq.to(dev), grid, start)
+    shape = (1, M, H, 128)
+    c = new_cache()
+    if c is not None:
+        Aw = c.attend(Qw.view(shape), Kw.view(shape), v[0].reshape(shape))
+    else:
+        z8 = torch.zeros(1, 1, H, 128, device=dev, dtype=torch.float8_e4m3fn)
+        one = torch.ones(1, 1, H, 1, device=dev)
+        Aw = sage_kv.attend(Qw.view(shape), z8, one, z8, one, 0, Kw.view(shape), v[0].reshape(shape))
+    assert torch.equal(got, m.o(Aw.reshape(1, M, dim)))
+    # the oracle
+    qkv = oblock._lin(X[0], P["qkv"]).to(torch.bfloat16)
+    Q = orope.rope_apply(oblock._rms(qkv[:, :dim], P["wq"]).reshape(1, M, H, 128), grid, freq, start)
+    K = orope.rope_apply(oblock._rms(qkv[:, dim:2 * dim], P["wk"]).reshape(1, M, H, 128), grid, freq, start)
+    V = qkv[:, 2 * dim:].contiguous()
+    ocache = dict(k=ck, ks=cks, v=ck, vs=cks, at=prior) if cached else None
+    # the cache rows [0, at) and the chunk's own bf16 K, V enter the attention (rows >= at are not read)
+    A = oblock.attention(Q.reshape(M, dim), ocache, K.reshape(M, dim), V, H)
+    c = new_cache()
+    Qd, Kd, Vd = (t.reshape(shape).to(dev) for t in (Q, K, V))
+    if c is not None:
+        Ag = c.attend(Qd, Kd, Vd)
+    else:
+        z8 = torch.zeros(1, 1, H, 128, device=dev, dtype=torch.float8_e4m3fn)
+        one = torch.ones(1, 1, H, 1, device=dev)
+        Ag = sage_kv.attend(Qd, z8, one, z8, one, 0, Kd, Vd)
+    Ag = Ag.cpu().reshape(M, dim)
+    rel = lambda a, b: float((a.float() - b.float()).norm() / b.float().norm())
+    assert rel(Ag, A) <= 2e-3 and osage.cosine(Ag, A) >= 0.99999
+    want = oblock._lin(A, P["o"]).to(torch.bfloat16)
+    e2e = rel(got.cpu().reshape(M, dim), want)
+    print(f"cached={cached}: attention stage rel {rel(Ag, A):.2e}, end to end rel-L2 {e2e:.2e}")
+    assert e2e <= 2e-2

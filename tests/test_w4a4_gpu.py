@@ -231,3 +231,18 @@ def test_linear_end_to_end_matches_oracle(gpu):
     ref = ow.linear_parts(x, ref_t)[0]
     diff = (y.cpu().double() - ref).abs()
     assert torch.all(diff <= ref.abs() * 2 ** -8 + 1e-4 * float(ref.abs().max()))
+
+
+def test_live_names_module_and_bare_op_agree(gpu):
+    """torch.ops.live.w4a4_linear (the reference's call site), PackedW4A4Linear (weights expanded once) and
+    wdl::w4a4_linear on packed nibbles (expanded per call) give the same bits."""
+    from wdl import w4a4
+    import wdl.live  # noqa: F401
+
+    g = torch.Generator(device="cuda").manual_seed(11)
+    t = w4a4.random_parts(384, 512, "cuda", g)
+    x = torch.randn(200, 512, device="cuda", generator=g).to(torch.bfloat16)
+    a = torch.ops.live.w4a4_linear(x, *(t[p] for p in w4a4.PARTS))
+    b = w4a4.PackedW4A4Linear(**t)(x)
+    c = w4a4.linear(x, t)
+    assert torch.equal(a, b) and torch.equal(a, c)

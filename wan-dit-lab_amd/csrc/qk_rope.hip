@@ -5,9 +5,12 @@
 //   rstd = 1 / sqrt(mean(x^2) + eps)     fp32; ordered sum: lane l owns the 8-value chunks c = l, l + 64, ... and
 //                                       adds their squares value by value, then an xor butterfly 32, 16, .., 1
 //   n   = bf16(x * rstd);  w = bf16(n * weight)                                (models/rms_norm.py:12-13)
-//   rot = bf16(w1 c - w2 s), bf16(w2 c + w1 s) on pairs (2p, 2p+1)             (models/rope.py:26-31, fp32)
-// with pair p of a head on the time axis for p < 22, height for p < 43, width otherwise; the token's position is
-// (start_frame + m / (h w), (m / w) % h, m % w) and (c, s) = freq[0/1][position][p] (fp32 table [2, P, 64]).
+//   rot = bf16(w1 c - w2 s), bf16(w2 c + w1 s) on pairs (2p, 2p+1)             (models/rope.py:26-31)
+// in the table's precision: fp32 for an fp32 table; for an fp64 table the products and differences are fp64 and the
+// result is rounded to fp32, then to bf16 (torch's double -> bfloat16 conversion goes through float). A null norm
+// weight skips the normalization of that input (rope_apply alone); a null k processes q only. Pair p of a head is
+// on the time axis for p < 22, height for p < 43, width otherwise; the token's position is
+// (start_frame + m / (h w), (m / w) % h, m % w) and (c, s) = freq[0/1][position][p] (table [2, P, 64]).
 // Rows m >= f h w (padding) are normalized but not rotated. Outputs are bf16 [M, H*D] (row stride ldo).
 //
 // quant_q: Sage's per-thread int8 Q (kernels/sage_kv.py:112-124): per 32-token block and head, lane l = 0..7 owns
@@ -27,7 +30,7 @@ struct NormRopeArgs {
     int64_t ldk;
     const uint16_t* wq;  // bf16 [H*D]
     const uint16_t* wk;
-    const float* freq;   // [2, P, D/2]
+    const void* freq;    // [2, P, D/2] fp32 or fp64
     int64_t P;
     int64_t M, C;        // rows, columns (H * D)
     int f, h, w, start;
@@ -35,6 +38,7 @@ struct NormRopeArgs {
     uint16_t* qo;
     uint16_t* ko;
     int64_t ldo;
+    int items;           // inputs per row: 2 (q and k) or 1 (q only)
 };
 
 __device__ __forceinline__ void load8(const uint16_t* p, float* f) {
@@ -47,15 +51,17 @@ __device__ __forceinline__ void load8(const uint16_t* p, float* f) {
     }
 }
 
+template <typename T>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs a) {
     const int lane = threadIdx.x % 64;
     const int64_t item = int64_t(blockIdx.x) * 4 + threadIdx.x / 64;  // (row, which)
-    if (item >= 2 * a.M) return;
-    const int64_t row = item / 2;
-    const int which = int(item % 2);
+    if (item >= a.items * a.M) return;
+    const int64_t row = item / a.items;
+    const int which = int(item % a.items);
     const uint16_t* src = (which == 0 ? a.q : a.k) + row * (which == 0 ? a.ldq : a.ldk);
     const uint16_t* wt = which == 0 ? a.wq : a.wk;
     uint16_t* dst = (which == 0 ? a.qo : a.ko) + row * a.ldo;
+    const T* freq = static_cast<const T*>(a.freq);
     const int64_t chunks = a.C / 8;
     float x[MAXCH][8];
 #pragma unroll
@@ -65,14 +71,17 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs a) {
         else
             for (int j = 0; j < 8; ++j) x[i][j] = 0.0f;
     }
-    float s = 0.0f;
+    float rstd = 1.0f;
+    if (wt) {
+        float s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < MAXCH; ++i)
+        for (int i = 0; i < MAXCH; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) s = s + x[i][j] * x[i][j];
+            for (int j = 0; j < 8; ++j) s = s + x[i][j] * x[i][j];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s = s + __shfl_xor(s, o);
-    const float rstd = 1.0f / sqrtf(s / float(a.C) + a.eps);
+        for (int o = 32; o > 0; o >>= 1) s = s + __shfl_xor(s, o);
+        rstd = 1.0f / sqrtf(s / float(a.C) + a.eps);
+    }
     const int64_t hw = int64_t(a.h) * a.w;
     const bool rot = row < int64_t(a.f) * hw;
     const int pos_t = a.start + int(row / hw);
@@ -84,28 +93,33 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs a) {
         const int64_t c = lane + 64 * i;
         if (c >= chunks) break;
         const int64_t col = c * 8;
-        float wf[8];
-        load8(wt + col, wf);
         float y[8];
+        if (wt) {
+            float wf[8];
+            load8(wt + col, wf);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float n = bf16_to_f32(f32_to_bf16(x[i][j] * rstd));
-            y[j] = bf16_to_f32(f32_to_bf16(n * wf[j]));
+            for (int j = 0; j < 8; ++j) {
+                const float n = bf16_to_f32(f32_to_bf16(x[i][j] * rstd));
+                y[j] = bf16_to_f32(f32_to_bf16(n * wf[j]));
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) y[j] = x[i][j];
         }
         uint16_t o[8];
 #pragma unroll
         for (int p2 = 0; p2 < 4; ++p2) {
-            const float x1 = y[2 * p2], x2 = y[2 * p2 + 1];
             if (rot) {
                 const int p = int((col + 2 * p2) % 128) / 2;
                 const int pos = p < tpairs ? pos_t : (p < tpairs + spairs ? pos_h : pos_w);
-                const float cs = a.freq[int64_t(pos) * half + p];
-                const float sn = a.freq[(a.P + pos) * half + p];
-                o[2 * p2] = f32_to_bf16(x1 * cs - x2 * sn);
-                o[2 * p2 + 1] = f32_to_bf16(x2 * cs + x1 * sn);
+                const T cs = freq[int64_t(pos) * half + p];
+                const T sn = freq[(a.P + pos) * half + p];
+                const T x1 = T(y[2 * p2]), x2 = T(y[2 * p2 + 1]);
+                o[2 * p2] = f32_to_bf16(float(x1 * cs - x2 * sn));
+                o[2 * p2 + 1] = f32_to_bf16(float(x2 * cs + x1 * sn));
             } else {
-                o[2 * p2] = f32_to_bf16(x1);
-                o[2 * p2 + 1] = f32_to_bf16(x2);
+                o[2 * p2] = f32_to_bf16(y[2 * p2]);
+                o[2 * p2 + 1] = f32_to_bf16(y[2 * p2 + 1]);
             }
         }
         *reinterpret_cast<uint4*>(dst + col) =
@@ -167,25 +181,30 @@ __global__ __launch_bounds__(256) void quant_q_kernel(const uint16_t* x, int64_t
 }  // namespace
 
 extern "C" int wdl_qk_norm_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* wq,
-                                const void* wk, const float* freq, int64_t positions, int64_t M, int64_t heads,
-                                int f, int h, int w, int start_frame, float eps, void* q_out, void* k_out,
-                                int64_t ldo, hipStream_t stream) {
+                                const void* wk, const void* freq, int freq_dtype, int64_t positions, int64_t M,
+                                int64_t heads, int f, int h, int w, int start_frame, float eps, void* q_out,
+                                void* k_out, int64_t ldo, hipStream_t stream) {
     const int64_t C = heads * 128;
-    if (M < 0 || heads <= 0 || ldq < C || ldk < C || ldo < C || f < 0 || h <= 0 || w <= 0 || start_frame < 0)
+    const int items = k ? 2 : 1;
+    if (M < 0 || heads <= 0 || ldq < C || (k && ldk < C) || ldo < C || f < 0 || h <= 0 || w <= 0 || start_frame < 0)
         return fail(WDL_EINVAL, "qk_norm_rope: bad shape");
+    if (freq_dtype != WDL_F32 && freq_dtype != WDL_F64) return fail(WDL_EINVAL, "qk_norm_rope: table must be fp32 or fp64");
     if (int64_t(f) * h * w > M) return fail(WDL_EINVAL, "qk_norm_rope: grid exceeds the rows");
     if (start_frame + f > positions || h > positions || w > positions)
         return fail(WDL_EINVAL, "qk_norm_rope: grid or offset exceeds the frequency table");
-    if (!q || !k || !wq || !wk || !freq || !q_out || !k_out) return fail(WDL_EINVAL, "qk_norm_rope: null pointer");
+    if (!q || !freq || !q_out || (k && !k_out)) return fail(WDL_EINVAL, "qk_norm_rope: null pointer");
     if (C > 64 * 8 * MAXCH) return fail(WDL_EINVAL, "qk_norm_rope: rows above 4096 values");
     if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(q_out) |
-         reinterpret_cast<uintptr_t>(k_out) | (ldq * 2) | (ldk * 2) | (ldo * 2)) % 16)
+         reinterpret_cast<uintptr_t>(k_out) | (ldq * 2) | (k ? ldk * 2 : 0) | (ldo * 2)) % 16)
         return fail(WDL_EINVAL, "qk_norm_rope: rows must be 16-byte aligned");
     if (M == 0) return WDL_OK;
     NormRopeArgs a{static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(k), ldk,
                    static_cast<const uint16_t*>(wq), static_cast<const uint16_t*>(wk), freq, positions, M, C,
-                   f, h, w, start_frame, eps, static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_out), ldo};
-    qk_norm_rope_kernel<<<unsigned((2 * M + 3) / 4), 256, 0, stream>>>(a);
+                   f, h, w, start_frame, eps, static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_out), ldo,
+                   items};
+    const unsigned grid = unsigned((items * M + 3) / 4);
+    if (freq_dtype == WDL_F64) qk_norm_rope_kernel<double><<<grid, 256, 0, stream>>>(a);
+    else qk_norm_rope_kernel<float><<<grid, 256, 0, stream>>>(a);
     return check_launch("qk_norm_rope");
 }
 

@@ -29,8 +29,8 @@ SIGNATURES: dict[str, list] = {
     "wdl_w4a4_weight_codes": [c_ptr, c_i64, c_i64, c_ptr, c_ptr],
     "wdl_w4a4_gemm": [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_ptr,
                       c_i64, c_int, c_ptr, c_ptr],
-    "wdl_qk_norm_rope": [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_int, c_int, c_int,
-                         c_int, c_f32, c_ptr, c_ptr, c_i64, c_ptr],
+    "wdl_qk_norm_rope": [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_int, c_i64, c_i64, c_i64, c_int, c_int,
+                         c_int, c_int, c_f32, c_ptr, c_ptr, c_i64, c_ptr],
     "wdl_quant_q": [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr],
     "wdl_sage_prep_workspace_floats": [c_i64, c_int],
     "wdl_sage_prep": [c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_i64, c_i64, c_i64, c_i64, c_int,

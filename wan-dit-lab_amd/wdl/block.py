@@ -56,7 +56,7 @@ class QuantizedWanBlock:
         """Cross-attention keys and values of a prompt, once per prompt (multi_head_attention.py:21-26;
         causal.Stream.cross, causal.py:557-568): K = RMSNorm(k(C)), V = v(C), then Sage's int8 K / fp8 V."""
         Kc = self.linear(C, "ck")
-        Kn, _ = ops.qk_norm_rope_launch(Kc, Kc, self.p["cwk"], self.p["cwk"], self._nofreq(C.device), (0, 1, 1), 0,
+        Kn, _ = ops.qk_norm_rope_launch(Kc, None, self.p["cwk"], None, self._nofreq(C.device), (0, 1, 1), 0,
                                         self.eps)
         Vc = self.linear(C, "cv")
         H = self.heads
@@ -90,7 +90,7 @@ class QuantizedWanBlock:
         qc = torch.empty(M, D, device=dev, dtype=torch.bfloat16)
         n3 = dict(weight=self.p["n3w"], bias=self.p["n3b"], eps=self.eps)
         self._gemm(self._quant(X, "cq", ln=n3), "cq", M, qc)
-        Qc, _ = ops.qk_norm_rope_launch(qc, qc, self.p["cwq"], self.p["cwq"], self._nofreq(dev), (0, 1, 1), 0,
+        Qc, _ = ops.qk_norm_rope_launch(qc, None, self.p["cwq"], None, self._nofreq(dev), (0, 1, 1), 0,
                                         self.eps)
         q_i8, q_sc = ops.quant_q_launch(Qc, H)
         Ac = ops.sage_attn_launch(q_i8, q_sc, ctx, ctx["L"], 128 ** -0.5)

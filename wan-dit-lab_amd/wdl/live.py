@@ -1,0 +1,57 @@
+"""`live::` operator names over libwdl, for code written against the reference's native ops.
+
+The reference registers `live::w4a4_linear` and `live::w4a4_gelu_mlp` from Nunchaku-based DLLs
+(src/wan_dit_lab/kernels/operators.py:12-24; native/ops/w4a4_ops.cpp:79-95) and calls them as
+`torch.ops.live.w4a4_linear(...)` (quantization/w4a4.py:212-213, 242-245). Importing this module registers the same
+names and schemas over this build's HIP kernels, so those call sites run unchanged on MI355X, given weights packed
+by wdl.w4a4.quantize (this build's layout; Nunchaku's tile order is not reproduced).
+
+`live::sage_sm89` is not aliased: its operands are laid out for SageAttention's sm89 kernel. The attention swap
+point is one level up, `sage_kv.attend` / `KVCache.attend` (kernels/sage_kv.py:127-134; generation/causal.py:193-
+220), whose replacement is wdl.sage_kv.attend / wdl.kvcache.KVCache.attend (see load()).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from wdl import ops
+
+__all__ = ["load", "w4a4_linear", "w4a4_gelu_mlp"]
+
+
+@torch.library.custom_op("live::w4a4_linear", mutates_args=())
+def w4a4_linear(x: torch.Tensor, qweight: torch.Tensor, wscales: torch.Tensor, proj_down: torch.Tensor,
+                proj_up: torch.Tensor, smooth: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    """live::w4a4_linear (w4a4_ops.cpp:31-40, 79-80) on libwdl."""
+    return ops.w4a4_linear(x, qweight, wscales, proj_down, proj_up, smooth, bias)
+
+
+@w4a4_linear.register_fake
+def _(x, qweight, wscales, proj_down, proj_up, smooth, bias):
+    return x.new_empty(x.shape[0], qweight.shape[0], dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("live::w4a4_gelu_mlp", mutates_args=())
+def w4a4_gelu_mlp(x: torch.Tensor, qweight1: torch.Tensor, wscales1: torch.Tensor, proj_down1: torch.Tensor,
+                  proj_up1: torch.Tensor, smooth1: torch.Tensor, bias1: torch.Tensor, qweight2: torch.Tensor,
+                  wscales2: torch.Tensor, proj_down2: torch.Tensor, proj_up2: torch.Tensor, smooth2: torch.Tensor,
+                  bias2: torch.Tensor) -> torch.Tensor:
+    """live::w4a4_gelu_mlp (w4a4_ops.cpp:44-63, 81-85) on libwdl."""
+    return ops.w4a4_gelu_mlp(x, qweight1, wscales1, proj_down1, proj_up1, smooth1, bias1, qweight2, wscales2,
+                             proj_down2, proj_up2, smooth2, bias2)
+
+
+@w4a4_gelu_mlp.register_fake
+def _(x, qweight1, wscales1, proj_down1, proj_up1, smooth1, bias1, qweight2, wscales2, proj_down2, proj_up2,
+      smooth2, bias2):
+    return x.new_empty(x.shape[0], qweight2.shape[0], dtype=torch.bfloat16)
+
+
+def load():
+    """The counterpart of operators.load() (kernels/operators.py:19-24): checks that libwdl.so is built (raises
+    FileNotFoundError otherwise, as the reference does for its DLLs) and returns torch.ops.live."""
+    from wdl import _lib
+
+    _lib.library()
+    return torch.ops.live

@@ -174,14 +174,18 @@ def _(x, qweight1, wscales1, proj_down1, proj_up1, smooth1, bias1, qweight2, wsc
 # ------------------------------------------------------------------------------------------------ Q/K norm + RoPE
 
 def qk_norm_rope_launch(q, k, wq, wk, freq, grid, start_frame, eps=1e-6, q_out=None, k_out=None):
-    """q, k bf16 [M, H*128] (row-strided views allowed) -> RMSNorm(all heads) + 3D RoPE, bf16 [M, H*128] each."""
+    """q, k bf16 [M, H*128] (row-strided views allowed) -> RMSNorm(all heads) + 3D RoPE, bf16 [M, H*128] each.
+    wq / wk None: that input is only rotated; k None: q alone (returns (q_out, None)). freq: contiguous fp32 or
+    fp64 [2, positions, 64]."""
     M, C = q.shape
     f, h, w = (int(v) for v in grid)
     q_out = torch.empty(M, C, device=q.device, dtype=torch.bfloat16) if q_out is None else q_out
-    k_out = torch.empty(M, C, device=q.device, dtype=torch.bfloat16) if k_out is None else k_out
-    _lib.call("wdl_qk_norm_rope", ptr(q), q.stride(0), ptr(k), k.stride(0), ptr(wq), ptr(wk), ptr(freq),
-              freq.shape[1], M, C // 128, f, h, w, int(start_frame), float(eps), ptr(q_out), ptr(k_out),
-              q_out.stride(0), stream_of(q))
+    if k is not None and k_out is None:
+        k_out = torch.empty(M, C, device=q.device, dtype=torch.bfloat16)
+    code = {torch.float32: 0, torch.float64: 3}[freq.dtype]
+    _lib.call("wdl_qk_norm_rope", ptr(q), q.stride(0), ptr(k), 0 if k is None else k.stride(0), ptr(wq), ptr(wk),
+              ptr(freq), code, freq.shape[1], M, C // 128, f, h, w, int(start_frame), float(eps), ptr(q_out),
+              ptr(k_out), q_out.stride(0), stream_of(q))
     return q_out, k_out
 
 

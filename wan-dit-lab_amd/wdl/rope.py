@@ -33,12 +33,36 @@ def freqs(dim: int = 128, positions: int = 1024, device=None) -> torch.Tensor:
     return f.to(torch.float32).contiguous().to(device)
 
 
+def _check_table(freq, grid, rows, start_frame):
+    if freq.dtype not in (torch.float32, torch.float64) or not freq.is_contiguous() or freq.ndim != 3 \
+            or freq.shape[0] != 2 or freq.shape[2] != 64:
+        raise TypeError("freq must be a contiguous fp32 or fp64 [2, positions, 64] table")
+    f, h, w = grid
+    if f * h * w > rows or start_frame < 0 or start_frame + f > freq.shape[1] or max(h, w) > freq.shape[1]:
+        raise ValueError("grid exceeds the rows or the frequency table")
+
+
 def norm_rope(q, k, wq, wk, freq, grid, start_frame=0, eps=1e-6):
     """q, k bf16 [M, H*128] (row-strided views of the QKV output allowed) -> (Q, K) bf16 [M, H*128]:
     bf16(bf16(x * rstd) * w) then the 3D rotation of the first f*h*w rows."""
-    if freq.dtype != torch.float32 or not freq.is_contiguous() or freq.ndim != 3 or freq.shape[0] != 2:
-        raise TypeError("freq must be a contiguous fp32 [2, positions, 64] table")
-    f, h, w = grid
-    if f * h * w > q.shape[0] or start_frame < 0 or start_frame + f > freq.shape[1]:
-        raise ValueError("grid exceeds the rows or the frequency table")
+    _check_table(freq, grid, q.shape[0], start_frame)
     return qk_norm_rope_launch(q, k, wq, wk, freq, grid, start_frame, eps)
+
+
+def rope_apply(X, grid_sizes, freq, start_frame=0):
+    """rope.py:12-31 / wan_dit_lab::rope3d_rotate (rope_triton.py:66-81) on MI355X: X bf16 [B, L, H, 128] (one
+    grid for the batch, grid_sizes[0] = (f, h, w)) -> a new bf16 tensor, tokens of the grid rotated in the table's
+    precision, tokens past f h w copied. The table: fp32 or fp64 [2, positions, 64] (rope()'s layout)."""
+    if X.dtype != torch.bfloat16 or X.dim() != 4 or X.shape[-1] != 128:
+        raise TypeError("X must be bf16 [B, L, H, 128]")
+    g = grid_sizes[0].tolist() if isinstance(grid_sizes, torch.Tensor) else grid_sizes[0]
+    f, h, w = (int(v) for v in g)
+    B, L, H, D = X.shape
+    _check_table(freq, (f, h, w), L, start_frame)
+    out = torch.empty(B, L, H, D, device=X.device, dtype=torch.bfloat16)
+    for b in range(B):
+        xb = X[b].reshape(L, H * D)
+        if xb.stride(1) != 1:
+            xb = xb.contiguous()
+        qk_norm_rope_launch(xb, None, None, None, freq, (f, h, w), start_frame, q_out=out[b].view(L, H * D))
+    return out

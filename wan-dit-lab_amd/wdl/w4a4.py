@@ -24,7 +24,8 @@ PARTS = ("qweight", "wscales", "proj_down", "proj_up", "smooth", "bias")  # w4a4
 MSE_STEPS = torch.linspace(0.5, 1.0, 26).tolist()
 
 __all__ = ["GROUP", "GELU_SHIFT", "PARTS", "int4_groups", "smoothing", "quantize", "pack_weight", "unpack_weight",
-           "linear", "gelu_mlp", "w4a4_linear", "w4a4_gelu_mlp", "PackedW4A4Linear", "PackedW4A4GeluMLP"]
+           "linear", "gelu_mlp", "w4a4_linear", "w4a4_gelu_mlp", "PackedW4A4Linear", "PackedW4A4GeluMLP",
+           "FusedQKVAttention"]
 
 
 @torch.no_grad()
@@ -163,6 +164,42 @@ class PackedW4A4GeluMLP(torch.nn.Module):
     def forward(self, X):
         y = w4a4_gelu_mlp(X.reshape(-1, X.shape[-1]).to(torch.bfloat16).contiguous(), *self.parts)
         return y.reshape(*X.shape[:-1], self.out_features)
+
+
+class FusedQKVAttention(torch.nn.Module):
+    """Self-attention with q, k, v as one W4A4 layer qkv [3 dim, dim] (w4a4.py:246-262): X quantized once, one GEMM,
+    then the fused Q/K RMSNorm + 3D RoPE kernel, the KVCache's Sage attention over the FP8 window (or, with no
+    cache, Sage attention over the chunk alone) and the W4A4 o projection. qkv / o: PackedW4A4Linear; norm_q /
+    norm_k: bf16 RMSNorm weights [dim]."""
+
+    def __init__(self, dim, num_heads, eps=1e-6):
+        super().__init__()
+        self.dim, self.num_heads, self.head_dim, self.eps = dim, num_heads, dim // num_heads, eps
+        self.qkv = self.o = None
+        self.norm_q = self.norm_k = None
+
+    def forward(self, X, grid_sizes=None, freq=None, context=None, start_frame=0, cache=None, context_kv=None):
+        from wdl import rope, sage_kv
+
+        assert context is None and context_kv is None, "q, k and v of one input: self-attention only"
+        if self.head_dim != 128:
+            raise ValueError("the MI355X kernels take heads of 128")
+        B, L = X.shape[0], X.shape[-2]
+        if B != 1:
+            raise ValueError("batch 1 (one chunk of one stream)")
+        qkv = self.qkv(X).reshape(L, 3 * self.dim)
+        g = grid_sizes[0].tolist() if isinstance(grid_sizes, torch.Tensor) else grid_sizes[0]
+        Q, K = rope.norm_rope(qkv[:, :self.dim], qkv[:, self.dim:2 * self.dim], self.norm_q, self.norm_k, freq,
+                              tuple(int(v) for v in g), start_frame, self.eps)
+        shape = (1, L, self.num_heads, self.head_dim)
+        V = qkv[:, 2 * self.dim:]
+        if cache is not None:
+            A = cache.attend(Q.view(shape), K.view(shape), V.reshape(shape))
+        else:
+            z8 = torch.zeros(1, 1, self.num_heads, 128, device=X.device, dtype=torch.float8_e4m3fn)
+            one = torch.ones(1, 1, self.num_heads, 1, device=X.device)
+            A = sage_kv.attend(Q.view(shape), z8, one, z8, one, 0, K.view(shape), V.reshape(shape))
+        return self.o(A.reshape(1, L, self.dim))
 
 
 def pack_parts(logical: dict, device=None) -> dict:
