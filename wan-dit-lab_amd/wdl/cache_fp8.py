@@ -45,11 +45,15 @@ def store_kv_fp8(k, v, cache_k, cache_ks, cache_v, cache_vs, at):
     store_kv_fp8_op(k, v, cache_k, cache_ks, cache_v, cache_vs, at)
 
 
-def install_cache_store():
-    """KVCache.store of wdl.kvcache through store_kv_fp8 for FP8 caches; returns the original method
-    (src/wan_dit_lab/kernels/cache_fp8.py:108-121)."""
-    from wdl.kvcache import KVCache
+def install_cache_store(cls=None):
+    """KVCache.store through store_kv_fp8 for FP8 caches; returns the original method
+    (src/wan_dit_lab/kernels/cache_fp8.py:108-121). cls: the cache class to patch (the reference's
+    generation.causal.KVCache, or by default wdl.kvcache.KVCache); it must keep fp8, k, ks, v, vs as the
+    reference's does (causal.py:159-163)."""
+    if cls is None:
+        from wdl.kvcache import KVCache as cls
 
+    KVCache = cls
     original = KVCache.store
 
     def store(cache, at, k, v):

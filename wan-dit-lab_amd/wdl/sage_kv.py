@@ -34,9 +34,12 @@ def _check(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V):
         raise ValueError("heads must be contiguous [.., heads, 128] rows")
 
 
-def attend(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, sm_scale=None):
+def attend(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, sm_scale=None, heads=None, tokens=None):
     """softmax(Q K^T * sm_scale) V over the cached tokens [0, at) and the chunk (sage_kv.py:127-134);
-    [1, nq, H, 128] bf16 (sm_scale defaults to 128^-0.5)."""
+    [1, nq, H, 128] bf16 (sm_scale defaults to 128^-0.5). The head and token maps of the static-head path
+    (KVCache.attend_split, causal.py:222-) are not implemented: passing them raises NotImplementedError."""
+    if heads is not None or tokens is not None:
+        raise NotImplementedError("head / token maps (static-head Forcing-KV attention) are not implemented")
     _check(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V)
     return sage_kv_attend(Q, cache_k.view(torch.uint8), cache_ks, cache_v.view(torch.uint8), cache_vs, K, V, at,
                           Q.shape[-1] ** -0.5 if sm_scale is None else float(sm_scale))
