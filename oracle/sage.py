@@ -191,32 +191,46 @@ def entropy_scale(keys: int, head_dim: int, ratio):
     return math.sqrt(math.log(keys) / math.log(keys * ratio) / head_dim)
 
 
-def attention_online(p: dict, sm_scale: float, block: int = 64, round_p: bool = True) -> torch.Tensor:
-    """The blockwise online-softmax restatement of the HIP kernel's arithmetic (fp32): per 64-key block, s = fp32
-    int dot * k_scale, running max m over s, P = 2^((s - m) * c) with c = q_scale * sm_scale * log2(e), P rounded
-    to e4m3 after * 448, O = O * alpha + P_fp8 . V_fp8 (fp32), l = l * alpha + sum P (unrounded); out =
-    O / (l * 448) * v_scale. Its exp2 is torch's, not the hardware's: P can differ by an ulp before rounding.
-    round_p=False keeps P in fp32: then the result is the exact softmax of attention_quantized up to fp32 rounding
-    (the check that pins the online rescaling)."""
+def attention_online(p: dict, sm_scale: float, block: int = 64, round_p: bool = True, splits: int = 2) -> torch.Tensor:
+    """The blockwise online-softmax restatement of the HIP kernel's arithmetic (fp32). In log2 units
+    y = int dot * k_scale * c with c = q_scale * sm_scale * log2(e). The key blocks are split in `splits`
+    contiguous parts (the first ceil(blocks / 2) blocks, then the rest, for two), each run as an online softmax:
+    per 64-key block the running max m over y, P448 = 2^(y - m + log2 448) rounded to e4m3 for the PV product,
+    O = O * 2^(m_old - m) + P448_fp8 . V_fp8 (fp32), l = l * 2^(m_old - m) + sum P448 (unrounded). The parts merge
+    as O = sum_i O_i 2^(m_i - m), l = sum_i l_i 2^(m_i - m) with m = max_i m_i, and out = O / l * v_scale. Its exp2
+    is torch's, not the hardware's: P can differ by an ulp before rounding. round_p=False keeps P in fp32: then the
+    result is the exact softmax of attention_quantized up to fp32 rounding (the check that pins the online
+    rescaling and the merge)."""
     q, k = p["q"].float(), p["k"].float()
     B, n, H, D = q.shape
     L = k.shape[1]
     c = (expand_q_scale(p["q_scale"], n).float() * (sm_scale * 1.4426950408889634)).permute(0, 2, 1)  # [B, H, n]
     ks = expand_k_scale(p["k_scale"], L).float().permute(0, 2, 1)  # [B, H, L]
     vq = p["v"].float()  # fp8 codes as values [B, L, H, D]
-    m = torch.full((B, H, n), float("-inf"))
-    l = torch.zeros(B, H, n)
-    O = torch.zeros(B, H, n, D)
-    for b0 in range(0, L, block):
-        b1 = min(L, b0 + block)
-        I = torch.einsum("bnhd,blhd->bhnl", q.double(), k[:, b0:b1].double()).float()
-        s = I * ks[:, :, None, b0:b1]
-        mn = torch.maximum(m, s.amax(-1))
-        alpha = torch.exp2((m - mn) * c)
-        P = torch.exp2(s * c[..., None] - (mn * c)[..., None])
-        Pq = (P * 448.0).to(torch.float8_e4m3fn).float() if round_p else P * 448.0
-        O = O * alpha[..., None] + torch.einsum("bhnl,blhd->bhnd", Pq.double(), vq[:, b0:b1].double()).float()
-        l = l * alpha + P.sum(-1)
-        m = mn
-    out = O / (l * 448.0)[..., None] * p["v_scale"].float()[:, :, None, :]
+    log2_448 = math.log2(448.0)
+    nblk = -(-L // block)
+    bounds = [0, -(-nblk // 2), nblk] if splits == 2 else [0, nblk]
+    parts = []
+    for s0, s1 in zip(bounds[:-1], bounds[1:]):
+        m = torch.full((B, H, n), float("-inf"))
+        l = torch.zeros(B, H, n)
+        O = torch.zeros(B, H, n, D)
+        for bi in range(s0, s1):
+            b0, b1 = bi * block, min(L, (bi + 1) * block)
+            I = torch.einsum("bnhd,blhd->bhnl", q.double(), k[:, b0:b1].double()).float()
+            y = I * ks[:, :, None, b0:b1] * c[..., None]
+            mn = torch.maximum(m, y.amax(-1))
+            alpha = torch.exp2(m - mn)
+            P = torch.exp2(y - mn[..., None] + log2_448)
+            Pq = P.to(torch.float8_e4m3fn).float() if round_p else P
+            O = O * alpha[..., None] + torch.einsum("bhnl,blhd->bhnd", Pq.double(), vq[:, b0:b1].double()).float()
+            l = l * alpha + P.sum(-1)
+            m = mn
+        parts.append((O, m, l))
+    mt = parts[0][1]
+    for _, mi, _ in parts[1:]:
+        mt = torch.maximum(mt, mi)
+    O = sum(Oi * torch.exp2(mi - mt)[..., None] for Oi, mi, _ in parts)
+    l = sum(li * torch.exp2(mi - mt) for _, mi, li in parts)
+    out = O / l[..., None] * p["v_scale"].float()[:, :, None, :]
     return out.permute(0, 2, 1, 3)
