@@ -194,7 +194,8 @@ def entropy_scale(keys: int, head_dim: int, ratio):
 def attention_online(p: dict, sm_scale: float, block: int = 64, round_p: bool = True, splits: int = 2) -> torch.Tensor:
     """The blockwise online-softmax restatement of the HIP kernel's arithmetic (fp32). In log2 units
     y = int dot * k_scale * c with c = q_scale * sm_scale * log2(e). The key blocks are split in `splits`
-    contiguous parts (the first ceil(blocks / 2) blocks, then the rest, for two), each run as an online softmax:
+    contiguous parts (for two: the first ceil(full blocks / 2) blocks, then the rest, a partial final block
+    included), each run as an online softmax:
     per 64-key block the running max m over y, P448 = 2^(y - m + log2 448) rounded to e4m3 for the PV product,
     O = O * 2^(m_old - m) + P448_fp8 . V_fp8 (fp32), l = l * 2^(m_old - m) + sum P448 (unrounded). The parts merge
     as O = sum_i O_i 2^(m_i - m), l = sum_i l_i 2^(m_i - m) with m = max_i m_i, and out = O / l * v_scale. Its exp2
@@ -208,8 +209,8 @@ def attention_online(p: dict, sm_scale: float, block: int = 64, round_p: bool = 
     ks = expand_k_scale(p["k_scale"], L).float().permute(0, 2, 1)  # [B, H, L]
     vq = p["v"].float()  # fp8 codes as values [B, L, H, D]
     log2_448 = math.log2(448.0)
-    nblk = -(-L // block)
-    bounds = [0, -(-nblk // 2), nblk] if splits == 2 else [0, nblk]
+    nblk, nfull = -(-L // block), L // block
+    bounds = [0, -(-nfull // 2), nblk] if splits == 2 else [0, nblk]
     parts = []
     for s0, s1 in zip(bounds[:-1], bounds[1:]):
         m = torch.full((B, H, n), float("-inf"))

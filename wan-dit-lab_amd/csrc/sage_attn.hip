@@ -104,12 +104,14 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
     const int64_t nks = a.Lpad / 16;
     for (int64_t i = t; i < nks; i += 512) sKs[i] = a.k_scale[h * nks + i];
 
-    // key blocks of this wave's group: [first, first + count); both groups run `iters` ring steps
-    const int64_t nblk = a.Lpad / 64, nb0 = (nblk + 1) / 2;
-    const int64_t first = grp == 0 ? 0 : nb0, count = grp == 0 ? nb0 : nblk - nb0;
+    // full key blocks of this wave's group: [first, first + count); both groups run `iters` ring steps. A ragged
+    // final block (L % 64 != 0) is group 1's, in a masked step after the ring.
+    const int64_t nblk = a.Lpad / 64;
+    const bool ragged = (a.L % 64) != 0;
+    const int64_t nfull = ragged ? nblk - 1 : nblk, nb0 = (nfull + 1) / 2;
+    const int64_t first = grp == 0 ? 0 : nb0, count = grp == 0 ? nb0 : nfull - nb0;
     const int64_t last = count > 0 ? first + count - 1 : 0;
     const int64_t iters = nb0;
-    const bool ragged = (a.L % 64) != 0;
 
     // this lane's load slots (block 0); block b adds b * 64 * D bytes of K, b * 64 bytes of V
     const int8_t* kbase = a.k + h * a.Lpad * D;
@@ -129,14 +131,16 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
             vsrc[j] = vbase + int64_t(ch) * a.Lpad + lq * 16;
         }
     }
-    auto issue = [&](int st, int64_t i) {  // ring step i's block (clamped to the group's last) into stage st
-        int64_t b = first + i;
-        b = b < last ? b : last;
+    auto load_block = [&](int st, int64_t b) {  // block b of this group's keys into stage st
         uint8_t* base = smem + st * STAGE + grp * GSTAGE;
 #pragma unroll
         for (int j = 0; j < 2; ++j) dma16(ksrc[j] + b * 64 * D, lds_addr(base + (sub * 2 + j) * 1024));
 #pragma unroll
         for (int j = 0; j < 2; ++j) dma16(vsrc[j] + b * 64, lds_addr(base + KT + (sub * 2 + j) * 1024));
+    };
+    auto issue = [&](int st, int64_t i) {  // ring step i's block (clamped to the group's last) into stage st
+        const int64_t b = first + i;
+        load_block(st, b < last ? b : last);
     };
 
     // per-lane LDS read offsets: K tile j, chunk c -> (c / 2) * 4096 + (32 j + lane % 32) * 64 + quarter;
@@ -235,14 +239,18 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
             wait_vmcnt<(STAGES - 2) * LPB>();
             __syncthreads();
             issue((k + STAGES - 1) % STAGES, i + STAGES - 1);
-            if (i < count) {
-                if (ragged && first + i == nblk - 1) compute(k, first + i, std::true_type{});
-                else compute(k, first + i, std::false_type{});
-            }
+            if (i < count) compute(k, first + i, std::false_type{});
         }
     }
     wait_vmcnt<0>();
-    __syncthreads();  // all loads landed and every wave is done with the ring: reuse it for the hand-over
+    __syncthreads();  // all loads landed and every wave is done with the ring
+    if (ragged) {     // the final, partial block: group 1, keys >= L masked
+        if (grp == 1) load_block(0, nblk - 1);
+        wait_vmcnt<0>();
+        __syncthreads();
+        if (grp == 1) compute(0, nblk - 1, std::true_type{});
+        __syncthreads();  // group 1 is done reading stage 0 before the hand-over overwrites it
+    }
 
     // group 1 hands (O, m, l) to group 0: per sub-wave [64 values][64 lanes] floats, then m and l per lane
     float* xo = reinterpret_cast<float*>(smem) + sub * (64 * 64 + 128);
