@@ -4,7 +4,7 @@
 // For rows m < M of x (bf16 [M, K], row stride ldx):
 //   v     = x                                                       (plain), or
 //   v     = bf16( LN(x)[*w + b] * (1 + mod_scale) + mod_shift )    (fused; fp32 math, one rounding)
-//   u     = (v + qshift) / smooth                                   (IEEE fp32)
+//   u     = (v + qshift) / smooth                                   (IEEE fp32 quotient)
 //   scale = bf16( max_{64 group} |u| / qmax )                       (qmax 7 signed, 15 unsigned)
 //   q     = clamp(rint(u / scale))                                  (0 where scale is 0)
 //   lora  = v . proj_down                                           (bf16 MFMA, fp32 sums)
@@ -15,13 +15,24 @@
 //   row_stats  (LN only): one wave per row; LN statistics in a fixed order — lane l owns the 8-value chunks
 //              c = l, l + 64, ... and sums them value by value; the 64 lane sums meet in an xor butterfly
 //              (32, 16, 8, 4, 2, 1); mean = sum / K, var = sum((x - mean)^2) / K, rstd = 1 / sqrt(var + eps).
-//   quant      grid (Mp / 32, ceil(K / 512)): 32 rows x 512 columns per workgroup, thread t owns row t / 8 and the
-//              8 columns (t % 8) * 8 .. of each 64-group; the low-rank product over those 512 columns is a
-//              32 x 32 partial (bf16 MFMA, the 4 waves' k-quarters summed in order).
+//   quant      grid (Mp / 32, ceil(K / 512)): 32 rows x 512 columns per workgroup of 16 waves, thread t owns row
+//              t / 32, groups 2 ((t / 8) % 4) and 2 ((t / 8) % 4) + 1 and their 8 columns (t % 8) * 8 ..; every load
+//              is issued up front (per-column vectors staged in LDS once); the low-rank product over the 512
+//              columns is a 32 x 32 partial (bf16 MFMA on 4 waves, their k-quarters summed in order).
 //   lora_sum   lora = sum of the column-block partials in increasing order (only when K > 512).
 #include "wdl_common.h"
 
 namespace {
+
+// The IEEE quotient w / d for a bf16-valued divisor d > 0, given r = RN(1/d): q0 = RN(w r), e = w - q0 d (exact by
+// fma), q = RN(q0 + e r). Markstein's correction step; for divisors with 8-bit significands it returns the
+// correctly rounded quotient (checked against IEEE division for every positive bf16 divisor). 3 instructions
+// instead of the ~10 of a full division.
+__device__ __forceinline__ float div_bf16(float w, float d, float r) {
+    const float q0 = w * r;
+    const float e = fmaf(-q0, d, w);
+    return fmaf(e, r, q0);
+}
 
 using namespace wdl;
 
@@ -103,61 +114,106 @@ struct QuantArgs {
     uint16_t* v_out;           // bf16 [M, K] copy of v, or null
 };
 
-__global__ __launch_bounds__(256) void quant_kernel(QuantArgs a) {
+constexpr int QT = 1024;  // threads of the quant launch: 32 threads per row, each 2 of the block's 8 groups
+
+__global__ __launch_bounds__(QT) void quant_kernel(QuantArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t tile[ROWS][CB + 8];
     __shared__ float part[4][ROWS * RANK];
+    // per-column vectors of this block's columns: smooth, LN weight, LN bias, 1 + mod_scale, mod_shift
+    __shared__ __attribute__((aligned(16))) float sp[6][CB];  // + 1 / smooth
 
     const int t = threadIdx.x, lane = t % 64, wave = t / 64;
-    const int rloc = t / 8, slot = t % 8;
+    const int rloc = t / 32, slot = t % 8, gsel = (t / 8) % 4;  // row, 8-column chunk, group pair
     const int64_t row = int64_t(blockIdx.x) * ROWS + rloc;
     const bool live = row < a.M;
     const int64_t K = a.K;
     const int64_t c0 = int64_t(blockIdx.y) * CB;
     const int ng = int(min(int64_t(CB), K - c0) / 64);  // 64-groups in this block
-    const uint16_t* xr = a.x + (live ? row : 0) * a.ldx;
+    const bool ln = a.stats != nullptr;
 
-    float v[8][8];
+    // loads first: 2 x 16 bytes of the row (absent rows read row 0, absent groups a present one; zeroed below),
+    // the row's LN statistics, this block's per-column vectors (thread t < 512: column t)
+    uint4 raw[2];
+    if (a.M > 0) {
+        const uint16_t* xr = a.x + (live ? row : 0) * a.ldx + c0 + slot * 8;
 #pragma unroll
-    for (int g = 0; g < 8; ++g) {
-        if (live && g < ng) load8(xr + c0 + g * 64 + slot * 8, v[g]);
-        else
-            for (int j = 0; j < 8; ++j) v[g][j] = 0.0f;
-    }
-    if (a.stats && live) {
-        const float2 st = a.stats[row];
-#pragma unroll
-        for (int g = 0; g < 8; ++g) {
-            if (g >= ng) break;
-            const int64_t col = c0 + g * 64 + slot * 8;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                float n = (v[g][j] - st.x) * st.y;
-                if (a.ln_w) n = n * a.ln_w[col + j];
-                if (a.ln_b) n = n + a.ln_b[col + j];
-                if (a.mod_scale) n = n * (1.0f + a.mod_scale[col + j]);
-                if (a.mod_shift) n = n + a.mod_shift[col + j];
-                v[g][j] = bf16_to_f32(f32_to_bf16(n));
-            }
+        for (int h = 0; h < 2; ++h) {
+            const int g = 2 * gsel + h;
+            raw[h] = *reinterpret_cast<const uint4*>(xr + (g < ng ? g : 0) * 64);
         }
     }
+    const float2 st = (ln && live) ? a.stats[row] : make_float2(0.0f, 0.0f);
+    if (t < CB) {
+        const int64_t c = c0 + (t < ng * 64 ? t : 0);
+        const uint16_t sm = a.smooth[c];
+        float p1 = 1.0f, p2 = 0.0f, p3 = 0.0f, p4 = 0.0f;
+        if (a.ln_w) p1 = a.ln_w[c];
+        if (a.ln_b) p2 = a.ln_b[c];
+        if (a.mod_scale) p3 = a.mod_scale[c];
+        if (a.mod_shift) p4 = a.mod_shift[c];
+        if (t < ng * 64) {
+            sp[0][t] = bf16_to_f32(sm);
+            sp[5][t] = 1.0f / bf16_to_f32(sm);
+            sp[1][t] = p1;
+            sp[2][t] = p2;
+            sp[3][t] = 1.0f + p3;
+            sp[4][t] = p4;
+        }
+    }
+    // the low-rank operand (waves 0..3: B = proj_down^T rows lane % 32, k = 128 wave + 16 s + 8 (lane / 32));
+    // columns past the block's groups read column 0 of the block (their A side is zero)
+    bf16x8 bv[8];
+    if (a.pdt && wave < 4) {
+#pragma unroll
+        for (int s8 = 0; s8 < 8; ++s8) {
+            int kk = wave * 128 + s8 * 16 + 8 * (lane / 32);
+            kk = kk < ng * 64 ? kk : 0;
+            bv[s8] = *reinterpret_cast<const bf16x8*>(a.pdt + int64_t(lane % 32) * K + c0 + kk);
+        }
+    }
+    __syncthreads();
+
     const float qmax = a.unsigned_q ? 15.0f : 7.0f;
     const float qlo = a.unsigned_q ? 0.0f : -8.0f;
 #pragma unroll
-    for (int g = 0; g < 8; ++g) {
-        if (g >= ng) break;
-        const int64_t col = c0 + g * 64 + slot * 8;
-        uint16_t vb[8];
+    for (int h = 0; h < 2; ++h) {
+        const int g = 2 * gsel + h;
+        const int cl = g * 64 + slot * 8;
+        const bool present = live && g < ng && a.M > 0;
+        float v[8];
+        {
+            const uint32_t w[4] = {raw[h].x, raw[h].y, raw[h].z, raw[h].w};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) vb[j] = f32_to_bf16(v[g][j]);
+            for (int j = 0; j < 4; ++j) {
+                v[2 * j] = present ? __uint_as_float(w[j] << 16) : 0.0f;
+                v[2 * j + 1] = present ? __uint_as_float(w[j] & 0xffff0000u) : 0.0f;
+            }
+        }
+        if (ln && present) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float n = (v[j] - st.x) * st.y;
+                if (a.ln_w) n = n * sp[1][cl + j];
+                if (a.ln_b) n = n + sp[2][cl + j];
+                if (a.mod_scale) n = n * sp[3][cl + j];
+                if (a.mod_shift) n = n + sp[4][cl + j];
+                v[j] = bf16_to_f32(f32_to_bf16(n));
+            }
+        }
+        uint16_t vb[8];  // v is bf16-valued here: its top 16 bits
+#pragma unroll
+        for (int j = 0; j < 8; ++j) vb[j] = uint16_t(__float_as_uint(v[j]) >> 16);
         const uint4 packed = make_uint4(vb[0] | (uint32_t(vb[1]) << 16), vb[2] | (uint32_t(vb[3]) << 16),
                                         vb[4] | (uint32_t(vb[5]) << 16), vb[6] | (uint32_t(vb[7]) << 16));
-        *reinterpret_cast<uint4*>(&tile[rloc][g * 64 + slot * 8]) = packed;
+        *reinterpret_cast<uint4*>(&tile[rloc][cl]) = packed;  // zeros for absent rows / groups
+        if (g >= ng) continue;  // uniform within each group's 8 lanes
+        const int64_t col = c0 + cl;
         if (a.v_out && live) *reinterpret_cast<uint4*>(a.v_out + row * K + col) = packed;
         float u[8];
         float amax = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            u[j] = (v[g][j] + a.qshift) / bf16_to_f32(a.smooth[col + j]);
+            u[j] = div_bf16(v[j] + a.qshift, sp[0][cl + j], sp[5][cl + j]);
             amax = fmaxf(amax, fabsf(u[j]));
         }
         amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
@@ -165,10 +221,11 @@ __global__ __launch_bounds__(256) void quant_kernel(QuantArgs a) {
         amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
         const uint16_t sb = f32_to_bf16(amax / qmax);
         const float sc = bf16_to_f32(sb);
+        const float rsc = sc > 0.0f ? 1.0f / sc : 0.0f;
         float qv[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float r = sc > 0.0f ? __builtin_rintf(u[j] / sc) : 0.0f;
+            const float r = sc > 0.0f ? __builtin_rintf(div_bf16(u[j], sc, rsc)) : 0.0f;
             qv[j] = live ? fminf(fmaxf(r, qlo), qmax) + 0.0f : 0.0f;  // + 0 turns -0 into +0
         }
         uint32_t w0 = 0, w1 = 0;
@@ -183,22 +240,21 @@ __global__ __launch_bounds__(256) void quant_kernel(QuantArgs a) {
     }
     if (!a.pdt) return;
     __syncthreads();
-    // wave w: k = 128 w .. 128 w + 127 of this block, 16 per MFMA; A = v rows (lane % 32), B = proj_down^T rows r
-    f32x16 acc = {};
-    const int kw = wave * 128;
+    if (wave < 4) {
+        // wave w: k = 128 w .. 128 w + 127 of this block, 16 per MFMA; A = v rows (lane % 32), B = proj_down^T rows
+        f32x16 acc = {};
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        const int kk = kw + s * 16 + 8 * (lane / 32);
-        if (kw + s * 16 >= ng * 64) break;
-        const bf16x8 av = *reinterpret_cast<const bf16x8*>(&tile[lane % 32][kk]);
-        const bf16x8 bv = *reinterpret_cast<const bf16x8*>(a.pdt + int64_t(lane % 32) * K + c0 + kk);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
+        for (int s8 = 0; s8 < 8; ++s8) {
+            const int kk = wave * 128 + s8 * 16 + 8 * (lane / 32);
+            const bf16x8 av = *reinterpret_cast<const bf16x8*>(&tile[lane % 32][kk]);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv[s8], acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) part[wave][(8 * (i / 4) + 4 * (lane / 32) + (i % 4)) * RANK + lane % 32] = acc[i];
     }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) part[wave][(8 * (i / 4) + 4 * (lane / 32) + (i % 4)) * RANK + lane % 32] = acc[i];
     __syncthreads();
     float* dst = a.lora + int64_t(blockIdx.y) * a.Mp * RANK;
-    for (int e = t; e < ROWS * RANK; e += 256) {
+    for (int e = t; e < ROWS * RANK; e += QT) {
         const int64_t r = int64_t(blockIdx.x) * ROWS + e / RANK;
         if (r < a.Mp) dst[r * RANK + e % RANK] = r < a.M ? (part[0][e] + part[1][e]) + (part[2][e] + part[3][e]) : 0.0f;
     }
@@ -246,7 +302,7 @@ extern "C" int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K
                 unsigned_q, static_cast<const uint16_t*>(proj_down_t), static_cast<uint8_t*>(q),
                 static_cast<uint16_t*>(ascales), nb > 1 ? workspace : lora, ln ? stats : nullptr, mod_shift,
                 mod_scale, ln_w, ln_b, static_cast<uint16_t*>(v_out)};
-    quant_kernel<<<dim3(unsigned(Mp / ROWS), unsigned(nb)), 256, 0, stream>>>(a);
+    quant_kernel<<<dim3(unsigned(Mp / ROWS), unsigned(nb)), QT, 0, stream>>>(a);
     int rc = check_launch("act_quant_w4 quant");
     if (rc || !proj_down_t || nb == 1) return rc;
     const int64_t n = Mp * RANK;
