@@ -77,6 +77,27 @@ int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wcodes, const
                   const void* proj_up, const void* bias, int64_t M, int64_t Mp, int64_t N, int64_t K, int64_t rank,
                   void* out, int64_t ldo, int epilogue, const float* gate, wdl_stream_t stream);
 
+/* Workspace (in floats) of wdl_fp8_quantize in per-tensor mode for an [M, K] operand. */
+int64_t wdl_fp8_quantize_workspace_floats(int64_t M, int64_t K);
+
+/* FP8 E4M3 quantization of a linear-layer operand. Replaces quantize and quantize_rows
+ * (src/wan_dit_lab/quantization/fp8.py:14-17, 37-41) as Fp8Linear, DynamicFp8Linear and PackedFp8Linear use them
+ * (fp8.py:20-94). x: bf16 (x_dtype 2) or fp32 (0) [M, K], row stride ldx (16-byte aligned rows), K % 16 == 0.
+ * rows != 0: scale[m] = max(max_k |x[m][k]|, 1e-12) / 448 (scale fp32 [Mp]); rows == 0: one scale for the tensor
+ * (scale fp32 [1], workspace: wdl_fp8_quantize_workspace_floats(M, K)). q [Mp, K] = e4m3(x / scale) (IEEE quotient,
+ * round to nearest even), rows M..Mp-1 zero (scale 0). Deterministic (no atomics). */
+int wdl_fp8_quantize(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, int64_t Mp, int rows, void* q,
+                     float* scale, float* workspace, wdl_stream_t stream);
+
+/* FP8 GEMM with torch._scaled_mm's scaled epilogue. Replaces the _scaled_mm calls of Fp8Linear,
+ * DynamicFp8Linear and PackedFp8Linear (src/wan_dit_lab/quantization/fp8.py:32-33, 60-66, 92-93; cuBLASLt there).
+ * xq: e4m3 [Mp, K] (wdl_fp8_quantize), wq: e4m3 [N, K] ([out, in]); acc = sum_k xq[m][k] wq[n][k] in fp32.
+ * rows != 0: out = bf16(float(bf16(acc)) * (x_scale[m] * w_scale[n]) + bias[n]) (fp8.py:57-62);
+ * rows == 0: out = bf16(acc * (x_scale[0] * w_scale[0]) + bias[n]) (one rounding). bias bf16 [N] or NULL;
+ * out bf16 [M, ldo]. Mp % 128 == 0, N % 128 == 0, K % 64 == 0, operands 16-byte aligned. */
+int wdl_fp8_gemm(const void* xq, const float* x_scale, const void* wq, const float* w_scale, const void* bias,
+                 int64_t M, int64_t Mp, int64_t N, int64_t K, int rows, void* out, int64_t ldo, wdl_stream_t stream);
+
 /* Q/K RMSNorm over all heads + 3D RoPE, fused. Replaces norm_q / norm_k (src/wan_dit_lab/models/rms_norm.py:10-13,
  * used at src/wan_dit_lab/quantization/w4a4.py:256-257) and rope_apply / wan_dit_lab::rope3d_rotate
  * (src/wan_dit_lab/models/rope.py:12-31; src/wan_dit_lab/kernels/rope_triton.py:66-81, 101-144).

@@ -68,10 +68,11 @@ def quantize_rows(X: torch.Tensor):
 
 
 def w8a8_linear_rows(x: torch.Tensor, W: torch.Tensor, b: torch.Tensor | None):
-    """fp8.py:55-59 (rows=True): per-token x scale, per-output-row W scale, unit-scale fp8 product in fp32 (exact
-    products of fp8 values, fp64 sum here), then y * (xs ⊗ ws) + b, output bf16."""
+    """fp8.py:57-62 (rows=True): per-token x scale, per-output-row W scale, the unit-scale fp8 product rounded to
+    bf16 (_scaled_mm's out_dtype; exact products of fp8 values, fp64 sum here), then y * (xs ⊗ ws) in fp32, + b,
+    output bf16."""
     (xq, xs), (wq, ws) = quantize_rows(x), quantize_rows(W)
-    y = (xq.double() @ wq.double().t()).float()
+    y = (xq.double() @ wq.double().t()).to(torch.bfloat16).float()
     y = y * (xs * ws.t())
     if b is not None:
         y = y + b.float()
@@ -79,7 +80,8 @@ def w8a8_linear_rows(x: torch.Tensor, W: torch.Tensor, b: torch.Tensor | None):
 
 
 def w8a8_linear_tensor(x: torch.Tensor, W: torch.Tensor, b: torch.Tensor | None):
-    """fp8.py:60-63 (rows=False) / Fp8Linear fp8.py:27-31: per-tensor scales."""
+    """fp8.py:63-66 (rows=False) / Fp8Linear fp8.py:27-31: per-tensor scales; _scaled_mm's acc * (xs ws) + b in
+    fp32, one bf16 rounding."""
     (xq, xs), (wq, ws) = quantize(x), quantize(W)
     y = (xq.double() @ wq.double().t()).float() * (xs * ws)
     if b is not None:

@@ -1,0 +1,169 @@
+// FP8 (E4M3FN) quantization of linear-layer operands (src/wan_dit_lab/quantization/fp8.py):
+//   per row    (quantize_rows, fp8.py:37-41): scale[m] = max(max_k |x[m][k]|, 1e-12) / 448, q = e4m3(x / scale)
+//   per tensor (quantize,      fp8.py:14-17): scale    = max(max    |x|,       1e-12) / 448, q = e4m3(x / scale)
+// x is bf16 or fp32 [M, K] (row stride ldx); q is [Mp, K] bytes (rows M..Mp-1 zero, the padding the FP8 GEMM
+// tiles need), scale fp32 [Mp] (rows: padding rows 0) or [1]. The quotient is IEEE fp32 and the conversion is the
+// hardware's round-to-nearest-even e4m3 conversion (torch's; the largest |x| lands on 448). Per tensor with a bf16
+// x, the reference's X / scale divides by a 0-d fp32 tensor, which does not promote the bf16 result: the quotient
+// is rounded to bf16 before the e4m3 conversion (the per-row scale [..., 1] does promote: fp32 quotient there).
+//
+// rows:   one wave per row, two passes over it (the maximum, then the codes; the second pass reads the row back
+//         from cache).
+// tensor: pass 1 writes one partial maximum per workgroup to the workspace; pass 2 has every workgroup reduce
+//         the partials (the same order in each: deterministic) and quantize its share. No atomics, no memory that
+//         has to start zeroed.
+#include "wdl_common.h"
+
+namespace {
+
+using namespace wdl;
+
+constexpr float FP8_MAX = 448.0f;
+constexpr int TBLOCKS = 512;  // workgroups of the per-tensor passes (at most)
+
+// 4 consecutive values of a row as floats (16-byte loads of fp32, 8-byte of bf16)
+template <typename T>
+__device__ __forceinline__ void ld4(const T* p, float* f);
+template <>
+__device__ __forceinline__ void ld4<uint16_t>(const uint16_t* p, float* f) {
+    const uint2 r = *reinterpret_cast<const uint2*>(p);
+    f[0] = __uint_as_float(r.x << 16), f[1] = __uint_as_float(r.x & 0xffff0000u);
+    f[2] = __uint_as_float(r.y << 16), f[3] = __uint_as_float(r.y & 0xffff0000u);
+}
+template <>
+__device__ __forceinline__ void ld4<float>(const float* p, float* f) {
+    const float4 r = *reinterpret_cast<const float4*>(p);
+    f[0] = r.x, f[1] = r.y, f[2] = r.z, f[3] = r.w;
+}
+
+__device__ __forceinline__ uint32_t e4m3x4(const float* y) {
+    uint32_t w = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+    return __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], w, true);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void rows_kernel(const T* x, int64_t ldx, int64_t M, int64_t Mp, int64_t K,
+                                                   uint8_t* q, float* scale) {
+    const int lane = threadIdx.x % 64;
+    const int64_t row = int64_t(blockIdx.x) * 4 + threadIdx.x / 64;
+    if (row >= Mp) return;
+    uint32_t* qr = reinterpret_cast<uint32_t*>(q + row * K);
+    if (row >= M) {
+        for (int64_t c = lane; c < K / 4; c += 64) qr[c] = 0u;
+        if (lane == 0) scale[row] = 0.0f;
+        return;
+    }
+    const T* xr = x + row * ldx;
+    float amax = 0.0f;
+    for (int64_t c = lane; c < K / 4; c += 64) {
+        float f[4];
+        ld4<T>(xr + 4 * c, f);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(f[e]));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    const float s = fmaxf(amax, 1e-12f) / FP8_MAX;
+    if (lane == 0) scale[row] = s;
+    for (int64_t c = lane; c < K / 4; c += 64) {
+        float f[4];
+        ld4<T>(xr + 4 * c, f);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f[e] = f[e] / s;
+        qr[c] = e4m3x4(f);
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void tensor_max_kernel(const T* x, int64_t ldx, int64_t M, int64_t K,
+                                                         float* partial) {
+    __shared__ float red[4];
+    const int64_t n4 = M * (K / 4);
+    float amax = 0.0f;
+    for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n4; i += int64_t(gridDim.x) * 256) {
+        const int64_t m = i / (K / 4), c = i % (K / 4);
+        float f[4];
+        ld4<T>(x + m * ldx + 4 * c, f);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(f[e]));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = amax;
+    __syncthreads();
+    if (threadIdx.x == 0) partial[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void tensor_quant_kernel(const T* x, int64_t ldx, int64_t M, int64_t Mp, int64_t K,
+                                                           const float* partial, int nparts, uint8_t* q, float* scale) {
+    __shared__ float red[4];
+    float amax = 0.0f;
+    for (int i = threadIdx.x; i < nparts; i += 256) amax = fmaxf(amax, partial[i]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = amax;
+    __syncthreads();
+    const float s = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), 1e-12f) / FP8_MAX;
+    if (blockIdx.x == 0 && threadIdx.x == 0) scale[0] = s;
+    const int64_t n4 = Mp * (K / 4);
+    for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n4; i += int64_t(gridDim.x) * 256) {
+        const int64_t m = i / (K / 4), c = i % (K / 4);
+        uint32_t w = 0u;
+        if (m < M) {
+            float f[4];
+            ld4<T>(x + m * ldx + 4 * c, f);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                f[e] = f[e] / s;
+                if constexpr (sizeof(T) == 2) f[e] = bf16_to_f32(f32_to_bf16(f[e]));
+            }
+            w = e4m3x4(f);
+        }
+        reinterpret_cast<uint32_t*>(q + m * K)[c] = w;
+    }
+}
+
+int tensor_blocks(int64_t M, int64_t K) {
+    const int64_t n4 = M * (K / 4);
+    const int64_t b = (n4 + 256 * 8 - 1) / (256 * 8);
+    return int(b < 1 ? 1 : (b > TBLOCKS ? TBLOCKS : b));
+}
+
+template <typename T>
+int quantize(const void* xv, int64_t ldx, int64_t M, int64_t K, int64_t Mp, int rows, void* q, float* scale,
+             float* workspace, hipStream_t stream) {
+    const T* x = static_cast<const T*>(xv);
+    uint8_t* qb = static_cast<uint8_t*>(q);
+    if (rows) {
+        rows_kernel<T><<<unsigned((Mp + 3) / 4), 256, 0, stream>>>(x, ldx, M, Mp, K, qb, scale);
+        return check_launch("fp8_quantize rows");
+    }
+    const int nb = tensor_blocks(M, K);
+    if (M > 0) {
+        tensor_max_kernel<T><<<unsigned(nb), 256, 0, stream>>>(x, ldx, M, K, workspace);
+        const int rc = check_launch("fp8_quantize tensor max");
+        if (rc) return rc;
+    }
+    tensor_quant_kernel<T><<<unsigned(nb), 256, 0, stream>>>(x, ldx, M, Mp, K, workspace, M > 0 ? nb : 0, qb, scale);
+    return check_launch("fp8_quantize tensor");
+}
+
+}  // namespace
+
+extern "C" int64_t wdl_fp8_quantize_workspace_floats(int64_t M, int64_t K) { return tensor_blocks(M, K); }
+
+extern "C" int wdl_fp8_quantize(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, int64_t Mp, int rows,
+                                void* q, float* scale, float* workspace, hipStream_t stream) {
+    if (M < 0 || K <= 0 || K % 16 || Mp < M || ldx < K)
+        return fail(WDL_EINVAL, "fp8_quantize: bad shape M=%lld K=%lld Mp=%lld ldx=%lld", (long long)M, (long long)K,
+                    (long long)Mp, (long long)ldx);
+    if (x_dtype != WDL_BF16 && x_dtype != WDL_F32) return fail(WDL_EINVAL, "fp8_quantize: x must be bf16 or fp32");
+    if (!x || !q || !scale || (!rows && !workspace)) return fail(WDL_EINVAL, "fp8_quantize: null pointer");
+    const int64_t esz = x_dtype == WDL_F32 ? 4 : 2;
+    if ((reinterpret_cast<uintptr_t>(x) | (ldx * esz) | reinterpret_cast<uintptr_t>(q)) % 16)
+        return fail(WDL_EINVAL, "fp8_quantize: rows must be 16-byte aligned");
+    if (Mp == 0) return WDL_OK;
+    return x_dtype == WDL_F32 ? quantize<float>(x, ldx, M, K, Mp, rows, q, scale, workspace, stream)
+                              : quantize<uint16_t>(x, ldx, M, K, Mp, rows, q, scale, workspace, stream);
+}

@@ -28,7 +28,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-enum Epilogue { EPI_BF16 = 0, EPI_F32 = 1, EPI_RESIDUAL = 2, EPI_GELU = 3 };
+enum Epilogue { EPI_BF16 = 0, EPI_F32 = 1, EPI_RESIDUAL = 2, EPI_GELU = 3, EPI_FP8_ROWS = 4, EPI_FP8_TENSOR = 5 };
 
 // GELU, tanh form: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), tanh(u) = 1 - 2 / (exp(2u) + 1)
 __device__ __forceinline__ float gelu_tanh(float x) {
@@ -49,6 +49,8 @@ struct GemmArgs {
     void* out;                // bf16 / fp32 [M, ldo]
     int64_t ldo;
     const float* gate;        // [N] fp32 (EPI_RESIDUAL: out += gate * bf16(y))
+    const float* xs;          // FP8 linears: activation scales fp32 [Mp] (rows) or [1] (tensor)
+    const float* wsf;         // FP8 linears: weight scales fp32 [N] (rows) or [1] (tensor)
 };
 
 // Tile BN (features) x BM (tokens), NW waves in a (BN / WN) x (BM / WM) grid. Per 64-deep group the workgroup
@@ -123,6 +125,10 @@ __device__ __forceinline__ void finish_tile(const GemmArgs& p, f32x16 (&acc)[TN]
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     y[e] = acc[i][j][4 * q + e];
+                    if (EPI == EPI_FP8_ROWS)  // fp8.py:57-62: bf16 product, then * (xs ws) in fp32, + b
+                        y[e] = bf16_to_f32(f32_to_bf16(y[e])) * (p.xs[m] * p.wsf[nb + e]);
+                    else if (EPI == EPI_FP8_TENSOR)  // _scaled_mm: acc * (xs ws) + b, one rounding
+                        y[e] = y[e] * (p.xs[0] * p.wsf[0]);
                     if (p.bias) y[e] = y[e] + bf16_to_f32(p.bias[nb + e]);
                 }
                 if (EPI == EPI_F32) {
@@ -153,21 +159,23 @@ __device__ __forceinline__ void finish_tile(const GemmArgs& p, f32x16 (&acc)[TN]
         }
 }
 
-template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES>
-__global__ __launch_bounds__(NW * 64) void w4a4_gemm_kernel(GemmArgs p) {
+// The main loop of both GEMMs. FOLD: the W4A4 product (per-group scale fold, scales streamed with the codes);
+// otherwise the FP8 product (codes only, one fp32 accumulation over all of K in the MFMA accumulator).
+template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES, bool FOLD>
+__device__ __forceinline__ void gemm_body(const GemmArgs& p) {
     static_assert((BN / WN) * (BM / WM) == NW, "wave grid");
     static_assert(STAGES >= 3 && STAGES <= 8, "ring depth");
     constexpr int TN = WN / 32, TM = WM / 32;
     constexpr int XI = BM * 4 / 64 / NW;   // 16-byte loads per wave per group: activation codes
     constexpr int WI = BN * 4 / 64 / NW;   // and weight codes
-    constexpr int LPG = XI + WI + 1;       // + one 4-byte load of scales: loads per wave per group
+    constexpr int LPG = XI + WI + (FOLD ? 1 : 0);  // + one 4-byte load of scales: loads per wave per group
     constexpr int SD = NW * 256;           // scale bytes loaded per stage (ws[BN], as[BM], then padding)
     constexpr int SB = SD + 256;           // + 64 zero bytes (rounded up) read by lanes 32..63
     static_assert(XI >= 1 && WI >= 1 && BM * 4 == XI * 64 * NW && BN * 4 == WI * 64 * NW, "tile vs waves");
     static_assert(2 * (BN + BM) <= SD, "scale stage");
     __shared__ __attribute__((aligned(1024))) uint8_t sX[STAGES][BM * 64];
     __shared__ __attribute__((aligned(1024))) uint8_t sW[STAGES][BN * 64];
-    __shared__ __attribute__((aligned(256))) uint8_t sS[STAGES][SB];
+    __shared__ __attribute__((aligned(256))) uint8_t sS[FOLD ? STAGES : 1][FOLD ? SB : 256];
 
     const int t = threadIdx.x, lane = t % 64;
     const int wave = __builtin_amdgcn_readfirstlane(t / 64);
@@ -180,7 +188,8 @@ __global__ __launch_bounds__(NW * 64) void w4a4_gemm_kernel(GemmArgs p) {
     const int64_t K = p.K, G = K / 64;
 
     // zero tails of the scale stages (written once; the loads never touch them)
-    if (t < STAGES * 16) *reinterpret_cast<uint32_t*>(&sS[t / 16][SD + (t % 16) * 4]) = 0u;
+    if constexpr (FOLD)
+        if (t < STAGES * 16) *reinterpret_cast<uint32_t*>(&sS[t / 16][SD + (t % 16) * 4]) = 0u;
 
     // this lane's sources for group 0; group g adds 64 g bytes (codes) or g times the scale row stride
     const uint8_t* xsrc[XI];
@@ -220,7 +229,7 @@ __global__ __launch_bounds__(NW * 64) void w4a4_gemm_kernel(GemmArgs p) {
         for (int j = 0; j < XI; ++j) dma16(xsrc[j] + gg * 64, lds_addr(&sX[st][(wave * XI + j) * 1024]));
 #pragma unroll
         for (int j = 0; j < WI; ++j) dma16(wsrc[j] + gg * 64, lds_addr(&sW[st][(wave * WI + j) * 1024]));
-        dma4(ssrc + gg * sstride, lds_addr(&sS[st][wave * 256]));
+        if constexpr (FOLD) dma4(ssrc + gg * sstride, lds_addr(&sS[st][wave * 256]));
     };
 
     // per-lane LDS offsets (stage-independent): operand rows with their swizzled quarters, scale entries
@@ -262,14 +271,23 @@ __global__ __launch_bounds__(NW * 64) void w4a4_gemm_kernel(GemmArgs p) {
             const uint8_t* r = &sW[st][aoff[i]];
             const uint4 a0 = *reinterpret_cast<const uint4*>(r + q0), a1 = *reinterpret_cast<const uint4*>(r + q1);
             af[i] = i32x8{int(a0.x), int(a0.y), int(a0.z), int(a0.w), int(a1.x), int(a1.y), int(a1.z), int(a1.w)};
-            sa[i] = *reinterpret_cast<const short*>(&sS[st][soa[i]]);
+            if constexpr (FOLD) sa[i] = *reinterpret_cast<const short*>(&sS[st][soa[i]]);
         }
 #pragma unroll
         for (int j = 0; j < TM; ++j) {
             const uint8_t* r = &sX[st][boff[j]];
             const uint4 b0 = *reinterpret_cast<const uint4*>(r + q0), b1 = *reinterpret_cast<const uint4*>(r + q1);
             bf[j] = i32x8{int(b0.x), int(b0.y), int(b0.z), int(b0.w), int(b1.x), int(b1.y), int(b1.z), int(b1.w)};
-            sb[j] = *reinterpret_cast<const short*>(&sS[st][sob[j]]);
+            if constexpr (FOLD) sb[j] = *reinterpret_cast<const short*>(&sS[st][sob[j]]);
+        }
+        if constexpr (!FOLD) {
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[i], bf[j], acc[i][j], 0, 0, 0, 0,
+                                                                                0, 0);
+            return;
         }
 #pragma unroll
         for (int i = 0; i < TN; ++i)
@@ -303,6 +321,16 @@ __global__ __launch_bounds__(NW * 64) void w4a4_gemm_kernel(GemmArgs p) {
     finish_tile<TN, TM, EPI>(p, acc, n0 + wn * WN, m0 + wm * WM, lane, -1);
 }
 
+template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES>
+__global__ __launch_bounds__(NW * 64) void w4a4_gemm_kernel(GemmArgs p) {
+    gemm_body<BN, BM, WN, WM, NW, EPI, STAGES, true>(p);
+}
+
+template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES>
+__global__ __launch_bounds__(NW * 64) void fp8_gemm_kernel(GemmArgs p) {
+    gemm_body<BN, BM, WN, WM, NW, EPI, STAGES, false>(p);
+}
+
 template <int BN, int BM, int WN, int WM, int NW, int ST>
 int launch(const GemmArgs& a, int epi, hipStream_t stream) {
     if (a.N % BN || a.Mp % BM) return fail(WDL_EINVAL, "w4a4_gemm: tile %dx%d does not divide N=%lld Mp=%lld", BN, BM,
@@ -316,6 +344,18 @@ int launch(const GemmArgs& a, int epi, hipStream_t stream) {
         default: return fail(WDL_EINVAL, "w4a4_gemm: bad epilogue %d", epi);
     }
     return check_launch("w4a4_gemm");
+}
+
+int launch_fp8(const GemmArgs& a, int epi, hipStream_t stream) {
+    if (a.N % 128 || a.Mp % 128) return fail(WDL_EINVAL, "fp8_gemm: tile 128x128 does not divide N=%lld Mp=%lld",
+                                             (long long)a.N, (long long)a.Mp);
+    const unsigned grid = unsigned((a.N / 128) * (a.Mp / 128));
+    switch (epi) {
+        case EPI_FP8_ROWS: fp8_gemm_kernel<128, 128, 64, 64, 4, EPI_FP8_ROWS, 4><<<grid, 256, 0, stream>>>(a); break;
+        case EPI_FP8_TENSOR: fp8_gemm_kernel<128, 128, 64, 64, 4, EPI_FP8_TENSOR, 4><<<grid, 256, 0, stream>>>(a); break;
+        default: return fail(WDL_EINVAL, "fp8_gemm: bad mode");
+    }
+    return check_launch("fp8_gemm");
 }
 
 // Tile configuration: 128 x 128 per workgroup, 4 waves of 64 x 64, a 4-stage ring (69 KB of LDS: two workgroups
@@ -371,7 +411,7 @@ extern "C" int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wc
     GemmArgs a{static_cast<const uint8_t*>(qa), static_cast<const uint16_t*>(ascales),
                static_cast<const uint8_t*>(wcodes), static_cast<const uint16_t*>(wscales), lora,
                static_cast<const uint16_t*>(proj_up), static_cast<const uint16_t*>(bias), M, Mp, N, K, out, ldo,
-               gate};
+               gate, nullptr, nullptr};
     return dispatch(a, epilogue, stream);
 }
 
@@ -386,4 +426,19 @@ extern "C" int wdl_w4a4_weight_codes(const void* qweight, int64_t N, int64_t K, 
     weight_codes_kernel<<<unsigned((words + 255) / 256), 256, 0, stream>>>(static_cast<const uint32_t*>(qweight),
                                                                           words, K, static_cast<uint32_t*>(codes));
     return check_launch("w4a4_weight_codes");
+}
+
+extern "C" int wdl_fp8_gemm(const void* xq, const float* x_scale, const void* wq, const float* w_scale,
+                            const void* bias, int64_t M, int64_t Mp, int64_t N, int64_t K, int rows, void* out,
+                            int64_t ldo, hipStream_t stream) {
+    if (M < 0 || Mp < M || Mp % 128 || N <= 0 || N % 128 || K <= 0 || K % 64 || ldo < N || ldo % 4)
+        return fail(WDL_EINVAL, "fp8_gemm: bad shape M=%lld Mp=%lld N=%lld K=%lld ldo=%lld", (long long)M,
+                    (long long)Mp, (long long)N, (long long)K, (long long)ldo);
+    if (!xq || !x_scale || !wq || !w_scale || !out) return fail(WDL_EINVAL, "fp8_gemm: null pointer");
+    if ((reinterpret_cast<uintptr_t>(xq) | reinterpret_cast<uintptr_t>(wq)) % 16)
+        return fail(WDL_EINVAL, "fp8_gemm: operands must be 16-byte aligned");
+    if (Mp == 0) return WDL_OK;
+    GemmArgs a{static_cast<const uint8_t*>(xq), nullptr, static_cast<const uint8_t*>(wq), nullptr, nullptr, nullptr,
+               static_cast<const uint16_t*>(bias), M, Mp, N, K, out, ldo, nullptr, x_scale, w_scale};
+    return launch_fp8(a, rows ? EPI_FP8_ROWS : EPI_FP8_TENSOR, stream);
 }

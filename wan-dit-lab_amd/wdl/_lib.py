@@ -29,6 +29,9 @@ SIGNATURES: dict[str, list] = {
     "wdl_w4a4_weight_codes": [c_ptr, c_i64, c_i64, c_ptr, c_ptr],
     "wdl_w4a4_gemm": [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_ptr,
                       c_i64, c_int, c_ptr, c_ptr],
+    "wdl_fp8_quantize_workspace_floats": [c_i64, c_i64],
+    "wdl_fp8_quantize": [c_ptr, c_int, c_i64, c_i64, c_i64, c_i64, c_int, c_ptr, c_ptr, c_ptr, c_ptr],
+    "wdl_fp8_gemm": [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_int, c_ptr, c_i64, c_ptr],
     "wdl_qk_norm_rope": [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_int, c_i64, c_i64, c_i64, c_int, c_int,
                          c_int, c_int, c_f32, c_ptr, c_ptr, c_i64, c_ptr],
     "wdl_quant_q": [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr],
@@ -39,7 +42,7 @@ SIGNATURES: dict[str, list] = {
                       c_ptr],
 }
 RESTYPES = {"wdl_last_error": ctypes.c_char_p, "wdl_sage_prep_workspace_floats": c_i64,
-            "wdl_act_quant_workspace_floats": c_i64}
+            "wdl_act_quant_workspace_floats": c_i64, "wdl_fp8_quantize_workspace_floats": c_i64}
 
 _LIB = None
 
