@@ -24,16 +24,6 @@
 
 namespace {
 
-// The IEEE quotient w / d for a bf16-valued divisor d > 0, given r = RN(1/d): q0 = RN(w r), e = w - q0 d (exact by
-// fma), q = RN(q0 + e r). Markstein's correction step; for divisors with 8-bit significands it returns the
-// correctly rounded quotient (checked against IEEE division for every positive bf16 divisor). 3 instructions
-// instead of the ~10 of a full division.
-__device__ __forceinline__ float div_bf16(float w, float d, float r) {
-    const float q0 = w * r;
-    const float e = fmaf(-q0, d, w);
-    return fmaf(e, r, q0);
-}
-
 using namespace wdl;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -213,7 +203,7 @@ __global__ __launch_bounds__(QT) void quant_kernel(QuantArgs a) {
         float amax = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            u[j] = div_bf16(v[j] + a.qshift, sp[0][cl + j], sp[5][cl + j]);
+            u[j] = div_rn(v[j] + a.qshift, sp[0][cl + j], sp[5][cl + j]);
             amax = fmaxf(amax, fabsf(u[j]));
         }
         amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
@@ -225,7 +215,7 @@ __global__ __launch_bounds__(QT) void quant_kernel(QuantArgs a) {
         float qv[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float r = sc > 0.0f ? __builtin_rintf(div_bf16(u[j], sc, rsc)) : 0.0f;
+            const float r = sc > 0.0f ? __builtin_rintf(div_rn(u[j], sc, rsc)) : 0.0f;
             qv[j] = live ? fminf(fmaxf(r, qlo), qmax) + 0.0f : 0.0f;  // + 0 turns -0 into +0
         }
         uint32_t w0 = 0, w1 = 0;

@@ -27,15 +27,20 @@ struct Src {
     int64_t ld;
 };
 
+// 8 channels d0 .. d0 + 7 of token t (head h) as floats: cached tokens from e4m3 times their row scale, chunk
+// tokens from bf16, tokens >= L zero. CACHE / CHUNK: the caller knows the token's source (uniform paths).
+enum { MIXED = 0, CACHE = 1, CHUNK = 2 };
+template <int SRC>
 __device__ __forceinline__ void load_token8(const Src& s, int64_t t, int64_t h, int64_t H, int64_t at, int64_t L,
                                             int d0, float* f) {
-    if (t < at) {
+    if (SRC == CACHE || (SRC == MIXED && t < at)) {
         const uint2 raw = *reinterpret_cast<const uint2*>(s.cache + (t * H + h) * D + d0);
         const float sc = s.cscale[t * H + h];
-        const uint32_t w[2] = {raw.x, raw.y};
+        e4m3x4_to_f32(raw.x, f);
+        e4m3x4_to_f32(raw.y, f + 4);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) f[j] = e4m3_to_f32(uint8_t(w[j / 4] >> (8 * (j % 4)))) * sc;
-    } else if (t < L) {
+        for (int j = 0; j < 8; ++j) f[j] = f[j] * sc;
+    } else if (SRC == CHUNK || t < L) {
         const uint4 raw = *reinterpret_cast<const uint4*>(s.chunk + (t - at) * s.ld + h * D + d0);
         const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
@@ -49,6 +54,40 @@ __device__ __forceinline__ void load_token8(const Src& s, int64_t t, int64_t h, 
     }
 }
 
+constexpr int UNROLL = 4;  // tokens per lane in flight in the statistics pass
+
+// tokens lo, lo + 16, ... < hi of one source: the K sums and |V| maxima of this lane's 8 channels, loads of UNROLL
+// tokens issued before they are used
+template <int SRC>
+__device__ __forceinline__ void colstats_range(const Src& k, const Src& v, int64_t h, int64_t H, int64_t at,
+                                               int64_t L, int64_t lo, int64_t hi, int d0, float* ks, float* vm) {
+    int64_t tok = lo;
+    for (; tok + 16 * (UNROLL - 1) < hi; tok += 16 * UNROLL) {
+        float fk[UNROLL][8], fv[UNROLL][8];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            load_token8<SRC>(k, tok + 16 * u, h, H, at, L, d0, fk[u]);
+            load_token8<SRC>(v, tok + 16 * u, h, H, at, L, d0, fv[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                ks[j] = ks[j] + fk[u][j];
+                vm[j] = fmaxf(vm[j], fabsf(fv[u][j]));
+            }
+    }
+    for (; tok < hi; tok += 16) {
+        float f[8];
+        load_token8<SRC>(k, tok, h, H, at, L, d0, f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ks[j] = ks[j] + f[j];
+        load_token8<SRC>(v, tok, h, H, at, L, d0, f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) vm[j] = fmaxf(vm[j], fabsf(f[j]));
+    }
+}
+
 __global__ __launch_bounds__(256) void colstats_kernel(Src k, Src v, int64_t H, int64_t at, int64_t L, int S,
                                                        float* part_k, float* part_v) {
     __shared__ float red[2][16][D];
@@ -57,15 +96,11 @@ __global__ __launch_bounds__(256) void colstats_kernel(Src k, Src v, int64_t H, 
     const int64_t per = (L + S - 1) / S;
     const int64_t lo = s * per, hi = min(L, lo + per);
     float ks[8] = {}, vm[8] = {};
-    for (int64_t tok = lo + lane_tok; tok < hi; tok += 16) {
-        float f[8];
-        load_token8(k, tok, h, H, at, L, d0, f);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) ks[j] = ks[j] + f[j];
-        load_token8(v, tok, h, H, at, L, d0, f);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) vm[j] = fmaxf(vm[j], fabsf(f[j]));
-    }
+    // this lane's tokens lo + lane_tok + 16 i: the cached ones first, then the chunk's
+    const int64_t first = lo + lane_tok;
+    const int64_t split = first >= at ? first : first + (at - first + 15) / 16 * 16;  // first chunk token
+    colstats_range<CACHE>(k, v, h, H, at, L, first, min(hi, split), d0, ks, vm);
+    colstats_range<CHUNK>(k, v, h, H, at, L, max(first, split), hi, d0, ks, vm);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         red[0][lane_tok][d0 + j] = ks[j];
@@ -98,41 +133,62 @@ __global__ void finalize_kernel(const float* part_k, const float* part_v, int S,
 
 __device__ __forceinline__ int v_position(int t) { return 32 * ((t % 8) / 4) + 4 * (t / 8) + t % 4; }
 
+template <int SRC>
+__device__ __forceinline__ void quant_block(const Src& k, const Src& v, int64_t h, int64_t H, int64_t at, int64_t L,
+                                            int64_t tok, int dq, float (&fk)[4][8], float (&fv)[4][8]) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        load_token8<SRC>(k, tok, h, H, at, L, dq + c * 8, fk[c]);
+        load_token8<SRC>(v, tok, h, H, at, L, dq + c * 8, fv[c]);
+    }
+}
+
 __global__ __launch_bounds__(256) void quant_kv_kernel(Src k, Src v, int64_t H, int64_t at, int64_t L, int64_t Lpad,
                                                        const float* k_mean, const float* v_scale, int8_t* k_out,
                                                        float* k_scale, uint8_t* v_out) {
     __shared__ float gmax[64][4];
     __shared__ uint8_t vt[D][64 + 4];  // codes [channel][position]
+    __shared__ __attribute__((aligned(16))) float stat[3][D];  // k_mean, v_scale, 1 / v_scale of the head
     const int64_t blk = blockIdx.x, h = blockIdx.y;
     const int t = threadIdx.x, tt = t / 4, dq = (t % 4) * 32;
     const int64_t tok = blk * 64 + tt;
-    // K: 32 channels of one token per thread
+    if (t < D) {
+        stat[0][t] = k_mean[h * D + t];
+        const float vs = v_scale[h * D + t];
+        stat[1][t] = vs;
+        stat[2][t] = 1.0f / vs;
+    }
+    // all loads of this thread's token first (the block's source is uniform unless it straddles at or L)
+    float fk[4][8], fv[4][8];
+    const int64_t b0 = blk * 64, b1 = b0 + 64;
+    if (b1 <= at) quant_block<CACHE>(k, v, h, H, at, L, tok, dq, fk, fv);
+    else if (b0 >= at && b1 <= L) quant_block<CHUNK>(k, v, h, H, at, L, tok, dq, fk, fv);
+    else quant_block<MIXED>(k, v, h, H, at, L, tok, dq, fk, fv);
+    __syncthreads();
+    // K - mean: 32 channels of one token per thread
     float x[32];
     float amax = 0.0f;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        float f[8];
-        load_token8(k, tok, h, H, at, L, dq + c * 8, f);
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float y = tok < L ? f[j] - k_mean[h * D + dq + c * 8 + j] : 0.0f;
+            const float y = tok < L ? fk[c][j] - stat[0][dq + c * 8 + j] : 0.0f;
             x[c * 8 + j] = y;
             amax = fmaxf(amax, fabsf(y));
         }
-    }
     gmax[tt][t % 4] = amax;
-    // V codes into the transposed tile
+    // V codes into the transposed tile (V / v_scale is below 2.25 in magnitude: the conversion never saturates)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        float f[8];
-        load_token8(v, tok, h, H, at, L, dq + c * 8, f);
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 8; j += 2) {
             const int d = dq + c * 8 + j;
-            const float y = f[j] / v_scale[h * D + d];
-            vt[d][v_position(tt)] = tok < L ? f32_to_e4m3(y) : uint8_t(0);
+            const float y0 = div_rn(fv[c][j], stat[1][d], stat[2][d]);
+            const float y1 = div_rn(fv[c][j + 1], stat[1][d + 1], stat[2][d + 1]);
+            const uint32_t w = __builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false);
+            vt[d][v_position(tt)] = tok < L ? uint8_t(w) : uint8_t(0);
+            vt[d + 1][v_position(tt)] = tok < L ? uint8_t(w >> 8) : uint8_t(0);
         }
-    }
     __syncthreads();
     const int g = (tt % 8) / 2;
     float m = 0.0f;
@@ -146,6 +202,7 @@ __global__ __launch_bounds__(256) void quant_kv_kernel(Src k, Src v, int64_t H, 
         }
     }
     const float scale = m / 127.0f + 1e-7f;
+    const float rscale = 1.0f / scale;
     if (t % 4 == 0 && (tt % 8) == 2 * g && tt < 8) k_scale[h * (Lpad / 64 * 4) + blk * 4 + g] = scale;
     int8_t* kd = k_out + (h * Lpad + tok) * D + dq;
 #pragma unroll
@@ -156,7 +213,7 @@ __global__ __launch_bounds__(256) void quant_kv_kernel(Src k, Src v, int64_t H, 
             uint32_t word = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float y = x[c * 16 + b * 4 + e] / scale;
+                const float y = div_rn(x[c * 16 + b * 4 + e], scale, rscale);
                 const float r = __builtin_truncf(y + (y >= 0.0f ? 0.5f : -0.5f));
                 word |= (uint32_t(int32_t(r)) & 0xffu) << (8 * e);
             }

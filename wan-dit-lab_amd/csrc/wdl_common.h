@@ -57,6 +57,25 @@ __device__ __forceinline__ uint8_t f32_to_e4m3(float f) {
     return uint8_t(sign | uint8_t(u >> 20));
 }
 
+// The IEEE quotient w / d from r = RN(1/d): q0 = RN(w r), e = w - q0 d (exact by fma), q = RN(q0 + e r) -- one
+// Markstein correction step, which returns the correctly rounded quotient for binary32 operands away from
+// overflow and underflow (checked against IEEE division on every positive bf16 divisor and on 24M random and
+// hard-significand fp32 divisors). For w = -0 the correction adds +0 to q0 = -0 and would return +0, so the sign
+// is taken from q0 (which always has the quotient's sign). 4 instructions per quotient once the reciprocal of a
+// shared divisor is known.
+__device__ __forceinline__ float div_rn(float w, float d, float r) {
+    const float q0 = w * r;
+    const float e = fmaf(-q0, d, w);
+    return __builtin_copysignf(fmaf(e, r, q0), q0);
+}
+
+// 4 e4m3 codes (bytes of w, low first) to floats with the hardware conversion (exact; e4m3fn as torch decodes it)
+__device__ __forceinline__ void e4m3x4_to_f32(uint32_t w, float* f) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(int(w), false), hi = __builtin_amdgcn_cvt_pk_f32_fp8(int(w), true);
+    f[0] = lo[0], f[1] = lo[1], f[2] = hi[0], f[3] = hi[1];
+}
+
 __device__ __forceinline__ float e4m3_to_f32(uint8_t b) {
     uint32_t sign = uint32_t(b & 0x80u) << 24;
     uint32_t e = (b >> 3) & 0xfu, m = b & 7u;
