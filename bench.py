@@ -125,7 +125,7 @@ def instrumented(step):
         e0.record()
         out = orig_gemm(q, ascales, lora, qweight, *a, **k)
         e1.record()
-        rec["gemm"].append((e0, e1, 2.0 * M * qweight.shape[0] * q.shape[1]))
+        rec["gemm"].append((e0, e1, 2.0 * M * ops.out_features(qweight) * q.shape[1] * q.shape[3]))
         return out
 
     def attn(q_i8, q_scale, prep, L, sm_scale, out=None):

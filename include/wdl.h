@@ -50,8 +50,9 @@ int64_t wdl_act_quant_workspace_floats(int64_t Mp, int64_t K);
  * x: bf16 [M, K], row stride ldx (16-byte aligned rows); smooth: bf16 [K]; proj_down_t: bf16 [32, K] or NULL.
  * v = x, or with ln != 0: v = bf16(LN(x)[*ln_w + ln_b] * (1 + mod_scale) + mod_shift) (fp32 vectors, NULL = absent).
  * u = (v + qshift) / smooth; per row and 64-group: scale = bf16(max|u| / qmax) (qmax 7, or 15 if unsigned_q),
- * q = clamp(rint(u / scale)). Outputs: q as e4m3 codes of the integers [Mp, K]; ascales bf16 [K/64, Mp];
- * lora fp32 [Mp, 32] = v . proj_down; rows M..Mp-1 zero. Mp % 32 == 0. v_out (bf16 [M, K]) optional copy of v.
+ * q = clamp(rint(u / scale)). Outputs: q as e4m3 codes of the integers [Mp, K] in the tile-blocked layout (below);
+ * ascales bf16 [K/64, Mp]; lora fp32 [Mp, 32] = v . proj_down; rows M..Mp-1 zero. Mp % 128 == 0. v_out (bf16
+ * [M, K]) optional copy of v.
  * LayerNorm statistics: lane l of a wave owns the 8-value chunks l, l+64, ..., summed value by value, the 64 lane
  * sums combined by an xor butterfly 32..1 (the oracle's order). workspace: wdl_act_quant_workspace_floats(Mp, K). */
 int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K, const void* smooth, float qshift,
@@ -59,17 +60,22 @@ int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K, const voi
                      int64_t Mp, const float* mod_shift, const float* mod_scale, const float* ln_w,
                      const float* ln_b, int ln, float eps, void* v_out, float* workspace, wdl_stream_t stream);
 
+/* Tile-blocked layout of the W4A4 GEMM's code operands: a byte matrix [R, K] (R % 128 == 0, K % 64 == 0) stored as
+ * [R/128][K/64][128][64], byte (r, k) at (r/128)*128*K + (k/64)*8192 + (r%128)*64 + k%64, so the 64-deep slice of a
+ * 128-row tile that one GEMM step reads is one contiguous 8 KB block. */
+
 /* Weight operand of the W4A4 GEMM: packed int4 weights qweight uint8 [N, K/2] (per 64-group, byte j holds k = j in
- * the low nibble and k = j + 32 in the high nibble, two's complement) -> codes uint8 [N, K], the e4m3 encodings of
- * the same integers. Done once per weight (module construction), the expansion of the int4 weights that
- * Nunchaku's gemm_w4a4 performs inside every call (native/ops/w4a4_ops.cpp:36-38). 16-byte aligned buffers. */
+ * the low nibble and k = j + 32 in the high nibble, two's complement) -> codes uint8 [N, K] in the tile-blocked
+ * layout, the e4m3 encodings of the same integers. N % 128 == 0. Done once per weight (module construction), the
+ * expansion of the int4 weights that Nunchaku's gemm_w4a4 performs inside every call
+ * (native/ops/w4a4_ops.cpp:36-38). 16-byte aligned buffers. */
 int wdl_w4a4_weight_codes(const void* qweight, int64_t N, int64_t K, void* codes, wdl_stream_t stream);
 
 /* W4A4 GEMM with fused dequantization, low-rank up projection and bias. Replaces Nunchaku's gemm_w4a4 behind
  * live::w4a4_linear and live::w4a4_gelu_mlp (native/ops/w4a4_ops.cpp:36-38, 55-61).
  * y[m][n] = sum_g ascales[g][m] wscales[g][n] I_g[m][n] + bf16(lora[m]) . proj_up[n] + bias[n], I_g the exact
  * integer sum over the 64-group g. qa: [Mp, K] e4m3 codes (wdl_act_quant_w4); wcodes: [N, K] e4m3 codes
- * (wdl_w4a4_weight_codes); wscales bf16 [K/64, N]; lora fp32 [Mp, 32] or NULL; proj_up bf16 [N, 32]; bias bf16 [N]
+ * (wdl_w4a4_weight_codes), both tile-blocked; wscales bf16 [K/64, N]; lora fp32 [Mp, 32] or NULL; proj_up bf16 [N, 32]; bias bf16 [N]
  * or NULL. epilogue: 0 out bf16 [M, ldo] = y; 1 out fp32 = y; 2 out bf16 = bf16(out + bf16(y) * gate[n]) in place
  * (gated residual; gate fp32 [N]); 3 out bf16 = GELU_tanh(y). Mp % 128 == 0, N % 128 == 0, K % 64 == 0; qa, wcodes
  * 16-byte aligned, scales 4-byte aligned. */

@@ -25,7 +25,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     for name in declared():
         assert hasattr(lib, name), name
     assert set(declared()) == set(_lib.SIGNATURES)
-    assert lib.wdl_abi_version() == 2
+    assert lib.wdl_abi_version() == 3
     assert lib.wdl_last_error() == b""
 
 
@@ -70,5 +70,27 @@ def test_weight_operand_shapes_are_checked_before_any_launch():
         ops.as_codes(torch.zeros(4, 48, dtype=torch.uint8), 128)
     with pytest.raises(TypeError):
         ops.as_codes(torch.zeros(4, 64, dtype=torch.float32), 128)
-    codes = torch.zeros(4, 128, dtype=torch.uint8)
-    assert ops.as_codes(codes, 128) is not None
+    codes = torch.zeros(128, 128, dtype=torch.uint8)
+    assert ops.as_codes(codes, 128).shape == (1, 2, 128, 64)  # [N, K] codes are blocked
+    with pytest.raises(ValueError):
+        ops.as_codes(torch.zeros(1, 3, 128, 64, dtype=torch.uint8), 128)  # blocked codes of another width
+    with pytest.raises(ValueError):
+        ops.block_rows(torch.zeros(100, 128, dtype=torch.uint8))  # rows not a multiple of 128
+
+
+def test_tile_blocked_layout_round_trip_and_offsets():
+    """block_rows / unblock_rows are inverse; element (r, k) of the blocked copy sits at the byte offset
+    (r // 128) * 128 * K + (k // 64) * 8192 + (r % 128) * 64 + k % 64, the one the kernels use."""
+    import torch
+
+    from wdl import ops
+
+    R, K = 256, 192
+    t = torch.randint(0, 256, (R, K), generator=torch.Generator().manual_seed(0), dtype=torch.int32).to(torch.uint8)
+    b = ops.block_rows(t)
+    assert b.shape == (2, 3, 128, 64) and b.is_contiguous()
+    assert torch.equal(ops.unblock_rows(b), t)
+    flat = b.reshape(-1)
+    for r, k in [(0, 0), (5, 70), (127, 191), (128, 0), (200, 100), (255, 191)]:
+        off = (r // 128) * 128 * K + (k // 64) * 8192 + (r % 128) * 64 + k % 64
+        assert int(flat[off]) == int(t[r, k])

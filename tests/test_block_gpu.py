@@ -159,7 +159,7 @@ def test_config1_stages_given_identical_inputs(gpu):
     def gpu_lin(x, name, shift=0.0, unsigned=False, epi=0):
         t = blk.p[name]
         qa = ops.act_quant_launch(x.to(dev).contiguous(), t["smooth"], t["proj_down"], shift, unsigned)
-        out = torch.empty(x.shape[0], t["wcodes"].shape[0], device=dev, dtype=BF)
+        out = torch.empty(x.shape[0], ops.out_features(t["wcodes"]), device=dev, dtype=BF)
         ops.gemm_launch(*qa, t["wcodes"], t["wscales"], t["proj_up"], t["bias"], x.shape[0], out, epi)
         return out.cpu()
 

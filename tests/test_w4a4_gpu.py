@@ -16,7 +16,13 @@ pytestmark = pytest.mark.gpu
 
 
 def codes_to_int(q):
-    return q.cpu().view(torch.float8_e4m3fn).float().to(torch.int32)
+    """e4m3 codes -> their integer values; tile-blocked operands [R/128, K/64, 128, 64] as the [R, K] matrix."""
+    from wdl import ops
+
+    q = q.cpu()
+    if q.dim() == 4:
+        q = ops.unblock_rows(q)
+    return q.view(torch.float8_e4m3fn).float().to(torch.int32)
 
 
 def data(M, K, seed=0, outliers=True):
@@ -42,7 +48,7 @@ def test_act_quant_bit_exact(gpu, M, K, unsigned):
     q, asc, lora = ops.act_quant_launch(x.cuda(), smooth.cuda(), pdt.cuda(), shift, unsigned)
     torch.cuda.synchronize()
     rq, rs = ow.act_quant(x, smooth, shift, unsigned)
-    Mp = q.shape[0]
+    Mp = asc.shape[1]
     assert Mp % 128 == 0 and Mp >= M
     assert torch.equal(codes_to_int(q)[:M], rq)  # bar: bit-exact int4 values
     assert torch.equal(codes_to_int(q)[M:], torch.zeros(Mp - M, K, dtype=torch.int32))
@@ -81,7 +87,7 @@ def launch_gemm(qa_int, asc, qweight, wsc, lora=None, pu=None, bias=None, M=None
     from wdl import ops
 
     Mp, K = qa_int.shape
-    codes = qa_int.float().to(torch.float8_e4m3fn).view(torch.uint8).cuda()
+    codes = ops.block_rows(qa_int.float().to(torch.float8_e4m3fn).view(torch.uint8)).cuda()
     N = qweight.shape[0]
     M = Mp if M is None else M
     if out is None:
@@ -93,13 +99,16 @@ def launch_gemm(qa_int, asc, qweight, wsc, lora=None, pu=None, bias=None, M=None
 
 @pytest.mark.parametrize("N,K", [(128, 64), (384, 3072), (256, 14336)])
 def test_weight_codes_are_the_e4m3_values_of_the_packed_integers(gpu, N, K):
-    """wdl_w4a4_weight_codes: packed nibbles [N, K/2] -> e4m3 codes [N, K], bit-exact against torch's e4m3 of the
-    unpacked integers (every int4 value is exactly representable)."""
+    """wdl_w4a4_weight_codes: packed nibbles [N, K/2] -> tile-blocked e4m3 codes of [N, K], bit-exact against torch's
+    e4m3 of the unpacked integers (every int4 value is exactly representable), in the blocked order."""
     from wdl import ops, w4a4
 
     q = torch.randint(-8, 8, (N, K), generator=torch.Generator().manual_seed(N + K), dtype=torch.int32)
     codes = ops.weight_codes(w4a4.pack_weight(q).cuda()).cpu()
-    assert torch.equal(codes, q.float().to(torch.float8_e4m3fn).view(torch.uint8))
+    want = q.float().to(torch.float8_e4m3fn).view(torch.uint8)
+    assert codes.shape == (N // 128, K // 64, 128, 64)
+    assert torch.equal(ops.unblock_rows(codes), want)
+    assert torch.equal(codes[-1, -1, 127], want[N - 1, K - 64:])  # the last 64-byte row of the last tile
 
 
 @pytest.mark.parametrize("M,N,K", [(128, 128, 64), (256, 384, 512), (128, 256, 3072), (128, 128, 14336),

@@ -8,8 +8,9 @@
 //   scale = bf16( max_{64 group} |u| / qmax )                       (qmax 7 signed, 15 unsigned)
 //   q     = clamp(rint(u / scale))                                  (0 where scale is 0)
 //   lora  = v . proj_down                                           (bf16 MFMA, fp32 sums)
-// Outputs: q as e4m3 codes of the integer values (exact), one byte per value [Mp, K] (rows >= M zero);
-// ascales bf16 [K/64, Mp]; lora fp32 [Mp, 32].
+// Outputs: q as e4m3 codes of the integer values (exact), one byte per value [Mp, K] (rows >= M zero) in the W4A4
+// GEMM's tile-blocked layout ([Mp / 128][K / 64][128][64], Mp a multiple of 128); ascales bf16 [K/64, Mp]; lora fp32
+// [Mp, 32].
 //
 // Launches (all parallel over rows and column blocks, nothing serial over K):
 //   row_stats  (LN only): one wave per row; LN statistics in a fixed order — lane l owns the 8-value chunks
@@ -93,7 +94,7 @@ struct QuantArgs {
     float qshift;
     int unsigned_q;
     const uint16_t* pdt;       // bf16 [RANK, K] (proj_down transposed), or null (no low-rank branch)
-    uint8_t* q;                // [Mp, K]
+    uint8_t* q;                // [Mp, K], tile-blocked
     uint16_t* ascales;         // [K/64, Mp]
     float* lora;               // [nblocks, Mp, RANK] partials (or [Mp, RANK] when nblocks == 1)
     const float2* stats;       // LN (mean, rstd) per row, or null (no LN)
@@ -224,7 +225,7 @@ __global__ __launch_bounds__(QT) void quant_kernel(QuantArgs a) {
         w1 = __builtin_amdgcn_cvt_pk_fp8_f32(qv[4], qv[5], w1, false);
         w1 = __builtin_amdgcn_cvt_pk_fp8_f32(qv[6], qv[7], w1, true);
         if (row < a.Mp) {
-            *reinterpret_cast<uint2*>(a.q + row * K + col) = make_uint2(w0, w1);
+            *reinterpret_cast<uint2*>(a.q + blocked_offset(row, col, K)) = make_uint2(w0, w1);
             if (slot == 0) a.ascales[(col / 64) * a.Mp + row] = live ? sb : uint16_t(0);
         }
     }
@@ -270,7 +271,7 @@ extern "C" int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K
                                 float* lora, int64_t Mp, const float* mod_shift, const float* mod_scale,
                                 const float* ln_w, const float* ln_b, int ln, float eps, void* v_out,
                                 float* workspace, hipStream_t stream) {
-    if (M < 0 || K <= 0 || K % 64 || Mp < M || Mp % ROWS || ldx < K)
+    if (M < 0 || K <= 0 || K % 64 || Mp < M || Mp % BLOCK_ROWS || ldx < K)
         return fail(WDL_EINVAL, "act_quant_w4: bad shape M=%lld K=%lld Mp=%lld ldx=%lld", (long long)M,
                     (long long)K, (long long)Mp, (long long)ldx);
     if (ln && K > 64 * 8 * MAXCH) return fail(WDL_EINVAL, "act_quant_w4: LayerNorm rows above 4096");

@@ -83,53 +83,100 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// Low-rank branch, bias and epilogue of one wave's TN x TM subtiles (rows nb0 + 32 i + .., tokens mb0 + 32 j + ..);
-// only >= 0 restricts the work to the subtile row i == only.
+// Low-rank branch, bias and epilogue of one wave's TN x TM subtiles (rows nb0 + 32 i + .., tokens mb0 + 32 j + ..).
+// Every load the epilogue needs (low-rank operands, bias, gate, the residual it updates, FP8 scales) is issued
+// before the first store: the output may alias nothing the compiler can see, so loads written between the stores
+// would each wait for the previous stores and pay a full memory round trip.
 template <int TN, int TM, int EPI>
 __device__ __forceinline__ void finish_tile(const GemmArgs& p, f32x16 (&acc)[TN][TM], int64_t nb0, int64_t mb0,
-                                            int lane, int only) {
-    // low-rank branch: acc += pu[n] . bf16(lora[m]) over r = 0..31, two 32x32x16 bf16 MFMAs per subtile
+                                            int lane) {
+    const int half = lane / 32;
+    // ---- loads
+    bf16x8 pa[TN][2];
+    float4 lr[TM][2][2];
     if (p.lora) {
 #pragma unroll
-        for (int i = 0; i < TN; ++i) {
-            if (only >= 0 && i != only) continue;
-            const int64_t n = nb0 + i * 32 + lane % 32;
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                pa[i][h] = *reinterpret_cast<const bf16x8*>(p.pu + (nb0 + i * 32 + lane % 32) * 32 + h * 16 + 8 * half);
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const bf16x8 pa = *reinterpret_cast<const bf16x8*>(p.pu + n * 32 + h * 16 + 8 * (lane / 32));
-#pragma unroll
-                for (int j = 0; j < TM; ++j) {
-                    const int64_t m = mb0 + j * 32 + lane % 32;
-                    const float* lr = p.lora + m * 32 + h * 16 + 8 * (lane / 32);
-                    bf16x8 lb;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) lb[e] = __builtin_bit_cast(__bf16, f32_to_bf16(lr[e]));
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa, lb, acc[i][j], 0, 0, 0);
-                }
+                const float* l = p.lora + (mb0 + j * 32 + lane % 32) * 32 + h * 16 + 8 * half;
+                lr[j][h][0] = *reinterpret_cast<const float4*>(l);
+                lr[j][h][1] = *reinterpret_cast<const float4*>(l + 4);
             }
+    }
+    // per (i, q): this lane's 4 output features nb = nb0 + 32 i + 8 q + 4 half .. + 3
+    uint2 bias[TN][4];
+    float4 gate[TN][4];
+    float4 wsf[TN][4];
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int64_t nb = nb0 + i * 32 + 8 * q + 4 * half;
+            bias[i][q] = p.bias ? *reinterpret_cast<const uint2*>(p.bias + nb) : make_uint2(0u, 0u);
+            if (EPI == EPI_RESIDUAL) gate[i][q] = *reinterpret_cast<const float4*>(p.gate + nb);
+            if (EPI == EPI_FP8_ROWS) wsf[i][q] = *reinterpret_cast<const float4*>(p.wsf + nb);
         }
+    uint2 old[TN][TM][4];
+    float xsm[TM];
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+        const int64_t m = mb0 + j * 32 + lane % 32;
+        const int64_t mm = m < p.M ? m : 0;  // rows past M read row 0 and are not stored
+        if (EPI == EPI_FP8_ROWS) xsm[j] = p.xs[m];
+        if (EPI == EPI_RESIDUAL)
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    old[i][j][q] = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.out) + mm * p.ldo +
+                                                                   nb0 + i * 32 + 8 * q + 4 * half);
+    }
+    const float xs0 = EPI == EPI_FP8_TENSOR ? p.xs[0] * p.wsf[0] : 0.0f;
+
+    // ---- low-rank branch: acc += pu[n] . bf16(lora[m]) over r = 0..31, two 32x32x16 bf16 MFMAs per subtile
+    if (p.lora) {
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                bf16x8 lb;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    lb[e] = __builtin_bit_cast(__bf16, f32_to_bf16(lr[j][h][0][e]));
+                    lb[4 + e] = __builtin_bit_cast(__bf16, f32_to_bf16(lr[j][h][1][e]));
+                }
+#pragma unroll
+                for (int i = 0; i < TN; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[i][h], lb, acc[i][j], 0, 0, 0);
+            }
     }
 
-    // epilogue
+    // ---- epilogue and stores
 #pragma unroll
     for (int i = 0; i < TN; ++i)
 #pragma unroll
         for (int j = 0; j < TM; ++j) {
-            if (only >= 0 && i != only) continue;
             const int64_t m = mb0 + j * 32 + lane % 32;
             if (m >= p.M) continue;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int64_t nb = nb0 + i * 32 + 8 * q + 4 * (lane / 32);
+                const int64_t nb = nb0 + i * 32 + 8 * q + 4 * half;
+                const uint16_t bv[4] = {uint16_t(bias[i][q].x), uint16_t(bias[i][q].x >> 16), uint16_t(bias[i][q].y),
+                                        uint16_t(bias[i][q].y >> 16)};
                 float y[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     y[e] = acc[i][j][4 * q + e];
                     if (EPI == EPI_FP8_ROWS)  // fp8.py:57-62: bf16 product, then * (xs ws) in fp32, + b
-                        y[e] = bf16_to_f32(f32_to_bf16(y[e])) * (p.xs[m] * p.wsf[nb + e]);
+                        y[e] = bf16_to_f32(f32_to_bf16(y[e])) * (xsm[j] * wsf[i][q][e]);
                     else if (EPI == EPI_FP8_TENSOR)  // _scaled_mm: acc * (xs ws) + b, one rounding
-                        y[e] = y[e] * (p.xs[0] * p.wsf[0]);
-                    if (p.bias) y[e] = y[e] + bf16_to_f32(p.bias[nb + e]);
+                        y[e] = y[e] * xs0;
+                    if (p.bias) y[e] = y[e] + bf16_to_f32(bv[e]);
                 }
                 if (EPI == EPI_F32) {
                     float* o = static_cast<float*>(p.out) + m * p.ldo + nb;
@@ -138,13 +185,12 @@ __device__ __forceinline__ void finish_tile(const GemmArgs& p, f32x16 (&acc)[TN]
                     uint16_t* o = static_cast<uint16_t*>(p.out) + m * p.ldo + nb;
                     uint16_t r[4];
                     if (EPI == EPI_RESIDUAL) {
-                        const uint2 old = *reinterpret_cast<const uint2*>(o);
-                        const uint16_t ov[4] = {uint16_t(old.x), uint16_t(old.x >> 16), uint16_t(old.y),
-                                                uint16_t(old.y >> 16)};
+                        const uint2 ow = old[i][j][q];
+                        const uint16_t ov[4] = {uint16_t(ow.x), uint16_t(ow.x >> 16), uint16_t(ow.y), uint16_t(ow.y >> 16)};
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const float yb = bf16_to_f32(f32_to_bf16(y[e]));
-                            r[e] = f32_to_bf16(bf16_to_f32(ov[e]) + yb * p.gate[nb + e]);
+                            r[e] = f32_to_bf16(bf16_to_f32(ov[e]) + yb * gate[i][q][e]);
                         }
                     } else if (EPI == EPI_GELU) {
 #pragma unroll
@@ -161,8 +207,9 @@ __device__ __forceinline__ void finish_tile(const GemmArgs& p, f32x16 (&acc)[TN]
 
 // The main loop of both GEMMs. FOLD: the W4A4 product (per-group scale fold, scales streamed with the codes);
 // otherwise the FP8 product (codes only, one fp32 accumulation over all of K in the MFMA accumulator).
-template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES, bool FOLD>
+template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES, bool FOLD, bool BLK>
 __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
+    static_assert(!BLK || (BN == BLOCK_ROWS && BM == BLOCK_ROWS), "blocked operands come in 128-row tiles");
     static_assert((BN / WN) * (BM / WM) == NW, "wave grid");
     static_assert(STAGES >= 3 && STAGES <= 8, "ring depth");
     constexpr int TN = WN / 32, TM = WM / 32;
@@ -197,14 +244,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
     for (int j = 0; j < XI; ++j) {
         const int slot = (wave * XI + j) * 64 + lane;          // 16-byte slot of the stage
         const int row = slot / 4, quarter = (slot % 4) ^ ((row >> 2) & 3);
-        xsrc[j] = p.qa + (m0 + row) * K + quarter * 16;
+        xsrc[j] = BLK ? p.qa + m0 * K + row * 64 + quarter * 16 : p.qa + (m0 + row) * K + quarter * 16;
     }
     const uint8_t* wsrc[WI];
 #pragma unroll
     for (int j = 0; j < WI; ++j) {
         const int slot = (wave * WI + j) * 64 + lane;
         const int row = slot / 4, quarter = (slot % 4) ^ ((row >> 2) & 3);
-        wsrc[j] = p.wc + (n0 + row) * K + quarter * 16;
+        wsrc[j] = BLK ? p.wc + n0 * K + row * 64 + quarter * 16 : p.wc + (n0 + row) * K + quarter * 16;
     }
     const uint8_t* ssrc;   // 4 bytes: ws pair, as pair or (padding lanes) a valid dummy
     int64_t sstride;
@@ -222,14 +269,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         }
     }
 
-    // direct loads of group g (clamped to the last group) into stage st
-    auto issue = [&](int st, int64_t g) {
+    // direct load u (0 .. LPG - 1: activation codes, weight codes, scales) of group g (clamped to the last group)
+    // into stage st
+    auto issue_one = [&](int st, int64_t g, int u) {
         const int64_t gg = g < G ? g : G - 1;
-#pragma unroll
-        for (int j = 0; j < XI; ++j) dma16(xsrc[j] + gg * 64, lds_addr(&sX[st][(wave * XI + j) * 1024]));
-#pragma unroll
-        for (int j = 0; j < WI; ++j) dma16(wsrc[j] + gg * 64, lds_addr(&sW[st][(wave * WI + j) * 1024]));
-        if constexpr (FOLD) dma4(ssrc + gg * sstride, lds_addr(&sS[st][wave * 256]));
+        if (u < XI) dma16(xsrc[u] + gg * (BLK ? BM * 64 : 64), lds_addr(&sX[st][(wave * XI + u) * 1024]));
+        else if (u < XI + WI)
+            dma16(wsrc[u - XI] + gg * (BLK ? BN * 64 : 64), lds_addr(&sW[st][(wave * WI + u - XI) * 1024]));
+        else if constexpr (FOLD) dma4(ssrc + gg * sstride, lds_addr(&sS[st][wave * 256]));
     };
 
     // per-lane LDS offsets (stage-independent): operand rows with their swizzled quarters, scale entries
@@ -263,72 +310,113 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         for (int j = 0; j < TM; ++j) acc[i][j] = f32x16{};
     const f32x16 zero = {};
 
-    auto multiply = [&](int st) {
-        i32x8 af[TN], bf[TM];
-        short sa[TN], sb[TM];
-#pragma unroll
-        for (int i = 0; i < TN; ++i) {
-            const uint8_t* r = &sW[st][aoff[i]];
-            const uint4 a0 = *reinterpret_cast<const uint4*>(r + q0), a1 = *reinterpret_cast<const uint4*>(r + q1);
-            af[i] = i32x8{int(a0.x), int(a0.y), int(a0.z), int(a0.w), int(a1.x), int(a1.y), int(a1.z), int(a1.w)};
-            if constexpr (FOLD) sa[i] = *reinterpret_cast<const short*>(&sS[st][soa[i]]);
-        }
-#pragma unroll
-        for (int j = 0; j < TM; ++j) {
-            const uint8_t* r = &sX[st][boff[j]];
-            const uint4 b0 = *reinterpret_cast<const uint4*>(r + q0), b1 = *reinterpret_cast<const uint4*>(r + q1);
-            bf[j] = i32x8{int(b0.x), int(b0.y), int(b0.z), int(b0.w), int(b1.x), int(b1.y), int(b1.z), int(b1.w)};
-            if constexpr (FOLD) sb[j] = *reinterpret_cast<const short*>(&sS[st][sob[j]]);
-        }
-        if constexpr (!FOLD) {
-#pragma unroll
-            for (int i = 0; i < TN; ++i)
-#pragma unroll
-                for (int j = 0; j < TM; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[i], bf[j], acc[i][j], 0, 0, 0, 0,
-                                                                                0, 0);
-            return;
-        }
-#pragma unroll
-        for (int i = 0; i < TN; ++i)
-#pragma unroll
-            for (int j = 0; j < TM; ++j) {
-                const i16x4 oa = {sa[i], 0, 0, 0}, ob = {sb[j], 0, 0, 0};
-                const f32x16 I = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[i], bf[j], zero, 0, 0, 0, 0, 0, 0);
-                const f32x16 P = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(oa, ob, zero, 0, 0, 0);
-#pragma unroll
-                for (int e = 0; e < 16; ++e) acc[i][j][e] = fmaf(I[e], P[e], acc[i][j][e]);
-            }
+    // one group's operands in registers: weight / activation code fragments and (FOLD) the bf16 scale of each
+    // fragment row, zero-extended (lanes 32..63 read the zero tail)
+    i32x8 fa[TN], fb[TM];
+    uint32_t fsa[TN], fsb[TM];
+    auto load_a = [&](int st, int i) {
+        const uint8_t* r = &sW[st][aoff[i]];
+        const uint4 a0 = *reinterpret_cast<const uint4*>(r + q0), a1 = *reinterpret_cast<const uint4*>(r + q1);
+        fa[i] = i32x8{int(a0.x), int(a0.y), int(a0.z), int(a0.w), int(a1.x), int(a1.y), int(a1.z), int(a1.w)};
+        if constexpr (FOLD) fsa[i] = *reinterpret_cast<const uint16_t*>(&sS[st][soa[i]]);
+    };
+    auto load_b = [&](int st, int j) {
+        const uint8_t* r = &sX[st][boff[j]];
+        const uint4 b0 = *reinterpret_cast<const uint4*>(r + q0), b1 = *reinterpret_cast<const uint4*>(r + q1);
+        fb[j] = i32x8{int(b0.x), int(b0.y), int(b0.z), int(b0.w), int(b1.x), int(b1.y), int(b1.z), int(b1.w)};
+        if constexpr (FOLD) fsb[j] = *reinterpret_cast<const uint16_t*>(&sS[st][sob[j]]);
     };
 
-    // Ring step for group g on stage g % STAGES: wait until this wave's loads of groups <= g have landed (the
-    // STAGES - 2 groups after it may still be in flight) and for every wave (barrier); the stage of group g - 1 is
-    // free again: issue group g + STAGES - 1 into it; multiply group g. Unrolled by STAGES (constant stages).
+    // Multiply one group from the fragment registers; each fragment is reloaded with the next group's operands
+    // (stage nst) right after its last use, so the reads overlap the remaining MFMAs and one register set serves.
+    // FOLD: the fold is software-pipelined by one subtile: the products of subtile s are folded while the MFMAs of
+    // subtile s + 1 run (the last subtile of a group while the first subtile of the next group runs). pI / pP hold
+    // the pending subtile; they start at zero (the first fold adds 0 * 0 to a zero accumulator: no change).
+    f32x16 pI = zero, pP = zero;
+    // The step's LPG direct loads (group ig into stage ist) are spread over its subtiles, one or two after each
+    // subtile's MFMAs, so a wave never waits on a full load queue with MFMA work still to issue.
+    auto step = [&](int nst, int ist, int64_t ig) {
 #pragma unroll
-    for (int k = 0; k < STAGES - 1; ++k) issue(k, k);
-    for (int64_t g = 0; g < G; g += STAGES) {
+        for (int s = 0; s < TN * TM; ++s) {
+            const int i = s / TM, j = s % TM;
+            if constexpr (FOLD) {
+                const int pi = s == 0 ? TN - 1 : (s - 1) / TM, pj = s == 0 ? TM - 1 : (s - 1) % TM;
+                const i16x4 oa = __builtin_bit_cast(i16x4, make_uint2(fsa[i], 0u));
+                const i16x4 ob = __builtin_bit_cast(i16x4, make_uint2(fsb[j], 0u));
+                const f32x16 I = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[i], fb[j], zero, 0, 0, 0, 0, 0, 0);
+                const f32x16 P = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(oa, ob, zero, 0, 0, 0);
 #pragma unroll
-        for (int k = 0; k < STAGES; ++k) {
-            if (g + k >= G) break;
-            wait_vmcnt<(STAGES - 2) * LPG>();
-            __syncthreads();
-            issue((k + STAGES - 1) % STAGES, g + k + STAGES - 1);
-            multiply(k);
+                for (int e = 0; e < 16; ++e) acc[pi][pj][e] = fmaf(pI[e], pP[e], acc[pi][pj][e]);
+                pI = I;
+                pP = P;
+            } else {
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[i], fb[j], acc[i][j], 0, 0, 0, 0, 0, 0);
+            }
+            if (j == TM - 1) load_a(nst, i);
+            if (i == TN - 1) load_b(nst, j);
+            // one wave issues in order and an MFMA waits at issue while the matrix core is busy, so the fold of
+            // subtile s - 1 is split around the two MFMAs of subtile s: it executes while they run
+            if constexpr (FOLD) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // I_s (64 cycles)
+                __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // fold of s - 1, first part
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // P_s (32 cycles)
+                __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // the rest
+                __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);   // the reloads subtile s freed
+            } else {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+            }
+#pragma unroll
+            for (int u = s * LPG / (TN * TM); u < (s + 1) * LPG / (TN * TM); ++u) issue_one(ist, ig, u);
         }
+    };
+
+    // Ring, one group per step. Step h: this wave's loads of group h + 1 have landed (the STAGES - 3 groups after
+    // it may still be in flight); after the barrier the same holds for every wave. The stage of group h - 1 is
+    // free: every wave read it into registers during step h - 2 and used them in step h - 1, so no wait on LDS
+    // reads comes before the barrier. Group h + STAGES - 1 goes into it (clamped to the last group, so every step
+    // issues the same loads and vmcnt counts stay exact). Then group h is multiplied from the registers while the
+    // reads of group h + 1 refill them. Whole turns of the ring are unrolled (constant stages); the remaining
+    // G % STAGES steps run with the stage computed at run time.
+    static_assert(STAGES >= 4, "the ring keeps one stage being read, one free and two or more in flight");
+#pragma unroll
+    for (int k = 0; k < STAGES - 1; ++k)
+#pragma unroll
+        for (int u = 0; u < LPG; ++u) issue_one(k, k, u);
+    wait_vmcnt<(STAGES - 2) * LPG>();
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TN; ++i) load_a(0, i);
+#pragma unroll
+    for (int j = 0; j < TM; ++j) load_b(0, j);
+    auto ring_step = [&](int k, int64_t h) {
+        wait_vmcnt<(STAGES - 3) * LPG>();
+        __syncthreads();
+        step(k + 1 == STAGES ? 0 : k + 1, k == 0 ? STAGES - 1 : k - 1, h + STAGES - 1);
+    };
+    int64_t g = 0;
+    for (; g + STAGES <= G; g += STAGES) {
+#pragma unroll
+        for (int k = 0; k < STAGES; ++k) ring_step(k, g + k);
+    }
+    for (int k = 0; g < G; ++g, ++k) ring_step(k, g);
+    if constexpr (FOLD) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[TN - 1][TM - 1][e] = fmaf(pI[e], pP[e], acc[TN - 1][TM - 1][e]);
     }
     wait_vmcnt<0>();  // the clamped tail loads land before the workgroup can end
 
-    finish_tile<TN, TM, EPI>(p, acc, n0 + wn * WN, m0 + wm * WM, lane, -1);
+    finish_tile<TN, TM, EPI>(p, acc, n0 + wn * WN, m0 + wm * WM, lane);
 }
 
 template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES>
 __global__ __launch_bounds__(NW * 64) void w4a4_gemm_kernel(GemmArgs p) {
-    gemm_body<BN, BM, WN, WM, NW, EPI, STAGES, true>(p);
+    gemm_body<BN, BM, WN, WM, NW, EPI, STAGES, true, true>(p);
 }
 
 template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES>
 __global__ __launch_bounds__(NW * 64) void fp8_gemm_kernel(GemmArgs p) {
-    gemm_body<BN, BM, WN, WM, NW, EPI, STAGES, false>(p);
+    gemm_body<BN, BM, WN, WM, NW, EPI, STAGES, false, false>(p);
 }
 
 template <int BN, int BM, int WN, int WM, int NW, int ST>
@@ -358,10 +446,20 @@ int launch_fp8(const GemmArgs& a, int epi, hipStream_t stream) {
     return check_launch("fp8_gemm");
 }
 
-// Tile configuration: 128 x 128 per workgroup, 4 waves of 64 x 64, a 4-stage ring (69 KB of LDS: two workgroups
-// per CU). Measured on the block shapes at 1392 and 2640 tokens against 6- and 8-stage rings (one workgroup per CU)
-// and an 8-wave even/odd split of the groups: this one is fastest on all of them.
-int dispatch(const GemmArgs& a, int epi, hipStream_t stream) { return launch<128, 128, 64, 64, 4, 4>(a, epi, stream); }
+// Tile configuration: 128 x 128 per workgroup, 4 waves of 64 x 64, a WDL_GEMM_STAGES-deep ring.
+#ifndef WDL_GEMM_STAGES
+#define WDL_GEMM_STAGES 4
+#endif
+#ifndef WDL_GEMM_WM
+#define WDL_GEMM_WM 64
+#endif
+#ifndef WDL_GEMM_WN
+#define WDL_GEMM_WN 64
+#endif
+int dispatch(const GemmArgs& a, int epi, hipStream_t stream) {
+    constexpr int NW = (128 / WDL_GEMM_WN) * (128 / WDL_GEMM_WM);
+    return launch<128, 128, WDL_GEMM_WN, WDL_GEMM_WM, NW, WDL_GEMM_STAGES>(a, epi, stream);
+}
 
 // e4m3 codes of the two's complement nibbles 0..7 (values 0..7) and 8..15 (values -8..-1)
 constexpr uint32_t LUT0 = 0x44403800u, LUT1 = 0x4E4C4A48u, LUT2 = 0xCACCCED0u, LUT3 = 0xB8C0C4C8u;
@@ -376,7 +474,7 @@ __device__ __forceinline__ uint32_t nib4_to_e4m3(uint32_t x) {
     return (neg & mask) | (pos & ~mask);
 }
 
-// packed nibbles [N, K/2] -> e4m3 codes [N, K]: one thread per 4 packed bytes (8 values)
+// packed nibbles [N, K/2] -> e4m3 codes [N, K] in the tile-blocked layout: one thread per 4 packed bytes (8 values)
 __global__ __launch_bounds__(256) void weight_codes_kernel(const uint32_t* qw, int64_t words, int64_t K,
                                                          uint32_t* codes) {
     const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
@@ -385,7 +483,7 @@ __global__ __launch_bounds__(256) void weight_codes_kernel(const uint32_t* qw, i
     const int64_t byte = 4 * i, row = byte / (K / 2), in_row = byte % (K / 2);
     const int64_t g = in_row / 32, j0 = in_row % 32;
     const uint32_t w = qw[i];
-    uint32_t* dst = codes + (row * K + g * 64 + j0) / 4;
+    uint32_t* dst = codes + blocked_offset(row, g * 64 + j0, K) / 4;
     dst[0] = nib4_to_e4m3(w & 0x0f0f0f0fu);              // k = j0..j0+3
     dst[8] = nib4_to_e4m3((w >> 4) & 0x0f0f0f0fu);       // k = 32 + j0..j0+3
 }
@@ -407,7 +505,11 @@ extern "C" int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wc
         (reinterpret_cast<uintptr_t>(ascales) | reinterpret_cast<uintptr_t>(wscales)) % 4)
         return fail(WDL_EINVAL, "w4a4_gemm: operands must be 16-byte (codes) / 4-byte (scales) aligned");
     if (epilogue == EPI_RESIDUAL && !gate) return fail(WDL_EINVAL, "w4a4_gemm: residual epilogue needs gate");
-    if (Mp == 0) return WDL_OK;
+    if (reinterpret_cast<uintptr_t>(gate) % 16 || reinterpret_cast<uintptr_t>(bias) % 8 ||
+        reinterpret_cast<uintptr_t>(out) % 8 || reinterpret_cast<uintptr_t>(proj_up) % 16 ||
+        reinterpret_cast<uintptr_t>(lora) % 16)
+        return fail(WDL_EINVAL, "w4a4_gemm: gate, lora and proj_up must be 16-byte aligned, bias and out 8-byte");
+    if (M == 0) return WDL_OK;
     GemmArgs a{static_cast<const uint8_t*>(qa), static_cast<const uint16_t*>(ascales),
                static_cast<const uint8_t*>(wcodes), static_cast<const uint16_t*>(wscales), lora,
                static_cast<const uint16_t*>(proj_up), static_cast<const uint16_t*>(bias), M, Mp, N, K, out, ldo,
@@ -416,8 +518,9 @@ extern "C" int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wc
 }
 
 extern "C" int wdl_w4a4_weight_codes(const void* qweight, int64_t N, int64_t K, void* codes, hipStream_t stream) {
-    if (N < 0 || K <= 0 || K % 64) return fail(WDL_EINVAL, "w4a4_weight_codes: bad shape N=%lld K=%lld",
-                                               (long long)N, (long long)K);
+    if (N < 0 || N % BLOCK_ROWS || K <= 0 || K % 64)
+        return fail(WDL_EINVAL, "w4a4_weight_codes: bad shape N=%lld K=%lld (N %% 128 == 0, K %% 64 == 0)",
+                    (long long)N, (long long)K);
     if (!qweight || !codes) return fail(WDL_EINVAL, "w4a4_weight_codes: null pointer");
     if ((reinterpret_cast<uintptr_t>(qweight) | reinterpret_cast<uintptr_t>(codes)) % 16)
         return fail(WDL_EINVAL, "w4a4_weight_codes: buffers must be 16-byte aligned");
@@ -437,7 +540,10 @@ extern "C" int wdl_fp8_gemm(const void* xq, const float* x_scale, const void* wq
     if (!xq || !x_scale || !wq || !w_scale || !out) return fail(WDL_EINVAL, "fp8_gemm: null pointer");
     if ((reinterpret_cast<uintptr_t>(xq) | reinterpret_cast<uintptr_t>(wq)) % 16)
         return fail(WDL_EINVAL, "fp8_gemm: operands must be 16-byte aligned");
-    if (Mp == 0) return WDL_OK;
+    if (reinterpret_cast<uintptr_t>(bias) % 8 || reinterpret_cast<uintptr_t>(out) % 8 ||
+        (rows && reinterpret_cast<uintptr_t>(w_scale) % 16))
+        return fail(WDL_EINVAL, "fp8_gemm: bias and out must be 8-byte aligned, row scales 16-byte");
+    if (M == 0) return WDL_OK;
     GemmArgs a{static_cast<const uint8_t*>(xq), nullptr, static_cast<const uint8_t*>(wq), nullptr, nullptr, nullptr,
                static_cast<const uint16_t*>(bias), M, Mp, N, K, out, ldo, nullptr, x_scale, w_scale};
     return launch_fp8(a, rows ? EPI_FP8_ROWS : EPI_FP8_TENSOR, stream);

@@ -26,6 +26,14 @@ namespace wdl {
 int fail(int code, const char* fmt, ...);
 int check_launch(const char* what);
 
+// The W4A4 GEMM's operand layout ("tile-blocked"): a byte matrix [R, K] (R a multiple of 128, K of 64) stored as
+// [R / 128][K / 64][128][64], so the 64-deep slice of a 128-row tile that one GEMM step reads is one contiguous
+// 8 KB block. Byte (r, k) sits at blocked_offset(r, k, K).
+constexpr int BLOCK_ROWS = 128;
+__host__ __device__ __forceinline__ int64_t blocked_offset(int64_t r, int64_t k, int64_t K) {
+    return (r / BLOCK_ROWS) * BLOCK_ROWS * K + (k / 64) * (BLOCK_ROWS * 64) + (r % BLOCK_ROWS) * 64 + k % 64;
+}
+
 // ---------------------------------------------------------------- bf16 / fp16 / fp8 conversions (exact, RNE)
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }

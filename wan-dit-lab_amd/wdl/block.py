@@ -33,7 +33,7 @@ class QuantizedWanBlock:
     def __init__(self, parts: dict, dim: int, heads: int, eps: float = 1e-6):
         self.p, self.dim, self.heads, self.eps = parts, dim, heads, eps
         dev = parts["qkv"]["qweight"].device
-        for name in LINEARS:  # the GEMM operand: e4m3 codes [N, K], expanded once from the packed nibbles
+        for name in LINEARS:  # the GEMM operand: tile-blocked e4m3 codes, expanded once from the packed nibbles
             parts[name]["wcodes"] = ops.weight_codes(parts[name]["qweight"])
         self.ones = torch.ones(dim, device=dev, dtype=torch.float32)
 
@@ -49,7 +49,7 @@ class QuantizedWanBlock:
                                gate)
 
     def linear(self, x, name):
-        out = torch.empty(x.shape[0], self.p[name]["wcodes"].shape[0], device=x.device, dtype=torch.bfloat16)
+        out = torch.empty(x.shape[0], ops.out_features(self.p[name]["wcodes"]), device=x.device, dtype=torch.bfloat16)
         return self._gemm(self._quant(x, name), name, x.shape[0], out)
 
     def prepare_context(self, C: torch.Tensor) -> dict:
@@ -96,7 +96,7 @@ class QuantizedWanBlock:
         Ac = ops.sage_attn_launch(q_i8, q_sc, ctx, ctx["L"], 128 ** -0.5)
         self._gemm(self._quant(Ac, "co"), "co", M, X, EPI_RESIDUAL, self.ones)
         # feed forward (W4A4 GELU MLP)
-        h = torch.empty(M, self.p["ffn1"]["wcodes"].shape[0], device=dev, dtype=torch.bfloat16)
+        h = torch.empty(M, ops.out_features(self.p["ffn1"]["wcodes"]), device=dev, dtype=torch.bfloat16)
         self._gemm(self._quant(X, "ffn1", ln=dict(shift=sh_f, scale=sc_f, eps=self.eps)), "ffn1", M, h, EPI_GELU)
         self._gemm(self._quant(h, "ffn2", shift=GELU_SHIFT, unsigned=True), "ffn2", M, X, EPI_RESIDUAL, g_f)
         return X

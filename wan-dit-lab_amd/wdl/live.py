@@ -29,7 +29,7 @@ def w4a4_linear(x: torch.Tensor, qweight: torch.Tensor, wscales: torch.Tensor, p
 
 @w4a4_linear.register_fake
 def _(x, qweight, wscales, proj_down, proj_up, smooth, bias):
-    return x.new_empty(x.shape[0], qweight.shape[0], dtype=torch.bfloat16)
+    return x.new_empty(x.shape[0], ops.out_features(qweight), dtype=torch.bfloat16)
 
 
 @torch.library.custom_op("live::w4a4_gelu_mlp", mutates_args=())
@@ -45,7 +45,7 @@ def w4a4_gelu_mlp(x: torch.Tensor, qweight1: torch.Tensor, wscales1: torch.Tenso
 @w4a4_gelu_mlp.register_fake
 def _(x, qweight1, wscales1, proj_down1, proj_up1, smooth1, bias1, qweight2, wscales2, proj_down2, proj_up2,
       smooth2, bias2):
-    return x.new_empty(x.shape[0], qweight2.shape[0], dtype=torch.bfloat16)
+    return x.new_empty(x.shape[0], ops.out_features(qweight2), dtype=torch.bfloat16)
 
 
 def load():

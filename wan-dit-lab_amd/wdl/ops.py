@@ -48,6 +48,9 @@ ROWS_PAD = 128  # activation rows padded to a multiple (GEMM token tile)
 RANK = 32
 
 
+BLOCK = 128  # rows per tile of the GEMM's blocked operands
+
+
 def padded_rows(m: int) -> int:
     return (m + ROWS_PAD - 1) // ROWS_PAD * ROWS_PAD
 
@@ -56,11 +59,12 @@ EPI_BF16, EPI_F32, EPI_RESIDUAL, EPI_GELU = 0, 1, 2, 3
 
 
 def act_quant_launch(x, smooth, proj_down_t, qshift=0.0, unsigned=False, *, ln=None, v_out=None):
-    """x bf16 [M, K] (rows 16-byte aligned) -> (q e4m3 codes uint8 [Mp, K], ascales bf16 [K/64, Mp],
-    lora fp32 [Mp, 32] or None). ln: dict(shift, scale, weight, bias, eps) fuses LayerNorm + modulation."""
+    """x bf16 [M, K] (rows 16-byte aligned) -> (q e4m3 codes uint8 [Mp, K] tile-blocked, shape [Mp/128, K/64, 128, 64]
+    (unblock_rows gives the [Mp, K] matrix), ascales bf16 [K/64, Mp], lora fp32 [Mp, 32] or None).
+    ln: dict(shift, scale, weight, bias, eps) fuses LayerNorm + modulation."""
     M, K = x.shape
     Mp = padded_rows(M)
-    q = torch.empty(Mp, K, device=x.device, dtype=torch.uint8)
+    q = torch.empty(Mp // BLOCK, K // 64, BLOCK, 64, device=x.device, dtype=torch.uint8)
     ascales = torch.empty(K // 64, Mp, device=x.device, dtype=torch.bfloat16)
     lora = None if proj_down_t is None else torch.empty(Mp, RANK, device=x.device, dtype=torch.float32)
     ln = ln or {}
@@ -72,31 +76,55 @@ def act_quant_launch(x, smooth, proj_down_t, qshift=0.0, unsigned=False, *, ln=N
     return q, ascales, lora
 
 
+def block_rows(t: torch.Tensor) -> torch.Tensor:
+    """A byte matrix [R, K] (R % 128 == 0, K % 64 == 0) in the GEMM's tile-blocked layout: [R/128, K/64, 128, 64],
+    element [r // 128, k // 64, r % 128, k % 64] = t[r, k] (a contiguous copy)."""
+    R, K = t.shape
+    if R % BLOCK or K % 64:
+        raise ValueError(f"tile-blocked operands need rows % {BLOCK} == 0 and K % 64 == 0, got {tuple(t.shape)}")
+    return t.reshape(R // BLOCK, BLOCK, K // 64, 64).permute(0, 2, 1, 3).contiguous()
+
+
+def unblock_rows(t: torch.Tensor) -> torch.Tensor:
+    """The inverse of block_rows: [R/128, K/64, 128, 64] -> the [R, K] matrix."""
+    nr, ng, b, w = t.shape
+    return t.permute(0, 2, 1, 3).reshape(nr * b, ng * w)
+
+
 def weight_codes(qweight: torch.Tensor) -> torch.Tensor:
-    """Packed int4 weights uint8 [N, K/2] -> the GEMM's operand, e4m3 codes of the same integers, uint8 [N, K]."""
+    """Packed int4 weights uint8 [N, K/2] -> the GEMM's operand, e4m3 codes of the same integers, tile-blocked
+    uint8 [N/128, K/64, 128, 64]."""
     N, half = qweight.shape
-    codes = torch.empty(N, 2 * half, device=qweight.device, dtype=torch.uint8)
+    if N % BLOCK:
+        raise ValueError(f"W4A4 weights need out_features % {BLOCK} == 0, got {N}")
+    codes = torch.empty(N // BLOCK, 2 * half // 64, BLOCK, 64, device=qweight.device, dtype=torch.uint8)
     _lib.call("wdl_w4a4_weight_codes", ptr(qweight.contiguous()), N, 2 * half, ptr(codes), stream_of(qweight))
     return codes
 
 
 def as_codes(qweight: torch.Tensor, K: int) -> torch.Tensor:
-    """The weight operand for input width K: uint8 [N, K] codes pass through, packed [N, K/2] nibbles are
-    expanded (once per call)."""
-    if qweight.dtype not in (torch.uint8, torch.int8) or qweight.dim() != 2:
-        raise TypeError(f"qweight must be a 2-d uint8 tensor, got {qweight.dtype} {tuple(qweight.shape)}")
-    if qweight.shape[1] == K:
+    """The weight operand for input width K: tile-blocked codes [N/128, K/64, 128, 64] pass through, packed [N, K/2]
+    nibbles are expanded and [N, K] codes blocked (once per call)."""
+    if qweight.dtype not in (torch.uint8, torch.int8) or qweight.dim() not in (2, 4):
+        raise TypeError(f"qweight must be a uint8 tensor of 2 or 4 dims, got {qweight.dtype} {tuple(qweight.shape)}")
+    if qweight.dim() == 4:
+        if tuple(qweight.shape[1:]) != (K // 64, BLOCK, 64) or K % 64:
+            raise ValueError(f"blocked weight codes {tuple(qweight.shape)} do not match input width {K}")
         return qweight.view(torch.uint8)
+    if qweight.shape[1] == K:
+        return block_rows(qweight.view(torch.uint8))
     if 2 * qweight.shape[1] == K:
         return weight_codes(qweight.view(torch.uint8))
     raise ValueError(f"qweight {tuple(qweight.shape)} fits neither [N, {K}] codes nor [N, {K // 2}] nibbles")
 
 
 def gemm_launch(q, ascales, lora, wcodes, wscales, proj_up, bias, M, out, epilogue=EPI_BF16, gate=None):
-    """W4A4 GEMM on the quantizer's outputs (q, ascales, lora) and e4m3 weight codes [N, K] (weight_codes)."""
-    Mp, K = q.shape
-    N = wcodes.shape[0]
-    if wcodes.shape[1] != K:
+    """W4A4 GEMM on the quantizer's outputs (q, ascales, lora) and tile-blocked e4m3 weight codes (weight_codes)."""
+    if q.dim() != 4 or wcodes.dim() != 4:
+        raise ValueError("the W4A4 GEMM takes tile-blocked operands [rows/128, K/64, 128, 64]")
+    Mp, K = q.shape[0] * BLOCK, q.shape[1] * 64
+    N = wcodes.shape[0] * BLOCK
+    if wcodes.shape[1] != q.shape[1]:
         raise ValueError(f"weight codes {tuple(wcodes.shape)} do not match activations of width {K}")
     _lib.call("wdl_w4a4_gemm", ptr(q), ptr(ascales), ptr(wcodes), ptr(wscales), ptr(lora), ptr(proj_up), ptr(bias),
               M, Mp, N, K, RANK, ptr(out), out.stride(0), epilogue, ptr(gate), stream_of(q))
@@ -113,21 +141,26 @@ def act_quant_w4(x: torch.Tensor, smooth: torch.Tensor, proj_down: torch.Tensor,
 def _(x, smooth, proj_down, qshift, unsigned):
     M, K = x.shape
     Mp = padded_rows(M)
-    return (x.new_empty(Mp, K, dtype=torch.uint8), x.new_empty(K // 64, Mp, dtype=torch.bfloat16),
-            x.new_empty(Mp, RANK, dtype=torch.float32))
+    return (x.new_empty(Mp // BLOCK, K // 64, BLOCK, 64, dtype=torch.uint8),
+            x.new_empty(K // 64, Mp, dtype=torch.bfloat16), x.new_empty(Mp, RANK, dtype=torch.float32))
+
+
+def out_features(qweight: torch.Tensor) -> int:
+    """N of a weight operand: packed [N, K/2] nibbles, [N, K] codes or tile-blocked [N/128, K/64, 128, 64] codes."""
+    return qweight.shape[0] * (BLOCK if qweight.dim() == 4 else 1)
 
 
 @torch.library.custom_op("wdl::w4a4_gemm", mutates_args=())
 def w4a4_gemm(q: torch.Tensor, ascales: torch.Tensor, lora: torch.Tensor, qweight: torch.Tensor,
               wscales: torch.Tensor, proj_up: torch.Tensor, bias: torch.Tensor, M: int, fp32_out: bool) -> torch.Tensor:
-    out = torch.empty(M, qweight.shape[0], device=q.device, dtype=torch.float32 if fp32_out else torch.bfloat16)
-    return gemm_launch(q, ascales, lora, as_codes(qweight, q.shape[1]), wscales, proj_up, bias, M, out,
+    out = torch.empty(M, out_features(qweight), device=q.device, dtype=torch.float32 if fp32_out else torch.bfloat16)
+    return gemm_launch(q, ascales, lora, as_codes(qweight, q.shape[1] * 64), wscales, proj_up, bias, M, out,
                        EPI_F32 if fp32_out else EPI_BF16)
 
 
 @w4a4_gemm.register_fake
 def _(q, ascales, lora, qweight, wscales, proj_up, bias, M, fp32_out):
-    return q.new_empty(M, qweight.shape[0], dtype=torch.float32 if fp32_out else torch.bfloat16)
+    return q.new_empty(M, out_features(qweight), dtype=torch.float32 if fp32_out else torch.bfloat16)
 
 
 @torch.library.custom_op("wdl::w4a4_linear", mutates_args=())
@@ -136,13 +169,13 @@ def w4a4_linear(x: torch.Tensor, qweight: torch.Tensor, wscales: torch.Tensor, p
     """live::w4a4_linear (native/ops/w4a4_ops.cpp:31-40): activation quantizer + low-rank down projection, then
     the W4A4 GEMM with the low-rank up projection and the bias; x bf16 [M, K] -> bf16 [M, N]."""
     q, asc, lora = act_quant_launch(x, smooth, proj_down)
-    out = torch.empty(x.shape[0], qweight.shape[0], device=x.device, dtype=torch.bfloat16)
+    out = torch.empty(x.shape[0], out_features(qweight), device=x.device, dtype=torch.bfloat16)
     return gemm_launch(q, asc, lora, as_codes(qweight, x.shape[1]), wscales, proj_up, bias, x.shape[0], out)
 
 
 @w4a4_linear.register_fake
 def _(x, qweight, wscales, proj_down, proj_up, smooth, bias):
-    return x.new_empty(x.shape[0], qweight.shape[0], dtype=torch.bfloat16)
+    return x.new_empty(x.shape[0], out_features(qweight), dtype=torch.bfloat16)
 
 
 GELU_SHIFT = 0.171875
@@ -158,17 +191,17 @@ def w4a4_gelu_mlp(x: torch.Tensor, qweight1: torch.Tensor, wscales1: torch.Tenso
     second GEMM."""
     M = x.shape[0]
     q, asc, lora = act_quant_launch(x, smooth1, proj_down1)
-    h = torch.empty(M, qweight1.shape[0], device=x.device, dtype=torch.bfloat16)
+    h = torch.empty(M, out_features(qweight1), device=x.device, dtype=torch.bfloat16)
     gemm_launch(q, asc, lora, as_codes(qweight1, x.shape[1]), wscales1, proj_up1, bias1, M, h, EPI_GELU)
     q2, asc2, lora2 = act_quant_launch(h, smooth2, proj_down2, GELU_SHIFT, True)
-    out = torch.empty(M, qweight2.shape[0], device=x.device, dtype=torch.bfloat16)
+    out = torch.empty(M, out_features(qweight2), device=x.device, dtype=torch.bfloat16)
     return gemm_launch(q2, asc2, lora2, as_codes(qweight2, h.shape[1]), wscales2, proj_up2, bias2, M, out)
 
 
 @w4a4_gelu_mlp.register_fake
 def _(x, qweight1, wscales1, proj_down1, proj_up1, smooth1, bias1, qweight2, wscales2, proj_down2, proj_up2,
       smooth2, bias2):
-    return x.new_empty(x.shape[0], qweight2.shape[0], dtype=torch.bfloat16)
+    return x.new_empty(x.shape[0], out_features(qweight2), dtype=torch.bfloat16)
 
 
 # ------------------------------------------------------------------------------------------------ Q/K norm + RoPE
