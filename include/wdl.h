@@ -137,12 +137,20 @@ int wdl_sage_prep(const void* cache_k, const float* cache_ks, const void* cache_
                   int64_t n, int splits, float* workspace, void* k_int8, float* k_scale, void* v_fp8,
                   float* k_mean_out, float* v_scale_out, wdl_stream_t stream);
 
+/* Workspace (bytes) of wdl_sage_attn for n queries, L keys and `heads` heads. */
+int64_t wdl_sage_attn_workspace_bytes(int64_t n, int64_t L, int64_t heads);
+
 /* Sage-2 style attention (int8 QK^T, fp32 online softmax, fp8 PV, non-causal). Replaces live::sage_sm89
  * (native/ops/sage_ops.cpp:12-19, 28-35) on the layouts of wdl_quant_q / wdl_sage_prep.
- * out: bf16 [n, heads, 128] (row stride ldo). */
+ * out: bf16 [n, heads, 128] (row stride ldo). workspace: 16-byte aligned, wdl_sage_attn_workspace_bytes(n, L,
+ * heads) bytes (no initial contents needed); calls that share a workspace must not overlap. When the (128-query
+ * tile, head) pairs just exceed a multiple of the CU count, every CU runs the same number of whole tiles and the
+ * key blocks of the remaining tiles are split evenly over the CUs; their partial softmax states go through the
+ * workspace to a second launch that merges them in a fixed order (deterministic). Otherwise the workspace is not
+ * touched and may be NULL. */
 int wdl_sage_attn(const void* q_i8, int64_t ldq, const float* q_scale, const void* k_i8, const float* k_scale,
                   const void* v_fp8, const float* v_scale, int64_t n, int64_t L, int64_t heads, float sm_scale,
-                  void* out, int64_t ldo, wdl_stream_t stream);
+                  void* out, int64_t ldo, void* workspace, wdl_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -106,6 +106,35 @@ def test_attention_matches_quantized_oracle_and_exact(gpu, at, n, H):
     assert osage.rel_err(out, exact) < 1.2 * osage.rel_err(emul8, exact) + 1e-3
 
 
+def test_attention_split_tiles_merge_across_workgroups(gpu):
+    """(128-query tile, head) pairs just above the CU count: every CU runs one whole tile and the key blocks of the
+    remaining tiles (the last head's, with the ragged query tile) are split over all CUs, their partial softmax
+    states merged by a second launch. Checked on the first head (whole tiles) and the last (split tiles) against the
+    oracle with the bars of the test above; two calls are bit-identical (the merge order is fixed)."""
+    from wdl import sage_kv
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    n, at = 1392, 8352                      # 11 query tiles, 9744 keys (153 key blocks, the last ragged)
+    H = cus // 11 + 1                       # 11 H tiles: just above the CU count
+    Q, k, ks, v, vs, at, K, V = setup(at, n, H=H, seed=11)
+    args = (*cuda(Q, k, ks, v, vs), at, *cuda(K, V))
+    out = sage_kv.attend(*args)
+    torch.cuda.synchronize()
+    again = sage_kv.attend(*args)
+    torch.cuda.synchronize()
+    assert torch.equal(out, again)
+    out = out.cpu().float()
+    for hh in (0, H - 1):
+        sl = lambda t: t[:, :, hh:hh + 1].contiguous()
+        p = osage.prep(sl(Q), sl(k), sl(ks), sl(v), sl(vs), at, sl(K), sl(V))
+        emul = osage.attention_quantized(p, 128 ** -0.5)
+        emul8 = osage.attention_quantized(p, 128 ** -0.5, p_fp8=True)
+        exact = osage.attention_exact(sl(Q), p["K"], p["V"])
+        got = out[:, :, hh:hh + 1]
+        assert osage.cosine(got, emul) >= 0.999, hh
+        assert osage.rel_err(got, exact) < 1.2 * osage.rel_err(emul8, exact) + 1e-3, hh
+
+
 def test_attention_single_key_and_ragged_lengths(gpu):
     from wdl import sage_kv
 

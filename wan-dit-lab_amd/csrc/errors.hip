@@ -29,4 +29,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* wdl_last_error(void) { return g_message; }
 
-extern "C" int wdl_abi_version(void) { return 3; }
+extern "C" int wdl_abi_version(void) { return 4; }

@@ -45,6 +45,8 @@ constexpr int GSTAGE = KT + VT;           // one group's share of a stage
 constexpr int STAGE = 2 * GSTAGE;
 constexpr int KS_MAX = 2048;              // k scales held in LDS: L <= 32768 keys
 constexpr float LOG2_448 = 8.807354922057604f;
+constexpr int SLOT_FLOATS = 4 * (64 * 64 + 128);  // one partial: per wave [64 values][64 lanes] of O, m, l
+constexpr int MAX_WG = 2048;                       // workgroups of a split launch (one per CU)
 
 struct AttnArgs {
     const int8_t* q;
@@ -58,6 +60,10 @@ struct AttnArgs {
     int64_t ldo;
     int64_t n, L, Lpad, H;
     float sm_scale_log2;  // sm_scale * log2(e)
+    float* part;          // [2 W][SLOT_FLOATS] partial (O, m, l) of split tiles (null when none is split)
+    int64_t W;            // workgroups
+    int64_t qtiles;       // query tiles (128 queries) per head
+    int64_t D;            // tiles run whole (the first D of the T = qtiles * H); the other T - D are split
 };
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -75,6 +81,14 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// The contributors of a split tile are the workgroups c whose unit range [c U / W, (c + 1) U / W) meets it.
+__device__ __forceinline__ int64_t wg_of(int64_t unit, int64_t U, int64_t W) {
+    int64_t c = unit * W / U;
+    while (c + 1 < W && (c + 1) * U / W <= unit) ++c;
+    while (c > 0 && c * U / W > unit) --c;
+    return c;
+}
+
 __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE];
     __shared__ float sKs[KS_MAX];
@@ -82,66 +96,17 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
     const int t = threadIdx.x, lane = t % 64, half = lane / 32;
     const int wave = __builtin_amdgcn_readfirstlane(t / 64);
     const int grp = wave / 4, sub = wave % 4;
-    const int64_t h = blockIdx.y;
-    const int64_t q = int64_t(blockIdx.x) * 128 + sub * 32 + lane % 32;
-    const bool qlive = q < a.n;
     const int64_t qblocks8 = (a.n + 127) / 128 * 32;
-
-    // Q fragment: B operand of S^T = K Q^T, chunk c covers d = 32c .. 32c + 31, lane half -> 16 of them
-    i32x4 qf[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        if (qlive) {
-            const uint4 r = *reinterpret_cast<const uint4*>(a.q + q * a.ldq + h * D + 32 * c + 16 * half);
-            qf[c] = i32x4{int(r.x), int(r.y), int(r.z), int(r.w)};
-        } else {
-            qf[c] = i32x4{0, 0, 0, 0};
-        }
-    }
-    const float qs = qlive ? a.q_scale[h * qblocks8 + (q / 32) * 8 + q % 8] : 0.0f;
-    const float cq = qs * a.sm_scale_log2;
-
-    const int64_t nks = a.Lpad / 16;
-    for (int64_t i = t; i < nks; i += 512) sKs[i] = a.k_scale[h * nks + i];
-
-    // full key blocks of this wave's group: [first, first + count); both groups run `iters` ring steps. A ragged
-    // final block (L % 64 != 0) is group 1's, in a masked step after the ring.
-    const int64_t nblk = a.Lpad / 64;
+    const int64_t nblk = a.Lpad / 64, nks = a.Lpad / 16;
     const bool ragged = (a.L % 64) != 0;
-    const int64_t nfull = ragged ? nblk - 1 : nblk, nb0 = (nfull + 1) / 2;
-    const int64_t first = grp == 0 ? 0 : nb0, count = grp == 0 ? nb0 : nfull - nb0;
-    const int64_t last = count > 0 ? first + count - 1 : 0;
-    const int64_t iters = nb0;
-
-    // this lane's load slots (block 0); block b adds b * 64 * D bytes of K, b * 64 bytes of V
-    const int8_t* kbase = a.k + h * a.Lpad * D;
-    const uint8_t* vbase = a.v + h * D * a.Lpad;
-    const int8_t* ksrc[2];
-    const uint8_t* vsrc[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int slot = (sub * 2 + j) * 64 + lane;  // 16-byte slot of the group's 8 KB K or V block
-        {
-            const int dh = slot / 256, s2 = slot % 256, key = s2 / 4;
-            const int lq = (s2 % 4) ^ ((key >> 2) & 3);
-            ksrc[j] = kbase + key * D + dh * 64 + lq * 16;
-        }
-        {
-            const int ch = slot / 4, lq = (slot % 4) ^ ((ch >> 2) & 3);
-            vsrc[j] = vbase + int64_t(ch) * a.Lpad + lq * 16;
-        }
-    }
-    auto load_block = [&](int st, int64_t b) {  // block b of this group's keys into stage st
-        uint8_t* base = smem + st * STAGE + grp * GSTAGE;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) dma16(ksrc[j] + b * 64 * D, lds_addr(base + (sub * 2 + j) * 1024));
-#pragma unroll
-        for (int j = 0; j < 2; ++j) dma16(vsrc[j] + b * 64, lds_addr(base + KT + (sub * 2 + j) * 1024));
-    };
-    auto issue = [&](int st, int64_t i) {  // ring step i's block (clamped to the group's last) into stage st
-        const int64_t b = first + i;
-        load_block(st, b < last ? b : last);
-    };
+    // Work of workgroup w: the whole tiles w, w + W, .. below D (their output written directly), then its share
+    // [s0, s1) of the key blocks of the R = T - D remaining tiles, laid end to end (each piece's partial softmax
+    // state goes to the workspace slot 2w for its first piece, 2w + 1 for a second; attn_merge_kernel combines them)
+    const int64_t w = blockIdx.x;
+    const int64_t T = a.qtiles * a.H, R = T - a.D, Usk = R * nblk;
+    const int64_t ndp = (a.D - w + a.W - 1) / a.W;
+    const int64_t s0 = w * Usk / a.W, s1 = (w + 1) * Usk / a.W;
+    int64_t cursor = s0;
 
     // per-lane LDS read offsets: K tile j, chunk c -> (c / 2) * 4096 + (32 j + lane % 32) * 64 + quarter;
     // V channel subtile ds -> KT + (32 ds + lane % 32) * 64 + quarter (two quarters per lane half)
@@ -149,150 +114,347 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
     const int kq[2] = {((0 + half) ^ swz) * 16, ((2 + half) ^ swz) * 16};      // chunk parity 0 / 1
     const int vq0 = ((2 * half) ^ swz) * 16, vq1 = ((2 * half + 1) ^ swz) * 16;
     const int rowoff = (lane % 32) * 64;
-
-    f32x16 o[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = f32x16{};
-    float m = -INFINITY, l = 0.0f;
     const i32x16 izero = {};
+    // group 1's hand-over area (stage 0 of the ring): per sub-wave [64 values][64 lanes] floats, then m and l
+    float* xo = reinterpret_cast<float*>(smem) + sub * (64 * 64 + 128);
 
-    // mask_tag: std::true_type for the final block of a ragged L (keys >= L get P = 0), else std::false_type
-    auto compute = [&](int st, int64_t b, auto mask_tag) {
-        constexpr bool MASK = decltype(mask_tag)::value;
-        const uint8_t* K = smem + st * STAGE + grp * GSTAGE;
-        const uint8_t* V = K + KT;
-        i32x16 acc[2];
+    int64_t head_loaded = -1;
+    for (int64_t seg = 0;; ++seg) {
+        // ---- segment: tile `tile` (head h, query tile qt), key blocks [b0, b1)
+        int64_t tile, b0, b1, slot = -1;
+        if (seg < ndp) {
+            tile = w + seg * a.W, b0 = 0, b1 = nblk;
+        } else {
+            if (cursor >= s1) break;
+            b0 = cursor % nblk;
+            b1 = b0 + (s1 - cursor) < nblk ? b0 + (s1 - cursor) : nblk;
+            tile = a.D + cursor / nblk;
+            slot = cursor == s0 ? 2 * w : 2 * w + 1;
+            cursor += b1 - b0;
+        }
+        const int64_t h = tile / a.qtiles, qt = tile % a.qtiles;
+        if (h != head_loaded) {  // every wave is past its last read of sKs (segment-end barrier)
+            for (int64_t i = t; i < nks; i += 512) sKs[i] = a.k_scale[h * nks + i];
+            head_loaded = h;
+        }
+        const int64_t q = qt * 128 + sub * 32 + lane % 32;
+        const bool qlive = q < a.n;
+
+        // Q fragment: B operand of S^T = K Q^T, chunk c covers d = 32c .. 32c + 31, lane half -> 16 of them
+        i32x4 qf[4];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            acc[j] = izero;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const uint4 r = *reinterpret_cast<const uint4*>(K + (c / 2) * 4096 + j * 2048 + rowoff + kq[c % 2]);
-                acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(i32x4{int(r.x), int(r.y), int(r.z), int(r.w)}, qf[c],
-                                                              acc[j], 0, 0, 0);
+        for (int c = 0; c < 4; ++c) {
+            if (qlive) {
+                const uint4 r = *reinterpret_cast<const uint4*>(a.q + q * a.ldq + h * D + 32 * c + 16 * half);
+                qf[c] = i32x4{int(r.x), int(r.y), int(r.z), int(r.w)};
+            } else {
+                qf[c] = i32x4{0, 0, 0, 0};
             }
         }
-        // key of register r of tile j: 64 b + 32 j + 8 (r / 4) + 4 half + r % 4; scale group 2 half + (r % 4) / 2
-        const float kc0 = sKs[b * 4 + 2 * half] * cq, kc1 = sKs[b * 4 + 2 * half + 1] * cq;
-        if (MASK) {
+        const float qs = qlive ? a.q_scale[h * qblocks8 + (q / 32) * 8 + q % 8] : 0.0f;
+        const float cq = qs * a.sm_scale_log2;
+
+        // full key blocks of the segment [b0, fe), split in halves between the groups; both groups run `iters`
+        // ring steps. A ragged final block (L % 64 != 0) in the segment is group 1's, in a masked step after it.
+        const bool ragged_here = ragged && b1 == nblk;
+        const int64_t fe = ragged_here ? nblk - 1 : b1;
+        const int64_t nfull = fe - b0, nb0 = (nfull + 1) / 2;
+        const int64_t first = grp == 0 ? b0 : b0 + nb0, count = grp == 0 ? nb0 : nfull - nb0;
+        const int64_t last = count > 0 ? first + count - 1 : b0;
+        const int64_t iters = nb0;
+
+        // this lane's load slots (block 0); block b adds b * 64 * D bytes of K, b * 64 bytes of V
+        const int8_t* kbase = a.k + h * a.Lpad * D;
+        const uint8_t* vbase = a.v + h * D * a.Lpad;
+        const int8_t* ksrc[2];
+        const uint8_t* vsrc[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int slot = (sub * 2 + j) * 64 + lane;  // 16-byte slot of the group's 8 KB K or V block
+            {
+                const int dh = slot / 256, s2 = slot % 256, key = s2 / 4;
+                const int lq = (s2 % 4) ^ ((key >> 2) & 3);
+                ksrc[j] = kbase + key * D + dh * 64 + lq * 16;
+            }
+            {
+                const int ch = slot / 4, lq = (slot % 4) ^ ((ch >> 2) & 3);
+                vsrc[j] = vbase + int64_t(ch) * a.Lpad + lq * 16;
+            }
+        }
+        auto load_block = [&](int st, int64_t blk) {  // block blk of this group's keys into stage st
+            uint8_t* base = smem + st * STAGE + grp * GSTAGE;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) dma16(ksrc[j] + blk * 64 * D, lds_addr(base + (sub * 2 + j) * 1024));
+#pragma unroll
+            for (int j = 0; j < 2; ++j) dma16(vsrc[j] + blk * 64, lds_addr(base + KT + (sub * 2 + j) * 1024));
+        };
+        auto issue = [&](int st, int64_t i) {  // ring step i's block (clamped to the group's last) into stage st
+            const int64_t blk = first + i;
+            load_block(st, blk < last ? blk : last);
+        };
+
+        f32x16 o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = f32x16{};
+        float m = -INFINITY, l = 0.0f;
+
+        // mask_tag: std::true_type for the final block of a ragged L (keys >= L get P = 0), else std::false_type
+        auto compute = [&](int st, int64_t blk, auto mask_tag) {
+            constexpr bool MASK = decltype(mask_tag)::value;
+            const uint8_t* K = smem + st * STAGE + grp * GSTAGE;
+            const uint8_t* V = K + KT;
+            // all eight K fragments are read before the first MFMA, so the reads overlap each other
+            uint4 kr[2][4];
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    if (b * 64 + 32 * j + 8 * (r / 4) + 4 * half + r % 4 >= a.L) acc[j][r] = INT32_MIN;
-        }
-        int mx0 = INT32_MIN, mx1 = INT32_MIN;
+                for (int c = 0; c < 4; ++c)
+                    kr[j][c] = *reinterpret_cast<const uint4*>(K + (c / 2) * 4096 + j * 2048 + rowoff + kq[c % 2]);
+            i32x16 acc[2];
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < 2; ++j) {
+                acc[j] = izero;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                if ((r % 4) < 2) mx0 = max(mx0, acc[j][r]);
-                else mx1 = max(mx1, acc[j][r]);
+                for (int c = 0; c < 4; ++c)
+                    acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                        i32x4{int(kr[j][c].x), int(kr[j][c].y), int(kr[j][c].z), int(kr[j][c].w)}, qf[c], acc[j], 0, 0, 0);
             }
-        float mb = fmaxf(float(mx0) * kc0, float(mx1) * kc1);
-        mb = fmaxf(mb, __shfl_xor(mb, 32));
-        const float mn = fmaxf(m, mb);
-        const float alpha = __builtin_amdgcn_exp2f(m - mn);
-        const float bias = LOG2_448 - mn;
-        float ls = 0.0f;
-        uint32_t pw[8];
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // the eight reads
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // then the eight MFMAs
+            // key of register r of tile j: 64 blk + 32 j + 8 (r / 4) + 4 half + r % 4; scale group 2 half + (r % 4) / 2
+            const float kc0 = sKs[blk * 4 + 2 * half] * cq, kc1 = sKs[blk * 4 + 2 * half + 1] * cq;
+            if (MASK) {
 #pragma unroll
-        for (int w = 0; w < 8; ++w) {
-            const int j = w / 4;
-            float p[4];
+                for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = 4 * (w % 4) + e;
-                // raw v_exp_f32: results below 2^-126 flush to 0 (below e4m3's range and the sum's precision)
-                p[e] = __builtin_amdgcn_exp2f(fmaf(float(acc[j][r]), (r % 4) < 2 ? kc0 : kc1, bias));
-                if (MASK && acc[j][r] == INT32_MIN) p[e] = 0.0f;
-                ls = ls + p[e];
+                    for (int r = 0; r < 16; ++r)
+                        if (blk * 64 + 32 * j + 8 * (r / 4) + 4 * half + r % 4 >= a.L) acc[j][r] = INT32_MIN;
             }
-            uint32_t word = __builtin_amdgcn_cvt_pk_fp8_f32(p[0], p[1], 0, false);
-            pw[w] = __builtin_amdgcn_cvt_pk_fp8_f32(p[2], p[3], word, true);
+            int mx0 = INT32_MIN, mx1 = INT32_MIN;
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    if ((r % 4) < 2) mx0 = max(mx0, acc[j][r]);
+                    else mx1 = max(mx1, acc[j][r]);
+                }
+            float mb = fmaxf(float(mx0) * kc0, float(mx1) * kc1);
+            mb = fmaxf(mb, __shfl_xor(mb, 32));
+            const float mn = fmaxf(m, mb);
+            const float alpha = __builtin_amdgcn_exp2f(m - mn);
+            const float bias = LOG2_448 - mn;
+            float ls = 0.0f;
+            uint32_t pw[8];
+#pragma unroll
+            for (int wd = 0; wd < 8; ++wd) {
+                const int j = wd / 4;
+                float p[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * (wd % 4) + e;
+                    // raw v_exp_f32: results below 2^-126 flush to 0 (below e4m3's range and the sum's precision)
+                    p[e] = __builtin_amdgcn_exp2f(fmaf(float(acc[j][r]), (r % 4) < 2 ? kc0 : kc1, bias));
+                    if (MASK && acc[j][r] == INT32_MIN) p[e] = 0.0f;
+                    ls = ls + p[e];
+                }
+                uint32_t word = __builtin_amdgcn_cvt_pk_fp8_f32(p[0], p[1], 0, false);
+                pw[wd] = __builtin_amdgcn_cvt_pk_fp8_f32(p[2], p[3], word, true);
+            }
+            l = l * alpha + ls;
+            m = mn;
+            if (__any(alpha != 1.0f)) {
+#pragma unroll
+                for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) o[ds][e] *= alpha;
+            }
+            const i32x8 pf = {int(pw[0]), int(pw[1]), int(pw[2]), int(pw[3]),
+                              int(pw[4]), int(pw[5]), int(pw[6]), int(pw[7])};
+#pragma unroll
+            for (int ds = 0; ds < 4; ++ds) {
+                const uint8_t* src = V + ds * 2048 + rowoff;
+                const uint4 v0 = *reinterpret_cast<const uint4*>(src + vq0), v1 = *reinterpret_cast<const uint4*>(src + vq1);
+                const i32x8 vf = {int(v0.x), int(v0.y), int(v0.z), int(v0.w), int(v1.x), int(v1.y), int(v1.z), int(v1.w)};
+                o[ds] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pf, o[ds], 0, 0, 0, 0, 0, 0);
+            }
+        };
+
+#pragma unroll
+        for (int k = 0; k < STAGES - 1; ++k) issue(k, k);
+        for (int64_t i0 = 0; i0 < iters; i0 += STAGES) {
+#pragma unroll
+            for (int k = 0; k < STAGES; ++k) {
+                const int64_t i = i0 + k;
+                if (i >= iters) break;
+                wait_vmcnt<(STAGES - 2) * LPB>();
+                __syncthreads();
+                issue((k + STAGES - 1) % STAGES, i + STAGES - 1);
+                if (i < count) compute(k, first + i, std::false_type{});
+            }
         }
-        l = l * alpha + ls;
-        m = mn;
-        if (__any(alpha != 1.0f)) {
+        wait_vmcnt<0>();
+        __syncthreads();  // all loads landed, every wave is done with the ring, sKs written
+        if (ragged_here) {  // the final, partial block: group 1, keys >= L masked
+            if (grp == 1) load_block(0, nblk - 1);
+            wait_vmcnt<0>();
+            __syncthreads();
+            if (grp == 1) compute(0, nblk - 1, std::true_type{});
+            __syncthreads();  // group 1 is done reading stage 0 before the hand-over overwrites it
+        }
+
+        // group 1 hands (O, m, l) to group 0, which merges: O = O0 2^(m0 - m) + O1 2^(m1 - m), l likewise
+        if (grp == 1) {
 #pragma unroll
             for (int ds = 0; ds < 4; ++ds)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) o[ds][e] *= alpha;
+                for (int e = 0; e < 16; ++e) xo[(ds * 16 + e) * 64 + lane] = o[ds][e];
+            xo[64 * 64 + lane] = m;
+            xo[64 * 64 + 64 + lane] = l;
         }
-        const i32x8 pf = {int(pw[0]), int(pw[1]), int(pw[2]), int(pw[3]), int(pw[4]), int(pw[5]), int(pw[6]), int(pw[7])};
-#pragma unroll
-        for (int ds = 0; ds < 4; ++ds) {
-            const uint8_t* src = V + ds * 2048 + rowoff;
-            const uint4 v0 = *reinterpret_cast<const uint4*>(src + vq0), v1 = *reinterpret_cast<const uint4*>(src + vq1);
-            const i32x8 vf = {int(v0.x), int(v0.y), int(v0.z), int(v0.w), int(v1.x), int(v1.y), int(v1.z), int(v1.w)};
-            o[ds] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pf, o[ds], 0, 0, 0, 0, 0, 0);
-        }
-    };
-
-#pragma unroll
-    for (int k = 0; k < STAGES - 1; ++k) issue(k, k);
-    for (int64_t i0 = 0; i0 < iters; i0 += STAGES) {
-#pragma unroll
-        for (int k = 0; k < STAGES; ++k) {
-            const int64_t i = i0 + k;
-            if (i >= iters) break;
-            wait_vmcnt<(STAGES - 2) * LPB>();
-            __syncthreads();
-            issue((k + STAGES - 1) % STAGES, i + STAGES - 1);
-            if (i < count) compute(k, first + i, std::false_type{});
-        }
-    }
-    wait_vmcnt<0>();
-    __syncthreads();  // all loads landed and every wave is done with the ring
-    if (ragged) {     // the final, partial block: group 1, keys >= L masked
-        if (grp == 1) load_block(0, nblk - 1);
-        wait_vmcnt<0>();
         __syncthreads();
-        if (grp == 1) compute(0, nblk - 1, std::true_type{});
-        __syncthreads();  // group 1 is done reading stage 0 before the hand-over overwrites it
-    }
+        float lt = 0.0f;
+        if (grp == 0) {
+            const float m1 = xo[64 * 64 + lane], l1 = xo[64 * 64 + 64 + lane];
+            const float mt = fmaxf(m, m1);
+            const float a0 = __builtin_amdgcn_exp2f(m - mt), a1 = __builtin_amdgcn_exp2f(m1 - mt);
+            const float lh = l * a0 + l1 * a1;
+            lt = lh + __shfl_xor(lh, 32);
+#pragma unroll
+            for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) o[ds][e] = o[ds][e] * a0 + xo[(ds * 16 + e) * 64 + lane] * a1;
+            m = mt;
+        }
 
-    // group 1 hands (O, m, l) to group 0: per sub-wave [64 values][64 lanes] floats, then m and l per lane
-    float* xo = reinterpret_cast<float*>(smem) + sub * (64 * 64 + 128);
-    if (grp == 1) {
+        // out = O / l * v_scale, bf16; lane half h holds channels 32 ds + 8 g + 4 h + e
+        auto write_out = [&](const f32x16 (&ov)[4], float lsum) {
+            if (!qlive) return;
+            const float inv = 1.0f / lsum;
+            uint16_t* dst = a.out + q * a.ldo + h * D;
 #pragma unroll
-        for (int ds = 0; ds < 4; ++ds)
+            for (int ds = 0; ds < 4; ++ds) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) xo[(ds * 16 + e) * 64 + lane] = o[ds][e];
-        xo[64 * 64 + lane] = m;
-        xo[64 * 64 + 64 + lane] = l;
+                for (int g = 0; g < 4; ++g) {
+                    const int d = 32 * ds + 8 * g + 4 * half;
+                    uint16_t r[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) r[e] = f32_to_bf16(ov[ds][4 * g + e] * inv * a.v_scale[h * D + d + e]);
+                    *reinterpret_cast<uint2*>(dst + d) =
+                        make_uint2(r[0] | (uint32_t(r[1]) << 16), r[2] | (uint32_t(r[3]) << 16));
+                }
+            }
+        };
+
+        if (slot < 0) {
+            if (grp == 0) write_out(o, lt);
+        } else if (grp == 0) {
+            float* ps = a.part + slot * SLOT_FLOATS + sub * (64 * 64 + 128);
+#pragma unroll
+            for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) ps[(ds * 16 + e) * 64 + lane] = o[ds][e];
+            ps[64 * 64 + lane] = m;
+            ps[64 * 64 + 64 + lane] = lt;
+        }
+        __syncthreads();  // the segment is done with the ring, the hand-over area and sKs
+    }
+}
+
+// The split tiles: tile D + r gathers the partial states of the workgroups whose key-block share meets it, in
+// workgroup order: m = max_c m_c, O = sum_c O_c 2^(m_c - m), l = sum_c l_c 2^(m_c - m), out = O / l * v_scale.
+// Grid (R, 4 query waves, 4 channel subtiles) x 256 threads: lane = query (and channel half), thread / 64 = one
+// group of 4 channels, in the partial layout of the main kernel.
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
+    const int lane = threadIdx.x % 64, half = lane / 32, g = threadIdx.x / 64;
+    const int64_t r = blockIdx.x, sub = blockIdx.y, ds = blockIdx.z;
+    const int64_t nblk = a.Lpad / 64, T = a.qtiles * a.H, Usk = (T - a.D) * nblk;
+    const int64_t tile = a.D + r, h = tile / a.qtiles, qt = tile % a.qtiles;
+    const int64_t q = qt * 128 + sub * 32 + lane % 32;
+    const int64_t cf = wg_of(r * nblk, Usk, a.W), cl = wg_of((r + 1) * nblk - 1, Usk, a.W);
+    // the contributors' slots, once per workgroup (one thread each): slot 2c if the tile is c's first piece, 2c + 1
+    // if its second, -1 if c's share is empty (fewer split key blocks than workgroups). Share starts in 32-bit
+    // arithmetic (the host keeps W * Usk below 2^31).
+    __shared__ int cslot[MAX_WG];
+    const uint32_t Uu = uint32_t(Usk), Wu = uint32_t(a.W), tile0 = uint32_t(r * nblk);
+    const int nc = int(cl - cf + 1);
+    for (int i = threadIdx.x; i < nc; i += 256) {
+        const uint32_t c = uint32_t(cf) + i, s0 = c * Uu / Wu, s1 = (c + 1) * Uu / Wu;
+        cslot[i] = s0 == s1 ? -1 : int(s0 >= tile0 ? 2 * c : 2 * c + 1);
     }
     __syncthreads();
-    if (grp == 1) return;
-    const float m1 = xo[64 * 64 + lane], l1 = xo[64 * 64 + 64 + lane];
-    const float mt = fmaxf(m, m1);
-    const float a0 = __builtin_amdgcn_exp2f(m - mt), a1 = __builtin_amdgcn_exp2f(m1 - mt);
-    const float lh = l * a0 + l1 * a1;
-    const float lt = lh + __shfl_xor(lh, 32);
-    if (!qlive) return;
-    const float inv = 1.0f / lt;
-    uint16_t* dst = a.out + q * a.ldo + h * D;
+    auto part = [&](int slot) { return a.part + int64_t(slot) * SLOT_FLOATS + sub * (64 * 64 + 128); };
+    // contributors in batches with all their loads issued together (one memory round trip per batch)
+    constexpr int BATCH = 8;
+    float mt = -INFINITY;
+    for (int i0 = 0; i0 < nc; i0 += BATCH) {
+        float mv[BATCH];
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds) {
+        for (int k = 0; k < BATCH; ++k) {
+            const int sl = i0 + k < nc ? cslot[i0 + k] : -1;
+            mv[k] = sl >= 0 ? part(sl)[64 * 64 + lane] : -INFINITY;
+        }
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int d = 32 * ds + 8 * g + 4 * half;
-            uint16_t r[4];
+        for (int k = 0; k < BATCH; ++k) mt = fmaxf(mt, mv[k]);
+    }
+    float ov[4] = {}, ls = 0.0f;
+    for (int i0 = 0; i0 < nc; i0 += BATCH) {
+        float mv[BATCH], lv[BATCH], pv[BATCH][4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float ov = o[ds][4 * g + e] * a0 + xo[(ds * 16 + 4 * g + e) * 64 + lane] * a1;
-                r[e] = f32_to_bf16(ov * inv * a.v_scale[h * D + d + e]);
-            }
-            *reinterpret_cast<uint2*>(dst + d) = make_uint2(r[0] | (uint32_t(r[1]) << 16), r[2] | (uint32_t(r[3]) << 16));
+        for (int k = 0; k < BATCH; ++k) {
+            const int sl = i0 + k < nc ? cslot[i0 + k] : -1;
+            const float* ps = part(sl >= 0 ? sl : cslot[0]);  // contributor cf always has a piece of the tile
+            mv[k] = sl >= 0 ? ps[64 * 64 + lane] : -INFINITY;
+            lv[k] = ps[64 * 64 + 64 + lane];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) pv[k][e] = ps[(ds * 16 + 4 * g + e) * 64 + lane];
+        }
+#pragma unroll
+        for (int k = 0; k < BATCH; ++k) {
+            const float f = __builtin_amdgcn_exp2f(mv[k] - mt);  // 0 for an absent contributor
+            ls = ls + lv[k] * f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ov[e] = ov[e] + pv[k][e] * f;
         }
     }
+    if (q >= a.n) return;
+    const float inv = 1.0f / ls;
+    const int d = 32 * int(ds) + 8 * g + 4 * half;
+    uint16_t rr[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) rr[e] = f32_to_bf16(ov[e] * inv * a.v_scale[h * D + d + e]);
+    *reinterpret_cast<uint2*>(a.out + q * a.ldo + h * D + d) =
+        make_uint2(rr[0] | (uint32_t(rr[1]) << 16), rr[2] | (uint32_t(rr[3]) << 16));
 }
 
 }  // namespace
 
+namespace {
+
+int cu_count() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+}  // namespace
+
+// workspace: [2 W][SLOT_FLOATS] fp32 partial states, W <= T (query tiles x heads)
+extern "C" int64_t wdl_sage_attn_workspace_bytes(int64_t n, int64_t L, int64_t heads) {
+    if (n <= 0 || L < 1 || heads <= 0) return 0;
+    const int64_t T = (n + 127) / 128 * heads;
+    return 2 * T * SLOT_FLOATS * 4;
+}
+
 extern "C" int wdl_sage_attn(const void* q_i8, int64_t ldq, const float* q_scale, const void* k_i8,
                              const float* k_scale, const void* v_fp8, const float* v_scale, int64_t n, int64_t L,
-                             int64_t heads, float sm_scale, void* out, int64_t ldo, hipStream_t stream) {
+                             int64_t heads, float sm_scale, void* out, int64_t ldo, void* workspace,
+                             hipStream_t stream) {
     if (n < 0 || L < 1 || heads <= 0 || ldq < heads * D || ldo < heads * D)
         return fail(WDL_EINVAL, "sage_attn: bad shape n=%lld L=%lld", (long long)n, (long long)L);
     if (!q_i8 || !q_scale || !k_i8 || !k_scale || !v_fp8 || !v_scale || !out)
@@ -304,9 +466,27 @@ extern "C" int wdl_sage_attn(const void* q_i8, int64_t ldq, const float* q_scale
     if (Lpad / 16 > KS_MAX) return fail(WDL_EINVAL, "sage_attn: L=%lld above %d keys", (long long)L, KS_MAX * 16);
     if ((reinterpret_cast<uintptr_t>(k_i8) | reinterpret_cast<uintptr_t>(v_fp8)) % 16)
         return fail(WDL_EINVAL, "sage_attn: K / V must be 16-byte aligned");
+    const int64_t qtiles = (n + 127) / 128, T = qtiles * heads, nblk = Lpad / 64;
+    // One workgroup per tile, unless that leaves a large share of the last round of CUs idle (tiles just above a
+    // multiple of the CU count): then one workgroup per CU runs floor(T / CUs) whole tiles each and the key blocks
+    // of the T mod CUs remaining tiles are split evenly over all of them, merged by a second launch. Short key
+    // ranges keep one workgroup per tile.
+    int64_t W = T, Dw = T;
+    const int64_t cus = cu_count();
+    if (cus > 0 && cus <= MAX_WG && T > cus && nblk >= 32) {
+        const int64_t rounds = (T + cus - 1) / cus;
+        const int64_t usk = (T % cus) * nblk;  // key blocks of the split tiles
+        if (T * 100 < 85 * rounds * cus && (cus + 1) * usk < (int64_t(1) << 31)) W = cus, Dw = cus * (T / cus);
+    }
+    if (Dw < T && (!workspace || reinterpret_cast<uintptr_t>(workspace) % 16))
+        return fail(WDL_EINVAL, "sage_attn: a 16-byte aligned workspace of wdl_sage_attn_workspace_bytes is needed");
+    float* part = Dw < T ? static_cast<float*>(workspace) : nullptr;
     AttnArgs a{static_cast<const int8_t*>(q_i8), ldq, q_scale, static_cast<const int8_t*>(k_i8), k_scale,
                static_cast<const uint8_t*>(v_fp8), v_scale, static_cast<uint16_t*>(out), ldo, n, L, Lpad, heads,
-               sm_scale * 1.4426950408889634f};
-    sage_attn_kernel<<<dim3(unsigned((n + 127) / 128), unsigned(heads)), 512, 0, stream>>>(a);
-    return check_launch("sage_attn");
+               sm_scale * 1.4426950408889634f, part, W, qtiles, Dw};
+    sage_attn_kernel<<<unsigned(W), 512, 0, stream>>>(a);
+    int rc = check_launch("sage_attn");
+    if (rc || Dw == T) return rc;
+    attn_merge_kernel<<<dim3(unsigned(T - Dw), 4, 4), 256, 0, stream>>>(a);
+    return check_launch("sage_attn merge");
 }

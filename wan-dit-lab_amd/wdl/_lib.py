@@ -38,10 +38,12 @@ SIGNATURES: dict[str, list] = {
     "wdl_sage_prep_workspace_floats": [c_i64, c_int],
     "wdl_sage_prep": [c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_i64, c_i64, c_i64, c_i64, c_int,
                       c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr],
+    "wdl_sage_attn_workspace_bytes": [c_i64, c_i64, c_i64],
     "wdl_sage_attn": [c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_f32, c_ptr, c_i64,
-                      c_ptr],
+                      c_ptr, c_ptr],
 }
 RESTYPES = {"wdl_last_error": ctypes.c_char_p, "wdl_sage_prep_workspace_floats": c_i64,
+            "wdl_sage_attn_workspace_bytes": c_i64,
             "wdl_act_quant_workspace_floats": c_i64, "wdl_fp8_quantize_workspace_floats": c_i64}
 
 _LIB = None
