@@ -75,10 +75,11 @@ int wdl_w4a4_weight_codes(const void* qweight, int64_t N, int64_t K, void* codes
  * live::w4a4_linear and live::w4a4_gelu_mlp (native/ops/w4a4_ops.cpp:36-38, 55-61).
  * y[m][n] = sum_g ascales[g][m] wscales[g][n] I_g[m][n] + bf16(lora[m]) . proj_up[n] + bias[n], I_g the exact
  * integer sum over the 64-group g. qa: [Mp, K] e4m3 codes (wdl_act_quant_w4); wcodes: [N, K] e4m3 codes
- * (wdl_w4a4_weight_codes), both tile-blocked; wscales bf16 [K/64, N]; lora fp32 [Mp, 32] or NULL; proj_up bf16 [N, 32]; bias bf16 [N]
- * or NULL. epilogue: 0 out bf16 [M, ldo] = y; 1 out fp32 = y; 2 out bf16 = bf16(out + bf16(y) * gate[n]) in place
- * (gated residual; gate fp32 [N]); 3 out bf16 = GELU_tanh(y). Mp % 128 == 0, N % 128 == 0, K % 64 == 0; qa, wcodes
- * 16-byte aligned, scales 4-byte aligned. */
+ * (wdl_w4a4_weight_codes), both tile-blocked; wscales bf16 [K/64, N]; lora fp32 [Mp, 32] or NULL; proj_up bf16
+ * [N, 32]; bias bf16 [N] or NULL. epilogue: 0 out bf16 [M, ldo] = y; 1 out fp32 = y; 2 out bf16 =
+ * bf16(out + bf16(y) * gate[n]) in place (gated residual; gate fp32 [N]); 3 out bf16 = GELU_tanh(y).
+ * Mp % 128 == 0, N % 128 == 0, K % 64 == 0; qa, wcodes, proj_up, lora, gate 16-byte aligned, bias and out 8-byte,
+ * scales 4-byte. */
 int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wcodes, const void* wscales, const float* lora,
                   const void* proj_up, const void* bias, int64_t M, int64_t Mp, int64_t N, int64_t K, int64_t rank,
                   void* out, int64_t ldo, int epilogue, const float* gate, wdl_stream_t stream);

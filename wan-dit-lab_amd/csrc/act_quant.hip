@@ -32,7 +32,9 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int ROWS = 32;
 constexpr int RANK = 32;
-constexpr int CB = 512;  // columns per workgroup of the quant launch
+// Columns per workgroup of the quant launch: 256 up to K = 4096 (more, smaller workgroups: at 1392 rows and
+// K = 3072, 528 of them instead of 264 on 256 CUs, several resident per CU), 512 above.
+constexpr int cb_of(int64_t K) { return K <= 4096 ? 256 : 512; }
 constexpr int MAXCH = 8; // row_stats keeps up to 8 chunks per lane in registers (K <= 4096)
 
 __device__ __forceinline__ void load8(const uint16_t* p, float* f) {
@@ -105,16 +107,19 @@ struct QuantArgs {
     uint16_t* v_out;           // bf16 [M, K] copy of v, or null
 };
 
-constexpr int QT = 1024;  // threads of the quant launch: 32 threads per row, each 2 of the block's 8 groups
-
-__global__ __launch_bounds__(QT) void quant_kernel(QuantArgs a) {
+// CB columns per workgroup, QT = 2 CB threads: CB / 16 threads per row, each 2 of the block's CB / 64 groups
+template <int CB>
+__global__ __launch_bounds__(2 * CB) void quant_kernel(QuantArgs a) {
+    constexpr int QT = 2 * CB;
+    static_assert(CB % 128 == 0 && QT / 64 >= 4, "4 waves for the low-rank product");
     __shared__ __attribute__((aligned(16))) uint16_t tile[ROWS][CB + 8];
     __shared__ float part[4][ROWS * RANK];
     // per-column vectors of this block's columns: smooth, LN weight, LN bias, 1 + mod_scale, mod_shift
     __shared__ __attribute__((aligned(16))) float sp[6][CB];  // + 1 / smooth
 
     const int t = threadIdx.x, lane = t % 64, wave = t / 64;
-    const int rloc = t / 32, slot = t % 8, gsel = (t / 8) % 4;  // row, 8-column chunk, group pair
+    // row, 8-column chunk, group pair
+    const int rloc = t / (CB / 16), slot = t % 8, gsel = (t / 8) % (CB / 128);
     const int64_t row = int64_t(blockIdx.x) * ROWS + rloc;
     const bool live = row < a.M;
     const int64_t K = a.K;
@@ -151,13 +156,14 @@ __global__ __launch_bounds__(QT) void quant_kernel(QuantArgs a) {
             sp[4][t] = p4;
         }
     }
-    // the low-rank operand (waves 0..3: B = proj_down^T rows lane % 32, k = 128 wave + 16 s + 8 (lane / 32));
+    // the low-rank operand (waves 0..3: B = proj_down^T rows lane % 32, k = CB/4 wave + 16 s + 8 (lane / 32));
     // columns past the block's groups read column 0 of the block (their A side is zero)
-    bf16x8 bv[8];
+    constexpr int NS = CB / 64;  // MFMAs (k = 16) per wave
+    bf16x8 bv[NS];
     if (a.pdt && wave < 4) {
 #pragma unroll
-        for (int s8 = 0; s8 < 8; ++s8) {
-            int kk = wave * 128 + s8 * 16 + 8 * (lane / 32);
+        for (int s8 = 0; s8 < NS; ++s8) {
+            int kk = wave * (CB / 4) + s8 * 16 + 8 * (lane / 32);
             kk = kk < ng * 64 ? kk : 0;
             bv[s8] = *reinterpret_cast<const bf16x8*>(a.pdt + int64_t(lane % 32) * K + c0 + kk);
         }
@@ -232,11 +238,11 @@ __global__ __launch_bounds__(QT) void quant_kernel(QuantArgs a) {
     if (!a.pdt) return;
     __syncthreads();
     if (wave < 4) {
-        // wave w: k = 128 w .. 128 w + 127 of this block, 16 per MFMA; A = v rows (lane % 32), B = proj_down^T rows
+        // wave w: k = CB/4 w .. of this block, 16 per MFMA; A = v rows (lane % 32), B = proj_down^T rows
         f32x16 acc = {};
 #pragma unroll
-        for (int s8 = 0; s8 < 8; ++s8) {
-            const int kk = wave * 128 + s8 * 16 + 8 * (lane / 32);
+        for (int s8 = 0; s8 < NS; ++s8) {
+            const int kk = wave * (CB / 4) + s8 * 16 + 8 * (lane / 32);
             const bf16x8 av = *reinterpret_cast<const bf16x8*>(&tile[lane % 32][kk]);
             acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv[s8], acc, 0, 0, 0);
         }
@@ -251,18 +257,28 @@ __global__ __launch_bounds__(QT) void quant_kernel(QuantArgs a) {
     }
 }
 
+// lora = sum of the nb column-block partials, in increasing block order; the loads of a batch of 16 partials are
+// all issued before the first add (one memory round trip per batch, not one per partial)
 __global__ void lora_sum_kernel(const float* part, int nb, int64_t n, float* out) {
     const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    float s = part[i];
-    for (int b = 1; b < nb; ++b) s = s + part[int64_t(b) * n + i];
+    constexpr int BATCH = 16;
+    float s = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += BATCH) {
+        float v[BATCH];
+#pragma unroll
+        for (int k = 0; k < BATCH; ++k) v[k] = b0 + k < nb ? part[int64_t(b0 + k) * n + i] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < BATCH; ++k)
+            if (b0 + k < nb) s = b0 + k == 0 ? v[k] : s + v[k];
+    }
     out[i] = s;
 }
 
 }  // namespace
 
 extern "C" int64_t wdl_act_quant_workspace_floats(int64_t Mp, int64_t K) {
-    const int64_t nb = (K + CB - 1) / CB;
+    const int64_t CB = cb_of(K), nb = (K + CB - 1) / CB;
     return (nb > 1 ? nb * Mp * RANK : 0) + 2 * Mp;
 }
 
@@ -281,7 +297,7 @@ extern "C" int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K
     if ((reinterpret_cast<uintptr_t>(x) | (ldx * 2)) % 16)
         return fail(WDL_EINVAL, "act_quant_w4: x rows must be 16-byte aligned");
     if (Mp == 0) return WDL_OK;
-    const int nb = int((K + CB - 1) / CB);
+    const int CB = cb_of(K), nb = int((K + CB - 1) / CB);
     float2* stats = reinterpret_cast<float2*>(workspace + (nb > 1 ? int64_t(nb) * Mp * RANK : 0));
     if (ln && M > 0) {
         row_stats_kernel<<<unsigned((M + 3) / 4), 256, 0, stream>>>(static_cast<const uint16_t*>(x), ldx, M, K, eps,
@@ -293,7 +309,8 @@ extern "C" int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K
                 unsigned_q, static_cast<const uint16_t*>(proj_down_t), static_cast<uint8_t*>(q),
                 static_cast<uint16_t*>(ascales), nb > 1 ? workspace : lora, ln ? stats : nullptr, mod_shift,
                 mod_scale, ln_w, ln_b, static_cast<uint16_t*>(v_out)};
-    quant_kernel<<<dim3(unsigned(Mp / ROWS), unsigned(nb)), QT, 0, stream>>>(a);
+    if (CB == 256) quant_kernel<256><<<dim3(unsigned(Mp / ROWS), unsigned(nb)), 512, 0, stream>>>(a);
+    else quant_kernel<512><<<dim3(unsigned(Mp / ROWS), unsigned(nb)), 1024, 0, stream>>>(a);
     int rc = check_launch("act_quant_w4 quant");
     if (rc || !proj_down_t || nb == 1) return rc;
     const int64_t n = Mp * RANK;

@@ -1,4 +1,5 @@
-// The error channel of the C ABI: a message per host thread, read with wdl_last_error().
+// The error channel of the C ABI (a message per host thread, read with wdl_last_error()) and the device query the
+// launchers share.
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -23,6 +24,18 @@ int check_launch(const char* what) {
     if (e != hipSuccess) return fail(WDL_EHIP, "%s: %s", what, hipGetErrorString(e));
     g_message[0] = 0;
     return WDL_OK;
+}
+
+int cu_count() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        cached[dev] = n;
+    }
+    return cached[dev];
 }
 
 }  // namespace wdl

@@ -428,21 +428,6 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
 
 }  // namespace
 
-namespace {
-
-int cu_count() {
-    static int cached[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-    if (!cached[dev]) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-        cached[dev] = n;
-    }
-    return cached[dev];
-}
-
-}  // namespace
 
 // workspace: [2 W][SLOT_FLOATS] fp32 partial states, W <= T (query tiles x heads)
 extern "C" int64_t wdl_sage_attn_workspace_bytes(int64_t n, int64_t L, int64_t heads) {

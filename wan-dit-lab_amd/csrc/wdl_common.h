@@ -25,6 +25,7 @@ namespace wdl {
 
 int fail(int code, const char* fmt, ...);
 int check_launch(const char* what);
+int cu_count();  // compute units of the current device (cached per device; 0 if the query fails)
 
 // The W4A4 GEMM's operand layout ("tile-blocked"): a byte matrix [R, K] (R a multiple of 128, K of 64) stored as
 // [R / 128][K / 64][128][64], so the 64-deep slice of a 128-row tile that one GEMM step reads is one contiguous

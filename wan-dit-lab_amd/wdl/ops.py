@@ -262,15 +262,17 @@ def sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, k, v, at, want_stats=
 _ATTN_WS: dict = {}
 
 
-def attn_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """The attention workspace of a device (partial softmax states of split tiles), grown when a call needs more.
-    One per device: attention calls on one device must not overlap (each launches on the current stream of its
-    tensors)."""
+def workspace(cache: dict, device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """A device's scratch buffer for one kind of call (partial results of split tiles), grown when a call needs
+    more; no initial contents are needed. One per device and kind: such calls on one device must not overlap (each
+    launches on the current stream of its tensors)."""
+    if nbytes <= 0:
+        return None
     key = device.index if device.index is not None else torch.cuda.current_device()
-    ws = _ATTN_WS.get(key)
+    ws = cache.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.empty(max(nbytes, 1 << 20), device=device, dtype=torch.uint8)
-        _ATTN_WS[key] = ws
+        cache[key] = ws
     return ws
 
 
@@ -279,7 +281,7 @@ def sage_attn_launch(q_i8, q_scale, prep, L, sm_scale, out=None):
     n, H, _ = q_i8.shape
     if out is None:
         out = torch.empty(n, H * 128, device=q_i8.device, dtype=torch.bfloat16)
-    ws = attn_workspace(q_i8.device, _lib.library().wdl_sage_attn_workspace_bytes(n, L, H))
+    ws = workspace(_ATTN_WS, q_i8.device, _lib.library().wdl_sage_attn_workspace_bytes(n, L, H))
     _lib.call("wdl_sage_attn", ptr(q_i8), H * 128, ptr(q_scale), ptr(prep["k"]), ptr(prep["k_scale"]),
               ptr(prep["v"]), ptr(prep["v_scale"]), n, L, H, float(sm_scale), ptr(out), out.stride(0), ptr(ws),
               stream_of(q_i8))
