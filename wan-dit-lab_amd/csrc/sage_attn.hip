@@ -123,7 +123,11 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
         // ---- segment: tile `tile` (head h, query tile qt), key blocks [b0, b1)
         int64_t tile, b0, b1, slot = -1;
         if (seg < ndp) {
-            tile = w + seg * a.W, b0 = 0, b1 = nblk;
+            // workgroup ids go round-robin over the 8 XCDs; each XCD takes a contiguous range of the whole tiles, so
+            // the query tiles of one head (consecutive tiles) share its K/V in one L2
+            const int64_t l = w + seg * a.W;
+            tile = a.D % 8 == 0 ? (l % 8) * (a.D / 8) + l / 8 : l;
+            b0 = 0, b1 = nblk;
         } else {
             if (cursor >= s1) break;
             b0 = cursor % nblk;
