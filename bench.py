@@ -125,7 +125,7 @@ def instrumented(step):
         e0.record()
         out = orig_gemm(q, ascales, lora, qweight, *a, **k)
         e1.record()
-        rec["gemm"].append((e0, e1, 2.0 * M * ops.out_features(qweight) * q.shape[1] * q.shape[3]))
+        rec["gemm"].append((e0, e1, 2.0 * M * ops.out_features(qweight) * q.shape[1] * 64))
         return out
 
     def attn(q_i8, q_scale, prep, L, sm_scale, out=None):
@@ -178,8 +178,9 @@ def gemm_traffic():
 
 
 def cpu_baseline():
-    """The oracle block of BASELINE config 1 (464-token frame over a 928-token FP8 cache, 512 context tokens,
-    dim 3072) timed on this host's cores; reported as latent tokens/s of a 30-block step."""
+    """The oracle block on the reference's CPU-sized workload (one 16 x 29 = 464-token frame over a 928-token FP8
+    cache, 512 context tokens, dim 3072) timed on this host's cores; reported as latent tokens/s of a 30-block
+    step."""
     import torch
 
     from oracle import block as oblock
@@ -215,7 +216,7 @@ def cpu_baseline():
         pass
     return dict(value=M / (BLOCKS * t_block), unit="latent tokens/s", cores=cores, kind="port",
                 sample=f"oracle block (CPU restatement, torch {torch.__version__}, fp32/fp64 CPU arithmetic) of "
-                       f"BASELINE config 1: 464-token frame over a 928-token FP8 cache + 512 context tokens, dim 3072; "
+                       f"one 464-token frame over a 928-token FP8 cache + 512 context tokens, dim 3072; "
                        f"median of 3 runs = {t_block:.2f} s per block, scaled to a 30-block step; CPU {cpu}")
 
 

@@ -50,7 +50,7 @@ int64_t wdl_act_quant_workspace_floats(int64_t Mp, int64_t K);
  * x: bf16 [M, K], row stride ldx (16-byte aligned rows); smooth: bf16 [K]; proj_down_t: bf16 [32, K] or NULL.
  * v = x, or with ln != 0: v = bf16(LN(x)[*ln_w + ln_b] * (1 + mod_scale) + mod_shift) (fp32 vectors, NULL = absent).
  * u = (v + qshift) / smooth; per row and 64-group: scale = bf16(max|u| / qmax) (qmax 7, or 15 if unsigned_q),
- * q = clamp(rint(u / scale)). Outputs: q as e4m3 codes of the integers [Mp, K] in the tile-blocked layout (below);
+ * q = clamp(rint(u / scale)). Outputs: q as fp6 codes of the integers [Mp, K] in the operand format (below);
  * ascales bf16 [K/64, Mp]; lora fp32 [Mp, 32] = v . proj_down; rows M..Mp-1 zero. Mp % 128 == 0. v_out (bf16
  * [M, K]) optional copy of v.
  * LayerNorm statistics: lane l of a wave owns the 8-value chunks l, l+64, ..., summed value by value, the 64 lane
@@ -60,13 +60,19 @@ int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K, const voi
                      int64_t Mp, const float* mod_shift, const float* mod_scale, const float* ln_w,
                      const float* ln_b, int ln, float eps, void* v_out, float* workspace, wdl_stream_t stream);
 
-/* Tile-blocked layout of the W4A4 GEMM's code operands: a byte matrix [R, K] (R % 128 == 0, K % 64 == 0) stored as
- * [R/128][K/64][128][64], byte (r, k) at (r/128)*128*K + (k/64)*8192 + (r%128)*64 + k%64, so the 64-deep slice of a
- * 128-row tile that one GEMM step reads is one contiguous 8 KB block. */
+/* Operand format of the W4A4 GEMM (both sides; R % 128 == 0, K % 64 == 0), R * K * 3/4 bytes:
+ * - values: weights w in [-8, 7] as the fp6 e3m2 code of 2w (sign, 3 exponent bits of bias 3, 2 mantissa bits);
+ *   activations q in [-8, 15] as the fp6 e2m3 code of q / 2 (bias 1, 3 mantissa bits). Both exact; the matrix
+ *   cores multiply them at the fp6 rate and (2w)(q/2) = wq.
+ * - bits: value k of a row's 64-deep group in half h = k / 32 at position i = k % 32; the 32 codes of a half packed
+ *   little-endian, code i at bits [6i, 6i + 6) of 24 bytes.
+ * - bytes: a row's group is 48 bytes [half 0 bytes 0..15][half 1 bytes 0..15][half 0 bytes 16..23][half 1 bytes
+ *   16..23]; the matrix is [R/128][K/64][128][48], group g of row r at (r/128)*(K/64)*6144 + g*6144 + (r%128)*48,
+ *   so the group of a 128-row tile that one GEMM step reads is one contiguous 6 KB block. */
 
 /* Weight operand of the W4A4 GEMM: packed int4 weights qweight uint8 [N, K/2] (per 64-group, byte j holds k = j in
- * the low nibble and k = j + 32 in the high nibble, two's complement) -> codes uint8 [N, K] in the tile-blocked
- * layout, the e4m3 encodings of the same integers. N % 128 == 0. Done once per weight (module construction), the
+ * the low nibble and k = j + 32 in the high nibble, two's complement) -> the fp6 codes of the same integers in the
+ * operand format (N * K * 3/4 bytes). N % 128 == 0. Done once per weight (module construction), the
  * expansion of the int4 weights that Nunchaku's gemm_w4a4 performs inside every call
  * (native/ops/w4a4_ops.cpp:36-38). 16-byte aligned buffers. */
 int wdl_w4a4_weight_codes(const void* qweight, int64_t N, int64_t K, void* codes, wdl_stream_t stream);
@@ -74,8 +80,8 @@ int wdl_w4a4_weight_codes(const void* qweight, int64_t N, int64_t K, void* codes
 /* W4A4 GEMM with fused dequantization, low-rank up projection and bias. Replaces Nunchaku's gemm_w4a4 behind
  * live::w4a4_linear and live::w4a4_gelu_mlp (native/ops/w4a4_ops.cpp:36-38, 55-61).
  * y[m][n] = sum_g ascales[g][m] wscales[g][n] I_g[m][n] + bf16(lora[m]) . proj_up[n] + bias[n], I_g the exact
- * integer sum over the 64-group g. qa: [Mp, K] e4m3 codes (wdl_act_quant_w4); wcodes: [N, K] e4m3 codes
- * (wdl_w4a4_weight_codes), both tile-blocked; wscales bf16 [K/64, N]; lora fp32 [Mp, 32] or NULL; proj_up bf16
+ * integer sum over the 64-group g. qa: [Mp, K] activation codes (wdl_act_quant_w4); wcodes: [N, K] weight codes
+ * (wdl_w4a4_weight_codes), both in the operand format above; wscales bf16 [K/64, N]; lora fp32 [Mp, 32] or NULL; proj_up bf16
  * [N, 32]; bias bf16 [N] or NULL. epilogue: 0 out bf16 [M, ldo] = y; 1 out fp32 = y; 2 out bf16 =
  * bf16(out + bf16(y) * gate[n]) in place (gated residual; gate fp32 [N]); 3 out bf16 = GELU_tanh(y).
  * Mp % 128 == 0, N % 128 == 0, K % 64 == 0; qa, wcodes, proj_up, lora, gate 16-byte aligned, bias and out 8-byte,

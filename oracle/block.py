@@ -86,7 +86,7 @@ def block_forward(X: torch.Tensor, time_in: torch.Tensor, P: dict, grid, freq: t
 
 
 def random_block(dim: int, ffn: int, generator: torch.Generator, rank: int = 32, init: str = "normal"):
-    """Float weights of a Wan block: linears N(0, 0.02^2) (init "normal", the BASELINE configs) or torch.nn.Linear's
+    """Float weights of a Wan block: linears N(0, 0.02^2) (init "normal", the benchmark workloads) or torch.nn.Linear's
     default U(-1/sqrt(in), 1/sqrt(in)) (init "torch", the reference's test blocks); RMSNorm weights 1, LN3 affine
     (1, 0), modulation randn / sqrt(dim) (block.py:20)."""
     g = generator

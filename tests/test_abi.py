@@ -25,7 +25,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     for name in declared():
         assert hasattr(lib, name), name
     assert set(declared()) == set(_lib.SIGNATURES)
-    assert lib.wdl_abi_version() == 4
+    assert lib.wdl_abi_version() == 5
     assert lib.wdl_last_error() == b""
 
 
@@ -70,27 +70,76 @@ def test_weight_operand_shapes_are_checked_before_any_launch():
         ops.as_codes(torch.zeros(4, 48, dtype=torch.uint8), 128)
     with pytest.raises(TypeError):
         ops.as_codes(torch.zeros(4, 64, dtype=torch.float32), 128)
-    codes = torch.zeros(128, 128, dtype=torch.uint8)
-    assert ops.as_codes(codes, 128).shape == (1, 2, 128, 64)  # [N, K] codes are blocked
+    codes = torch.zeros(1, 2, 128, 48, dtype=torch.uint8)
+    assert ops.as_codes(codes, 128) is not None  # blocked fp6 codes pass through
     with pytest.raises(ValueError):
-        ops.as_codes(torch.zeros(1, 3, 128, 64, dtype=torch.uint8), 128)  # blocked codes of another width
+        ops.as_codes(torch.zeros(128, 128, dtype=torch.uint8), 128)  # one byte per value is not an operand
     with pytest.raises(ValueError):
-        ops.block_rows(torch.zeros(100, 128, dtype=torch.uint8))  # rows not a multiple of 128
+        ops.as_codes(torch.zeros(1, 3, 128, 48, dtype=torch.uint8), 128)  # blocked codes of another width
+    with pytest.raises(ValueError):
+        ops.as_codes(torch.zeros(1, 2, 128, 64, dtype=torch.uint8), 128)  # 64-byte rows
+    with pytest.raises(ValueError):
+        ops.encode_weights(torch.zeros(100, 128, dtype=torch.int32))  # rows not a multiple of 128
+    with pytest.raises(ValueError):
+        ops.encode_weights(torch.full((128, 64), 8, dtype=torch.int32))  # not an int4 weight
+    with pytest.raises(ValueError):
+        ops.encode_acts(torch.full((128, 64), 16, dtype=torch.int32))  # not an int4 activation
 
 
-def test_tile_blocked_layout_round_trip_and_offsets():
-    """block_rows / unblock_rows are inverse; element (r, k) of the blocked copy sits at the byte offset
-    (r // 128) * 128 * K + (k // 64) * 8192 + (r % 128) * 64 + k % 64, the one the kernels use."""
+def test_fp6_codes_are_the_formats_values():
+    """Each code the format helpers write is the fp6 code of the stated value: weights e3m2(2w) (bias 3, 2 mantissa
+    bits), activations e2m3(q / 2) (bias 1, 3 mantissa bits), checked on the closed forms of both formats for every
+    int4 value, and decode inverts encode."""
+    import torch
+
+    from wdl import ops
+
+    def e3m2(c):
+        s, e, m = (-1 if c & 32 else 1), (c >> 2) & 7, c & 3
+        return s * (m / 4 * 2.0 ** -2 if e == 0 else 2.0 ** (e - 3) * (1 + m / 4))
+
+    def e2m3(c):
+        s, e, m = (-1 if c & 32 else 1), (c >> 3) & 3, c & 7
+        return s * (m / 8 if e == 0 else 2.0 ** (e - 1) * (1 + m / 8))
+
+    w = torch.arange(-8, 8).repeat(128, 4)            # [128, 64]
+    q = torch.arange(-8, 16).repeat(128, 3)[:, :64]   # [128, 64]
+    cw = ops._unpack6(ops.encode_weights(w))
+    ca = ops._unpack6(ops.encode_acts(q))
+    assert all(e3m2(int(c)) == 2 * int(v) for c, v in zip(cw[0], w[0]))
+    assert all(e2m3(int(c)) == int(v) / 2 for c, v in zip(ca[0], q[0]))
+    assert torch.equal(cw, cw[:1].expand_as(cw)) and torch.equal(ca, ca[:1].expand_as(ca))
+    assert int(cw[0, 9]) == 0b010000 and int(cw[0, 0]) == 0b111100  # w = 1: 2 = 1.0 * 2^1; w = -8: -16
+    assert int(ca[0, 9]) == 0b000100 and int(ca[0, 23]) == 0b011111  # q = 1: subnormal 0.5; q = 15: 7.5
+    assert torch.equal(ops.decode_weights(ops.encode_weights(w)), w.to(torch.int32))
+    assert torch.equal(ops.decode_acts(ops.encode_acts(q)), q.to(torch.int32))
+
+
+def test_tile_blocked_layout_offsets():
+    """Code k of row r sits where the kernels put it: 128-row tiles of [K/64][128][48 bytes] (group g of row r at
+    (r // 128) * (K / 64) * 6144 + g * 6144 + (r % 128) * 48), value k of the group in half h = k // 32 at bits
+    6 (k % 32) of the half's 24 bytes, the half's bytes 0..15 at 16 h and bytes 16..23 at 32 + 8 h."""
     import torch
 
     from wdl import ops
 
     R, K = 256, 192
-    t = torch.randint(0, 256, (R, K), generator=torch.Generator().manual_seed(0), dtype=torch.int32).to(torch.uint8)
-    b = ops.block_rows(t)
-    assert b.shape == (2, 3, 128, 64) and b.is_contiguous()
-    assert torch.equal(ops.unblock_rows(b), t)
+    g = torch.Generator().manual_seed(0)
+    w = torch.randint(-8, 8, (R, K), generator=g, dtype=torch.int32)
+    b = ops.encode_weights(w)
+    assert b.shape == (2, 3, 128, 48) and b.is_contiguous()
+    codes = ops._W_ENC[(w + 8).long()]
     flat = b.reshape(-1)
-    for r, k in [(0, 0), (5, 70), (127, 191), (128, 0), (200, 100), (255, 191)]:
-        off = (r // 128) * 128 * K + (k // 64) * 8192 + (r % 128) * 64 + k % 64
-        assert int(flat[off]) == int(t[r, k])
+
+    def byte_at(r, grp, h, hb):
+        base = (r // 128) * (K // 64) * 6144 + grp * 6144 + (r % 128) * 48
+        return int(flat[base + (16 * h + hb if hb < 16 else 32 + 8 * h + hb - 16)])
+
+    for r in [0, 5, 127, 128, 200, 255]:
+        for k in range(K):
+            grp, h, i = k // 64, (k % 64) // 32, k % 32
+            bit = 6 * i
+            lo = byte_at(r, grp, h, bit // 8)
+            hi = byte_at(r, grp, h, bit // 8 + 1) if bit // 8 + 1 < 24 else 0
+            assert ((lo | hi << 8) >> (bit % 8)) & 63 == int(codes[r, k]), (r, k)
+    assert torch.equal(ops.decode_weights(b), w)

@@ -81,8 +81,8 @@ def test_small_block_matches_oracle(gpu, seed):
     assert float(same.float().mean()) > 0.97
 
 
-def test_baseline_config1_block_matches_oracle(gpu):
-    """dim 3072, 24 x 128 heads, FFN 14336, 464-token frame (16 x 29) at start frame 2 over a
+def test_full_width_block_on_one_frame_matches_oracle(gpu):
+    """The full-width block on one frame: dim 3072, 24 x 128 heads, FFN 14336, 464-token frame (16 x 29) at start frame 2 over a
     928-token FP8 cache (two prior frames), 512 context tokens, random-init W4A4 weights."""
     X, out, ref, cache, ocache, inp = run_pair(3072, 24, 14336, (1, 16, 29), 2, 928, 512, 7)
     err = float((out.float() - ref.float()).abs().max()) / float(ref.float().abs().max())

@@ -16,13 +16,10 @@ pytestmark = pytest.mark.gpu
 
 
 def codes_to_int(q):
-    """e4m3 codes -> their integer values; tile-blocked operands [R/128, K/64, 128, 64] as the [R, K] matrix."""
+    """Activation operand (tile-blocked fp6 codes [R/128, K/64, 128, 48]) -> the integer values [R, K]."""
     from wdl import ops
 
-    q = q.cpu()
-    if q.dim() == 4:
-        q = ops.unblock_rows(q)
-    return q.view(torch.float8_e4m3fn).float().to(torch.int32)
+    return ops.decode_acts(q.cpu())
 
 
 def data(M, K, seed=0, outliers=True):
@@ -87,7 +84,7 @@ def launch_gemm(qa_int, asc, qweight, wsc, lora=None, pu=None, bias=None, M=None
     from wdl import ops
 
     Mp, K = qa_int.shape
-    codes = ops.block_rows(qa_int.float().to(torch.float8_e4m3fn).view(torch.uint8)).cuda()
+    codes = ops.encode_acts(qa_int).cuda()
     N = qweight.shape[0]
     M = Mp if M is None else M
     if out is None:
@@ -98,17 +95,17 @@ def launch_gemm(qa_int, asc, qweight, wsc, lora=None, pu=None, bias=None, M=None
 
 
 @pytest.mark.parametrize("N,K", [(128, 64), (384, 3072), (256, 14336)])
-def test_weight_codes_are_the_e4m3_values_of_the_packed_integers(gpu, N, K):
-    """wdl_w4a4_weight_codes: packed nibbles [N, K/2] -> tile-blocked e4m3 codes of [N, K], bit-exact against torch's
-    e4m3 of the unpacked integers (every int4 value is exactly representable), in the blocked order."""
+def test_weight_codes_are_the_fp6_codes_of_the_packed_integers(gpu, N, K):
+    """wdl_w4a4_weight_codes: packed nibbles [N, K/2] -> tile-blocked fp6 codes (e3m2 of 2w) of [N, K], bit-exact
+    against the format's statement (ops.encode_weights, itself checked on the closed form of e3m2)."""
     from wdl import ops, w4a4
 
     q = torch.randint(-8, 8, (N, K), generator=torch.Generator().manual_seed(N + K), dtype=torch.int32)
     codes = ops.weight_codes(w4a4.pack_weight(q).cuda()).cpu()
-    want = q.float().to(torch.float8_e4m3fn).view(torch.uint8)
-    assert codes.shape == (N // 128, K // 64, 128, 64)
-    assert torch.equal(ops.unblock_rows(codes), want)
-    assert torch.equal(codes[-1, -1, 127], want[N - 1, K - 64:])  # the last 64-byte row of the last tile
+    want = ops.encode_weights(q)
+    assert codes.shape == (N // 128, K // 64, 128, 48)
+    assert torch.equal(codes, want)
+    assert torch.equal(ops.decode_weights(codes), q)
 
 
 @pytest.mark.parametrize("M,N,K", [(128, 128, 64), (256, 384, 512), (128, 256, 3072), (128, 128, 14336),

@@ -8,9 +8,9 @@
 //   scale = bf16( max_{64 group} |u| / qmax )                       (qmax 7 signed, 15 unsigned)
 //   q     = clamp(rint(u / scale))                                  (0 where scale is 0)
 //   lora  = v . proj_down                                           (bf16 MFMA, fp32 sums)
-// Outputs: q as e4m3 codes of the integer values (exact), one byte per value [Mp, K] (rows >= M zero) in the W4A4
-// GEMM's tile-blocked layout ([Mp / 128][K / 64][128][64], Mp a multiple of 128); ascales bf16 [K/64, Mp]; lora fp32
-// [Mp, 32].
+// Outputs: q as fp6 codes (e2m3 of q / 2, exact) [Mp, K] (rows >= M zero) in the W4A4 GEMM's tile-blocked layout
+// ([Mp / 128][K / 64][128][48 bytes], Mp a multiple of 128; see blocked6_offset); ascales bf16 [K/64, Mp]; lora
+// fp32 [Mp, 32].
 //
 // Launches (all parallel over rows and column blocks, nothing serial over K):
 //   row_stats  (LN only): one wave per row; LN statistics in a fixed order — lane l owns the 8-value chunks
@@ -225,13 +225,25 @@ __global__ __launch_bounds__(2 * CB) void quant_kernel(QuantArgs a) {
             const float r = sc > 0.0f ? __builtin_rintf(div_rn(u[j], sc, rsc)) : 0.0f;
             qv[j] = live ? fminf(fmaxf(r, qlo), qmax) + 0.0f : 0.0f;  // + 0 turns -0 into +0
         }
-        uint32_t w0 = 0, w1 = 0;
-        w0 = __builtin_amdgcn_cvt_pk_fp8_f32(qv[0], qv[1], w0, false);
-        w0 = __builtin_amdgcn_cvt_pk_fp8_f32(qv[2], qv[3], w0, true);
-        w1 = __builtin_amdgcn_cvt_pk_fp8_f32(qv[4], qv[5], w1, false);
-        w1 = __builtin_amdgcn_cvt_pk_fp8_f32(qv[6], qv[7], w1, true);
+        // fp6 codes (e2m3 of q / 2) of the lane's 8 values: k = 8 slot .. 8 slot + 7 of the group, i.e. half
+        // slot / 4, positions 8 (slot % 4) ..; 48 bits = half bytes 6 (slot % 4) .. + 5, stored as a dword and a
+        // short at their aligned places (the even slots start on a dword, the odd ones on a short)
+        uint32_t c[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c[j] = act_code6(qv[j]);
+        const uint32_t v0 = c[0] | (c[1] << 6) | (c[2] << 12) | (c[3] << 18);
+        const uint32_t v1 = c[4] | (c[5] << 6) | (c[6] << 12) | (c[7] << 18);
+        const uint32_t lo = v0 | (v1 << 24), hi = v1 >> 8;  // bits 0..31 and 32..47
         if (row < a.Mp) {
-            *reinterpret_cast<uint2*>(a.q + blocked_offset(row, col, K)) = make_uint2(w0, w1);
+            uint8_t* dst = a.q + blocked6_offset(row, col / 64, K);
+            const int h = (slot / 4), b = 6 * (slot % 4);
+            if (slot % 2 == 0) {
+                *reinterpret_cast<uint32_t*>(dst + half_byte(h, b)) = lo;
+                *reinterpret_cast<uint16_t*>(dst + half_byte(h, b + 4)) = uint16_t(hi);
+            } else {
+                *reinterpret_cast<uint16_t*>(dst + half_byte(h, b)) = uint16_t(lo);
+                *reinterpret_cast<uint32_t*>(dst + half_byte(h, b + 2)) = (lo >> 16) | (hi << 16);
+            }
             if (slot == 0) a.ascales[(col / 64) * a.Mp + row] = live ? sb : uint16_t(0);
         }
     }

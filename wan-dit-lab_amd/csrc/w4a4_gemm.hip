@@ -3,20 +3,24 @@
 //   y[m][n] = sum_g as[g][m] * ws[g][n] * I_g[m][n]  +  bf16(lora[m]) . pu[n]  +  bias[n]
 //   I_g[m][n] = sum_{k in group g} qa[m][k] * qw[n][k]          (exact integers)
 //
-// Operands: qa — activation int4 values as e4m3 codes, one byte each, [Mp, K] (wdl_act_quant_w4); wc — weight
-// int4 values as e4m3 codes [N, K] (wdl_w4a4_weight_codes, expanded once from the packed [N, K/2] nibbles);
-// as [K/64, Mp], ws [K/64, N] bf16; lora fp32 [Mp, 32]; pu bf16 [N, 32]; bias bf16 [N].
+// Operands: qa — activation int4 values as fp6 codes (wdl_act_quant_w4); wc — weight int4 values as fp6 codes
+// (wdl_w4a4_weight_codes, expanded once from the packed [N, K/2] nibbles), both tile-blocked 48 bytes per row
+// and 64-deep group (the format is described with blocked6_offset); as [K/64, Mp], ws [K/64, N] bf16; lora fp32
+// [Mp, 32]; pu bf16 [N, 32]; bias bf16 [N].
 //
-// Arithmetic: every int4 value is exactly an e4m3 value, so v_mfma_f32_32x32x64_f8f6f4 (one 64-deep group per
-// instruction, the int8 rate) returns I_g exactly as an fp32 integer (|I_g| <= 64 * 8 * 15 < 2^24). The per-group
-// scale product ws[n] * as[m] comes from a bf16 outer-product MFMA (exact: 8-bit by 8-bit significands), and each
-// group is folded in with one fmaf per element, groups in increasing order. The low-rank term is two bf16 MFMAs
-// accumulated into the result, then the bias.
+// Arithmetic: weights are e3m2 codes of 2w and activations e2m3 codes of q / 2, so v_mfma_f32_32x32x64_f8f6f4 in
+// its fp6 x fp6 form (one 64-deep group per instruction, 32 cycles: twice the int8 rate) returns I_g exactly as
+// an fp32 integer (|I_g| <= 64 * 8 * 15 < 2^24). The per-group scale product ws[n] * as[m] comes from a bf16
+// outer-product MFMA (exact: 8-bit by 8-bit significands), and each group is folded in with one fmaf per element,
+// groups in increasing order. The low-rank term is two bf16 MFMAs accumulated into the result, then the bias.
 //
 // Orientation: the tile is computed transposed, C^T[n][m] (rows = output features, columns = tokens), so a lane
 // holds one token and 16 features: row n = 8*(i/4) + 4*(lane/32) + i%4, column m = lane%32 of each 32x32 subtile.
 // Both operands arrive as codes, so the main loop issues no conversion work: per MFMA pair its vector ALU work is
 // the 16 fmaf of the scale fold.
+//
+// The FP8 linears (wdl_fp8_gemm) share the main loop with e4m3 codes in plain row-major [rows, K] operands and
+// one fp32 accumulation over all of K.
 #include "wdl_common.h"
 
 namespace {
@@ -53,15 +57,18 @@ struct GemmArgs {
     const float* wsf;         // FP8 linears: weight scales fp32 [N] (rows) or [1] (tensor)
 };
 
-// Tile BN (features) x BM (tokens), NW waves in a (BN / WN) x (BM / WM) grid. Per 64-deep group the workgroup
-// needs the activation codes [BM][64 B], the weight codes [BN][64 B] and the scales ws[BN], as[BM]; all three
-// stream straight from global memory into a 4-stage LDS ring with global_load_lds (lane-linear in LDS: 16 bytes
-// per lane for codes, 4 for scales), issued 3 groups ahead, so no staging registers are involved. Every wave
-// issues the same number of these loads per group, so each wave's vmcnt names exactly the groups still in flight;
-// the loads are written as inline asm so that the compiler's own wait insertion, which cannot tell the ring
-// stages apart, does not add vmcnt(0) waits in front of every LDS read. Code rows sit in LDS with their four
-// 16-byte quarters XOR-swizzled by (row / 4) % 4 (conflict-free operand reads). Each scale stage ends in 64 zero
-// bytes that lanes 32..63 read, which zeroes their half of the outer-product operands without a select.
+// Tile BN (features) x BM (tokens), NW waves in a (BN / WN) x (BM / WM) grid. Every operand byte streams from
+// global memory straight into a STAGES-deep LDS ring with global_load_lds (lane-linear in LDS: 16 or 4 bytes per
+// lane), issued STAGES - 1 groups ahead, so no staging registers are involved. Every wave issues the same number
+// of these loads per group, so each wave's vmcnt names exactly the groups still in flight; the loads are written
+// as inline asm so that the compiler's own wait insertion, which cannot tell the ring stages apart, does not add
+// vmcnt(0) waits in front of every LDS read.
+//   W4A4: a stage is the group's fp6 weight codes [BN][48 B] then activation codes [BM][48 B] — contiguous 6 KB
+//   blocks in global memory — split evenly over the waves, plus the scales ws[BN], as[BM]. Rows of 48 bytes read
+//   as 16 + 8 bytes per lane are free of bank conflicts on the 16-byte reads. Each scale stage ends in 64 zero
+//   bytes that lanes 32..63 read, which zeroes their half of the outer-product operands without a select.
+//   FP8: separate activation [BM][64 B] and weight [BN][64 B] stages, code rows with their four 16-byte quarters
+//   XOR-swizzled by (row / 4) % 4 (conflict-free operand reads).
 // Workgroup ids are remapped so that the tiles of one weight slab run on one XCD.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return uint32_t(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
@@ -205,24 +212,31 @@ __device__ __forceinline__ void finish_tile(const GemmArgs& p, f32x16 (&acc)[TN]
         }
 }
 
-// The main loop of both GEMMs. FOLD: the W4A4 product (per-group scale fold, scales streamed with the codes);
-// otherwise the FP8 product (codes only, one fp32 accumulation over all of K in the MFMA accumulator).
-template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES, bool FOLD, bool BLK>
+// The main loop of both GEMMs. W4: the W4A4 product (fp6 tile-blocked codes, per-group scale fold, scales
+// streamed with the codes); otherwise the FP8 product (e4m3 row-major codes only, one fp32 accumulation over all
+// of K in the MFMA accumulator).
+template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES, bool W4>
 __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
-    static_assert(!BLK || (BN % BLOCK_ROWS == 0 && BM % BLOCK_ROWS == 0), "blocked operands come in 128-row tiles");
+    static_assert(!W4 || (BN % BLOCK_ROWS == 0 && BM % BLOCK_ROWS == 0), "blocked operands come in 128-row tiles");
     static_assert((BN / WN) * (BM / WM) == NW, "wave grid");
-    static_assert(STAGES >= 3 && STAGES <= 8, "ring depth");
+    static_assert(STAGES >= 4 && STAGES <= 8, "ring depth");
     constexpr int TN = WN / 32, TM = WM / 32;
-    constexpr int XI = BM * 4 / 64 / NW;   // 16-byte loads per wave per group: activation codes
-    constexpr int WI = BN * 4 / 64 / NW;   // and weight codes
-    constexpr int LPG = XI + WI + (FOLD ? 1 : 0);  // + one 4-byte load of scales: loads per wave per group
+    // FP8: 16-byte loads per wave per group of activation codes and of weight codes
+    constexpr int XI = W4 ? 0 : BM * 4 / 64 / NW;
+    constexpr int WI = W4 ? 0 : BN * 4 / 64 / NW;
+    static_assert(W4 || (XI >= 1 && WI >= 1 && BM * 4 == XI * 64 * NW && BN * 4 == WI * 64 * NW), "tile vs waves");
+    // W4A4: a stage's codes ((BN + BM) rows of 48 bytes) in CB bytes per wave: N16 16-byte and N4 4-byte loads
+    constexpr int CS = (BN + BM) * ROW6, CB = CS / NW;
+    constexpr int N16 = W4 ? CB / 1024 : 0, N4 = W4 ? CB % 1024 / 256 : 0;
+    static_assert(!W4 || (CS % NW == 0 && CB % 256 == 0), "fp6 stage vs waves");
+    constexpr int LPG = W4 ? N16 + N4 + 1 : XI + WI;  // loads per wave per group (W4: + one 4-byte load of scales)
     constexpr int SD = NW * 256;           // scale bytes loaded per stage (ws[BN], as[BM], then padding)
     constexpr int SB = SD + 256;           // + 64 zero bytes (rounded up) read by lanes 32..63
-    static_assert(XI >= 1 && WI >= 1 && BM * 4 == XI * 64 * NW && BN * 4 == WI * 64 * NW, "tile vs waves");
     static_assert(2 * (BN + BM) <= SD, "scale stage");
-    __shared__ __attribute__((aligned(1024))) uint8_t sX[STAGES][BM * 64];
-    __shared__ __attribute__((aligned(1024))) uint8_t sW[STAGES][BN * 64];
-    __shared__ __attribute__((aligned(256))) uint8_t sS[FOLD ? STAGES : 1][FOLD ? SB : 256];
+    __shared__ __attribute__((aligned(1024))) uint8_t sX[W4 ? 1 : STAGES][W4 ? 16 : BM * 64];
+    __shared__ __attribute__((aligned(1024))) uint8_t sW[W4 ? 1 : STAGES][W4 ? 16 : BN * 64];
+    __shared__ __attribute__((aligned(1024))) uint8_t sC[W4 ? STAGES : 1][W4 ? CS : 16];
+    __shared__ __attribute__((aligned(256))) uint8_t sS[W4 ? STAGES : 1][W4 ? SB : 256];
 
     const int t = threadIdx.x, lane = t % 64;
     const int wave = __builtin_amdgcn_readfirstlane(t / 64);
@@ -235,25 +249,35 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
     const int64_t K = p.K, G = K / 64;
 
     // zero tails of the scale stages (written once; the loads never touch them)
-    if constexpr (FOLD)
+    if constexpr (W4)
         if (t < STAGES * 16) *reinterpret_cast<uint32_t*>(&sS[t / 16][SD + (t % 16) * 4]) = 0u;
 
-    // this lane's sources for group 0; group g adds 64 g bytes (codes) or g times the scale row stride
-    const uint8_t* xsrc[XI];
+    // this lane's sources for group 0; group g adds g BLOCK6 bytes (W4 codes), 64 g bytes (FP8 codes) or g times
+    // the scale row stride
+    const uint8_t* xsrc[W4 ? N16 + N4 : XI];
+    const uint8_t* wsrc[W4 ? 1 : WI];
+    if constexpr (W4) {
 #pragma unroll
-    for (int j = 0; j < XI; ++j) {
-        const int slot = (wave * XI + j) * 64 + lane;          // 16-byte slot of the stage
-        const int row = slot / 4, quarter = (slot % 4) ^ ((row >> 2) & 3);
-        xsrc[j] = BLK ? p.qa + (m0 + row / BLOCK_ROWS * BLOCK_ROWS) * K + (row % BLOCK_ROWS) * 64 + quarter * 16
-                      : p.qa + (m0 + row) * K + quarter * 16;
-    }
-    const uint8_t* wsrc[WI];
+        for (int u = 0; u < N16 + N4; ++u) {
+            // stage byte o: weight rows [0, BN), then activation rows; each 128-row tile is one 6 KB block
+            const int o = wave * CB + (u < N16 ? u * 1024 + lane * 16 : N16 * 1024 + (u - N16) * 256 + lane * 4);
+            xsrc[u] = o < BN * ROW6 ? p.wc + (n0 / BLOCK_ROWS + o / BLOCK6) * G * BLOCK6 + o % BLOCK6
+                                    : p.qa + (m0 / BLOCK_ROWS + (o - BN * ROW6) / BLOCK6) * G * BLOCK6 +
+                                          (o - BN * ROW6) % BLOCK6;
+        }
+    } else {
 #pragma unroll
-    for (int j = 0; j < WI; ++j) {
-        const int slot = (wave * WI + j) * 64 + lane;
-        const int row = slot / 4, quarter = (slot % 4) ^ ((row >> 2) & 3);
-        wsrc[j] = BLK ? p.wc + (n0 + row / BLOCK_ROWS * BLOCK_ROWS) * K + (row % BLOCK_ROWS) * 64 + quarter * 16
-                      : p.wc + (n0 + row) * K + quarter * 16;
+        for (int j = 0; j < XI; ++j) {
+            const int slot = (wave * XI + j) * 64 + lane;          // 16-byte slot of the stage
+            const int row = slot / 4, quarter = (slot % 4) ^ ((row >> 2) & 3);
+            xsrc[j] = p.qa + (m0 + row) * K + quarter * 16;
+        }
+#pragma unroll
+        for (int j = 0; j < WI; ++j) {
+            const int slot = (wave * WI + j) * 64 + lane;
+            const int row = slot / 4, quarter = (slot % 4) ^ ((row >> 2) & 3);
+            wsrc[j] = p.wc + (n0 + row) * K + quarter * 16;
+        }
     }
     const uint8_t* ssrc;   // 4 bytes: ws pair, as pair or (padding lanes) a valid dummy
     int64_t sstride;
@@ -271,37 +295,46 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         }
     }
 
-    // direct load u (0 .. LPG - 1: activation codes, weight codes, scales) of group g (clamped to the last group)
-    // into stage st
+    // direct load u (0 .. LPG - 1) of group g (clamped to the last group) into stage st
     auto issue_one = [&](int st, int64_t g, int u) {
         const int64_t gg = g < G ? g : G - 1;
-        if (u < XI) dma16(xsrc[u] + gg * (BLK ? BLOCK_ROWS * 64 : 64), lds_addr(&sX[st][(wave * XI + u) * 1024]));
-        else if (u < XI + WI)
-            dma16(wsrc[u - XI] + gg * (BLK ? BLOCK_ROWS * 64 : 64), lds_addr(&sW[st][(wave * WI + u - XI) * 1024]));
-        else if constexpr (FOLD) dma4(ssrc + gg * sstride, lds_addr(&sS[st][wave * 256]));
+        if constexpr (W4) {
+            if (u < N16) dma16(xsrc[u] + gg * BLOCK6, lds_addr(&sC[st][wave * CB + u * 1024]));
+            else if (u < N16 + N4)
+                dma4(xsrc[u] + gg * BLOCK6, lds_addr(&sC[st][wave * CB + N16 * 1024 + (u - N16) * 256]));
+            else dma4(ssrc + gg * sstride, lds_addr(&sS[st][wave * 256]));
+        } else {
+            if (u < XI) dma16(xsrc[u] + gg * 64, lds_addr(&sX[st][(wave * XI + u) * 1024]));
+            else dma16(wsrc[u - XI] + gg * 64, lds_addr(&sW[st][(wave * WI + u - XI) * 1024]));
+        }
     };
 
-    // per-lane LDS offsets (stage-independent): operand rows with their swizzled quarters, scale entries
+    // per-lane LDS offsets (stage-independent). W4: a lane's 16-byte and 8-byte pieces of its operand row, the
+    // scale entries. FP8: operand rows and the two swizzled quarters.
     const bool low = lane < 32;
+    const int half = lane / 32;
     int aoff[TN], soa[TN], boff[TM], sob[TM];
     int q0, q1;
 #pragma unroll
     for (int i = 0; i < TN; ++i) {
         const int row = wn * WN + i * 32 + lane % 32;
-        aoff[i] = row * 64;
+        aoff[i] = W4 ? row * ROW6 : row * 64;
         soa[i] = low ? 2 * row : SD + 2 * (lane % 32);
     }
 #pragma unroll
     for (int j = 0; j < TM; ++j) {
         const int row = wm * WM + j * 32 + lane % 32;
-        boff[j] = row * 64;
+        boff[j] = W4 ? (BN + row) * ROW6 : row * 64;
         sob[j] = low ? 2 * BN + 2 * row : SD + 2 * (lane % 32);
     }
-    {
+    if constexpr (W4) {
+        q0 = 16 * half;      // bytes 0..15 of the lane's half
+        q1 = 32 + 8 * half;  // bytes 16..23
+    } else {
         // every operand row index here is 32-aligned plus lane % 32, so (row / 4) % 4 = (lane % 32 / 4) % 4
         const int sw = ((lane % 32) >> 2) & 3;
-        q0 = ((2 * (lane / 32)) ^ sw) * 16;
-        q1 = ((2 * (lane / 32) + 1) ^ sw) * 16;
+        q0 = ((2 * half) ^ sw) * 16;
+        q1 = ((2 * half + 1) ^ sw) * 16;
     }
     static_assert(WN % 32 == 0 && WM % 32 == 0, "32-aligned subtiles");
 
@@ -312,26 +345,40 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         for (int j = 0; j < TM; ++j) acc[i][j] = f32x16{};
     const f32x16 zero = {};
 
-    // one group's operands in registers: weight / activation code fragments and (FOLD) the bf16 scale of each
-    // fragment row, zero-extended (lanes 32..63 read the zero tail)
+    // one group's operands in registers: weight / activation code fragments (W4: 6 dwords of fp6 codes, FP8: 8 of
+    // e4m3) and (W4) the bf16 scale of each fragment row, zero-extended (lanes 32..63 read the zero tail)
     i32x8 fa[TN], fb[TM];
     uint32_t fsa[TN], fsb[TM];
+    auto load_frag = [&](const uint8_t* r) {
+        if constexpr (W4) {
+            const uint4 x = *reinterpret_cast<const uint4*>(r + q0);
+            const uint2 y = *reinterpret_cast<const uint2*>(r + q1);
+            return i32x8{int(x.x), int(x.y), int(x.z), int(x.w), int(y.x), int(y.y), 0, 0};
+        } else {
+            const uint4 x = *reinterpret_cast<const uint4*>(r + q0), y = *reinterpret_cast<const uint4*>(r + q1);
+            return i32x8{int(x.x), int(x.y), int(x.z), int(x.w), int(y.x), int(y.y), int(y.z), int(y.w)};
+        }
+    };
     auto load_a = [&](int st, int i) {
-        const uint8_t* r = &sW[st][aoff[i]];
-        const uint4 a0 = *reinterpret_cast<const uint4*>(r + q0), a1 = *reinterpret_cast<const uint4*>(r + q1);
-        fa[i] = i32x8{int(a0.x), int(a0.y), int(a0.z), int(a0.w), int(a1.x), int(a1.y), int(a1.z), int(a1.w)};
-        if constexpr (FOLD) fsa[i] = *reinterpret_cast<const uint16_t*>(&sS[st][soa[i]]);
+        if constexpr (W4) {
+            fa[i] = load_frag(&sC[st][aoff[i]]);
+            fsa[i] = *reinterpret_cast<const uint16_t*>(&sS[st][soa[i]]);
+        } else {
+            fa[i] = load_frag(&sW[st][aoff[i]]);
+        }
     };
     auto load_b = [&](int st, int j) {
-        const uint8_t* r = &sX[st][boff[j]];
-        const uint4 b0 = *reinterpret_cast<const uint4*>(r + q0), b1 = *reinterpret_cast<const uint4*>(r + q1);
-        fb[j] = i32x8{int(b0.x), int(b0.y), int(b0.z), int(b0.w), int(b1.x), int(b1.y), int(b1.z), int(b1.w)};
-        if constexpr (FOLD) fsb[j] = *reinterpret_cast<const uint16_t*>(&sS[st][sob[j]]);
+        if constexpr (W4) {
+            fb[j] = load_frag(&sC[st][boff[j]]);
+            fsb[j] = *reinterpret_cast<const uint16_t*>(&sS[st][sob[j]]);
+        } else {
+            fb[j] = load_frag(&sX[st][boff[j]]);
+        }
     };
 
     // Multiply one group from the fragment registers; each fragment is reloaded with the next group's operands
     // (stage nst) right after its last use, so the reads overlap the remaining MFMAs and one register set serves.
-    // FOLD: the fold is software-pipelined by one subtile: the products of subtile s are folded while the MFMAs of
+    // W4: the fold is software-pipelined by one subtile: the products of subtile s are folded while the MFMAs of
     // subtile s + 1 run (the last subtile of a group while the first subtile of the next group runs). pI / pP hold
     // the pending subtile; they start at zero (the first fold adds 0 * 0 to a zero accumulator: no change).
     f32x16 pI = zero, pP = zero;
@@ -341,11 +388,12 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
 #pragma unroll
         for (int s = 0; s < TN * TM; ++s) {
             const int i = s / TM, j = s % TM;
-            if constexpr (FOLD) {
+            if constexpr (W4) {
                 const int pi = s == 0 ? TN - 1 : (s - 1) / TM, pj = s == 0 ? TM - 1 : (s - 1) % TM;
                 const i16x4 oa = __builtin_bit_cast(i16x4, make_uint2(fsa[i], 0u));
                 const i16x4 ob = __builtin_bit_cast(i16x4, make_uint2(fsb[j], 0u));
-                const f32x16 I = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[i], fb[j], zero, 0, 0, 0, 0, 0, 0);
+                // A: weights as e3m2 (format 3), B: activations as e2m3 (format 2)
+                const f32x16 I = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[i], fb[j], zero, 3, 2, 0, 0, 0, 0);
                 const f32x16 P = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(oa, ob, zero, 0, 0, 0);
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[pi][pj][e] = fmaf(pI[e], pP[e], acc[pi][pj][e]);
@@ -358,8 +406,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
             if (i == TN - 1) load_b(nst, j);
             // one wave issues in order and an MFMA waits at issue while the matrix core is busy, so the fold of
             // subtile s - 1 is split around the two MFMAs of subtile s: it executes while they run
-            if constexpr (FOLD) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // I_s (64 cycles)
+            if constexpr (W4) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // I_s (32 cycles)
                 __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // fold of s - 1, first part
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // P_s (32 cycles)
                 __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // the rest
@@ -402,7 +450,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         for (int k = 0; k < STAGES; ++k) ring_step(k, g + k);
     }
     for (int k = 0; g < G; ++g, ++k) ring_step(k, g);
-    if constexpr (FOLD) {
+    if constexpr (W4) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[TN - 1][TM - 1][e] = fmaf(pI[e], pP[e], acc[TN - 1][TM - 1][e]);
     }
@@ -413,12 +461,12 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
 
 template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES>
 __global__ __launch_bounds__(NW * 64) void w4a4_gemm_kernel(GemmArgs p) {
-    gemm_body<BN, BM, WN, WM, NW, EPI, STAGES, true, true>(p);
+    gemm_body<BN, BM, WN, WM, NW, EPI, STAGES, true>(p);
 }
 
 template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES>
 __global__ __launch_bounds__(NW * 64) void fp8_gemm_kernel(GemmArgs p) {
-    gemm_body<BN, BM, WN, WM, NW, EPI, STAGES, false, false>(p);
+    gemm_body<BN, BM, WN, WM, NW, EPI, STAGES, false>(p);
 }
 
 template <int BN, int BM, int WN, int WM, int NW, int ST>
@@ -463,11 +511,11 @@ int dispatch(const GemmArgs& a, int epi, hipStream_t stream) {
     return launch<128, 128, 64, 64, 4, WDL_GEMM_STAGES>(a, epi, stream);
 }
 
-// e4m3 codes of the two's complement nibbles 0..7 (values 0..7) and 8..15 (values -8..-1)
-constexpr uint32_t LUT0 = 0x44403800u, LUT1 = 0x4E4C4A48u, LUT2 = 0xCACCCED0u, LUT3 = 0xB8C0C4C8u;
+// fp6 codes (e3m2 of 2w) of the two's complement nibbles 0..7 (w = 0..7) and 8..15 (w = -8..-1)
+constexpr uint32_t LUT0 = 0x16141000u, LUT1 = 0x1B1A1918u, LUT2 = 0x393A3B3Cu, LUT3 = 0x30343638u;
 
-// four nibbles in the low 4 bits of each byte of x -> four e4m3 codes
-__device__ __forceinline__ uint32_t nib4_to_e4m3(uint32_t x) {
+// four nibbles in the low 4 bits of each byte of x -> four 6-bit codes, one per byte
+__device__ __forceinline__ uint32_t nib4_to_code6(uint32_t x) {
     const uint32_t sel = x & 0x07070707u;
     const uint32_t pos = __builtin_amdgcn_perm(LUT1, LUT0, sel);
     const uint32_t neg = __builtin_amdgcn_perm(LUT3, LUT2, sel);
@@ -476,18 +524,30 @@ __device__ __forceinline__ uint32_t nib4_to_e4m3(uint32_t x) {
     return (neg & mask) | (pos & ~mask);
 }
 
-// packed nibbles [N, K/2] -> e4m3 codes [N, K] in the tile-blocked layout: one thread per 4 packed bytes (8 values)
-__global__ __launch_bounds__(256) void weight_codes_kernel(const uint32_t* qw, int64_t words, int64_t K,
-                                                         uint32_t* codes) {
+// packed nibbles [N, K/2] -> fp6 codes in the tile-blocked layout. The 32 packed bytes of a row's group hold
+// value k = j in the low nibble and k = 32 + j in the high nibble of byte j, so the low nibbles are half 0 and the
+// high nibbles half 1 (position j). One thread per 16 packed bytes: 16 codes of each half, 12 bytes each.
+__global__ __launch_bounds__(256) void weight_codes_kernel(const uint4* qw, int64_t units, int64_t K, uint8_t* codes) {
     const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= words) return;
-    // word i covers packed bytes 4i..4i+3 of row n = 4i / (K/2): group g, byte offset j0 = (4i) % 32 in the group
-    const int64_t byte = 4 * i, row = byte / (K / 2), in_row = byte % (K / 2);
-    const int64_t g = in_row / 32, j0 = in_row % 32;
-    const uint32_t w = qw[i];
-    uint32_t* dst = codes + blocked_offset(row, g * 64 + j0, K) / 4;
-    dst[0] = nib4_to_e4m3(w & 0x0f0f0f0fu);              // k = j0..j0+3
-    dst[8] = nib4_to_e4m3((w >> 4) & 0x0f0f0f0fu);       // k = 32 + j0..j0+3
+    if (i >= units) return;
+    const int64_t per_row = K / 32;  // 16-byte units per row
+    const int64_t row = i / per_row, in_row = i % per_row;
+    const int64_t g = in_row / 2;
+    const int u = int(in_row % 2);   // positions 16u .. 16u + 15
+    const uint4 w = qw[i];
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+    uint8_t* dst = codes + blocked6_offset(row, g, K);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        uint32_t q[4];  // 24-bit quads: positions 16u + 4j .. + 3
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[j] = pack4x6(nib4_to_code6((words[j] >> (4 * h)) & 0x0f0f0f0fu));
+        const uint32_t d0 = q[0] | (q[1] << 24), d1 = (q[1] >> 8) | (q[2] << 16), d2 = (q[2] >> 16) | (q[3] << 8);
+        // half bytes 12u .. 12u + 11
+        *reinterpret_cast<uint32_t*>(dst + half_byte(h, 12 * u)) = d0;
+        *reinterpret_cast<uint32_t*>(dst + half_byte(h, 12 * u + 4)) = d1;
+        *reinterpret_cast<uint32_t*>(dst + half_byte(h, 12 * u + 8)) = d2;
+    }
 }
 
 }  // namespace
@@ -526,10 +586,10 @@ extern "C" int wdl_w4a4_weight_codes(const void* qweight, int64_t N, int64_t K, 
     if (!qweight || !codes) return fail(WDL_EINVAL, "w4a4_weight_codes: null pointer");
     if ((reinterpret_cast<uintptr_t>(qweight) | reinterpret_cast<uintptr_t>(codes)) % 16)
         return fail(WDL_EINVAL, "w4a4_weight_codes: buffers must be 16-byte aligned");
-    const int64_t words = N * K / 8;
-    if (words == 0) return WDL_OK;
-    weight_codes_kernel<<<unsigned((words + 255) / 256), 256, 0, stream>>>(static_cast<const uint32_t*>(qweight),
-                                                                          words, K, static_cast<uint32_t*>(codes));
+    const int64_t units = N * K / 32;
+    if (units == 0) return WDL_OK;
+    weight_codes_kernel<<<unsigned((units + 255) / 256), 256, 0, stream>>>(static_cast<const uint4*>(qweight), units,
+                                                                          K, static_cast<uint8_t*>(codes));
     return check_launch("w4a4_weight_codes");
 }
 

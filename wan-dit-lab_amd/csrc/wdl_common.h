@@ -27,12 +27,42 @@ int fail(int code, const char* fmt, ...);
 int check_launch(const char* what);
 int cu_count();  // compute units of the current device (cached per device; 0 if the query fails)
 
-// The W4A4 GEMM's operand layout ("tile-blocked"): a byte matrix [R, K] (R a multiple of 128, K of 64) stored as
-// [R / 128][K / 64][128][64], so the 64-deep slice of a 128-row tile that one GEMM step reads is one contiguous
-// 8 KB block. Byte (r, k) sits at blocked_offset(r, k, K).
+// The W4A4 GEMM's operands: fp6 codes, tile-blocked.
+//
+// Values. Weights w in [-8, 7] are stored as the e3m2 code of 2w (sign, 3 exponent bits of bias 3, 2 mantissa
+// bits: every even integer in [-16, 14] is exact); activations q in [-8, 15] as the e2m3 code of q / 2 (bias 1,
+// 3 mantissa bits: every multiple of 1/2 in [-4, 7.5] is exact). The matrix cores multiply the two formats at the
+// fp6 rate and each product (2w)(q/2) = wq is an exact integer, so a 64-deep group sums to the same integer as the
+// int4 dot product.
+//
+// Bits. Value k (0..63) of a row's 64-deep group goes to half h = k / 32 at position i = k % 32; the 32 codes of
+// a half are packed little-endian, code i at bits [6i, 6i + 6) of 24 bytes (four codes in three bytes). This is
+// the register layout of v_mfma_f32_32x32x64_f8f6f4 for fp6 operands: lane (row, h) supplies its half's 24 bytes.
+//
+// Bytes. One row's group is 48 bytes: [half 0 bytes 0..15][half 1 bytes 0..15][half 0 bytes 16..23][half 1 bytes
+// 16..23], so a lane reads its 24 bytes as one aligned 16-byte and one aligned 8-byte load. A matrix [R, K]
+// (R a multiple of 128, K of 64) is stored as [R / 128][K / 64][128][48]: the group of a 128-row tile that one
+// GEMM step reads is one contiguous 6 KB block. The group g of row r starts at blocked6_offset(r, g, K).
 constexpr int BLOCK_ROWS = 128;
-__host__ __device__ __forceinline__ int64_t blocked_offset(int64_t r, int64_t k, int64_t K) {
-    return (r / BLOCK_ROWS) * BLOCK_ROWS * K + (k / 64) * (BLOCK_ROWS * 64) + (r % BLOCK_ROWS) * 64 + k % 64;
+constexpr int ROW6 = 48;                     // bytes of one row's 64-deep group
+constexpr int BLOCK6 = BLOCK_ROWS * ROW6;    // bytes of one 128-row tile's group
+__host__ __device__ __forceinline__ int64_t blocked6_offset(int64_t r, int64_t g, int64_t K) {
+    return (r / BLOCK_ROWS) * (K / 64) * BLOCK6 + g * BLOCK6 + (r % BLOCK_ROWS) * ROW6;
+}
+// offset in the 48-byte group row of byte b (0..23) of half h
+__host__ __device__ __forceinline__ int half_byte(int h, int b) { return b < 16 ? 16 * h + b : 32 + 8 * h + b - 16; }
+
+// e2m3 code of q / 2 for an integer-valued q with |q| <= 15: |q| 0..3 -> 4|q| (0.5 steps, subnormal up to 1.5),
+// 4..7 -> 2|q| + 8, 8..15 -> |q| + 16; the sign in bit 5
+__device__ __forceinline__ uint32_t act_code6(float q) {
+    const uint32_t m = uint32_t(fabsf(q));
+    const uint32_t c = m < 4 ? 4 * m : (m < 8 ? 2 * m + 8 : m + 16);
+    return c | (q < 0.0f ? 32u : 0u);
+}
+
+// four 6-bit codes in the bytes of x (low first) -> 24 packed bits
+__device__ __forceinline__ uint32_t pack4x6(uint32_t x) {
+    return (x & 0x3fu) | ((x >> 2) & 0xfc0u) | ((x >> 4) & 0x3f000u) | ((x >> 6) & 0xfc0000u);
 }
 
 // ---------------------------------------------------------------- bf16 / fp16 / fp8 conversions (exact, RNE)

@@ -49,6 +49,7 @@ RANK = 32
 
 
 BLOCK = 128  # rows per tile of the GEMM's blocked operands
+ROW6 = 48    # bytes of one row's 64-deep group of fp6 codes
 
 
 def padded_rows(m: int) -> int:
@@ -59,12 +60,13 @@ EPI_BF16, EPI_F32, EPI_RESIDUAL, EPI_GELU = 0, 1, 2, 3
 
 
 def act_quant_launch(x, smooth, proj_down_t, qshift=0.0, unsigned=False, *, ln=None, v_out=None):
-    """x bf16 [M, K] (rows 16-byte aligned) -> (q e4m3 codes uint8 [Mp, K] tile-blocked, shape [Mp/128, K/64, 128, 64]
-    (unblock_rows gives the [Mp, K] matrix), ascales bf16 [K/64, Mp], lora fp32 [Mp, 32] or None).
+    """x bf16 [M, K] (rows 16-byte aligned) -> (q fp6 codes of the int4 values, tile-blocked uint8
+    [Mp/128, K/64, 128, 48] (decode_acts gives the [Mp, K] integers), ascales bf16 [K/64, Mp], lora fp32 [Mp, 32]
+    or None).
     ln: dict(shift, scale, weight, bias, eps) fuses LayerNorm + modulation."""
     M, K = x.shape
     Mp = padded_rows(M)
-    q = torch.empty(Mp // BLOCK, K // 64, BLOCK, 64, device=x.device, dtype=torch.uint8)
+    q = torch.empty(Mp // BLOCK, K // 64, BLOCK, ROW6, device=x.device, dtype=torch.uint8)
     ascales = torch.empty(K // 64, Mp, device=x.device, dtype=torch.bfloat16)
     lora = None if proj_down_t is None else torch.empty(Mp, RANK, device=x.device, dtype=torch.float32)
     ln = ln or {}
@@ -76,52 +78,121 @@ def act_quant_launch(x, smooth, proj_down_t, qshift=0.0, unsigned=False, *, ln=N
     return q, ascales, lora
 
 
-def block_rows(t: torch.Tensor) -> torch.Tensor:
-    """A byte matrix [R, K] (R % 128 == 0, K % 64 == 0) in the GEMM's tile-blocked layout: [R/128, K/64, 128, 64],
-    element [r // 128, k // 64, r % 128, k % 64] = t[r, k] (a contiguous copy)."""
-    R, K = t.shape
+# ---- the GEMM's operand format (tile-blocked fp6 codes): weights w in [-8, 7] as e3m2 codes of 2w, activations
+# q in [-8, 15] as e2m3 codes of q / 2, value k of a row's 64-deep group in half k // 32 at position k % 32, the 32
+# codes of a half packed 6 bits each (24 bytes), a row's group stored as [half 0 bytes 0..15][half 1 bytes 0..15]
+# [half 0 bytes 16..23][half 1 bytes 16..23] (48 bytes), a matrix [R, K] as [R/128, K/64, 128, 48]. These torch
+# helpers state the format for callers that build or inspect operands; the product path writes it on the GPU.
+
+
+def _e3m2_value(c: int) -> float:
+    s, e, m = -1 if c & 32 else 1, (c >> 2) & 7, c & 3
+    return s * (m / 16 if e == 0 else 2.0 ** (e - 3) * (1 + m / 4))
+
+
+def _e2m3_value(c: int) -> float:
+    s, e, m = -1 if c & 32 else 1, (c >> 3) & 3, c & 7
+    return s * (m / 8 if e == 0 else 2.0 ** (e - 1) * (1 + m / 8))
+
+
+def _code_tables():
+    # value -> code for the integer range of each side, and code -> integer value (a code of no integer decodes
+    # to -128)
+    w_dec = torch.full((64,), -128, dtype=torch.int32)
+    a_dec = torch.full((64,), -128, dtype=torch.int32)
+    w_enc = torch.zeros(16, dtype=torch.int64)
+    a_enc = torch.zeros(24, dtype=torch.int64)
+    for c in range(64):
+        wv, av = _e3m2_value(c) / 2, _e2m3_value(c) * 2
+        if wv == int(wv) and -8 <= wv <= 7 and not (c == 32):
+            w_dec[c] = int(wv)
+            w_enc[int(wv) + 8] = c
+        if av == int(av) and -8 <= av <= 15 and not (c == 32):
+            a_dec[c] = int(av)
+            a_enc[int(av) + 8] = c
+    return w_enc, w_dec, a_enc, a_dec
+
+
+_W_ENC, _W_DEC, _A_ENC, _A_DEC = _code_tables()
+
+
+def _pack6(codes: torch.Tensor) -> torch.Tensor:
+    R, K = codes.shape
     if R % BLOCK or K % 64:
-        raise ValueError(f"tile-blocked operands need rows % {BLOCK} == 0 and K % 64 == 0, got {tuple(t.shape)}")
-    return t.reshape(R // BLOCK, BLOCK, K // 64, 64).permute(0, 2, 1, 3).contiguous()
+        raise ValueError(f"tile-blocked operands need rows % {BLOCK} == 0 and K % 64 == 0, got {tuple(codes.shape)}")
+    c = codes.to(torch.int64).reshape(R, K // 64, 2, 8, 4)  # row, group, half, quad, code
+    v = c[..., 0] | (c[..., 1] << 6) | (c[..., 2] << 12) | (c[..., 3] << 18)
+    b = torch.stack([v & 255, (v >> 8) & 255, v >> 16], -1).reshape(R, K // 64, 2, 24)
+    rowg = torch.cat([b[:, :, 0, :16], b[:, :, 1, :16], b[:, :, 0, 16:], b[:, :, 1, 16:]], -1)  # [R, G, 48]
+    return rowg.to(torch.uint8).reshape(R // BLOCK, BLOCK, K // 64, ROW6).permute(0, 2, 1, 3).contiguous()
 
 
-def unblock_rows(t: torch.Tensor) -> torch.Tensor:
-    """The inverse of block_rows: [R/128, K/64, 128, 64] -> the [R, K] matrix."""
-    nr, ng, b, w = t.shape
-    return t.permute(0, 2, 1, 3).reshape(nr * b, ng * w)
+def _unpack6(t: torch.Tensor) -> torch.Tensor:
+    if t.dim() != 4 or t.shape[2] != BLOCK or t.shape[3] != ROW6:
+        raise ValueError(f"tile-blocked fp6 operands have shape [R/128, K/64, 128, 48], got {tuple(t.shape)}")
+    nr, ng = t.shape[0], t.shape[1]
+    rowg = t.permute(0, 2, 1, 3).reshape(nr * BLOCK, ng, ROW6).to(torch.int64)
+    halves = torch.stack([torch.cat([rowg[..., 0:16], rowg[..., 32:40]], -1),
+                          torch.cat([rowg[..., 16:32], rowg[..., 40:48]], -1)], 2)  # [R, G, 2, 24]
+    b = halves.reshape(nr * BLOCK, ng, 2, 8, 3)
+    v = b[..., 0] | (b[..., 1] << 8) | (b[..., 2] << 16)
+    c = torch.stack([(v >> (6 * i)) & 63 for i in range(4)], -1)
+    return c.reshape(nr * BLOCK, ng * 64)
+
+
+def encode_weights(w: torch.Tensor) -> torch.Tensor:
+    """Integer weights [N, K] in [-8, 7] -> the GEMM's weight operand (tile-blocked fp6 codes)."""
+    if int(w.min()) < -8 or int(w.max()) > 7:
+        raise ValueError("int4 weights must lie in [-8, 7]")
+    return _pack6(_W_ENC.to(w.device)[(w.to(torch.int64) + 8)])
+
+
+def decode_weights(t: torch.Tensor) -> torch.Tensor:
+    """The inverse of encode_weights: [N/128, K/64, 128, 48] -> int32 [N, K]."""
+    return _W_DEC.to(t.device)[_unpack6(t)]
+
+
+def encode_acts(q: torch.Tensor) -> torch.Tensor:
+    """Integer activations [Mp, K] in [-8, 15] -> the GEMM's activation operand (tile-blocked fp6 codes)."""
+    if int(q.min()) < -8 or int(q.max()) > 15:
+        raise ValueError("int4 activations must lie in [-8, 15]")
+    return _pack6(_A_ENC.to(q.device)[(q.to(torch.int64) + 8)])
+
+
+def decode_acts(t: torch.Tensor) -> torch.Tensor:
+    """The inverse of encode_acts: [Mp/128, K/64, 128, 48] -> int32 [Mp, K]."""
+    return _A_DEC.to(t.device)[_unpack6(t)]
 
 
 def weight_codes(qweight: torch.Tensor) -> torch.Tensor:
-    """Packed int4 weights uint8 [N, K/2] -> the GEMM's operand, e4m3 codes of the same integers, tile-blocked
-    uint8 [N/128, K/64, 128, 64]."""
+    """Packed int4 weights uint8 [N, K/2] -> the GEMM's weight operand, tile-blocked fp6 codes of the same integers,
+    uint8 [N/128, K/64, 128, 48] (on the GPU)."""
     N, half = qweight.shape
     if N % BLOCK:
         raise ValueError(f"W4A4 weights need out_features % {BLOCK} == 0, got {N}")
-    codes = torch.empty(N // BLOCK, 2 * half // 64, BLOCK, 64, device=qweight.device, dtype=torch.uint8)
+    codes = torch.empty(N // BLOCK, 2 * half // 64, BLOCK, ROW6, device=qweight.device, dtype=torch.uint8)
     _lib.call("wdl_w4a4_weight_codes", ptr(qweight.contiguous()), N, 2 * half, ptr(codes), stream_of(qweight))
     return codes
 
 
 def as_codes(qweight: torch.Tensor, K: int) -> torch.Tensor:
-    """The weight operand for input width K: tile-blocked codes [N/128, K/64, 128, 64] pass through, packed [N, K/2]
-    nibbles are expanded and [N, K] codes blocked (once per call)."""
+    """The weight operand for input width K: tile-blocked fp6 codes [N/128, K/64, 128, 48] pass through, packed
+    [N, K/2] nibbles are expanded (once per call)."""
     if qweight.dtype not in (torch.uint8, torch.int8) or qweight.dim() not in (2, 4):
         raise TypeError(f"qweight must be a uint8 tensor of 2 or 4 dims, got {qweight.dtype} {tuple(qweight.shape)}")
     if qweight.dim() == 4:
-        if tuple(qweight.shape[1:]) != (K // 64, BLOCK, 64) or K % 64:
+        if tuple(qweight.shape[1:]) != (K // 64, BLOCK, ROW6) or K % 64:
             raise ValueError(f"blocked weight codes {tuple(qweight.shape)} do not match input width {K}")
         return qweight.view(torch.uint8)
-    if qweight.shape[1] == K:
-        return block_rows(qweight.view(torch.uint8))
     if 2 * qweight.shape[1] == K:
         return weight_codes(qweight.view(torch.uint8))
-    raise ValueError(f"qweight {tuple(qweight.shape)} fits neither [N, {K}] codes nor [N, {K // 2}] nibbles")
+    raise ValueError(f"qweight {tuple(qweight.shape)} fits neither blocked codes nor [N, {K // 2}] nibbles")
 
 
 def gemm_launch(q, ascales, lora, wcodes, wscales, proj_up, bias, M, out, epilogue=EPI_BF16, gate=None):
-    """W4A4 GEMM on the quantizer's outputs (q, ascales, lora) and tile-blocked e4m3 weight codes (weight_codes)."""
-    if q.dim() != 4 or wcodes.dim() != 4:
-        raise ValueError("the W4A4 GEMM takes tile-blocked operands [rows/128, K/64, 128, 64]")
+    """W4A4 GEMM on the quantizer's outputs (q, ascales, lora) and tile-blocked fp6 weight codes (weight_codes)."""
+    if q.dim() != 4 or wcodes.dim() != 4 or q.shape[2:] != (BLOCK, ROW6) or wcodes.shape[2:] != (BLOCK, ROW6):
+        raise ValueError("the W4A4 GEMM takes tile-blocked fp6 operands [rows/128, K/64, 128, 48]")
     Mp, K = q.shape[0] * BLOCK, q.shape[1] * 64
     N = wcodes.shape[0] * BLOCK
     if wcodes.shape[1] != q.shape[1]:
@@ -141,12 +212,12 @@ def act_quant_w4(x: torch.Tensor, smooth: torch.Tensor, proj_down: torch.Tensor,
 def _(x, smooth, proj_down, qshift, unsigned):
     M, K = x.shape
     Mp = padded_rows(M)
-    return (x.new_empty(Mp // BLOCK, K // 64, BLOCK, 64, dtype=torch.uint8),
+    return (x.new_empty(Mp // BLOCK, K // 64, BLOCK, ROW6, dtype=torch.uint8),
             x.new_empty(K // 64, Mp, dtype=torch.bfloat16), x.new_empty(Mp, RANK, dtype=torch.float32))
 
 
 def out_features(qweight: torch.Tensor) -> int:
-    """N of a weight operand: packed [N, K/2] nibbles, [N, K] codes or tile-blocked [N/128, K/64, 128, 64] codes."""
+    """N of a weight operand: packed [N, K/2] nibbles or tile-blocked [N/128, K/64, 128, 48] codes."""
     return qweight.shape[0] * (BLOCK if qweight.dim() == 4 else 1)
 
 
