@@ -78,9 +78,13 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
     asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds) : "memory");
 }
-// 64 lanes x 4 bytes to LDS [m0, m0 + 256)
-__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
-    asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds) : "memory");
+// The same from a wave-uniform base (scalar registers) plus a 32-bit per-lane offset: the address arithmetic of a
+// load stays on the scalar unit
+__device__ __forceinline__ void dma16s(const void* base, uint32_t voff, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void dma4s(const void* base, uint32_t voff, uint32_t lds) {
+    asm volatile("global_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds) : "memory");
 }
 
 // s_waitcnt vmcnt(n) only (expcnt and lgkmcnt left at their maxima)
@@ -247,23 +251,30 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
     if (total % 8 == 0) tile = (pid % 8) * (total / 8) + pid / 8;
     const int64_t n0 = (tile / ntm) * BN, m0 = (tile % ntm) * BM;
     const int64_t K = p.K, G = K / 64;
+    const int GI = int(G);  // groups (K < 2^31 is checked by the launcher)
 
     // zero tails of the scale stages (written once; the loads never touch them)
     if constexpr (W4)
         if (t < STAGES * 16) *reinterpret_cast<uint32_t*>(&sS[t / 16][SD + (t % 16) * 4]) = 0u;
 
-    // this lane's sources for group 0; group g adds g BLOCK6 bytes (W4 codes), 64 g bytes (FP8 codes) or g times
-    // the scale row stride
-    const uint8_t* xsrc[W4 ? N16 + N4 : XI];
+    // W4: the stage is cut into 1 KB chunks (16-byte loads) and then 256-byte chunks (4-byte loads); wave w takes
+    // 1 KB chunks w N16 .. and 256-byte chunks w N4 ... Each chunk lies inside one operand's 6 KB block (block
+    // and operand boundaries are multiples of 1 KB), so a load reads from a wave-uniform base (scalar registers:
+    // operand, tile row block, chunk; group g adds g BLOCK6) plus lane * 16 or lane * 4. The scale chunk of wave w
+    // is bytes 256 w .. of [ws[BN] | as[BM] | padding], also uniform per wave (2 BN and 2 BM are multiples of 256).
+    // FP8: this lane's sources for group 0; group g adds 64 g bytes.
+    const uint8_t* cbase[W4 ? N16 + N4 : 1];
+    int cdst[W4 ? N16 + N4 : 1];
+    const uint8_t* xsrc[W4 ? 1 : XI];
     const uint8_t* wsrc[W4 ? 1 : WI];
     if constexpr (W4) {
 #pragma unroll
         for (int u = 0; u < N16 + N4; ++u) {
-            // stage byte o: weight rows [0, BN), then activation rows; each 128-row tile is one 6 KB block
-            const int o = wave * CB + (u < N16 ? u * 1024 + lane * 16 : N16 * 1024 + (u - N16) * 256 + lane * 4);
-            xsrc[u] = o < BN * ROW6 ? p.wc + (n0 / BLOCK_ROWS + o / BLOCK6) * G * BLOCK6 + o % BLOCK6
-                                    : p.qa + (m0 / BLOCK_ROWS + (o - BN * ROW6) / BLOCK6) * G * BLOCK6 +
-                                          (o - BN * ROW6) % BLOCK6;
+            const int o = u < N16 ? (wave * N16 + u) * 1024 : NW * N16 * 1024 + (wave * N4 + u - N16) * 256;
+            cdst[u] = o;
+            cbase[u] = o < BN * ROW6 ? p.wc + (n0 / BLOCK_ROWS + o / BLOCK6) * G * BLOCK6 + o % BLOCK6
+                                     : p.qa + (m0 / BLOCK_ROWS + (o - BN * ROW6) / BLOCK6) * G * BLOCK6 +
+                                           (o - BN * ROW6) % BLOCK6;
         }
     } else {
 #pragma unroll
@@ -279,33 +290,33 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
             wsrc[j] = p.wc + (n0 + row) * K + quarter * 16;
         }
     }
-    const uint8_t* ssrc;   // 4 bytes: ws pair, as pair or (padding lanes) a valid dummy
+    const uint8_t* sbase;   // the wave's 256 scale bytes of group 0: ws, as or (padding waves) a valid dummy
     int64_t sstride;
     {
-        const int b = 4 * (wave * 64 + lane);
+        const int b = 256 * wave;
         if (b < 2 * BN) {
-            ssrc = reinterpret_cast<const uint8_t*>(p.ws + n0) + b;
+            sbase = reinterpret_cast<const uint8_t*>(p.ws + n0) + b;
             sstride = 2 * p.N;
         } else if (b < 2 * (BN + BM)) {
-            ssrc = reinterpret_cast<const uint8_t*>(p.as + m0) + (b - 2 * BN);
+            sbase = reinterpret_cast<const uint8_t*>(p.as + m0) + (b - 2 * BN);
             sstride = 2 * p.Mp;
         } else {
-            ssrc = reinterpret_cast<const uint8_t*>(p.ws + n0);
+            sbase = reinterpret_cast<const uint8_t*>(p.ws + n0);
             sstride = 0;
         }
     }
+    const uint32_t off16 = uint32_t(lane) * 16, off4 = uint32_t(lane) * 4;
 
     // direct load u (0 .. LPG - 1) of group g (clamped to the last group) into stage st
-    auto issue_one = [&](int st, int64_t g, int u) {
-        const int64_t gg = g < G ? g : G - 1;
+    auto issue_one = [&](int st, int g, int u) {
+        const int gg = g < GI ? g : GI - 1;
         if constexpr (W4) {
-            if (u < N16) dma16(xsrc[u] + gg * BLOCK6, lds_addr(&sC[st][wave * CB + u * 1024]));
-            else if (u < N16 + N4)
-                dma4(xsrc[u] + gg * BLOCK6, lds_addr(&sC[st][wave * CB + N16 * 1024 + (u - N16) * 256]));
-            else dma4(ssrc + gg * sstride, lds_addr(&sS[st][wave * 256]));
+            if (u < N16) dma16s(cbase[u] + int64_t(gg) * BLOCK6, off16, lds_addr(&sC[st][cdst[u]]));
+            else if (u < N16 + N4) dma4s(cbase[u] + int64_t(gg) * BLOCK6, off4, lds_addr(&sC[st][cdst[u]]));
+            else dma4s(sbase + gg * sstride, off4, lds_addr(&sS[st][wave * 256]));
         } else {
-            if (u < XI) dma16(xsrc[u] + gg * 64, lds_addr(&sX[st][(wave * XI + u) * 1024]));
-            else dma16(wsrc[u - XI] + gg * 64, lds_addr(&sW[st][(wave * WI + u - XI) * 1024]));
+            if (u < XI) dma16(xsrc[u] + int64_t(gg) * 64, lds_addr(&sX[st][(wave * XI + u) * 1024]));
+            else dma16(wsrc[u - XI] + int64_t(gg) * 64, lds_addr(&sW[st][(wave * WI + u - XI) * 1024]));
         }
     };
 
@@ -345,10 +356,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         for (int j = 0; j < TM; ++j) acc[i][j] = f32x16{};
     const f32x16 zero = {};
 
-    // one group's operands in registers: weight / activation code fragments (W4: 6 dwords of fp6 codes, FP8: 8 of
-    // e4m3) and (W4) the bf16 scale of each fragment row, zero-extended (lanes 32..63 read the zero tail)
-    i32x8 fa[TN], fb[TM];
-    uint32_t fsa[TN], fsb[TM];
+    // Two register sets of one group's operands: weight / activation code fragments (W4: 6 dwords of fp6 codes,
+    // FP8: 8 of e4m3) and (W4) the bf16 scale of each fragment row, zero-extended (lanes 32..63 read the zero tail).
+    // Group h is multiplied from set h % 2 while group h + 1 is read into the other set.
+    i32x8 fa[2][TN], fb[2][TM];
+    uint32_t fsa[2][TN], fsb[2][TM];
     auto load_frag = [&](const uint8_t* r) {
         if constexpr (W4) {
             const uint4 x = *reinterpret_cast<const uint4*>(r + q0);
@@ -359,76 +371,86 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
             return i32x8{int(x.x), int(x.y), int(x.z), int(x.w), int(y.x), int(y.y), int(y.z), int(y.w)};
         }
     };
-    auto load_a = [&](int st, int i) {
+    auto load_a = [&](int set, int st, int i) {
         if constexpr (W4) {
-            fa[i] = load_frag(&sC[st][aoff[i]]);
-            fsa[i] = *reinterpret_cast<const uint16_t*>(&sS[st][soa[i]]);
+            fa[set][i] = load_frag(&sC[st][aoff[i]]);
+            fsa[set][i] = *reinterpret_cast<const uint16_t*>(&sS[st][soa[i]]);
         } else {
-            fa[i] = load_frag(&sW[st][aoff[i]]);
+            fa[set][i] = load_frag(&sW[st][aoff[i]]);
         }
     };
-    auto load_b = [&](int st, int j) {
+    auto load_b = [&](int set, int st, int j) {
         if constexpr (W4) {
-            fb[j] = load_frag(&sC[st][boff[j]]);
-            fsb[j] = *reinterpret_cast<const uint16_t*>(&sS[st][sob[j]]);
+            fb[set][j] = load_frag(&sC[st][boff[j]]);
+            fsb[set][j] = *reinterpret_cast<const uint16_t*>(&sS[st][sob[j]]);
         } else {
-            fb[j] = load_frag(&sX[st][boff[j]]);
+            fb[set][j] = load_frag(&sX[st][boff[j]]);
         }
+    };
+    // fragment r of the next group (r < TN: weight rows i = r, else activation rows j = r - TN)
+    auto load_next = [&](int set, int st, int r) {
+        if (r < TN) load_a(set, st, r);
+        else load_b(set, st, r - TN);
     };
 
-    // Multiply one group from the fragment registers; each fragment is reloaded with the next group's operands
-    // (stage nst) right after its last use, so the reads overlap the remaining MFMAs and one register set serves.
+    // Multiply one group from register set cur while the next group's operands (stage nst) are read into the other
+    // set, TN + TM fragments spread over the TN x TM subtiles: the reads have a whole step to land, so LDS latency
+    // stays off the MFMA chain.
     // W4: the fold is software-pipelined by one subtile: the products of subtile s are folded while the MFMAs of
     // subtile s + 1 run (the last subtile of a group while the first subtile of the next group runs). pI / pP hold
     // the pending subtile; they start at zero (the first fold adds 0 * 0 to a zero accumulator: no change).
     f32x16 pI = zero, pP = zero;
     // The step's LPG direct loads (group ig into stage ist) are spread over its subtiles, one or two after each
     // subtile's MFMAs, so a wave never waits on a full load queue with MFMA work still to issue.
-    auto step = [&](int nst, int ist, int64_t ig) {
+    constexpr int NF = TN + TM, NS = TN * TM;
+    auto step = [&](int cur, int nst, int ist, int ig) {
 #pragma unroll
-        for (int s = 0; s < TN * TM; ++s) {
+        for (int s = 0; s < NS; ++s) {
             const int i = s / TM, j = s % TM;
             if constexpr (W4) {
                 const int pi = s == 0 ? TN - 1 : (s - 1) / TM, pj = s == 0 ? TM - 1 : (s - 1) % TM;
-                const i16x4 oa = __builtin_bit_cast(i16x4, make_uint2(fsa[i], 0u));
-                const i16x4 ob = __builtin_bit_cast(i16x4, make_uint2(fsb[j], 0u));
+                const i16x4 oa = __builtin_bit_cast(i16x4, make_uint2(fsa[cur][i], 0u));
+                const i16x4 ob = __builtin_bit_cast(i16x4, make_uint2(fsb[cur][j], 0u));
                 // A: weights as e3m2 (format 3), B: activations as e2m3 (format 2)
-                const f32x16 I = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[i], fb[j], zero, 3, 2, 0, 0, 0, 0);
+                const f32x16 I =
+                    __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[cur][i], fb[cur][j], zero, 3, 2, 0, 0, 0, 0);
                 const f32x16 P = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(oa, ob, zero, 0, 0, 0);
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[pi][pj][e] = fmaf(pI[e], pP[e], acc[pi][pj][e]);
                 pI = I;
                 pP = P;
             } else {
-                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[i], fb[j], acc[i][j], 0, 0, 0, 0, 0, 0);
+                acc[i][j] =
+                    __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0, 0, 0, 0);
             }
-            if (j == TM - 1) load_a(nst, i);
-            if (i == TN - 1) load_b(nst, j);
+#pragma unroll
+            for (int r = s * NF / NS; r < (s + 1) * NF / NS; ++r) load_next(1 - cur, nst, r);
             // one wave issues in order and an MFMA waits at issue while the matrix core is busy, so the fold of
             // subtile s - 1 is split around the two MFMAs of subtile s: it executes while they run
             if constexpr (W4) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // I_s (32 cycles)
+                __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);   // reads of the next group
                 __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // fold of s - 1, first part
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // P_s (32 cycles)
                 __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // the rest
-                __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);   // the reloads subtile s freed
             } else {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
             }
 #pragma unroll
-            for (int u = s * LPG / (TN * TM); u < (s + 1) * LPG / (TN * TM); ++u) issue_one(ist, ig, u);
+            for (int u = s * LPG / NS; u < (s + 1) * LPG / NS; ++u) issue_one(ist, ig, u);
         }
     };
 
     // Ring, one group per step. Step h: this wave's loads of group h + 1 have landed (the STAGES - 3 groups after
-    // it may still be in flight); after the barrier the same holds for every wave. The stage of group h - 1 is
-    // free: every wave read it into registers during step h - 2 and used them in step h - 1, so no wait on LDS
-    // reads comes before the barrier. Group h + STAGES - 1 goes into it (clamped to the last group, so every step
-    // issues the same loads and vmcnt counts stay exact). Then group h is multiplied from the registers while the
-    // reads of group h + 1 refill them. Whole turns of the ring are unrolled (constant stages); the remaining
-    // G % STAGES steps run with the stage computed at run time.
-    static_assert(STAGES >= 4, "the ring keeps one stage being read, one free and two or more in flight");
+    // it may still be in flight); after the barrier the same holds for every wave, and group h + 1 is read into
+    // registers during the step. The stage of group h - 1 is free: every wave read it during step h - 2 and used
+    // the registers in step h - 1, so no wait on LDS reads comes before the barrier. Group h + STAGES - 1 goes into
+    // it (clamped to the last group, so every step issues the same loads and vmcnt counts stay exact). Stages and
+    // register sets are compile-time constants throughout: whole turns of the ring are unrolled, and so are the
+    // G % STAGES remaining steps (each under a uniform branch); STAGES is even, so group h uses set h % 2.
+    static_assert(STAGES >= 4 && STAGES % 2 == 0, "the ring keeps one stage being read, one free and two or more in "
+                                                  "flight; register sets alternate over a turn");
 #pragma unroll
     for (int k = 0; k < STAGES - 1; ++k)
 #pragma unroll
@@ -436,20 +458,20 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
     wait_vmcnt<(STAGES - 2) * LPG>();
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < TN; ++i) load_a(0, i);
-#pragma unroll
-    for (int j = 0; j < TM; ++j) load_b(0, j);
-    auto ring_step = [&](int k, int64_t h) {
+    for (int r = 0; r < NF; ++r) load_next(0, 0, r);
+    auto ring_step = [&](int k, int h) {
         wait_vmcnt<(STAGES - 3) * LPG>();
         __syncthreads();
-        step(k + 1 == STAGES ? 0 : k + 1, k == 0 ? STAGES - 1 : k - 1, h + STAGES - 1);
+        step(k % 2, k + 1 == STAGES ? 0 : k + 1, k == 0 ? STAGES - 1 : k - 1, h + STAGES - 1);
     };
-    int64_t g = 0;
-    for (; g + STAGES <= G; g += STAGES) {
+    int g = 0;  // wave-uniform: kept in scalar registers
+    for (; g + STAGES <= GI; g = __builtin_amdgcn_readfirstlane(g + STAGES)) {
 #pragma unroll
         for (int k = 0; k < STAGES; ++k) ring_step(k, g + k);
     }
-    for (int k = 0; g < G; ++g, ++k) ring_step(k, g);
+#pragma unroll
+    for (int k = 0; k < STAGES - 1; ++k)
+        if (g + k < GI) ring_step(k, g + k);
     if constexpr (W4) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[TN - 1][TM - 1][e] = fmaf(pI[e], pP[e], acc[TN - 1][TM - 1][e]);
@@ -558,7 +580,8 @@ extern "C" int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wc
                              const float* lora, const void* proj_up, const void* bias, int64_t M, int64_t Mp,
                              int64_t N, int64_t K, int64_t rank, void* out, int64_t ldo, int epilogue,
                              const float* gate, hipStream_t stream) {
-    if (M < 0 || Mp < M || Mp % 128 || N <= 0 || N % 128 || K <= 0 || K % 64 || ldo < N || ldo % 4)
+    if (M < 0 || Mp < M || Mp % 128 || N <= 0 || N % 128 || K <= 0 || K % 64 || K > (int64_t(1) << 30) || ldo < N ||
+        ldo % 4)
         return fail(WDL_EINVAL, "w4a4_gemm: bad shape M=%lld Mp=%lld N=%lld K=%lld ldo=%lld", (long long)M,
                     (long long)Mp, (long long)N, (long long)K, (long long)ldo);
     if (lora && (rank != 32 || !proj_up)) return fail(WDL_EINVAL, "w4a4_gemm: low-rank branch needs rank 32");
@@ -596,7 +619,8 @@ extern "C" int wdl_w4a4_weight_codes(const void* qweight, int64_t N, int64_t K, 
 extern "C" int wdl_fp8_gemm(const void* xq, const float* x_scale, const void* wq, const float* w_scale,
                             const void* bias, int64_t M, int64_t Mp, int64_t N, int64_t K, int rows, void* out,
                             int64_t ldo, hipStream_t stream) {
-    if (M < 0 || Mp < M || Mp % 128 || N <= 0 || N % 128 || K <= 0 || K % 64 || ldo < N || ldo % 4)
+    if (M < 0 || Mp < M || Mp % 128 || N <= 0 || N % 128 || K <= 0 || K % 64 || K > (int64_t(1) << 30) || ldo < N ||
+        ldo % 4)
         return fail(WDL_EINVAL, "fp8_gemm: bad shape M=%lld Mp=%lld N=%lld K=%lld ldo=%lld", (long long)M,
                     (long long)Mp, (long long)N, (long long)K, (long long)ldo);
     if (!xq || !x_scale || !wq || !w_scale || !out) return fail(WDL_EINVAL, "fp8_gemm: null pointer");
