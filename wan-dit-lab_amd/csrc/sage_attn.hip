@@ -70,9 +70,10 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return uint32_t(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
 }
 
-// 64 lanes x 16 bytes from per-lane global addresses to LDS [m0, m0 + 1024)
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
-    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds) : "memory");
+// 64 lanes x 16 bytes from a wave-uniform base (scalar registers) plus a 32-bit per-lane offset to LDS
+// [m0, m0 + 1024): the address arithmetic of a load stays on the scalar unit
+__device__ __forceinline__ void dma16s(const void* base, uint32_t voff, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds) : "memory");
 }
 
 template <int N>
@@ -161,39 +162,42 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
         // full key blocks of the segment [b0, fe), split in halves between the groups; both groups run `iters`
         // ring steps. A ragged final block (L % 64 != 0) in the segment is group 1's, in a masked step after it.
         const bool ragged_here = ragged && b1 == nblk;
-        const int64_t fe = ragged_here ? nblk - 1 : b1;
-        const int64_t nfull = fe - b0, nb0 = (nfull + 1) / 2;
-        const int64_t first = grp == 0 ? b0 : b0 + nb0, count = grp == 0 ? nb0 : nfull - nb0;
-        const int64_t last = count > 0 ? first + count - 1 : b0;
-        const int64_t iters = nb0;
+        // (32-bit ring counters: uniform 64-bit compares would run on the vector unit; blocks < 2^9)
+        const int fe = int(ragged_here ? nblk - 1 : b1), ib0 = int(b0);
+        const int nfull = fe - ib0, nb0 = (nfull + 1) / 2;
+        const int first = grp == 0 ? ib0 : ib0 + nb0, count = grp == 0 ? nb0 : nfull - nb0;
+        const int last = count > 0 ? first + count - 1 : ib0;
+        const int iters = nb0;
 
-        // this lane's load slots (block 0); block b adds b * 64 * D bytes of K, b * 64 bytes of V
+        // this lane's load offsets inside a block (block b of the head starts at kbase + 64 D b for K, at
+        // vbase + 64 b for V: wave-uniform bases)
         const int8_t* kbase = a.k + h * a.Lpad * D;
         const uint8_t* vbase = a.v + h * D * a.Lpad;
-        const int8_t* ksrc[2];
-        const uint8_t* vsrc[2];
+        uint32_t koff[2], voff[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int slot = (sub * 2 + j) * 64 + lane;  // 16-byte slot of the group's 8 KB K or V block
             {
                 const int dh = slot / 256, s2 = slot % 256, key = s2 / 4;
                 const int lq = (s2 % 4) ^ ((key >> 2) & 3);
-                ksrc[j] = kbase + key * D + dh * 64 + lq * 16;
+                koff[j] = uint32_t(key * D + dh * 64 + lq * 16);
             }
             {
                 const int ch = slot / 4, lq = (slot % 4) ^ ((ch >> 2) & 3);
-                vsrc[j] = vbase + int64_t(ch) * a.Lpad + lq * 16;
+                voff[j] = uint32_t(ch * a.Lpad + lq * 16);  // 128 Lpad < 2^32 (checked by the launcher)
             }
         }
-        auto load_block = [&](int st, int64_t blk) {  // block blk of this group's keys into stage st
+        auto load_block = [&](int st, int blk) {  // block blk of this group's keys into stage st
             uint8_t* base = smem + st * STAGE + grp * GSTAGE;
+            const int8_t* kb = kbase + blk * 64 * D;
+            const uint8_t* vb = vbase + blk * 64;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) dma16(ksrc[j] + blk * 64 * D, lds_addr(base + (sub * 2 + j) * 1024));
+            for (int j = 0; j < 2; ++j) dma16s(kb, koff[j], lds_addr(base + (sub * 2 + j) * 1024));
 #pragma unroll
-            for (int j = 0; j < 2; ++j) dma16(vsrc[j] + blk * 64, lds_addr(base + KT + (sub * 2 + j) * 1024));
+            for (int j = 0; j < 2; ++j) dma16s(vb, voff[j], lds_addr(base + KT + (sub * 2 + j) * 1024));
         };
-        auto issue = [&](int st, int64_t i) {  // ring step i's block (clamped to the group's last) into stage st
-            const int64_t blk = first + i;
+        auto issue = [&](int st, int i) {  // ring step i's block (clamped to the group's last) into stage st
+            const int blk = first + i;
             load_block(st, blk < last ? blk : last);
         };
 
@@ -203,7 +207,7 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
         float m = -INFINITY, l = 0.0f;
 
         // mask_tag: std::true_type for the final block of a ragged L (keys >= L get P = 0), else std::false_type
-        auto compute = [&](int st, int64_t blk, auto mask_tag) {
+        auto compute = [&](int st, int blk, auto mask_tag) {
             constexpr bool MASK = decltype(mask_tag)::value;
             const uint8_t* K = smem + st * STAGE + grp * GSTAGE;
             const uint8_t* V = K + KT;
@@ -248,7 +252,7 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
             const float alpha = __builtin_amdgcn_exp2f(m - mn);
             const float bias = LOG2_448 - mn;
             float ls = 0.0f;
-            uint32_t pw[8];
+            i32x8 pf;
 #pragma unroll
             for (int wd = 0; wd < 8; ++wd) {
                 const int j = wd / 4;
@@ -261,8 +265,10 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
                     if (MASK && acc[j][r] == INT32_MIN) p[e] = 0.0f;
                     ls = ls + p[e];
                 }
-                uint32_t word = __builtin_amdgcn_cvt_pk_fp8_f32(p[0], p[1], 0, false);
-                pw[wd] = __builtin_amdgcn_cvt_pk_fp8_f32(p[2], p[3], word, true);
+                // the low pair's conversion keeps the upper half of its old operand, which the high pair's then
+                // replaces: any register serves as the old value (p[0]'s bits: no zero to materialise)
+                const uint32_t word = __builtin_amdgcn_cvt_pk_fp8_f32(p[0], p[1], __float_as_int(p[0]), false);
+                pf[wd] = int(__builtin_amdgcn_cvt_pk_fp8_f32(p[2], p[3], word, true));
             }
             l = l * alpha + ls;
             m = mn;
@@ -272,8 +278,6 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
 #pragma unroll
                     for (int e = 0; e < 16; ++e) o[ds][e] *= alpha;
             }
-            const i32x8 pf = {int(pw[0]), int(pw[1]), int(pw[2]), int(pw[3]),
-                              int(pw[4]), int(pw[5]), int(pw[6]), int(pw[7])};
 #pragma unroll
             for (int ds = 0; ds < 4; ++ds) {
                 const uint8_t* src = V + ds * 2048 + rowoff;
@@ -285,10 +289,10 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
 
 #pragma unroll
         for (int k = 0; k < STAGES - 1; ++k) issue(k, k);
-        for (int64_t i0 = 0; i0 < iters; i0 += STAGES) {
+        for (int i0 = 0; i0 < iters; i0 += STAGES) {
 #pragma unroll
             for (int k = 0; k < STAGES; ++k) {
-                const int64_t i = i0 + k;
+                const int i = i0 + k;
                 if (i >= iters) break;
                 wait_vmcnt<(STAGES - 2) * LPB>();
                 __syncthreads();
