@@ -216,6 +216,121 @@ __device__ __forceinline__ void finish_tile(const GemmArgs& p, f32x16 (&acc)[TN]
         }
 }
 
+// Staged epilogue of the W4A4 GEMM's bf16 outputs (bf16, GELU, gated residual) for a wave's 64 x 64 subtiles.
+// The low-rank term, bias and GELU are applied in the MFMA layout (lane = token), the bf16 results go through the
+// wave's LDS area, and the output is then read and written token-major: lane l owns features 8 (l % 8) .. + 7 of
+// tokens 8 k + l / 8 (k = 0..7), so 8 lanes cover one token's 128 contiguous bytes and every global access is 16
+// bytes per lane (in the MFMA layout a store touches 32 rows in 8-byte pieces). The residual rows and the gate
+// are loaded first, with the low-rank operands, so their latency overlaps the low-rank MFMAs and the staging.
+// Arithmetic as in finish_tile.
+constexpr int STG = 64 + 4;  // staged row: 64 bf16 + 4 pad (136 bytes: conflict-free 8-byte writes of 32 rows)
+template <int TN, int TM, int EPI>
+__device__ __forceinline__ void finish_tile_rows(const GemmArgs& p, f32x16 (&acc)[TN][TM], int64_t nb0, int64_t mb0,
+                                                 int lane, uint16_t* stage) {
+    static_assert(TN == 2 && TM == 2, "64 x 64 per wave");
+    static_assert(EPI == EPI_BF16 || EPI == EPI_RESIDUAL || EPI == EPI_GELU, "bf16 outputs");
+    const int half = lane / 32;
+    const int rc = lane % 8;  // token-major phase: feature chunk
+    // ---- loads
+    bf16x8 pa[TN][2];
+    float4 lr[TM][2][2];
+    if (p.lora) {
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                pa[i][h] = *reinterpret_cast<const bf16x8*>(p.pu + (nb0 + i * 32 + lane % 32) * 32 + h * 16 + 8 * half);
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float* l = p.lora + (mb0 + j * 32 + lane % 32) * 32 + h * 16 + 8 * half;
+                lr[j][h][0] = *reinterpret_cast<const float4*>(l);
+                lr[j][h][1] = *reinterpret_cast<const float4*>(l + 4);
+            }
+    }
+    uint2 bias[TN][4];
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            bias[i][q] = p.bias ? *reinterpret_cast<const uint2*>(p.bias + nb0 + i * 32 + 8 * q + 4 * half)
+                                : make_uint2(0u, 0u);
+    float4 gate[2];
+    uint4 old[8];
+    if (EPI == EPI_RESIDUAL) {
+        gate[0] = *reinterpret_cast<const float4*>(p.gate + nb0 + 8 * rc);
+        gate[1] = *reinterpret_cast<const float4*>(p.gate + nb0 + 8 * rc + 4);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int64_t m = mb0 + 8 * k + lane / 8;
+            const int64_t mm = m < p.M ? m : 0;  // rows past M read row 0 and are not stored
+            old[k] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.out) + mm * p.ldo + nb0 + 8 * rc);
+        }
+    }
+
+    // ---- low-rank branch: acc += pu[n] . bf16(lora[m]) over r = 0..31, two 32x32x16 bf16 MFMAs per subtile
+    if (p.lora) {
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                bf16x8 lb;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    lb[e] = __builtin_bit_cast(__bf16, f32_to_bf16(lr[j][h][0][e]));
+                    lb[4 + e] = __builtin_bit_cast(__bf16, f32_to_bf16(lr[j][h][1][e]));
+                }
+#pragma unroll
+                for (int i = 0; i < TN; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[i][h], lb, acc[i][j], 0, 0, 0);
+            }
+    }
+
+    // ---- bias, activation, bf16, into the staging rows (token j * 32 + lane % 32, feature i * 32 + 8 q + 4 half)
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint16_t bv[4] = {uint16_t(bias[i][q].x), uint16_t(bias[i][q].x >> 16), uint16_t(bias[i][q].y),
+                                        uint16_t(bias[i][q].y >> 16)};
+                uint16_t r[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float y = acc[i][j][4 * q + e];
+                    if (p.bias) y = y + bf16_to_f32(bv[e]);
+                    r[e] = f32_to_bf16(EPI == EPI_GELU ? gelu_tanh(y) : y);
+                }
+                *reinterpret_cast<uint2*>(stage + (j * 32 + lane % 32) * STG + i * 32 + 8 * q + 4 * half) =
+                    make_uint2(r[0] | (uint32_t(r[1]) << 16), r[2] | (uint32_t(r[3]) << 16));
+            }
+    asm volatile("" ::: "memory");  // the staging writes stay ahead of the reads (one wave: LDS keeps its order)
+
+    // ---- token-major: out[m][nb0 + 8 rc ..] for m = mb0 + 8 k + lane / 8
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int ml = 8 * k + lane / 8;
+        const int64_t m = mb0 + ml;
+        const uint16_t* sr = stage + ml * STG + 8 * rc;
+        const uint2 a0 = *reinterpret_cast<const uint2*>(sr), a1 = *reinterpret_cast<const uint2*>(sr + 4);
+        uint4 w = make_uint4(a0.x, a0.y, a1.x, a1.y);
+        if (EPI == EPI_RESIDUAL) {
+            const uint32_t yw[4] = {w.x, w.y, w.z, w.w}, ow[4] = {old[k].x, old[k].y, old[k].z, old[k].w};
+            const float g[8] = {gate[0].x, gate[0].y, gate[0].z, gate[0].w, gate[1].x, gate[1].y, gate[1].z, gate[1].w};
+            uint32_t rw[4];
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const float y0 = bf16_to_f32(uint16_t(yw[d])), y1 = bf16_to_f32(uint16_t(yw[d] >> 16));
+                const float o0 = bf16_to_f32(uint16_t(ow[d])), o1 = bf16_to_f32(uint16_t(ow[d] >> 16));
+                rw[d] = f32_to_bf16(o0 + y0 * g[2 * d]) | (uint32_t(f32_to_bf16(o1 + y1 * g[2 * d + 1])) << 16);
+            }
+            w = make_uint4(rw[0], rw[1], rw[2], rw[3]);
+        }
+        if (m < p.M) *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.out) + m * p.ldo + nb0 + 8 * rc) = w;
+    }
+}
+
 // The main loop of both GEMMs. W4: the W4A4 product (fp6 tile-blocked codes, per-group scale fold, scales
 // streamed with the codes); otherwise the FP8 product (e4m3 row-major codes only, one fp32 accumulation over all
 // of K in the MFMA accumulator).
@@ -478,7 +593,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
     }
     wait_vmcnt<0>();  // the clamped tail loads land before the workgroup can end
 
-    finish_tile<TN, TM, EPI>(p, acc, n0 + wn * WN, m0 + wm * WM, lane);
+    if constexpr (W4 && EPI != EPI_F32) {
+        __syncthreads();  // every wave is past its last read of the ring, whose LDS the staging reuses
+        static_assert(NW * 64 * STG * 2 <= STAGES * CS, "staging fits in the ring");
+        finish_tile_rows<TN, TM, EPI>(p, acc, n0 + wn * WN, m0 + wm * WM, lane,
+                                      reinterpret_cast<uint16_t*>(&sC[0][0]) + wave * 64 * STG);
+    } else {
+        finish_tile<TN, TM, EPI>(p, acc, n0 + wn * WN, m0 + wm * WM, lane);
+    }
 }
 
 template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES>
@@ -591,9 +713,10 @@ extern "C" int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wc
         return fail(WDL_EINVAL, "w4a4_gemm: operands must be 16-byte (codes) / 4-byte (scales) aligned");
     if (epilogue == EPI_RESIDUAL && !gate) return fail(WDL_EINVAL, "w4a4_gemm: residual epilogue needs gate");
     if (reinterpret_cast<uintptr_t>(gate) % 16 || reinterpret_cast<uintptr_t>(bias) % 8 ||
-        reinterpret_cast<uintptr_t>(out) % 8 || reinterpret_cast<uintptr_t>(proj_up) % 16 ||
-        reinterpret_cast<uintptr_t>(lora) % 16)
-        return fail(WDL_EINVAL, "w4a4_gemm: gate, lora and proj_up must be 16-byte aligned, bias and out 8-byte");
+        reinterpret_cast<uintptr_t>(out) % 16 || reinterpret_cast<uintptr_t>(proj_up) % 16 ||
+        reinterpret_cast<uintptr_t>(lora) % 16 || (epilogue != EPI_F32 && ldo % 8))
+        return fail(WDL_EINVAL, "w4a4_gemm: out, gate, lora and proj_up must be 16-byte aligned, bias 8-byte, and "
+                                "bf16 output rows a multiple of 8 elements");
     if (M == 0) return WDL_OK;
     GemmArgs a{static_cast<const uint8_t*>(qa), static_cast<const uint16_t*>(ascales),
                static_cast<const uint8_t*>(wcodes), static_cast<const uint16_t*>(wscales), lora,
