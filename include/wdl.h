@@ -84,11 +84,16 @@ int wdl_w4a4_weight_codes(const void* qweight, int64_t N, int64_t K, void* codes
  * (wdl_w4a4_weight_codes), both in the operand format above; wscales bf16 [K/64, N]; lora fp32 [Mp, 32] or NULL; proj_up bf16
  * [N, 32]; bias bf16 [N] or NULL. epilogue: 0 out bf16 [M, ldo] = y; 1 out fp32 = y; 2 out bf16 =
  * bf16(out + bf16(y) * gate[n]) in place (gated residual; gate fp32 [N]); 3 out bf16 = GELU_tanh(y).
- * Mp % 128 == 0, N % 128 == 0, K % 64 == 0; qa, wcodes, proj_up, lora, gate 16-byte aligned, bias and out 8-byte,
- * scales 4-byte. */
+ * Mp % 128 == 0, N % 128 == 0, K % 64 == 0, K <= 2^30; qa, wcodes, out, proj_up, lora, gate and workspace 16-byte
+ * aligned, bias 8-byte, scales 4-byte; bf16 outputs: ldo % 8 == 0.
+ * workspace: wdl_w4a4_gemm_workspace_bytes(Mp, N, K) bytes (no initial contents), or NULL. When the size is not 0
+ * the product runs split in K over one workgroup per CU (stream-K, for shapes whose tiles leave CUs idle) and a
+ * second launch adds the pieces in a fixed order: deterministic, rounding not identical to the one-pass launch.
+ * With NULL the one-pass launch runs. Calls sharing a workspace must not overlap. */
+int64_t wdl_w4a4_gemm_workspace_bytes(int64_t Mp, int64_t N, int64_t K);
 int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wcodes, const void* wscales, const float* lora,
                   const void* proj_up, const void* bias, int64_t M, int64_t Mp, int64_t N, int64_t K, int64_t rank,
-                  void* out, int64_t ldo, int epilogue, const float* gate, wdl_stream_t stream);
+                  void* out, int64_t ldo, int epilogue, const float* gate, void* workspace, wdl_stream_t stream);
 
 /* Workspace (in floats) of wdl_fp8_quantize in per-tensor mode for an [M, K] operand. */
 int64_t wdl_fp8_quantize_workspace_floats(int64_t M, int64_t K);

@@ -80,7 +80,8 @@ def test_fused_layernorm_modulation_quant_bit_exact(gpu, affine):
     assert torch.equal(asc.cpu()[:, :M].t(), rs)
 
 
-def launch_gemm(qa_int, asc, qweight, wsc, lora=None, pu=None, bias=None, M=None, epi=1, out=None, gate=None):
+def launch_gemm(qa_int, asc, qweight, wsc, lora=None, pu=None, bias=None, M=None, epi=1, out=None, gate=None,
+                stream_k=True):
     from wdl import ops
 
     Mp, K = qa_int.shape
@@ -91,7 +92,7 @@ def launch_gemm(qa_int, asc, qweight, wsc, lora=None, pu=None, bias=None, M=None
         out = torch.empty(M, N, device="cuda", dtype=torch.float32 if epi == 1 else torch.bfloat16)
     c = lambda t: None if t is None else t.cuda()
     return ops.gemm_launch(codes, c(asc), c(lora), ops.as_codes(qweight.cuda(), K), c(wsc), c(pu), c(bias), M, out,
-                           epi, c(gate))
+                           epi, c(gate), stream_k)
 
 
 @pytest.mark.parametrize("N,K", [(128, 64), (384, 3072), (256, 14336)])
@@ -109,7 +110,7 @@ def test_weight_codes_are_the_fp6_codes_of_the_packed_integers(gpu, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(128, 128, 64), (256, 384, 512), (128, 256, 3072), (128, 128, 14336),
-                                   (1408, 3072, 3072)])
+                                   (1408, 3072, 3072), (1408, 3072, 8192), (128, 256, 14336)])
 def test_gemm_integer_accumulation_is_exact(gpu, M, N, K):
     """Unit scales, no low-rank, fp32 out: y must equal the exact integer product (bar: bit-exact)."""
     from wdl import w4a4
@@ -149,6 +150,42 @@ def test_gemm_scaled_lowrank_bias_matches_oracle(gpu, M, N, K, valid):
     # bf16 result: one bf16 rounding of that
     diff = (yb.cpu().double() - ref).abs()
     assert torch.all(diff <= ref.abs() * 2 ** -8 + 2 ** -20 * scale * (K // 64))
+
+
+@pytest.mark.parametrize("M,N,K,valid", [(1408, 3072, 8192, 1392), (512, 512, 14336, 464)])
+def test_gemm_stream_k_matches_one_pass_and_oracle(gpu, M, N, K, valid):
+    """Shapes whose tiles leave CUs idle run split in K (stream-K + merge, when the library asks for a workspace):
+    the result is deterministic, within fp32 rounding of the one-pass launch, and meets the oracle bar of the
+    one-pass test; gated residual epilogue in place."""
+    from wdl import _lib, ops, w4a4
+
+    assert _lib.library().wdl_w4a4_gemm_workspace_bytes(M, N, K) > 0  # the split path is the one under test
+    g = torch.Generator().manual_seed(11 + M)
+    qa = torch.randint(-7, 8, (M, K), generator=g, dtype=torch.int32)
+    qw = torch.randint(-8, 8, (N, K), generator=g, dtype=torch.int32)
+    asc = (torch.rand(K // 64, M, generator=g) * 0.3 + 0.01).to(torch.bfloat16)
+    wsc = (torch.rand(K // 64, N, generator=g) * 0.01 + 1e-4).to(torch.bfloat16)
+    lora = torch.randn(M, 32, generator=g)
+    pu = (torch.randn(N, 32, generator=g) * 0.05).to(torch.bfloat16)
+    bias = (torch.randn(N, generator=g) * 0.1).to(torch.bfloat16)
+    X = torch.randn(valid, N, generator=g).to(torch.bfloat16)
+    gate = torch.randn(N, generator=g)
+    wq = w4a4.pack_weight(qw)
+    y1 = launch_gemm(qa, asc, wq, wsc, lora, pu, bias, M=valid, epi=1)
+    y2 = launch_gemm(qa, asc, wq, wsc, lora, pu, bias, M=valid, epi=1)
+    y0 = launch_gemm(qa, asc, wq, wsc, lora, pu, bias, M=valid, epi=1, stream_k=False)
+    outs = X.cuda().clone()
+    launch_gemm(qa, asc, wq, wsc, lora, pu, bias, M=valid, epi=2, out=outs, gate=gate)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)  # deterministic
+    ref = ow.group_gemm(qa[:valid], asc.t()[:valid].float(), qw, wsc.t().float())
+    ref += lora[:valid].to(torch.bfloat16).double() @ pu.double().t() + bias.double()
+    scale = float(ref.abs().max())
+    bar = 2 ** -20 * scale * (K // 64)  # fp32 rounding of ~K/64 fused steps, as in the one-pass test
+    assert float((y1.cpu().double() - ref).abs().max()) <= bar
+    assert float((y1 - y0).abs().max()) <= bar
+    expect = (X.float() + y1.cpu().to(torch.bfloat16).float() * gate).to(torch.bfloat16)
+    assert torch.equal(outs.cpu(), expect)  # the residual epilogue of the merge: bf16(x + bf16(y) gate)
 
 
 def test_gemm_residual_and_gelu_epilogues(gpu):

@@ -55,6 +55,7 @@ struct GemmArgs {
     const float* gate;        // [N] fp32 (EPI_RESIDUAL: out += gate * bf16(y))
     const float* xs;          // FP8 linears: activation scales fp32 [Mp] (rows) or [1] (tensor)
     const float* wsf;         // FP8 linears: weight scales fp32 [N] (rows) or [1] (tensor)
+    float* part;              // stream-K partial sums (workspace), or null
 };
 
 // Tile BN (features) x BM (tokens), NW waves in a (BN / WN) x (BM / WM) grid. Every operand byte streams from
@@ -334,7 +335,7 @@ __device__ __forceinline__ void finish_tile_rows(const GemmArgs& p, f32x16 (&acc
 // The main loop of both GEMMs. W4: the W4A4 product (fp6 tile-blocked codes, per-group scale fold, scales
 // streamed with the codes); otherwise the FP8 product (e4m3 row-major codes only, one fp32 accumulation over all
 // of K in the MFMA accumulator).
-template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES, bool W4>
+template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES, bool W4, bool SK = false>
 __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
     static_assert(!W4 || (BN % BLOCK_ROWS == 0 && BM % BLOCK_ROWS == 0), "blocked operands come in 128-row tiles");
     static_assert((BN / WN) * (BM / WM) == NW, "wave grid");
@@ -361,79 +362,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
     const int wave = __builtin_amdgcn_readfirstlane(t / 64);
     const int wn = wave % (BN / WN), wm = wave / (BN / WN);
     const int64_t ntn = p.N / BN, ntm = p.Mp / BM, total = ntn * ntm;
-    const int64_t pid = blockIdx.x;
-    int64_t tile = pid;
-    if (total % 8 == 0) tile = (pid % 8) * (total / 8) + pid / 8;
-    const int64_t n0 = (tile / ntm) * BN, m0 = (tile % ntm) * BM;
     const int64_t K = p.K, G = K / 64;
-    const int GI = int(G);  // groups (K < 2^31 is checked by the launcher)
 
     // zero tails of the scale stages (written once; the loads never touch them)
     if constexpr (W4)
         if (t < STAGES * 16) *reinterpret_cast<uint32_t*>(&sS[t / 16][SD + (t % 16) * 4]) = 0u;
-
-    // W4: the stage is cut into 1 KB chunks (16-byte loads) and then 256-byte chunks (4-byte loads); wave w takes
-    // 1 KB chunks w N16 .. and 256-byte chunks w N4 ... Each chunk lies inside one operand's 6 KB block (block
-    // and operand boundaries are multiples of 1 KB), so a load reads from a wave-uniform base (scalar registers:
-    // operand, tile row block, chunk; group g adds g BLOCK6) plus lane * 16 or lane * 4. The scale chunk of wave w
-    // is bytes 256 w .. of [ws[BN] | as[BM] | padding], also uniform per wave (2 BN and 2 BM are multiples of 256).
-    // FP8: this lane's sources for group 0; group g adds 64 g bytes.
-    const uint8_t* cbase[W4 ? N16 + N4 : 1];
-    int cdst[W4 ? N16 + N4 : 1];
-    const uint8_t* xsrc[W4 ? 1 : XI];
-    const uint8_t* wsrc[W4 ? 1 : WI];
-    if constexpr (W4) {
-#pragma unroll
-        for (int u = 0; u < N16 + N4; ++u) {
-            const int o = u < N16 ? (wave * N16 + u) * 1024 : NW * N16 * 1024 + (wave * N4 + u - N16) * 256;
-            cdst[u] = o;
-            cbase[u] = o < BN * ROW6 ? p.wc + (n0 / BLOCK_ROWS + o / BLOCK6) * G * BLOCK6 + o % BLOCK6
-                                     : p.qa + (m0 / BLOCK_ROWS + (o - BN * ROW6) / BLOCK6) * G * BLOCK6 +
-                                           (o - BN * ROW6) % BLOCK6;
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < XI; ++j) {
-            const int slot = (wave * XI + j) * 64 + lane;          // 16-byte slot of the stage
-            const int row = slot / 4, quarter = (slot % 4) ^ ((row >> 2) & 3);
-            xsrc[j] = p.qa + (m0 + row) * K + quarter * 16;
-        }
-#pragma unroll
-        for (int j = 0; j < WI; ++j) {
-            const int slot = (wave * WI + j) * 64 + lane;
-            const int row = slot / 4, quarter = (slot % 4) ^ ((row >> 2) & 3);
-            wsrc[j] = p.wc + (n0 + row) * K + quarter * 16;
-        }
-    }
-    const uint8_t* sbase;   // the wave's 256 scale bytes of group 0: ws, as or (padding waves) a valid dummy
-    int64_t sstride;
-    {
-        const int b = 256 * wave;
-        if (b < 2 * BN) {
-            sbase = reinterpret_cast<const uint8_t*>(p.ws + n0) + b;
-            sstride = 2 * p.N;
-        } else if (b < 2 * (BN + BM)) {
-            sbase = reinterpret_cast<const uint8_t*>(p.as + m0) + (b - 2 * BN);
-            sstride = 2 * p.Mp;
-        } else {
-            sbase = reinterpret_cast<const uint8_t*>(p.ws + n0);
-            sstride = 0;
-        }
-    }
-    const uint32_t off16 = uint32_t(lane) * 16, off4 = uint32_t(lane) * 4;
-
-    // direct load u (0 .. LPG - 1) of group g (clamped to the last group) into stage st
-    auto issue_one = [&](int st, int g, int u) {
-        const int gg = g < GI ? g : GI - 1;
-        if constexpr (W4) {
-            if (u < N16) dma16s(cbase[u] + int64_t(gg) * BLOCK6, off16, lds_addr(&sC[st][cdst[u]]));
-            else if (u < N16 + N4) dma4s(cbase[u] + int64_t(gg) * BLOCK6, off4, lds_addr(&sC[st][cdst[u]]));
-            else dma4s(sbase + gg * sstride, off4, lds_addr(&sS[st][wave * 256]));
-        } else {
-            if (u < XI) dma16(xsrc[u] + int64_t(gg) * 64, lds_addr(&sX[st][(wave * XI + u) * 1024]));
-            else dma16(wsrc[u - XI] + int64_t(gg) * 64, lds_addr(&sW[st][(wave * WI + u - XI) * 1024]));
-        }
-    };
 
     // per-lane LDS offsets (stage-independent). W4: a lane's 16-byte and 8-byte pieces of its operand row, the
     // scale entries. FP8: operand rows and the two swizzled quarters.
@@ -465,147 +398,310 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
     static_assert(WN % 32 == 0 && WM % 32 == 0, "32-aligned subtiles");
 
     f32x16 acc[TN][TM];
-#pragma unroll
-    for (int i = 0; i < TN; ++i)
-#pragma unroll
-        for (int j = 0; j < TM; ++j) acc[i][j] = f32x16{};
-    const f32x16 zero = {};
-
-    // Two register sets of one group's operands: weight / activation code fragments (W4: 6 dwords of fp6 codes,
-    // FP8: 8 of e4m3) and (W4) the bf16 scale of each fragment row, zero-extended (lanes 32..63 read the zero tail).
-    // Group h is multiplied from set h % 2 while group h + 1 is read into the other set.
-    i32x8 fa[2][TN], fb[2][TM];
-    uint32_t fsa[2][TN], fsb[2][TM];
-    auto load_frag = [&](const uint8_t* r) {
+    // Multiply groups [g0, g1) of the tile at features n0, tokens m0 into acc (zeroed first); on return every load
+    // of the piece has landed.
+    auto mainloop = [&](int64_t n0, int64_t m0, int g0, int g1) {
+        const int GI = g1 - g0;
+        // W4: the stage is cut into 1 KB chunks (16-byte loads) and then 256-byte chunks (4-byte loads); wave w takes
+        // 1 KB chunks w N16 .. and 256-byte chunks w N4 ... Each chunk lies inside one operand's 6 KB block (block
+        // and operand boundaries are multiples of 1 KB), so a load reads from a wave-uniform base (scalar registers:
+        // operand, tile row block, chunk; group g adds g BLOCK6) plus lane * 16 or lane * 4. The scale chunk of wave w
+        // is bytes 256 w .. of [ws[BN] | as[BM] | padding], also uniform per wave (2 BN and 2 BM are multiples of 256).
+        // FP8: this lane's sources. Both relative to group g0 of the piece.
+        const uint8_t* cbase[W4 ? N16 + N4 : 1];
+        int cdst[W4 ? N16 + N4 : 1];
+        const uint8_t* xsrc[W4 ? 1 : XI];
+        const uint8_t* wsrc[W4 ? 1 : WI];
         if constexpr (W4) {
-            const uint4 x = *reinterpret_cast<const uint4*>(r + q0);
-            const uint2 y = *reinterpret_cast<const uint2*>(r + q1);
-            return i32x8{int(x.x), int(x.y), int(x.z), int(x.w), int(y.x), int(y.y), 0, 0};
-        } else {
-            const uint4 x = *reinterpret_cast<const uint4*>(r + q0), y = *reinterpret_cast<const uint4*>(r + q1);
-            return i32x8{int(x.x), int(x.y), int(x.z), int(x.w), int(y.x), int(y.y), int(y.z), int(y.w)};
-        }
-    };
-    auto load_a = [&](int set, int st, int i) {
-        if constexpr (W4) {
-            fa[set][i] = load_frag(&sC[st][aoff[i]]);
-            fsa[set][i] = *reinterpret_cast<const uint16_t*>(&sS[st][soa[i]]);
-        } else {
-            fa[set][i] = load_frag(&sW[st][aoff[i]]);
-        }
-    };
-    auto load_b = [&](int set, int st, int j) {
-        if constexpr (W4) {
-            fb[set][j] = load_frag(&sC[st][boff[j]]);
-            fsb[set][j] = *reinterpret_cast<const uint16_t*>(&sS[st][sob[j]]);
-        } else {
-            fb[set][j] = load_frag(&sX[st][boff[j]]);
-        }
-    };
-    // fragment r of the next group (r < TN: weight rows i = r, else activation rows j = r - TN)
-    auto load_next = [&](int set, int st, int r) {
-        if (r < TN) load_a(set, st, r);
-        else load_b(set, st, r - TN);
-    };
-
-    // Multiply one group from register set cur while the next group's operands (stage nst) are read into the other
-    // set, TN + TM fragments spread over the TN x TM subtiles: the reads have a whole step to land, so LDS latency
-    // stays off the MFMA chain.
-    // W4: the fold is software-pipelined by one subtile: the products of subtile s are folded while the MFMAs of
-    // subtile s + 1 run (the last subtile of a group while the first subtile of the next group runs). pI / pP hold
-    // the pending subtile; they start at zero (the first fold adds 0 * 0 to a zero accumulator: no change).
-    f32x16 pI = zero, pP = zero;
-    // The step's LPG direct loads (group ig into stage ist) are spread over its subtiles, one or two after each
-    // subtile's MFMAs, so a wave never waits on a full load queue with MFMA work still to issue.
-    constexpr int NF = TN + TM, NS = TN * TM;
-    auto step = [&](int cur, int nst, int ist, int ig) {
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            const int i = s / TM, j = s % TM;
-            if constexpr (W4) {
-                const int pi = s == 0 ? TN - 1 : (s - 1) / TM, pj = s == 0 ? TM - 1 : (s - 1) % TM;
-                const i16x4 oa = __builtin_bit_cast(i16x4, make_uint2(fsa[cur][i], 0u));
-                const i16x4 ob = __builtin_bit_cast(i16x4, make_uint2(fsb[cur][j], 0u));
-                // A: weights as e3m2 (format 3), B: activations as e2m3 (format 2)
-                const f32x16 I =
-                    __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[cur][i], fb[cur][j], zero, 3, 2, 0, 0, 0, 0);
-                const f32x16 P = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(oa, ob, zero, 0, 0, 0);
+            for (int u = 0; u < N16 + N4; ++u) {
+                const int o = u < N16 ? (wave * N16 + u) * 1024 : NW * N16 * 1024 + (wave * N4 + u - N16) * 256;
+                cdst[u] = o;
+                cbase[u] = (o < BN * ROW6 ? p.wc + (n0 / BLOCK_ROWS + o / BLOCK6) * G * BLOCK6 + o % BLOCK6
+                                          : p.qa + (m0 / BLOCK_ROWS + (o - BN * ROW6) / BLOCK6) * G * BLOCK6 +
+                                                (o - BN * ROW6) % BLOCK6) +
+                           int64_t(g0) * BLOCK6;
+            }
+        } else {
 #pragma unroll
-                for (int e = 0; e < 16; ++e) acc[pi][pj][e] = fmaf(pI[e], pP[e], acc[pi][pj][e]);
-                pI = I;
-                pP = P;
-            } else {
-                acc[i][j] =
-                    __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0, 0, 0, 0);
+            for (int j = 0; j < XI; ++j) {
+                const int slot = (wave * XI + j) * 64 + lane;          // 16-byte slot of the stage
+                const int row = slot / 4, quarter = (slot % 4) ^ ((row >> 2) & 3);
+                xsrc[j] = p.qa + (m0 + row) * K + quarter * 16 + int64_t(g0) * 64;
             }
 #pragma unroll
-            for (int r = s * NF / NS; r < (s + 1) * NF / NS; ++r) load_next(1 - cur, nst, r);
-            // one wave issues in order and an MFMA waits at issue while the matrix core is busy, so the fold of
-            // subtile s - 1 is split around the two MFMAs of subtile s: it executes while they run
-            if constexpr (W4) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // I_s (32 cycles)
-                __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);   // reads of the next group
-                __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // fold of s - 1, first part
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // P_s (32 cycles)
-                __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // the rest
-            } else {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+            for (int j = 0; j < WI; ++j) {
+                const int slot = (wave * WI + j) * 64 + lane;
+                const int row = slot / 4, quarter = (slot % 4) ^ ((row >> 2) & 3);
+                wsrc[j] = p.wc + (n0 + row) * K + quarter * 16 + int64_t(g0) * 64;
             }
-#pragma unroll
-            for (int u = s * LPG / NS; u < (s + 1) * LPG / NS; ++u) issue_one(ist, ig, u);
         }
-    };
+        const uint8_t* sbase;   // the wave's 256 scale bytes of group g0: ws, as or (padding waves) a valid dummy
+        int64_t sstride;
+        {
+            const int b = 256 * wave;
+            if (b < 2 * BN) {
+                sstride = 2 * p.N;
+                sbase = reinterpret_cast<const uint8_t*>(p.ws + n0) + b + g0 * sstride;
+            } else if (b < 2 * (BN + BM)) {
+                sstride = 2 * p.Mp;
+                sbase = reinterpret_cast<const uint8_t*>(p.as + m0) + (b - 2 * BN) + g0 * sstride;
+            } else {
+                sbase = reinterpret_cast<const uint8_t*>(p.ws + n0);
+                sstride = 0;
+            }
+        }
+        const uint32_t off16 = uint32_t(lane) * 16, off4 = uint32_t(lane) * 4;
 
-    // Ring, one group per step. Step h: this wave's loads of group h + 1 have landed (the STAGES - 3 groups after
-    // it may still be in flight); after the barrier the same holds for every wave, and group h + 1 is read into
-    // registers during the step. The stage of group h - 1 is free: every wave read it during step h - 2 and used
-    // the registers in step h - 1, so no wait on LDS reads comes before the barrier. Group h + STAGES - 1 goes into
-    // it (clamped to the last group, so every step issues the same loads and vmcnt counts stay exact). Stages and
-    // register sets are compile-time constants throughout: whole turns of the ring are unrolled, and so are the
-    // G % STAGES remaining steps (each under a uniform branch); STAGES is even, so group h uses set h % 2.
-    static_assert(STAGES >= 4 && STAGES % 2 == 0, "the ring keeps one stage being read, one free and two or more in "
-                                                  "flight; register sets alternate over a turn");
+        // direct load u (0 .. LPG - 1) of group g0 + g (clamped to the piece's last group) into stage st
+        auto issue_one = [&](int st, int g, int u) {
+            const int gg = g < GI ? g : GI - 1;
+            if constexpr (W4) {
+                if (u < N16) dma16s(cbase[u] + int64_t(gg) * BLOCK6, off16, lds_addr(&sC[st][cdst[u]]));
+                else if (u < N16 + N4) dma4s(cbase[u] + int64_t(gg) * BLOCK6, off4, lds_addr(&sC[st][cdst[u]]));
+                else dma4s(sbase + gg * sstride, off4, lds_addr(&sS[st][wave * 256]));
+            } else {
+                if (u < XI) dma16(xsrc[u] + int64_t(gg) * 64, lds_addr(&sX[st][(wave * XI + u) * 1024]));
+                else dma16(wsrc[u - XI] + int64_t(gg) * 64, lds_addr(&sW[st][(wave * WI + u - XI) * 1024]));
+            }
+        };
+
 #pragma unroll
-    for (int k = 0; k < STAGES - 1; ++k)
+        for (int i = 0; i < TN; ++i)
 #pragma unroll
-        for (int u = 0; u < LPG; ++u) issue_one(k, k, u);
-    wait_vmcnt<(STAGES - 2) * LPG>();
-    __syncthreads();
+            for (int j = 0; j < TM; ++j) acc[i][j] = f32x16{};
+        const f32x16 zero = {};
+
+        // Two register sets of one group's operands: weight / activation code fragments (W4: 6 dwords of fp6 codes,
+        // FP8: 8 of e4m3) and (W4) the bf16 scale of each fragment row, zero-extended (lanes 32..63 read the zero tail).
+        // Group h is multiplied from set h % 2 while group h + 1 is read into the other set.
+        i32x8 fa[2][TN], fb[2][TM];
+        uint32_t fsa[2][TN], fsb[2][TM];
+        auto load_frag = [&](const uint8_t* r) {
+            if constexpr (W4) {
+                const uint4 x = *reinterpret_cast<const uint4*>(r + q0);
+                const uint2 y = *reinterpret_cast<const uint2*>(r + q1);
+                return i32x8{int(x.x), int(x.y), int(x.z), int(x.w), int(y.x), int(y.y), 0, 0};
+            } else {
+                const uint4 x = *reinterpret_cast<const uint4*>(r + q0), y = *reinterpret_cast<const uint4*>(r + q1);
+                return i32x8{int(x.x), int(x.y), int(x.z), int(x.w), int(y.x), int(y.y), int(y.z), int(y.w)};
+            }
+        };
+        auto load_a = [&](int set, int st, int i) {
+            if constexpr (W4) {
+                fa[set][i] = load_frag(&sC[st][aoff[i]]);
+                fsa[set][i] = *reinterpret_cast<const uint16_t*>(&sS[st][soa[i]]);
+            } else {
+                fa[set][i] = load_frag(&sW[st][aoff[i]]);
+            }
+        };
+        auto load_b = [&](int set, int st, int j) {
+            if constexpr (W4) {
+                fb[set][j] = load_frag(&sC[st][boff[j]]);
+                fsb[set][j] = *reinterpret_cast<const uint16_t*>(&sS[st][sob[j]]);
+            } else {
+                fb[set][j] = load_frag(&sX[st][boff[j]]);
+            }
+        };
+        // fragment r of the next group (r < TN: weight rows i = r, else activation rows j = r - TN)
+        auto load_next = [&](int set, int st, int r) {
+            if (r < TN) load_a(set, st, r);
+            else load_b(set, st, r - TN);
+        };
+
+        // Multiply one group from register set cur while the next group's operands (stage nst) are read into the other
+        // set, TN + TM fragments spread over the TN x TM subtiles: the reads have a whole step to land, so LDS latency
+        // stays off the MFMA chain.
+        // W4: the fold is software-pipelined by one subtile: the products of subtile s are folded while the MFMAs of
+        // subtile s + 1 run (the last subtile of a group while the first subtile of the next group runs). pI / pP hold
+        // the pending subtile; they start at zero (the first fold adds 0 * 0 to a zero accumulator: no change).
+        f32x16 pI = zero, pP = zero;
+        // The step's LPG direct loads (group ig into stage ist) are spread over its subtiles, one or two after each
+        // subtile's MFMAs, so a wave never waits on a full load queue with MFMA work still to issue.
+        constexpr int NF = TN + TM, NS = TN * TM;
+        auto step = [&](int cur, int nst, int ist, int ig) {
 #pragma unroll
-    for (int r = 0; r < NF; ++r) load_next(0, 0, r);
-    auto ring_step = [&](int k, int h) {
-        wait_vmcnt<(STAGES - 3) * LPG>();
+            for (int s = 0; s < NS; ++s) {
+                const int i = s / TM, j = s % TM;
+                if constexpr (W4) {
+                    const int pi = s == 0 ? TN - 1 : (s - 1) / TM, pj = s == 0 ? TM - 1 : (s - 1) % TM;
+                    const i16x4 oa = __builtin_bit_cast(i16x4, make_uint2(fsa[cur][i], 0u));
+                    const i16x4 ob = __builtin_bit_cast(i16x4, make_uint2(fsb[cur][j], 0u));
+                    // A: weights as e3m2 (format 3), B: activations as e2m3 (format 2)
+                    const f32x16 I =
+                        __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[cur][i], fb[cur][j], zero, 3, 2, 0, 0, 0, 0);
+                    const f32x16 P = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(oa, ob, zero, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) acc[pi][pj][e] = fmaf(pI[e], pP[e], acc[pi][pj][e]);
+                    pI = I;
+                    pP = P;
+                } else {
+                    acc[i][j] =
+                        __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0, 0, 0, 0);
+                }
+#pragma unroll
+                for (int r = s * NF / NS; r < (s + 1) * NF / NS; ++r) load_next(1 - cur, nst, r);
+                // one wave issues in order and an MFMA waits at issue while the matrix core is busy, so the fold of
+                // subtile s - 1 is split around the two MFMAs of subtile s: it executes while they run
+                if constexpr (W4) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // I_s (32 cycles)
+                    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);   // reads of the next group
+                    __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // fold of s - 1, first part
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // P_s (32 cycles)
+                    __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // the rest
+                } else {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+                }
+#pragma unroll
+                for (int u = s * LPG / NS; u < (s + 1) * LPG / NS; ++u) issue_one(ist, ig, u);
+            }
+        };
+
+        // Ring, one group per step. Step h: this wave's loads of group h + 1 have landed (the STAGES - 3 groups after
+        // it may still be in flight); after the barrier the same holds for every wave, and group h + 1 is read into
+        // registers during the step. The stage of group h - 1 is free: every wave read it during step h - 2 and used
+        // the registers in step h - 1, so no wait on LDS reads comes before the barrier. Group h + STAGES - 1 goes into
+        // it (clamped to the last group, so every step issues the same loads and vmcnt counts stay exact). Stages and
+        // register sets are compile-time constants throughout: whole turns of the ring are unrolled, and so are the
+        // G % STAGES remaining steps (each under a uniform branch); STAGES is even, so group h uses set h % 2.
+        static_assert(STAGES >= 4 && STAGES % 2 == 0, "the ring keeps one stage being read, one free and two or more in "
+                                                      "flight; register sets alternate over a turn");
+#pragma unroll
+        for (int k = 0; k < STAGES - 1; ++k)
+#pragma unroll
+            for (int u = 0; u < LPG; ++u) issue_one(k, k, u);
+        wait_vmcnt<(STAGES - 2) * LPG>();
         __syncthreads();
-        step(k % 2, k + 1 == STAGES ? 0 : k + 1, k == 0 ? STAGES - 1 : k - 1, h + STAGES - 1);
+#pragma unroll
+        for (int r = 0; r < NF; ++r) load_next(0, 0, r);
+        auto ring_step = [&](int k, int h) {
+            wait_vmcnt<(STAGES - 3) * LPG>();
+            __syncthreads();
+            step(k % 2, k + 1 == STAGES ? 0 : k + 1, k == 0 ? STAGES - 1 : k - 1, h + STAGES - 1);
+        };
+        int g = 0;  // wave-uniform: kept in scalar registers
+        for (; g + STAGES <= GI; g = __builtin_amdgcn_readfirstlane(g + STAGES)) {
+#pragma unroll
+            for (int k = 0; k < STAGES; ++k) ring_step(k, g + k);
+        }
+#pragma unroll
+        for (int k = 0; k < STAGES - 1; ++k)
+            if (g + k < GI) ring_step(k, g + k);
+        if constexpr (W4) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[TN - 1][TM - 1][e] = fmaf(pI[e], pP[e], acc[TN - 1][TM - 1][e]);
+        }
+        wait_vmcnt<0>();  // the clamped tail loads land before the workgroup can end
     };
-    int g = 0;  // wave-uniform: kept in scalar registers
-    for (; g + STAGES <= GI; g = __builtin_amdgcn_readfirstlane(g + STAGES)) {
-#pragma unroll
-        for (int k = 0; k < STAGES; ++k) ring_step(k, g + k);
-    }
-#pragma unroll
-    for (int k = 0; k < STAGES - 1; ++k)
-        if (g + k < GI) ring_step(k, g + k);
-    if constexpr (W4) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[TN - 1][TM - 1][e] = fmaf(pI[e], pP[e], acc[TN - 1][TM - 1][e]);
-    }
-    wait_vmcnt<0>();  // the clamped tail loads land before the workgroup can end
 
-    if constexpr (W4 && EPI != EPI_F32) {
-        __syncthreads();  // every wave is past its last read of the ring, whose LDS the staging reuses
-        static_assert(NW * 64 * STG * 2 <= STAGES * CS, "staging fits in the ring");
-        finish_tile_rows<TN, TM, EPI>(p, acc, n0 + wn * WN, m0 + wm * WM, lane,
-                                      reinterpret_cast<uint16_t*>(&sC[0][0]) + wave * 64 * STG);
+    if constexpr (!SK) {
+        // the whole tile `pid`, ids remapped so that the tiles of one weight slab run on one XCD
+        const int64_t pid = blockIdx.x;
+        int64_t tile = pid;
+        if (total % 8 == 0) tile = (pid % 8) * (total / 8) + pid / 8;
+        const int64_t n0 = (tile / ntm) * BN, m0 = (tile % ntm) * BM;
+        mainloop(n0, m0, 0, int(G));
+        if constexpr (W4 && EPI != EPI_F32) {
+            __syncthreads();  // every wave is past its last read of the ring, whose LDS the staging reuses
+            static_assert(NW * 64 * STG * 2 <= STAGES * CS, "staging fits in the ring");
+            finish_tile_rows<TN, TM, EPI>(p, acc, n0 + wn * WN, m0 + wm * WM, lane,
+                                          reinterpret_cast<uint16_t*>(&sC[0][0]) + wave * 64 * STG);
+        } else {
+            finish_tile<TN, TM, EPI>(p, acc, n0 + wn * WN, m0 + wm * WM, lane);
+        }
     } else {
-        finish_tile<TN, TM, EPI>(p, acc, n0 + wn * WN, m0 + wm * WM, lane);
+        // Stream-K share of this workgroup: the U = total * G (tile, group) iterations in tile-major order split
+        // evenly over the W workgroups of the launch, W > total, so a share covers less than one tile: at most two
+        // pieces, whose partial sums go to workspace slots 2 c and 2 c + 1 (c: the logical index, workgroup ids
+        // remapped so that consecutive shares run on one XCD); w4a4_merge_kernel adds them per tile and finishes.
+        const int64_t W = gridDim.x, U = total * G, pid = blockIdx.x;
+        const int64_t c = W % 8 == 0 ? (pid % 8) * (W / 8) + pid / 8 : pid;
+        const int64_t s0 = c * U / W, s1 = (c + 1) * U / W;
+#pragma unroll 1
+        for (int piece = 0; piece < 2; ++piece) {
+            const int64_t a0 = piece == 0 ? s0 : (s0 / G + 1) * G;
+            if (a0 >= s1) break;
+            const int64_t tl = a0 / G;
+            const int g0 = int(a0 - tl * G), g1 = int(s1 - tl * G < G ? s1 - tl * G : G);
+            if (piece == 1) __syncthreads();  // every wave is past the first piece's ring before the refill
+            mainloop((tl / ntm) * BN, (tl % ntm) * BM, g0, g1);
+            float4* dst = reinterpret_cast<float4*>(p.part + (2 * c + piece) * (NW * 64 * TN * TM * 16)) +
+                          wave * (TN * TM * 4 * 64) + lane;
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j)
+#pragma unroll
+                    for (int f4 = 0; f4 < 4; ++f4)
+                        dst[((i * TM + j) * 4 + f4) * 64] = make_float4(acc[i][j][4 * f4], acc[i][j][4 * f4 + 1],
+                                                                        acc[i][j][4 * f4 + 2], acc[i][j][4 * f4 + 3]);
+        }
     }
 }
 
 template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES>
 __global__ __launch_bounds__(NW * 64) void w4a4_gemm_kernel(GemmArgs p) {
     gemm_body<BN, BM, WN, WM, NW, EPI, STAGES, true>(p);
+}
+
+template <int BN, int BM, int WN, int WM, int NW, int STAGES>
+__global__ __launch_bounds__(NW * 64) void w4a4_gemm_sk_kernel(GemmArgs p) {
+    gemm_body<BN, BM, WN, WM, NW, EPI_F32, STAGES, true, true>(p);
+}
+
+// The stream-K share c (of W) whose iteration range [c U / W, (c + 1) U / W) contains iteration `it`
+__device__ __forceinline__ int64_t share_of(int64_t it, int64_t U, int64_t W) {
+    int64_t c = it * W / U;
+    while (c + 1 < W && (c + 1) * U / W <= it) ++c;
+    while (c > 0 && c * U / W > it) --c;
+    return c;
+}
+
+// One tile of a stream-K launch: the partial sums of its contributors (the shares that meet its G iterations, in
+// increasing order, i.e. in increasing K) added in that fixed order into the accumulator layout of the main loop,
+// then the low-rank term, bias and epilogue as in the plain launch.
+template <int BN, int BM, int WN, int WM, int NW, int EPI>
+__global__ __launch_bounds__(NW * 64) void w4a4_merge_kernel(GemmArgs p, int64_t W) {
+    constexpr int TN = WN / 32, TM = WM / 32;
+    __shared__ __attribute__((aligned(16))) uint16_t stage[EPI == EPI_F32 ? 8 : NW * 64 * STG];
+    const int t = threadIdx.x, lane = t % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(t / 64);
+    const int wn = wave % (BN / WN), wm = wave / (BN / WN);
+    const int64_t ntm = p.Mp / BM, total = (p.N / BN) * ntm, G = p.K / 64, U = total * G;
+    const int64_t tl = blockIdx.x;
+    const int64_t cf = share_of(tl * G, U, W), cl = share_of((tl + 1) * G - 1, U, W);
+    f32x16 acc[TN][TM];
+    bool first = true;
+    for (int64_t c = cf; c <= cl; ++c) {
+        const int64_t cs0 = c * U / W;
+        if (cs0 == (c + 1) * U / W) continue;  // an empty share (U < W) wrote nothing
+        const int piece = cs0 >= tl * G ? 0 : 1;  // the tile is the first or the second piece of share c
+        const float4* src = reinterpret_cast<const float4*>(p.part + (2 * c + piece) * (NW * 64 * TN * TM * 16)) +
+                            wave * (TN * TM * 4 * 64) + lane;
+        float4 v[TN][TM][4];
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+#pragma unroll
+                for (int f4 = 0; f4 < 4; ++f4) v[i][j][f4] = src[((i * TM + j) * 4 + f4) * 64];
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+#pragma unroll
+                for (int f4 = 0; f4 < 4; ++f4) {
+                    const float w4[4] = {v[i][j][f4].x, v[i][j][f4].y, v[i][j][f4].z, v[i][j][f4].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        acc[i][j][4 * f4 + e] = first ? w4[e] : acc[i][j][4 * f4 + e] + w4[e];
+                }
+        first = false;
+    }
+    const int64_t n0 = (tl / ntm) * BN + wn * WN, m0 = (tl % ntm) * BM + wm * WM;
+    if constexpr (EPI != EPI_F32) finish_tile_rows<TN, TM, EPI>(p, acc, n0, m0, lane, stage + wave * 64 * STG);
+    else finish_tile<TN, TM, EPI>(p, acc, n0, m0, lane);
 }
 
 template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES>
@@ -640,16 +736,53 @@ int launch_fp8(const GemmArgs& a, int epi, hipStream_t stream) {
     return check_launch("fp8_gemm");
 }
 
-// Tile configuration: 128 x 128 per workgroup (4 waves of 64 x 64, 69 KB of LDS: two workgroups per CU), except
+// Tile configuration: 128 x 128 per workgroup (4 waves of 64 x 64, 54 KB of LDS: two workgroups per CU), except
 // when those tiles just exceed the CU count (cus < T <= 1.25 cus, e.g. 11 x 24 = 264 at 1392 tokens and
-// N = 3072): then 8 CUs would run two tiles and the rest one, and 256 x 128 tiles (8 waves of 64 x 64, 105 KB:
+// N = 3072): then 8 CUs would run two tiles and the rest one, and 256 x 128 tiles (8 waves of 64 x 64, 83 KB:
 // one per CU, 132 of them) finish sooner (measured: 41.7 -> 38.3 us at K = 3072, 136.6 -> 130.4 us at
 // K = 14336). Elsewhere the 128 x 128 tiles are as fast or faster.
+//
+// Stream-K: when even the 256 x 128 tiles leave a quarter of the CUs or more idle and K is long enough to pay for
+// the partial sums (measured: at 1392 tokens, N = 3072, K = 14336, 132 tiles: 113.7 -> 89.9 us; at 2688 tokens,
+// 252 tiles on 256 CUs, the partial sums cost 20 us and nothing is gained), one workgroup per CU takes an equal share of the (tile, 64-deep group) iterations and writes
+// fp32 partial sums of its (at most two) tile pieces; a second launch adds each tile's pieces in a fixed order and
+// applies the epilogue. The sums of a tile are then split in K, so the rounding differs from the one-pass fold
+// (the same fp32 fold per piece, then fp32 adds of the pieces): results are deterministic but not bit-identical to
+// the plain launch.
 #ifndef WDL_GEMM_STAGES
 #define WDL_GEMM_STAGES 4
 #endif
+#ifndef WDL_SK_MIN_GROUPS
+#define WDL_SK_MIN_GROUPS 96
+#endif
+constexpr int SK_NW = 8;                                    // the 256 x 128 configuration
+constexpr int64_t SK_SLOT = SK_NW * 64 * 2 * 2 * 16;        // floats per partial: the workgroup's accumulators
+
+// stream-K workgroups for an M x N x K product (0: plain launch)
+int64_t sk_shares(int64_t Mp, int64_t N, int64_t K) {
+    const int64_t cus = cu_count();
+    if (N % 256 || cus <= 0 || K / 64 < WDL_SK_MIN_GROUPS) return 0;
+    const int64_t Tw = (N / 256) * (Mp / 128);
+    return 4 * Tw <= 3 * cus ? cus : 0;  // the 256 x 128 launch would leave a quarter of the CUs or more idle
+}
+
 int dispatch(const GemmArgs& a, int epi, hipStream_t stream) {
     const int64_t T = (a.N / 128) * (a.Mp / 128), cus = cu_count();
+    const int64_t W = a.part ? sk_shares(a.Mp, a.N, a.K) : 0;
+    if (W) {
+        const int64_t tiles = (a.N / 256) * (a.Mp / 128);
+        w4a4_gemm_sk_kernel<256, 128, 64, 64, SK_NW, WDL_GEMM_STAGES><<<unsigned(W), SK_NW * 64, 0, stream>>>(a);
+        int rc = check_launch("w4a4_gemm stream-K");
+        if (rc) return rc;
+        switch (epi) {
+            case EPI_BF16: w4a4_merge_kernel<256, 128, 64, 64, SK_NW, EPI_BF16><<<unsigned(tiles), SK_NW * 64, 0, stream>>>(a, W); break;
+            case EPI_F32: w4a4_merge_kernel<256, 128, 64, 64, SK_NW, EPI_F32><<<unsigned(tiles), SK_NW * 64, 0, stream>>>(a, W); break;
+            case EPI_RESIDUAL: w4a4_merge_kernel<256, 128, 64, 64, SK_NW, EPI_RESIDUAL><<<unsigned(tiles), SK_NW * 64, 0, stream>>>(a, W); break;
+            case EPI_GELU: w4a4_merge_kernel<256, 128, 64, 64, SK_NW, EPI_GELU><<<unsigned(tiles), SK_NW * 64, 0, stream>>>(a, W); break;
+            default: return fail(WDL_EINVAL, "w4a4_gemm: bad epilogue %d", epi);
+        }
+        return check_launch("w4a4_gemm merge");
+    }
     if (a.N % 256 == 0 && cus > 0 && T > cus && 4 * T <= 5 * cus)
         return launch<256, 128, 64, 64, 8, WDL_GEMM_STAGES>(a, epi, stream);
     return launch<128, 128, 64, 64, 4, WDL_GEMM_STAGES>(a, epi, stream);
@@ -698,10 +831,15 @@ __global__ __launch_bounds__(256) void weight_codes_kernel(const uint4* qw, int6
 
 // epilogue: 0 = bf16 out, 1 = fp32 out, 2 = out(bf16) = bf16(out + bf16(y) * gate) (gated residual in place),
 // 3 = bf16(GELU_tanh(y)) out
+extern "C" int64_t wdl_w4a4_gemm_workspace_bytes(int64_t Mp, int64_t N, int64_t K) {
+    if (Mp <= 0 || Mp % 128 || N <= 0 || K <= 0 || K % 64) return 0;
+    return 2 * sk_shares(Mp, N, K) * SK_SLOT * int64_t(sizeof(float));
+}
+
 extern "C" int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wcodes, const void* wscales,
                              const float* lora, const void* proj_up, const void* bias, int64_t M, int64_t Mp,
                              int64_t N, int64_t K, int64_t rank, void* out, int64_t ldo, int epilogue,
-                             const float* gate, hipStream_t stream) {
+                             const float* gate, void* workspace, hipStream_t stream) {
     if (M < 0 || Mp < M || Mp % 128 || N <= 0 || N % 128 || K <= 0 || K % 64 || K > (int64_t(1) << 30) || ldo < N ||
         ldo % 4)
         return fail(WDL_EINVAL, "w4a4_gemm: bad shape M=%lld Mp=%lld N=%lld K=%lld ldo=%lld", (long long)M,
@@ -721,7 +859,9 @@ extern "C" int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wc
     GemmArgs a{static_cast<const uint8_t*>(qa), static_cast<const uint16_t*>(ascales),
                static_cast<const uint8_t*>(wcodes), static_cast<const uint16_t*>(wscales), lora,
                static_cast<const uint16_t*>(proj_up), static_cast<const uint16_t*>(bias), M, Mp, N, K, out, ldo,
-               gate, nullptr, nullptr};
+               gate, nullptr, nullptr, static_cast<float*>(workspace)};
+    if (reinterpret_cast<uintptr_t>(workspace) % 16)
+        return fail(WDL_EINVAL, "w4a4_gemm: workspace must be 16-byte aligned");
     return dispatch(a, epilogue, stream);
 }
 
@@ -754,6 +894,6 @@ extern "C" int wdl_fp8_gemm(const void* xq, const float* x_scale, const void* wq
         return fail(WDL_EINVAL, "fp8_gemm: bias and out must be 8-byte aligned, row scales 16-byte");
     if (M == 0) return WDL_OK;
     GemmArgs a{static_cast<const uint8_t*>(xq), nullptr, static_cast<const uint8_t*>(wq), nullptr, nullptr, nullptr,
-               static_cast<const uint16_t*>(bias), M, Mp, N, K, out, ldo, nullptr, x_scale, w_scale};
+               static_cast<const uint16_t*>(bias), M, Mp, N, K, out, ldo, nullptr, x_scale, w_scale, nullptr};
     return launch_fp8(a, rows ? EPI_FP8_ROWS : EPI_FP8_TENSOR, stream);
 }

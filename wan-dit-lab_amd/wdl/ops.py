@@ -189,16 +189,20 @@ def as_codes(qweight: torch.Tensor, K: int) -> torch.Tensor:
     raise ValueError(f"qweight {tuple(qweight.shape)} fits neither blocked codes nor [N, {K // 2}] nibbles")
 
 
-def gemm_launch(q, ascales, lora, wcodes, wscales, proj_up, bias, M, out, epilogue=EPI_BF16, gate=None):
-    """W4A4 GEMM on the quantizer's outputs (q, ascales, lora) and tile-blocked fp6 weight codes (weight_codes)."""
+def gemm_launch(q, ascales, lora, wcodes, wscales, proj_up, bias, M, out, epilogue=EPI_BF16, gate=None,
+                stream_k=True):
+    """W4A4 GEMM on the quantizer's outputs (q, ascales, lora) and tile-blocked fp6 weight codes (weight_codes).
+    stream_k=False runs the one-pass launch also for the shapes that the library splits in K."""
     if q.dim() != 4 or wcodes.dim() != 4 or q.shape[2:] != (BLOCK, ROW6) or wcodes.shape[2:] != (BLOCK, ROW6):
         raise ValueError("the W4A4 GEMM takes tile-blocked fp6 operands [rows/128, K/64, 128, 48]")
     Mp, K = q.shape[0] * BLOCK, q.shape[1] * 64
     N = wcodes.shape[0] * BLOCK
     if wcodes.shape[1] != q.shape[1]:
         raise ValueError(f"weight codes {tuple(wcodes.shape)} do not match activations of width {K}")
+    nbytes = _lib.library().wdl_w4a4_gemm_workspace_bytes(Mp, N, K) if stream_k else 0
+    ws = workspace(_GEMM_WS, q.device, nbytes) if nbytes else None
     _lib.call("wdl_w4a4_gemm", ptr(q), ptr(ascales), ptr(wcodes), ptr(wscales), ptr(lora), ptr(proj_up), ptr(bias),
-              M, Mp, N, K, RANK, ptr(out), out.stride(0), epilogue, ptr(gate), stream_of(q))
+              M, Mp, N, K, RANK, ptr(out), out.stride(0), epilogue, ptr(gate), ptr(ws), stream_of(q))
     return out
 
 
@@ -331,6 +335,7 @@ def sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, k, v, at, want_stats=
 
 
 _ATTN_WS: dict = {}
+_GEMM_WS: dict = {}
 
 
 def workspace(cache: dict, device: torch.device, nbytes: int) -> torch.Tensor | None:
