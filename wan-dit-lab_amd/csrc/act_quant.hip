@@ -16,10 +16,12 @@
 //   row_stats  (LN only): one wave per row; LN statistics in a fixed order — lane l owns the 8-value chunks
 //              c = l, l + 64, ... and sums them value by value; the 64 lane sums meet in an xor butterfly
 //              (32, 16, 8, 4, 2, 1); mean = sum / K, var = sum((x - mean)^2) / K, rstd = 1 / sqrt(var + eps).
-//   quant      grid (Mp / 32, ceil(K / 512)): 32 rows x 512 columns per workgroup of 16 waves, thread t owns row
-//              t / 32, groups 2 ((t / 8) % 4) and 2 ((t / 8) % 4) + 1 and their 8 columns (t % 8) * 8 ..; every load
-//              is issued up front (per-column vectors staged in LDS once); the low-rank product over the 512
-//              columns is a 32 x 32 partial (bf16 MFMA on 4 waves, their k-quarters summed in order).
+//   quant      grid (Mp / 32, ceil(K / CB)), CB = 256 columns up to K = 4096, else 512; 32 rows x CB columns per
+//              workgroup of CB threads, thread t owns row t / (CB / 32) and the 32 columns of one half of a 64-group
+//              (the group's two halves in adjacent lanes); every load is issued up front (per-column vectors
+//              staged in LDS once); the codes of a half are packed by one hardware fp6 conversion and written
+//              with two aligned stores; the low-rank product over the CB columns is a 32 x 32 partial (bf16 MFMA
+//              on 4 waves, their k-quarters summed in order).
 //   lora_sum   lora = sum of the column-block partials in increasing order (only when K > 512).
 #include "wdl_common.h"
 
@@ -29,6 +31,7 @@ using namespace wdl;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned u32x6 __attribute__((ext_vector_type(6)));
 
 constexpr int ROWS = 32;
 constexpr int RANK = 32;
@@ -107,10 +110,13 @@ struct QuantArgs {
     uint16_t* v_out;           // bf16 [M, K] copy of v, or null
 };
 
-// CB columns per workgroup, QT = 2 CB threads: CB / 16 threads per row, each 2 of the block's CB / 64 groups
-template <int CB>
-__global__ __launch_bounds__(2 * CB) void quant_kernel(QuantArgs a) {
-    constexpr int QT = 2 * CB;
+// CB columns per workgroup and CB threads: thread t owns row t / (CB / 32) and the 32 columns of half-group
+// hg = t % (CB / 32) of the block (group hg / 2, half hg % 2); the two halves of a group sit in adjacent lanes, so
+// the group maximum takes one exchange. The 32 codes of a half are exactly one lane's fp6 operand of the GEMM: one
+// hardware conversion packs them (value p of the half in field p, 6 bits each) and two aligned stores write them.
+template <int CB, bool LN>
+__global__ __launch_bounds__(CB) void quant_kernel(QuantArgs a) {
+    constexpr int QT = CB, HPR = CB / 32;
     static_assert(CB % 128 == 0 && QT / 64 >= 4, "4 waves for the low-rank product");
     __shared__ __attribute__((aligned(16))) uint16_t tile[ROWS][CB + 8];
     __shared__ float part[4][ROWS * RANK];
@@ -118,41 +124,42 @@ __global__ __launch_bounds__(2 * CB) void quant_kernel(QuantArgs a) {
     __shared__ __attribute__((aligned(16))) float sp[6][CB];  // + 1 / smooth
 
     const int t = threadIdx.x, lane = t % 64, wave = t / 64;
-    // row, 8-column chunk, group pair
-    const int rloc = t / (CB / 16), slot = t % 8, gsel = (t / 8) % (CB / 128);
+    const int rloc = t / HPR, hg = t % HPR, grp = hg / 2, hh = hg % 2;
     const int64_t row = int64_t(blockIdx.x) * ROWS + rloc;
     const bool live = row < a.M;
     const int64_t K = a.K;
     const int64_t c0 = int64_t(blockIdx.y) * CB;
     const int ng = int(min(int64_t(CB), K - c0) / 64);  // 64-groups in this block
-    const bool ln = a.stats != nullptr;
+    const bool gp = grp < ng;                            // the thread's group is in the block
+    const int cl = hg * 32;                              // its first column in the block
 
-    // loads first: 2 x 16 bytes of the row (absent rows read row 0, absent groups a present one; zeroed below),
-    // the row's LN statistics, this block's per-column vectors (thread t < 512: column t)
-    uint4 raw[2];
+    // loads first: 64 bytes of the row (absent rows read row 0, absent groups the block's first; zeroed below),
+    // the row's LN statistics, this block's per-column vectors (thread t: column t)
+    uint4 raw[4];
     if (a.M > 0) {
-        const uint16_t* xr = a.x + (live ? row : 0) * a.ldx + c0 + slot * 8;
+        const uint16_t* xr = a.x + (live ? row : 0) * a.ldx + c0 + (gp ? cl : 0);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int g = 2 * gsel + h;
-            raw[h] = *reinterpret_cast<const uint4*>(xr + (g < ng ? g : 0) * 64);
-        }
+        for (int j = 0; j < 4; ++j) raw[j] = *reinterpret_cast<const uint4*>(xr + 8 * j);
     }
-    const float2 st = (ln && live) ? a.stats[row] : make_float2(0.0f, 0.0f);
-    if (t < CB) {
+    const float2 st = (LN && live) ? a.stats[row] : make_float2(0.0f, 0.0f);
+    {
         const int64_t c = c0 + (t < ng * 64 ? t : 0);
         const uint16_t sm = a.smooth[c];
-        float p1 = 1.0f, p2 = 0.0f, p3 = 0.0f, p4 = 0.0f;
-        if (a.ln_w) p1 = a.ln_w[c];
-        if (a.ln_b) p2 = a.ln_b[c];
-        if (a.mod_scale) p3 = a.mod_scale[c];
-        if (a.mod_shift) p4 = a.mod_shift[c];
+        // an absent LN weight / modulation scale is x 1 and an absent bias / shift is + (-0): exact identities
+        // (x + -0 = x for every x, signed zeros included), so the LayerNorm below needs no per-value branches
+        float p1 = 1.0f, p2 = -0.0f, p3 = 1.0f, p4 = -0.0f;
+        if (LN) {
+            if (a.ln_w) p1 = a.ln_w[c];
+            if (a.ln_b) p2 = a.ln_b[c];
+            if (a.mod_scale) p3 = 1.0f + a.mod_scale[c];
+            if (a.mod_shift) p4 = a.mod_shift[c];
+        }
         if (t < ng * 64) {
             sp[0][t] = bf16_to_f32(sm);
             sp[5][t] = 1.0f / bf16_to_f32(sm);
             sp[1][t] = p1;
             sp[2][t] = p2;
-            sp[3][t] = 1.0f + p3;
+            sp[3][t] = p3;
             sp[4][t] = p4;
         }
     }
@@ -172,80 +179,88 @@ __global__ __launch_bounds__(2 * CB) void quant_kernel(QuantArgs a) {
 
     const float qmax = a.unsigned_q ? 15.0f : 7.0f;
     const float qlo = a.unsigned_q ? 0.0f : -8.0f;
+    const bool present = live && gp && a.M > 0;
+    float v[32];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int g = 2 * gsel + h;
-        const int cl = g * 64 + slot * 8;
-        const bool present = live && g < ng && a.M > 0;
-        float v[8];
-        {
-            const uint32_t w[4] = {raw[h].x, raw[h].y, raw[h].z, raw[h].w};
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t w[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                v[2 * j] = present ? __uint_as_float(w[j] << 16) : 0.0f;
-                v[2 * j + 1] = present ? __uint_as_float(w[j] & 0xffff0000u) : 0.0f;
-            }
+        for (int e = 0; e < 4; ++e) {
+            v[8 * j + 2 * e] = present ? __uint_as_float(w[e] << 16) : 0.0f;
+            v[8 * j + 2 * e + 1] = present ? __uint_as_float(w[e] & 0xffff0000u) : 0.0f;
         }
-        if (ln && present) {
+    }
+    if (LN && present) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
+        for (int j4 = 0; j4 < 8; ++j4) {
+            const float4 w4 = *reinterpret_cast<const float4*>(&sp[1][cl + 4 * j4]);
+            const float4 b4 = *reinterpret_cast<const float4*>(&sp[2][cl + 4 * j4]);
+            const float4 s4 = *reinterpret_cast<const float4*>(&sp[3][cl + 4 * j4]);
+            const float4 h4 = *reinterpret_cast<const float4*>(&sp[4][cl + 4 * j4]);
+            const float wv[4] = {w4.x, w4.y, w4.z, w4.w}, bv4[4] = {b4.x, b4.y, b4.z, b4.w};
+            const float sv[4] = {s4.x, s4.y, s4.z, s4.w}, hv[4] = {h4.x, h4.y, h4.z, h4.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = 4 * j4 + e;
                 float n = (v[j] - st.x) * st.y;
-                if (a.ln_w) n = n * sp[1][cl + j];
-                if (a.ln_b) n = n + sp[2][cl + j];
-                if (a.mod_scale) n = n * sp[3][cl + j];
-                if (a.mod_shift) n = n + sp[4][cl + j];
+                n = n * wv[e];
+                n = n + bv4[e];
+                n = n * sv[e];
+                n = n + hv[e];
                 v[j] = bf16_to_f32(f32_to_bf16(n));
             }
         }
-        uint16_t vb[8];  // v is bf16-valued here: its top 16 bits
+    }
+    // v is bf16-valued here: its top 16 bits, into the low-rank tile (zeros for absent rows / groups) and v_out
 #pragma unroll
-        for (int j = 0; j < 8; ++j) vb[j] = uint16_t(__float_as_uint(v[j]) >> 16);
-        const uint4 packed = make_uint4(vb[0] | (uint32_t(vb[1]) << 16), vb[2] | (uint32_t(vb[3]) << 16),
-                                        vb[4] | (uint32_t(vb[5]) << 16), vb[6] | (uint32_t(vb[7]) << 16));
-        *reinterpret_cast<uint4*>(&tile[rloc][cl]) = packed;  // zeros for absent rows / groups
-        if (g >= ng) continue;  // uniform within each group's 8 lanes
-        const int64_t col = c0 + cl;
-        if (a.v_out && live) *reinterpret_cast<uint4*>(a.v_out + row * K + col) = packed;
-        float u[8];
+    for (int j = 0; j < 4; ++j) {
+        uint32_t pw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            pw[e] = (__float_as_uint(v[8 * j + 2 * e]) >> 16) | (__float_as_uint(v[8 * j + 2 * e + 1]) & 0xffff0000u);
+        const uint4 packed = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+        *reinterpret_cast<uint4*>(&tile[rloc][cl + 8 * j]) = packed;
+        if (a.v_out && live && gp) *reinterpret_cast<uint4*>(a.v_out + row * K + c0 + cl + 8 * j) = packed;
+    }
+    if (gp) {  // uniform within each group's two lanes
+        float u[32];
         float amax = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            u[j] = div_rn(v[j] + a.qshift, sp[0][cl + j], sp[5][cl + j]);
-            amax = fmaxf(amax, fabsf(u[j]));
+        for (int j4 = 0; j4 < 8; ++j4) {
+            const float4 d4 = *reinterpret_cast<const float4*>(&sp[0][cl + 4 * j4]);
+            const float4 r4 = *reinterpret_cast<const float4*>(&sp[5][cl + 4 * j4]);
+            const float dv[4] = {d4.x, d4.y, d4.z, d4.w}, rv[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = 4 * j4 + e;
+                u[j] = div_rn(v[j] + a.qshift, dv[e], rv[e]);
+                amax = fmaxf(amax, fabsf(u[j]));
+            }
         }
-        amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
+        amax = fmaxf(amax, __shfl_xor(amax, 1));  // the group's other half
         const uint16_t sb = f32_to_bf16(amax / qmax);
         const float sc = bf16_to_f32(sb);
         const float rsc = sc > 0.0f ? 1.0f / sc : 0.0f;
-        float qv[8];
+        // fp6 codes of q / 2 (e2m3, exact): even positions go in the first operand, odd in the second, because
+        // the conversion places element i of its first operand in field 2i and of its second in field 2i + 1
+        f32x16 ea, eb;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 32; ++j) {
             const float r = sc > 0.0f ? __builtin_rintf(div_rn(u[j], sc, rsc)) : 0.0f;
-            qv[j] = live ? fminf(fmaxf(r, qlo), qmax) + 0.0f : 0.0f;  // + 0 turns -0 into +0
+            const float qv = live ? fminf(fmaxf(r, qlo), qmax) + 0.0f : 0.0f;  // + 0 turns -0 into +0
+            if (j % 2 == 0) ea[j / 2] = qv * 0.5f;
+            else eb[j / 2] = qv * 0.5f;
         }
-        // fp6 codes (e2m3 of q / 2) of the lane's 8 values: k = 8 slot .. 8 slot + 7 of the group, i.e. half
-        // slot / 4, positions 8 (slot % 4) ..; 48 bits = half bytes 6 (slot % 4) .. + 5, stored as a dword and a
-        // short at their aligned places (the even slots start on a dword, the odd ones on a short)
-        uint32_t c[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) c[j] = act_code6(qv[j]);
-        const uint32_t v0 = c[0] | (c[1] << 6) | (c[2] << 12) | (c[3] << 18);
-        const uint32_t v1 = c[4] | (c[5] << 6) | (c[6] << 12) | (c[7] << 18);
-        const uint32_t lo = v0 | (v1 << 24), hi = v1 >> 8;  // bits 0..31 and 32..47
-        if (row < a.Mp) {
-            uint8_t* dst = a.q + blocked6_offset(row, col / 64, K);
-            const int h = (slot / 4), b = 6 * (slot % 4);
-            if (slot % 2 == 0) {
-                *reinterpret_cast<uint32_t*>(dst + half_byte(h, b)) = lo;
-                *reinterpret_cast<uint16_t*>(dst + half_byte(h, b + 4)) = uint16_t(hi);
-            } else {
-                *reinterpret_cast<uint16_t*>(dst + half_byte(h, b)) = uint16_t(lo);
-                *reinterpret_cast<uint32_t*>(dst + half_byte(h, b + 2)) = (lo >> 16) | (hi << 16);
-            }
-            if (slot == 0) a.ascales[(col / 64) * a.Mp + row] = live ? sb : uint16_t(0);
-        }
+        // early-clobber output: the instruction writes its first result dwords before it has read all of its
+        // sources, and the builtin lets the compiler place the result over the first operand (which corrupted
+        // field 4, measured); scale 1.0 (the values are exact fp6 values)
+        u32x6 w;
+        asm volatile("v_cvt_scalef32_2xpk16_fp6_f32 %0, %1, %2, 1.0" : "=&v"(w) : "v"(ea), "v"(eb));
+        const int64_t gi = (c0 + cl) / 64;
+        uint8_t* dst = a.q + blocked6_offset(row, gi, K);
+        *reinterpret_cast<uint4*>(dst + 16 * hh) = make_uint4(w[0], w[1], w[2], w[3]);
+        *reinterpret_cast<uint2*>(dst + 32 + 8 * hh) = make_uint2(w[4], w[5]);
+        if (hh == 0) a.ascales[gi * a.Mp + row] = live ? sb : uint16_t(0);
     }
     if (!a.pdt) return;
     __syncthreads();
@@ -321,8 +336,14 @@ extern "C" int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K
                 unsigned_q, static_cast<const uint16_t*>(proj_down_t), static_cast<uint8_t*>(q),
                 static_cast<uint16_t*>(ascales), nb > 1 ? workspace : lora, ln ? stats : nullptr, mod_shift,
                 mod_scale, ln_w, ln_b, static_cast<uint16_t*>(v_out)};
-    if (CB == 256) quant_kernel<256><<<dim3(unsigned(Mp / ROWS), unsigned(nb)), 512, 0, stream>>>(a);
-    else quant_kernel<512><<<dim3(unsigned(Mp / ROWS), unsigned(nb)), 1024, 0, stream>>>(a);
+    const dim3 grid(unsigned(Mp / ROWS), unsigned(nb));
+    if (CB == 256) {
+        if (ln) quant_kernel<256, true><<<grid, 256, 0, stream>>>(a);
+        else quant_kernel<256, false><<<grid, 256, 0, stream>>>(a);
+    } else {
+        if (ln) quant_kernel<512, true><<<grid, 512, 0, stream>>>(a);
+        else quant_kernel<512, false><<<grid, 512, 0, stream>>>(a);
+    }
     int rc = check_launch("act_quant_w4 quant");
     if (rc || !proj_down_t || nb == 1) return rc;
     const int64_t n = Mp * RANK;
