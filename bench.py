@@ -67,6 +67,8 @@ class Step:
             self.caches.append(c)
         context = torch.randn(CONTEXT, DIM, generator=g, device=device).to(torch.bfloat16)
         self.ctx = [b.prepare_context(context) for b in self.blocks]
+        # every block's modulation table, stacked: e = time_in + modulation for all blocks is one add per step
+        self.modulation = torch.stack([b.p["modulation"] for b in self.blocks])
         self.freq = freqs(128, 1024, device)
         bf = torch.bfloat16
         r = lambda *s: torch.randn(*s, generator=g, device=device)
@@ -98,8 +100,8 @@ class Step:
         temb = torch.cat([torch.cos(theta), torch.sin(theta)], dim=1).to(torch.bfloat16)
         temb = F.linear(F.silu(F.linear(temb, self.w_t1, self.b_t1)), self.w_t2, self.b_t2)
         e0 = F.linear(F.silu(temb), self.w_proj, self.b_proj).float().view(6, DIM)
-        for blk, cache, ctx in zip(self.blocks, self.caches, self.ctx):
-            e = e0 + blk.p["modulation"]
+        e_all = e0 + self.modulation  # [blocks, 6, DIM]: the same sums as e0 + modulation per block
+        for blk, cache, ctx, e in zip(self.blocks, self.caches, self.ctx, e_all):
             blk.forward(self.X, e, GRID, self.freq, self.start_frame, cache, ctx)
         # head + unpatchify (head.py:13-18; model.py:81-84)
         shift, scale = (self.head_mod + temb.float()).chunk(2, dim=0)

@@ -164,6 +164,14 @@ int wdl_sage_attn(const void* q_i8, int64_t ldq, const float* q_scale, const voi
                   const void* v_fp8, const float* v_scale, int64_t n, int64_t L, int64_t heads, float sm_scale,
                   void* out, int64_t ldo, void* workspace, wdl_stream_t stream);
 
+/* wdl_sage_attn with Q given in bf16 [n, heads, 128] (row stride ldq): the kernel quantizes it by Sage's per-thread
+ * int8 rule of wdl_quant_q (kernels/sage_kv.py:112-124) as it loads each query tile, so the result is bit-identical
+ * to wdl_quant_q followed by wdl_sage_attn, without the int8 Q round trip through memory. Replaces the pair
+ * quant_q + live::sage_sm89 that sage_kv_attend runs (kernels/sage_kv.py:170-176). Same workspace rules. */
+int wdl_sage_attn_q16(const void* q_bf16, int64_t ldq, const void* k_i8, const float* k_scale, const void* v_fp8,
+                      const float* v_scale, int64_t n, int64_t L, int64_t heads, float sm_scale, void* out,
+                      int64_t ldo, void* workspace, wdl_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -135,6 +135,28 @@ def test_attention_split_tiles_merge_across_workgroups(gpu):
         assert osage.rel_err(got, exact) < 1.2 * osage.rel_err(emul8, exact) + 1e-3, hh
 
 
+@pytest.mark.parametrize("at,n,H", [(200, 150, 3), (0, 1, 2), (127, 70, 2), (8352, 1392, 24)])
+def test_attention_q16_is_quant_q_then_attention(gpu, at, n, H):
+    """wdl_sage_attn_q16 (Q quantized inside the attention kernel) against wdl_quant_q + wdl_sage_attn on the same
+    operands: bit-identical outputs, also for a row-strided Q (a column slice of a wider buffer), ragged query
+    counts and the split-tile launch (11 x 24 tiles on 256 CUs)."""
+    from wdl import ops
+
+    Q, k, ks, v, vs, at, K, V = setup(at, n, nq=n, H=H, seed=5)
+    Qc, k, ks, v, vs, K, V = cuda(Q, k, ks, v, vs, K, V)
+    prep = ops.sage_prep_launch(k.view(torch.uint8), ks, v.view(torch.uint8), vs, K[0].flatten(1), V[0].flatten(1),
+                                at)
+    q2 = Qc[0].flatten(1)
+    wide = torch.zeros(n, H * 128 + 64, device="cuda", dtype=torch.bfloat16)
+    wide[:, 32:32 + H * 128] = q2
+    for q in (q2, wide[:, 32:32 + H * 128]):
+        q_i8, q_sc = ops.quant_q_launch(q2, H)
+        ref = ops.sage_attn_launch(q_i8, q_sc, prep, at + n, 128 ** -0.5)
+        got = ops.sage_attn_q16_launch(q, prep, at + n, 128 ** -0.5)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), (at, n, H, q.stride(0))
+
+
 def test_attention_single_key_and_ragged_lengths(gpu):
     from wdl import sage_kv
 

@@ -16,13 +16,13 @@
 //   row_stats  (LN only): one wave per row; LN statistics in a fixed order — lane l owns the 8-value chunks
 //              c = l, l + 64, ... and sums them value by value; the 64 lane sums meet in an xor butterfly
 //              (32, 16, 8, 4, 2, 1); mean = sum / K, var = sum((x - mean)^2) / K, rstd = 1 / sqrt(var + eps).
-//   quant      grid (Mp / 32, ceil(K / CB)), CB = 256 columns up to K = 4096, else 512; 32 rows x CB columns per
-//              workgroup of CB threads, thread t owns row t / (CB / 32) and the 32 columns of one half of a 64-group
-//              (the group's two halves in adjacent lanes); every load is issued up front (per-column vectors
-//              staged in LDS once); the codes of a half are packed by one hardware fp6 conversion and written
-//              with two aligned stores; the low-rank product over the CB columns is a 32 x 32 partial (bf16 MFMA
-//              on 4 waves, their k-quarters summed in order).
-//   lora_sum   lora = sum of the column-block partials in increasing order (only when K > 512).
+//   quant      grid (Mp / 32, ceil(K / 64 / S)): 32 rows x S 64-groups per workgroup of S waves (S = 4 up to
+//              K = 4096, 8 above), each wave one group of the 32 rows; lane l owns row l % 32 and half
+//              l / 32 of a group (64 bytes of x, loaded up front with the matching 64 bytes of proj_down^T); the
+//              group maximum is one exchange between lanes l and l ^ 32, the codes of a half are packed by one
+//              hardware fp6 conversion and written with two aligned stores, and the low-rank product runs on the
+//              values in registers (bf16 MFMA), the waves' 32 x 32 partials summed in wave order.
+//   lora_sum   lora = sum of the column-block partials in increasing order (only when K / 64 > S).
 #include "wdl_common.h"
 
 namespace {
@@ -35,9 +35,11 @@ typedef unsigned u32x6 __attribute__((ext_vector_type(6)));
 
 constexpr int ROWS = 32;
 constexpr int RANK = 32;
-// Columns per workgroup of the quant launch: 256 up to K = 4096 (more, smaller workgroups: at 1392 rows and
-// K = 3072, 528 of them instead of 264 on 256 CUs, several resident per CU), 512 above.
-constexpr int cb_of(int64_t K) { return K <= 4096 ? 256 : 512; }
+// Shape of the quant launch's workgroups: WAVES waves on 32 rows, G 64-groups per wave (S = WAVES * G groups per
+// workgroup), one shape up to K = 4096 and one above. Measured at 1392 rows: 4 x 1 at K = 3072 (10.0 us; 8 x 1,
+// 4 x 2 and 16 x 1 take 10.8 - 12.6 us), 8 x 1 at K = 14336 (22.1 us; 8 x 2, 4 x 2 and 16 x 1 take 25 - 33 us).
+constexpr int SMALL_WAVES = 4, SMALL_G = 1, BIG_WAVES = 8, BIG_G = 1;
+constexpr int groups_per_block(int64_t K) { return K <= 4096 ? SMALL_WAVES * SMALL_G : BIG_WAVES * BIG_G; }
 constexpr int MAXCH = 8; // row_stats keeps up to 8 chunks per lane in registers (K <= 4096)
 
 __device__ __forceinline__ void load8(const uint16_t* p, float* f) {
@@ -110,119 +112,134 @@ struct QuantArgs {
     uint16_t* v_out;           // bf16 [M, K] copy of v, or null
 };
 
-// CB columns per workgroup and CB threads: thread t owns row t / (CB / 32) and the 32 columns of half-group
-// hg = t % (CB / 32) of the block (group hg / 2, half hg % 2); the two halves of a group sit in adjacent lanes, so
-// the group maximum takes one exchange. The 32 codes of a half are exactly one lane's fp6 operand of the GEMM: one
-// hardware conversion packs them (value p of the half in field p, 6 bits each) and two aligned stores write them.
-template <int CB, bool LN>
-__global__ __launch_bounds__(CB) void quant_kernel(QuantArgs a) {
-    constexpr int QT = CB, HPR = CB / 32;
-    static_assert(CB % 128 == 0 && QT / 64 >= 4, "4 waves for the low-rank product");
-    __shared__ __attribute__((aligned(16))) uint16_t tile[ROWS][CB + 8];
-    __shared__ float part[4][ROWS * RANK];
-    // per-column vectors of this block's columns: smooth, LN weight, LN bias, 1 + mod_scale, mod_shift
-    __shared__ __attribute__((aligned(16))) float sp[6][CB];  // + 1 / smooth
+// Workgroups of WAVES waves on the same 32 rows; wave w takes the 64-groups w, w + WAVES, ... (G of them) of the
+// workgroup's S = WAVES * G groups. Lane l of a wave owns row l % 32 and half h = l / 32 of each of its groups (32
+// columns, 64 bytes of x): the group maximum is one exchange with lane l ^ 32, the 32 codes of the half are one
+// hardware fp6 conversion, and the 32 lanes of a half write the 48-byte group rows of 32 consecutive tokens (1.5 KB
+// contiguous in the tile-blocked layout). The lane's bf16 values are also the A operand of the low-rank MFMA
+// (32 x 32 x 16: lane l supplies row l % 32 and k-slots 8h..8h+7, here columns 32h + 8s .. 32h + 8s + 7 of the
+// group for the s-th of its 4 MFMAs) and the B operand comes from proj_down^T with the same column map, so the
+// product needs no LDS tile; the waves' 32 x 32 partials are summed in wave order through LDS at the end.
+template <int WAVES, int G, bool LN>
+__global__ __launch_bounds__(64 * WAVES) void quant_kernel(QuantArgs a) {
+    constexpr int S = WAVES * G, NT = 64 * WAVES, SC = 64 * S;  // groups, threads and columns of the workgroup
+    // per-column vectors of the workgroup's columns: smooth, LN weight, LN bias, 1 + mod_scale, mod_shift,
+    // 1 / smooth
+    __shared__ __attribute__((aligned(16))) float sp[6][SC];
+    __shared__ float part[WAVES][ROWS * RANK];
 
     const int t = threadIdx.x, lane = t % 64, wave = t / 64;
-    const int rloc = t / HPR, hg = t % HPR, grp = hg / 2, hh = hg % 2;
-    const int64_t row = int64_t(blockIdx.x) * ROWS + rloc;
+    const int r = lane % 32, h = lane / 32;
+    const int64_t row = int64_t(blockIdx.x) * ROWS + r;
     const bool live = row < a.M;
     const int64_t K = a.K;
-    const int64_t c0 = int64_t(blockIdx.y) * CB;
-    const int ng = int(min(int64_t(CB), K - c0) / 64);  // 64-groups in this block
-    const bool gp = grp < ng;                            // the thread's group is in the block
-    const int cl = hg * 32;                              // its first column in the block
+    const int64_t gb = int64_t(blockIdx.y) * S;             // first group of the workgroup
+    const int nsg = int(min(int64_t(S), K / 64 - gb));     // its groups present in the matrix
 
-    // loads first: 64 bytes of the row (absent rows read row 0, absent groups the block's first; zeroed below),
-    // the row's LN statistics, this block's per-column vectors (thread t: column t)
-    uint4 raw[4];
-    if (a.M > 0) {
-        const uint16_t* xr = a.x + (live ? row : 0) * a.ldx + c0 + (gp ? cl : 0);
+    // loads first: each present group's 64 bytes of the row (absent rows read row 0; zeroed below) and of
+    // proj_down^T row r, the row's LN statistics, the workgroup's per-column vectors (thread t: columns t + NT i)
+    uint4 raw[G][4], pd[G][4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) raw[j] = *reinterpret_cast<const uint4*>(xr + 8 * j);
+    for (int j = 0; j < G; ++j) {
+        const int gl = wave + WAVES * j;
+        if (gl >= nsg) continue;  // uniform over the wave
+        const int64_t col = (gb + gl) * 64 + 32 * h;
+        if (a.M > 0) {
+            const uint16_t* xr = a.x + (live ? row : 0) * a.ldx + col;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) raw[j][i] = *reinterpret_cast<const uint4*>(xr + 8 * i);
+        }
+        if (a.pdt) {
+            const uint16_t* pr = a.pdt + int64_t(r) * K + col;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pd[j][i] = *reinterpret_cast<const uint4*>(pr + 8 * i);
+        }
     }
     const float2 st = (LN && live) ? a.stats[row] : make_float2(0.0f, 0.0f);
-    {
-        const int64_t c = c0 + (t < ng * 64 ? t : 0);
-        const uint16_t sm = a.smooth[c];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+        const int c = t + NT * i;
+        if (c >= nsg * 64) continue;
+        const int64_t cg = gb * 64 + c;
+        const float sm = bf16_to_f32(a.smooth[cg]);
         // an absent LN weight / modulation scale is x 1 and an absent bias / shift is + (-0): exact identities
         // (x + -0 = x for every x, signed zeros included), so the LayerNorm below needs no per-value branches
         float p1 = 1.0f, p2 = -0.0f, p3 = 1.0f, p4 = -0.0f;
         if (LN) {
-            if (a.ln_w) p1 = a.ln_w[c];
-            if (a.ln_b) p2 = a.ln_b[c];
-            if (a.mod_scale) p3 = 1.0f + a.mod_scale[c];
-            if (a.mod_shift) p4 = a.mod_shift[c];
+            if (a.ln_w) p1 = a.ln_w[cg];
+            if (a.ln_b) p2 = a.ln_b[cg];
+            if (a.mod_scale) p3 = 1.0f + a.mod_scale[cg];
+            if (a.mod_shift) p4 = a.mod_shift[cg];
         }
-        if (t < ng * 64) {
-            sp[0][t] = bf16_to_f32(sm);
-            sp[5][t] = 1.0f / bf16_to_f32(sm);
-            sp[1][t] = p1;
-            sp[2][t] = p2;
-            sp[3][t] = p3;
-            sp[4][t] = p4;
-        }
-    }
-    // the low-rank operand (waves 0..3: B = proj_down^T rows lane % 32, k = CB/4 wave + 16 s + 8 (lane / 32));
-    // columns past the block's groups read column 0 of the block (their A side is zero)
-    constexpr int NS = CB / 64;  // MFMAs (k = 16) per wave
-    bf16x8 bv[NS];
-    if (a.pdt && wave < 4) {
-#pragma unroll
-        for (int s8 = 0; s8 < NS; ++s8) {
-            int kk = wave * (CB / 4) + s8 * 16 + 8 * (lane / 32);
-            kk = kk < ng * 64 ? kk : 0;
-            bv[s8] = *reinterpret_cast<const bf16x8*>(a.pdt + int64_t(lane % 32) * K + c0 + kk);
-        }
+        sp[0][c] = sm;
+        sp[1][c] = p1;
+        sp[2][c] = p2;
+        sp[3][c] = p3;
+        sp[4][c] = p4;
+        sp[5][c] = 1.0f / sm;
     }
     __syncthreads();
 
     const float qmax = a.unsigned_q ? 15.0f : 7.0f;
     const float qlo = a.unsigned_q ? 0.0f : -8.0f;
-    const bool present = live && gp && a.M > 0;
-    float v[32];
+    const bool present = live && a.M > 0;
+    f32x16 acc = {};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t w[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+    for (int j = 0; j < G; ++j) {
+        const int gl = wave + WAVES * j;
+        if (gl >= nsg) continue;
+        const int cl = 64 * gl + 32 * h;  // the lane's first column in the workgroup
+        float v[32];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            v[8 * j + 2 * e] = present ? __uint_as_float(w[e] << 16) : 0.0f;
-            v[8 * j + 2 * e + 1] = present ? __uint_as_float(w[e] & 0xffff0000u) : 0.0f;
-        }
-    }
-    if (LN && present) {
-#pragma unroll
-        for (int j4 = 0; j4 < 8; ++j4) {
-            const float4 w4 = *reinterpret_cast<const float4*>(&sp[1][cl + 4 * j4]);
-            const float4 b4 = *reinterpret_cast<const float4*>(&sp[2][cl + 4 * j4]);
-            const float4 s4 = *reinterpret_cast<const float4*>(&sp[3][cl + 4 * j4]);
-            const float4 h4 = *reinterpret_cast<const float4*>(&sp[4][cl + 4 * j4]);
-            const float wv[4] = {w4.x, w4.y, w4.z, w4.w}, bv4[4] = {b4.x, b4.y, b4.z, b4.w};
-            const float sv[4] = {s4.x, s4.y, s4.z, s4.w}, hv[4] = {h4.x, h4.y, h4.z, h4.w};
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t w[4] = {raw[j][i].x, raw[j][i].y, raw[j][i].z, raw[j][i].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int j = 4 * j4 + e;
-                float n = (v[j] - st.x) * st.y;
-                n = n * wv[e];
-                n = n + bv4[e];
-                n = n * sv[e];
-                n = n + hv[e];
-                v[j] = bf16_to_f32(f32_to_bf16(n));
+                v[8 * i + 2 * e] = present ? __uint_as_float(w[e] << 16) : 0.0f;
+                v[8 * i + 2 * e + 1] = present ? __uint_as_float(w[e] & 0xffff0000u) : 0.0f;
             }
         }
-    }
-    // v is bf16-valued here: its top 16 bits, into the low-rank tile (zeros for absent rows / groups) and v_out
+        if (LN && present) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        uint32_t pw[4];
+            for (int j4 = 0; j4 < 8; ++j4) {
+                const float4 w4 = *reinterpret_cast<const float4*>(&sp[1][cl + 4 * j4]);
+                const float4 b4 = *reinterpret_cast<const float4*>(&sp[2][cl + 4 * j4]);
+                const float4 s4 = *reinterpret_cast<const float4*>(&sp[3][cl + 4 * j4]);
+                const float4 h4 = *reinterpret_cast<const float4*>(&sp[4][cl + 4 * j4]);
+                const float wv[4] = {w4.x, w4.y, w4.z, w4.w}, bv4[4] = {b4.x, b4.y, b4.z, b4.w};
+                const float sv[4] = {s4.x, s4.y, s4.z, s4.w}, hv[4] = {h4.x, h4.y, h4.z, h4.w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            pw[e] = (__float_as_uint(v[8 * j + 2 * e]) >> 16) | (__float_as_uint(v[8 * j + 2 * e + 1]) & 0xffff0000u);
-        const uint4 packed = make_uint4(pw[0], pw[1], pw[2], pw[3]);
-        *reinterpret_cast<uint4*>(&tile[rloc][cl + 8 * j]) = packed;
-        if (a.v_out && live && gp) *reinterpret_cast<uint4*>(a.v_out + row * K + c0 + cl + 8 * j) = packed;
-    }
-    if (gp) {  // uniform within each group's two lanes
+                for (int e = 0; e < 4; ++e) {
+                    const int k = 4 * j4 + e;
+                    float n = (v[k] - st.x) * st.y;
+                    n = n * wv[e];
+                    n = n + bv4[e];
+                    n = n * sv[e];
+                    n = n + hv[e];
+                    v[k] = bf16_to_f32(f32_to_bf16(n));
+                }
+            }
+        }
+        // v is bf16-valued here: its top 16 bits, packed in pairs, are the MFMA operand and the v_out row
+        const int64_t g = gb + gl;
+        uint32_t pw[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            pw[k] = (__float_as_uint(v[2 * k]) >> 16) | (__float_as_uint(v[2 * k + 1]) & 0xffff0000u);
+        if (a.v_out && live) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<uint4*>(a.v_out + row * K + g * 64 + 32 * h + 8 * i) =
+                    make_uint4(pw[4 * i], pw[4 * i + 1], pw[4 * i + 2], pw[4 * i + 3]);
+        }
+        if (a.pdt) {
+#pragma unroll
+            for (int s8 = 0; s8 < 4; ++s8) {
+                const uint4 av = make_uint4(pw[4 * s8], pw[4 * s8 + 1], pw[4 * s8 + 2], pw[4 * s8 + 3]);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av),
+                                                              __builtin_bit_cast(bf16x8, pd[j][s8]), acc, 0, 0, 0);
+            }
+        }
         float u[32];
         float amax = 0.0f;
 #pragma unroll
@@ -232,12 +249,12 @@ __global__ __launch_bounds__(CB) void quant_kernel(QuantArgs a) {
             const float dv[4] = {d4.x, d4.y, d4.z, d4.w}, rv[4] = {r4.x, r4.y, r4.z, r4.w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int j = 4 * j4 + e;
-                u[j] = div_rn(v[j] + a.qshift, dv[e], rv[e]);
-                amax = fmaxf(amax, fabsf(u[j]));
+                const int k = 4 * j4 + e;
+                u[k] = div_rn(v[k] + a.qshift, dv[e], rv[e]);
+                amax = fmaxf(amax, fabsf(u[k]));
             }
         }
-        amax = fmaxf(amax, __shfl_xor(amax, 1));  // the group's other half
+        amax = fmaxf(amax, __shfl_xor(amax, 32));  // the group's other half
         const uint16_t sb = f32_to_bf16(amax / qmax);
         const float sc = bf16_to_f32(sb);
         const float rsc = sc > 0.0f ? 1.0f / sc : 0.0f;
@@ -245,42 +262,34 @@ __global__ __launch_bounds__(CB) void quant_kernel(QuantArgs a) {
         // the conversion places element i of its first operand in field 2i and of its second in field 2i + 1
         f32x16 ea, eb;
 #pragma unroll
-        for (int j = 0; j < 32; ++j) {
-            const float r = sc > 0.0f ? __builtin_rintf(div_rn(u[j], sc, rsc)) : 0.0f;
-            const float qv = live ? fminf(fmaxf(r, qlo), qmax) + 0.0f : 0.0f;  // + 0 turns -0 into +0
-            if (j % 2 == 0) ea[j / 2] = qv * 0.5f;
-            else eb[j / 2] = qv * 0.5f;
+        for (int k = 0; k < 32; ++k) {
+            const float rq = sc > 0.0f ? __builtin_rintf(div_rn(u[k], sc, rsc)) : 0.0f;
+            const float qv = live ? fminf(fmaxf(rq, qlo), qmax) + 0.0f : 0.0f;  // + 0 turns -0 into +0
+            if (k % 2 == 0) ea[k / 2] = qv * 0.5f;
+            else eb[k / 2] = qv * 0.5f;
         }
         // early-clobber output: the instruction writes its first result dwords before it has read all of its
         // sources, and the builtin lets the compiler place the result over the first operand (which corrupted
         // field 4, measured); scale 1.0 (the values are exact fp6 values)
         u32x6 w;
         asm volatile("v_cvt_scalef32_2xpk16_fp6_f32 %0, %1, %2, 1.0" : "=&v"(w) : "v"(ea), "v"(eb));
-        const int64_t gi = (c0 + cl) / 64;
-        uint8_t* dst = a.q + blocked6_offset(row, gi, K);
-        *reinterpret_cast<uint4*>(dst + 16 * hh) = make_uint4(w[0], w[1], w[2], w[3]);
-        *reinterpret_cast<uint2*>(dst + 32 + 8 * hh) = make_uint2(w[4], w[5]);
-        if (hh == 0) a.ascales[gi * a.Mp + row] = live ? sb : uint16_t(0);
+        uint8_t* dst = a.q + blocked6_offset(row, g, K);
+        *reinterpret_cast<uint4*>(dst + 16 * h) = make_uint4(w[0], w[1], w[2], w[3]);
+        *reinterpret_cast<uint2*>(dst + 32 + 8 * h) = make_uint2(w[4], w[5]);
+        if (h == 0) a.ascales[g * a.Mp + row] = live ? sb : uint16_t(0);
     }
     if (!a.pdt) return;
-    __syncthreads();
-    if (wave < 4) {
-        // wave w: k = CB/4 w .. of this block, 16 per MFMA; A = v rows (lane % 32), B = proj_down^T rows
-        f32x16 acc = {};
+    // lane l holds the partial of token 8 (i / 4) + 4 h + i % 4 and rank r in acc[i]
 #pragma unroll
-        for (int s8 = 0; s8 < NS; ++s8) {
-            const int kk = wave * (CB / 4) + s8 * 16 + 8 * (lane / 32);
-            const bf16x8 av = *reinterpret_cast<const bf16x8*>(&tile[lane % 32][kk]);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv[s8], acc, 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) part[wave][(8 * (i / 4) + 4 * (lane / 32) + (i % 4)) * RANK + lane % 32] = acc[i];
-    }
+    for (int i = 0; i < 16; ++i) part[wave][(8 * (i / 4) + 4 * h + (i % 4)) * RANK + r] = acc[i];
     __syncthreads();
     float* dst = a.lora + int64_t(blockIdx.y) * a.Mp * RANK;
-    for (int e = t; e < ROWS * RANK; e += QT) {
-        const int64_t r = int64_t(blockIdx.x) * ROWS + e / RANK;
-        if (r < a.Mp) dst[r * RANK + e % RANK] = r < a.M ? (part[0][e] + part[1][e]) + (part[2][e] + part[3][e]) : 0.0f;
+    for (int e = t; e < ROWS * RANK; e += NT) {
+        const int64_t rr = int64_t(blockIdx.x) * ROWS + e / RANK;
+        float sum = part[0][e];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) sum = sum + part[w][e];
+        dst[rr * RANK + e % RANK] = rr < a.M ? sum : 0.0f;
     }
 }
 
@@ -305,7 +314,7 @@ __global__ void lora_sum_kernel(const float* part, int nb, int64_t n, float* out
 }  // namespace
 
 extern "C" int64_t wdl_act_quant_workspace_floats(int64_t Mp, int64_t K) {
-    const int64_t CB = cb_of(K), nb = (K + CB - 1) / CB;
+    const int64_t S = groups_per_block(K), nb = (K / 64 + S - 1) / S;
     return (nb > 1 ? nb * Mp * RANK : 0) + 2 * Mp;
 }
 
@@ -324,7 +333,7 @@ extern "C" int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K
     if ((reinterpret_cast<uintptr_t>(x) | (ldx * 2)) % 16)
         return fail(WDL_EINVAL, "act_quant_w4: x rows must be 16-byte aligned");
     if (Mp == 0) return WDL_OK;
-    const int CB = cb_of(K), nb = int((K + CB - 1) / CB);
+    const int S = groups_per_block(K), nb = int((K / 64 + S - 1) / S);
     float2* stats = reinterpret_cast<float2*>(workspace + (nb > 1 ? int64_t(nb) * Mp * RANK : 0));
     if (ln && M > 0) {
         row_stats_kernel<<<unsigned((M + 3) / 4), 256, 0, stream>>>(static_cast<const uint16_t*>(x), ldx, M, K, eps,
@@ -337,12 +346,12 @@ extern "C" int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K
                 static_cast<uint16_t*>(ascales), nb > 1 ? workspace : lora, ln ? stats : nullptr, mod_shift,
                 mod_scale, ln_w, ln_b, static_cast<uint16_t*>(v_out)};
     const dim3 grid(unsigned(Mp / ROWS), unsigned(nb));
-    if (CB == 256) {
-        if (ln) quant_kernel<256, true><<<grid, 256, 0, stream>>>(a);
-        else quant_kernel<256, false><<<grid, 256, 0, stream>>>(a);
+    if (K <= 4096) {
+        if (ln) quant_kernel<SMALL_WAVES, SMALL_G, true><<<grid, 64 * SMALL_WAVES, 0, stream>>>(a);
+        else quant_kernel<SMALL_WAVES, SMALL_G, false><<<grid, 64 * SMALL_WAVES, 0, stream>>>(a);
     } else {
-        if (ln) quant_kernel<512, true><<<grid, 512, 0, stream>>>(a);
-        else quant_kernel<512, false><<<grid, 512, 0, stream>>>(a);
+        if (ln) quant_kernel<BIG_WAVES, BIG_G, true><<<grid, 64 * BIG_WAVES, 0, stream>>>(a);
+        else quant_kernel<BIG_WAVES, BIG_G, false><<<grid, 64 * BIG_WAVES, 0, stream>>>(a);
     }
     int rc = check_launch("act_quant_w4 quant");
     if (rc || !proj_down_t || nb == 1) return rc;

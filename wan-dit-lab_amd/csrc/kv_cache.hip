@@ -65,6 +65,44 @@ __global__ __launch_bounds__(256) void kv_append_kernel(Rows k, Rows v, int64_t 
     if (lane == 0) r.scale[target] = scale;
 }
 
+// Rows of D = 128 two-byte elements, unit element stride and 16-byte aligned: 16 lanes per row, lane l loads
+// elements 8l .. 8l + 7 with one 16-byte load and stores their 8 codes with one 8-byte store (the same values as
+// kv_append_kernel: the row maximum does not depend on the lane map).
+template <typename T>
+__global__ __launch_bounds__(256) void kv_append_vec_kernel(Rows k, Rows v, int64_t n, int64_t H, int64_t rows,
+                                                            int64_t capacity, int64_t at) {
+    const Rows& r = blockIdx.y == 0 ? k : v;
+    const int lane = threadIdx.x % 16;
+    const int64_t row = int64_t(blockIdx.x) * 16 + threadIdx.x / 16;
+    const bool live = row < rows;
+    const int64_t h = row % H, tok = (row / H) % n, b = row / (H * n);
+    uint4 raw = make_uint4(0, 0, 0, 0);
+    if (live)
+        raw = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(r.x) + b * r.s0 + tok * r.s1 + h * r.s2 +
+                                              8 * lane);
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+    float val[8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        val[2 * j] = to_f32<T>(uint16_t(w[j] & 0xffffu));
+        val[2 * j + 1] = to_f32<T>(uint16_t(w[j] >> 16));
+        amax = fmaxf(amax, fmaxf(fabsf(val[2 * j]), fabsf(val[2 * j + 1])));
+    }
+    amax = group_max<16>(amax);
+    const float scale = fmaxf(amax, 1e-12f) / 448.0f;
+    if (!live) return;
+    const int64_t target = (b * capacity + at + tok) * H + h;
+    uint32_t c[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+        c[j] = uint32_t(f32_to_e4m3(val[4 * j] / scale)) | (uint32_t(f32_to_e4m3(val[4 * j + 1] / scale)) << 8) |
+               (uint32_t(f32_to_e4m3(val[4 * j + 2] / scale)) << 16) |
+               (uint32_t(f32_to_e4m3(val[4 * j + 3] / scale)) << 24);
+    *reinterpret_cast<uint2*>(r.cache + target * 128 + 8 * lane) = make_uint2(c[0], c[1]);
+    if (lane == 0) r.scale[target] = scale;
+}
+
 template <typename T, int G, int E>
 void launch_rows(const Rows& k, const Rows& v, int two, int64_t n, int64_t H, int64_t D, int64_t rows,
                  int64_t capacity, int64_t at, hipStream_t stream) {
@@ -76,7 +114,14 @@ void launch_rows(const Rows& k, const Rows& v, int two, int64_t n, int64_t H, in
 template <typename T>
 int dispatch(const Rows& k, const Rows& v, int two, int64_t n, int64_t H, int64_t D, int64_t rows,
              int64_t capacity, int64_t at, hipStream_t stream) {
-    if (D <= 64) {
+    const auto vec_ok = [](const Rows& r) {
+        return r.s3 == 1 && (reinterpret_cast<uintptr_t>(r.x) | ((r.s0 | r.s1 | r.s2) * 2)) % 16 == 0 &&
+               reinterpret_cast<uintptr_t>(r.cache) % 8 == 0;
+    };
+    if (sizeof(typename Elem<T>::raw) == 2 && D == 128 && vec_ok(k) && vec_ok(v)) {
+        const dim3 grid(unsigned((rows + 15) / 16), unsigned(two));
+        kv_append_vec_kernel<T><<<grid, 256, 0, stream>>>(k, v, n, H, rows, capacity, at);
+    } else if (D <= 64) {
         launch_rows<T, 16, 4>(k, v, two, n, H, D, rows, capacity, at, stream);
     } else if (D <= 128) {
         launch_rows<T, 16, 8>(k, v, two, n, H, D, rows, capacity, at, stream);

@@ -64,6 +64,7 @@ struct AttnArgs {
     int64_t W;            // workgroups
     int64_t qtiles;       // query tiles (128 queries) per head
     int64_t D;            // tiles run whole (the first D of the T = qtiles * H); the other T - D are split
+    const uint16_t* qb;   // bf16 Q [n, H, 128] (row stride ldq) quantized in the kernel, or null (q, q_scale given)
 };
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -145,19 +146,11 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
         const int64_t q = qt * 128 + sub * 32 + lane % 32;
         const bool qlive = q < a.n;
 
-        // Q fragment: B operand of S^T = K Q^T, chunk c covers d = 32c .. 32c + 31, lane half -> 16 of them
+        // Q fragment (B operand of S^T = K Q^T, chunk c covers d = 32c .. 32c + 31, lane half -> 16 of them) and
+        // scale, filled after the ring prologue is issued (the Q loads and the first K / V blocks are in flight
+        // together)
         i32x4 qf[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            if (qlive) {
-                const uint4 r = *reinterpret_cast<const uint4*>(a.q + q * a.ldq + h * D + 32 * c + 16 * half);
-                qf[c] = i32x4{int(r.x), int(r.y), int(r.z), int(r.w)};
-            } else {
-                qf[c] = i32x4{0, 0, 0, 0};
-            }
-        }
-        const float qs = qlive ? a.q_scale[h * qblocks8 + (q / 32) * 8 + q % 8] : 0.0f;
-        const float cq = qs * a.sm_scale_log2;
+        float cq;
 
         // full key blocks of the segment [b0, fe), split in halves between the groups; both groups run `iters`
         // ring steps. A ragged final block (L % 64 != 0) in the segment is group 1's, in a masked step after it.
@@ -289,6 +282,66 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
 
 #pragma unroll
         for (int k = 0; k < STAGES - 1; ++k) issue(k, k);
+        float qs;
+        if (a.qb) {
+            // Sage's per-thread int8 Q from bf16, the rule of quant_q_kernel: the wave's 32 queries are one 32-token
+            // block, and the group of query q is the 4 tokens with its q % 8 (lanes l, l ^ 8, l ^ 16, l ^ 24 of a
+            // half, both halves): scale = max|x| / 127 + 1e-7, q = trunc(x / scale +- 0.5)
+            float x[4][16];
+            float amax = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                uint4 r0 = make_uint4(0, 0, 0, 0), r1 = r0;
+                if (qlive) {
+                    const uint16_t* src = a.qb + q * a.ldq + h * D + 32 * c + 16 * half;
+                    r0 = *reinterpret_cast<const uint4*>(src);
+                    r1 = *reinterpret_cast<const uint4*>(src + 8);
+                }
+                const uint32_t w[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    x[c][2 * e] = __uint_as_float(w[e] << 16);
+                    x[c][2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+                    amax = fmaxf(amax, fmaxf(fabsf(x[c][2 * e]), fabsf(x[c][2 * e + 1])));
+                }
+            }
+            amax = fmaxf(amax, __shfl_xor(amax, 8));
+            amax = fmaxf(amax, __shfl_xor(amax, 16));
+            amax = fmaxf(amax, __shfl_xor(amax, 32));
+            const float scale = amax / 127.0f + 1e-7f;
+            // x / scale through the reciprocal (div_rn: the IEEE quotient wherever |x / scale| >= 2^-126, and below
+            // that both round to a zero code)
+            const float rscale = 1.0f / scale;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                int wv[4];
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    uint32_t word = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float y = div_rn(x[c][4 * b + e], scale, rscale);
+                        const float r = __builtin_truncf(y + (y >= 0.0f ? 0.5f : -0.5f));
+                        word |= (uint32_t(int32_t(r)) & 0xffu) << (8 * e);
+                    }
+                    wv[b] = int(word);
+                }
+                qf[c] = i32x4{wv[0], wv[1], wv[2], wv[3]};
+            }
+            qs = qlive ? scale : 0.0f;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                if (qlive) {
+                    const uint4 r = *reinterpret_cast<const uint4*>(a.q + q * a.ldq + h * D + 32 * c + 16 * half);
+                    qf[c] = i32x4{int(r.x), int(r.y), int(r.z), int(r.w)};
+                } else {
+                    qf[c] = i32x4{0, 0, 0, 0};
+                }
+            }
+            qs = qlive ? a.q_scale[h * qblocks8 + (q / 32) * 8 + q % 8] : 0.0f;
+        }
+        cq = qs * a.sm_scale_log2;
         for (int i0 = 0; i0 < iters; i0 += STAGES) {
 #pragma unroll
             for (int k = 0; k < STAGES; ++k) {
@@ -392,17 +445,17 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     __syncthreads();
     auto part = [&](int slot) { return a.part + int64_t(slot) * SLOT_FLOATS + sub * (64 * 64 + 128); };
     // contributors in batches with all their loads issued together (one memory round trip per batch)
-    constexpr int BATCH = 8;
+    constexpr int BATCH = 16, MBATCH = 32;
     float mt = -INFINITY;
-    for (int i0 = 0; i0 < nc; i0 += BATCH) {
-        float mv[BATCH];
+    for (int i0 = 0; i0 < nc; i0 += MBATCH) {
+        float mv[MBATCH];
 #pragma unroll
-        for (int k = 0; k < BATCH; ++k) {
+        for (int k = 0; k < MBATCH; ++k) {
             const int sl = i0 + k < nc ? cslot[i0 + k] : -1;
             mv[k] = sl >= 0 ? part(sl)[64 * 64 + lane] : -INFINITY;
         }
 #pragma unroll
-        for (int k = 0; k < BATCH; ++k) mt = fmaxf(mt, mv[k]);
+        for (int k = 0; k < MBATCH; ++k) mt = fmaxf(mt, mv[k]);
     }
     float ov[4] = {}, ls = 0.0f;
     for (int i0 = 0; i0 < nc; i0 += BATCH) {
@@ -444,15 +497,16 @@ extern "C" int64_t wdl_sage_attn_workspace_bytes(int64_t n, int64_t L, int64_t h
     return 2 * T * SLOT_FLOATS * 4;
 }
 
-extern "C" int wdl_sage_attn(const void* q_i8, int64_t ldq, const float* q_scale, const void* k_i8,
-                             const float* k_scale, const void* v_fp8, const float* v_scale, int64_t n, int64_t L,
-                             int64_t heads, float sm_scale, void* out, int64_t ldo, void* workspace,
-                             hipStream_t stream) {
+static int attn_launch(const void* q_i8, const float* q_scale, const void* q_bf16, int64_t ldq, const void* k_i8,
+                       const float* k_scale, const void* v_fp8, const float* v_scale, int64_t n, int64_t L,
+                       int64_t heads, float sm_scale, void* out, int64_t ldo, void* workspace, hipStream_t stream) {
+    const void* q = q_bf16 ? q_bf16 : q_i8;
+    const int64_t qbytes = q_bf16 ? 2 : 1;
     if (n < 0 || L < 1 || heads <= 0 || ldq < heads * D || ldo < heads * D)
         return fail(WDL_EINVAL, "sage_attn: bad shape n=%lld L=%lld", (long long)n, (long long)L);
-    if (!q_i8 || !q_scale || !k_i8 || !k_scale || !v_fp8 || !v_scale || !out)
+    if (!q || (!q_bf16 && !q_scale) || !k_i8 || !k_scale || !v_fp8 || !v_scale || !out)
         return fail(WDL_EINVAL, "sage_attn: null pointer");
-    if ((reinterpret_cast<uintptr_t>(q_i8) | reinterpret_cast<uintptr_t>(out) | ldq | (ldo * 2)) % 16)
+    if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) | (ldq * qbytes) | (ldo * 2)) % 16)
         return fail(WDL_EINVAL, "sage_attn: unaligned rows");
     if (n == 0) return WDL_OK;
     const int64_t Lpad = (L + 63) / 64 * 64;
@@ -476,10 +530,27 @@ extern "C" int wdl_sage_attn(const void* q_i8, int64_t ldq, const float* q_scale
     float* part = Dw < T ? static_cast<float*>(workspace) : nullptr;
     AttnArgs a{static_cast<const int8_t*>(q_i8), ldq, q_scale, static_cast<const int8_t*>(k_i8), k_scale,
                static_cast<const uint8_t*>(v_fp8), v_scale, static_cast<uint16_t*>(out), ldo, n, L, Lpad, heads,
-               sm_scale * 1.4426950408889634f, part, W, qtiles, Dw};
+               sm_scale * 1.4426950408889634f, part, W, qtiles, Dw, static_cast<const uint16_t*>(q_bf16)};
     sage_attn_kernel<<<unsigned(W), 512, 0, stream>>>(a);
     int rc = check_launch("sage_attn");
     if (rc || Dw == T) return rc;
     attn_merge_kernel<<<dim3(unsigned(T - Dw), 4, 4), 256, 0, stream>>>(a);
     return check_launch("sage_attn merge");
+}
+
+extern "C" int wdl_sage_attn(const void* q_i8, int64_t ldq, const float* q_scale, const void* k_i8,
+                             const float* k_scale, const void* v_fp8, const float* v_scale, int64_t n, int64_t L,
+                             int64_t heads, float sm_scale, void* out, int64_t ldo, void* workspace,
+                             hipStream_t stream) {
+    if (!q_i8) return fail(WDL_EINVAL, "sage_attn: null pointer");
+    return attn_launch(q_i8, q_scale, nullptr, ldq, k_i8, k_scale, v_fp8, v_scale, n, L, heads, sm_scale, out, ldo,
+                       workspace, stream);
+}
+
+extern "C" int wdl_sage_attn_q16(const void* q_bf16, int64_t ldq, const void* k_i8, const float* k_scale,
+                                 const void* v_fp8, const float* v_scale, int64_t n, int64_t L, int64_t heads,
+                                 float sm_scale, void* out, int64_t ldo, void* workspace, hipStream_t stream) {
+    if (!q_bf16) return fail(WDL_EINVAL, "sage_attn_q16: null pointer");
+    return attn_launch(nullptr, nullptr, q_bf16, ldq, k_i8, k_scale, v_fp8, v_scale, n, L, heads, sm_scale, out, ldo,
+                       workspace, stream);
 }

@@ -122,10 +122,24 @@ __global__ void finalize_kernel(const float* part_k, const float* part_v, int S,
                                 float* v_scale) {
     const int64_t h = blockIdx.x;
     const int d = threadIdx.x;
+    // the splits in increasing order; the loads of a batch of 16 are all issued before the first add (one memory
+    // round trip per batch, not one per split)
+    constexpr int BATCH = 16;
     float a = 0.0f, m = 0.0f;
-    for (int s = 0; s < S; ++s) {
-        a = a + part_k[(s * H + h) * D + d];
-        m = fmaxf(m, part_v[(s * H + h) * D + d]);
+    for (int s0 = 0; s0 < S; s0 += BATCH) {
+        float pk[BATCH], pv[BATCH];
+#pragma unroll
+        for (int j = 0; j < BATCH; ++j) {
+            const bool in = s0 + j < S;
+            pk[j] = in ? part_k[((s0 + j) * H + h) * D + d] : 0.0f;
+            pv[j] = in ? part_v[((s0 + j) * H + h) * D + d] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < BATCH; ++j)
+            if (s0 + j < S) {
+                a = a + pk[j];
+                m = fmaxf(m, pv[j]);
+            }
     }
     k_mean[h * D + d] = a / float(L);
     v_scale[h * D + d] = fmaxf(m, 1e-8f) / 2.25f;

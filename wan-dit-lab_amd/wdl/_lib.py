@@ -42,6 +42,8 @@ SIGNATURES: dict[str, list] = {
     "wdl_sage_attn_workspace_bytes": [c_i64, c_i64, c_i64],
     "wdl_sage_attn": [c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_f32, c_ptr, c_i64,
                       c_ptr, c_ptr],
+    "wdl_sage_attn_q16": [c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_f32, c_ptr, c_i64,
+                          c_ptr, c_ptr],
 }
 RESTYPES = {"wdl_last_error": ctypes.c_char_p, "wdl_sage_prep_workspace_floats": c_i64,
             "wdl_sage_attn_workspace_bytes": c_i64,

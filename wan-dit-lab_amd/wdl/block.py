@@ -3,11 +3,12 @@
 WanBlock.forward (src/wan_dit_lab/models/block.py:22-29) with the W4A4 layers installed as the reference's fused
 pack installs them (quantization/w4a4.py:336-352: self_attn.qkv FusedQKVAttention, ffn PackedW4A4GeluMLP, every
 other linear PackedW4A4Linear) and the FP8 KV cache attended through Sage (generation/causal.py:193-210). The
-kernel sequence of one block (about 21 launches, all on the current stream, capturable into one HIP graph):
+kernel sequence of one block (about 19 launches, all on the current stream, capturable into one HIP graph):
 
   act_quant(X; LN + (1 + scale_a), + shift_a)  -> W4A4 qkv -> norm_rope(q, k) -> kv_append(K, V @ at)
-  -> sage_prep(cache[:at] ++ K, V) -> quant_q(Q) -> sage_attn -> act_quant(A) -> W4A4 o  (X += gate_a * y, fused)
-  act_quant(X; LN3 affine) -> W4A4 cross q -> RMSNorm -> quant_q -> sage_attn(context K/V, prepared once per
+  -> sage_prep(cache[:at] ++ K, V) -> sage_attn (int8 Q quantized in the kernel) -> act_quant(A) -> W4A4 o
+  (X += gate_a * y, fused)
+  act_quant(X; LN3 affine) -> W4A4 cross q -> RMSNorm -> sage_attn(int8 Q in the kernel; context K/V, prepared once per
   prompt) -> act_quant -> W4A4 cross o (X += y, fused)
   act_quant(X; LN + (1 + scale_f), + shift_f) -> W4A4 ffn.0 (GELU epilogue) -> act_quant((h + 0.171875) / s2,
   unsigned) -> W4A4 ffn.2 (X += gate_f * y, fused)
@@ -92,8 +93,7 @@ class QuantizedWanBlock:
         self._gemm(self._quant(X, "cq", ln=n3), "cq", M, qc)
         Qc, _ = ops.qk_norm_rope_launch(qc, None, self.p["cwq"], None, self._nofreq(dev), (0, 1, 1), 0,
                                         self.eps)
-        q_i8, q_sc = ops.quant_q_launch(Qc, H)
-        Ac = ops.sage_attn_launch(q_i8, q_sc, ctx, ctx["L"], 128 ** -0.5)
+        Ac = ops.sage_attn_q16_launch(Qc, ctx, ctx["L"], 128 ** -0.5)
         self._gemm(self._quant(Ac, "co"), "co", M, X, EPI_RESIDUAL, self.ones)
         # feed forward (W4A4 GELU MLP)
         h = torch.empty(M, ops.out_features(self.p["ffn1"]["wcodes"]), device=dev, dtype=torch.bfloat16)

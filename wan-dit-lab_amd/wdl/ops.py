@@ -364,6 +364,21 @@ def sage_attn_launch(q_i8, q_scale, prep, L, sm_scale, out=None):
     return out
 
 
+def sage_attn_q16_launch(Q, prep, L, sm_scale, out=None):
+    """Q bf16 [n, H*128] (row-strided) -> bf16 [n, H*128]: Sage attention with the int8 quantization of Q done in
+    the kernel (bit-identical to quant_q_launch followed by sage_attn_launch)."""
+    n = Q.shape[0]
+    H = Q.shape[1] // 128
+    if Q.dtype != torch.bfloat16 or Q.dim() != 2 or Q.shape[1] % 128 or Q.stride(1) != 1:
+        raise ValueError("sage_attn_q16: Q must be bf16 [n, H*128] with unit column stride")
+    if out is None:
+        out = torch.empty(n, H * 128, device=Q.device, dtype=torch.bfloat16)
+    ws = workspace(_ATTN_WS, Q.device, _lib.library().wdl_sage_attn_workspace_bytes(n, L, H))
+    _lib.call("wdl_sage_attn_q16", ptr(Q), Q.stride(0), ptr(prep["k"]), ptr(prep["k_scale"]), ptr(prep["v"]),
+              ptr(prep["v_scale"]), n, L, H, float(sm_scale), ptr(out), out.stride(0), ptr(ws), stream_of(Q))
+    return out
+
+
 @torch.library.custom_op("wdl::sage_kv_attend", mutates_args=())
 def sage_kv_attend(Q: torch.Tensor, cache_k: torch.Tensor, cache_ks: torch.Tensor, cache_v: torch.Tensor,
                    cache_vs: torch.Tensor, K: torch.Tensor, V: torch.Tensor, at: int, sm_scale: float) -> torch.Tensor:
@@ -374,8 +389,7 @@ def sage_kv_attend(Q: torch.Tensor, cache_k: torch.Tensor, cache_ks: torch.Tenso
     n = K.shape[1]
     prep = sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, K[0].reshape(n, H * D) if K.is_contiguous() else
                             K[0].flatten(1), V[0].flatten(1), at)
-    q_i8, q_sc = quant_q_launch(Q[0].flatten(1), H)
-    return sage_attn_launch(q_i8, q_sc, prep, at + n, sm_scale).view(1, nq, H, D)
+    return sage_attn_q16_launch(Q[0].flatten(1), prep, at + n, sm_scale).view(1, nq, H, D)
 
 
 @sage_kv_attend.register_fake
