@@ -119,7 +119,7 @@ def instrumented(step):
     from wdl import ops
 
     rec = {"gemm": [], "attn": []}
-    orig_gemm, orig_attn = ops.gemm_launch, ops.sage_attn_launch
+    orig_gemm, orig_attn, orig_attn16 = ops.gemm_launch, ops.sage_attn_launch, ops.sage_attn_q16_launch
 
     def gemm(q, ascales, lora, qweight, *a, **k):
         M = a[3]
@@ -139,9 +139,15 @@ def instrumented(step):
         rec["attn"].append((e0, e1, 4.0 * n * L * d * H))
         return r
 
-    ops.gemm_launch, ops.sage_attn_launch = gemm, attn
-    import wdl.block as wblock
-    wblock.ops.gemm_launch, wblock.ops.sage_attn_launch = gemm, attn
+    def attn16(Q, prep, L, sm_scale, out=None):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        r = orig_attn16(Q, prep, L, sm_scale, out)
+        e1.record()
+        rec["attn"].append((e0, e1, 4.0 * Q.shape[0] * L * Q.shape[1]))
+        return r
+
+    ops.gemm_launch, ops.sage_attn_launch, ops.sage_attn_q16_launch = gemm, attn, attn16
     # Keep the GPU behind the host while the step is enqueued, so that each start event is followed at once by its
     # (already queued) kernel and no host launch latency falls between the events: a spin kernel of ~0.5 s first.
     probe = 10_000_000
@@ -156,7 +162,7 @@ def instrumented(step):
         step()
         torch.cuda.synchronize()
     finally:
-        ops.gemm_launch, ops.sage_attn_launch = orig_gemm, orig_attn
+        ops.gemm_launch, ops.sage_attn_launch, ops.sage_attn_q16_launch = orig_gemm, orig_attn, orig_attn16
     out = {}
     for name, items in rec.items():
         ms = sum(a.elapsed_time(b) for a, b, _ in items)
@@ -316,7 +322,9 @@ def main():
                      "unit": "TFLOP/s", "frac": gemm_frac, "traffic": gemm_traffic(),
                      "basis": "2*M*N*K int ops per launch (M = 1392 tokens) summed over the step's "
                               f"{g['launches']} W4A4 GEMM launches / their summed HIP-event durations; traffic = "
-                              "calibrated HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE"},
+                              "calibrated HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE; peak = the "
+                              "metric's dense int8 MFMA peak (the kernel issues fp6 MFMAs, dense peak 10.1 POP/s: "
+                              "against that the fraction is half)"},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()

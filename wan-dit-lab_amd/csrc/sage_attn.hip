@@ -94,6 +94,7 @@ __device__ __forceinline__ int64_t wg_of(int64_t unit, int64_t U, int64_t W) {
 __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE];
     __shared__ float sKs[KS_MAX];
+    __shared__ float sVs[D];  // v_scale of the head
 
     const int t = threadIdx.x, lane = t % 64, half = lane / 32;
     const int wave = __builtin_amdgcn_readfirstlane(t / 64);
@@ -139,9 +140,17 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
             cursor += b1 - b0;
         }
         const int64_t h = tile / a.qtiles, qt = tile % a.qtiles;
-        if (h != head_loaded) {  // every wave is past its last read of sKs (segment-end barrier)
-            for (int64_t i = t; i < nks; i += 512) sKs[i] = a.k_scale[h * nks + i];
-            head_loaded = h;
+        // a new head's k scales: loaded here, written to sKs after the ring prologue and Q are issued (so the load
+        // latencies overlap); every wave is past its last read of sKs (segment-end barrier)
+        const bool new_head = h != head_loaded;
+        float ksr[KS_MAX / 512], vsr = 0.0f;
+        if (new_head) {
+#pragma unroll
+            for (int i = 0; i < KS_MAX / 512; ++i) {
+                const int64_t j = t + 512 * i;
+                ksr[i] = j < nks ? a.k_scale[h * nks + j] : 0.0f;
+            }
+            if (t < D) vsr = a.v_scale[h * D + t];
         }
         const int64_t q = qt * 128 + sub * 32 + lane % 32;
         const bool qlive = q < a.n;
@@ -342,6 +351,13 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
             qs = qlive ? a.q_scale[h * qblocks8 + (q / 32) * 8 + q % 8] : 0.0f;
         }
         cq = qs * a.sm_scale_log2;
+        if (new_head) {  // read only after the first ring step's barrier
+#pragma unroll
+            for (int i = 0; i < KS_MAX / 512; ++i)
+                if (t + 512 * i < nks) sKs[t + 512 * i] = ksr[i];
+            if (t < D) sVs[t] = vsr;
+            head_loaded = h;
+        }
         for (int i0 = 0; i0 < iters; i0 += STAGES) {
 #pragma unroll
             for (int k = 0; k < STAGES; ++k) {
@@ -399,7 +415,7 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
                     const int d = 32 * ds + 8 * g + 4 * half;
                     uint16_t r[4];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) r[e] = f32_to_bf16(ov[ds][4 * g + e] * inv * a.v_scale[h * D + d + e]);
+                    for (int e = 0; e < 4; ++e) r[e] = f32_to_bf16(ov[ds][4 * g + e] * inv * sVs[d + e]);
                     *reinterpret_cast<uint2*>(dst + d) =
                         make_uint2(r[0] | (uint32_t(r[1]) << 16), r[2] | (uint32_t(r[3]) << 16));
                 }
@@ -417,7 +433,7 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
             ps[64 * 64 + lane] = m;
             ps[64 * 64 + 64 + lane] = lt;
         }
-        __syncthreads();  // the segment is done with the ring, the hand-over area and sKs
+        __syncthreads();  // the segment is done with the ring, the hand-over area, sKs and sVs
     }
 }
 
