@@ -87,8 +87,10 @@ def test_sage_prep_k_and_v(gpu, at, n, H):
 
 
 
-@pytest.mark.parametrize("at,n,H", [(200, 150, 3), (0, 2640, 2), (6600, 2640, 2), (928, 464, 24)])
+@pytest.mark.parametrize("at,n,H", [(200, 150, 3), (0, 2640, 2), (6600, 2640, 2), (928, 464, 24), (0, 1392, 24)])
 def test_attention_matches_quantized_oracle_and_exact(gpu, at, n, H):
+    """(0, 1392, 24): 11 x 24 = 264 tiles over 1392 keys (22 blocks, the last ragged): on 256 CUs the first 8
+    workgroups run two whole tiles, one per group, each over all the key blocks and its own masked final block."""
     from wdl import sage_kv
 
     Q, k, ks, v, vs, at, K, V = setup(at, n, H=H, seed=3)

@@ -65,6 +65,7 @@ struct AttnArgs {
     int64_t qtiles;       // query tiles (128 queries) per head
     int64_t D;            // tiles run whole (the first D of the T = qtiles * H); the other T - D are split
     const uint16_t* qb;   // bf16 Q [n, H, 128] (row stride ldq) quantized in the kernel, or null (q, q_scale given)
+    int64_t dual;         // workgroups 0 .. dual - 1 run two whole tiles, one per group (D == T; else 0)
 };
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -93,12 +94,14 @@ __device__ __forceinline__ int64_t wg_of(int64_t unit, int64_t U, int64_t W) {
 
 __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE];
-    __shared__ float sKs[KS_MAX];
-    __shared__ float sVs[D];  // v_scale of the head
+    __shared__ float sKs_[2][KS_MAX];  // k scales of each group's head
+    __shared__ float sVs_[2][D];       // v_scale of each group's head
 
     const int t = threadIdx.x, lane = t % 64, half = lane / 32;
     const int wave = __builtin_amdgcn_readfirstlane(t / 64);
-    const int grp = wave / 4, sub = wave % 4;
+    const int grp = wave / 4, sub = wave % 4, tg = t % 256;
+    float* sKs = sKs_[grp];
+    float* sVs = sVs_[grp];
     const int64_t qblocks8 = (a.n + 127) / 128 * 32;
     const int64_t nblk = a.Lpad / 64, nks = a.Lpad / 16;
     const bool ragged = (a.L % 64) != 0;
@@ -106,6 +109,8 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
     // [s0, s1) of the key blocks of the R = T - D remaining tiles, laid end to end (each piece's partial softmax
     // state goes to the workspace slot 2w for its first piece, 2w + 1 for a second; attn_merge_kernel combines them)
     const int64_t w = blockIdx.x;
+    // a dual workgroup: its two groups take whole tiles 2w and 2w + 1 with all the key blocks each, no hand-over
+    const bool dualwg = w < a.dual;
     const int64_t T = a.qtiles * a.H, R = T - a.D, Usk = R * nblk;
     const int64_t ndp = (a.D - w + a.W - 1) / a.W;
     const int64_t s0 = w * Usk / a.W, s1 = (w + 1) * Usk / a.W;
@@ -125,7 +130,11 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
     for (int64_t seg = 0;; ++seg) {
         // ---- segment: tile `tile` (head h, query tile qt), key blocks [b0, b1)
         int64_t tile, b0, b1, slot = -1;
-        if (seg < ndp) {
+        if (a.dual > 0) {  // one whole tile per workgroup, or one per group for the first `dual` of them
+            if (seg > 0) break;
+            tile = dualwg ? 2 * w + grp : a.dual + w;
+            b0 = 0, b1 = nblk;
+        } else if (seg < ndp) {
             // workgroup ids go round-robin over the 8 XCDs; each XCD takes a contiguous range of the whole tiles, so
             // the query tiles of one head (consecutive tiles) share its K/V in one L2
             const int64_t l = w + seg * a.W;
@@ -143,14 +152,14 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
         // a new head's k scales: loaded here, written to sKs after the ring prologue and Q are issued (so the load
         // latencies overlap); every wave is past its last read of sKs (segment-end barrier)
         const bool new_head = h != head_loaded;
-        float ksr[KS_MAX / 512], vsr = 0.0f;
-        if (new_head) {
+        float ksr[KS_MAX / 256], vsr = 0.0f;
+        if (new_head) {  // each group fills its own copy
 #pragma unroll
-            for (int i = 0; i < KS_MAX / 512; ++i) {
-                const int64_t j = t + 512 * i;
+            for (int i = 0; i < KS_MAX / 256; ++i) {
+                const int64_t j = tg + 256 * i;
                 ksr[i] = j < nks ? a.k_scale[h * nks + j] : 0.0f;
             }
-            if (t < D) vsr = a.v_scale[h * D + t];
+            if (tg < D) vsr = a.v_scale[h * D + tg];
         }
         const int64_t q = qt * 128 + sub * 32 + lane % 32;
         const bool qlive = q < a.n;
@@ -166,8 +175,8 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
         const bool ragged_here = ragged && b1 == nblk;
         // (32-bit ring counters: uniform 64-bit compares would run on the vector unit; blocks < 2^9)
         const int fe = int(ragged_here ? nblk - 1 : b1), ib0 = int(b0);
-        const int nfull = fe - ib0, nb0 = (nfull + 1) / 2;
-        const int first = grp == 0 ? ib0 : ib0 + nb0, count = grp == 0 ? nb0 : nfull - nb0;
+        const int nfull = fe - ib0, nb0 = dualwg ? nfull : (nfull + 1) / 2;
+        const int first = grp == 0 || dualwg ? ib0 : ib0 + nb0, count = grp == 0 || dualwg ? nb0 : nfull - nb0;
         const int last = count > 0 ? first + count - 1 : ib0;
         const int iters = nb0;
 
@@ -353,9 +362,9 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
         cq = qs * a.sm_scale_log2;
         if (new_head) {  // read only after the first ring step's barrier
 #pragma unroll
-            for (int i = 0; i < KS_MAX / 512; ++i)
-                if (t + 512 * i < nks) sKs[t + 512 * i] = ksr[i];
-            if (t < D) sVs[t] = vsr;
+            for (int i = 0; i < KS_MAX / 256; ++i)
+                if (tg + 256 * i < nks) sKs[tg + 256 * i] = ksr[i];
+            if (tg < D) sVs[tg] = vsr;
             head_loaded = h;
         }
         for (int i0 = 0; i0 < iters; i0 += STAGES) {
@@ -372,15 +381,15 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
         wait_vmcnt<0>();
         __syncthreads();  // all loads landed, every wave is done with the ring, sKs written
         if (ragged_here) {  // the final, partial block: group 1, keys >= L masked
-            if (grp == 1) load_block(0, nblk - 1);
+            if (grp == 1 || dualwg) load_block(0, nblk - 1);
             wait_vmcnt<0>();
             __syncthreads();
-            if (grp == 1) compute(0, nblk - 1, std::true_type{});
+            if (grp == 1 || dualwg) compute(0, nblk - 1, std::true_type{});
             __syncthreads();  // group 1 is done reading stage 0 before the hand-over overwrites it
         }
 
         // group 1 hands (O, m, l) to group 0, which merges: O = O0 2^(m0 - m) + O1 2^(m1 - m), l likewise
-        if (grp == 1) {
+        if (grp == 1 && !dualwg) {
 #pragma unroll
             for (int ds = 0; ds < 4; ++ds)
 #pragma unroll
@@ -390,7 +399,9 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
         }
         __syncthreads();
         float lt = 0.0f;
-        if (grp == 0) {
+        if (dualwg) {
+            lt = l + __shfl_xor(l, 32);
+        } else if (grp == 0) {
             const float m1 = xo[64 * 64 + lane], l1 = xo[64 * 64 + 64 + lane];
             const float mt = fmaxf(m, m1);
             const float a0 = __builtin_amdgcn_exp2f(m - mt), a1 = __builtin_amdgcn_exp2f(m1 - mt);
@@ -423,7 +434,7 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
         };
 
         if (slot < 0) {
-            if (grp == 0) write_out(o, lt);
+            if (grp == 0 || dualwg) write_out(o, lt);
         } else if (grp == 0) {
             float* ps = a.part + slot * SLOT_FLOATS + sub * (64 * 64 + 128);
 #pragma unroll
@@ -534,19 +545,24 @@ static int attn_launch(const void* q_i8, const float* q_scale, const void* q_bf1
     // multiple of the CU count): then one workgroup per CU runs floor(T / CUs) whole tiles each and the key blocks
     // of the T mod CUs remaining tiles are split evenly over all of them, merged by a second launch. Short key
     // ranges keep one workgroup per tile.
-    int64_t W = T, Dw = T;
+    // Short key ranges (no split) with CUs < T <= 2 CUs: one workgroup per CU, and the first T - CUs of them run
+    // two whole tiles, one per group of 4 waves over all the key blocks (the other workgroups split their tile's
+    // blocks between the groups), so the tiles take one round instead of two.
+    int64_t W = T, Dw = T, dual = 0;
     const int64_t cus = cu_count();
     if (cus > 0 && cus <= MAX_WG && T > cus && nblk >= 32) {
         const int64_t rounds = (T + cus - 1) / cus;
         const int64_t usk = (T % cus) * nblk;  // key blocks of the split tiles
         if (T * 100 < 85 * rounds * cus && (cus + 1) * usk < (int64_t(1) << 31)) W = cus, Dw = cus * (T / cus);
+    } else if (cus > 0 && T > cus && T <= 2 * cus) {
+        W = cus, dual = T - cus;
     }
     if (Dw < T && (!workspace || reinterpret_cast<uintptr_t>(workspace) % 16))
         return fail(WDL_EINVAL, "sage_attn: a 16-byte aligned workspace of wdl_sage_attn_workspace_bytes is needed");
     float* part = Dw < T ? static_cast<float*>(workspace) : nullptr;
     AttnArgs a{static_cast<const int8_t*>(q_i8), ldq, q_scale, static_cast<const int8_t*>(k_i8), k_scale,
                static_cast<const uint8_t*>(v_fp8), v_scale, static_cast<uint16_t*>(out), ldo, n, L, Lpad, heads,
-               sm_scale * 1.4426950408889634f, part, W, qtiles, Dw, static_cast<const uint16_t*>(q_bf16)};
+               sm_scale * 1.4426950408889634f, part, W, qtiles, Dw, static_cast<const uint16_t*>(q_bf16), dual};
     sage_attn_kernel<<<unsigned(W), 512, 0, stream>>>(a);
     int rc = check_launch("sage_attn");
     if (rc || Dw == T) return rc;
