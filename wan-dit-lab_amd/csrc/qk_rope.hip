@@ -1,9 +1,10 @@
 // Q/K RMSNorm over the whole row (all heads) and 3D RoPE, fused, plus Sage's per-thread int8 quantization of Q.
 //
-// qk_norm_rope: one wave per (row m, q or k), the row held in registers (bf16, row strides ldq / ldk, H heads of
+// qk_norm_rope: two waves per (row m, q or k), the row held in registers (bf16, row strides ldq / ldk, H heads of
 // D = 128, H * D <= 4096):
 //   rstd = 1 / sqrt(mean(x^2) + eps)     fp32; ordered sum: lane l owns the 8-value chunks c = l, l + 64, ... and
-//                                       adds their squares value by value, then an xor butterfly 32, 16, .., 1
+//                                       adds their squares value by value (the first wave's chunks, then the
+//                                       second's), then an xor butterfly 32, 16, .., 1
 //   n   = bf16(x * rstd);  w = bf16(n * weight)                                (models/rms_norm.py:12-13)
 //   rot = bf16(w1 c - w2 s), bf16(w2 c + w1 s) on pairs (2p, 2p+1)             (models/rope.py:26-31)
 // in the table's precision: fp32 for an fp32 table; for an fp64 table the products and differences are fp64 and the
@@ -51,72 +52,114 @@ __device__ __forceinline__ void load8(const uint16_t* p, float* f) {
     }
 }
 
+// Two waves per (row, q|k), two rows per workgroup. Lane l of the row's first wave owns the chunks c = l + 64 i
+// for i < I0 = ceil(I / 2) (I = ceil(chunks / 64)), of the second wave those for I0 <= i < I: the same lane->chunk
+// map as one wave over the row. The sum of squares keeps the one-wave order exactly: the first wave's lane sums go
+// through LDS and the second wave continues each from there, value by value, then reduces across lanes. Every load
+// of a wave (its x chunks, norm weights and rotation table entries) is issued before any arithmetic.
 template <typename T>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs a) {
-    const int lane = threadIdx.x % 64;
-    const int64_t item = int64_t(blockIdx.x) * 4 + threadIdx.x / 64;  // (row, which)
-    if (item >= a.items * a.M) return;
-    const int64_t row = item / a.items;
+    constexpr int CW = MAXCH / 2;  // chunks per lane and wave
+    __shared__ float part[2][64];  // the first wave's lane sums, per row slot
+    __shared__ float srstd[2];
+    const int lane = threadIdx.x % 64, wv = threadIdx.x / 64, slot = wv / 2, hw = wv % 2;
+    const int64_t item = int64_t(blockIdx.x) * 2 + slot;  // (row, which)
+    const bool valid = item < a.items * a.M;
+    const int64_t row = valid ? item / a.items : 0;
     const int which = int(item % a.items);
     const uint16_t* src = (which == 0 ? a.q : a.k) + row * (which == 0 ? a.ldq : a.ldk);
     const uint16_t* wt = which == 0 ? a.wq : a.wk;
     uint16_t* dst = (which == 0 ? a.qo : a.ko) + row * a.ldo;
     const T* freq = static_cast<const T*>(a.freq);
     const int64_t chunks = a.C / 8;
-    float x[MAXCH][8];
-#pragma unroll
-    for (int i = 0; i < MAXCH; ++i) {
-        const int64_t c = lane + 64 * i;
-        if (c < chunks) load8(src + c * 8, x[i]);
-        else
-            for (int j = 0; j < 8; ++j) x[i][j] = 0.0f;
-    }
-    float rstd = 1.0f;
-    if (wt) {
-        float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < MAXCH; ++i)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) s = s + x[i][j] * x[i][j];
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) s = s + __shfl_xor(s, o);
-        rstd = 1.0f / sqrtf(s / float(a.C) + a.eps);
-    }
-    const int64_t hw = int64_t(a.h) * a.w;
-    const bool rot = row < int64_t(a.f) * hw;
-    const int pos_t = a.start + int(row / hw);
+    const int nI = int((chunks + 63) / 64), nI0 = (nI + 1) / 2;
+    const int i0 = hw == 0 ? 0 : nI0, i1 = hw == 0 ? nI0 : nI;  // this wave's chunk slots [i0, i1)
+    const int64_t hwn = int64_t(a.h) * a.w;
+    const bool rot = row < int64_t(a.f) * hwn;
+    const int pos_t = a.start + int(row / hwn);
     const int pos_h = int((row / a.w) % a.h);
     const int pos_w = int(row % a.w);
     constexpr int half = 64, tpairs = half - 2 * (half / 3), spairs = half / 3;  // 22, 21
+    uint4 xr[CW], wr[CW];
+    T cs[CW][4], sn[CW][4];
 #pragma unroll
-    for (int i = 0; i < MAXCH; ++i) {
-        const int64_t c = lane + 64 * i;
-        if (c >= chunks) break;
-        const int64_t col = c * 8;
-        float y[8];
-        if (wt) {
-            float wf[8];
-            load8(wt + col, wf);
+    for (int k = 0; k < CW; ++k) {
+        const int64_t c = lane + 64 * int64_t(i0 + k);
+        xr[k] = wr[k] = make_uint4(0, 0, 0, 0);
+        if (valid && i0 + k < i1 && c < chunks) {
+            xr[k] = *reinterpret_cast<const uint4*>(src + c * 8);
+            if (wt) wr[k] = *reinterpret_cast<const uint4*>(wt + c * 8);
+            if (rot) {
+#pragma unroll
+                for (int p2 = 0; p2 < 4; ++p2) {
+                    const int p = int((c * 8 + 2 * p2) % 128) / 2;
+                    const int pos = p < tpairs ? pos_t : (p < tpairs + spairs ? pos_h : pos_w);
+                    cs[k][p2] = freq[int64_t(pos) * half + p];
+                    sn[k][p2] = freq[(a.P + pos) * half + p];
+                }
+            }
+        }
+    }
+    // sum of squares in the one-wave order: the first wave sums its slots from 0 (absent chunks would add + 0,
+    // exact), the second continues each lane's sum through its own slots
+    float s = 0.0f;
+    if (wt && hw == 0) {
+#pragma unroll
+        for (int k = 0; k < CW; ++k) {
+            const uint32_t xw[4] = {xr[k].x, xr[k].y, xr[k].z, xr[k].w};
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float n = bf16_to_f32(f32_to_bf16(x[i][j] * rstd));
-                y[j] = bf16_to_f32(f32_to_bf16(n * wf[j]));
+                const float v = __uint_as_float(j % 2 == 0 ? xw[j / 2] << 16 : xw[j / 2] & 0xffff0000u);
+                if (i0 + k < i1) s = s + v * v;
             }
-        } else {
+        }
+    }
+    if (hw == 0) part[slot][lane] = s;
+    __syncthreads();
+    if (hw == 1 && wt) {
+        float t = part[slot][lane];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) y[j] = x[i][j];
+        for (int k = 0; k < CW; ++k) {
+            const uint32_t xw[4] = {xr[k].x, xr[k].y, xr[k].z, xr[k].w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float v = __uint_as_float(j % 2 == 0 ? xw[j / 2] << 16 : xw[j / 2] & 0xffff0000u);
+                if (i0 + k < i1) t = t + v * v;
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) t = t + __shfl_xor(t, o);
+        if (lane == 0) srstd[slot] = 1.0f / sqrtf(t / float(a.C) + a.eps);
+    }
+    __syncthreads();
+    if (!valid) return;
+    const float rstd = wt ? srstd[slot] : 1.0f;
+#pragma unroll
+    for (int k = 0; k < CW; ++k) {
+        const int64_t c = lane + 64 * int64_t(i0 + k);
+        if (i0 + k >= i1 || c >= chunks) continue;
+        const int64_t col = c * 8;
+        const uint32_t xw[4] = {xr[k].x, xr[k].y, xr[k].z, xr[k].w};
+        const uint32_t ww[4] = {wr[k].x, wr[k].y, wr[k].z, wr[k].w};
+        float y[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float x = __uint_as_float(j % 2 == 0 ? xw[j / 2] << 16 : xw[j / 2] & 0xffff0000u);
+            if (wt) {
+                const float w = __uint_as_float(j % 2 == 0 ? ww[j / 2] << 16 : ww[j / 2] & 0xffff0000u);
+                const float n = bf16_to_f32(f32_to_bf16(x * rstd));
+                y[j] = bf16_to_f32(f32_to_bf16(n * w));
+            } else {
+                y[j] = x;
+            }
         }
         uint16_t o[8];
 #pragma unroll
         for (int p2 = 0; p2 < 4; ++p2) {
             if (rot) {
-                const int p = int((col + 2 * p2) % 128) / 2;
-                const int pos = p < tpairs ? pos_t : (p < tpairs + spairs ? pos_h : pos_w);
-                const T cs = freq[int64_t(pos) * half + p];
-                const T sn = freq[(a.P + pos) * half + p];
                 const T x1 = T(y[2 * p2]), x2 = T(y[2 * p2 + 1]);
-                o[2 * p2] = f32_to_bf16(float(x1 * cs - x2 * sn));
-                o[2 * p2 + 1] = f32_to_bf16(float(x2 * cs + x1 * sn));
+                o[2 * p2] = f32_to_bf16(float(x1 * cs[k][p2] - x2 * sn[k][p2]));
+                o[2 * p2 + 1] = f32_to_bf16(float(x2 * cs[k][p2] + x1 * sn[k][p2]));
             } else {
                 o[2 * p2] = f32_to_bf16(y[2 * p2]);
                 o[2 * p2 + 1] = f32_to_bf16(y[2 * p2 + 1]);
@@ -202,7 +245,7 @@ extern "C" int wdl_qk_norm_rope(const void* q, int64_t ldq, const void* k, int64
                    static_cast<const uint16_t*>(wq), static_cast<const uint16_t*>(wk), freq, positions, M, C,
                    f, h, w, start_frame, eps, static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_out), ldo,
                    items};
-    const unsigned grid = unsigned((items * M + 3) / 4);
+    const unsigned grid = unsigned((items * M + 1) / 2);
     if (freq_dtype == WDL_F64) qk_norm_rope_kernel<double><<<grid, 256, 0, stream>>>(a);
     else qk_norm_rope_kernel<float><<<grid, 256, 0, stream>>>(a);
     return check_launch("qk_norm_rope");
