@@ -51,6 +51,7 @@ class Step:
 
         from wdl.block import random_block
         from wdl.kvcache import KVCache
+        from wdl.model import DiTModel, ModelEdges, random_edges
         from wdl.rope import freqs
 
         g = torch.Generator(device=device).manual_seed(seed)
@@ -66,50 +67,18 @@ class Step:
             c.fill_for_benchmark(g)
             self.caches.append(c)
         context = torch.randn(CONTEXT, DIM, generator=g, device=device).to(torch.bfloat16)
-        self.ctx = [b.prepare_context(context) for b in self.blocks]
-        # every block's modulation table, stacked: e = time_in + modulation for all blocks is one add per step
-        self.modulation = torch.stack([b.p["modulation"] for b in self.blocks])
         self.freq = freqs(128, 1024, device)
-        bf = torch.bfloat16
-        r = lambda *s: torch.randn(*s, generator=g, device=device)
-        patch = LATENT * 4
-        self.w_patch, self.b_patch = (r(DIM, patch) * 0.02).to(bf), (r(DIM) * 0.02).to(bf)
-        self.w_t1, self.b_t1 = (r(DIM, 256) * 0.02).to(bf), (r(DIM) * 0.02).to(bf)
-        self.w_t2, self.b_t2 = (r(DIM, DIM) * 0.02).to(bf), (r(DIM) * 0.02).to(bf)
-        self.w_proj, self.b_proj = (r(6 * DIM, DIM) * 0.02).to(bf), (r(6 * DIM) * 0.02).to(bf)
-        self.w_head, self.b_head = (r(patch, DIM) * 0.02).to(bf), (r(patch) * 0.02).to(bf)
-        self.head_mod = r(2, DIM) / DIM ** 0.5
-        self.latent = r(1, LATENT, GRID[0], 2 * GRID[1], 2 * GRID[2]).to(bf)
+        # WanModel's step on one chunk: patch embedding, time embedding and projection, the blocks (each
+        # attending over its full FP8 window and the prompt), Head and unpatchify (wdl.model, model.py:32-84)
+        edges = ModelEdges(random_edges(DIM, LATENT, LATENT, g), device)
+        self.model = DiTModel(edges, self.blocks, self.caches, context, self.freq)
+        self.latent = torch.randn(LATENT, GRID[0], 2 * GRID[1], 2 * GRID[2], generator=g, device=device)
         self.t = torch.tensor([750.0], device=device)
-        self.X = torch.empty(TOKENS, DIM, device=device, dtype=bf)
-        self.out = torch.empty(1, LATENT, GRID[0], 2 * GRID[1], 2 * GRID[2], device=device, dtype=bf)
         # the chunk sits after the window's cached frames: its first frame is frame 18
         self.start_frame = WINDOW - GRID[0]
 
     def __call__(self):
-        import torch
-        import torch.nn.functional as F
-
-        f, h, w = GRID
-        # patch embedding: conv3d (1, 2, 2) / (1, 2, 2) as a matmul over patches (model.py:13, 37)
-        x = self.latent.view(1, LATENT, f, h, 2, w, 2).permute(0, 2, 3, 5, 1, 4, 6).reshape(TOKENS, LATENT * 4)
-        self.X.copy_(F.linear(x, self.w_patch, self.b_patch))
-        # time embedding (model.py:38-41)
-        omega = 10000 ** (-torch.arange(128, dtype=torch.float64, device=self.device) / 128)
-        theta = self.t.double()[:, None] * omega[None, :]
-        temb = torch.cat([torch.cos(theta), torch.sin(theta)], dim=1).to(torch.bfloat16)
-        temb = F.linear(F.silu(F.linear(temb, self.w_t1, self.b_t1)), self.w_t2, self.b_t2)
-        e0 = F.linear(F.silu(temb), self.w_proj, self.b_proj).float().view(6, DIM)
-        e_all = e0 + self.modulation  # [blocks, 6, DIM]: the same sums as e0 + modulation per block
-        for blk, cache, ctx, e in zip(self.blocks, self.caches, self.ctx, e_all):
-            blk.forward(self.X, e, GRID, self.freq, self.start_frame, cache, ctx)
-        # head + unpatchify (head.py:13-18; model.py:81-84)
-        shift, scale = (self.head_mod + temb.float()).chunk(2, dim=0)
-        y = F.layer_norm(self.X.float(), (DIM,), eps=1e-6) * (1 + scale) + shift
-        y = F.linear(y.to(torch.bfloat16), self.w_head, self.b_head)
-        y = y.view(1, f, h, w, 1, 2, 2, LATENT).permute(0, 7, 1, 4, 2, 5, 3, 6).reshape(self.out.shape)
-        self.out.copy_(y)
-        return self.out
+        return self.model.forward(self.latent, self.t, self.start_frame)
 
 
 def instrumented(step):

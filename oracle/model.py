@@ -1,0 +1,102 @@
+"""The model edges and the DMD chunk loop on the CPU — test infrastructure, a restatement of
+src/wan_dit_lab/models/model.py:32-84, models/head.py:13-18 and generation/causal.py:41-45, 680-740 around
+oracle.block.block_forward. Only tests/ may import it.
+
+Arithmetic as the reference runs it under bf16 autocast (causal.py:388-390): a linear or the patch convolution
+takes bf16 operands, accumulates exactly enough to round once (fp64 here) and returns bf16; SiLU on bf16; the
+Head's LayerNorm (no affine, eps 1e-6) and modulation in fp32, then the bf16 linear; the sinusoid in fp64.
+
+Pinned by: the noise levels against the reference's own fixture (tests/test_causal_schedule.py:14:
+[1, 0.9375, 5/6, 0.625]); the patch embedding as torch.nn.functional.conv3d (a textbook routine) of the same
+weights; unpatchify as the exact inverse of the patch order (an index identity); the time features against
+their closed form at t = 0 (cos 1, sin 0) and t with omega_0 = 1.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from oracle import block as oblock
+
+BF = torch.bfloat16
+
+
+def sigmas(shift: float = 5.0, steps=(1000, 750, 500, 250)) -> list:
+    """causal.py:41-45 in fp64 scalars (no torch): sigma = shift u / (1 + (shift - 1) u), u = t / 1000."""
+    out = []
+    for t in steps:
+        u = t / 1000.0
+        out.append(shift * u / (1.0 + (shift - 1.0) * u))
+    return out
+
+
+def linear_bf16(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None) -> torch.Tensor:
+    """A bf16 linear: bf16 operands, the sum in fp64, one rounding of (sum + bias) to bf16."""
+    y = x.to(BF).double() @ w.to(BF).double().t()
+    if b is not None:
+        y = y + b.to(BF).double()
+    return y.to(BF)
+
+
+def patch_embed(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Conv3d(in_dim, dim, (1, 2, 2), (1, 2, 2)) of the latent [C, f, H, W] (model.py:13, 36), through
+    torch's conv3d in fp64 on bf16-rounded operands, rounded to bf16: tokens [f h w, dim] in (f, i, j) order."""
+    y = F.conv3d(x.to(BF).double()[None], w.to(BF).double(), b.to(BF).double(), stride=(1, 2, 2))[0]
+    return y.flatten(1).t().contiguous().to(BF)
+
+
+def time_embed(t: torch.Tensor, P: dict):
+    """model.py:38-41: (t_emb bf16 [dim], e0 bf16 [6, dim])."""
+    omega = 10000 ** (-torch.arange(128, dtype=torch.float64) / 128)
+    theta = t.double()[:, None] * omega[None, :]
+    feats = torch.cat([torch.cos(theta), torch.sin(theta)], dim=1).float()
+    h = linear_bf16(feats, P["t1_w"], P["t1_b"])
+    t_emb = linear_bf16(F.silu(h.float()).to(BF), P["t2_w"], P["t2_b"])
+    e0 = linear_bf16(F.silu(t_emb.float()).to(BF), P["proj_w"], P["proj_b"])
+    return t_emb[0], e0.reshape(6, -1)
+
+
+def head(X: torch.Tensor, t_emb: torch.Tensor, P: dict, grid, eps: float = 1e-6) -> torch.Tensor:
+    """Head.forward (head.py:13-18) and unpatchify (model.py:82-84): tokens [f h w, dim] -> bf16 [out, f, 2h, 2w]."""
+    dim = X.shape[1]
+    shift, scale = P["head_mod"].float().reshape(2, dim) + t_emb.float()[None, :]
+    y = F.layer_norm(X.float(), (dim,), eps=eps) * (1 + scale) + shift
+    o = linear_bf16(y, P["head_w"], P["head_b"])
+    out_dim = P["head_w"].shape[0] // 4
+    f, h, w = grid
+    return o.view(f, h, w, 1, 2, 2, out_dim).permute(6, 0, 3, 1, 4, 2, 5).reshape(out_dim, f, 2 * h, 2 * w)
+
+
+def model_forward(x: torch.Tensor, t: torch.Tensor, E: dict, blocks: list, caches: list, ctx_kvs: list, freq,
+                  start_frame: int, heads: int) -> torch.Tensor:
+    """WanModel.forward on one chunk (model.py:32-84) with oracle blocks: latent [C, f, H, W] -> flow bf16. Each
+    block's cache dict (k, ks, v, vs, at) receives the chunk's keys and values at `at`."""
+    _, f, H, W = x.shape
+    grid = (f, H // 2, W // 2)
+    X = patch_embed(x, E["patch_w"], E["patch_b"])
+    t_emb, e0 = time_embed(t, E)
+    for P, cache, kv in zip(blocks, caches, ctx_kvs):
+        X = oblock.block_forward(X, e0.float(), P, grid, freq, start_frame, cache, kv, heads)
+    return head(X, t_emb, E, grid)
+
+
+def next_chunk(noise: torch.Tensor, fresh: list, E: dict, blocks: list, caches: list, ctx_kvs: list, freq,
+               start_frame: int, heads: int, levels=None) -> torch.Tensor:
+    """Stream.next_chunk's DMD loop (causal.py:680-740): x0 of one chunk from `noise`, renoising with the given
+    `fresh` noises (one per level after the first), then the write pass at t = 0; the caches' write offsets `at`
+    advance by the chunk's tokens (the commit of a cache that is not full)."""
+    levels = sigmas() if levels is None else levels
+    x = noise.float()
+    x0 = x
+    for i, sigma in enumerate(levels):
+        flow = model_forward(x, torch.full((1,), 1000 * sigma), E, blocks, caches, ctx_kvs, freq, start_frame,
+                             heads).float()
+        x0 = x - sigma * flow
+        if i + 1 < len(levels):
+            x = (1 - levels[i + 1]) * x0 + levels[i + 1] * fresh[i]
+    model_forward(x0, torch.zeros(1), E, blocks, caches, ctx_kvs, freq, start_frame, heads)
+    n = x0.shape[1] * (x0.shape[2] // 2) * (x0.shape[3] // 2)
+    for cache in caches:
+        cache["at"] += n
+    return x0
