@@ -1,0 +1,76 @@
+"""The on-disk weight pack (wdl/pack.py; the reference's block_w4a4_v2 rows + manifest, quantization/w4a4.py:279-436)
+on the CPU: a round trip is bit-exact for every tensor, entries are 16-byte aligned, the manifest's sha256 is the
+file's, and a pack that exists, is incomplete, has another format / source or a wrong digest is refused."""
+
+import hashlib
+import json
+
+import pytest
+import torch
+
+from wdl import pack, w4a4
+
+
+def parts_of(dim, ffn, seed):
+    g = torch.Generator().manual_seed(seed)
+    shapes = dict(qkv=(3 * dim, dim), o=(dim, dim), cq=(dim, dim), ck=(dim, dim), cv=(dim, dim), co=(dim, dim),
+                  ffn1=(ffn, dim), ffn2=(dim, ffn))
+    P = {k: w4a4.random_parts(n, kk, "cpu", g) for k, (n, kk) in shapes.items()}
+    for k in ("wq", "wk", "cwq", "cwk"):
+        P[k] = torch.randn(dim, generator=g).to(torch.bfloat16)
+    P["n3w"], P["n3b"] = torch.randn(dim, generator=g), torch.randn(dim, generator=g)
+    P["modulation"] = torch.randn(6, dim, generator=g)
+    return P
+
+
+def same(a, b):
+    assert a.dtype == b.dtype and a.shape == b.shape
+    assert torch.equal(a.view(torch.uint8) if a.dtype != torch.uint8 else a,
+                       b.view(torch.uint8) if b.dtype != torch.uint8 else b)
+
+
+def test_round_trip_is_bit_exact(tmp_path):
+    blocks = [parts_of(256, 1024, s) for s in (0, 1)]
+    path = tmp_path / "blocks.pack"
+    info = pack.build_pack(blocks, path, source="test", calibrated=False)
+    assert info["format"] == pack.FORMAT and info["blocks"] == 2 and info["calibrated"] is False
+    rows, layout, meta = pack.mapped_pack(path, source="test", verify=True)
+    assert rows.shape == (2, meta["bytes_per_block"]) and meta["bytes"] == path.stat().st_size
+    assert all(e["offset"] % 16 == 0 for e in layout)
+    assert hashlib.sha256(path.read_bytes()).hexdigest() == meta["sha256"]
+    for i, parts in enumerate(blocks):
+        got = pack.slot(rows[i], layout)
+        for k in pack.LAYERS:
+            for p in pack.PARTS:
+                same(got[k][p], parts[k][p])
+        for k in pack.OTHERS:
+            same(got[k], parts[k])
+    assert not path.with_suffix(".pack.tmp").exists()
+
+
+def test_refusals(tmp_path):
+    blocks = [parts_of(128, 256, 2)]
+    path = tmp_path / "b.pack"
+    pack.build_pack(blocks, path, source="a")
+    with pytest.raises(FileExistsError):
+        pack.build_pack(blocks, path, source="a")
+    with pytest.raises(ValueError):
+        pack.mapped_pack(path, source="b")
+    data = bytearray(path.read_bytes())
+    data[100] ^= 1
+    path.write_bytes(bytes(data))
+    pack.mapped_pack(path)  # the digest is only checked on request
+    with pytest.raises(ValueError):
+        pack.mapped_pack(path, verify=True)
+    path.write_bytes(bytes(data[:-16]))
+    with pytest.raises(ValueError):
+        pack.mapped_pack(path)
+    manifest = path.with_suffix(".pack.json")
+    meta = json.loads(manifest.read_text())
+    meta["format"] = "block_w4a4_v2"  # the reference's Nunchaku layout is another format
+    manifest.write_text(json.dumps(meta))
+    with pytest.raises(ValueError):
+        pack.mapped_pack(path)
+    with pytest.raises(ValueError):  # blocks of different shapes cannot share a pack
+        pack.build_pack([parts_of(128, 256, 3), parts_of(128, 512, 4)], tmp_path / "c.pack")
+    assert not (tmp_path / "c.pack").exists() and not (tmp_path / "c.pack.json").exists()

@@ -1,0 +1,168 @@
+"""On-disk weight pack of quantized blocks in this build's physical layout (block_w4a4_v2_gfx950).
+
+The reference's block_w4a4_v2 pack (quantization/w4a4.py:279-313 pack_layout, 360-436 build_pack / mapped_pack;
+weight_pack.py:84-171 for the FP8 sibling): one uint8 row per block, each tensor of the block at a 16-byte aligned
+offset of the row, the rows back to back in one file, and a JSON manifest beside it (`<path>.json`) with the format,
+the layout (name, dtype, shape, offset, bytes per entry), the bytes per block, the sha256 of the whole file and the
+source identity. The file is written to `<path>.tmp` first and renamed when complete; an existing target raises
+FileExistsError; any failure removes what was written.
+
+This build's rows hold the QuantizedWanBlock parts in its own layouts (the reference's hold Nunchaku's): per W4A4
+layer — fused self_attn.qkv, self_attn.o, cross_attn.q / k / v / o, ffn.0 and ffn.2 (the GELU MLP's second layer,
+quantized for GELU's output + 0.171875) — qweight uint8 [N, K/2] (per 64-group byte j = k_j low nibble, k_{j+32}
+high nibble), wscales bf16 [K/64, N], proj_down bf16 [32, K], proj_up bf16 [N, 32], smooth bf16 [K], bias bf16
+[N]; then the Q/K RMSNorm weights (bf16), norm3's affine (fp32) and the modulation (fp32 [6, dim]). The manifest
+names that layout ("layout_notes"), so a reader never guesses it.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+from pathlib import Path
+
+import numpy as np
+import torch
+
+FORMAT = "block_w4a4_v2_gfx950"
+ALIGN = 16
+# this build's part names -> the reference block's module names (models/block.py, multi_head_attention.py)
+LAYERS = {"qkv": "self_attn.qkv", "o": "self_attn.o", "cq": "cross_attn.q", "ck": "cross_attn.k",
+          "cv": "cross_attn.v", "co": "cross_attn.o", "ffn1": "ffn.0", "ffn2": "ffn.2"}
+PARTS = ("qweight", "wscales", "proj_down", "proj_up", "smooth", "bias")
+OTHERS = {"wq": "self_attn.norm_q.weight", "wk": "self_attn.norm_k.weight", "cwq": "cross_attn.norm_q.weight",
+          "cwk": "cross_attn.norm_k.weight", "n3w": "norm3.weight", "n3b": "norm3.bias", "modulation": "modulation"}
+DTYPES = {torch.uint8: "uint8", torch.bfloat16: "bfloat16", torch.float32: "float32"}
+LAYOUT_NOTES = ("qweight uint8 [N, K/2]: per 64-group byte j holds k_j (low nibble) and k_{j+32} (high), int4 in "
+                "two's complement; wscales bf16 [K/64, N] group-major; proj_down bf16 [32, K] (transposed); proj_up "
+                "bf16 [N, 32]; smooth bf16 [K]; bias bf16 [N]; ffn.2 quantized for the GELU output + 0.171875 "
+                "(unsigned int4 activations); norm weights bf16; norm3 affine and modulation fp32")
+
+
+def _entries(parts: dict):
+    """(name, tensor) of a block's parts, in row order."""
+    for key, name in LAYERS.items():
+        for p in PARTS:
+            yield f"{name}.{p}", parts[key][p]
+    for key, name in OTHERS.items():
+        yield name, parts[key]
+
+
+def pack_layout(parts: dict):
+    """The row layout of a block's parts: [dict(name, dtype, shape, offset, bytes)], bytes per row."""
+    layout, offset = [], 0
+    for name, t in _entries(parts):
+        if t.dtype not in DTYPES:
+            raise TypeError(f"{name}: dtype {t.dtype} has no pack type")
+        size = t.numel() * t.element_size()
+        layout.append(dict(name=name, dtype=DTYPES[t.dtype], shape=list(t.shape), offset=offset, bytes=size))
+        offset += -(-size // ALIGN) * ALIGN
+    return layout, offset
+
+
+def build_pack(blocks: list, path, source: str = "", **metadata) -> dict:
+    """Writes the parts dicts of `blocks` (QuantizedWanBlock.p or build_block inputs; any device) as a pack at
+    `path` + its manifest; returns the manifest without the layout."""
+    path = Path(path)
+    manifest, temporary = path.with_suffix(path.suffix + ".json"), path.with_suffix(path.suffix + ".tmp")
+    if any(p.exists() for p in (path, manifest, temporary)):
+        raise FileExistsError(path)
+    if not blocks:
+        raise ValueError("a pack needs at least one block")
+    layout, size = pack_layout(blocks[0])
+    for b in blocks[1:]:
+        if pack_layout(b) != (layout, size):
+            raise ValueError("packed blocks must share one layout")
+    digest = hashlib.sha256()
+    try:
+        with temporary.open("xb") as stream:
+            for parts in blocks:
+                row = torch.zeros(size, dtype=torch.uint8)
+                for e, (name, t) in zip(layout, _entries(parts)):
+                    row[e["offset"]:e["offset"] + e["bytes"]] = t.detach().contiguous().cpu().reshape(-1).view(
+                        torch.uint8)
+                payload = row.numpy().tobytes()
+                digest.update(payload)
+                stream.write(payload)
+            stream.flush()
+            os.fsync(stream.fileno())
+        os.replace(temporary, path)
+        meta = dict(format=FORMAT, blocks=len(blocks), layout=layout, bytes_per_block=size,
+                    bytes=size * len(blocks), sha256=digest.hexdigest(), source=source, layout_notes=LAYOUT_NOTES,
+                    quantization="SVDQuant W4A4: int4 groups of 64, rank-32 low-rank branch in bf16, smoothing; "
+                                 "q, k, v of self-attention as one layer, the feed forward as the fused GELU MLP",
+                    **metadata)
+        manifest.write_text(json.dumps(meta, indent=1), encoding="utf-8")
+        return {k: v for k, v in meta.items() if k != "layout"}
+    except BaseException:
+        temporary.unlink(missing_ok=True)
+        path.unlink(missing_ok=True)
+        manifest.unlink(missing_ok=True)
+        raise
+
+
+def read_manifest(path) -> dict:
+    path = Path(path)
+    return json.loads(path.with_suffix(path.suffix + ".json").read_text(encoding="utf-8"))
+
+
+def mapped_pack(path, source: str | None = None, verify: bool = False):
+    """The pack at `path` mapped read-only: (uint8 [blocks, bytes per block], layout, manifest). Raises ValueError
+    for another format or source, an incomplete file, or (verify) a sha256 mismatch."""
+    path = Path(path)
+    meta = read_manifest(path)
+    if meta.get("format") != FORMAT:
+        raise ValueError(f"weight pack format {meta.get('format')!r} is not {FORMAT}")
+    if source is not None and meta.get("source") != source:
+        raise ValueError("weight pack was made from another source")
+    size, n = meta["bytes_per_block"], meta["blocks"]
+    if path.stat().st_size != size * n:
+        raise ValueError("weight pack is incomplete")
+    if verify:
+        digest = hashlib.sha256()
+        with path.open("rb") as f:
+            for chunk in iter(lambda: f.read(1 << 24), b""):
+                digest.update(chunk)
+        if digest.hexdigest() != meta["sha256"]:
+            raise ValueError("weight pack sha256 differs from its manifest")
+    data = np.memmap(path, dtype=np.uint8, mode="r")
+    import warnings
+
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore", UserWarning)  # a read-only map: torch warns that it is not writable
+        rows = torch.from_numpy(data).reshape(n, size)
+    return rows, meta["layout"], meta
+
+
+def slot(row: torch.Tensor, layout: list, device=None) -> dict:
+    """The parts dict of one row of a pack (copies on `device`), as QuantizedWanBlock takes it."""
+    inv_layers = {v: k for k, v in LAYERS.items()}
+    inv_others = {v: k for k, v in OTHERS.items()}
+    types = {v: k for k, v in DTYPES.items()}
+    parts = {k: {} for k in LAYERS}
+    for e in layout:
+        raw = row[e["offset"]:e["offset"] + e["bytes"]].clone()
+        t = raw.view(types[e["dtype"]]).reshape(e["shape"])
+        t = t.to(device) if device is not None else t
+        name = e["name"]
+        layer, _, part = name.rpartition(".")
+        if layer in inv_layers and part in PARTS:
+            parts[inv_layers[layer]][part] = t
+        elif name in inv_others:
+            parts[inv_others[name]] = t
+        else:
+            raise ValueError(f"unknown pack entry {name}")
+    return parts
+
+
+def load_blocks(path, heads: int, device, source: str | None = None, verify: bool = False) -> list:
+    """The QuantizedWanBlocks of the pack at `path` on `device` (each expands its weight codes once)."""
+    from wdl.block import QuantizedWanBlock
+
+    rows, layout, _ = mapped_pack(path, source, verify)
+    blocks = []
+    for i in range(rows.shape[0]):
+        parts = slot(rows[i], layout, device)
+        blocks.append(QuantizedWanBlock(parts, parts["modulation"].shape[1], heads))
+    return blocks
