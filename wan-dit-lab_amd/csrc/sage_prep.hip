@@ -147,9 +147,31 @@ __global__ void finalize_kernel(const float* part_k, const float* part_v, int S,
 
 __device__ __forceinline__ int v_position(int t) { return 32 * ((t % 8) / 4) + 4 * (t / 8) + t % 4; }
 
+// 32 e4m3 values (channels d0 .. d0 + 31, 32 contiguous bytes) of cached token t times the row's scale: two 16-byte
+// loads and one scale load (the values and products of four load_token8<CACHE> calls)
+__device__ __forceinline__ void load_cached32(const Src& s, int64_t t, int64_t h, int64_t H, int d0,
+                                              float (&f)[4][8]) {
+    const uint4* src = reinterpret_cast<const uint4*>(s.cache + (t * H + h) * D + d0);
+    const uint4 r0 = src[0], r1 = src[1];
+    const float sc = s.cscale[t * H + h];
+    const uint32_t w[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        e4m3x4_to_f32(w[2 * c], f[c]);
+        e4m3x4_to_f32(w[2 * c + 1], f[c] + 4);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[c][j] = f[c][j] * sc;
+    }
+}
+
 template <int SRC>
 __device__ __forceinline__ void quant_block(const Src& k, const Src& v, int64_t h, int64_t H, int64_t at, int64_t L,
                                             int64_t tok, int dq, float (&fk)[4][8], float (&fv)[4][8]) {
+    if (SRC == CACHE) {
+        load_cached32(k, tok, h, H, dq, fk);
+        load_cached32(v, tok, h, H, dq, fv);
+        return;
+    }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         load_token8<SRC>(k, tok, h, H, at, L, dq + c * 8, fk[c]);
@@ -265,6 +287,8 @@ extern "C" int wdl_sage_prep(const void* cache_k, const float* cache_ks, const v
         return fail(WDL_EINVAL, "sage_prep: null pointer");
     if ((reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) | (ldk * 2) | (ldv * 2)) % 16)
         return fail(WDL_EINVAL, "sage_prep: chunk rows must be 16-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(cache_k) | reinterpret_cast<uintptr_t>(cache_v)) % 16)
+        return fail(WDL_EINVAL, "sage_prep: the caches must be 16-byte aligned");
     if (L == 0) return WDL_OK;
     const int64_t Lpad = (L + 63) / 64 * 64;
     Src sk{static_cast<const uint8_t*>(cache_k), cache_ks, static_cast<const uint16_t*>(k), ldk};
