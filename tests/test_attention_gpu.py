@@ -108,6 +108,26 @@ def test_attention_matches_quantized_oracle_and_exact(gpu, at, n, H):
     assert osage.rel_err(out, exact) < 1.2 * osage.rel_err(emul8, exact) + 1e-3
 
 
+def test_attention_longest_window_with_k_bias(gpu):
+    """The chunk-causal attention workload's longest case: 2640 queries over 18480 cached + 2640 chunk keys (21120),
+    K with a per-channel bias N(0, 3^2) that the mean smoothing removes; one head (the oracle's CPU cost), at the
+    bars of the test above."""
+    from wdl import sage_kv
+
+    H = 1
+    kbias = torch.randn(1, 1, H, 128, generator=torch.Generator().manual_seed(8)) * 3
+    Q, k, ks, v, vs, at, K, V = setup(18480, 2640, H=H, seed=21, kbias=kbias)
+    out = sage_kv.attend(*cuda(Q, k, ks, v, vs), at, *cuda(K, V)).cpu().float()
+    p = osage.prep(Q, k, ks, v, vs, at, K, V)
+    emul = osage.attention_quantized(p, 128 ** -0.5)
+    emul8 = osage.attention_quantized(p, 128 ** -0.5, p_fp8=True)
+    exact = osage.attention_exact(Q, p["K"], p["V"])
+    cos = osage.cosine(out, emul)
+    print(f"21120 keys: cos vs emulation {cos:.6f}, err vs exact {osage.rel_err(out, exact):.4f}")
+    assert cos >= 0.999
+    assert osage.rel_err(out, exact) < 1.2 * osage.rel_err(emul8, exact) + 1e-3
+
+
 def test_attention_split_tiles_merge_across_workgroups(gpu):
     """(128-query tile, head) pairs just above the CU count: every CU runs one whole tile and the key blocks of the
     remaining tiles (the last head's, with the ragged query tile) are split over all CUs, their partial softmax

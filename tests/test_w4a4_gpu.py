@@ -127,7 +127,8 @@ def test_gemm_integer_accumulation_is_exact(gpu, M, N, K):
     assert torch.equal(y.cpu().double(), exact.double())
 
 
-@pytest.mark.parametrize("M,N,K,valid", [(128, 256, 512, 100), (256, 128, 3072, 256), (1408, 384, 3072, 1392)])
+@pytest.mark.parametrize("M,N,K,valid", [(128, 256, 512, 100), (256, 128, 3072, 256), (1408, 384, 3072, 1392),
+                                         (2688, 384, 3072, 2640)])
 def test_gemm_scaled_lowrank_bias_matches_oracle(gpu, M, N, K, valid):
     from wdl import w4a4
 
