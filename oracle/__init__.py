@@ -5,7 +5,7 @@ This package restates, on the CPU and in plain torch/numpy, the arithmetic of th
 RMSNorm/LayerNorm/modulation, the Sage-2 preparation (K mean, int8 K/Q, fp8 V) and quantized attention, and the
 Wan block. Every function cites the reference file:line it follows.
 
-Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import it, and only as the checker (or the
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import it, and only to check results (or as the
 timed CPU baseline). The product path (the wdl package and lib/libwdl.so) never imports or calls it.
 
 Pinning (what checks each function beyond its own formula) is listed in each module's docstring; functions whose

@@ -1,6 +1,6 @@
 """The quantized Wan DiT block on the CPU, restating src/wan_dit_lab/models/block.py:22-29 with the W4A4 linears
 (quantization/w4a4.py:248-262 FusedQKVAttention, 234-245 PackedW4A4GeluMLP), the FP8 KV cache and Sage attention
-(generation/causal.py:177-210; kernels/sage_kv.py), in the arithmetic this build defines for the fused kernels:
+(generation/causal.py:177-210; kernels/sage_kv.py), in the arithmetic wdl defines for the fused kernels:
 
   e = time_in + modulation (fp32), chunks shift_a, scale_a, gate_a, shift_f, scale_f, gate_f   (block.py:24)
   x1  = bf16(LN(X) * (1 + scale_a) + shift_a)                     one rounding (norms.ln_mod)

@@ -10,7 +10,7 @@ Tokens [0, at) come from the FP8 cache (value * per-row scale, fp32), [at, at + 
   scale = max|K - mean| / 127 + 1e-7; q = trunc(x / scale +- 0.5) (half away from zero); tokens >= L zero.
 - quant_v (sage_kv.py:88-105): e4m3(V / v_scale[d]), rounded to nearest even straight from fp32 (the reference's
   Triton cast goes through fp16 first; its own test allows 0.1 % differing bytes against Sage, test_sage_kv.py:55).
-  Values are returned token-major [B, L, H, D]; the layouts (the reference's 16-token permutation and this build's
+  Values are returned token-major [B, L, H, D]; the layouts (the reference's 16-token permutation and wdl's
   64-token one) are separate index maps (sage_v_layout, wdl_v_layout).
 - quant_q (sage_kv.py:112-124): per 32-token block, lane l = 0..7 owns tokens l, l+8, l+16, l+24 with one scale
   max|Q| / 127 + 1e-7; q = trunc(Q / scale +- 0.5).
@@ -111,7 +111,7 @@ def sage_v_layout(v_fp8: torch.Tensor) -> torch.Tensor:
 
 
 def wdl_v_position(t: torch.Tensor) -> torch.Tensor:
-    """This build's V order within a 64-token block: position p holds token perm[p], where the first 32 positions
+    """wdl's V order within a 64-token block: position p holds token perm[p], where the first 32 positions
     are tokens 8a + r (a = 0..7, r = 0..3) and the last 32 are 8a + 4 + r — the token order of one lane half of the
     transposed QK^T MFMA tile, so P feeds the PV MFMA without a shuffle. Returns the position of token t."""
     r = t % 64

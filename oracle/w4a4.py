@@ -84,7 +84,7 @@ def quantize_weight(weight: torch.Tensor, bias=None, smooth=None, rank: int = 32
 
 
 def act_quant(x: torch.Tensor, smooth: torch.Tensor, shift: float = 0.0, unsigned: bool = False):
-    """The activation quantizer (definition of this build; see the module docstring).
+    """The activation quantizer (definition of wdl; see the module docstring).
     x [M, K] (bf16 or fp32) -> q int32 [M, K] ([-8, 7] signed / [0, 15] unsigned), scales bf16 [M, K/64]."""
     M, K = x.shape
     v = x.float()

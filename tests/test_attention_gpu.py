@@ -79,7 +79,7 @@ def test_sage_prep_k_and_v(gpu, at, n, H):
     qk64, qks64 = osage.quant_k(Kf, ref_mean)
     assert int((got_k.int() - qk64.int()).abs().max()) <= 1
     assert torch.allclose(p["k_scale"].cpu()[None], qks64, rtol=2e-2)
-    # V: codes in this build's layout, bit-exact
+    # V: codes in wdl's layout, bit-exact
     vq = osage.quant_v(Vf, p["v_scale"].cpu()[None])
     want = osage.wdl_v_layout(vq)[0].view(torch.uint8)  # [H, 128, Lpad]
     assert p["v"].shape == (H, 128, Lp)

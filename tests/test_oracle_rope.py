@@ -9,7 +9,7 @@
 - the axis split [22, 21, 21] of a 128-dim head (tests/test_kv_cache.py:12);
 - tokens past f h w pass through unchanged (kernels/rope_triton.py:54-56);
 - KVCache.scale's known answers (tests/test_resolution_adaptation.py:16-21) and rope_at's
-  (tests/test_resolution_adaptation.py:36-40), the latter on this build's host tables (wdl.rope).
+  (tests/test_resolution_adaptation.py:36-40), the latter on wdl's host tables (wdl.rope).
 """
 
 import math

@@ -1,5 +1,5 @@
 // Sage-2 style attention on gfx950: int8 Q K^T, fp32 online softmax, fp8 P V, non-causal over L keys
-// (the computation of live::sage_sm89, native/ops/sage_ops.cpp:12-19, on this build's operand layouts).
+// (the computation of live::sage_sm89, native/ops/sage_ops.cpp:12-19, on wdl's operand layouts).
 //
 //   s[q][t]  = q_scale[q] * k_scale[t] * (q_i8 . k_i8)               (exact int32 dot product, then fp32)
 //   O[q][d]  = sum_t softmax_t(s * sm_scale)[q][t] * v_fp8[t][d] * v_scale[d]
@@ -9,7 +9,7 @@
 //
 // Work split: one workgroup = 128 queries of one head and 8 waves: two groups of 4 waves split the key blocks in
 // halves (so every SIMD runs two waves), each wave owning 32 queries. A group streams its 64-key blocks of K
-// (int8 [64][128]) and V (fp8 [128][64], this build's token order) straight from global memory into a 4-stage LDS
+// (int8 [64][128]) and V (fp8 [128][64], wdl's token order) straight from global memory into a 4-stage LDS
 // ring (global_load_lds, 16 bytes per lane, 4 loads per wave per block, issued 3 blocks ahead, waited for with an
 // explicit vmcnt); rows are 64 bytes with their 16-byte quarters XOR-swizzled by (row / 4) % 4. Both groups step
 // through the same number of ring steps (the shorter one idles through its last), so the barriers match.

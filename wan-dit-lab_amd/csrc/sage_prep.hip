@@ -7,7 +7,7 @@
 //   finalize   (grid H):     k_mean = (sum over splits, in order) / L;  v_scale = max(max |V|, 1e-8) / 2.25;
 //   quant_kv   (grid blocks x H): K - mean to int8 with one scale per group g = 0..3 of each 64-token block (tokens
 //              8i + 2g, 8i + 2g + 1): scale = max|x| / 127 + 1e-7, q = trunc(x / scale +- 0.5);
-//              V / v_scale to e4m3, stored per (head, channel) along the tokens in this build's order: within a
+//              V / v_scale to e4m3, stored per (head, channel) along the tokens in wdl's order: within a
 //              64-token block, position 32 * ((t % 8) / 4) + 4 * (t / 8) + t % 4 holds token t (the key order one
 //              lane half of the transposed QK^T MFMA tile produces, so P feeds the PV MFMA unshuffled).
 // Layouts: k_int8 [H, Lpad, 128]; k_scale fp32 [H, Lpad / 64 * 4]; v_fp8 [H, 128, Lpad]; Lpad = 64 * ceil(L / 64);

@@ -1,4 +1,4 @@
-"""FP8 (E4M3) linear layers on MI355X: the API of src/wan_dit_lab/quantization/fp8.py over this build's HIP kernels.
+"""FP8 (E4M3) linear layers on MI355X: the API of src/wan_dit_lab/quantization/fp8.py over wdl's HIP kernels.
 
 W8A8: the weight in FP8 with one scale per tensor (Fp8Linear, PackedFp8Linear, DynamicFp8Linear rows=False) or one
 per output row (DynamicFp8Linear rows=True), the activation quantized on every call by its own maximum (per tensor

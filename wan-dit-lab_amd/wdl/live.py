@@ -3,8 +3,8 @@
 The reference registers `live::w4a4_linear` and `live::w4a4_gelu_mlp` from Nunchaku-based DLLs
 (src/wan_dit_lab/kernels/operators.py:12-24; native/ops/w4a4_ops.cpp:79-95) and calls them as
 `torch.ops.live.w4a4_linear(...)` (quantization/w4a4.py:212-213, 242-245). Importing this module registers the same
-names and schemas over this build's HIP kernels, so those call sites run unchanged on MI355X, given weights packed
-by wdl.w4a4.quantize (this build's layout; Nunchaku's tile order is not reproduced).
+names and schemas over wdl's HIP kernels, so those call sites run unchanged on MI355X, given weights packed
+by wdl.w4a4.quantize (wdl's layout; Nunchaku's tile order is not reproduced).
 
 `live::sage_sm89` is not aliased: its operands are laid out for SageAttention's sm89 kernel. The attention swap
 point is one level up, `sage_kv.attend` / `KVCache.attend` (kernels/sage_kv.py:127-134; generation/causal.py:193-

@@ -1,4 +1,4 @@
-"""On-disk weight pack of quantized blocks in this build's physical layout (block_w4a4_v2_gfx950).
+"""On-disk weight pack of quantized blocks in wdl's physical layout (block_w4a4_v2_gfx950).
 
 The reference's block_w4a4_v2 pack (quantization/w4a4.py:279-313 pack_layout, 360-436 build_pack / mapped_pack;
 weight_pack.py:84-171 for the FP8 sibling): one uint8 row per block, each tensor of the block at a 16-byte aligned
@@ -7,7 +7,7 @@ the layout (name, dtype, shape, offset, bytes per entry), the bytes per block, t
 source identity. The file is written to `<path>.tmp` first and renamed when complete; an existing target raises
 FileExistsError; any failure removes what was written.
 
-This build's rows hold the QuantizedWanBlock parts in its own layouts (the reference's hold Nunchaku's): per W4A4
+The library's rows hold the QuantizedWanBlock parts in its own layouts (the reference's hold Nunchaku's): per W4A4
 layer — fused self_attn.qkv, self_attn.o, cross_attn.q / k / v / o, ffn.0 and ffn.2 (the GELU MLP's second layer,
 quantized for GELU's output + 0.171875) — qweight uint8 [N, K/2] (per 64-group byte j = k_j low nibble, k_{j+32}
 high nibble), wscales bf16 [K/64, N], proj_down bf16 [32, K], proj_up bf16 [N, 32], smooth bf16 [K], bias bf16
@@ -27,7 +27,7 @@ import torch
 
 FORMAT = "block_w4a4_v2_gfx950"
 ALIGN = 16
-# this build's part names -> the reference block's module names (models/block.py, multi_head_attention.py)
+# wdl's part names -> the reference block's module names (models/block.py, multi_head_attention.py)
 LAYERS = {"qkv": "self_attn.qkv", "o": "self_attn.o", "cq": "cross_attn.q", "ck": "cross_attn.k",
           "cv": "cross_attn.v", "co": "cross_attn.o", "ffn1": "ffn.0", "ffn2": "ffn.2"}
 PARTS = ("qweight", "wscales", "proj_down", "proj_up", "smooth", "bias")

@@ -53,6 +53,6 @@ def quant_q(Q):
 
 
 def prep(cache_k, cache_ks, cache_v, cache_vs, at, K, V):
-    """The quantized K/V operands of one call in this build's layouts (see wdl_sage_prep in include/wdl.h)."""
+    """The quantized K/V operands of one call in wdl's layouts (see wdl_sage_prep in include/wdl.h)."""
     return sage_prep_launch(cache_k.view(torch.uint8), cache_ks, cache_v.view(torch.uint8), cache_vs,
                             K[0].flatten(1), V[0].flatten(1), at, want_stats=True)

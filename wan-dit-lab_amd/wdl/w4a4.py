@@ -2,7 +2,7 @@
 
     y = x W^T + b = Q(x / s) Q(R)^T + (x proj_down) proj_up^T + b,      W diag(s) = up down + R     (w4a4.py:4-10)
 
-Weights are quantized offline (quantize, w4a4.py:140-180) into this build's own packed layout (the reference packs
+Weights are quantized offline (quantize, w4a4.py:140-180) into wdl's own packed layout (the reference packs
 into Nunchaku's MMA tile order, which lives outside its tree):
 - qweight uint8 [N, K/2]: per 64-channel group, byte j holds k = j in the low nibble and k = j + 32 in the high
   nibble, two's complement int4 (pack_weight / unpack_weight);
@@ -63,7 +63,7 @@ def smoothing(act_amax: torch.Tensor, weight: torch.Tensor, alpha: float = 0.5) 
 
 
 def pack_weight(q: torch.Tensor) -> torch.Tensor:
-    """int4 values [N, K] -> uint8 [N, K/2] in this build's layout (module docstring)."""
+    """int4 values [N, K] -> uint8 [N, K/2] in wdl's layout (module docstring)."""
     N, K = q.shape
     u = (q.to(torch.int32) & 0xF).to(torch.uint8).reshape(N, K // GROUP, 2, GROUP // 2)
     return (u[:, :, 0] | (u[:, :, 1] << 4)).reshape(N, K // 2).contiguous()
@@ -80,7 +80,7 @@ def unpack_weight(p: torch.Tensor) -> torch.Tensor:
 
 @torch.no_grad()
 def quantize(weight, bias=None, smooth=None, rank: int = 32, shift: float = 0.0, rule: str = "max", R=None):
-    """The tensors of a W4A4 layer for y = x W^T + b (w4a4.py:140-180) in this build's packed layout.
+    """The tensors of a W4A4 layer for y = x W^T + b (w4a4.py:140-180) in wdl's packed layout.
     weight [N, K]; smooth [K] (ones when None); shift: the second GELU-MLP layer quantizes x + shift unsigned, so
     its bias takes off shift * (Q(R) / s) 1. R: the quantizer input, when given (parity tests)."""
     W = weight.float()
@@ -204,7 +204,7 @@ class FusedQKVAttention(torch.nn.Module):
 
 def pack_parts(logical: dict, device=None) -> dict:
     """Logical parts (q int [N, K], wscales [N, K/64], proj_down [K, r], proj_up [N, r], smooth [K], bias [N]) ->
-    this build's packed layout, on `device`."""
+    wdl's packed layout, on `device`."""
     return dict(
         qweight=pack_weight(logical["q"]).to(device),
         wscales=logical["wscales"].to(torch.bfloat16).t().contiguous().to(device),
