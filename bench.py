@@ -209,8 +209,8 @@ def main():
                          "known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: the quantized Wan block hot path runs on a single MI355X; "
-              "--gpus above 1 is not supported: the benchmark runs on one GPU", file=sys.stderr)
+        print("bench.py measures one GPU: the quantized Wan block hot path runs on a single MI355X, so --gpus "
+              "above 1 is not supported", file=sys.stderr)
         sys.exit(2)
     import torch
 
