@@ -1,0 +1,84 @@
+"""Kernel timings at the step's shapes, for profiling runs: `python -m wdl.kbench attention|gemm [lib]`.
+
+attention: Sage prep + attention of 1280 and 1392 queries over a full 9744-key window (8352 cached FP8 tokens + the
+chunk), 24 x 128 heads; gemm: the W4A4 GEMMs of one block at 1392 tokens (QKV 3072 -> 9216, o 3072 -> 3072 with the
+gated residual, FFN-up 3072 -> 14336 with GELU, FFN-down 14336 -> 3072 with the gated residual), random weights.
+Each shape is captured into a HIP graph of 10 launches and replayed; one line per shape with microseconds per
+launch. An optional library path replaces lib/libwdl.so (for comparing builds).
+"""
+
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+
+def _replay_us(fn, reps: int = 10) -> float:
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps * 1e3
+
+
+def attention():
+    import torch
+
+    from wdl import ops
+
+    dev, H = "cuda", 24
+    g = torch.Generator(device=dev).manual_seed(0)
+    for n, at in ((1280, 8464), (1392, 8352)):
+        L = at + n
+        ck = (torch.randn(1, at, H, 128, device=dev, generator=g) * 50).clamp(-448, 448).to(torch.float8_e4m3fn)
+        cks = torch.rand(1, at, H, 1, device=dev, generator=g) * 0.02
+        K, V, Q = (torch.randn(n, H * 128, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+        prep = ops.sage_prep_launch(ck.view(torch.uint8), cks, ck.view(torch.uint8), cks, K, V, at)
+        out = torch.empty(n, H * 128, device=dev, dtype=torch.bfloat16)
+        us = _replay_us(lambda: ops.sage_attn_q16_launch(Q, prep, L, 128 ** -0.5, out))
+        print(f"attention n={n} L={L}: {us:.1f} us ({4 * n * L * 128 * H / us / 1e6:.0f} TOP/s)", flush=True)
+
+
+def gemm():
+    import torch
+
+    from wdl import ops, w4a4
+
+    dev, M = "cuda", 1392
+    g = torch.Generator(device=dev).manual_seed(0)
+    for name, N, K, epi in (("qkv", 9216, 3072, ops.EPI_BF16), ("o", 3072, 3072, ops.EPI_RESIDUAL),
+                            ("ffn1", 14336, 3072, ops.EPI_GELU), ("ffn2", 3072, 14336, ops.EPI_RESIDUAL)):
+        t = w4a4.random_parts(N, K, dev, g)
+        wc = ops.as_codes(t["qweight"], K)
+        x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+        q, asc, lora = ops.act_quant_launch(x, t["smooth"], t["proj_down"])
+        out = torch.randn(M, N, device=dev, generator=g).to(torch.bfloat16)
+        gate = torch.rand(N, device=dev) if epi == ops.EPI_RESIDUAL else None
+        us = _replay_us(lambda: ops.gemm_launch(q, asc, lora, wc, t["wscales"], t["proj_up"], t["bias"], M, out, epi,
+                                                gate))
+        print(f"gemm {name} {M}x{N}x{K}: {us:.1f} us ({2 * M * N * K / us / 1e6:.0f} TOP/s)", flush=True)
+
+
+def main(argv):
+    if len(argv) < 2 or argv[1] not in ("attention", "gemm"):
+        raise SystemExit("usage: python -m wdl.kbench attention|gemm [library path]")
+    if len(argv) > 2:
+        from wdl import _lib
+
+        _lib.LIB_PATH = Path(argv[2])
+    {"attention": attention, "gemm": gemm}[argv[1]]()
+
+
+if __name__ == "__main__":
+    main(sys.argv)
