@@ -81,6 +81,30 @@ class Step:
         return self.model.forward(self.latent, self.t, self.start_frame)
 
 
+def chunk_ms(step, chunks: int) -> float:
+    """Milliseconds per chunk of Stream.next_chunk's DMD loop over the step's model (generation/causal.py:680-740):
+    four levels, the write pass and the commit of every block's full FP8 window (the oldest frames evicted), eager;
+    one chunk of warm-up first."""
+    import torch
+
+    from wdl.model import ChunkStream
+
+    gen = torch.Generator(device=step.latent.device).manual_seed(1)
+    stream = ChunkStream(step.model, tuple(step.latent.shape), gen)
+    stream.start = step.start_frame
+    stream.next_chunk()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(chunks):
+        stream.next_chunk()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / chunks
+    log(f"bench: {ms:.2f} ms per chunk (DMD loop, eager)")
+    return ms
+
+
 def instrumented(step):
     """One eager step with HIP events around every W4A4 GEMM and attention launch (on the launch stream)."""
     import torch
@@ -204,6 +228,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of the HIP graph")
+    ap.add_argument("--chunks", type=int, default=0, metavar="C",
+                    help="also time C whole chunks of the DMD loop (4 levels + write pass + cache commit, eager) "
+                         "after the step measurement, as chunk_ms")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain elementwise copy of MIB MiB (bitwise_not, uint8) three times: the "
                          "known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -295,6 +322,8 @@ def main():
                               "metric's dense int8 MFMA peak (the kernel issues fp6 MFMAs, dense peak 10.1 POP/s: "
                               "against that the fraction is half)"},
     }
+    if args.chunks > 0:
+        result["chunk_ms"] = chunk_ms(step, args.chunks)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)
