@@ -1,8 +1,9 @@
-"""Kernel timings at the step's shapes, for profiling runs: `python -m wdl.kbench attention|gemm [lib]`.
+"""Kernel timings at the step's shapes, for profiling runs: `python -m wdl.kbench attention|gemm|quant [lib]`.
 
 attention: Sage prep + attention of 1280 and 1392 queries over a full 9744-key window (8352 cached FP8 tokens + the
 chunk), 24 x 128 heads; gemm: the W4A4 GEMMs of one block at 1392 tokens (QKV 3072 -> 9216, o 3072 -> 3072 with the
-gated residual, FFN-up 3072 -> 14336 with GELU, FFN-down 14336 -> 3072 with the gated residual), random weights.
+gated residual, FFN-up 3072 -> 14336 with GELU, FFN-down 14336 -> 3072 with the gated residual), random weights; quant: the activation quantizer with its low-rank down projection at 1392 tokens
+(K 3072 with the fused LayerNorm and modulation, K 3072 plain, K 14336 unsigned).
 Each shape is captured into a HIP graph of 10 launches and replayed; one line per shape with microseconds per
 launch. An optional library path replaces lib/libwdl.so (for comparing builds).
 """
@@ -70,14 +71,32 @@ def gemm():
         print(f"gemm {name} {M}x{N}x{K}: {us:.1f} us ({2 * M * N * K / us / 1e6:.0f} TOP/s)", flush=True)
 
 
+def quant():
+    import torch
+
+    from wdl import ops, w4a4
+
+    dev, M = "cuda", 1392
+    g = torch.Generator(device=dev).manual_seed(0)
+    for name, K, ln, unsigned in (("ln", 3072, True, False), ("plain", 3072, False, False),
+                                  ("unsigned", 14336, False, True)):
+        t = w4a4.random_parts(64, K, dev, g)
+        x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+        lnd = dict(shift=torch.randn(K, device=dev, generator=g) * 0.1, scale=torch.randn(K, device=dev,
+                   generator=g) * 0.1, weight=None, bias=None, eps=1e-6) if ln else None
+        us = _replay_us(lambda: ops.act_quant_launch(x, t["smooth"], t["proj_down"], 0.171875 if unsigned else 0.0,
+                                                     unsigned, ln=lnd))
+        print(f"quant {name} {M}x{K}: {us:.1f} us ({M * K * 2 / us / 1e3:.0f} GB/s of x)", flush=True)
+
+
 def main(argv):
-    if len(argv) < 2 or argv[1] not in ("attention", "gemm"):
-        raise SystemExit("usage: python -m wdl.kbench attention|gemm [library path]")
+    if len(argv) < 2 or argv[1] not in ("attention", "gemm", "quant"):
+        raise SystemExit("usage: python -m wdl.kbench attention|gemm|quant [library path]")
     if len(argv) > 2:
         from wdl import _lib
 
         _lib.LIB_PATH = Path(argv[2])
-    {"attention": attention, "gemm": gemm}[argv[1]]()
+    {"attention": attention, "gemm": gemm, "quant": quant}[argv[1]]()
 
 
 if __name__ == "__main__":
