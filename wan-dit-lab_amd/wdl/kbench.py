@@ -1,7 +1,8 @@
-"""Kernel timings at the step's shapes, for profiling runs: `python -m wdl.kbench attention|gemm|quant [lib]`.
+"""Kernel timings at the step's shapes, for profiling runs: `python -m wdl.kbench attention|prep|gemm|quant [lib]`.
 
 attention: Sage prep + attention of 1280 and 1392 queries over a full 9744-key window (8352 cached FP8 tokens + the
-chunk), 24 x 128 heads; gemm: the W4A4 GEMMs of one block at 1392 tokens (QKV 3072 -> 9216, o 3072 -> 3072 with the
+chunk), 24 x 128 heads; prep: the Sage preparation (K mean and V maxima, int8 K and fp8 V of the whole window) of
+the same two shapes; gemm: the W4A4 GEMMs of one block at 1392 tokens (QKV 3072 -> 9216, o 3072 -> 3072 with the
 gated residual, FFN-up 3072 -> 14336 with GELU, FFN-down 14336 -> 3072 with the gated residual), random weights; quant: the activation quantizer with its low-rank down projection at 1392 tokens
 (K 3072 with the fused LayerNorm and modulation, K 3072 plain, K 14336 unsigned).
 Each shape is captured into a HIP graph of 10 launches and replayed; one line per shape with microseconds per
@@ -51,6 +52,23 @@ def attention():
         print(f"attention n={n} L={L}: {us:.1f} us ({4 * n * L * 128 * H / us / 1e6:.0f} TOP/s)", flush=True)
 
 
+def prep():
+    import torch
+
+    from wdl import ops
+
+    dev, H = "cuda", 24
+    g = torch.Generator(device=dev).manual_seed(0)
+    for n, at in ((1280, 8464), (1392, 8352)):
+        ck = (torch.randn(1, at, H, 128, device=dev, generator=g) * 50).clamp(-448, 448).to(torch.float8_e4m3fn)
+        cks = torch.rand(1, at, H, 1, device=dev, generator=g) * 0.02
+        K, V = (torch.randn(n, H * 128, device=dev, generator=g).to(torch.bfloat16) for _ in range(2))
+        us = _replay_us(lambda: ops.sage_prep_launch(ck.view(torch.uint8), cks, ck.view(torch.uint8), cks, K, V, at))
+        L = at + n
+        moved = 2 * (2 * at * H * 132 + 2 * n * H * 256) + 2 * L * H * 128  # inputs read twice, outputs written once
+        print(f"prep n={n} L={L}: {us:.1f} us ({moved / us / 1e3:.0f} GB/s)", flush=True)
+
+
 def gemm():
     import torch
 
@@ -90,13 +108,13 @@ def quant():
 
 
 def main(argv):
-    if len(argv) < 2 or argv[1] not in ("attention", "gemm", "quant"):
-        raise SystemExit("usage: python -m wdl.kbench attention|gemm|quant [library path]")
+    if len(argv) < 2 or argv[1] not in ("attention", "prep", "gemm", "quant"):
+        raise SystemExit("usage: python -m wdl.kbench attention|prep|gemm|quant [library path]")
     if len(argv) > 2:
         from wdl import _lib
 
         _lib.LIB_PATH = Path(argv[2])
-    {"attention": attention, "gemm": gemm, "quant": quant}[argv[1]]()
+    {"attention": attention, "prep": prep, "gemm": gemm, "quant": quant}[argv[1]]()
 
 
 if __name__ == "__main__":
