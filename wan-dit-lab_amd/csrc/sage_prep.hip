@@ -201,14 +201,16 @@ __global__ __launch_bounds__(256) void quant_kv_kernel(Src k, Src v, int64_t H, 
     else if (b0 >= at && b1 <= L) quant_block<CHUNK>(k, v, h, H, at, L, tok, dq, fk, fv);
     else quant_block<MIXED>(k, v, h, H, at, L, tok, dq, fk, fv);
     __syncthreads();
-    // K - mean: 32 channels of one token per thread
+    // K - mean: 32 channels of one token per thread. Tokens >= L loaded as +0 (load_token8), so with live = 0 the
+    // fma gives +0 and with live = 1 it is the one rounding of fk - mean; their V quotients are +0, code 0.
+    const float live = tok < L ? 1.0f : 0.0f;
     float x[32];
     float amax = 0.0f;
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float y = tok < L ? fk[c][j] - stat[0][dq + c * 8 + j] : 0.0f;
+            const float y = fmaf(-stat[0][dq + c * 8 + j], live, fk[c][j]);
             x[c * 8 + j] = y;
             amax = fmaxf(amax, fabsf(y));
         }
@@ -222,8 +224,8 @@ __global__ __launch_bounds__(256) void quant_kv_kernel(Src k, Src v, int64_t H, 
             const float y0 = div_rn(fv[c][j], stat[1][d], stat[2][d]);
             const float y1 = div_rn(fv[c][j + 1], stat[1][d + 1], stat[2][d + 1]);
             const uint32_t w = __builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false);
-            vt[d][v_position(tt)] = tok < L ? uint8_t(w) : uint8_t(0);
-            vt[d + 1][v_position(tt)] = tok < L ? uint8_t(w >> 8) : uint8_t(0);
+            vt[d][v_position(tt)] = uint8_t(w);
+            vt[d + 1][v_position(tt)] = uint8_t(w >> 8);
         }
     __syncthreads();
     const int g = (tt % 8) / 2;
@@ -250,7 +252,7 @@ __global__ __launch_bounds__(256) void quant_kv_kernel(Src k, Src v, int64_t H, 
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float y = div_rn(x[c * 16 + b * 4 + e], scale, rscale);
-                const float r = __builtin_truncf(y + (y >= 0.0f ? 0.5f : -0.5f));
+                const float r = __builtin_truncf(y + __builtin_copysignf(0.5f, y));  // half away from zero
                 word |= (uint32_t(int32_t(r)) & 0xffu) << (8 * e);
             }
             w[b] = word;
