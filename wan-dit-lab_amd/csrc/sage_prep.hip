@@ -251,11 +251,16 @@ __global__ __launch_bounds__(256) void quant_kv_kernel(Src k, Src v, int64_t H, 
             uint32_t word = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float y = div_rn(x[c * 16 + b * 4 + e], scale, rscale);
-                const float r = __builtin_truncf(y + __builtin_copysignf(0.5f, y));  // half away from zero
-                word |= (uint32_t(int32_t(r)) & 0xffu) << (8 * e);
+                // the correctly rounded quotient (div_rn without its sign fix: a zero of either sign rounds to 0),
+                // rounded half away from zero; r + 128 is an integer in [1, 255], packed as an exact u8 conversion
+                // and turned into the two's-complement byte by the xor below
+                const float xv = x[c * 16 + b * 4 + e];
+                const float q0 = xv * rscale;
+                const float y = fmaf(fmaf(-q0, scale, xv), rscale, q0);
+                const float r = __builtin_truncf(y + __builtin_copysignf(0.5f, y)) + 128.0f;
+                word = __builtin_amdgcn_cvt_pk_u8_f32(r, e, word);
             }
-            w[b] = word;
+            w[b] = word ^ 0x80808080u;
         }
         *reinterpret_cast<uint4*>(kd + c * 16) = make_uint4(w[0], w[1], w[2], w[3]);
     }
