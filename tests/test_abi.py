@@ -29,6 +29,25 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert lib.wdl_last_error() == b""
 
 
+def test_return_types_follow_the_header():
+    """Every entry point the header declares as returning int64_t is bound with a 64-bit ctypes result (the c_int
+    default would silently truncate a workspace size), and every other int entry point with c_int."""
+    import ctypes
+
+    from wdl import _lib
+
+    text = (ROOT / "include" / "wdl.h").read_text()
+    wide = set(re.findall(r"^\s*int64_t\s+(wdl_\w+)\(", text, re.M))
+    narrow = set(re.findall(r"^\s*int\s+(wdl_\w+)\(", text, re.M))
+    assert wide and narrow
+    lib = _lib.library()
+    for name in wide:
+        assert _lib.RESTYPES.get(name) is ctypes.c_int64, name
+        assert getattr(lib, name).restype is ctypes.c_int64, name
+    for name in narrow:
+        assert getattr(lib, name).restype is ctypes.c_int, name
+
+
 def test_invalid_call_reports_error_without_launch():
     from wdl import _lib
 

@@ -42,9 +42,9 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 }
 
 struct GemmArgs {
-    const uint8_t* qa;        // [Mp, K] e4m3 codes
+    const uint8_t* qa;        // W4A4: fp6 e2m3 codes, tile-blocked [Mp/128][K/64][128][48]; FP8: e4m3 [Mp, K]
     const uint16_t* as;       // [G, Mp]
-    const uint8_t* wc;        // [N, K] e4m3 codes
+    const uint8_t* wc;        // W4A4: fp6 e3m2 codes, tile-blocked [N/128][K/64][128][48]; FP8: e4m3 [N, K]
     const uint16_t* ws;       // [G, N]
     const float* lora;        // [Mp, 32] or null
     const uint16_t* pu;       // [N, 32] or null

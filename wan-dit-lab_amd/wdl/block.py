@@ -34,7 +34,7 @@ class QuantizedWanBlock:
     def __init__(self, parts: dict, dim: int, heads: int, eps: float = 1e-6):
         self.p, self.dim, self.heads, self.eps = parts, dim, heads, eps
         dev = parts["qkv"]["qweight"].device
-        for name in LINEARS:  # the GEMM operand: tile-blocked e4m3 codes, expanded once from the packed nibbles
+        for name in LINEARS:  # the GEMM operand: tile-blocked fp6 codes (e3m2 of 2w), expanded once from the nibbles
             parts[name]["wcodes"] = ops.weight_codes(parts[name]["qweight"])
         self.ones = torch.ones(dim, device=dev, dtype=torch.float32)
 

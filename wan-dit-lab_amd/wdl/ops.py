@@ -336,20 +336,41 @@ def sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, k, v, at, want_stats=
 
 _ATTN_WS: dict = {}
 _GEMM_WS: dict = {}
+# Buffers a larger request replaced. A HIP graph captured while one of them was current keeps its address in its
+# kernel arguments, so none is ever freed: a replay after the growth still writes memory that is its own.
+_RETIRED: list = []
 
 
 def workspace(cache: dict, device: torch.device, nbytes: int) -> torch.Tensor | None:
-    """A device's scratch buffer for one kind of call (partial results of split tiles), grown when a call needs
-    more; no initial contents are needed. One per device and kind: such calls on one device must not overlap (each
-    launches on the current stream of its tensors)."""
+    """A device's scratch buffer for one kind of call (partial results of split tiles); no initial contents are
+    needed. One per device and kind: such calls on one device must not overlap (each launches on the current stream
+    of its tensors). A request larger than the buffer replaces it (the old one is kept alive, see _RETIRED); during
+    stream capture that raises instead, since the captured graph would hold an allocation made inside the capture:
+    size the buffer first with reserve()."""
     if nbytes <= 0:
         return None
     key = device.index if device.index is not None else torch.cuda.current_device()
     ws = cache.get(key)
     if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(f"workspace of {nbytes} bytes requested during graph capture (have "
+                               f"{0 if ws is None else ws.numel()}): call wdl.ops.reserve() for the largest shape "
+                               f"before capturing")
+        if ws is not None:
+            _RETIRED.append(ws)
         ws = torch.empty(max(nbytes, 1 << 20), device=device, dtype=torch.uint8)
         cache[key] = ws
     return ws
+
+
+def reserve(device: torch.device, *, gemm: tuple | None = None, attn: tuple | None = None) -> None:
+    """Sizes the scratch buffers up front for the largest shapes a caller will run (and capture): gemm = (Mp, N, K)
+    of the largest W4A4 product, attn = (n, L, heads) of the largest attention."""
+    lib = _lib.library()
+    if gemm is not None:
+        workspace(_GEMM_WS, device, lib.wdl_w4a4_gemm_workspace_bytes(*(int(v) for v in gemm)))
+    if attn is not None:
+        workspace(_ATTN_WS, device, lib.wdl_sage_attn_workspace_bytes(*(int(v) for v in attn)))
 
 
 def sage_attn_launch(q_i8, q_scale, prep, L, sm_scale, out=None):

@@ -28,6 +28,13 @@ def _check(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V):
         raise TypeError("cache scales must be FP32")
     if Q.dtype != torch.bfloat16 or K.dtype != torch.bfloat16 or V.dtype != torch.bfloat16:
         raise TypeError("Q, K, V must be bf16")
+    H = K.shape[2]
+    if cache_k.ndim != 4 or cache_k.shape[0] != 1 or cache_k.shape[2:] != (H, 128) or cache_v.shape != cache_k.shape:
+        raise ValueError("cache_k / cache_v must be [1, capacity, heads, 128] (batch 1)")
+    if cache_ks.shape != (*cache_k.shape[:3], 1) or cache_vs.shape != cache_ks.shape:
+        raise ValueError("cache_ks / cache_vs must be [1, capacity, heads, 1]: one scale per cache row")
+    if any(not t.is_contiguous() for t in (cache_k, cache_ks, cache_v, cache_vs)):
+        raise ValueError("cache buffers must be contiguous (the kernels index rows as (token * heads + head))")
     if not isinstance(at, int) or at < 0 or at > cache_k.shape[1]:
         raise ValueError("at outside the cache")
     if any(t.stride(-1) != 1 or t.stride(-2) != 128 for t in (Q, K, V)):

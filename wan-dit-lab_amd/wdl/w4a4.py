@@ -135,7 +135,7 @@ def gelu_mlp(x: torch.Tensor, t1: dict, t2: dict) -> torch.Tensor:
 
 
 def _operand(parts: dict, name: str):
-    """Module operands: packed weights on the GPU are expanded once to the GEMM's e4m3 codes [N, K]."""
+    """Module operands: packed weights on the GPU are expanded once to the GEMM's tile-blocked fp6 codes (e3m2 of 2w) of [N, K]."""
     t = parts[name]
     return ops.weight_codes(t) if name == "qweight" and t.is_cuda else t
 
