@@ -1,5 +1,8 @@
-"""The oracle's FP8 rule against the reference's known answers (tests/test_cache_fp8.py:47-58, 150-158) and an
-independent brute-force nearest-value search over the e4m3 codes."""
+"""The oracle's FP8 rule against the reference's known answers (tests/test_cache_fp8.py:47-58, 150-158, kept as data in
+tests/golden/fp8_known_answers.json) and an independent brute-force nearest-value search over the e4m3 codes."""
+
+import json
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -7,26 +10,24 @@ import torch
 
 from oracle import fp8
 
+KNOWN = json.loads((Path(__file__).parent / "golden" / "fp8_known_answers.json").read_text())
+
 
 def test_fp32_midpoints_known_answers():
-    # reference tests/test_cache_fp8.py:150-158: 84.021 -> 88 directly (80 through an fp16 step)
-    k = torch.tensor([448., 84.021, -84.021, 1.06251, -1.06251, 1.06249, -1.06249, 0.]).reshape(1, 1, 1, 8)
-    q, scale = fp8.quantize_rows(k)
-    assert float(scale) == 1.0
-    assert q.float().flatten().tolist() == [448., 88., -88., 1.125, -1.125, 1.0, -1.0, 0.]
+    m = KNOWN["midpoint_row"]
+    q, scale = fp8.quantize_rows(torch.tensor(m["values"]).reshape(1, 1, 1, -1))
+    assert float(scale) == m["scale"]
+    assert q.float().flatten().tolist() == m["expected"]
     assert float(torch.tensor(84.021).half().float().to(fp8.FP8).float()) == 80.0  # the fp16 path it avoids
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 def test_boundary_row_known_answers(dtype):
-    # reference tests/test_cache_fp8.py:47-57
-    values = torch.tensor([0., -0., 1e-15, -1e-15, .5, -.5, 1., -1., 3., -3., 448., -448.]).to(dtype)
-    q, scale = fp8.quantize_rows(values.repeat(8).reshape(1, 1, 1, 96))
-    assert float(scale) == 1.0
-    bits = q.view(torch.uint8).flatten()[:12].tolist()
-    # +0, -0, tiny -> signed zero, then exact values
-    assert bits[:4] == [0x00, 0x80, 0x00, 0x80]
-    assert q.float().flatten()[4:12].tolist() == [.5, -.5, 1., -1., 3., -3., 448., -448.]
+    b = KNOWN["boundary_row"]
+    q, scale = fp8.quantize_rows(torch.tensor(b["values"] * b["repeat"]).to(dtype).reshape(1, 1, 1, -1))
+    assert float(scale) == b["scale"]
+    assert q.view(torch.uint8).flatten()[:4].tolist() == b["bits_first4"]  # +0, -0, tiny -> signed zero
+    assert q.float().flatten()[4:12].tolist() == b["values_4_to_12"]
 
 
 def test_torch_conversion_equals_brute_force_nearest():

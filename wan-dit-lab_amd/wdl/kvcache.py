@@ -1,14 +1,19 @@
-"""KVCache of one block on MI355X: the FP8 keys/values of the finished frames in one buffer allocated once, the
+"""KVCache of one block on MI355X: the FP8 keys/values of the finished frames in one device buffer allocated once, the
 hot-path subset of src/wan_dit_lab/generation/causal.py:48-343 (KVCache).
 
-Buffer [1, max_tokens + n, H, D] in e4m3 with fp32 scales per (token, head) ([1, max_tokens + n, H, 1]). The first
-sink_tokens are the sink, never evicted; the rest of max_tokens is the ring. While the ring fills, a chunk is
-written right after the saved tokens and committing it moves a counter; once full, the chunk goes into the last n
-rows and committing copies it over the tokens of the oldest unpinned frames (causal.py:297-337). pin_last keeps
-the last committed chunk (a new shot's first chunk) in the ring until the next pin (causal.py:126-133).
+Device side. One buffer [1, max_tokens + n, H, D] in e4m3 per K and V with fp32 scales per (token, head)
+([1, max_tokens + n, H, 1]). Rows [0, sink_tokens) are the sink, never evicted; rows [sink_tokens, max_tokens) are
+the ring; the last n rows take the chunk once the ring is full. attend() writes the chunk (wdl_kv_append_fp8) at
+row `saved` and attends over rows [0, saved) and the chunk (wdl::sage_kv_attend), the sage + fp8 branch of
+KVCache.attend (causal.py:193-210).
 
-attend writes the chunk (wdl_kv_append_fp8) and attends over the saved tokens and the chunk (wdl::sage_kv_attend:
-cache tokens from FP8, the chunk's own K, V in bf16), as KVCache.attend's sage + fp8 branch (causal.py:193-210).
+Host side. Which ring slot holds which token is bookkeeping on the host (`_FrameQueue`): the ring's frames in the
+order they were committed, each with the slots of its tokens in token order. Attention does not depend on where a
+key sits, only the eviction order does, and the reference defines it as "the oldest unpinned tokens of the video
+first" (causal.py:329-337); walking the queue from its head, skipping pinned slots, yields exactly that order
+without sorting. The slot numbers a commit produces are pinned by the reference's own fixture
+(native/live/tests/fixtures/ring.json, in tests/golden/).
+
 Positions-in-window turns, Echo-Forcing decay, Participative Compression and Forcing-KV head splits are not on
 this hot path and are not implemented here.
 """
@@ -26,13 +31,52 @@ CHUNK = 3
 CONTEXT = 21
 
 
+class _FrameQueue:
+    """The ring's frames, oldest first: entries [frame number, [slot of each remaining token, in token order]].
+    A frame loses tokens from its front when they are evicted; an empty frame leaves the queue."""
+
+    def __init__(self):
+        self.frames: list[list] = []
+        self.pinned: frozenset = frozenset()
+
+    def clear(self):
+        self.frames = []
+        self.pinned = frozenset()
+
+    def append(self, first_frame: int, per_frame: int, tokens: list[int], slots: list[int]):
+        """Chunk tokens `tokens` (indices within the chunk, increasing) now live in `slots`."""
+        for i, s in zip(tokens, slots):
+            f = first_frame + i // per_frame
+            if not self.frames or self.frames[-1][0] != f:
+                self.frames.append([f, []])
+            self.frames[-1][1].append(s)
+
+    def take_oldest(self, n: int) -> list[int]:
+        """Removes and returns the n oldest unpinned slots (in token order of the video)."""
+        out: list[int] = []
+        for entry in self.frames:
+            keep = []
+            for s in entry[1]:
+                if len(out) < n and s not in self.pinned:
+                    out.append(s)
+                else:
+                    keep.append(s)
+            entry[1] = keep
+            if len(out) == n:
+                break
+        self.frames = [e for e in self.frames if e[1]]
+        if len(out) < n:
+            raise RuntimeError(f"the ring has {len(out)} evictable tokens, the chunk needs {n}")
+        return out
+
+
 class KVCache:
     def __init__(self, max_tokens: int, sink_tokens: int = 0, chunk: int = CHUNK, entropy_ratio=None):
         self.max_tokens, self.sink_tokens, self.chunk = max_tokens, sink_tokens, chunk
         self.entropy_ratio = entropy_ratio
         self.fp8 = True
         self.k = self.v = None
-        self.pinned = None
+        self.queue = _FrameQueue()
         self.reset()
 
     def reset(self):
@@ -40,8 +84,7 @@ class KVCache:
         self.saved = 0
         self.frames = 0
         self.last_slots = None
-        if self.pinned is not None:
-            self.pinned.zero_()
+        self.queue.clear()
 
     def full(self) -> bool:
         return self.k is not None and self.saved == self.max_tokens
@@ -62,11 +105,8 @@ class KVCache:
         self.v = torch.zeros_like(self.k)
         self.ks = torch.ones(B, rows, H, 1, device=dev)
         self.vs = torch.ones_like(self.ks)
-        ring = self.max_tokens - self.sink_tokens
-        self.frame_of = torch.zeros(ring, dtype=torch.long, device=dev)
-        self.place_in_frame = torch.zeros_like(self.frame_of)
-        self.pinned = torch.zeros(ring, dtype=torch.bool, device=dev)
         self.last_slots = None
+        self.queue.clear()
 
     def store(self, at: int, K: torch.Tensor, V: torch.Tensor):
         store_kv_fp8(K, V, self.k, self.ks, self.v, self.vs, at)
@@ -82,42 +122,45 @@ class KVCache:
         return attend(Q, self.k, self.ks, self.v, self.vs, at, K, V, sm_scale=self.scale(at + n, Q.shape[-1]))
 
     def commit(self):
-        """Keeps the chunk last written by attend (causal.py:297-327, without turns, decay or compression)."""
-        n, at, per, sink = self.n, self.saved, self.per_frame, self.sink_tokens
-        dev = self.frame_of.device
-        i = torch.arange(n, device=dev)
-        slots = None
+        """Keeps the chunk that attend last wrote at row `saved` (causal.py:297-327, without turns, decay or
+        compression). While the ring has room the chunk stays where it is; once full it moves into the slots of
+        the oldest unpinned tokens. last_slots: the ring slots its tokens took (None when the window is the chunk
+        alone)."""
+        n, at, sink = self.n, self.saved, self.sink_tokens
         if at + n <= self.max_tokens:
-            self.saved += n
-            o = torch.arange(max(at, sink), max(at + n, sink), device=dev)
-            slots, i = o - sink, o - at
+            first = max(at, sink)  # rows of the chunk in the sink stay there; the rest enter the ring in place
+            tokens = list(range(first - at, n))
+            slots = [at + i - sink for i in tokens]
+            self.saved = at + n
         elif self.max_tokens > sink:
-            slots = self.evicted(n)
-            self.copy(sink + slots, at, n)
-        self.last_slots = slots
-        if slots is not None and len(slots):
-            self.frame_of[slots] = self.frames + i // per
-            self.place_in_frame[slots] = i % per
+            tokens = list(range(n))
+            slots = self.queue.take_oldest(n)
+            self._move_rows(at, n, slots)
+        else:
+            tokens = slots = None
+        if slots is not None:
+            self.queue.append(self.frames, self.per_frame, tokens, slots)
+            self.last_slots = torch.tensor(slots, dtype=torch.long)
+        else:
+            self.last_slots = None
         self.frames += self.chunk
 
-    def evicted(self, n: int) -> torch.Tensor:
-        """Ring indices of the n tokens a chunk replaces: the oldest unpinned (causal.py:329-337)."""
-        order = self.frame_of * self.per_frame + self.place_in_frame
-        order = order.masked_fill(self.pinned, torch.iinfo(order.dtype).max)
-        return torch.topk(order, n, largest=False).indices
-
-    def copy(self, to: torch.Tensor, at: int, n: int):
-        """Rows [at, at + n) of the four buffers to rows `to`, as bytes (causal.py:339-343)."""
+    def _move_rows(self, at: int, n: int, slots: list[int]):
+        """Device rows [at, at + n) of the four buffers into the rows of ring slots `slots`, one row per token in
+        order; FP8 rows move as bytes."""
+        dev = self.k.device
+        dst = torch.tensor(slots, dtype=torch.long, device=dev) + self.sink_tokens
         for buf in (self.k, self.v, self.ks, self.vs):
-            raw = buf.view(torch.uint8) if buf.dtype == FP8 else buf
-            raw[:, to] = raw[:, at:at + n].clone()
+            rows = buf[0].view(torch.uint8) if buf.dtype == FP8 else buf[0]
+            rows.index_copy_(0, dst, rows[at:at + n].clone())
 
     def pin_last(self):
-        """The chunk just committed stays in the ring until the next pin (causal.py:126-133)."""
-        self.pinned.zero_()
-        if self.last_slots is not None:
-            assert int(self.last_slots.numel()) < len(self.pinned), "the ring must hold more than the pinned chunk"
-            self.pinned[self.last_slots] = True
+        """The chunk just committed (a new shot's first chunk) stays in the ring until the next pin; the one pinned
+        before becomes evictable (causal.py:126-133)."""
+        pins = [] if self.last_slots is None else self.last_slots.tolist()
+        if len(pins) >= self.max_tokens - self.sink_tokens:
+            raise ValueError("a pinned chunk must leave room in the ring for the next one")
+        self.queue.pinned = frozenset(pins)
 
     def fill_for_benchmark(self, generator=None):
         """A full window of random FP8 keys/values (scales 1/448-ish), as after max_tokens / per_frame committed
@@ -129,8 +172,8 @@ class KVCache:
             buf[:, :rows] = (x * 100).clamp(-448, 448).to(FP8)
             sc[:, :rows] = 0.01
         self.saved = rows
+        self.queue.clear()
         ring = self.max_tokens - self.sink_tokens
-        idx = torch.arange(ring, device=self.frame_of.device)
-        self.frame_of.copy_(self.sink_tokens // self.per_frame + idx // self.per_frame)
-        self.place_in_frame.copy_(idx % self.per_frame)
+        first = self.sink_tokens // self.per_frame
+        self.queue.append(first, self.per_frame, list(range(ring)), list(range(ring)))
         self.frames = rows // self.per_frame

@@ -61,78 +61,115 @@ def pack_layout(parts: dict):
     return layout, offset
 
 
+class _StagedFile:
+    """Writes `target` under a temporary name and publishes it by rename only when the whole body succeeded;
+    on any exception the temporary, and a companion file written inside the body, are removed. The bytes written
+    are hashed as they go."""
+
+    def __init__(self, target: Path, companion: Path):
+        self.target, self.companion = target, companion
+        self.temp = target.with_name(target.name + ".tmp")
+        self.sha = hashlib.sha256()
+        self.written = 0
+
+    def __enter__(self):
+        for p in (self.target, self.companion, self.temp):
+            if p.exists():
+                raise FileExistsError(p)
+        self.fd = os.open(self.temp, os.O_WRONLY | os.O_CREAT | os.O_EXCL, 0o644)
+        return self
+
+    def write(self, data: bytes):
+        self.sha.update(data)
+        view = memoryview(data)
+        while view:
+            view = view[os.write(self.fd, view):]
+        self.written += len(data)
+
+    def __exit__(self, kind, value, tb):
+        try:
+            if kind is None:
+                os.fsync(self.fd)
+        finally:
+            os.close(self.fd)
+        if kind is None:
+            os.replace(self.temp, self.target)
+            return False
+        for p in (self.temp, self.target, self.companion):
+            if p.exists():
+                p.unlink()
+        return False
+
+
+def _row_bytes(parts: dict, layout: list, size: int) -> bytes:
+    """One block's row: every entry's raw bytes at its offset, zero padding between entries."""
+    row = np.zeros(size, dtype=np.uint8)
+    for e, (_, t) in zip(layout, _entries(parts)):
+        raw = t.detach().cpu().contiguous().view(torch.uint8).reshape(-1).numpy()
+        row[e["offset"]:e["offset"] + raw.size] = raw
+    return row.tobytes()
+
+
 def build_pack(blocks: list, path, source: str = "", **metadata) -> dict:
     """Writes the parts dicts of `blocks` (QuantizedWanBlock.p or build_block inputs; any device) as a pack at
-    `path` + its manifest; returns the manifest without the layout."""
+    `path` with its manifest `<path>.json`; returns the manifest without the layout. Refuses an existing pack
+    (FileExistsError) and blocks of differing layouts (ValueError) before writing anything."""
     path = Path(path)
-    manifest, temporary = path.with_suffix(path.suffix + ".json"), path.with_suffix(path.suffix + ".tmp")
-    if any(p.exists() for p in (path, manifest, temporary)):
-        raise FileExistsError(path)
     if not blocks:
         raise ValueError("a pack needs at least one block")
-    layout, size = pack_layout(blocks[0])
-    for b in blocks[1:]:
-        if pack_layout(b) != (layout, size):
-            raise ValueError("packed blocks must share one layout")
-    digest = hashlib.sha256()
-    try:
-        with temporary.open("xb") as stream:
-            for parts in blocks:
-                row = torch.zeros(size, dtype=torch.uint8)
-                for e, (name, t) in zip(layout, _entries(parts)):
-                    row[e["offset"]:e["offset"] + e["bytes"]] = t.detach().contiguous().cpu().reshape(-1).view(
-                        torch.uint8)
-                payload = row.numpy().tobytes()
-                digest.update(payload)
-                stream.write(payload)
-            stream.flush()
-            os.fsync(stream.fileno())
-        os.replace(temporary, path)
-        meta = dict(format=FORMAT, blocks=len(blocks), layout=layout, bytes_per_block=size,
-                    bytes=size * len(blocks), sha256=digest.hexdigest(), source=source, layout_notes=LAYOUT_NOTES,
+    layouts = [pack_layout(b) for b in blocks]
+    if any(lay != layouts[0] for lay in layouts[1:]):
+        raise ValueError("packed blocks must share one layout")
+    layout, size = layouts[0]
+    manifest = path.with_name(path.name + ".json")
+    with _StagedFile(path, manifest) as out:
+        for parts in blocks:
+            out.write(_row_bytes(parts, layout, size))
+        meta = dict(format=FORMAT, blocks=len(blocks), layout=layout, bytes_per_block=size, bytes=out.written,
+                    sha256=out.sha.hexdigest(), source=source, layout_notes=LAYOUT_NOTES,
                     quantization="SVDQuant W4A4: int4 groups of 64, rank-32 low-rank branch in bf16, smoothing; "
                                  "q, k, v of self-attention as one layer, the feed forward as the fused GELU MLP",
                     **metadata)
         manifest.write_text(json.dumps(meta, indent=1), encoding="utf-8")
-        return {k: v for k, v in meta.items() if k != "layout"}
-    except BaseException:
-        temporary.unlink(missing_ok=True)
-        path.unlink(missing_ok=True)
-        manifest.unlink(missing_ok=True)
-        raise
+    return {k: v for k, v in meta.items() if k != "layout"}
 
 
 def read_manifest(path) -> dict:
     path = Path(path)
-    return json.loads(path.with_suffix(path.suffix + ".json").read_text(encoding="utf-8"))
+    return json.loads(path.with_name(path.name + ".json").read_text(encoding="utf-8"))
+
+
+def _file_sha256(path: Path) -> str:
+    sha = hashlib.sha256()
+    with open(path, "rb", buffering=0) as f:
+        block = bytearray(1 << 24)
+        while True:
+            got = f.readinto(block)
+            if not got:
+                return sha.hexdigest()
+            sha.update(memoryview(block)[:got])
 
 
 def mapped_pack(path, source: str | None = None, verify: bool = False):
-    """The pack at `path` mapped read-only: (uint8 [blocks, bytes per block], layout, manifest). Raises ValueError
-    for another format or source, an incomplete file, or (verify) a sha256 mismatch."""
+    """The pack at `path` mapped without reading it: (uint8 [blocks, bytes per block], layout, manifest). The map is
+    copy-on-write, so nothing done to the tensor reaches the file. Raises ValueError for another format or source,
+    a file whose size is not the manifest's, or (verify) a sha256 mismatch."""
     path = Path(path)
     meta = read_manifest(path)
+    problems = []
     if meta.get("format") != FORMAT:
-        raise ValueError(f"weight pack format {meta.get('format')!r} is not {FORMAT}")
+        problems.append(f"format {meta.get('format')!r} is not {FORMAT}")
     if source is not None and meta.get("source") != source:
-        raise ValueError("weight pack was made from another source")
-    size, n = meta["bytes_per_block"], meta["blocks"]
-    if path.stat().st_size != size * n:
-        raise ValueError("weight pack is incomplete")
-    if verify:
-        digest = hashlib.sha256()
-        with path.open("rb") as f:
-            for chunk in iter(lambda: f.read(1 << 24), b""):
-                digest.update(chunk)
-        if digest.hexdigest() != meta["sha256"]:
-            raise ValueError("weight pack sha256 differs from its manifest")
-    data = np.memmap(path, dtype=np.uint8, mode="r")
-    import warnings
-
-    with warnings.catch_warnings():
-        warnings.simplefilter("ignore", UserWarning)  # a read-only map: torch warns that it is not writable
-        rows = torch.from_numpy(data).reshape(n, size)
-    return rows, meta["layout"], meta
+        problems.append(f"made from {meta.get('source')!r}, not {source!r}")
+    rows, size = meta["blocks"], meta["bytes_per_block"]
+    if path.stat().st_size != rows * size:
+        problems.append(f"{path.stat().st_size} bytes on disk, {rows * size} in the manifest (incomplete)")
+    if not problems and verify and _file_sha256(path) != meta["sha256"]:
+        problems.append("sha256 differs from the manifest")
+    if problems:
+        raise ValueError(f"weight pack {path}: " + "; ".join(problems))
+    table = np.memmap(path, dtype=np.uint8, mode="c", shape=(rows, size))
+    return torch.from_numpy(table), meta["layout"], meta
 
 
 def slot(row: torch.Tensor, layout: list, device=None) -> dict:
