@@ -114,9 +114,11 @@ def test_replays_of_a_captured_append(gpu):
     t = Target(1, 12, 2, 128)
     t.write(k, v, 4)  # eager once before capture
     t.check()
+    from wdl.cache_fp8 import store_kv_fp8
+
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        t.write(k, v, 4)
+        store_kv_fp8(k, v, *t.buffers(), 4)
     for _ in range(3):
         k.copy_(torch.randn(k.shape, device="cuda", generator=g))
         v.copy_(torch.randn(v.shape, device="cuda", generator=g))
