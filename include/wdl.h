@@ -60,6 +60,21 @@ int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K, const voi
                      int64_t Mp, const float* mod_shift, const float* mod_scale, const float* ln_w,
                      const float* ln_b, int ln, float eps, void* v_out, float* workspace, wdl_stream_t stream);
 
+/* wdl_act_quant_w4 without the workspace argument, for callers that cannot allocate device memory (code under HIP
+ * graph capture that must not allocate, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. The scratch is a static device array of WDL_ACT_QUANT_STATIC_FLOATS floats (16 MiB) per GPU, held
+ * until the process ends; a shape with wdl_act_quant_workspace_floats(Mp, K) above that is rejected (WDL_EINVAL)
+ * before any launch (Mp <= 4608 at K = 14336, Mp <= 10752 at K = 3072). Nothing is allocated or freed. The first
+ * call on a device looks up that device's copy of the array; the stream must belong to the current device. All
+ * calls on one GPU share its array: calls that overlap in time on one GPU (different streams, or threads) race,
+ * as calls sharing one workspace of wdl_act_quant_w4 do. Outputs are bit-identical to wdl_act_quant_w4's. */
+#define WDL_ACT_QUANT_STATIC_FLOATS ((int64_t)4 << 20)
+int wdl_act_quant_w4_static(const void* x, int64_t ldx, int64_t M, int64_t K, const void* smooth, float qshift,
+                            int unsigned_q, const void* proj_down_t, int64_t rank, void* q, void* ascales,
+                            float* lora, int64_t Mp, const float* mod_shift, const float* mod_scale,
+                            const float* ln_w, const float* ln_b, int ln, float eps, void* v_out,
+                            wdl_stream_t stream);
+
 /* Operand format of the W4A4 GEMM (both sides; R % 128 == 0, K % 64 == 0), R * K * 3/4 bytes:
  * - values: weights w in [-8, 7] as the fp6 e3m2 code of 2w (sign, 3 exponent bits of bias 3, 2 mantissa bits);
  *   activations q in [-8, 15] as the fp6 e2m3 code of q / 2 (bias 1, 3 mantissa bits). Both exact; the matrix

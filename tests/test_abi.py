@@ -25,7 +25,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     for name in declared():
         assert hasattr(lib, name), name
     assert set(declared()) == set(_lib.SIGNATURES)
-    assert lib.wdl_abi_version() == 6
+    assert lib.wdl_abi_version() == 7
     assert lib.wdl_last_error() == b""
 
 
@@ -162,3 +162,12 @@ def test_tile_blocked_layout_offsets():
             hi = byte_at(r, grp, h, bit // 8 + 1) if bit // 8 + 1 < 24 else 0
             assert ((lo | hi << 8) >> (bit % 8)) & 63 == int(codes[r, k]), (r, k)
     assert torch.equal(ops.decode_weights(b), w)
+
+
+def test_static_scratch_size_is_one_value():
+    """WDL_ACT_QUANT_STATIC_FLOATS (the no-workspace quantizer's static array) is stated once in the public header
+    and once for the kernels: both must be the same 4 Mi floats."""
+    public = (ROOT / "include" / "wdl.h").read_text()
+    private = (ROOT / "wan-dit-lab_amd" / "csrc" / "wdl_common.h").read_text()
+    assert "#define WDL_ACT_QUANT_STATIC_FLOATS ((int64_t)4 << 20)" in public
+    assert "#define WDL_ACT_QUANT_STATIC_FLOATS (int64_t(4) << 20)" in private

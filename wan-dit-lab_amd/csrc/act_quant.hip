@@ -23,6 +23,8 @@
 //              hardware fp6 conversion and written with two aligned stores, and the low-rank product runs on the
 //              values in registers (bf16 MFMA), the waves' 32 x 32 partials summed in wave order.
 //   lora_sum   lora = sum of the column-block partials in increasing order (only when K / 64 > S).
+#include <mutex>
+
 #include "wdl_common.h"
 
 namespace {
@@ -318,11 +320,12 @@ extern "C" int64_t wdl_act_quant_workspace_floats(int64_t Mp, int64_t K) {
     return (nb > 1 ? nb * Mp * RANK : 0) + 2 * Mp;
 }
 
-extern "C" int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K, const void* smooth, float qshift,
-                                int unsigned_q, const void* proj_down_t, int64_t rank, void* q, void* ascales,
-                                float* lora, int64_t Mp, const float* mod_shift, const float* mod_scale,
-                                const float* ln_w, const float* ln_b, int ln, float eps, void* v_out,
-                                float* workspace, hipStream_t stream) {
+namespace {
+
+int act_quant_launch(const void* x, int64_t ldx, int64_t M, int64_t K, const void* smooth, float qshift,
+                     int unsigned_q, const void* proj_down_t, int64_t rank, void* q, void* ascales, float* lora,
+                     int64_t Mp, const float* mod_shift, const float* mod_scale, const float* ln_w, const float* ln_b,
+                     int ln, float eps, void* v_out, float* workspace, hipStream_t stream) {
     if (M < 0 || K <= 0 || K % 64 || Mp < M || Mp % BLOCK_ROWS || ldx < K)
         return fail(WDL_EINVAL, "act_quant_w4: bad shape M=%lld K=%lld Mp=%lld ldx=%lld", (long long)M,
                     (long long)K, (long long)Mp, (long long)ldx);
@@ -358,4 +361,68 @@ extern "C" int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K
     const int64_t n = Mp * RANK;
     lora_sum_kernel<<<unsigned((n + 255) / 256), 256, 0, stream>>>(workspace, nb, n, lora);
     return check_launch("act_quant_w4 lora_sum");
+}
+
+// Scratch of wdl_act_quant_w4_static: the quantizer's workspace (column-block partials of the low-rank sums, LN
+// statistics) as a file-scope device array, one copy per GPU for the life of the process. Its device address is
+// taken once per device with that device current (hipGetSymbolAddress) and kept in scratch_ptr; in host code the
+// array's name is not a device address and is never passed to a kernel. Every kernel writes the parts of it that
+// a later kernel of the same call reads before that kernel runs (the partials of every column block and row, the
+// statistics of every row < M), so nothing needs clearing between calls.
+static __device__ __align__(256) float scratch[WDL_ACT_QUANT_STATIC_FLOATS];
+
+constexpr int MAX_DEVICES = 64;
+float* scratch_ptr[MAX_DEVICES] = {};
+std::mutex scratch_lock;
+
+int static_scratch(hipStream_t stream, float** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES)
+        return fail(WDL_EHIP, "act_quant_w4_static: no current device");
+    if (stream) {
+        hipDevice_t sdev = -1;
+        if (hipStreamGetDevice(stream, &sdev) != hipSuccess || sdev != dev)
+            return fail(WDL_EINVAL, "act_quant_w4_static: the stream belongs to device %d, the current device is %d",
+                        int(sdev), dev);
+    }
+    std::lock_guard<std::mutex> hold(scratch_lock);
+    if (!scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(WDL_EHIP, "act_quant_w4_static: hipGetSymbolAddress: %s", hipGetErrorString(e));
+        scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *out = scratch_ptr[dev];
+    return WDL_OK;
+}
+
+}  // namespace
+
+extern "C" int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K, const void* smooth, float qshift,
+                                int unsigned_q, const void* proj_down_t, int64_t rank, void* q, void* ascales,
+                                float* lora, int64_t Mp, const float* mod_shift, const float* mod_scale,
+                                const float* ln_w, const float* ln_b, int ln, float eps, void* v_out,
+                                float* workspace, hipStream_t stream) {
+    return act_quant_launch(x, ldx, M, K, smooth, qshift, unsigned_q, proj_down_t, rank, q, ascales, lora, Mp,
+                            mod_shift, mod_scale, ln_w, ln_b, ln, eps, v_out, workspace, stream);
+}
+
+extern "C" int wdl_act_quant_w4_static(const void* x, int64_t ldx, int64_t M, int64_t K, const void* smooth,
+                                       float qshift, int unsigned_q, const void* proj_down_t, int64_t rank, void* q,
+                                       void* ascales, float* lora, int64_t Mp, const float* mod_shift,
+                                       const float* mod_scale, const float* ln_w, const float* ln_b, int ln,
+                                       float eps, void* v_out, hipStream_t stream) {
+    if (Mp < 0 || K <= 0 || K % 64)
+        return fail(WDL_EINVAL, "act_quant_w4_static: bad shape K=%lld Mp=%lld", (long long)K, (long long)Mp);
+    const int64_t need = wdl_act_quant_workspace_floats(Mp, K);
+    if (need > WDL_ACT_QUANT_STATIC_FLOATS)
+        return fail(WDL_EINVAL, "act_quant_w4_static: Mp=%lld K=%lld needs %lld scratch floats, above the static "
+                                "maximum of %lld (use wdl_act_quant_w4 with a workspace)", (long long)Mp,
+                    (long long)K, (long long)need, (long long)WDL_ACT_QUANT_STATIC_FLOATS);
+    float* ws = nullptr;
+    const int rc = static_scratch(stream, &ws);
+    if (rc) return rc;
+    return act_quant_launch(x, ldx, M, K, smooth, qshift, unsigned_q, proj_down_t, rank, q, ascales, lora, Mp,
+                            mod_shift, mod_scale, ln_w, ln_b, ln, eps, v_out, ws, stream);
 }

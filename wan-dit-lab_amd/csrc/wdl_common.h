@@ -15,6 +15,10 @@
 #define WDL_EINVAL 1
 #define WDL_EHIP 2
 
+// floats of the static scratch array of wdl_act_quant_w4_static (16 MiB per GPU); the same value as in
+// include/wdl.h
+#define WDL_ACT_QUANT_STATIC_FLOATS (int64_t(4) << 20)
+
 // element types of strided inputs
 #define WDL_F32 0
 #define WDL_F16 1
