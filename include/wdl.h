@@ -110,6 +110,26 @@ int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wcodes, const
                   const void* proj_up, const void* bias, int64_t M, int64_t Mp, int64_t N, int64_t K, int64_t rank,
                   void* out, int64_t ldo, int epilogue, const float* gate, void* workspace, wdl_stream_t stream);
 
+/* Workspace (in floats) of wdl_w4a4_gemm_gelu_quant for Mp tokens and a hidden layer of N features. */
+int64_t wdl_w4a4_gemm_gelu_quant_workspace_floats(int64_t Mp, int64_t N);
+
+/* The first GEMM of the fused W4A4 GELU MLP with the second layer's input quantization in its epilogue. Replaces
+ * the first gemm_w4a4 call of live::w4a4_gelu_mlp (native/ops/w4a4_ops.cpp:42-57; Nunchaku's fused_gelu_mlp as
+ * quantization/w4a4.py:198-204 describes it: the hidden layer never goes to memory in 16 bits).
+ * y as wdl_w4a4_gemm computes it (qa, ascales, wcodes, wscales, lora, proj_up, bias; N = the hidden width), then
+ * per token m < M: h = GELU_tanh(y) in fp32; u = (h + 0.171875) / smooth2 (IEEE fp32 quotient); per 64-feature
+ * group scale = bf16(max|u| / 15), q = clamp(rint(u / scale), 0, 15). Outputs, the inputs of the second layer's
+ * wdl_w4a4_gemm: q2 the fp6 codes of q in the operand format [Mp, N], ascales2 bf16 [N/64, Mp], lora2 fp32
+ * [Mp, 32] = h . proj_down2 (rows >= M: zero codes, scales and sums). smooth2 bf16 [N]; proj_down2_t bf16 [32, N].
+ * The low-rank sum is formed per 128-feature tile (h split exactly into two bf16 parts for the matrix cores) and
+ * the tiles are added in increasing order by a second launch: deterministic. workspace: fp32,
+ * wdl_w4a4_gemm_gelu_quant_workspace_floats(Mp, N). Mp % 128 == 0, N % 128 == 0, K % 64 == 0; codes, lora,
+ * lora2, proj_up and workspace 16-byte aligned, bias, smooth2 and proj_down2_t 8-byte, scales 4-byte. */
+int wdl_w4a4_gemm_gelu_quant(const void* qa, const void* ascales, const void* wcodes, const void* wscales,
+                             const float* lora, const void* proj_up, const void* bias, int64_t M, int64_t Mp,
+                             int64_t N, int64_t K, int64_t rank, const void* smooth2, const void* proj_down2_t,
+                             void* q2, void* ascales2, float* lora2, float* workspace, wdl_stream_t stream);
+
 /* Workspace (in floats) of wdl_fp8_quantize in per-tensor mode for an [M, K] operand. */
 int64_t wdl_fp8_quantize_workspace_floats(int64_t M, int64_t K);
 

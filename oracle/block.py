@@ -8,8 +8,10 @@
   cache[at:at+n] = quantize_rows(K), quantize_rows(V);  A = Sage(Q; cache[:at] ++ (K, V))   (causal.py:193-210)
   X   = bf16(X + bf16(W4A4(A)) * gate_a)                                                     (block.py:25-26)
   Xc  = bf16(LN3_affine(X));  Qc = RMSNorm(W4A4(Xc));  X = bf16(X + bf16(W4A4(Sage(Qc; Kc, Vc))))  (block.py:27)
-  h   = bf16(GELU(W4A4(bf16(LN(X) * (1 + scale_f) + shift_f))));  X = bf16(X + bf16(W4A4_u(h)) * gate_f) (28)
-with W4A4_u the second GELU-MLP layer (unsigned (h + 0.171875) / s2). The attention is the blockwise online
+  h   = GELU(W4A4(bf16(LN(X) * (1 + scale_f) + shift_f))) in fp32;  X = bf16(X + bf16(W4A4_u(h)) * gate_f)  (28)
+with W4A4_u the second GELU-MLP layer: its INT4 branch quantizes (h + 0.171875) / s2 unsigned and its low-rank
+branch reads h itself, the hidden layer never rounded to 16 bits (the fused GELU MLP, w4a4.py:198-204,
+w4a4_ops.cpp:42-63; w4a4.gelu_mlp of this oracle). The attention is the blockwise online
 softmax of the kernel (sage.attention_online). The reference applies the modulation in bf16 op by op and adds
 the residual in bf16 after a bf16 product; the bar against it is the tolerance of tests/test_w4a4.py:62-87.
 """
@@ -80,8 +82,7 @@ def block_forward(X: torch.Tensor, time_in: torch.Tensor, P: dict, grid, freq: t
     yc = _lin(Ac, P["co"]).to(BF)
     X = (X.float() + yc.float()).to(BF)
     x2 = onorms.ln_mod(X, sh_f, sc_f, eps=eps)
-    h = ow.gelu_tanh(_lin(x2, P["ffn1"])).to(BF)
-    y2 = _lin(h, P["ffn2"], ow.GELU_SHIFT, True).to(BF)
+    y2 = ow.gelu_mlp(x2, P["ffn1"], P["ffn2"])  # the hidden layer in fp32 (w4a4.py:198-204)
     return (X.float() + y2.float() * g_f).to(BF)
 
 

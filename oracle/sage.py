@@ -168,13 +168,6 @@ def attention_exact(Q, Kf, Vf, sm_scale=None) -> torch.Tensor:
     return torch.einsum("bhnl,blhd->bnhd", torch.softmax(S, -1), Vf.double()).float()
 
 
-def attend(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, sm_scale=None):
-    """sage_kv.attend (sage_kv.py:127-134) emulated: fp32 [B, n, H, D]."""
-    D = Q.shape[-1]
-    p = prep(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V)
-    return attention_quantized(p, D ** -0.5 if sm_scale is None else sm_scale)
-
-
 def cosine(a: torch.Tensor, b: torch.Tensor) -> float:
     a, b = a.double().flatten(), b.double().flatten()
     return float((a @ b) / (a.norm() * b.norm()))

@@ -5,7 +5,8 @@ Bars:
 - config 1 (dim 3072): max-rel-err 1e-2, and relative L2 within 1.5x of the oracle's own change under 50 one-ulp
   changes of its bf16 input (a random-weight W4A4 block without smoothing is chaotic at that level: one
   activation-int4 flip moves a whole quantization step; measured in the test);
-- stage by stage at config 1, each HIP stage fed the oracle's own input: 1e-4 relative L2 (linears), 2e-3 with
+- stage by stage at config 1, each HIP stage fed the oracle's own input: 1e-4 relative L2 (linears), 1e-3 (the
+  fused GELU MLP, whose fp32 hidden layer meets GELU's last-bit differences before its int4 rounding), 2e-3 with
   cosine >= 0.99999 (attention);
 - the reference's own contract (tests/test_w4a4.py:62-87): the W4A4 block's update against the float block's,
   within 5 % of the oracle's own error there and below 0.21 (the reference's 0.2 was stated for exact SDPA; the
@@ -178,8 +179,16 @@ def test_config1_stages_given_identical_inputs(gpu):
     xc = onorms.ln_mod(X, None, None, P["n3w"], P["n3b"])
     assert rel(gpu_lin(xc, "cq"), oblock._lin(xc, P["cq"]).to(BF)) <= 1e-4
     assert rel(gpu_lin(C, "ck"), oblock._lin(C, P["ck"]).to(BF)) <= 1e-4
+    # the fused GELU MLP: the oracle's hidden layer is fp32 (w4a4.py:198-204); the kernel's GELU differs from
+    # torch's in the last bits, so a few int4 values of the hidden layer land one step apart (the epilogue test
+    # bounds them): relative L2 1e-3 here
     x2 = onorms.ln_mod(X, e[3], e[4])
-    h = ow.gelu_tanh(oblock._lin(x2, P["ffn1"])).to(BF)
-    assert rel(gpu_lin(x2, "ffn1", epi=3), h) <= 1e-4
-    y2 = oblock._lin(h, P["ffn2"], ow.GELU_SHIFT, True).to(BF)
-    assert rel(gpu_lin(h, "ffn2", ow.GELU_SHIFT, True), y2) <= 1e-4
+    y2 = ow.gelu_mlp(x2, P["ffn1"], P["ffn2"])
+    t1, t2 = blk.p["ffn1"], blk.p["ffn2"]
+    qa = ops.act_quant_launch(x2.to(dev).contiguous(), t1["smooth"], t1["proj_down"])
+    hq = ops.gelu_quant_launch(*qa, t1["wcodes"], t1["wscales"], t1["proj_up"], t1["bias"], M, t2["smooth"],
+                               t2["proj_down"])
+    out = torch.empty(M, dim, device=dev, dtype=BF)
+    ops.gemm_launch(*hq, t2["wcodes"], t2["wscales"], t2["proj_up"], t2["bias"], M, out)
+    print(f"fused MLP stage: rel-L2 {rel(out.cpu(), y2):.2e}")
+    assert rel(out.cpu(), y2) <= 1e-3

@@ -132,3 +132,57 @@ def test_ln_mod_and_rms_close_to_torch():
     r = onorms.rms_norm(x, w).float()
     rref = x.float() * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + 1e-6) * w.float()
     assert float((r - rref).abs().max()) <= 2 ** -7 * float(rref.abs().max())
+
+
+def _mlp_case():
+    """The reference's fused-MLP contract case (tests/test_w4a4.py:32-45): M not a multiple of the padding, a few
+    outlier channels, float weights of the two layers."""
+    g = torch.Generator().manual_seed(0)
+    M, K, H, N = 300, 256, 1024, 256
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    x[:, :4] *= 10
+    W1, b1 = torch.randn(H, K, generator=g) * 0.08, torch.randn(H, generator=g) * 0.1
+    W2, b2 = torch.randn(N, H, generator=g) * 0.05, torch.randn(N, generator=g) * 0.1
+    h = ow.gelu_tanh(x.float() @ W1.t() + b1)
+    return x, W1, b1, W2, b2, h, h @ W2.t() + b2
+
+
+def test_gelu_mlp_meets_the_reference_contract():
+    """The oracle's fused GELU MLP (fp32 hidden layer quantized unsigned after the shift, shift-corrected bias)
+    against the float feed forward, as the reference's own test states it (tests/test_w4a4.py:32-59): error below
+    0.2 and below the layer-by-layer pair (whose hidden layer is bf16 and signed); the shift without its bias
+    correction leaves an offset, the corrected one does not."""
+    x, W1, b1, W2, b2, h, ref = _mlp_case()
+    err = lambda y: float((y.float() - ref).norm() / ref.norm())
+    offset = lambda y: float((y.float() - ref).mean(0).norm() / ref.mean(0).norm())
+    t1 = ow.quantize_weight(W1, b1, smooth=ow.smoothing(x.float().abs().amax(0), W1))
+    s2 = ow.smoothing(h.abs().amax(0) + ow.GELU_SHIFT, W2)
+    plain = ow.quantize_weight(W2, b2, smooth=s2)
+    lin = lambda v, t: ow.linear_parts(v, t)[0].to(torch.bfloat16)
+    unfused = lin(ow.gelu_tanh(lin(x, t1).float()).to(torch.bfloat16), plain)
+    fused = ow.gelu_mlp(x, t1, ow.quantize_weight(W2, b2, smooth=s2, shift=ow.GELU_SHIFT))
+    uncorrected = ow.gelu_mlp(x, t1, plain)
+    assert err(fused) < 0.2 and err(fused) < err(unfused)
+    assert offset(fused) < 1.1 * offset(unfused) and offset(uncorrected) > 1.5 * offset(fused)
+
+
+def test_gelu_mlp_hidden_layer_is_fp32_and_quantized_unsigned_after_the_shift():
+    """The second layer's inputs inside gelu_mlp come from the fp32 hidden layer: its codes are the nearest points
+    of [0, 15] to (h + 0.171875) / s2 / scale with scale = bf16(max / 15) from the fp32 quotients (brute force in
+    float64), and its low-rank input is h . proj_down2 of the unrounded h; rounding h to bf16 first (what a bf16
+    hidden buffer would do) changes the codes."""
+    x, W1, b1, W2, b2, h, ref = _mlp_case()
+    t1 = ow.quantize_weight(W1, b1)
+    t2 = ow.quantize_weight(W2, b2, smooth=ow.smoothing(h.abs().amax(0) + ow.GELU_SHIFT, W2), shift=ow.GELU_SHIFT)
+    hid = ow.gelu_tanh(ow.linear_parts(x, t1)[0].float())
+    y, q, sc, la = ow.linear_parts(hid, t2, ow.GELU_SHIFT, True)
+    u32 = (hid + torch.tensor(ow.GELU_SHIFT)) / t2["smooth"].float()
+    assert torch.equal(sc, (u32.view(300, -1, 64).abs().amax(-1) / torch.tensor(15.0)).to(torch.bfloat16))
+    u = (u32.double().view(300, -1, 64) / sc.double()[..., None]).view(300, -1)
+    grid = torch.arange(0, 16, dtype=torch.float64)
+    best = (u[..., None] - grid).abs().min(-1).values
+    assert torch.all((u - q.double()).abs() <= best + 1e-12) and q.min() >= 0 and q.max() <= 15
+    assert torch.allclose(la.double(), hid.double() @ t2["proj_down"].double(), rtol=0, atol=1e-6)
+    q16, _ = ow.act_quant(hid.to(torch.bfloat16), t2["smooth"], ow.GELU_SHIFT, True)
+    assert not torch.equal(q16, q)
+    assert torch.equal(ow.gelu_mlp(x, t1, t2), y.to(torch.bfloat16))

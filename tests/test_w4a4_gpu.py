@@ -290,3 +290,70 @@ def test_live_names_module_and_bare_op_agree(gpu):
     b = w4a4.PackedW4A4Linear(**t)(x)
     c = w4a4.linear(x, t)
     assert torch.equal(a, b) and torch.equal(a, c)
+
+
+@pytest.mark.parametrize("M,K,N", [(300, 256, 1024), (1392, 3072, 14336)])
+def test_fused_gelu_quant_epilogue_on_the_kernels_own_sums(gpu, M, K, N):
+    """The fused GELU MLP's first GEMM (wdl_w4a4_gemm_gelu_quant) against the oracle's second-layer inputs computed
+    from the same GEMM's fp32 result y (the plain launch with an fp32 output, identical sums): h = GELU_tanh(y) in
+    fp32, u = (h + 0.171875) / s2, unsigned int4 per 64-group, lora2 = h . proj_down2. The kernel's GELU and
+    torch's differ in the last bits (an exp-based tanh against tanhf), so a value on a rounding boundary may land
+    one step apart: bar — scales bit-equal except at most 0.1 % of groups (those one bf16 ulp apart), codes equal
+    where the scales are except at most 0.01 % of values (those one step apart); lora2 within 1e-5 relative L2 (h
+    split into two bf16 parts: ~16 significant bits); padding rows zero. At 1392 x 3072 -> 14336 this is the
+    step's FFN-up shape."""
+    from wdl import ops
+
+    g = torch.Generator().manual_seed(N + M)
+    x, _ = data(M, K, seed=M)
+    from oracle.block import random_logical
+
+    t1 = random_logical(N, K, g)
+    s2 = (torch.rand(N, generator=g) + 0.5).to(torch.bfloat16)
+    pd2 = (torch.randn(N, 32, generator=g) / N ** 0.5).to(torch.bfloat16)
+    from wdl import w4a4
+
+    p1 = w4a4.pack_parts(t1, "cuda")
+    wcodes = ops.weight_codes(p1["qweight"])
+    qa = ops.act_quant_launch(x.cuda(), p1["smooth"], p1["proj_down"])
+    y = torch.empty(M, N, device="cuda", dtype=torch.float32)
+    ops.gemm_launch(*qa, wcodes, p1["wscales"], p1["proj_up"], p1["bias"], M, y, ops.EPI_F32, stream_k=False)
+    q2, asc2, lora2 = ops.gelu_quant_launch(*qa, wcodes, p1["wscales"], p1["proj_up"], p1["bias"], M, s2.cuda(),
+                                            pd2.t().contiguous().cuda())
+    torch.cuda.synchronize()
+    h = ow.gelu_tanh(y.cpu())
+    rq, rs = ow.act_quant(h, s2, ow.GELU_SHIFT, True)
+    rl = ow.lora_down(h, pd2)
+    Mp = asc2.shape[1]
+    q = codes_to_int(q2)
+    sc = asc2.cpu().t()
+    assert torch.all(q[M:] == 0) and torch.all(sc[M:].float() == 0) and torch.all(lora2.cpu()[M:] == 0)
+    sb, rb = sc[:M].contiguous().view(torch.int16).int(), rs.view(torch.int16).int()
+    scale_diff = (sb != rb)
+    assert int((sb - rb).abs().max()) <= 1
+    assert float(scale_diff.float().mean()) <= 1e-3
+    same = ~scale_diff.repeat_interleave(64, dim=1)
+    dq = (q[:M] - rq)[same]
+    print(f"M={M} N={N}: scales differing {int(scale_diff.sum())} of {scale_diff.numel()}, codes differing "
+          f"{int((dq != 0).sum())} of {dq.numel()}")
+    assert int(dq.abs().max()) <= 1 and float((dq != 0).float().mean()) <= 1e-4
+    assert float((lora2.cpu()[:M] - rl).norm() / rl.norm()) <= 1e-5
+
+
+def test_fused_gelu_mlp_matches_oracle_at_the_block_shapes(gpu):
+    """wdl::w4a4_gelu_mlp (fused epilogue, then the second GEMM) against the oracle's gelu_mlp (fp32 hidden layer)
+    at 464 tokens, 3072 -> 14336 -> 3072, random-init parts with the shift-corrected second-layer bias: bar —
+    max-rel-err 1e-2 and relative L2 1e-3 (the GELU last-bit differences of the epilogue test, propagated)."""
+    from wdl import w4a4
+
+    g = torch.Generator().manual_seed(31)
+    x, _ = data(464, 3072, seed=31)
+    from oracle.block import random_logical
+
+    t1, t2 = random_logical(14336, 3072, g), random_logical(3072, 14336, g, shift=ow.GELU_SHIFT)
+    ref = ow.gelu_mlp(x, t1, t2)
+    y = w4a4.gelu_mlp(x.cuda(), w4a4.pack_parts(t1, "cuda"), w4a4.pack_parts(t2, "cuda")).cpu()
+    err = float((y.float() - ref.float()).abs().max()) / float(ref.float().abs().max())
+    rel = float((y.float() - ref.float()).norm() / ref.float().norm())
+    print(f"fused GELU MLP vs oracle: max-rel-err {err:.2e}, rel-L2 {rel:.2e}")
+    assert err <= 1e-2 and rel <= 1e-3

@@ -315,6 +315,15 @@ __global__ void lora_sum_kernel(const float* part, int nb, int64_t n, float* out
 
 }  // namespace
 
+namespace wdl {
+
+int lora_sum(const float* part, int nb, int64_t n, float* out, hipStream_t stream) {
+    lora_sum_kernel<<<unsigned((n + 255) / 256), 256, 0, stream>>>(part, nb, n, out);
+    return check_launch("lora_sum");
+}
+
+}  // namespace wdl
+
 extern "C" int64_t wdl_act_quant_workspace_floats(int64_t Mp, int64_t K) {
     const int64_t S = groups_per_block(K), nb = (K / 64 + S - 1) / S;
     return (nb > 1 ? nb * Mp * RANK : 0) + 2 * Mp;
@@ -358,9 +367,7 @@ int act_quant_launch(const void* x, int64_t ldx, int64_t M, int64_t K, const voi
     }
     int rc = check_launch("act_quant_w4 quant");
     if (rc || !proj_down_t || nb == 1) return rc;
-    const int64_t n = Mp * RANK;
-    lora_sum_kernel<<<unsigned((n + 255) / 256), 256, 0, stream>>>(workspace, nb, n, lora);
-    return check_launch("act_quant_w4 lora_sum");
+    return lora_sum(workspace, nb, Mp * RANK, lora, stream);
 }
 
 // Scratch of wdl_act_quant_w4_static: the quantizer's workspace (column-block partials of the low-rank sums, LN

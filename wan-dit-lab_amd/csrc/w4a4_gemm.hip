@@ -31,8 +31,13 @@ typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned u32x6 __attribute__((ext_vector_type(6)));
 
-enum Epilogue { EPI_BF16 = 0, EPI_F32 = 1, EPI_RESIDUAL = 2, EPI_GELU = 3, EPI_FP8_ROWS = 4, EPI_FP8_TENSOR = 5 };
+enum Epilogue {
+    EPI_BF16 = 0, EPI_F32 = 1, EPI_RESIDUAL = 2, EPI_GELU = 3, EPI_FP8_ROWS = 4, EPI_FP8_TENSOR = 5,
+    EPI_GELU_QUANT = 6  // the fused GELU MLP's first layer: codes, scales and low-rank partials of the second's input
+};
+constexpr float GELU_SHIFT = 0.171875f;  // quantization/w4a4.py:195: GELU(x) > -0.17, so GELU(x) + shift >= 0
 
 // GELU, tanh form: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), tanh(u) = 1 - 2 / (exp(2u) + 1)
 __device__ __forceinline__ float gelu_tanh(float x) {
@@ -56,6 +61,12 @@ struct GemmArgs {
     const float* xs;          // FP8 linears: activation scales fp32 [Mp] (rows) or [1] (tensor)
     const float* wsf;         // FP8 linears: weight scales fp32 [N] (rows) or [1] (tensor)
     float* part;              // stream-K partial sums (workspace), or null
+    // EPI_GELU_QUANT: the second layer's input (the hidden layer, N = its width)
+    uint8_t* q2;              // fp6 e2m3 codes of the unsigned int4 values, tile-blocked [Mp/128][N/64][128][48]
+    uint16_t* as2;            // bf16 [N/64, Mp]
+    const uint16_t* sm2;      // smooth2, bf16 [N]
+    const uint16_t* pd2t;     // proj_down2^T, bf16 [32, N]
+    float* lpart;             // low-rank partials fp32 [N/128][Mp][32]
 };
 
 // Tile BN (features) x BM (tokens), NW waves in a (BN / WN) x (BM / WM) grid. Every operand byte streams from
@@ -332,6 +343,198 @@ __device__ __forceinline__ void finish_tile_rows(const GemmArgs& p, f32x16 (&acc
     }
 }
 
+// Epilogue of the fused GELU MLP's first GEMM (Nunchaku's fused_gelu_mlp, as live::w4a4_gelu_mlp runs it:
+// native/ops/w4a4_ops.cpp:42-63; quantization/w4a4.py:195-204), for a wave's 64 x 64 subtile of a 128 x 128 tile:
+//   y  = the group sums + bf16(lora[m]) . pu[n] + bias[n]        (as the plain epilogue)
+//   h  = GELU_tanh(y) in fp32 (never stored)
+//   u  = (h + 0.171875) / smooth2[n] (IEEE quotient); per token and 64-feature group: scale = bf16(max|u| / 15),
+//        q = clamp(rint(u / scale), 0, 15) -> the second GEMM's activation codes and scales;
+//   lora2 partial = h . proj_down2 over the tile's 128 features, into lpart[tile][m] (a second launch adds the
+//        tiles in order).
+// The wave's 64 features are one 64-group, so lane (token, half) holds 32 of the group's features (rows
+// 32 ti + 8 q + 4 half + e) and the group maximum is one exchange with lane ^ 32. One v_permlane32_swap per value
+// pair then gives each lane the 32 features of its own half of the group in order (positions 8 q + e from the
+// first result, 8 q + 4 + e from the second), which one hardware fp6 conversion packs. The low-rank product uses
+// h split exactly into bf16 hi + lo parts (two MFMAs per 16 features, about 16 significant bits of h) with the
+// k-slots of both operands mapped to the features the lane already holds. Rows m >= M get zero codes, scales and
+// partials.
+// element e (0..3) of four packed bf16 values, as fp32
+__device__ __forceinline__ float smooth_at(uint2 v, int e) {
+    return bf16_to_f32(uint16_t(e < 2 ? (e ? v.x >> 16 : v.x) : (e == 3 ? v.y >> 16 : v.y)));
+}
+
+template <int TN, int TM>
+__device__ __forceinline__ void finish_tile_gelu_quant(const GemmArgs& p, f32x16 (&acc)[TN][TM], int64_t nb0,
+                                                       int64_t mb0, int wn, int wm, int lane, float* xch) {
+    static_assert(TN == 2 && TM == 2, "64 x 64 per wave: one 64-feature group");
+    const int half = lane / 32, tok = lane % 32;
+    const int64_t N = p.N;
+    // ---- loads: this layer's low-rank operands and bias, smooth2 and proj_down2^T for the lane's features
+    bf16x8 pa[TN][2];
+    float4 lr[TM][2][2];
+    if (p.lora) {
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                pa[i][h] = *reinterpret_cast<const bf16x8*>(p.pu + (nb0 + i * 32 + tok) * 32 + h * 16 + 8 * half);
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float* l = p.lora + (mb0 + j * 32 + tok) * 32 + h * 16 + 8 * half;
+                lr[j][h][0] = *reinterpret_cast<const float4*>(l);
+                lr[j][h][1] = *reinterpret_cast<const float4*>(l + 4);
+            }
+    }
+    uint2 bias[TN][4], smv[TN][4];
+    uint2 pdv[TN][2][2];  // proj_down2^T row tok: features 32 ti + 16 qp + 8 part + 4 half .. + 3
+#pragma unroll
+    for (int i = 0; i < TN; ++i) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int64_t nb = nb0 + i * 32 + 8 * q + 4 * half;
+            bias[i][q] = p.bias ? *reinterpret_cast<const uint2*>(p.bias + nb) : make_uint2(0u, 0u);
+            smv[i][q] = *reinterpret_cast<const uint2*>(p.sm2 + nb);
+        }
+#pragma unroll
+        for (int qp = 0; qp < 2; ++qp)
+#pragma unroll
+            for (int part = 0; part < 2; ++part)
+                pdv[i][qp][part] = *reinterpret_cast<const uint2*>(p.pd2t + int64_t(tok) * N + nb0 + i * 32 + 16 * qp +
+                                                                  8 * part + 4 * half);
+    }
+
+    // ---- this layer's low-rank term, then h = GELU(y + bias) in place
+    if (p.lora) {
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                bf16x8 lb;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    lb[e] = __builtin_bit_cast(__bf16, f32_to_bf16(lr[j][h][0][e]));
+                    lb[4 + e] = __builtin_bit_cast(__bf16, f32_to_bf16(lr[j][h][1][e]));
+                }
+#pragma unroll
+                for (int i = 0; i < TN; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[i][h], lb, acc[i][j], 0, 0, 0);
+            }
+    }
+    float rsm[TN][16];  // IEEE reciprocals of smooth2 at the lane's features
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint16_t bv[4] = {uint16_t(bias[i][q].x), uint16_t(bias[i][q].x >> 16), uint16_t(bias[i][q].y),
+                                    uint16_t(bias[i][q].y >> 16)};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                rsm[i][4 * q + e] = 1.0f / smooth_at(smv[i][q], e);
+#pragma unroll
+                for (int j = 0; j < TM; ++j) {
+                    float y = acc[i][j][4 * q + e];
+                    if (p.bias) y = y + bf16_to_f32(bv[e]);
+                    acc[i][j][4 * q + e] = gelu_tanh(y);
+                }
+            }
+        }
+
+    const int64_t g = nb0 / 64;  // the group of the second layer's input
+    float* mine = xch + (wm * 2 + wn) * TM * 16 * 64;  // this wave's low-rank partials, lane-linear
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+        const int64_t m = mb0 + j * 32 + tok;
+        const bool live = m < p.M;
+        // ---- second layer's low-rank down projection: la[r][m] = sum over the 64 features of pd2[n][r] h[m][n]
+        f32x16 la = {};
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int qp = 0; qp < 2; ++qp) {
+                bf16x8 hi, lo;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const float v = acc[i][j][4 * (2 * qp + t / 4) + t % 4];
+                    const uint16_t b = f32_to_bf16(v);
+                    hi[t] = __builtin_bit_cast(__bf16, b);
+                    lo[t] = __builtin_bit_cast(__bf16, f32_to_bf16(v - bf16_to_f32(b)));
+                }
+                const bf16x8 a = __builtin_bit_cast(bf16x8, make_uint4(pdv[i][qp][0].x, pdv[i][qp][0].y,
+                                                                        pdv[i][qp][1].x, pdv[i][qp][1].y));
+                la = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, hi, la, 0, 0, 0);
+                la = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, lo, la, 0, 0, 0);
+            }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mine[(j * 16 + i) * 64 + lane] = live ? la[i] : 0.0f;
+
+        // ---- unsigned int4 quantization of (h + shift) / smooth2 over the token's 64-feature group
+        float u[TN][16];
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                u[i][k] = div_rn(acc[i][j][k] + GELU_SHIFT, smooth_at(smv[i][k / 4], k % 4), rsm[i][k]);
+                amax = fmaxf(amax, fabsf(u[i][k]));
+            }
+        amax = fmaxf(amax, __shfl_xor(amax, 32));  // the group's other 32 features
+        const uint16_t sb = f32_to_bf16(amax / 15.0f);
+        const float sc = bf16_to_f32(sb);
+        const float rsc = sc > 0.0f ? 1.0f / sc : 0.0f;
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {  // u becomes q / 2 (an fp6 e2m3 value) of feature 32 i + 8 (k / 4) + 4 half + k % 4
+                const float rq = sc > 0.0f ? __builtin_rintf(div_rn(u[i][k], sc, rsc)) : 0.0f;
+                u[i][k] = live ? fminf(fmaxf(rq, 0.0f), 15.0f) * 0.5f : 0.0f;
+            }
+        // lanes l and l + 32 trade: afterwards the first result holds feature 32 half + 8 q + e of the group and
+        // the second 32 half + 8 q + 4 + e (the swap exchanges the upper 32 lanes of its first operand with the
+        // lower 32 lanes of its second)
+        f32x16 ea, eb;  // even / odd positions of the lane's half (the conversion interleaves its operands)
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(u[0][k]), __float_as_uint(u[1][k]), false,
+                                                            false);
+            const int q = k / 4, e = k % 4;
+            const int p0 = 8 * q + e, p1 = 8 * q + 4 + e;
+            if (p0 % 2 == 0) ea[p0 / 2] = __uint_as_float(r[0]);
+            else eb[p0 / 2] = __uint_as_float(r[0]);
+            if (p1 % 2 == 0) ea[p1 / 2] = __uint_as_float(r[1]);
+            else eb[p1 / 2] = __uint_as_float(r[1]);
+        }
+        u32x6 w;
+        asm volatile("v_cvt_scalef32_2xpk16_fp6_f32 %0, %1, %2, 1.0" : "=&v"(w) : "v"(ea), "v"(eb));
+        uint8_t* dst = p.q2 + blocked6_offset(m, g, N);
+        *reinterpret_cast<uint4*>(dst + 16 * half) = make_uint4(w[0], w[1], w[2], w[3]);
+        *reinterpret_cast<uint2*>(dst + 32 + 8 * half) = make_uint2(w[4], w[5]);
+        if (half == 0) p.as2[g * p.Mp + m] = live ? sb : uint16_t(0);
+    }
+
+    // ---- the tile's two 64-feature halves (waves wn = 0, 1 of a token row) added in that order
+    __syncthreads();
+    if (wn == 0) {
+        const float* other = xch + (wm * 2 + 1) * TM * 16 * 64;
+        const int64_t tile = nb0 / 128;
+#pragma unroll
+        for (int j = 0; j < TM; ++j) {
+            const int64_t m = mb0 + j * 32 + tok;
+            float* dst = p.lpart + (tile * p.Mp + m) * 32 + 4 * half;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int i = (j * 16 + 4 * q + e) * 64 + lane;
+                    v[e] = mine[i] + other[i];
+                }
+                *reinterpret_cast<float4*>(dst + 8 * q) = make_float4(v[0], v[1], v[2], v[3]);
+            }
+        }
+    }
+}
+
 // The main loop of both GEMMs. W4: the W4A4 product (fp6 tile-blocked codes, per-group scale fold, scales
 // streamed with the codes); otherwise the FP8 product (e4m3 row-major codes only, one fp32 accumulation over all
 // of K in the MFMA accumulator).
@@ -602,7 +805,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         if (total % 8 == 0) tile = (pid % 8) * (total / 8) + pid / 8;
         const int64_t n0 = (tile / ntm) * BN, m0 = (tile % ntm) * BM;
         mainloop(n0, m0, 0, int(G));
-        if constexpr (W4 && EPI != EPI_F32) {
+        if constexpr (EPI == EPI_GELU_QUANT) {
+            static_assert(W4 && BN == 128 && BM == 128 && NW == 4, "the fused GELU epilogue runs on 128 x 128 tiles");
+            __syncthreads();  // every wave is past its last read of the ring, whose LDS the exchange reuses
+            static_assert(4 * 2 * 16 * 64 * 4 <= STAGES * CS, "exchange fits in the ring");
+            finish_tile_gelu_quant<TN, TM>(p, acc, n0 + wn * WN, m0 + wm * WM, wn, wm, lane,
+                                           reinterpret_cast<float*>(&sC[0][0]));
+        } else if constexpr (W4 && EPI != EPI_F32) {
             __syncthreads();  // every wave is past its last read of the ring, whose LDS the staging reuses
             static_assert(NW * 64 * STG * 2 <= STAGES * CS, "staging fits in the ring");
             finish_tile_rows<TN, TM, EPI>(p, acc, n0 + wn * WN, m0 + wm * WM, lane,
@@ -788,6 +997,16 @@ int dispatch(const GemmArgs& a, int epi, hipStream_t stream) {
     return launch<128, 128, 64, 64, 4, WDL_GEMM_STAGES>(a, epi, stream);
 }
 
+// The fused GELU MLP's first GEMM always runs the one-pass 128 x 128 launch (its epilogue owns one 64-feature
+// group per wave), then the low-rank partials of its N / 128 feature tiles are added per token.
+int dispatch_gelu_quant(const GemmArgs& a, float* lora2, hipStream_t stream) {
+    const unsigned grid = unsigned((a.N / 128) * (a.Mp / 128));
+    w4a4_gemm_kernel<128, 128, 64, 64, 4, EPI_GELU_QUANT, WDL_GEMM_STAGES><<<grid, 256, 0, stream>>>(a);
+    const int rc = check_launch("w4a4_gemm_gelu_quant");
+    if (rc) return rc;
+    return lora_sum(a.lpart, int(a.N / 128), a.Mp * 32, lora2, stream);
+}
+
 // fp6 codes (e3m2 of 2w) of the two's complement nibbles 0..7 (w = 0..7) and 8..15 (w = -8..-1)
 constexpr uint32_t LUT0 = 0x16141000u, LUT1 = 0x1B1A1918u, LUT2 = 0x393A3B3Cu, LUT3 = 0x30343638u;
 
@@ -863,6 +1082,42 @@ extern "C" int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wc
     if (reinterpret_cast<uintptr_t>(workspace) % 16)
         return fail(WDL_EINVAL, "w4a4_gemm: workspace must be 16-byte aligned");
     return dispatch(a, epilogue, stream);
+}
+
+extern "C" int64_t wdl_w4a4_gemm_gelu_quant_workspace_floats(int64_t Mp, int64_t N) {
+    if (Mp <= 0 || Mp % 128 || N <= 0 || N % 128) return 0;
+    return (N / 128) * Mp * 32;
+}
+
+extern "C" int wdl_w4a4_gemm_gelu_quant(const void* qa, const void* ascales, const void* wcodes, const void* wscales,
+                                        const float* lora, const void* proj_up, const void* bias, int64_t M,
+                                        int64_t Mp, int64_t N, int64_t K, int64_t rank, const void* smooth2,
+                                        const void* proj_down2_t, void* q2, void* ascales2, float* lora2,
+                                        float* workspace, hipStream_t stream) {
+    if (M < 0 || Mp < M || Mp % 128 || N <= 0 || N % 128 || K <= 0 || K % 64 || K > (int64_t(1) << 30))
+        return fail(WDL_EINVAL, "w4a4_gemm_gelu_quant: bad shape M=%lld Mp=%lld N=%lld K=%lld", (long long)M,
+                    (long long)Mp, (long long)N, (long long)K);
+    if (lora && (rank != 32 || !proj_up)) return fail(WDL_EINVAL, "w4a4_gemm_gelu_quant: low-rank branch needs rank 32");
+    if (!qa || !ascales || !wcodes || !wscales || !smooth2 || !proj_down2_t || !q2 || !ascales2 || !lora2 ||
+        !workspace)
+        return fail(WDL_EINVAL, "w4a4_gemm_gelu_quant: null pointer");
+    const uintptr_t a16 = reinterpret_cast<uintptr_t>(qa) | reinterpret_cast<uintptr_t>(wcodes) |
+                          reinterpret_cast<uintptr_t>(q2) | reinterpret_cast<uintptr_t>(lora2) |
+                          reinterpret_cast<uintptr_t>(workspace) | reinterpret_cast<uintptr_t>(proj_up) |
+                          reinterpret_cast<uintptr_t>(lora);
+    const uintptr_t a8 = reinterpret_cast<uintptr_t>(bias) | reinterpret_cast<uintptr_t>(smooth2) |
+                         reinterpret_cast<uintptr_t>(proj_down2_t);
+    if (a16 % 16 || a8 % 8 || (reinterpret_cast<uintptr_t>(ascales) | reinterpret_cast<uintptr_t>(wscales) |
+                               reinterpret_cast<uintptr_t>(ascales2)) % 4)
+        return fail(WDL_EINVAL, "w4a4_gemm_gelu_quant: codes, lora, proj_up and workspace must be 16-byte aligned, "
+                                "bias, smooth2 and proj_down2_t 8-byte, scales 4-byte");
+    if (M == 0) return WDL_OK;
+    GemmArgs a{static_cast<const uint8_t*>(qa), static_cast<const uint16_t*>(ascales),
+               static_cast<const uint8_t*>(wcodes), static_cast<const uint16_t*>(wscales), lora,
+               static_cast<const uint16_t*>(proj_up), static_cast<const uint16_t*>(bias), M, Mp, N, K, nullptr, N,
+               nullptr, nullptr, nullptr, nullptr, static_cast<uint8_t*>(q2), static_cast<uint16_t*>(ascales2),
+               static_cast<const uint16_t*>(smooth2), static_cast<const uint16_t*>(proj_down2_t), workspace};
+    return dispatch_gelu_quant(a, lora2, stream);
 }
 
 extern "C" int wdl_w4a4_weight_codes(const void* qweight, int64_t N, int64_t K, void* codes, hipStream_t stream) {

@@ -30,6 +30,8 @@ namespace wdl {
 int fail(int code, const char* fmt, ...);
 int check_launch(const char* what);
 int cu_count();  // compute units of the current device (cached per device; 0 if the query fails)
+// out[i] = sum over b = 0 .. nb-1 (in increasing order) of part[b * n + i], i < n (low-rank partial sums)
+int lora_sum(const float* part, int nb, int64_t n, float* out, hipStream_t stream);
 
 // The W4A4 GEMM's operands: fp6 codes, tile-blocked.
 //

@@ -32,6 +32,9 @@ SIGNATURES: dict[str, list] = {
     "wdl_w4a4_gemm_workspace_bytes": [c_i64, c_i64, c_i64],
     "wdl_w4a4_gemm": [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_ptr,
                       c_i64, c_int, c_ptr, c_ptr, c_ptr],
+    "wdl_w4a4_gemm_gelu_quant_workspace_floats": [c_i64, c_i64],
+    "wdl_w4a4_gemm_gelu_quant": [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                 c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr],
     "wdl_fp8_quantize_workspace_floats": [c_i64, c_i64],
     "wdl_fp8_quantize": [c_ptr, c_int, c_i64, c_i64, c_i64, c_i64, c_int, c_ptr, c_ptr, c_ptr, c_ptr],
     "wdl_fp8_gemm": [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_int, c_ptr, c_i64, c_ptr],
@@ -50,7 +53,8 @@ SIGNATURES: dict[str, list] = {
 # return types other than int: the workspace-size queries return int64_t (a c_int default would truncate them)
 RESTYPES = {"wdl_last_error": ctypes.c_char_p, "wdl_sage_prep_workspace_floats": c_i64,
             "wdl_sage_attn_workspace_bytes": c_i64, "wdl_w4a4_gemm_workspace_bytes": c_i64,
-            "wdl_act_quant_workspace_floats": c_i64, "wdl_fp8_quantize_workspace_floats": c_i64}
+            "wdl_act_quant_workspace_floats": c_i64, "wdl_fp8_quantize_workspace_floats": c_i64,
+            "wdl_w4a4_gemm_gelu_quant_workspace_floats": c_i64}
 
 _LIB = None
 

@@ -10,8 +10,8 @@ kernel sequence of one block (about 19 launches, all on the current stream, capt
   (X += gate_a * y, fused)
   act_quant(X; LN3 affine) -> W4A4 cross q -> RMSNorm -> sage_attn(int8 Q in the kernel; context K/V, prepared once per
   prompt) -> act_quant -> W4A4 cross o (X += y, fused)
-  act_quant(X; LN + (1 + scale_f), + shift_f) -> W4A4 ffn.0 (GELU epilogue) -> act_quant((h + 0.171875) / s2,
-  unsigned) -> W4A4 ffn.2 (X += gate_f * y, fused)
+  act_quant(X; LN + (1 + scale_f), + shift_f) -> W4A4 ffn.0 (epilogue: GELU, (h + 0.171875) / s2 quantized
+  unsigned, h . proj_down2 partials) -> low-rank sum -> W4A4 ffn.2 (X += gate_f * y, fused)
 
 X is updated in place (a bf16 [M, dim] buffer owned by the caller).
 """
@@ -22,7 +22,7 @@ import torch
 
 from wdl import ops
 from wdl.kvcache import KVCache
-from wdl.ops import EPI_BF16, EPI_GELU, EPI_RESIDUAL, GELU_SHIFT
+from wdl.ops import EPI_BF16, EPI_RESIDUAL
 
 LINEARS = ("qkv", "o", "cq", "ck", "cv", "co", "ffn1", "ffn2")
 
@@ -95,10 +95,13 @@ class QuantizedWanBlock:
                                         self.eps)
         Ac = ops.sage_attn_q16_launch(Qc, ctx, ctx["L"], 128 ** -0.5)
         self._gemm(self._quant(Ac, "co"), "co", M, X, EPI_RESIDUAL, self.ones)
-        # feed forward (W4A4 GELU MLP)
-        h = torch.empty(M, ops.out_features(self.p["ffn1"]["wcodes"]), device=dev, dtype=torch.bfloat16)
-        self._gemm(self._quant(X, "ffn1", ln=dict(shift=sh_f, scale=sc_f, eps=self.eps)), "ffn1", M, h, EPI_GELU)
-        self._gemm(self._quant(h, "ffn2", shift=GELU_SHIFT, unsigned=True), "ffn2", M, X, EPI_RESIDUAL, g_f)
+        # feed forward: the fused W4A4 GELU MLP (the hidden layer goes from the first GEMM's epilogue to the second
+        # GEMM as int4 codes, scales and low-rank sums)
+        q, asc, lora = self._quant(X, "ffn1", ln=dict(shift=sh_f, scale=sc_f, eps=self.eps))
+        t1, t2 = self.p["ffn1"], self.p["ffn2"]
+        hq = ops.gelu_quant_launch(q, asc, lora, t1["wcodes"], t1["wscales"], t1["proj_up"], t1["bias"], M,
+                                   t2["smooth"], t2["proj_down"])
+        self._gemm(hq, "ffn2", M, X, EPI_RESIDUAL, g_f)
         return X
 
 

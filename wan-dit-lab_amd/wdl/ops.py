@@ -206,6 +206,31 @@ def gemm_launch(q, ascales, lora, wcodes, wscales, proj_up, bias, M, out, epilog
     return out
 
 
+def gelu_quant_launch(q, ascales, lora, wcodes, wscales, proj_up, bias, M, smooth2, proj_down2_t):
+    """The fused GELU MLP's first GEMM: the quantizer's outputs of x (q, ascales, lora) and the first layer's
+    operands -> the second layer's inputs (q2 fp6 codes [Mp/128, N/64, 128, 48], ascales2 bf16 [N/64, Mp], lora2
+    fp32 [Mp, 32]) for h = GELU(x W1^T + b1) quantized as (h + 0.171875) / smooth2, unsigned; h stays in
+    registers."""
+    if q.dim() != 4 or wcodes.dim() != 4 or q.shape[2:] != (BLOCK, ROW6) or wcodes.shape[2:] != (BLOCK, ROW6):
+        raise ValueError("the W4A4 GEMM takes tile-blocked fp6 operands [rows/128, K/64, 128, 48]")
+    Mp, K = q.shape[0] * BLOCK, q.shape[1] * 64
+    N = wcodes.shape[0] * BLOCK
+    if wcodes.shape[1] != q.shape[1]:
+        raise ValueError(f"weight codes {tuple(wcodes.shape)} do not match activations of width {K}")
+    if smooth2.shape != (N,) or proj_down2_t.shape != (RANK, N):
+        raise ValueError(f"smooth2 must be [{N}] and proj_down2 [{RANK}, {N}] for a hidden layer of {N}")
+    dev = q.device
+    q2 = torch.empty(Mp // BLOCK, N // 64, BLOCK, ROW6, device=dev, dtype=torch.uint8)
+    asc2 = torch.empty(N // 64, Mp, device=dev, dtype=torch.bfloat16)
+    lora2 = torch.empty(Mp, RANK, device=dev, dtype=torch.float32)
+    ws = torch.empty(_lib.library().wdl_w4a4_gemm_gelu_quant_workspace_floats(Mp, N), device=dev,
+                     dtype=torch.float32)
+    _lib.call("wdl_w4a4_gemm_gelu_quant", ptr(q), ptr(ascales), ptr(wcodes), ptr(wscales), ptr(lora), ptr(proj_up),
+              ptr(bias), M, Mp, N, K, RANK, ptr(smooth2), ptr(proj_down2_t), ptr(q2), ptr(asc2), ptr(lora2), ptr(ws),
+              stream_of(q))
+    return q2, asc2, lora2
+
+
 @torch.library.custom_op("wdl::act_quant_w4", mutates_args=())
 def act_quant_w4(x: torch.Tensor, smooth: torch.Tensor, proj_down: torch.Tensor, qshift: float,
                  unsigned: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
@@ -261,16 +286,16 @@ def w4a4_gelu_mlp(x: torch.Tensor, qweight1: torch.Tensor, wscales1: torch.Tenso
                   proj_up1: torch.Tensor, smooth1: torch.Tensor, bias1: torch.Tensor, qweight2: torch.Tensor,
                   wscales2: torch.Tensor, proj_down2: torch.Tensor, proj_up2: torch.Tensor, smooth2: torch.Tensor,
                   bias2: torch.Tensor) -> torch.Tensor:
-    """live::w4a4_gelu_mlp (native/ops/w4a4_ops.cpp:44-63): h = GELU(x W1^T + b1) in the first GEMM's epilogue
-    (bf16 h), then (h + 0.171875) / smooth2 quantized unsigned with the low-rank down projection of h, then the
-    second GEMM."""
+    """live::w4a4_gelu_mlp (native/ops/w4a4_ops.cpp:44-63): the first GEMM applies GELU, quantizes
+    (h + 0.171875) / smooth2 unsigned and forms the low-rank down projection of h in its epilogue (h in fp32, never
+    in memory), then the second GEMM."""
     M = x.shape[0]
     q, asc, lora = act_quant_launch(x, smooth1, proj_down1)
-    h = torch.empty(M, out_features(qweight1), device=x.device, dtype=torch.bfloat16)
-    gemm_launch(q, asc, lora, as_codes(qweight1, x.shape[1]), wscales1, proj_up1, bias1, M, h, EPI_GELU)
-    q2, asc2, lora2 = act_quant_launch(h, smooth2, proj_down2, GELU_SHIFT, True)
+    hidden = out_features(qweight1)
+    q2, asc2, lora2 = gelu_quant_launch(q, asc, lora, as_codes(qweight1, x.shape[1]), wscales1, proj_up1, bias1, M,
+                                        smooth2, proj_down2)
     out = torch.empty(M, out_features(qweight2), device=x.device, dtype=torch.bfloat16)
-    return gemm_launch(q2, asc2, lora2, as_codes(qweight2, h.shape[1]), wscales2, proj_up2, bias2, M, out)
+    return gemm_launch(q2, asc2, lora2, as_codes(qweight2, hidden), wscales2, proj_up2, bias2, M, out)
 
 
 @w4a4_gelu_mlp.register_fake
