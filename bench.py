@@ -113,6 +113,7 @@ def instrumented(step):
 
     rec = {"gemm": [], "attn": []}
     orig_gemm, orig_attn, orig_attn16 = ops.gemm_launch, ops.sage_attn_launch, ops.sage_attn_q16_launch
+    orig_gq = ops.gelu_quant_launch
 
     def gemm(q, ascales, lora, qweight, *a, **k):
         M = a[3]
@@ -121,6 +122,15 @@ def instrumented(step):
         out = orig_gemm(q, ascales, lora, qweight, *a, **k)
         e1.record()
         rec["gemm"].append((e0, e1, 2.0 * M * ops.out_features(qweight) * q.shape[1] * 64))
+        return out
+
+    def gelu_quant(q, ascales, lora, wcodes, *a, **k):
+        M = a[3]  # (wscales, proj_up, bias, M, smooth2, proj_down2_t)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        out = orig_gq(q, ascales, lora, wcodes, *a, **k)
+        e1.record()
+        rec["gemm"].append((e0, e1, 2.0 * M * ops.out_features(wcodes) * q.shape[1] * 64))
         return out
 
     def attn(q_i8, q_scale, prep, L, sm_scale, out=None):
@@ -141,6 +151,7 @@ def instrumented(step):
         return r
 
     ops.gemm_launch, ops.sage_attn_launch, ops.sage_attn_q16_launch = gemm, attn, attn16
+    ops.gelu_quant_launch = gelu_quant
     # Keep the GPU behind the host while the step is enqueued, so that each start event is followed at once by its
     # (already queued) kernel and no host launch latency falls between the events: a spin kernel of ~0.5 s first.
     probe = 10_000_000
@@ -156,6 +167,7 @@ def instrumented(step):
         torch.cuda.synchronize()
     finally:
         ops.gemm_launch, ops.sage_attn_launch, ops.sage_attn_q16_launch = orig_gemm, orig_attn, orig_attn16
+        ops.gelu_quant_launch = orig_gq
     out = {}
     for name, items in rec.items():
         ms = sum(a.elapsed_time(b) for a, b, _ in items)
@@ -178,35 +190,106 @@ def gemm_traffic():
     return int(m.group(1)) if m else None
 
 
-def cpu_baseline():
-    """The oracle block on the reference's CPU-sized workload (one 16 x 29 = 464-token frame over a 928-token FP8
-    cache, 512 context tokens, dim 3072) timed on this host's cores; reported as latent tokens/s of a 30-block
-    step."""
-    import torch
+class CpuBlock:
+    """The quantized Wan block as a PyTorch program on the host CPU, in one floating dtype (bf16 or fp32): the
+    reference's block (models/block.py:22-29) with its W4A4 linears computed as fake quantization (activations per
+    token and 64-channel group to int4 with a bf16 scale, then dequantized; int4 weights dequantized once), the
+    fused GELU MLP's hidden layer quantized unsigned after the 0.171875 shift, the FP8 cache dequantized, Q/K
+    RMSNorm, 3D RoPE (fp32 table) and torch's scaled_dot_product_attention over the window and over the prompt.
+    Random-init parts of the Wan2.2-TI2V-5B block shapes (int4 in [-7, 7], N(0, 0.02^2)-sized group scales)."""
 
-    from oracle import block as oblock
-    from oracle import rope as orope
+    def __init__(self, dtype, seed=0):
+        import torch
+
+        g = torch.Generator().manual_seed(seed)
+        self.dt = dtype
+        shapes = dict(qkv=(3 * DIM, DIM), o=(DIM, DIM), cq=(DIM, DIM), ck=(DIM, DIM), cv=(DIM, DIM), co=(DIM, DIM),
+                      ffn1=(FFN, DIM), ffn2=(DIM, FFN))
+        self.lin = {}
+        for name, (n, k) in shapes.items():
+            q = torch.randint(-7, 8, (n, k), generator=g).float()
+            ws = (torch.rand(n, k // 64, generator=g) * 0.5 + 0.75) * (3 * 0.02 / 7)
+            self.lin[name] = dict(
+                W=(q.view(n, k // 64, 64) * ws.to(torch.bfloat16).float()[..., None]).view(n, k).to(dtype),
+                pd=(torch.randn(k, 32, generator=g) / k ** 0.5).to(dtype),
+                pu=(torch.randn(n, 32, generator=g) * 0.02).to(dtype),
+                b=(torch.randn(n, generator=g) * 0.02).to(dtype))
+        self.mod = torch.randn(6, DIM, generator=g) / DIM ** 0.5
+        from oracle import rope as orope
+
+        self.freq = orope.freqs(128, 1024, torch.float64).float()
+
+    def linear(self, x, name, shift=0.0, unsigned=False):
+        import torch
+
+        t = self.lin[name]
+        M, K = x.shape
+        u = (x.float() + shift).view(M, K // 64, 64)
+        qmax = 15.0 if unsigned else 7.0
+        s = (u.abs().amax(-1, keepdim=True) / qmax).to(torch.bfloat16).float()
+        q = torch.round(u / torch.where(s > 0, s, torch.ones_like(s))).clamp(0.0 if unsigned else -8.0, qmax)
+        xq = (q * s).view(M, K).to(self.dt)
+        return xq @ t["W"].t() + (x.to(self.dt) @ t["pd"]) @ t["pu"].t() + t["b"]
+
+    def attention(self, Q, K, V):
+        import torch
+
+        o = torch.nn.functional.scaled_dot_product_attention(Q.transpose(0, 1)[None], K.transpose(0, 1)[None],
+                                                             V.transpose(0, 1)[None])
+        return o[0].transpose(0, 1).reshape(Q.shape[0], -1)
+
+    def forward(self, X, time_in, cache_k, cache_v, ctx_k, ctx_v, grid, start):
+        import torch
+        from oracle import rope as orope
+
+        dt, H = self.dt, HEADS
+        e = (time_in + self.mod).to(dt)
+        M = X.shape[0]
+        ln = lambda x: torch.nn.functional.layer_norm(x.float(), (DIM,), eps=1e-6).to(dt)
+        rms = lambda x: (x.float() * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + 1e-6)).to(dt)
+        qkv = self.linear(ln(X) * (1 + e[1]) + e[0], "qkv")
+        Q = orope.rope_apply(rms(qkv[:, :DIM]).view(1, M, H, 128).float(), grid, self.freq, start)[0].to(dt)
+        K = orope.rope_apply(rms(qkv[:, DIM:2 * DIM]).view(1, M, H, 128).float(), grid, self.freq, start)[0].to(dt)
+        V = qkv[:, 2 * DIM:].reshape(M, H, 128)
+        A = self.attention(Q, torch.cat([cache_k, K]), torch.cat([cache_v, V]))
+        X = X + self.linear(A, "o") * e[2]
+        qc = rms(self.linear(ln(X), "cq")).view(M, H, 128)
+        X = X + self.linear(self.attention(qc, ctx_k, ctx_v), "co")
+        h = torch.nn.functional.gelu(self.linear(ln(X) * (1 + e[4]) + e[3], "ffn1").float(), approximate="tanh")
+        return X + self.linear(h, "ffn2", 0.171875, True) * e[5]
+
+
+def cpu_baseline(runs=5, warmups=2):
+    """The block on this host's CPU cores (CpuBlock, bf16 and fp32), on the step's own block workload: 1392 tokens
+    (3 frames of 16 x 29) over a full window (8352 cached FP8 tokens + the chunk = 9744 keys) and 512 prompt tokens.
+    Per dtype: `warmups` untimed runs, then the median of `runs` timed ones (time.perf_counter). Reported as latent
+    tokens/s of a 30-block step (one block timed, x 30: the blocks of a step are alike)."""
+    import torch
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    g = torch.Generator().manual_seed(0)
-    P = oblock.random_logical_block(DIM, FFN, g)
-    grid, M, prior = (1, 16, 29), 464, 928
-    X = torch.randn(M, DIM, generator=g).to(torch.bfloat16)
+    g = torch.Generator().manual_seed(1)
+    X = torch.randn(TOKENS, DIM, generator=g)
     time_in = torch.randn(6, DIM, generator=g) * 0.1
-    C = torch.randn(CONTEXT, DIM, generator=g).to(torch.bfloat16)
-    freq = orope.freqs(128, 1024, torch.float64).float()
-    ck = (torch.randn(1, prior + M, HEADS, 128, generator=g) * 100).clamp(-448, 448).to(torch.float8_e4m3fn)
-    cks = torch.rand(1, prior + M, HEADS, 1, generator=g) * 0.02
-    ctx = oblock.context_kv(C, P)
-    runs = []
-    for i in range(3):
-        cache = dict(k=ck.clone(), ks=cks.clone(), v=ck.clone(), vs=cks.clone(), at=prior)
-        t0 = time.perf_counter()
-        oblock.block_forward(X, time_in, P, grid, freq, 2, cache, ctx, HEADS)
-        runs.append(time.perf_counter() - t0)
-        log(f"bench: cpu oracle block run {i}: {runs[-1]:.2f} s")
-    t_block = sorted(runs)[len(runs) // 2]
+    fp8 = (torch.randn(CACHED, HEADS, 128, generator=g) * 100).clamp(-448, 448).to(torch.float8_e4m3fn)
+    scales = torch.rand(CACHED, HEADS, 1, generator=g) * 0.02
+    ctx = torch.randn(2, CONTEXT, HEADS, 128, generator=g)
+    per = {}
+    with torch.no_grad():
+        for dt in (torch.bfloat16, torch.float32):
+            blk = CpuBlock(dt)
+            cache = (fp8.float() * scales).to(dt)  # the FP8 window dequantized, as the bf16 cache path reads it
+            args = (X.to(dt), time_in, cache, cache, ctx[0].to(dt), ctx[1].to(dt), GRID, WINDOW - GRID[0])
+            times = []
+            for i in range(warmups + runs):
+                t0 = time.perf_counter()
+                blk.forward(*args)
+                if i >= warmups:
+                    times.append(time.perf_counter() - t0)
+            per[str(dt).split(".")[-1]] = sorted(times)[len(times) // 2]
+            log(f"bench: cpu block ({dt}): median {per[str(dt).split('.')[-1]]:.3f} s of {runs} after {warmups} "
+                f"warm-ups")
+            del blk
     cpu = "unknown"
     try:
         for line in open("/proc/cpuinfo"):
@@ -215,10 +298,13 @@ def cpu_baseline():
                 break
     except OSError:
         pass
-    return dict(value=M / (BLOCKS * t_block), unit="latent tokens/s", cores=cores, kind="port",
-                sample=f"oracle block (CPU restatement, torch {torch.__version__}, fp32/fp64 CPU arithmetic) of "
-                       f"one 464-token frame over a 928-token FP8 cache + 512 context tokens, dim 3072; "
-                       f"median of 3 runs = {t_block:.2f} s per block, scaled to a 30-block step; CPU {cpu}")
+    best = min(per, key=per.get)
+    return dict(value=TOKENS / (BLOCKS * per[best]), unit="latent tokens/s", cores=cores, kind="port",
+                dtype=best, seconds_per_block={k: round(v, 4) for k, v in per.items()},
+                sample=f"one block of the step's workload ({TOKENS} tokens over {CACHED + TOKENS} keys + "
+                       f"{CONTEXT} prompt tokens, dim {DIM}, FFN {FFN}) as a PyTorch fake-quant W4A4 block "
+                       f"(bench.CpuBlock) in bf16 and fp32, {warmups} warm-ups then the median of {runs} runs each; "
+                       f"value from the faster dtype ({best}) x {BLOCKS} blocks; CPU {cpu}, torch {torch.__version__}")
 
 
 def main():

@@ -39,10 +39,12 @@ enum Epilogue {
 };
 constexpr float GELU_SHIFT = 0.171875f;  // quantization/w4a4.py:195: GELU(x) > -0.17, so GELU(x) + shift >= 0
 
-// GELU, tanh form: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), tanh(u) = 1 - 2 / (exp(2u) + 1)
+// GELU, tanh form: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), tanh(u) = 1 - 2 / (exp(2u) + 1) with the
+// hardware exp2 and reciprocal (about 1 ulp each; exp(2u) -> inf gives tanh 1, -> 0 gives -1)
 __device__ __forceinline__ float gelu_tanh(float x) {
     const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-    const float th = 1.0f - 2.0f / (__expf(2.0f * u) + 1.0f);
+    const float e = __builtin_amdgcn_exp2f(u * 2.8853900817779268f);  // exp(2u) = 2^(2u log2 e)
+    const float th = fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
     return 0.5f * x * (1.0f + th);
 }
 

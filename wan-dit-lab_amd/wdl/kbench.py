@@ -3,7 +3,7 @@
 attention: Sage prep + attention of 1280 and 1392 queries over a full 9744-key window (8352 cached FP8 tokens + the
 chunk), 24 x 128 heads; prep: the Sage preparation (K mean and V maxima, int8 K and fp8 V of the whole window) of
 the same two shapes; gemm: the W4A4 GEMMs of one block at 1392 tokens (QKV 3072 -> 9216, o 3072 -> 3072 with the
-gated residual, FFN-up 3072 -> 14336 with GELU, FFN-down 14336 -> 3072 with the gated residual), random weights; quant: the activation quantizer with its low-rank down projection at 1392 tokens
+gated residual, FFN-up 3072 -> 14336 with GELU (bf16 out) and fused with the second layer's quantization, FFN-down 14336 -> 3072 with the gated residual), random weights; quant: the activation quantizer with its low-rank down projection at 1392 tokens
 (K 3072 with the fused LayerNorm and modulation, K 3072 plain, K 14336 unsigned).
 Each shape is captured into a HIP graph of 10 launches and replayed; one line per shape with microseconds per
 launch. An optional library path replaces lib/libwdl.so (for comparing builds).
@@ -87,6 +87,13 @@ def gemm():
         us = _replay_us(lambda: ops.gemm_launch(q, asc, lora, wc, t["wscales"], t["proj_up"], t["bias"], M, out, epi,
                                                 gate))
         print(f"gemm {name} {M}x{N}x{K}: {us:.1f} us ({2 * M * N * K / us / 1e6:.0f} TOP/s)", flush=True)
+        if name == "ffn1":  # the fused GELU MLP's first GEMM (epilogue: GELU, second layer's int4 input, low rank)
+            s2 = torch.ones(N, device=dev, dtype=torch.bfloat16)
+            pd2 = (torch.randn(32, N, device=dev, generator=g) / N ** 0.5).to(torch.bfloat16)
+            us = _replay_us(lambda: ops.gelu_quant_launch(q, asc, lora, wc, t["wscales"], t["proj_up"], t["bias"],
+                                                          M, s2, pd2))
+            print(f"gemm ffn1 fused {M}x{N}x{K}: {us:.1f} us ({2 * M * N * K / us / 1e6:.0f} TOP/s, with the "
+                  f"low-rank sum launch)", flush=True)
 
 
 def quant():
