@@ -113,7 +113,7 @@ def instrumented(step):
 
     rec = {"gemm": [], "attn": []}
     orig_gemm, orig_attn, orig_attn16 = ops.gemm_launch, ops.sage_attn_launch, ops.sage_attn_q16_launch
-    orig_gq = ops.gelu_quant_launch
+    orig_gq, orig_bf16 = ops.gelu_quant_launch, ops.attn_bf16_launch
 
     def gemm(q, ascales, lora, qweight, *a, **k):
         M = a[3]
@@ -142,6 +142,14 @@ def instrumented(step):
         rec["attn"].append((e0, e1, 4.0 * n * L * d * H))
         return r
 
+    def attn_bf16(Q, prep, sm_scale, out=None):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        r = orig_bf16(Q, prep, sm_scale, out)
+        e1.record()
+        rec["attn"].append((e0, e1, 4.0 * Q.shape[0] * prep["L"] * Q.shape[1]))
+        return r
+
     def attn16(Q, prep, L, sm_scale, out=None):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -151,7 +159,7 @@ def instrumented(step):
         return r
 
     ops.gemm_launch, ops.sage_attn_launch, ops.sage_attn_q16_launch = gemm, attn, attn16
-    ops.gelu_quant_launch = gelu_quant
+    ops.gelu_quant_launch, ops.attn_bf16_launch = gelu_quant, attn_bf16
     # Keep the GPU behind the host while the step is enqueued, so that each start event is followed at once by its
     # (already queued) kernel and no host launch latency falls between the events: a spin kernel of ~0.5 s first.
     probe = 10_000_000
@@ -167,7 +175,7 @@ def instrumented(step):
         torch.cuda.synchronize()
     finally:
         ops.gemm_launch, ops.sage_attn_launch, ops.sage_attn_q16_launch = orig_gemm, orig_attn, orig_attn16
-        ops.gelu_quant_launch = orig_gq
+        ops.gelu_quant_launch, ops.attn_bf16_launch = orig_gq, orig_bf16
     out = {}
     for name, items in rec.items():
         ms = sum(a.elapsed_time(b) for a, b, _ in items)

@@ -207,6 +207,26 @@ int wdl_sage_attn_q16(const void* q_bf16, int64_t ldq, const void* k_i8, const f
                       const float* v_scale, int64_t n, int64_t L, int64_t heads, float sm_scale, void* out,
                       int64_t ldo, void* workspace, wdl_stream_t stream);
 
+/* Elements (bf16) of each of the two operands wdl_attn_bf16_prep writes for L keys and `heads` heads. */
+int64_t wdl_attn_bf16_prep_elems(int64_t L, int64_t heads);
+
+/* The keys and values of a bf16 attention laid out for wdl_attn_bf16, once per prompt: K, V bf16 [L, heads, 128]
+ * (token strides ldk, ldv; K rows 16-byte aligned) -> Kp bf16 [heads][Lpad][128] (each key row's 16-byte chunks
+ * XOR-swizzled by key % 16) and Vp bf16 [heads][128][Lpad] (V transposed; in each 16-key group the keys ordered
+ * 0..3, 8..11, 4..7, 12..15; each channel row's 16-byte chunks of a 64-key block XOR-swizzled by (channel / 2) % 8),
+ * Lpad = 64 ceil(L / 64), keys >= L zero. Part of the cross-attention that keys_values and Stream.cross compute once
+ * per prompt (models/multi_head_attention.py:21-26; generation/causal.py:557-568). */
+int wdl_attn_bf16_prep(const void* k, int64_t ldk, const void* v, int64_t ldv, int64_t L, int64_t heads, void* kp,
+                       void* vp, wdl_stream_t stream);
+
+/* bf16 attention (non-causal, fp32 online softmax, P rounded to bf16 for the P V product, fp32 accumulation):
+ * out = softmax(Q K^T sm_scale) V. Replaces torch.nn.functional.scaled_dot_product_attention on bf16 operands, as
+ * the reference's cross-attention runs it (models/multi_head_attention.py:37-44 with the context's keys and values;
+ * generation/causal.py:418-420). q: bf16 [n, heads, 128] (row stride ldq); kp, vp: wdl_attn_bf16_prep's layouts of
+ * L keys; out bf16 [n, heads, 128] (row stride ldo). No workspace. */
+int wdl_attn_bf16(const void* q, int64_t ldq, const void* kp, const void* vp, int64_t n, int64_t L, int64_t heads,
+                  float sm_scale, void* out, int64_t ldo, wdl_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -7,12 +7,13 @@
   qkv = W4A4(x1) -> bf16;  Q, K = RoPE(RMSNorm(q)), RoPE(RMSNorm(k));  V = v                (w4a4.py:255-258)
   cache[at:at+n] = quantize_rows(K), quantize_rows(V);  A = Sage(Q; cache[:at] ++ (K, V))   (causal.py:193-210)
   X   = bf16(X + bf16(W4A4(A)) * gate_a)                                                     (block.py:25-26)
-  Xc  = bf16(LN3_affine(X));  Qc = RMSNorm(W4A4(Xc));  X = bf16(X + bf16(W4A4(Sage(Qc; Kc, Vc))))  (block.py:27)
+  Xc  = bf16(LN3_affine(X));  Qc = RMSNorm(W4A4(Xc));  X = bf16(X + bf16(W4A4(SDPA(Qc; Kc, Vc))))  (block.py:27)
   h   = GELU(W4A4(bf16(LN(X) * (1 + scale_f) + shift_f))) in fp32;  X = bf16(X + bf16(W4A4_u(h)) * gate_f)  (28)
 with W4A4_u the second GELU-MLP layer: its INT4 branch quantizes (h + 0.171875) / s2 unsigned and its low-rank
 branch reads h itself, the hidden layer never rounded to 16 bits (the fused GELU MLP, w4a4.py:198-204,
 w4a4_ops.cpp:42-63; w4a4.gelu_mlp of this oracle). The attention is the blockwise online
-softmax of the kernel (sage.attention_online). The reference applies the modulation in bf16 op by op and adds
+softmax of the kernel (sage.attention_online); the cross-attention over the prompt is the exact softmax on
+bf16 operands (the reference's SDPA). The reference applies the modulation in bf16 op by op and adds
 the residual in bf16 after a bf16 product; the bar against it is the tolerance of tests/test_w4a4.py:62-87.
 """
 
@@ -42,6 +43,15 @@ def context_kv(C: torch.Tensor, P: dict):
     K = _rms(_lin(C, P["ck"]).to(BF), P["cwk"])
     V = _lin(C, P["cv"]).to(BF)
     return K, V
+
+
+def cross_attention(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, heads: int) -> torch.Tensor:
+    """The context attention as the reference computes it: scaled_dot_product_attention on the bf16 Qc, Kc, Vc
+    (multi_head_attention.py:37-44; causal.py:418-420 keep SDPA for cross-attention), here the exact softmax in
+    float64 -> bf16 [M, D]."""
+    M, D = Q.shape
+    Q4, K4, V4 = (t.reshape(1, -1, heads, 128) for t in (Q, K, V))
+    return osage.attention_exact(Q4, K4.float(), V4.float()).reshape(M, D).to(BF)
 
 
 def attention(Q: torch.Tensor, cache: dict | None, K: torch.Tensor, V: torch.Tensor, heads: int) -> torch.Tensor:
@@ -78,7 +88,7 @@ def block_forward(X: torch.Tensor, time_in: torch.Tensor, P: dict, grid, freq: t
     xc = onorms.ln_mod(X, None, None, P["n3w"], P["n3b"], eps=eps)
     Qc = _rms(_lin(xc, P["cq"]).to(BF), P["cwq"])
     Kc, Vc = ctx_kv
-    Ac = attention(Qc, None, Kc, Vc, heads)
+    Ac = cross_attention(Qc, Kc, Vc, heads)
     yc = _lin(Ac, P["co"]).to(BF)
     X = (X.float() + yc.float()).to(BF)
     x2 = onorms.ln_mod(X, sh_f, sc_f, eps=eps)

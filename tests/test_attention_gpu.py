@@ -325,3 +325,26 @@ def test_fused_qkv_attention_module_matches_oracle(gpu, cached):
     e2e = rel(got.cpu().reshape(M, dim), want)
     print(f"cached={cached}: attention stage rel {rel(Ag, A):.2e}, end to end rel-L2 {e2e:.2e}")
     assert e2e <= 2e-2
+
+
+@pytest.mark.parametrize("n,L,H", [(1392, 512, 24), (464, 512, 24), (100, 77, 2), (300, 1000, 3)])
+def test_bf16_attention_is_the_exact_softmax(gpu, n, L, H):
+    """wdl_attn_bf16 (the cross-attention: bf16 operands, fp32 online softmax, P rounded to bf16 as flash attention
+    does) against the exact softmax in float64 on the same bf16 values. 1392 x 512 x 24 heads is the step's
+    cross-attention (264 tiles: two per workgroup on the first ones), 464 x 512 one tile per workgroup; L = 77 and
+    1000 end in a partial 64-key block. Bar: relative L2 <= 2 * 2^-9 and cosine >= 0.99999 (P's bf16 rounding is the
+    only approximation: up to 2^-9 relative per weight; measured 2.2e-3 at the step's shape)."""
+    from oracle import sage as osage
+    from wdl import ops
+
+    g = torch.Generator().manual_seed(n + L + H)
+    Q = torch.randn(n, H * 128, generator=g).to(torch.bfloat16)
+    K = (torch.randn(L, H * 128, generator=g) + torch.randn(1, H * 128, generator=g) * 2).to(torch.bfloat16)
+    V = torch.randn(L, H * 128, generator=g).to(torch.bfloat16)
+    sm = 128 ** -0.5
+    prep = ops.attn_bf16_prep_launch(K.cuda(), V.cuda())
+    out = ops.attn_bf16_launch(Q.cuda(), prep, sm).cpu()
+    ref = osage.attention_exact(Q.view(1, n, H, 128), K.view(1, L, H, 128).float(), V.view(1, L, H, 128).float(), sm)
+    rel, cos = osage.rel_err(out.view(1, n, H, 128), ref), osage.cosine(out, ref)
+    print(f"bf16 attention n={n} L={L} H={H}: rel-L2 {rel:.2e}, cosine {cos:.7f}")
+    assert rel <= 2 * 2 ** -9 and cos >= 0.99999

@@ -179,6 +179,12 @@ def test_config1_stages_given_identical_inputs(gpu):
     xc = onorms.ln_mod(X, None, None, P["n3w"], P["n3b"])
     assert rel(gpu_lin(xc, "cq"), oblock._lin(xc, P["cq"]).to(BF)) <= 1e-4
     assert rel(gpu_lin(C, "ck"), oblock._lin(C, P["ck"]).to(BF)) <= 1e-4
+    # cross-attention: the oracle's exact softmax on bf16 operands (the reference's SDPA) against the bf16 kernel
+    Qc = oblock._rms(oblock._lin(xc, P["cq"]).to(BF), P["cwq"])
+    Kc, Vc = oblock.context_kv(C, P)
+    Ac = oblock.cross_attention(Qc, Kc, Vc, heads)
+    Acg = ops.attn_bf16_launch(Qc.to(dev), ops.attn_bf16_prep_launch(Kc.to(dev), Vc.to(dev)), 128 ** -0.5).cpu()
+    assert rel(Acg, Ac) <= 2 * 2 ** -9 and osage.cosine(Acg, Ac) >= 0.99999  # P rounded to bf16: 2^-9 per weight
     # the fused GELU MLP: the oracle's hidden layer is fp32 (w4a4.py:198-204); the kernel's GELU differs from
     # torch's in the last bits, so a few int4 values of the hidden layer land one step apart (the epilogue test
     # bounds them): relative L2 1e-3 here

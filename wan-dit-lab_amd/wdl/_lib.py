@@ -49,12 +49,15 @@ SIGNATURES: dict[str, list] = {
                       c_ptr, c_ptr],
     "wdl_sage_attn_q16": [c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_f32, c_ptr, c_i64,
                           c_ptr, c_ptr],
+    "wdl_attn_bf16_prep_elems": [c_i64, c_i64],
+    "wdl_attn_bf16_prep": [c_ptr, c_i64, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr],
+    "wdl_attn_bf16": [c_ptr, c_i64, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_f32, c_ptr, c_i64, c_ptr],
 }
 # return types other than int: the workspace-size queries return int64_t (a c_int default would truncate them)
 RESTYPES = {"wdl_last_error": ctypes.c_char_p, "wdl_sage_prep_workspace_floats": c_i64,
             "wdl_sage_attn_workspace_bytes": c_i64, "wdl_w4a4_gemm_workspace_bytes": c_i64,
             "wdl_act_quant_workspace_floats": c_i64, "wdl_fp8_quantize_workspace_floats": c_i64,
-            "wdl_w4a4_gemm_gelu_quant_workspace_floats": c_i64}
+            "wdl_w4a4_gemm_gelu_quant_workspace_floats": c_i64, "wdl_attn_bf16_prep_elems": c_i64}
 
 _LIB = None
 

@@ -8,8 +8,8 @@ kernel sequence of one block (about 19 launches, all on the current stream, capt
   act_quant(X; LN + (1 + scale_a), + shift_a)  -> W4A4 qkv -> norm_rope(q, k) -> kv_append(K, V @ at)
   -> sage_prep(cache[:at] ++ K, V) -> sage_attn (int8 Q quantized in the kernel) -> act_quant(A) -> W4A4 o
   (X += gate_a * y, fused)
-  act_quant(X; LN3 affine) -> W4A4 cross q -> RMSNorm -> sage_attn(int8 Q in the kernel; context K/V, prepared once per
-  prompt) -> act_quant -> W4A4 cross o (X += y, fused)
+  act_quant(X; LN3 affine) -> W4A4 cross q -> RMSNorm -> bf16 attention over the context K/V (laid out once per
+  prompt; exact fp32 softmax, as the reference's SDPA) -> act_quant -> W4A4 cross o (X += y, fused)
   act_quant(X; LN + (1 + scale_f), + shift_f) -> W4A4 ffn.0 (epilogue: GELU, (h + 0.171875) / s2 quantized
   unsigned, h . proj_down2 partials) -> low-rank sum -> W4A4 ffn.2 (X += gate_f * y, fused)
 
@@ -31,8 +31,14 @@ class QuantizedWanBlock:
     """parts: {linear: packed W4A4 parts (w4a4.quantize / pack_parts)} for LINEARS, plus wq, wk, cwq, cwk (bf16
     RMSNorm weights [dim]), n3w, n3b (fp32 LayerNorm-3 affine [dim]) and modulation (fp32 [6, dim])."""
 
-    def __init__(self, parts: dict, dim: int, heads: int, eps: float = 1e-6):
+    def __init__(self, parts: dict, dim: int, heads: int, eps: float = 1e-6, cross_attention: str = "sdpa"):
+        """cross_attention: "sdpa" — bf16 attention with an exact fp32 softmax, what the reference runs for the
+        context (scaled_dot_product_attention, causal.py:418-420); "sage" — int8 QK / fp8 PV Sage attention over
+        the context too (an opt-in deviation: faster on long prompts, within Sage's error bars)."""
+        if cross_attention not in ("sdpa", "sage"):
+            raise ValueError(f"cross_attention must be 'sdpa' or 'sage', got {cross_attention!r}")
         self.p, self.dim, self.heads, self.eps = parts, dim, heads, eps
+        self.cross_attention = cross_attention
         dev = parts["qkv"]["qweight"].device
         for name in LINEARS:  # the GEMM operand: tile-blocked fp6 codes (e3m2 of 2w), expanded once from the nibbles
             parts[name]["wcodes"] = ops.weight_codes(parts[name]["qweight"])
@@ -55,11 +61,14 @@ class QuantizedWanBlock:
 
     def prepare_context(self, C: torch.Tensor) -> dict:
         """Cross-attention keys and values of a prompt, once per prompt (multi_head_attention.py:21-26;
-        causal.Stream.cross, causal.py:557-568): K = RMSNorm(k(C)), V = v(C), then Sage's int8 K / fp8 V."""
+        causal.Stream.cross, causal.py:557-568): K = RMSNorm(k(C)), V = v(C), laid out for the bf16 attention
+        (or quantized to Sage's int8 K / fp8 V with cross_attention="sage")."""
         Kc = self.linear(C, "ck")
         Kn, _ = ops.qk_norm_rope_launch(Kc, None, self.p["cwk"], None, self._nofreq(C.device), (0, 1, 1), 0,
                                         self.eps)
         Vc = self.linear(C, "cv")
+        if self.cross_attention == "sdpa":
+            return ops.attn_bf16_prep_launch(Kn, Vc)
         H = self.heads
         z8 = torch.zeros(1, 1, H, 128, device=C.device, dtype=torch.uint8)
         z = torch.ones(1, 1, H, 1, device=C.device)
@@ -93,7 +102,10 @@ class QuantizedWanBlock:
         self._gemm(self._quant(X, "cq", ln=n3), "cq", M, qc)
         Qc, _ = ops.qk_norm_rope_launch(qc, None, self.p["cwq"], None, self._nofreq(dev), (0, 1, 1), 0,
                                         self.eps)
-        Ac = ops.sage_attn_q16_launch(Qc, ctx, ctx["L"], 128 ** -0.5)
+        if "kp" in ctx:
+            Ac = ops.attn_bf16_launch(Qc, ctx, 128 ** -0.5)
+        else:
+            Ac = ops.sage_attn_q16_launch(Qc, ctx, ctx["L"], 128 ** -0.5)
         self._gemm(self._quant(Ac, "co"), "co", M, X, EPI_RESIDUAL, self.ones)
         # feed forward: the fused W4A4 GELU MLP (the hidden layer goes from the first GEMM's epilogue to the second
         # GEMM as int4 codes, scales and low-rank sums)
@@ -105,7 +117,7 @@ class QuantizedWanBlock:
         return X
 
 
-def build_block(P_logical: dict, dim: int, heads: int, device) -> QuantizedWanBlock:
+def build_block(P_logical: dict, dim: int, heads: int, device, cross_attention: str = "sdpa") -> QuantizedWanBlock:
     """A QuantizedWanBlock from the logical parts of oracle-style quantization (tests) or of quantize_block."""
     from wdl.w4a4 import pack_parts
 
@@ -115,7 +127,7 @@ def build_block(P_logical: dict, dim: int, heads: int, device) -> QuantizedWanBl
     parts["n3w"] = P_logical["n3w"].float().to(device)
     parts["n3b"] = P_logical["n3b"].float().to(device)
     parts["modulation"] = P_logical["modulation"].float().to(device)
-    return QuantizedWanBlock(parts, dim, heads)
+    return QuantizedWanBlock(parts, dim, heads, cross_attention=cross_attention)
 
 
 def random_block(dim: int, ffn: int, heads: int, device, generator=None) -> QuantizedWanBlock:

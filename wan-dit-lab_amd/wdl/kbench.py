@@ -1,4 +1,5 @@
-"""Kernel timings at the step's shapes, for profiling runs: `python -m wdl.kbench attention|prep|gemm|quant [lib]`.
+"""Kernel timings at the step's shapes, for profiling runs: `python -m wdl.kbench attention|cross|prep|gemm|quant
+[lib]`.
 
 attention: Sage prep + attention of 1280 and 1392 queries over a full 9744-key window (8352 cached FP8 tokens + the
 chunk), 24 x 128 heads; prep: the Sage preparation (K mean and V maxima, int8 K and fp8 V of the whole window) of
@@ -50,6 +51,27 @@ def attention():
         out = torch.empty(n, H * 128, device=dev, dtype=torch.bfloat16)
         us = _replay_us(lambda: ops.sage_attn_q16_launch(Q, prep, L, 128 ** -0.5, out))
         print(f"attention n={n} L={L}: {us:.1f} us ({4 * n * L * 128 * H / us / 1e6:.0f} TOP/s)", flush=True)
+
+
+def cross():
+    """The cross-attention of the step (1392 queries over 512 prompt keys, 24 x 128 heads): bf16 attention (the
+    reference's SDPA semantics) and Sage (int8 QK, fp8 PV), each over K / V laid out once."""
+    import torch
+
+    from wdl import ops
+
+    dev, H, n, L = "cuda", 24, 1392, 512
+    g = torch.Generator(device=dev).manual_seed(0)
+    Q, K, V = (torch.randn(m, H * 128, device=dev, generator=g).to(torch.bfloat16) for m in (n, L, L))
+    pb = ops.attn_bf16_prep_launch(K, V)
+    out = torch.empty(n, H * 128, device=dev, dtype=torch.bfloat16)
+    us = _replay_us(lambda: ops.attn_bf16_launch(Q, pb, 128 ** -0.5, out))
+    print(f"cross bf16 n={n} L={L}: {us:.1f} us ({4 * n * L * 128 * H / us / 1e6:.0f} TFLOP/s)", flush=True)
+    z8 = torch.zeros(1, 1, H, 128, device=dev, dtype=torch.uint8)
+    one = torch.ones(1, 1, H, 1, device=dev)
+    ps = ops.sage_prep_launch(z8, one, z8, one, K, V, 0)
+    us = _replay_us(lambda: ops.sage_attn_q16_launch(Q, ps, L, 128 ** -0.5, out))
+    print(f"cross sage n={n} L={L}: {us:.1f} us ({4 * n * L * 128 * H / us / 1e6:.0f} TOP/s)", flush=True)
 
 
 def prep():
@@ -115,13 +137,13 @@ def quant():
 
 
 def main(argv):
-    if len(argv) < 2 or argv[1] not in ("attention", "prep", "gemm", "quant"):
-        raise SystemExit("usage: python -m wdl.kbench attention|prep|gemm|quant [library path]")
+    if len(argv) < 2 or argv[1] not in ("attention", "cross", "prep", "gemm", "quant"):
+        raise SystemExit("usage: python -m wdl.kbench attention|cross|prep|gemm|quant [library path]")
     if len(argv) > 2:
         from wdl import _lib
 
         _lib.LIB_PATH = Path(argv[2])
-    {"attention": attention, "prep": prep, "gemm": gemm, "quant": quant}[argv[1]]()
+    {"attention": attention, "cross": cross, "prep": prep, "gemm": gemm, "quant": quant}[argv[1]]()
 
 
 if __name__ == "__main__":

@@ -425,6 +425,34 @@ def sage_attn_q16_launch(Q, prep, L, sm_scale, out=None):
     return out
 
 
+def attn_bf16_prep_launch(K, V):
+    """The keys and values of a bf16 attention (the prompt's, for the cross-attention) in wdl_attn_bf16's layouts:
+    K, V bf16 [L, H*128] (row-strided views allowed) -> dict(kp, vp, L, heads)."""
+    L, C = K.shape
+    if K.dtype != torch.bfloat16 or V.dtype != torch.bfloat16 or V.shape != K.shape or C % 128 or \
+            K.stride(1) != 1 or V.stride(1) != 1:
+        raise ValueError("attn_bf16_prep: K, V must be bf16 [L, heads*128] with unit column stride")
+    H = C // 128
+    n = _lib.library().wdl_attn_bf16_prep_elems(L, H)
+    kp = torch.empty(n, device=K.device, dtype=torch.bfloat16)
+    vp = torch.empty(n, device=K.device, dtype=torch.bfloat16)
+    _lib.call("wdl_attn_bf16_prep", ptr(K), K.stride(0), ptr(V), V.stride(0), L, H, ptr(kp), ptr(vp), stream_of(K))
+    return dict(kp=kp, vp=vp, L=L, heads=H)
+
+
+def attn_bf16_launch(Q, prep, sm_scale, out=None):
+    """Q bf16 [n, H*128] (row-strided) -> bf16 [n, H*128]: exact-softmax bf16 attention over prep's keys."""
+    n, C = Q.shape
+    H = prep["heads"]
+    if Q.dtype != torch.bfloat16 or C != H * 128 or Q.stride(1) != 1:
+        raise ValueError(f"attn_bf16: Q must be bf16 [n, {H * 128}] with unit column stride")
+    if out is None:
+        out = torch.empty(n, C, device=Q.device, dtype=torch.bfloat16)
+    _lib.call("wdl_attn_bf16", ptr(Q), Q.stride(0), ptr(prep["kp"]), ptr(prep["vp"]), n, prep["L"], H,
+              float(sm_scale), ptr(out), out.stride(0), stream_of(Q))
+    return out
+
+
 @torch.library.custom_op("wdl::sage_kv_attend", mutates_args=())
 def sage_kv_attend(Q: torch.Tensor, cache_k: torch.Tensor, cache_ks: torch.Tensor, cache_v: torch.Tensor,
                    cache_vs: torch.Tensor, K: torch.Tensor, V: torch.Tensor, at: int, sm_scale: float) -> torch.Tensor:
