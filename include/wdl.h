@@ -164,6 +164,20 @@ int wdl_qk_norm_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, con
                      const void* freq, int freq_dtype, int64_t positions, int64_t M, int64_t heads, int f, int h,
                      int w, int start_frame, float eps, void* q_out, void* k_out, int64_t ldo, wdl_stream_t stream);
 
+/* The standalone 3D RoPE rotation. Replaces wan_dit_lab::rope3d_rotate (src/wan_dit_lab/kernels/rope_triton.py:14-81)
+ * and rope_apply (rope_triton.py:84-139; models/rope.py:12-31). x: [B, L, H, dim] of type x_dtype (0 fp32, 1 fp16,
+ * 2 bf16, 3 fp64) with element strides x_strides[4]; freq: [2, positions, dim/2] (cos, sin) fp32 or fp64 with
+ * element strides freq_strides[3]; grids: host int32 [B][3] (f, h, w) per sample, 1 <= B <= 64; even dim.
+ * Pair p of token i of sample b (i < f h w) turns by the table's angle at: start + i / (h w) for the first
+ * dim/2 - 2 ((dim/2) / 3) pairs (time), (i / w) % h for the next (dim/2) / 3 (height), i % w for the rest
+ * (width); (e, o) -> (e c - o s, o c + e s), s negated when inverse != 0. Arithmetic in fp64 if x or freq is fp64,
+ * else fp32, each product rounded; fp16 / bf16 results through fp32. Tokens i >= f h w are copied. out: contiguous
+ * [B, L, H, dim] of out_dtype. Grids that exceed L or the table are rejected before the launch. */
+int wdl_rope3d_rotate(const void* x, int x_dtype, const int64_t* x_strides, const void* freq, int freq_dtype,
+                      const int64_t* freq_strides, int64_t positions, int64_t B, int64_t L, int64_t H, int64_t dim,
+                      const int32_t* grids, int64_t start, int inverse, void* out, int out_dtype,
+                      wdl_stream_t stream);
+
 /* Sage per-thread int8 quantization of Q. Replaces sage_kv.quant_q (src/wan_dit_lab/kernels/sage_kv.py:112-124).
  * x: bf16 [n, heads, 128] (token stride ldx); q: int8 [n, heads, 128]; q_scale: fp32 [heads, ceil(n/128)*32].
  * Per 32-token block, tokens l, l+8, l+16, l+24 share scale = max|x| / 127 + 1e-7; q = trunc(x/scale +- 0.5). */
@@ -183,6 +197,17 @@ int wdl_sage_prep(const void* cache_k, const float* cache_ks, const void* cache_
                   int64_t capacity, const void* k, int64_t ldk, const void* v, int64_t ldv, int64_t heads, int64_t at,
                   int64_t n, int splits, float* workspace, void* k_int8, float* k_scale, void* v_fp8,
                   float* k_mean_out, float* v_scale_out, wdl_stream_t stream);
+
+/* wdl_sage_prep with the head and token maps of sage_kv.attend (src/wan_dit_lab/kernels/sage_kv.py:127-134, 137-140;
+ * used by KVCache.attend_split, generation/causal.py:222-241): the cache holds cache_heads >= heads heads; head h of
+ * the call reads cache head heads_map[h] (int32 [heads], device; NULL: h, and then cache_heads == heads); cached
+ * token t < at is cache row tokens_map[t] (int32 [at], device; NULL: t). Neither copies the cache. Map values outside
+ * [0, cache_heads) / [0, capacity) are clamped into the cache by the kernels (the host wrapper rejects them first). */
+int wdl_sage_prep_mapped(const void* cache_k, const float* cache_ks, const void* cache_v, const float* cache_vs,
+                         int64_t capacity, int64_t cache_heads, const int32_t* heads_map, const int32_t* tokens_map,
+                         const void* k, int64_t ldk, const void* v, int64_t ldv, int64_t heads, int64_t at,
+                         int64_t n, int splits, float* workspace, void* k_int8, float* k_scale, void* v_fp8,
+                         float* k_mean_out, float* v_scale_out, wdl_stream_t stream);
 
 /* Workspace (bytes) of wdl_sage_attn for n queries, L keys and `heads` heads. */
 int64_t wdl_sage_attn_workspace_bytes(int64_t n, int64_t L, int64_t heads);

@@ -76,3 +76,38 @@ def rope_complex(x: torch.Tensor, grid, freq: torch.Tensor, start: int = 0) -> t
     even, odd = v[..., 0], v[..., 1]
     rot = torch.stack((even * phase.real - odd * phase.imag, odd * phase.real + even * phase.imag), dim=-1)
     return torch.cat((rot.flatten(-2).to(x.dtype), x[:, n:]), dim=1)
+
+
+def rope_rotate(x: torch.Tensor, grids, freq: torch.Tensor, start: int = 0, inverse: bool = False,
+                out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """The rotation of wan_dit_lab::rope3d_rotate (kernels/rope_triton.py:14-63, 66-81), x [B, L, H, dim] (any
+    strides), one (f, h, w) grid per sample. Pair p of token i rotates by the angle of its axis: time pairs (the
+    first dim/2 - 2 (dim/2 // 3)) at start + i // (h w), height pairs at (i // w) % h, width pairs at i % w;
+    (e, o) -> (e c - o s, o c + e s), with s negated when inverse. Arithmetic in fp64 when x or freq is fp64, else
+    fp32, each product rounded (no fused multiply-add); results for fp16 / bf16 outputs pass through fp32 (torch's
+    own fp64 -> half casts do); tokens i >= f h w are copied."""
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    ct = torch.float64 if torch.float64 in (x.dtype, freq.dtype) else torch.float32
+    B, L, H, dim = x.shape
+    pairs = dim // 2
+    t, s, _ = axis_split(dim)
+    out = torch.empty(B, L, H, dim, dtype=out_dtype)
+    to_out = (lambda v: v.float().to(out_dtype)) if out_dtype in (torch.float16, torch.bfloat16) else \
+        (lambda v: v.to(out_dtype))
+    for b, (f, h, w) in enumerate(grids):
+        n = f * h * w
+        i = torch.arange(n)
+        pos = torch.empty(n, pairs, dtype=torch.long)
+        pos[:, :t] = (start + i // (h * w))[:, None]
+        pos[:, t:t + s] = ((i // w) % h)[:, None]
+        pos[:, t + s:] = (i % w)[:, None]
+        cols = torch.arange(pairs).expand(n, pairs)
+        c = freq[0][pos, cols].to(ct)[:, None, :]
+        sn = freq[1][pos, cols].to(ct)[:, None, :]
+        if inverse:
+            sn = -sn
+        e, o = x[b, :n, :, 0::2].to(ct), x[b, :n, :, 1::2].to(ct)
+        rot = torch.stack((e * c - o * sn, o * c + e * sn), dim=-1).flatten(-2)
+        out[b, :n] = to_out(rot)
+        out[b, n:] = to_out(x[b, n:].to(ct))
+    return out

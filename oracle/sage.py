@@ -35,9 +35,14 @@ V_MAX = 2.25  # sage_kv.py:24
 BLKQ, WARPQ, BLKK = 128, 32, 64  # sage_kv.py:25
 
 
-def gather(cache: torch.Tensor, scale: torch.Tensor, chunk: torch.Tensor, at: int) -> torch.Tensor:
-    """fp32 [B, at + n, H, D]: cache[:, :at] * scale then the chunk (sage_kv.py:28-40)."""
-    c = cache[:, :at].float() * scale[:, :at].float()
+def gather(cache: torch.Tensor, scale: torch.Tensor, chunk: torch.Tensor, at: int, heads=None,
+           tokens=None) -> torch.Tensor:
+    """fp32 [B, at + n, H, D]: the cached tokens times their scales, then the chunk (sage_kv.py:28-40). With the maps
+    of sage_kv.attend (sage_kv.py:127-134): head h is cache head heads[h] (the cache keeps all of them), cached token
+    i is buffer token tokens[i]; without them, cache tokens 0 .. at - 1 and heads 0 .. H - 1."""
+    rows = torch.arange(at) if tokens is None else tokens[:at].long()
+    cols = torch.arange(chunk.shape[2]) if heads is None else heads.long()
+    c = cache[:, rows][:, :, cols].float() * scale[:, rows][:, :, cols].float()
     return torch.cat([c, chunk.float()], dim=1)
 
 
@@ -128,10 +133,10 @@ def wdl_v_layout(v_fp8: torch.Tensor) -> torch.Tensor:
     return raw.view(torch.float8_e4m3fn)
 
 
-def prep(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V):
+def prep(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, heads=None, tokens=None):
     """All quantized operands of one attend call."""
-    Kf = gather(cache_k, cache_ks, K, at)
-    Vf = gather(cache_v, cache_vs, V, at)
+    Kf = gather(cache_k, cache_ks, K, at, heads, tokens)
+    Vf = gather(cache_v, cache_vs, V, at, heads, tokens)
     k_mean, v_scale = colstats(Kf, Vf)
     k_i8, k_scale = quant_k(Kf, k_mean)
     v_fp8 = quant_v(Vf, v_scale)

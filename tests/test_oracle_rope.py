@@ -97,3 +97,39 @@ def test_host_rope_tables_and_rope_at_known_answers():
     assert torch.equal(wrope.rope_at(1024, 42, 1.0), wrope.rope(1024, 42))
     assert torch.allclose(wrope.rope_at(64, 42, 1.5)[:, 2], wrope.rope(64, 42)[:, 3])
     assert torch.equal(wrope.freqs(128, 64), frequencies(128, 64).float())
+
+
+def test_general_rotation_equals_the_complex_oracle_per_sample():
+    """rope_rotate (the op's general form: per-sample grids, padding, any dim) against the fp64 complex-phase
+    oracle of the reference's tests (test_rope_triton.py:21-45) on fp64 inputs: equal to the last bit, since both
+    compute e c - o s, o c + e s in fp64."""
+    g = torch.Generator().manual_seed(3)
+    for dim in (2, 6, 12, 128):
+        freq = orope.freqs(dim, 64)
+        x = torch.randn(2, 33, 3, dim, generator=g, dtype=torch.float64)
+        grids = ((2, 3, 5), (1, 2, 4))
+        got = orope.rope_rotate(x, grids, freq, 3)
+        for b, grid in enumerate(grids):
+            assert torch.equal(got[b:b + 1], orope.rope_complex(x[b:b + 1], grid, freq, 3))
+
+
+def test_inverse_undoes_the_rotation_and_half_outputs_round_through_fp32():
+    g = torch.Generator().manual_seed(4)
+    freq = orope.freqs(128, 64)
+    x = torch.randn(1, 30, 2, 128, generator=g, dtype=torch.float64)
+    back = orope.rope_rotate(orope.rope_rotate(x, ((2, 3, 5),), freq, 7), ((2, 3, 5),), freq, 7, inverse=True)
+    assert float((back - x).abs().max()) < 1e-14
+    fwd = orope.rope_rotate(x, ((2, 3, 5),), freq, 7)
+    assert not torch.equal(orope.rope_rotate(x, ((2, 3, 5),), freq, 7, inverse=True), fwd)
+    half = orope.rope_rotate(x, ((2, 3, 5),), freq, 7, out_dtype=torch.bfloat16)
+    assert torch.equal(half, fwd.float().to(torch.bfloat16))
+    # fp32 inputs with fp32 tables: fp32 products, each rounded
+    x32, f32 = x.float(), freq.float()
+    r32 = orope.rope_rotate(x32, ((2, 3, 5),), f32, 7)
+    e, o = x32[0, :30, :, 0::2], x32[0, :30, :, 1::2]
+    pos = orope.positions((2, 3, 5), 7)
+    t, s, _ = orope.axis_split(128)
+    col = torch.cat([pos[:, :1].expand(30, t), pos[:, 1:2].expand(30, s), pos[:, 2:3].expand(30, s)], 1)
+    c = f32[0][col, torch.arange(64)][:, None]
+    sn = f32[1][col, torch.arange(64)][:, None]
+    assert torch.equal(r32[0, :, :, 0::2], e * c - o * sn) and torch.equal(r32[0, :, :, 1::2], o * c + e * sn)

@@ -21,11 +21,23 @@ using namespace wdl;
 constexpr int D = 128;
 
 struct Src {
-    const uint8_t* cache;   // [cap, H, D] e4m3
-    const float* cscale;    // [cap, H]
+    const uint8_t* cache;   // [cap, Hc, D] e4m3
+    const float* cscale;    // [cap, Hc]
     const uint16_t* chunk;  // bf16, token stride ld, head stride D
     int64_t ld;
+    int64_t Hc, cap;        // heads and rows of the cache
+    const int32_t* hmap;    // head h of the call reads cache head hmap[h] (null: h)
+    const int32_t* tmap;    // cached token t is cache row tmap[t] (null: t)
 };
+
+// cache row index (token row * Hc + head) of cached token t of head h; mapped indices are clamped into the cache
+// (the host checks the maps' ranges; the clamp keeps every access inside the buffers whatever they hold)
+__device__ __forceinline__ int64_t cache_row(const Src& s, int64_t t, int64_t h) {
+    int64_t ct = t, ch = h;
+    if (s.tmap) ct = min(max(int64_t(s.tmap[t]), int64_t(0)), s.cap - 1);
+    if (s.hmap) ch = min(max(int64_t(s.hmap[h]), int64_t(0)), s.Hc - 1);
+    return ct * s.Hc + ch;
+}
 
 // 8 channels d0 .. d0 + 7 of token t (head h) as floats: cached tokens from e4m3 times their row scale, chunk
 // tokens from bf16, tokens >= L zero. CACHE / CHUNK: the caller knows the token's source (uniform paths).
@@ -34,8 +46,9 @@ template <int SRC>
 __device__ __forceinline__ void load_token8(const Src& s, int64_t t, int64_t h, int64_t H, int64_t at, int64_t L,
                                             int d0, float* f) {
     if (SRC == CACHE || (SRC == MIXED && t < at)) {
-        const uint2 raw = *reinterpret_cast<const uint2*>(s.cache + (t * H + h) * D + d0);
-        const float sc = s.cscale[t * H + h];
+        const int64_t row = cache_row(s, t, h);
+        const uint2 raw = *reinterpret_cast<const uint2*>(s.cache + row * D + d0);
+        const float sc = s.cscale[row];
         e4m3x4_to_f32(raw.x, f);
         e4m3x4_to_f32(raw.y, f + 4);
 #pragma unroll
@@ -151,9 +164,10 @@ __device__ __forceinline__ int v_position(int t) { return 32 * ((t % 8) / 4) + 4
 // loads and one scale load (the values and products of four load_token8<CACHE> calls)
 __device__ __forceinline__ void load_cached32(const Src& s, int64_t t, int64_t h, int64_t H, int d0,
                                               float (&f)[4][8]) {
-    const uint4* src = reinterpret_cast<const uint4*>(s.cache + (t * H + h) * D + d0);
+    const int64_t row = cache_row(s, t, h);
+    const uint4* src = reinterpret_cast<const uint4*>(s.cache + row * D + d0);
     const uint4 r0 = src[0], r1 = src[1];
-    const float sc = s.cscale[t * H + h];
+    const float sc = s.cscale[row];
     const uint32_t w[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -283,12 +297,14 @@ __global__ __launch_bounds__(256) void quant_kv_kernel(Src k, Src v, int64_t H, 
 // workspace floats: 2 * S * H * 128 (partials) + 2 * H * 128 (k_mean, v_scale)
 extern "C" int64_t wdl_sage_prep_workspace_floats(int64_t heads, int splits) { return (2 * splits + 2) * heads * D; }
 
-extern "C" int wdl_sage_prep(const void* cache_k, const float* cache_ks, const void* cache_v, const float* cache_vs,
-                             int64_t capacity, const void* k, int64_t ldk, const void* v, int64_t ldv, int64_t heads,
-                             int64_t at, int64_t n, int splits, float* workspace, void* k_int8, float* k_scale,
-                             void* v_fp8, float* k_mean_out, float* v_scale_out, hipStream_t stream) {
+static int sage_prep_launch(const void* cache_k, const float* cache_ks, const void* cache_v, const float* cache_vs,
+                            int64_t capacity, int64_t cache_heads, const int32_t* heads_map,
+                            const int32_t* tokens_map, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                            int64_t heads, int64_t at, int64_t n, int splits, float* workspace, void* k_int8,
+                            float* k_scale, void* v_fp8, float* k_mean_out, float* v_scale_out, hipStream_t stream) {
     const int64_t L = at + n;
-    if (at < 0 || n < 0 || heads <= 0 || at > capacity || splits < 1 || ldk < heads * D || ldv < heads * D)
+    if (at < 0 || n < 0 || heads <= 0 || at > capacity || splits < 1 || ldk < heads * D || ldv < heads * D ||
+        cache_heads < heads || (!heads_map && cache_heads != heads))
         return fail(WDL_EINVAL, "sage_prep: bad shape");
     if (!cache_k || !cache_ks || !cache_v || !cache_vs || !k || !v || !workspace || !k_int8 || !k_scale || !v_fp8)
         return fail(WDL_EINVAL, "sage_prep: null pointer");
@@ -297,9 +313,12 @@ extern "C" int wdl_sage_prep(const void* cache_k, const float* cache_ks, const v
     if ((reinterpret_cast<uintptr_t>(cache_k) | reinterpret_cast<uintptr_t>(cache_v)) % 16)
         return fail(WDL_EINVAL, "sage_prep: the caches must be 16-byte aligned");
     if (L == 0) return WDL_OK;
+    if (capacity < 1) return fail(WDL_EINVAL, "sage_prep: empty cache");
     const int64_t Lpad = (L + 63) / 64 * 64;
-    Src sk{static_cast<const uint8_t*>(cache_k), cache_ks, static_cast<const uint16_t*>(k), ldk};
-    Src sv{static_cast<const uint8_t*>(cache_v), cache_vs, static_cast<const uint16_t*>(v), ldv};
+    Src sk{static_cast<const uint8_t*>(cache_k), cache_ks, static_cast<const uint16_t*>(k), ldk, cache_heads,
+           capacity, heads_map, tokens_map};
+    Src sv{static_cast<const uint8_t*>(cache_v), cache_vs, static_cast<const uint16_t*>(v), ldv, cache_heads,
+           capacity, heads_map, tokens_map};
     float* part_k = workspace;
     float* part_v = workspace + int64_t(splits) * heads * D;
     float* k_mean = k_mean_out ? k_mean_out : workspace + 2 * int64_t(splits) * heads * D;
@@ -315,4 +334,23 @@ extern "C" int wdl_sage_prep(const void* cache_k, const float* cache_ks, const v
         sk, sv, heads, at, L, Lpad, k_mean, v_scale, static_cast<int8_t*>(k_int8), k_scale,
         static_cast<uint8_t*>(v_fp8));
     return check_launch("sage_prep quant_kv");
+}
+
+extern "C" int wdl_sage_prep(const void* cache_k, const float* cache_ks, const void* cache_v, const float* cache_vs,
+                             int64_t capacity, const void* k, int64_t ldk, const void* v, int64_t ldv, int64_t heads,
+                             int64_t at, int64_t n, int splits, float* workspace, void* k_int8, float* k_scale,
+                             void* v_fp8, float* k_mean_out, float* v_scale_out, hipStream_t stream) {
+    return sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, capacity, heads, nullptr, nullptr, k, ldk, v, ldv,
+                            heads, at, n, splits, workspace, k_int8, k_scale, v_fp8, k_mean_out, v_scale_out, stream);
+}
+
+extern "C" int wdl_sage_prep_mapped(const void* cache_k, const float* cache_ks, const void* cache_v,
+                                    const float* cache_vs, int64_t capacity, int64_t cache_heads,
+                                    const int32_t* heads_map, const int32_t* tokens_map, const void* k, int64_t ldk,
+                                    const void* v, int64_t ldv, int64_t heads, int64_t at, int64_t n, int splits,
+                                    float* workspace, void* k_int8, float* k_scale, void* v_fp8, float* k_mean_out,
+                                    float* v_scale_out, hipStream_t stream) {
+    return sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, capacity, cache_heads, heads_map, tokens_map, k,
+                            ldk, v, ldv, heads, at, n, splits, workspace, k_int8, k_scale, v_fp8, k_mean_out,
+                            v_scale_out, stream);
 }

@@ -16,6 +16,7 @@ c_int = ctypes.c_int
 c_ptr = ctypes.c_void_p
 c_f32 = ctypes.c_float
 c_i64p = ctypes.POINTER(ctypes.c_int64)
+c_i32p = ctypes.POINTER(ctypes.c_int32)
 
 # name -> argtypes, in the order of include/wdl.h
 SIGNATURES: dict[str, list] = {
@@ -44,11 +45,15 @@ SIGNATURES: dict[str, list] = {
     "wdl_sage_prep_workspace_floats": [c_i64, c_int],
     "wdl_sage_prep": [c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_i64, c_i64, c_i64, c_i64, c_int,
                       c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr],
+    "wdl_sage_prep_mapped": [c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_i64, c_i64,
+                             c_i64, c_i64, c_int, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr],
     "wdl_sage_attn_workspace_bytes": [c_i64, c_i64, c_i64],
     "wdl_sage_attn": [c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_f32, c_ptr, c_i64,
                       c_ptr, c_ptr],
     "wdl_sage_attn_q16": [c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_f32, c_ptr, c_i64,
                           c_ptr, c_ptr],
+    "wdl_rope3d_rotate": [c_ptr, c_int, c_i64p, c_ptr, c_int, c_i64p, c_i64, c_i64, c_i64, c_i64, c_i64, c_i32p,
+                          c_i64, c_int, c_ptr, c_int, c_ptr],
     "wdl_attn_bf16_prep_elems": [c_i64, c_i64],
     "wdl_attn_bf16_prep": [c_ptr, c_i64, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr],
     "wdl_attn_bf16": [c_ptr, c_i64, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_f32, c_ptr, c_i64, c_ptr],
@@ -91,3 +96,7 @@ def call(name: str, *args) -> None:
 
 def i64s(values) -> ctypes.Array:
     return (ctypes.c_int64 * len(values))(*[int(v) for v in values])
+
+
+def i32s(values) -> ctypes.Array:
+    return (ctypes.c_int32 * len(values))(*[int(v) for v in values])

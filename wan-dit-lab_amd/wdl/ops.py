@@ -335,12 +335,14 @@ def quant_q_launch(x, heads):
 SPLITS = 32
 
 
-def sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, k, v, at, want_stats=False):
-    """Cache (fp8 [1, cap, H, 128] + fp32 scales [1, cap, H, 1]) tokens [0, at) and the chunk k, v
+def sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, k, v, at, want_stats=False, heads=None, tokens=None):
+    """Cache (fp8 [1, cap, Hc, 128] + fp32 scales [1, cap, Hc, 1]) tokens [0, at) and the chunk k, v
     (bf16 [n, H*128] row-strided) -> k_int8 [H, Lpad, 128], k_scale [H, Lpad/16], v_fp8 [H, 128, Lpad],
-    v_scale [H, 128] (and k_mean when want_stats)."""
+    v_scale [H, 128] (and k_mean when want_stats). heads (int32 [H], device): head h reads cache head heads[h];
+    tokens (int32 [>= at], device): cached token i is cache row tokens[i]; without them Hc = H and rows 0 .. at-1."""
     n = k.shape[0]
-    H = cache_k.shape[2]
+    H = k.shape[1] // 128
+    Hc = cache_k.shape[2]
     L = at + n
     Lp = (L + 63) // 64 * 64
     dev = k.device
@@ -350,9 +352,14 @@ def sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, k, v, at, want_stats=
     v_f8 = torch.empty(H, 128, Lp, device=dev, dtype=torch.uint8)
     k_mean = torch.empty(H, 128, device=dev, dtype=torch.float32)
     v_sc = torch.empty(H, 128, device=dev, dtype=torch.float32)
-    _lib.call("wdl_sage_prep", ptr(cache_k), ptr(cache_ks), ptr(cache_v), ptr(cache_vs), cache_k.shape[1], ptr(k),
-              k.stride(0), ptr(v), v.stride(0), H, at, n, SPLITS, ptr(ws), ptr(k_i8), ptr(k_sc), ptr(v_f8),
-              ptr(k_mean), ptr(v_sc), stream_of(k))
+    if heads is None and tokens is None:
+        _lib.call("wdl_sage_prep", ptr(cache_k), ptr(cache_ks), ptr(cache_v), ptr(cache_vs), cache_k.shape[1],
+                  ptr(k), k.stride(0), ptr(v), v.stride(0), H, at, n, SPLITS, ptr(ws), ptr(k_i8), ptr(k_sc),
+                  ptr(v_f8), ptr(k_mean), ptr(v_sc), stream_of(k))
+    else:
+        _lib.call("wdl_sage_prep_mapped", ptr(cache_k), ptr(cache_ks), ptr(cache_v), ptr(cache_vs),
+                  cache_k.shape[1], Hc, ptr(heads), ptr(tokens), ptr(k), k.stride(0), ptr(v), v.stride(0), H, at, n,
+                  SPLITS, ptr(ws), ptr(k_i8), ptr(k_sc), ptr(v_f8), ptr(k_mean), ptr(v_sc), stream_of(k))
     out = dict(k=k_i8, k_scale=k_sc, v=v_f8, v_scale=v_sc)
     if want_stats:
         out["k_mean"] = k_mean
@@ -440,32 +447,70 @@ def attn_bf16_prep_launch(K, V):
     return dict(kp=kp, vp=vp, L=L, heads=H)
 
 
+def _attn_bf16_into(Q, kp, vp, L, H, sm_scale, out):
+    _lib.call("wdl_attn_bf16", ptr(Q), Q.stride(0), ptr(kp), ptr(vp), Q.shape[0], L, H, float(sm_scale), ptr(out),
+              out.stride(0), stream_of(Q))
+    return out
+
+
+@torch.library.custom_op("wdl::attn_bf16", mutates_args=())
+def attn_bf16(q: torch.Tensor, kp: torch.Tensor, vp: torch.Tensor, keys: int, sm_scale: float) -> torch.Tensor:
+    """softmax(q K^T sm_scale) V in bf16 with an fp32 softmax (the reference's SDPA on bf16 operands) for q bf16
+    [n, H*128] over the `keys` keys laid out by attn_bf16_prep_launch (kp, vp) -> bf16 [n, H*128]."""
+    out = torch.empty(q.shape, device=q.device, dtype=torch.bfloat16)
+    return _attn_bf16_into(q, kp, vp, keys, q.shape[1] // 128, sm_scale, out)
+
+
+@attn_bf16.register_fake
+def _(q, kp, vp, keys, sm_scale):
+    return q.new_empty(q.shape, dtype=torch.bfloat16)
+
+
 def attn_bf16_launch(Q, prep, sm_scale, out=None):
-    """Q bf16 [n, H*128] (row-strided) -> bf16 [n, H*128]: exact-softmax bf16 attention over prep's keys."""
+    """Q bf16 [n, H*128] (row-strided) -> bf16 [n, H*128]: exact-softmax bf16 attention over prep's keys (into
+    `out` when given: a row-strided [n, H*128] view)."""
     n, C = Q.shape
     H = prep["heads"]
     if Q.dtype != torch.bfloat16 or C != H * 128 or Q.stride(1) != 1:
         raise ValueError(f"attn_bf16: Q must be bf16 [n, {H * 128}] with unit column stride")
     if out is None:
-        out = torch.empty(n, C, device=Q.device, dtype=torch.bfloat16)
-    _lib.call("wdl_attn_bf16", ptr(Q), Q.stride(0), ptr(prep["kp"]), ptr(prep["vp"]), n, prep["L"], H,
-              float(sm_scale), ptr(out), out.stride(0), stream_of(Q))
-    return out
+        return attn_bf16(Q, prep["kp"], prep["vp"], prep["L"], float(sm_scale))
+    return _attn_bf16_into(Q, prep["kp"], prep["vp"], prep["L"], H, sm_scale, out)
 
 
 @torch.library.custom_op("wdl::sage_kv_attend", mutates_args=())
 def sage_kv_attend(Q: torch.Tensor, cache_k: torch.Tensor, cache_ks: torch.Tensor, cache_v: torch.Tensor,
-                   cache_vs: torch.Tensor, K: torch.Tensor, V: torch.Tensor, at: int, sm_scale: float) -> torch.Tensor:
-    """wan_dit_lab::sage_kv_attend (src/wan_dit_lab/kernels/sage_kv.py:137-176) without the head/token maps:
-    Q [1, nq, H, 128], K, V [1, n, H, 128] bf16 (row-strided token dim allowed), cache fp8 [1, cap, H, 128] with
-    fp32 scales [1, cap, H, 1] -> [1, nq, H, 128] bf16."""
+                   cache_vs: torch.Tensor, K: torch.Tensor, V: torch.Tensor, at: int, sm_scale: float,
+                   heads: torch.Tensor | None = None, tokens: torch.Tensor | None = None) -> torch.Tensor:
+    """wan_dit_lab::sage_kv_attend (src/wan_dit_lab/kernels/sage_kv.py:137-176): Q [1, nq, H, 128], K, V
+    [1, n, H, 128] bf16 (row-strided token dim allowed), cache fp8 (as uint8) [1, cap, Hc, 128] with fp32 scales
+    [1, cap, Hc, 1] -> [1, nq, H, 128] bf16. heads (int32 [H]): head h is cache head heads[h]; tokens (int32 [at]):
+    cached token i is cache row tokens[i] (neither copies the cache)."""
     _, nq, H, D = Q.shape
     n = K.shape[1]
     prep = sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, K[0].reshape(n, H * D) if K.is_contiguous() else
-                            K[0].flatten(1), V[0].flatten(1), at)
+                            K[0].flatten(1), V[0].flatten(1), at, heads=heads, tokens=tokens)
     return sage_attn_q16_launch(Q[0].flatten(1), prep, at + n, sm_scale).view(1, nq, H, D)
 
 
 @sage_kv_attend.register_fake
-def _(Q, cache_k, cache_ks, cache_v, cache_vs, K, V, at, sm_scale):
+def _(Q, cache_k, cache_ks, cache_v, cache_vs, K, V, at, sm_scale, heads=None, tokens=None):
     return Q.new_empty(Q.shape, dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("wdl::sage_attn", mutates_args=())
+def sage_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_scale: torch.Tensor, k_scale: torch.Tensor,
+              v_scale: torch.Tensor, sm_scale: float, keys: int) -> torch.Tensor:
+    """The Sage kernel alone, the counterpart of live::sage_sm89(q, k, v, q_scale, k_scale, v_scale, sm_scale)
+    (native/ops/sage_ops.cpp:12-19, 28-31) on wdl's operand layouts: q int8 [1, n, H, 128] with q_scale fp32
+    [1, H, ceil(n/128)*32] (wdl.sage_kv.quant_q), k int8 [H, Lpad, 128] with k_scale [H, Lpad/16], v fp8 (as uint8)
+    [H, 128, Lpad], v_scale [H, 128] (wdl.sage_kv.prep); `keys` = L, the unpadded key count (wdl's K and V are
+    padded to 64-key blocks) -> [1, n, H, 128] bf16."""
+    _, n, H, D = q.shape
+    prep = dict(k=k, k_scale=k_scale, v=v, v_scale=v_scale)
+    return sage_attn_launch(q[0], q_scale[0], prep, keys, sm_scale).view(1, n, H, D)
+
+
+@sage_attn.register_fake
+def _(q, k, v, q_scale, k_scale, v_scale, sm_scale, keys):
+    return q.new_empty(q.shape, dtype=torch.bfloat16)

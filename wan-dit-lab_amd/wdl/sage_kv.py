@@ -2,7 +2,7 @@
 
 Tokens [0, at) come from the FP8 cache (value * per-row scale), [at, at + n) from the chunk's own bf16 K, V; the
 K mean, int8 K, fp8 V (wdl_sage_prep), int8 Q (wdl_quant_q) and the attention (wdl_sage_attn) are HIP kernels.
-The head/token maps of the reference (Forcing-KV, sage_kv.py:127-134) are not part of this hot path.
+The head/token maps of the reference (Forcing-KV, sage_kv.py:127-134) select cache heads and rows in place.
 """
 
 from __future__ import annotations
@@ -17,18 +17,26 @@ BLKQ, WARPQ, BLKK = 128, 32, 64
 __all__ = ["V_MAX", "attend", "quant_q", "prep"]
 
 
-def _check(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V):
+def _check(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, heads=None, tokens=None):
     if Q.ndim != 4 or K.ndim != 4 or V.shape != K.shape or Q.shape[0] != 1 or Q.shape[-1] != 128:
         raise ValueError("Q, K, V must be [1, tokens, heads, 128]")
-    if Q.shape[2] != K.shape[2] or cache_k.shape[2] != K.shape[2]:
+    if Q.shape[2] != K.shape[2] or (heads is None and cache_k.shape[2] != K.shape[2]):
         raise ValueError("head counts differ")
+    for name, m, count, bound in (("heads", heads, K.shape[2], cache_k.shape[2]),
+                                  ("tokens", tokens, at, cache_k.shape[1])):
+        if m is None:
+            continue
+        if m.dtype != torch.int32 or m.ndim != 1 or m.shape[0] < count or m.device != cache_k.device:
+            raise ValueError(f"{name} must be an int32 vector of at least {count} entries on the cache's device")
+        if count and (int(m[:count].min()) < 0 or int(m[:count].max()) >= bound):
+            raise ValueError(f"{name} maps outside the cache (0 .. {bound - 1})")
     if cache_k.dtype != torch.float8_e4m3fn or cache_v.dtype != torch.float8_e4m3fn:
         raise TypeError("cache values must be FP8 E4M3FN")
     if cache_ks.dtype != torch.float32 or cache_vs.dtype != torch.float32:
         raise TypeError("cache scales must be FP32")
     if Q.dtype != torch.bfloat16 or K.dtype != torch.bfloat16 or V.dtype != torch.bfloat16:
         raise TypeError("Q, K, V must be bf16")
-    H = K.shape[2]
+    H = K.shape[2] if heads is None else cache_k.shape[2]
     if cache_k.ndim != 4 or cache_k.shape[0] != 1 or cache_k.shape[2:] != (H, 128) or cache_v.shape != cache_k.shape:
         raise ValueError("cache_k / cache_v must be [1, capacity, heads, 128] (batch 1)")
     if cache_ks.shape != (*cache_k.shape[:3], 1) or cache_vs.shape != cache_ks.shape:
@@ -42,14 +50,13 @@ def _check(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V):
 
 
 def attend(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, sm_scale=None, heads=None, tokens=None):
-    """softmax(Q K^T * sm_scale) V over the cached tokens [0, at) and the chunk (sage_kv.py:127-134);
-    [1, nq, H, 128] bf16 (sm_scale defaults to 128^-0.5). The head and token maps of the static-head path
-    (KVCache.attend_split, causal.py:222-) are not implemented: passing them raises NotImplementedError."""
-    if heads is not None or tokens is not None:
-        raise NotImplementedError("head / token maps (static-head Forcing-KV attention) are not implemented")
-    _check(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V)
+    """softmax(Q K^T * sm_scale) V over the cached tokens and the chunk (sage_kv.py:127-134); [1, nq, H, 128] bf16
+    (sm_scale defaults to 128^-0.5). heads (int32 [H]): head h of Q, K, V is cache head heads[h], the cache keeping
+    all of them; tokens (int32 [at]): cached token i is cache row tokens[i] (KVCache.attend_split's static heads,
+    causal.py:222-241). Neither copies the cache. The maps' ranges are checked on the host (one synchronisation)."""
+    _check(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, heads, tokens)
     return sage_kv_attend(Q, cache_k.view(torch.uint8), cache_ks, cache_v.view(torch.uint8), cache_vs, K, V, at,
-                          Q.shape[-1] ** -0.5 if sm_scale is None else float(sm_scale))
+                          Q.shape[-1] ** -0.5 if sm_scale is None else float(sm_scale), heads, tokens)
 
 
 def quant_q(Q):
