@@ -71,6 +71,12 @@ def test_sage_attn_operator_is_the_kernel_of_sage_kv_attend(gpu):
     p = sage_kv.prep(k, ks, v, vs, at, K, V)
     out = torch.ops.wdl.sage_attn(q, p["k"], p["v"], qs, p["k_scale"], p["v_scale"], 128 ** -0.5, at + K.shape[1])
     assert torch.equal(out, sage_kv.attend(Q, k, ks, v, vs, at, K, V))
+    # the reference's schema (live::sage_sm89): the key count from the views' shapes
+    import wdl.live  # noqa: F401
+
+    L = at + K.shape[1]
+    sm = torch.ops.live.sage_sm89(q, p["k"][:, :L], p["v"][:, :, :L], qs, p["k_scale"], p["v_scale"], 128 ** -0.5)
+    assert torch.equal(sm, out)
 
 
 def _compiled_and_captured(fn, check):

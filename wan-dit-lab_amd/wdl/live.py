@@ -6,9 +6,10 @@ The reference registers `live::w4a4_linear` and `live::w4a4_gelu_mlp` from Nunch
 names and schemas over wdl's HIP kernels, so those call sites run unchanged on MI355X, given weights packed
 by wdl.w4a4.quantize (wdl's layout; Nunchaku's tile order is not reproduced).
 
-`live::sage_sm89` is not aliased: its operands are laid out for SageAttention's sm89 kernel. The attention swap
-point is one level up, `sage_kv.attend` / `KVCache.attend` (kernels/sage_kv.py:127-134; generation/causal.py:193-
-220), whose replacement is wdl.sage_kv.attend / wdl.kvcache.KVCache.attend (see load()).
+`live::sage_sm89` takes the reference's argument list over wdl's operand layouts (wdl.sage_kv.quant_q / prep, the
+keys and values as [H, L, 128] / [H, 128, L] views of the padded buffers); SageAttention's own sm89 layouts are not
+reproduced. The usual attention swap point is one level up, `sage_kv.attend` / `KVCache.attend`
+(kernels/sage_kv.py:127-134; generation/causal.py:193-220), replaced by wdl.sage_kv.attend / wdl.kvcache.KVCache.
 """
 
 from __future__ import annotations
@@ -17,7 +18,7 @@ import torch
 
 from wdl import ops
 
-__all__ = ["load", "w4a4_linear", "w4a4_gelu_mlp"]
+__all__ = ["load", "w4a4_linear", "w4a4_gelu_mlp", "sage_sm89"]
 
 
 @torch.library.custom_op("live::w4a4_linear", mutates_args=())
@@ -46,6 +47,18 @@ def w4a4_gelu_mlp(x: torch.Tensor, qweight1: torch.Tensor, wscales1: torch.Tenso
 def _(x, qweight1, wscales1, proj_down1, proj_up1, smooth1, bias1, qweight2, wscales2, proj_down2, proj_up2,
       smooth2, bias2):
     return x.new_empty(x.shape[0], ops.out_features(qweight2), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("live::sage_sm89", mutates_args=())
+def sage_sm89(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_scale: torch.Tensor, k_scale: torch.Tensor,
+              v_scale: torch.Tensor, sm_scale: float) -> torch.Tensor:
+    """live::sage_sm89 (sage_ops.cpp:12-19, 28-31) on libwdl (wdl's layouts, see the module docstring)."""
+    return ops.sage_sm89(q, k, v, q_scale, k_scale, v_scale, sm_scale)
+
+
+@sage_sm89.register_fake
+def _(q, k, v, q_scale, k_scale, v_scale, sm_scale):
+    return q.new_empty(q.shape, dtype=torch.bfloat16)
 
 
 def load():

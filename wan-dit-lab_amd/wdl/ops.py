@@ -514,3 +514,25 @@ def sage_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_scale: torch.
 @sage_attn.register_fake
 def _(q, k, v, q_scale, k_scale, v_scale, sm_scale, keys):
     return q.new_empty(q.shape, dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("wdl::sage_sm89", mutates_args=())
+def sage_sm89(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_scale: torch.Tensor, k_scale: torch.Tensor,
+              v_scale: torch.Tensor, sm_scale: float) -> torch.Tensor:
+    """live::sage_sm89's schema (native/ops/sage_ops.cpp:28-31) on wdl's layouts, the key count in the shapes: k the
+    [H, L, 128] view of the padded int8 keys (k_int8[:, :L]), v the [H, 128, L] view of the fp8 values
+    (v_fp8[:, :, :L]); q, q_scale, k_scale, v_scale as wdl::sage_attn takes them."""
+    H, L, D = k.shape
+    Lpad = (L + 63) // 64 * 64  # the kernel's row pitch for L keys: the views must come from buffers of that pitch
+    if k.stride(1) != D or k.stride(2) != 1 or k.stride(0) != Lpad * D or v.stride(2) != 1 or v.stride(1) != Lpad \
+            or v.shape != (H, D, L):
+        raise ValueError("sage_sm89: k must be a [H, L, 128] view of wdl's [H, Lpad, 128] keys and v the matching "
+                         "[H, 128, L] view of the [H, 128, Lpad] values")
+    _, n, _, _ = q.shape
+    prep = dict(k=k, k_scale=k_scale, v=v, v_scale=v_scale)
+    return sage_attn_launch(q[0], q_scale[0], prep, L, sm_scale).view(1, n, H, D)
+
+
+@sage_sm89.register_fake
+def _(q, k, v, q_scale, k_scale, v_scale, sm_scale):
+    return q.new_empty(q.shape, dtype=torch.bfloat16)
