@@ -136,8 +136,11 @@ def test_w4a4_block_stays_close_to_the_float_block(gpu):
     assert err <= 1.05 * oerr and err < 0.21
 
 
-def test_config1_stages_given_identical_inputs(gpu):
-    """Each stage of the config-1 block on the HIP path, fed the oracle's own input for that stage."""
+@pytest.mark.parametrize("M,prior,grid,start", [(464, 928, (1, 16, 29), 2), (1392, 8352, (3, 16, 29), 18)])
+def test_block_stages_given_identical_inputs(gpu, M, prior, grid, start):
+    """Each stage of the full-width block on the HIP path, fed the oracle's own input for that stage: one frame over
+    two cached frames (464 over 928 keys), and the step's chunk of three frames over the full window (1392 over
+    8352 + 1392 keys)."""
     from oracle import norms as onorms
     from oracle import sage as osage
     from oracle import w4a4 as ow
@@ -145,7 +148,7 @@ def test_config1_stages_given_identical_inputs(gpu):
     from wdl.block import build_block
 
     dev = torch.device("cuda")
-    dim, heads, ffn, M, prior, grid, start = 3072, 24, 14336, 464, 928, (1, 16, 29), 2
+    dim, heads, ffn = 3072, 24, 14336
     g = torch.Generator().manual_seed(7)
     P = oblock.random_logical_block(dim, ffn, g)
     X = torch.randn(M, dim, generator=g).to(BF)

@@ -1,0 +1,201 @@
+"""The benchmark workloads at their exact shapes, on the HIP path against the oracle:
+
+- the GEMM sweep: every W4A4 shape of a block (QKV 3072 -> 9216, o 3072 -> 3072, FFN-up 3072 -> 14336, FFN-down
+  14336 -> 3072) at 1392 and 2640 tokens, weights N(0, 0.02^2) quantized by the max rule, activations N(0, 1) with 1%
+  outlier channels x 20 quantized per token and 64-group, through the launches the library picks (stream-K for
+  FFN-down at 1392 tokens); the same eight shapes as FP8 linears (per-row scales, the reference's rows mode);
+- the chunk attention: 24 heads, 2640 queries (3 latent frames of 22 x 40), 2640 / 9240 / 18480 keys (the chunk
+  alone, and 6600 / 15840 FP8-cached keys), K with a per-channel bias N(0, 3^2), the chunk's Q and K rotated by the 3D
+  RoPE at its start frame; the full 24-head launch, two heads checked against the oracle (its CPU cost);
+- the DiT step's block: 1392 tokens over 8352 cached FP8 keys + the chunk (9744) and 512 prompt tokens against the
+  oracle block; the 30-block step on latents through its graph, checked for finite output, replay == eager bit for
+  bit, and the chunk's keys and values written to cache rows 8352 .. 9743.
+
+Bars are those of the per-kernel tests, stated at each check."""
+
+import pytest
+import torch
+
+from oracle import block as oblock
+from oracle import fp8 as ofp8
+from oracle import rope as orope
+from oracle import sage as osage
+from oracle import w4a4 as ow
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+SHAPES = [("qkv", 9216, 3072), ("o", 3072, 3072), ("up", 14336, 3072), ("down", 3072, 14336)]
+
+
+def activations(M, K, g):
+    x = torch.randn(M, K, generator=g)
+    x[:, torch.randperm(K, generator=g)[: K // 100]] *= 20
+    return x.to(BF)
+
+
+@pytest.mark.parametrize("M", [1392, 2640])
+@pytest.mark.parametrize("name,N,K", SHAPES)
+def test_w4a4_linear_sweep(gpu, name, N, K, M):
+    """Quantizer + GEMM (low-rank branch, bias) as the product runs them against the oracle's linear: the int4
+    activations and their scales bit-exact; the fp32 result within the fold's rounding bound, element by element:
+    each of the K/64 group steps rounds once (the scale product is exact), by at most 2^-24 of a partial sum that
+    is bounded by the absolute sum A = sum_g |as ws I_g| + |low-rank| + |bias| (computed by the oracle from |q|):
+    |y - oracle| <= (K/64 + 2) 2^-23 A; the bf16 result one bf16 rounding from the oracle on top."""
+    from wdl import ops, w4a4
+
+    g = torch.Generator().manual_seed(M + N + K)
+    W = torch.randn(N, K, generator=g) * 0.02
+    q, scale = ow.int4_groups(W)
+    t = dict(q=q, wscales=scale.to(BF), proj_down=(torch.randn(K, 32, generator=g) / K ** 0.5).to(BF),
+             proj_up=(torch.randn(N, 32, generator=g) * 0.02).to(BF), smooth=torch.ones(K, dtype=BF),
+             bias=(torch.randn(N, generator=g) * 0.02).to(BF))
+    x = activations(M, K, g)
+    p = w4a4.pack_parts(t, "cuda")
+    qa = ops.act_quant_launch(x.cuda(), p["smooth"], p["proj_down"])
+    wc = ops.weight_codes(p["qweight"])
+    y32 = torch.empty(M, N, device="cuda")
+    ops.gemm_launch(*qa, wc, p["wscales"], p["proj_up"], p["bias"], M, y32, ops.EPI_F32)
+    y16 = torch.empty(M, N, device="cuda", dtype=BF)
+    ops.gemm_launch(*qa, wc, p["wscales"], p["proj_up"], p["bias"], M, y16, ops.EPI_BF16)
+    torch.cuda.synchronize()
+    # the low-rank sums: within fp32 rounding of the oracle's; the GEMM is then checked on the kernel's own sums
+    # (their bf16 rounding, which the GEMM applies, can fall on either side of a tie between the two)
+    la = qa[2].cpu()[:M]
+    la64 = ow.lora_down(x, t["proj_down"])
+    assert float((la - la64).abs().max()) <= 1e-5 * float(la64.abs().max()) + 1e-6
+    ref, rq, rs, _ = ow.linear_parts(x, t, lora=la)
+    assert torch.equal(ops.decode_acts(qa[0].cpu())[:M], rq)
+    assert torch.equal(qa[1].cpu()[:, :M].t(), rs)
+    A = ow.group_gemm(rq.abs(), rs.float(), t["q"].abs(), t["wscales"].float())
+    A += (la.to(BF).double() @ t["proj_up"].double().t()).abs() + t["bias"].double().abs()
+    bar = (K // 64 + 2) * 2 ** -23 * A
+    diff = (y32.cpu().double() - ref).abs()
+    print(f"{name} {M}x{N}x{K}: max |fp32 - oracle| {float(diff.max()):.3e}, max ratio to the bound "
+          f"{float((diff / bar).max()):.3f}")
+    assert torch.all(diff <= bar)
+    assert torch.all((y16.cpu().double() - ref).abs() <= ref.abs() * 2 ** -8 + bar)
+
+
+@pytest.mark.parametrize("M", [1392, 2640])
+@pytest.mark.parametrize("name,N,K", SHAPES)
+def test_fp8_linear_sweep(gpu, name, N, K, M):
+    """The same shapes as FP8 W8A8 linears with per-row scales (DynamicFp8Linear rows, fp8.py:44-67): quantizers
+    bit-exact, the product within 1e-2 max-rel and 2^-8 relative L2 of the oracle (cuBLASLt's accumulation order
+    is not the reference's to pin)."""
+    from wdl import fp8
+
+    g = torch.Generator().manual_seed(M + N)
+    x = activations(M, K, g)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(BF)
+    b = (torch.randn(N, generator=g) * 0.02).to(BF)
+    q, s = fp8.quantize_padded(x.cuda(), True)
+    wq, ws = fp8.quantize_padded(w.cuda(), True, pad=1)
+    y = fp8.gemm(q, s, M, wq, ws, b.cuda(), True).cpu().float()
+    ref, (xq, xs, _, _) = ofp8.w8a8_linear_rows(x, w, b)
+    assert torch.equal(q.cpu()[:M].view(torch.uint8), xq.view(torch.uint8))
+    assert torch.equal(s.cpu()[:M], xs.reshape(-1))
+    ref = ref.float()
+    err = float((y - ref).abs().max()) / float(ref.abs().max())
+    rel = float((y - ref).norm() / ref.norm())
+    print(f"fp8 {name} {M}x{N}x{K}: max-rel {err:.2e}, rel-L2 {rel:.2e}")
+    assert err <= 1e-2 and rel <= 2 ** -8
+
+
+def test_norm_rope_on_the_704x1280_grid(gpu):
+    """The fused Q/K RMSNorm + RoPE on a 3-frame chunk of 22 x 40 tokens at start frame 7, 24 heads: bit-exact to
+    the oracle's ordered-sum RMSNorm and fp32 rotation."""
+    from wdl import rope
+
+    g = torch.Generator().manual_seed(40)
+    M, C = 2640, 3072
+    d = torch.randn(M, 3 * C, generator=g).to(BF)
+    wq, wk = ((torch.rand(C, generator=g) + 0.5).to(BF) for _ in range(2))
+    freq = orope.freqs(128, 1024, torch.float64).float()
+    dc = d.cuda()
+    Qo, Ko = rope.norm_rope(dc[:, :C], dc[:, C:2 * C], wq.cuda(), wk.cuda(), freq.cuda(), (3, 22, 40), 7)
+    from oracle import norms as onorms
+
+    for got, src, w in ((Qo, d[:, :C], wq), (Ko, d[:, C:2 * C], wk)):
+        want = orope.rope_apply(onorms.rms_norm(src.contiguous(), w).reshape(1, M, 24, 128), (3, 22, 40), freq, 7)
+        assert torch.equal(got.cpu().reshape(1, M, 24, 128), want)
+
+
+@pytest.mark.parametrize("at", [0, 6600, 15840])
+def test_chunk_attention_at_24_heads(gpu, at):
+    """The full 24-head launch (2640 queries: 21 x 24 = 504 query tiles, the scheduling of this shape) over at
+    cached FP8 keys + the 2640-token chunk, K with a per-channel bias; RoPE on the chunk's Q and K at start frame
+    at // 880. Heads 0 and 23 against the oracle: cosine >= 0.999 with the quantized emulation, error against exact
+    attention within 1.2x that of the fp8-P emulation + 1e-3."""
+    from wdl import sage_kv
+
+    H, n = 24, 2640
+    g = torch.Generator().manual_seed(at + 3)
+    kbias = torch.randn(1, 1, H, 128, generator=g) * 3
+    freq = orope.freqs(128, 1024, torch.float64).float()
+    start = at // 880
+    Q = orope.rope_apply(torch.randn(1, n, H, 128, generator=g).to(BF), (3, 22, 40), freq, start)
+    K = orope.rope_apply((torch.randn(1, n, H, 128, generator=g) + kbias).to(BF), (3, 22, 40), freq, start)
+    V = torch.randn(1, n, H, 128, generator=g).to(BF)
+    cap = max(at, 1)
+    kc, ksc = ofp8.quantize_rows(torch.randn(1, cap, H, 128, generator=g) + kbias)
+    vc, vsc = ofp8.quantize_rows(torch.randn(1, cap, H, 128, generator=g))
+    out = sage_kv.attend(Q.cuda(), kc.cuda(), ksc.cuda(), vc.cuda(), vsc.cuda(), at, K.cuda(), V.cuda()).cpu().float()
+    for hh in (0, H - 1):
+        sl = lambda t: t[:, :, hh:hh + 1].contiguous()
+        p = osage.prep(sl(Q), sl(kc), sl(ksc), sl(vc), sl(vsc), at, sl(K), sl(V))
+        emul = osage.attention_quantized(p, 128 ** -0.5)
+        emul8 = osage.attention_quantized(p, 128 ** -0.5, p_fp8=True)
+        exact = osage.attention_exact(sl(Q), p["K"], p["V"])
+        got = out[:, :, hh:hh + 1]
+        cos, err = osage.cosine(got, emul), osage.rel_err(got, exact)
+        print(f"L={at + n} head {hh}: cos {cos:.6f}, err vs exact {err:.4f} (fp8-P emulation "
+              f"{osage.rel_err(emul8, exact):.4f})")
+        assert cos >= 0.999
+        assert err < 1.2 * osage.rel_err(emul8, exact) + 1e-3
+
+
+def test_step_block_over_the_full_window(gpu):
+    """The step's block at full size: 1392 tokens (3 frames of 16 x 29, start frame 18) over 8352 cached FP8 keys
+    + the chunk and 512 prompt tokens, random-init W4A4 parts, against the oracle block: max-rel-err 1e-2 (the
+    block bar); each stage is checked on its own at this shape in test_block_gpu.py's stage test."""
+    from test_block_gpu import run_pair
+
+    X, out, ref, cache, ocache, inp = run_pair(3072, 24, 14336, (3, 16, 29), 18, 8352, 512, 17)
+    err = float((out.float() - ref.float()).abs().max()) / float(ref.float().abs().max())
+    rel = float((out.float() - ref.float()).norm() / ref.float().norm())
+    print(f"step block: max-rel-err {err:.2e}, rel-L2 {rel:.3e}")
+    assert err <= 1e-2
+    # the chunk's K / V went to cache rows 8352 .. 9743 (fp8 bytes equal up to bf16 flips upstream)
+    same = (cache.k.cpu()[:, 8352:].view(torch.uint8) == ocache["k"][:, 8352:].view(torch.uint8))
+    assert float(same.float().mean()) > 0.97
+
+
+def test_thirty_block_step_graph_properties(gpu):
+    """The benchmark's 30-block step on latents (patch embedding, time embedding, the blocks over full FP8 windows
+    and the prompt, head): finite; a captured graph's replay equals the eager step bit for bit; each block's chunk
+    keys and values land in its cache rows 8352 .. 9743 (the rows before them untouched)."""
+    import bench
+
+    dev = torch.device("cuda")
+    with torch.no_grad():
+        step = bench.Step(dev)
+        before = step.caches[0].k[:, :bench.CACHED].clone()
+        eager = step().clone()
+        torch.cuda.synchronize()
+        assert torch.isfinite(eager).all()
+        c0 = step.caches[0]
+        rows = c0.k[:, bench.CACHED:bench.CACHED + bench.TOKENS].view(torch.uint8)
+        assert rows.float().abs().sum() > 0 and torch.equal(c0.k[:, :bench.CACHED], before)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = step()
+        for _ in range(2):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager)
