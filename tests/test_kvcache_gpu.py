@@ -1,0 +1,61 @@
+"""The FP8 KV cache on the GPU over many chunks, well past a full window (tests/test_kv_cache.py:36-118 states the
+window invariants for the reference's cache): after every commit the cache rows hold exactly the sink frames and
+the newest frames of the window (the oldest evicted, the chunk's rows copied into their slots), as FP8 rows of the
+keys and values that were written; attention over the window meets the Sage bars against the oracle emulation of
+the cache as it stands: cosine >= 0.999, and an error against exact attention over the unquantized window within
+1.2x (+ 1e-3) of the error the emulation itself carries (FP8 cache rows, int8 Q / K, fp8 P: the reference's
+quantized baseline, tests/test_sage_kv.py:97)."""
+
+import pytest
+import torch
+
+from oracle import fp8 as ofp8
+from oracle import sage as osage
+
+pytestmark = pytest.mark.gpu
+T, H, CHUNK = 4, 2, 3  # tokens per latent frame, heads, frames per chunk
+
+
+def rows_as_set(k: torch.Tensor) -> list:
+    """The FP8 rows of a [n, H, 128] key block as a sorted list of byte strings (the ring's order is its own)."""
+    b = k.view(torch.uint8).reshape(k.shape[0], -1)
+    return sorted(bytes(r.tolist()) for r in b)
+
+
+@pytest.mark.parametrize("window,sink", [(21, 0), (21, 3), (9, 3), (12, 4), (21, 10)])
+def test_window_holds_sink_and_newest_frames_past_many_commits(gpu, window, sink):
+    from wdl.kvcache import KVCache
+
+    g = torch.Generator().manual_seed(window * 31 + sink)
+    cache = KVCache((window - CHUNK) * T, sink * T, chunk=CHUNK)
+    frames = []  # (K, V) bf16 [T, H, 128] of every committed frame, in video order
+    worst = 0.0
+    for c in range(12):
+        Q, K, V = (torch.randn(1, CHUNK * T, H, 128, generator=g).to(torch.bfloat16) for _ in range(3))
+        out = cache.attend(Q.cuda(), K.cuda(), V.cuda()).cpu()
+        at = cache.saved
+        ring = window - CHUNK - sink
+        seen = frames if len(frames) <= window - CHUNK else frames[:sink] + frames[len(frames) - ring:]
+        assert at == len(seen) * T
+        # the cache rows before the chunk: exactly the FP8 rows of the seen frames' keys and values
+        if seen:
+            want_k = torch.cat([ofp8.quantize_rows(k)[0] for k, _ in seen])
+            want_v = torch.cat([ofp8.quantize_rows(v)[0] for _, v in seen])
+            assert rows_as_set(cache.k[0, :at].cpu()) == rows_as_set(want_k)
+            assert rows_as_set(cache.v[0, :at].cpu()) == rows_as_set(want_v)
+        # attention: the Sage bars against the oracle on the cache as it stands
+        p = osage.prep(Q, cache.k[:, :max(at, 1)].cpu(), cache.ks[:, :max(at, 1)].cpu(), cache.v[:, :max(at, 1)].cpu(),
+                       cache.vs[:, :max(at, 1)].cpu(), at, K, V)
+        emul = osage.attention_quantized(p, 128 ** -0.5)
+        assert osage.cosine(out, emul) >= 0.999
+        # and against exact attention over the unquantized window, relative to the quantized emulation's own error
+        Kw = torch.cat([k for k, _ in seen] + [K[0]]).float()[None]
+        Vw = torch.cat([v for _, v in seen] + [V[0]]).float()[None]
+        exact = osage.attention_exact(Q, Kw, Vw)
+        base = osage.rel_err(osage.attention_quantized(p, 128 ** -0.5, p_fp8=True), exact)
+        assert osage.rel_err(out, exact) < 1.2 * base + 1e-3
+        worst = max(worst, osage.rel_err(out, exact))
+        cache.commit()
+        frames += [(K[0, f * T:(f + 1) * T], V[0, f * T:(f + 1) * T]) for f in range(CHUNK)]
+    print(f"window {window}, sink {sink}: worst error against exact attention {worst:.4f}")
+    assert cache.full()
