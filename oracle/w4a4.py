@@ -6,6 +6,10 @@ with W diag(s) = up down + R (rank r by SVD), R in symmetric INT4 groups of 64 i
 Functions and what pins them:
 - int4_groups (w4a4.py:80-100): "max" rule. Pinned by the reference's own closed form
   (tests/test_w4a4.py:175-176, round/clamp) and by brute force (the nearest grid point of every value).
+- gptq (w4a4.py:103-137): pinned by the reference's contract (tests/test_w4a4.py:144-160: the layer output error
+  below 0.8 x that of rounding to the nearest, on correlated inputs), by the closed form that with H = I every
+  update term vanishes and GPTQ is the max-rule rounding to the nearest exactly, and by dead input channels
+  (zero Hessian diagonal) coming out zero (tests/test_oracle_w4a4.py).
 - smoothing (w4a4.py:183-186), quantize_weight (w4a4.py:140-180 without the Nunchaku packer; the shift-corrected
   bias of 168-170). Pinned by the reference's tolerance contracts (tests/test_w4a4.py:7-59): a rank-32 weight is
   carried by the 16-bit branch to < 1 %, smoothing beats none, the shift correction halves the GELU offset.
@@ -53,6 +57,43 @@ def int4_groups(R: torch.Tensor, rule: str = "max"):
     return q, scale
 
 
+@torch.no_grad()
+def gptq(R: torch.Tensor, H: torch.Tensor, damp: float = 0.01, block: int = 128):
+    """w4a4.py:103-137 — GPTQ of R [N, K] into int4 groups of 64 with inputs' Hessian H [K, K]: dead channels
+    zeroed (unit diagonal), diagonal damped by damp * mean, U = upper Cholesky of H^-1; columns rounded in order in
+    blocks of `block`, a group's scale (amax / 7) taken when its first column is reached from the columns as
+    updated so far; a column's error (w - q s) / U[i, i] spread over the block's later columns through U[i, i:],
+    the block's errors over the columns after it at the block's end. -> (q int32 [N, K], scale fp32 [N, K/64])."""
+    W = R.clone().float()
+    N, K = W.shape
+    H = H.float().clone()
+    dead = torch.diag(H) == 0
+    H[dead, dead] = 1
+    W[:, dead] = 0
+    H += damp * torch.diag(H).mean() * torch.eye(K)
+    Hinv = torch.linalg.cholesky(torch.cholesky_inverse(torch.linalg.cholesky(H)), upper=True)
+    q = torch.zeros(N, K, dtype=torch.int32)
+    scale = torch.zeros(N, K // GROUP)
+    for i1 in range(0, K, block):
+        i2 = min(i1 + block, K)
+        W1, Err = W[:, i1:i2].clone(), torch.zeros(N, i2 - i1)
+        Hb = Hinv[i1:i2, i1:i2]
+        for i in range(i2 - i1):
+            col = i1 + i
+            if col % GROUP == 0:
+                g = torch.cat([W1[:, i:], W[:, i2:]], dim=1)[:, :GROUP]
+                scale[:, col // GROUP] = g.abs().amax(dim=1).clamp(min=1e-8) / 7
+            sc = scale[:, col // GROUP]
+            w = W1[:, i]
+            qi = torch.round(w / sc).clamp(-8, 7)
+            q[:, col] = qi.to(torch.int32)
+            err = (w - qi * sc) / Hb[i, i]
+            W1[:, i:] -= err[:, None] * Hb[i, i:][None, :]
+            Err[:, i] = err
+        W[:, i2:] -= Err @ Hinv[i1:i2, i2:]
+    return q, scale
+
+
 def smoothing(act_amax: torch.Tensor, weight: torch.Tensor, alpha: float = 0.5) -> torch.Tensor:
     """w4a4.py:183-186 — SmoothQuant s_j = max|x_j|^alpha / max|W_:j|^(1-alpha), clamped to [1e-2, 1e2]."""
     w = weight.float().abs().amax(dim=0).clamp(min=1e-5)
@@ -61,7 +102,7 @@ def smoothing(act_amax: torch.Tensor, weight: torch.Tensor, alpha: float = 0.5) 
 
 @torch.no_grad()
 def quantize_weight(weight: torch.Tensor, bias=None, smooth=None, rank: int = 32, shift: float = 0.0,
-                    rule: str = "max", R: torch.Tensor | None = None):
+                    rule: str = "max", R: torch.Tensor | None = None, hessian: torch.Tensor | None = None):
     """w4a4.py:140-180 in logical (unpacked) form: dict(q int32 [N, K], wscales bf16 [N, K/64],
     proj_down bf16 [K, r], proj_up bf16 [N, r], smooth bf16 [K], bias bf16 [N], R fp32 [N, K]).
     R may be given (the quantizer input on which int4 parity is defined)."""
@@ -74,7 +115,10 @@ def quantize_weight(weight: torch.Tensor, bias=None, smooth=None, rank: int = 32
     down = Vh[:rank]
     if R is None:
         R = Ws - up @ down
-    q, scale = int4_groups(R, rule)
+    if hessian is None:
+        q, scale = int4_groups(R, rule)
+    else:  # w4a4.py:155-160: GPTQ in the smoothed space, whose Hessian is diag(1/s) H diag(1/s)
+        q, scale = gptq(R, hessian.float() / s[:, None] / s[None, :])
     b = torch.zeros(N) if bias is None else bias.float()
     if shift:
         Rq = (q.view(N, K // GROUP, GROUP).float() * scale[..., None]).view(N, K)

@@ -23,7 +23,8 @@ GROUP = 64
 PARTS = ("qweight", "wscales", "proj_down", "proj_up", "smooth", "bias")  # w4a4.py:207
 MSE_STEPS = torch.linspace(0.5, 1.0, 26).tolist()
 
-__all__ = ["GROUP", "GELU_SHIFT", "PARTS", "int4_groups", "smoothing", "quantize", "pack_weight", "unpack_weight",
+__all__ = ["GROUP", "GELU_SHIFT", "PARTS", "int4_groups", "gptq", "smoothing", "quantize", "pack_weight",
+           "unpack_weight",
            "linear", "gelu_mlp", "w4a4_linear", "w4a4_gelu_mlp", "PackedW4A4Linear", "PackedW4A4GeluMLP",
            "FusedQKVAttention"]
 
@@ -54,6 +55,50 @@ def int4_groups(R: torch.Tensor, rule: str = "max"):
     return q, scale
 
 
+@torch.no_grad()
+def gptq(R: torch.Tensor, H: torch.Tensor, damp: float = 0.01):
+    """GPTQ rounding (Frantar et al., "GPTQ: Accurate Post-Training Quantization for Generative Pre-trained
+    Transformers", ICLR 2023) of R [N, K] into symmetric int4 groups of 64 input channels, minimising
+    ||X R^T - X Q(R)^T|| for inputs with H = X^T X [K, K] (w4a4.py:103-137 states the same method).
+
+    Channels that never carry input (H[k, k] = 0) are zeroed and given a unit diagonal; the diagonal is damped by
+    damp * its mean. U is the upper Cholesky factor of H^-1. Columns are rounded in order, one 64-column group at a
+    time: the group's scale is amax / 7 of its columns as the earlier groups' updates left them; inside the group
+    each column's rounding error e = (w - q s) / U[c, c] is pushed onto the group's later columns at once (e
+    U[c, later]); at the end of the group its errors E update every later column in one product (E U[group,
+    later]). Returns the integers int32 [N, K] and the fp32 scales [N, K / 64]."""
+    W = R.float().clone()
+    N, K = W.shape
+    if K % GROUP:
+        raise ValueError(f"K = {K} is not a multiple of {GROUP}")
+    Hd = H.float().clone().to(W.device)
+    diag = Hd.diagonal()
+    dead = diag == 0
+    diag[dead] = 1.0
+    W[:, dead] = 0.0
+    diag += damp * diag.mean()
+    U = torch.linalg.cholesky(torch.cholesky_inverse(torch.linalg.cholesky(Hd)), upper=True)
+    q = torch.empty(N, K, dtype=torch.int32, device=W.device)
+    scales = torch.empty(N, K // GROUP, device=W.device)
+    for g0 in range(0, K, GROUP):
+        g1 = g0 + GROUP
+        s = W[:, g0:g1].abs().amax(dim=1).clamp(min=1e-8) / 7
+        scales[:, g0 // GROUP] = s
+        E = torch.empty(N, GROUP, device=W.device)
+        for j in range(GROUP):
+            c = g0 + j
+            w = W[:, c]
+            qc = torch.round(w / s).clamp(-8, 7)
+            q[:, c] = qc.to(torch.int32)
+            e = (w - qc * s) / U[c, c]
+            E[:, j] = e
+            if c + 1 < g1:
+                W[:, c + 1:g1] -= e[:, None] * U[c, c + 1:g1][None, :]
+        if g1 < K:
+            W[:, g1:] -= E @ U[g0:g1, g1:]
+    return q, scales
+
+
 def smoothing(act_amax: torch.Tensor, weight: torch.Tensor, alpha: float = 0.5) -> torch.Tensor:
     """SmoothQuant's per-input-channel s = max|x|^alpha / max|W|^(1-alpha), clamped to [1e-2, 1e2]
     (w4a4.py:183-186)."""
@@ -79,10 +124,14 @@ def unpack_weight(p: torch.Tensor) -> torch.Tensor:
 
 
 @torch.no_grad()
-def quantize(weight, bias=None, smooth=None, rank: int = 32, shift: float = 0.0, rule: str = "max", R=None):
+def quantize(weight, bias=None, smooth=None, rank: int = 32, shift: float = 0.0, rule: str = "max", R=None,
+             hessian=None):
     """The tensors of a W4A4 layer for y = x W^T + b (w4a4.py:140-180) in wdl's packed layout.
     weight [N, K]; smooth [K] (ones when None); shift: the second GELU-MLP layer quantizes x + shift unsigned, so
-    its bias takes off shift * (Q(R) / s) 1. R: the quantizer input, when given (parity tests)."""
+    its bias takes off shift * (Q(R) / s) 1. R: the quantizer input, when given (parity tests). hessian [K, K]:
+    X^T X of the inputs the int4 branch multiplies by R (x + shift for the GELU MLP's second layer, before
+    smoothing): R is then rounded by gptq in the smoothed space (whose Hessian is diag(1/s) H diag(1/s)) instead
+    of to the nearest."""
     W = weight.float()
     N, K = W.shape
     dev = W.device
@@ -92,7 +141,11 @@ def quantize(weight, bias=None, smooth=None, rank: int = 32, shift: float = 0.0,
     up, down = U[:, :rank] * S[:rank], Vh[:rank]
     if R is None:
         R = Ws - up @ down
-    q, scale = int4_groups(R.to(dev), rule)
+    if hessian is None:
+        q, scale = int4_groups(R.to(dev), rule)
+    else:
+        Hs = hessian.float().to(dev) / s[:, None] / s[None, :]
+        q, scale = gptq(R.to(dev), Hs)
     b = torch.zeros(N, device=dev) if bias is None else bias.float().to(dev)
     if shift:
         deq = (q.reshape(N, K // GROUP, GROUP).float() * scale[..., None]).reshape(N, K)
