@@ -18,6 +18,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle import block as oblock
+from oracle import unipc as ounipc
 
 BF = torch.bfloat16
 
@@ -95,6 +96,23 @@ def next_chunk(noise: torch.Tensor, fresh: list, E: dict, blocks: list, caches: 
         x0 = x - sigma * flow
         if i + 1 < len(levels):
             x = (1 - levels[i + 1]) * x0 + levels[i + 1] * fresh[i]
+    model_forward(x0, torch.zeros(1), E, blocks, caches, ctx_kvs, freq, start_frame, heads)
+    n = x0.shape[1] * (x0.shape[2] // 2) * (x0.shape[3] // 2)
+    for cache in caches:
+        cache["at"] += n
+    return x0
+
+
+def next_chunk_unipc(noise: torch.Tensor, E: dict, blocks: list, caches: list, ctx_kvs: list, freq, start_frame: int,
+                     heads: int, steps: int = 2) -> torch.Tensor:
+    """Stream.next_chunk with sampler "unipc" (causal.py:620-636, 709-710): oracle.unipc's sampler in float64 over
+    the oracle model at the scheduler's integer timesteps, then the write pass at t = 0 and the commit."""
+    def flow(x, t, k):
+        f = model_forward(torch.from_numpy(x).float(), torch.full((1,), float(t)), E, blocks, caches, ctx_kvs, freq,
+                          start_frame, heads)
+        return f.double().numpy()
+
+    x0 = torch.from_numpy(ounipc.sample(noise.double().numpy(), flow, steps)).float()
     model_forward(x0, torch.zeros(1), E, blocks, caches, ctx_kvs, freq, start_frame, heads)
     n = x0.shape[1] * (x0.shape[2] // 2) * (x0.shape[3] // 2)
     for cache in caches:

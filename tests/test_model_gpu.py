@@ -139,3 +139,27 @@ def test_chunk_loop_matches_oracle(gpu):
         floor = float((deq(po["k"], po["ks"]) - ref_k).norm() / ref_k.norm())
         print(f"cached keys: rel-L2 {rel:.3e} (oracle under 50 one-step changes: {floor:.3e})")
         assert rel <= 1.5 * max(floor, 0.02)
+
+
+def test_unipc_chunk_loop_matches_oracle(gpu):
+    """Two chunks of the "unipc" loop (2 steps at t = 999, 833, then the write pass) from the same noises: x0's
+    error relative to its change from the noise within 1.5x of the oracle's own under 50 one-step noise changes
+    (floor 2 %), and the caches' write offsets advance by a chunk."""
+    import copy
+
+    from wdl import model as wmodel
+
+    model, (E, Ps, ocaches, octx, freq), g, n = setup(6)
+    stream = wmodel.ChunkStream(model, SHAPE, torch.Generator(device="cuda"), sampler="unipc", steps=2)
+    assert stream.timesteps == [999, 833]
+    for chunk in range(2):
+        noise = torch.randn(SHAPE, generator=g)
+        x0 = stream.next_chunk(noise.cuda()).cpu()
+        pert = omodel.next_chunk_unipc(perturbed(noise, 50, 40 + chunk), E, Ps, copy.deepcopy(ocaches), octx, freq,
+                                       chunk * SHAPE[1], HEADS)
+        ref = omodel.next_chunk_unipc(noise, E, Ps, ocaches, octx, freq, chunk * SHAPE[1], HEADS)
+        rel = float((x0 - ref).norm() / (ref - noise).norm())
+        floor = float((pert - ref).norm() / (ref - noise).norm())
+        print(f"unipc chunk {chunk}: x0 error / x0 change {rel:.3e} (oracle under 50 one-step changes: {floor:.3e})")
+        assert rel <= 1.5 * max(floor, 0.02)
+        assert all(c.saved == (chunk + 1) * n for c in model.caches)

@@ -14,14 +14,18 @@ go through torch (hipBLASLt for the GEMMs); the blocks run the wdl kernels.
 
 ChunkStream.next_chunk restates Stream.next_chunk's DMD sampler (generation/causal.py:680-740) for the default
 "video" positions: at each level sigma (causal.py:41-45) x0 = x - sigma flow, renoised to the next level with fresh
-noise; then the write pass at t = 0 puts the final keys and values in the caches, which commit. Not restated: prompt
-blending, UniPC, re-anchoring, shots and context noise.
+noise; then the write pass at t = 0 puts the final keys and values in the caches, which commit. With sampler "unipc"
+the chunk is denoised by the UniPC sampler instead (causal.py:620-636, LongLive 2.0's; wdl.unipc): the model at the
+sampler's integer timesteps, each input x_0 - C[k] . flows of the plan, the clean latents its last row. Not restated:
+prompt blending, re-anchoring, shots and context noise.
 """
 
 from __future__ import annotations
 
 import torch
 import torch.nn.functional as F
+
+from wdl import unipc
 
 SHIFT = 5.0                    # timestep_shift of the distilled model (causal.py:35)
 STEPS = (1000, 750, 500, 250)  # its four timesteps before the shift (causal.py:36)
@@ -127,13 +131,23 @@ class DiTModel:
 
 
 class ChunkStream:
-    """Stream.next_chunk's DMD loop (causal.py:680-740, positions "video", write pass on, no context noise) over
-    a DiTModel: chunks of `shape` [in_dim, chunk, H, W] latents, one after another."""
+    """Stream.next_chunk's loop (causal.py:680-740, positions "video", no context noise) over a DiTModel: chunks of
+    `shape` [in_dim, chunk, H, W] latents, one after another. sampler "dmd" (Self-Forcing's, at `levels`) or "unipc"
+    (`steps` of LongLive 2.0's sampler, 4 by default as the reference's; its live preset runs 2); `steps` only with
+    "unipc" (causal.py:525-528)."""
 
-    def __init__(self, model: DiTModel, shape, generator: torch.Generator, levels=None, write_pass: bool = True):
+    def __init__(self, model: DiTModel, shape, generator: torch.Generator, levels=None, write_pass: bool = True,
+                 sampler: str = "dmd", steps: int | None = None, shift: float = SHIFT):
+        if sampler not in ("dmd", "unipc"):
+            raise ValueError(f"unknown sampler {sampler!r}")
+        if steps is not None and sampler != "unipc":
+            raise ValueError("the dmd sampler has the fixed timesteps of its levels")
         self.model, self.shape, self.generator = model, tuple(shape), generator
-        self.levels = sigmas() if levels is None else list(levels)
-        self.write_pass, self.start = write_pass, 0
+        self.levels = sigmas(shift) if levels is None else list(levels)
+        self.write_pass, self.start, self.sampler = write_pass, 0, sampler
+        if sampler == "unipc":
+            timesteps, C = unipc.plan(steps or len(STEPS), shift)
+            self.timesteps, self.plan = timesteps, C.tolist()
 
     @torch.no_grad()
     def next_chunk(self, noise: torch.Tensor | None = None) -> torch.Tensor:
@@ -141,7 +155,9 @@ class ChunkStream:
         dev = self.model.freq.device
         x = torch.randn(self.shape, generator=self.generator, device=dev) if noise is None else noise.float()
         x0 = x
-        for i, sigma in enumerate(self.levels):
+        if self.sampler == "unipc":
+            x0 = self._unipc(x)
+        for i, sigma in enumerate(self.levels if self.sampler == "dmd" else ()):
             t = torch.full((1,), 1000 * sigma, device=dev)
             flow = self.model.forward(x, t, self.start).float()
             x0 = x - sigma * flow  # x_t = (1 - sigma) x0 + sigma noise, flow = noise - x0
@@ -154,3 +170,13 @@ class ChunkStream:
             cache.commit()
         self.start += self.shape[1]
         return x0
+
+    def _unipc(self, noise: torch.Tensor) -> torch.Tensor:
+        """The UniPC steps from `noise`: the model at each timestep on x_0 - C[k] . flows; the clean latents."""
+        flows, x = [], noise
+        for k, t in enumerate(self.timesteps):
+            flows.append(self.model.forward(x, torch.full((1,), float(t), device=noise.device), self.start).float())
+            x = noise
+            for c, f in zip(self.plan[k + 1], flows):
+                x = x - c * f
+        return x
