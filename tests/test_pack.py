@@ -74,3 +74,18 @@ def test_refusals(tmp_path):
     with pytest.raises(ValueError):  # blocks of different shapes cannot share a pack
         pack.build_pack([parts_of(128, 256, 3), parts_of(128, 512, 4)], tmp_path / "c.pack")
     assert not (tmp_path / "c.pack").exists() and not (tmp_path / "c.pack.json").exists()
+
+
+def test_blocks_holding_only_weight_codes_write_the_same_pack(tmp_path):
+    """A QuantizedWanBlock keeps only the GEMM's fp6 weight codes; its parts write the nibbles they decode to, so
+    the pack is byte-identical to the one written from the packed parts."""
+    from wdl import ops
+
+    P = parts_of(256, 1024, 3)
+    codes_only = {k: (dict(v) if isinstance(v, dict) else v) for k, v in P.items()}
+    for k, v in codes_only.items():
+        if isinstance(v, dict):
+            v["wcodes"] = ops.encode_weights(w4a4.unpack_weight(v.pop("qweight")))
+    pack.build_pack([P], tmp_path / "a.pack")
+    pack.build_pack([codes_only], tmp_path / "b.pack")
+    assert (tmp_path / "a.pack").read_bytes() == (tmp_path / "b.pack").read_bytes()

@@ -29,9 +29,13 @@ LINEARS = ("qkv", "o", "cq", "ck", "cv", "co", "ffn1", "ffn2")
 
 class QuantizedWanBlock:
     """parts: {linear: packed W4A4 parts (w4a4.quantize / pack_parts)} for LINEARS, plus wq, wk, cwq, cwk (bf16
-    RMSNorm weights [dim]), n3w, n3b (fp32 LayerNorm-3 affine [dim]) and modulation (fp32 [6, dim])."""
+    RMSNorm weights [dim]), n3w, n3b (fp32 LayerNorm-3 affine [dim]) and modulation (fp32 [6, dim]). The block owns
+    `parts`: each linear's packed nibbles ([N, K/2], 0.5 B per weight) are replaced by the GEMM's tile-blocked fp6
+    codes (0.75 B per weight), so the weights are held once (3.7 GB of fp6 codes for the 30 blocks of Wan 5B
+    instead of that plus 2.45 GB of nibbles); keep_packed keeps both."""
 
-    def __init__(self, parts: dict, dim: int, heads: int, eps: float = 1e-6, cross_attention: str = "sdpa"):
+    def __init__(self, parts: dict, dim: int, heads: int, eps: float = 1e-6, cross_attention: str = "sdpa",
+                 keep_packed: bool = False):
         """cross_attention: "sdpa" — bf16 attention with an exact fp32 softmax, what the reference runs for the
         context (scaled_dot_product_attention, causal.py:418-420); "sage" — int8 QK / fp8 PV Sage attention over
         the context too (an opt-in deviation: faster on long prompts, within Sage's error bars)."""
@@ -42,6 +46,8 @@ class QuantizedWanBlock:
         dev = parts["qkv"]["qweight"].device
         for name in LINEARS:  # the GEMM operand: tile-blocked fp6 codes (e3m2 of 2w), expanded once from the nibbles
             parts[name]["wcodes"] = ops.weight_codes(parts[name]["qweight"])
+            if not keep_packed:
+                del parts[name]["qweight"]
         self.ones = torch.ones(dim, device=dev, dtype=torch.float32)
 
     # --------------------------------------------------------------------------------------- pieces

@@ -41,9 +41,16 @@ LAYOUT_NOTES = ("qweight uint8 [N, K/2]: per 64-group byte j holds k_j (low nibb
 
 
 def _entries(parts: dict):
-    """(name, tensor) of a block's parts, in row order."""
+    """(name, tensor) of a block's parts, in row order. A layer that holds only the GEMM's weight codes (a
+    QuantizedWanBlock drops the packed nibbles once it has them) is written as the nibbles those codes decode to."""
     for key, name in LAYERS.items():
         for p in PARTS:
+            if p == "qweight" and p not in parts[key]:
+                from wdl.ops import decode_weights
+                from wdl.w4a4 import pack_weight
+
+                yield f"{name}.{p}", pack_weight(decode_weights(parts[key]["wcodes"].cpu()))
+                continue
             yield f"{name}.{p}", parts[key][p]
     for key, name in OTHERS.items():
         yield name, parts[key]
