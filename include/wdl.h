@@ -92,12 +92,20 @@ int wdl_act_quant_w4_static(const void* x, int64_t ldx, int64_t M, int64_t K, co
  * (native/ops/w4a4_ops.cpp:36-38). 16-byte aligned buffers. */
 int wdl_w4a4_weight_codes(const void* qweight, int64_t N, int64_t K, void* codes, wdl_stream_t stream);
 
+/* Weight-scale operand of the W4A4 GEMM: n scales (bf16, or fp16 when fp16 != 0) -> n bf16 pairs packed in 32 bits,
+ * hi | lo << 16, hi + lo = the scale exactly (hi the scale truncated to bf16, lo the rest: (s, 0) for a bf16 scale,
+ * two exact bf16 parts for an fp16 one). The GEMM forms ws * as from both parts on the matrix cores, so fp16 weight
+ * scales cost no extra work (the reference keeps bf16 scales, quantization/w4a4.py:171-174; fp16 is the other mode
+ * Nunchaku's kernels accept). Done once per weight. scales 2-byte, pairs 4-byte aligned; finite scales. */
+int wdl_w4a4_scale_pairs(const void* scales, int fp16, int64_t n, void* pairs, wdl_stream_t stream);
+
 /* W4A4 GEMM with fused dequantization, low-rank up projection and bias. Replaces Nunchaku's gemm_w4a4 behind
  * live::w4a4_linear and live::w4a4_gelu_mlp (native/ops/w4a4_ops.cpp:36-38, 55-61).
  * y[m][n] = sum_g ascales[g][m] wscales[g][n] I_g[m][n] + bf16(lora[m]) . proj_up[n] + bias[n], I_g the exact
  * integer sum over the 64-group g. qa: [Mp, K] activation codes (wdl_act_quant_w4); wcodes: [N, K] weight codes
- * (wdl_w4a4_weight_codes), both in the operand format above; wscales bf16 [K/64, N]; lora fp32 [Mp, 32] or NULL; proj_up bf16
- * [N, 32]; bias bf16 [N] or NULL. epilogue: 0 out bf16 [M, ldo] = y; 1 out fp32 = y; 2 out bf16 =
+ * (wdl_w4a4_weight_codes), both in the operand format above; wscales [K/64, N] scale pairs (wdl_w4a4_scale_pairs);
+ * lora fp32 [Mp, 32] or NULL; proj_up bf16 [N, 32]; bias bf16 [N] or NULL. epilogue: 0 out bf16 [M, ldo] = y;
+ * 1 out fp32 = y; 2 out bf16 =
  * bf16(out + bf16(y) * gate[n]) in place (gated residual; gate fp32 [N]); 3 out bf16 = GELU_tanh(y).
  * Mp % 128 == 0, N % 128 == 0, K % 64 == 0, K <= 2^30; qa, wcodes, out, proj_up, lora, gate and workspace 16-byte
  * aligned, bias 8-byte, scales 4-byte; bf16 outputs: ldo % 8 == 0.

@@ -243,13 +243,13 @@ def test_rope_apply_bit_exact_with_padding_and_batch(gpu, table):
     freq = orope.freqs(128, 64, torch.float64)
     if table == "fp32":
         freq = freq.float()
-    got = rope.rope_apply(X.cuda(), [grid], freq.cuda(), start).cpu()
+    got = rope.rope_apply(X.cuda(), [grid, grid], freq.cuda(), start).cpu()  # one grid per sample
     for b in range(2):
         want = orope.rope_apply(X[b:b + 1], grid, freq, start)
         assert torch.equal(got[b:b + 1], want)
     assert torch.equal(got[:, 30:], X[:, 30:])
     with pytest.raises(ValueError):
-        rope.rope_apply(X.cuda(), [(3, 3, 5)], freq.cuda(), start)
+        rope.rope_apply(X.cuda(), [(3, 3, 5)] * 2, freq.cuda(), start)
 
 
 @pytest.mark.parametrize("cached", [False, True])

@@ -22,13 +22,16 @@ pytestmark = pytest.mark.gpu
 BF = torch.bfloat16
 
 
-def run_pair(dim, heads, ffn, grid, start, prior, Lc, seed, svd=False):
-    from wdl.block import build_block
+def run_pair(dim, heads, ffn, grid, start, prior, Lc, seed, svd=False, scale_dtype=None):
+    from wdl.block import LINEARS, build_block
     from wdl.kvcache import KVCache
 
     g = torch.Generator().manual_seed(seed)
     P = (oblock.quantize_block(oblock.random_block(dim, ffn, g)) if svd
          else oblock.random_logical_block(dim, ffn, g))
+    if scale_dtype is not None:  # both sides take the weight scales in this type
+        for name in LINEARS:
+            P[name]["wscales"] = P[name]["wscales"].to(scale_dtype)
     M = grid[0] * grid[1] * grid[2]
     X = torch.randn(M, dim, generator=g)
     X[:, torch.randperm(dim, generator=g)[: max(1, dim // 100)]] *= 20
@@ -80,6 +83,14 @@ def test_small_block_matches_oracle(gpu, seed):
     at, M = ocache["at"], X.shape[0]
     same = (cache.k.cpu()[:, at:at + M].view(torch.uint8) == ocache["k"][:, at:at + M].view(torch.uint8))
     assert float(same.float().mean()) > 0.97
+
+
+def test_small_block_with_fp16_weight_scales_matches_oracle(gpu):
+    """The fp16 weight-scale mode (the benchmark configurations quantize with fp16 scales; the reference keeps bf16):
+    the same bars as the bf16 block."""
+    X, out, ref, cache, ocache, _ = run_pair(256, 2, 1024, (2, 4, 6), 2, 96, 16, 3, svd=True,
+                                             scale_dtype=torch.float16)
+    check("fp16 scales", out, ref)
 
 
 def test_full_width_block_on_one_frame_matches_oracle(gpu):

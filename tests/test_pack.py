@@ -89,3 +89,17 @@ def test_blocks_holding_only_weight_codes_write_the_same_pack(tmp_path):
     pack.build_pack([P], tmp_path / "a.pack")
     pack.build_pack([codes_only], tmp_path / "b.pack")
     assert (tmp_path / "a.pack").read_bytes() == (tmp_path / "b.pack").read_bytes()
+
+
+def test_fp16_weight_scales_round_trip(tmp_path):
+    P = parts_of(256, 1024, 4)
+    for v in P.values():
+        if isinstance(v, dict):
+            v["wscales"] = v["wscales"].to(torch.float16)
+    pack.build_pack([P], tmp_path / "h.pack")
+    rows, layout, _ = pack.mapped_pack(tmp_path / "h.pack")
+    back = pack.slot(rows[0], layout)
+    for k, v in P.items():
+        if isinstance(v, dict):
+            assert back[k]["wscales"].dtype == torch.float16
+            same(back[k]["wscales"], v["wscales"])

@@ -127,16 +127,37 @@ def test_gemm_integer_accumulation_is_exact(gpu, M, N, K):
     assert torch.equal(y.cpu().double(), exact.double())
 
 
+def test_scale_pairs_are_exact_for_every_fp16_and_bf16_scale(gpu):
+    """The weight-scale operand: every finite fp16 value (all 63488 bit patterns) and every finite bf16 value split
+    into bf16 hi + lo equal to it exactly (hi the truncation, lo the remainder); bf16 scales give (s, 0)."""
+    from wdl import ops
+
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    for dt in (torch.float16, torch.bfloat16):
+        v = bits.view(dt)
+        v = v[torch.isfinite(v.float())]
+        pairs = ops.scale_pairs(v.cuda()).cpu()
+        hi = (pairs & 0xFFFF).to(torch.int16).view(torch.bfloat16).float()
+        lo = ((pairs >> 16) & 0xFFFF).to(torch.int16).view(torch.bfloat16).float()
+        assert torch.equal(hi + lo, v.float())  # both exact bf16 values, their fp32 sum exact
+        if dt == torch.bfloat16:
+            assert torch.equal(hi, v.float()) and torch.all(lo == 0)
+        else:
+            assert torch.equal(hi, (v.float().view(torch.int32) & -65536).view(torch.float32))
+
+
+@pytest.mark.parametrize("sdt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("M,N,K,valid", [(128, 256, 512, 100), (256, 128, 3072, 256), (1408, 384, 3072, 1392),
                                          (2688, 384, 3072, 2640)])
-def test_gemm_scaled_lowrank_bias_matches_oracle(gpu, M, N, K, valid):
+def test_gemm_scaled_lowrank_bias_matches_oracle(gpu, M, N, K, valid, sdt):
+    """bf16 and fp16 weight scales (the two modes; fp16 goes through the exact hi + lo pair)."""
     from wdl import w4a4
 
     g = torch.Generator().manual_seed(7 + M)
     qa = torch.randint(-7, 8, (M, K), generator=g, dtype=torch.int32)
     qw = torch.randint(-8, 8, (N, K), generator=g, dtype=torch.int32)
     asc = (torch.rand(K // 64, M, generator=g) * 0.3 + 0.01).to(torch.bfloat16)
-    wsc = (torch.rand(K // 64, N, generator=g) * 0.01 + 1e-4).to(torch.bfloat16)
+    wsc = (torch.rand(K // 64, N, generator=g) * 0.01 + 1e-4).to(sdt)
     lora = torch.randn(M, 32, generator=g)
     pu = (torch.randn(N, 32, generator=g) * 0.05).to(torch.bfloat16)
     bias = (torch.randn(N, generator=g) * 0.1).to(torch.bfloat16)

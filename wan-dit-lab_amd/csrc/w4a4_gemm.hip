@@ -5,13 +5,15 @@
 //
 // Operands: qa — activation int4 values as fp6 codes (wdl_act_quant_w4); wc — weight int4 values as fp6 codes
 // (wdl_w4a4_weight_codes, expanded once from the packed [N, K/2] nibbles), both tile-blocked 48 bytes per row
-// and 64-deep group (the format is described with blocked6_offset); as [K/64, Mp], ws [K/64, N] bf16; lora fp32
-// [Mp, 32]; pu bf16 [N, 32]; bias bf16 [N].
+// and 64-deep group (the format is described with blocked6_offset); as [K/64, Mp] bf16; ws [K/64, N] as bf16 pairs
+// (hi, lo) with hi + lo = the weight scale exactly (a bf16 scale is (s, 0), an fp16 scale splits into two bf16
+// parts: wdl_w4a4_scale_pairs); lora fp32 [Mp, 32]; pu bf16 [N, 32]; bias bf16 [N].
 //
 // Arithmetic: weights are e3m2 codes of 2w and activations e2m3 codes of q / 2, so v_mfma_f32_32x32x64_f8f6f4 in
 // its fp6 x fp6 form (one 64-deep group per instruction, 32 cycles: twice the int8 rate) returns I_g exactly as
 // an fp32 integer (|I_g| <= 64 * 8 * 15 < 2^24). The per-group scale product ws[n] * as[m] comes from a bf16
-// outer-product MFMA (exact: 8-bit by 8-bit significands), and each group is folded in with one fmaf per element,
+// MFMA with two k-slots, hi as + lo as (exact: each product 8 by 8 significant bits, the sum at most 11 by 8), and
+// each group is folded in with one fmaf per element,
 // groups in increasing order. The low-rank term is two bf16 MFMAs accumulated into the result, then the bias.
 //
 // Orientation: the tile is computed transposed, C^T[n][m] (rows = output features, columns = tokens), so a lane
@@ -52,7 +54,7 @@ struct GemmArgs {
     const uint8_t* qa;        // W4A4: fp6 e2m3 codes, tile-blocked [Mp/128][K/64][128][48]; FP8: e4m3 [Mp, K]
     const uint16_t* as;       // [G, Mp]
     const uint8_t* wc;        // W4A4: fp6 e3m2 codes, tile-blocked [N/128][K/64][128][48]; FP8: e4m3 [N, K]
-    const uint16_t* ws;       // [G, N]
+    const uint32_t* ws;       // W4A4: [G, N] weight scale pairs (hi | lo << 16), bf16 parts
     const float* lora;        // [Mp, 32] or null
     const uint16_t* pu;       // [N, 32] or null
     const uint16_t* bias;     // [N] or null
@@ -78,9 +80,9 @@ struct GemmArgs {
 // as inline asm so that the compiler's own wait insertion, which cannot tell the ring stages apart, does not add
 // vmcnt(0) waits in front of every LDS read.
 //   W4A4: a stage is the group's fp6 weight codes [BN][48 B] then activation codes [BM][48 B] — contiguous 6 KB
-//   blocks in global memory — split evenly over the waves, plus the scales ws[BN], as[BM]. Rows of 48 bytes read
-//   as 16 + 8 bytes per lane are free of bank conflicts on the 16-byte reads. Each scale stage ends in 64 zero
-//   bytes that lanes 32..63 read, which zeroes their half of the outer-product operands without a select.
+//   blocks in global memory — split evenly over the waves, plus the scales: ws[BN] pairs, as[BM]. Rows of 48 bytes
+//   read as 16 + 8 bytes per lane are free of bank conflicts on the 16-byte reads. Each scale stage ends in 128 zero
+//   bytes that lanes 32..63 read, which zeroes their half of the scale-product operands without a select.
 //   FP8: separate activation [BM][64 B] and weight [BN][64 B] stages, code rows with their four 16-byte quarters
 //   XOR-swizzled by (row / 4) % 4 (conflict-free operand reads).
 // Workgroup ids are remapped so that the tiles of one weight slab run on one XCD.
@@ -555,9 +557,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
     constexpr int N16 = W4 ? CB / 1024 : 0, N4 = W4 ? CB % 1024 / 256 : 0;
     static_assert(!W4 || (CS % NW == 0 && CB % 256 == 0), "fp6 stage vs waves");
     constexpr int LPG = W4 ? N16 + N4 + 1 : XI + WI;  // loads per wave per group (W4: + one 4-byte load of scales)
-    constexpr int SD = NW * 256;           // scale bytes loaded per stage (ws[BN], as[BM], then padding)
-    constexpr int SB = SD + 256;           // + 64 zero bytes (rounded up) read by lanes 32..63
-    static_assert(2 * (BN + BM) <= SD, "scale stage");
+    constexpr int SD = NW * 256;           // scale bytes loaded per stage (ws[BN] pairs, as[BM], then padding)
+    constexpr int SB = SD + 256;           // + 128 zero bytes (rounded up) read by lanes 32..63
+    static_assert(4 * BN + 2 * BM <= SD, "scale stage");
     __shared__ __attribute__((aligned(1024))) uint8_t sX[W4 ? 1 : STAGES][W4 ? 16 : BM * 64];
     __shared__ __attribute__((aligned(1024))) uint8_t sW[W4 ? 1 : STAGES][W4 ? 16 : BN * 64];
     __shared__ __attribute__((aligned(1024))) uint8_t sC[W4 ? STAGES : 1][W4 ? CS : 16];
@@ -571,7 +573,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
 
     // zero tails of the scale stages (written once; the loads never touch them)
     if constexpr (W4)
-        if (t < STAGES * 16) *reinterpret_cast<uint32_t*>(&sS[t / 16][SD + (t % 16) * 4]) = 0u;
+        if (t < STAGES * 32) *reinterpret_cast<uint32_t*>(&sS[t / 32][SD + (t % 32) * 4]) = 0u;
 
     // per-lane LDS offsets (stage-independent). W4: a lane's 16-byte and 8-byte pieces of its operand row, the
     // scale entries. FP8: operand rows and the two swizzled quarters.
@@ -583,13 +585,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
     for (int i = 0; i < TN; ++i) {
         const int row = wn * WN + i * 32 + lane % 32;
         aoff[i] = W4 ? row * ROW6 : row * 64;
-        soa[i] = low ? 2 * row : SD + 2 * (lane % 32);
+        soa[i] = low ? 4 * row : SD + 4 * (lane % 32);
     }
 #pragma unroll
     for (int j = 0; j < TM; ++j) {
         const int row = wm * WM + j * 32 + lane % 32;
         boff[j] = W4 ? (BN + row) * ROW6 : row * 64;
-        sob[j] = low ? 2 * BN + 2 * row : SD + 2 * (lane % 32);
+        sob[j] = low ? 4 * BN + 2 * row : SD + 2 * (lane % 32);
     }
     if constexpr (W4) {
         q0 = 16 * half;      // bytes 0..15 of the lane's half
@@ -611,7 +613,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         // 1 KB chunks w N16 .. and 256-byte chunks w N4 ... Each chunk lies inside one operand's 6 KB block (block
         // and operand boundaries are multiples of 1 KB), so a load reads from a wave-uniform base (scalar registers:
         // operand, tile row block, chunk; group g adds g BLOCK6) plus lane * 16 or lane * 4. The scale chunk of wave w
-        // is bytes 256 w .. of [ws[BN] | as[BM] | padding], also uniform per wave (2 BN and 2 BM are multiples of 256).
+        // is bytes 256 w .. of [ws[BN] pairs | as[BM] | padding], also uniform per wave (4 BN and 2 BM are multiples
+        // of 256).
         // FP8: this lane's sources. Both relative to group g0 of the piece.
         const uint8_t* cbase[W4 ? N16 + N4 : 1];
         int cdst[W4 ? N16 + N4 : 1];
@@ -645,12 +648,12 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         int64_t sstride;
         {
             const int b = 256 * wave;
-            if (b < 2 * BN) {
-                sstride = 2 * p.N;
+            if (b < 4 * BN) {
+                sstride = 4 * p.N;
                 sbase = reinterpret_cast<const uint8_t*>(p.ws + n0) + b + g0 * sstride;
-            } else if (b < 2 * (BN + BM)) {
+            } else if (b < 4 * BN + 2 * BM) {
                 sstride = 2 * p.Mp;
-                sbase = reinterpret_cast<const uint8_t*>(p.as + m0) + (b - 2 * BN) + g0 * sstride;
+                sbase = reinterpret_cast<const uint8_t*>(p.as + m0) + (b - 4 * BN) + g0 * sstride;
             } else {
                 sbase = reinterpret_cast<const uint8_t*>(p.ws + n0);
                 sstride = 0;
@@ -678,7 +681,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         const f32x16 zero = {};
 
         // Two register sets of one group's operands: weight / activation code fragments (W4: 6 dwords of fp6 codes,
-        // FP8: 8 of e4m3) and (W4) the bf16 scale of each fragment row, zero-extended (lanes 32..63 read the zero tail).
+        // FP8: 8 of e4m3) and (W4) the scales of each fragment row: the weight scale's bf16 pair, the activation
+        // scale zero-extended (lanes 32..63 read the zero tail).
         // Group h is multiplied from set h % 2 while group h + 1 is read into the other set.
         i32x8 fa[2][TN], fb[2][TM];
         uint32_t fsa[2][TN], fsb[2][TM];
@@ -695,7 +699,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         auto load_a = [&](int set, int st, int i) {
             if constexpr (W4) {
                 fa[set][i] = load_frag(&sC[st][aoff[i]]);
-                fsa[set][i] = *reinterpret_cast<const uint16_t*>(&sS[st][soa[i]]);
+                fsa[set][i] = *reinterpret_cast<const uint32_t*>(&sS[st][soa[i]]);
             } else {
                 fa[set][i] = load_frag(&sW[st][aoff[i]]);
             }
@@ -730,8 +734,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
                 const int i = s / TM, j = s % TM;
                 if constexpr (W4) {
                     const int pi = s == 0 ? TN - 1 : (s - 1) / TM, pj = s == 0 ? TM - 1 : (s - 1) % TM;
+                    // k-slots 0 and 1: (hi, lo) of ws against (as, as)
                     const i16x4 oa = __builtin_bit_cast(i16x4, make_uint2(fsa[cur][i], 0u));
-                    const i16x4 ob = __builtin_bit_cast(i16x4, make_uint2(fsb[cur][j], 0u));
+                    const i16x4 ob = __builtin_bit_cast(i16x4, make_uint2(fsb[cur][j] * 0x10001u, 0u));
                     // A: weights as e3m2 (format 3), B: activations as e2m3 (format 2)
                     const f32x16 I =
                         __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[cur][i], fb[cur][j], zero, 3, 2, 0, 0, 0, 0);
@@ -1022,6 +1027,18 @@ __device__ __forceinline__ uint32_t nib4_to_code6(uint32_t x) {
     return (neg & mask) | (pos & ~mask);
 }
 
+// weight scales -> the GEMM's pairs: hi = the scale truncated to bf16 (the scale itself when it is bf16), lo = the
+// rest, exact in bf16 (an fp16 scale has 11 significant bits, hi takes 8), packed hi | lo << 16
+__global__ __launch_bounds__(256) void scale_pairs_kernel(const uint16_t* s, int fp16, int64_t n, uint32_t* out) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n) return;
+    const uint16_t v = s[i];
+    const float f = fp16 ? __half2float(__ushort_as_half(v)) : bf16_to_f32(v);
+    const uint32_t fb = __float_as_uint(f);
+    const float lo = f - __uint_as_float(fb & 0xffff0000u);  // exact
+    out[i] = (fb >> 16) | (__float_as_uint(lo) & 0xffff0000u);
+}
+
 // packed nibbles [N, K/2] -> fp6 codes in the tile-blocked layout. The 32 packed bytes of a row's group hold
 // value k = j in the low nibble and k = 32 + j in the high nibble of byte j, so the low nibbles are half 0 and the
 // high nibbles half 1 (position j). One thread per 16 packed bytes: 16 codes of each half, 12 bytes each.
@@ -1078,7 +1095,7 @@ extern "C" int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wc
                                 "bf16 output rows a multiple of 8 elements");
     if (M == 0) return WDL_OK;
     GemmArgs a{static_cast<const uint8_t*>(qa), static_cast<const uint16_t*>(ascales),
-               static_cast<const uint8_t*>(wcodes), static_cast<const uint16_t*>(wscales), lora,
+               static_cast<const uint8_t*>(wcodes), static_cast<const uint32_t*>(wscales), lora,
                static_cast<const uint16_t*>(proj_up), static_cast<const uint16_t*>(bias), M, Mp, N, K, out, ldo,
                gate, nullptr, nullptr, static_cast<float*>(workspace)};
     if (reinterpret_cast<uintptr_t>(workspace) % 16)
@@ -1115,11 +1132,22 @@ extern "C" int wdl_w4a4_gemm_gelu_quant(const void* qa, const void* ascales, con
                                 "bias, smooth2 and proj_down2_t 8-byte, scales 4-byte");
     if (M == 0) return WDL_OK;
     GemmArgs a{static_cast<const uint8_t*>(qa), static_cast<const uint16_t*>(ascales),
-               static_cast<const uint8_t*>(wcodes), static_cast<const uint16_t*>(wscales), lora,
+               static_cast<const uint8_t*>(wcodes), static_cast<const uint32_t*>(wscales), lora,
                static_cast<const uint16_t*>(proj_up), static_cast<const uint16_t*>(bias), M, Mp, N, K, nullptr, N,
                nullptr, nullptr, nullptr, nullptr, static_cast<uint8_t*>(q2), static_cast<uint16_t*>(ascales2),
                static_cast<const uint16_t*>(smooth2), static_cast<const uint16_t*>(proj_down2_t), workspace};
     return dispatch_gelu_quant(a, lora2, stream);
+}
+
+extern "C" int wdl_w4a4_scale_pairs(const void* scales, int fp16, int64_t n, void* pairs, hipStream_t stream) {
+    if (n < 0) return fail(WDL_EINVAL, "w4a4_scale_pairs: bad count %lld", (long long)n);
+    if (n == 0) return WDL_OK;
+    if (!scales || !pairs) return fail(WDL_EINVAL, "w4a4_scale_pairs: null pointer");
+    if (reinterpret_cast<uintptr_t>(scales) % 2 || reinterpret_cast<uintptr_t>(pairs) % 4)
+        return fail(WDL_EINVAL, "w4a4_scale_pairs: scales must be 2-byte and pairs 4-byte aligned");
+    scale_pairs_kernel<<<unsigned((n + 255) / 256), 256, 0, stream>>>(static_cast<const uint16_t*>(scales), fp16 != 0,
+                                                                     n, static_cast<uint32_t*>(pairs));
+    return check_launch("w4a4_scale_pairs");
 }
 
 extern "C" int wdl_w4a4_weight_codes(const void* qweight, int64_t N, int64_t K, void* codes, hipStream_t stream) {

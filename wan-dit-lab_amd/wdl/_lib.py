@@ -30,6 +30,7 @@ SIGNATURES: dict[str, list] = {
     "wdl_act_quant_w4_static": [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_f32, c_int, c_ptr, c_i64, c_ptr, c_ptr, c_ptr,
                                 c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_int, c_f32, c_ptr, c_ptr],
     "wdl_w4a4_weight_codes": [c_ptr, c_i64, c_i64, c_ptr, c_ptr],
+    "wdl_w4a4_scale_pairs": [c_ptr, c_int, c_i64, c_ptr, c_ptr],
     "wdl_w4a4_gemm_workspace_bytes": [c_i64, c_i64, c_i64],
     "wdl_w4a4_gemm": [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_ptr,
                       c_i64, c_int, c_ptr, c_ptr, c_ptr],

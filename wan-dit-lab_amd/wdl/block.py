@@ -46,6 +46,7 @@ class QuantizedWanBlock:
         dev = parts["qkv"]["qweight"].device
         for name in LINEARS:  # the GEMM operand: tile-blocked fp6 codes (e3m2 of 2w), expanded once from the nibbles
             parts[name]["wcodes"] = ops.weight_codes(parts[name]["qweight"])
+            parts[name]["wspairs"] = ops.scale_pairs(parts[name]["wscales"])  # bf16 or fp16 scales, exactly
             if not keep_packed:
                 del parts[name]["qweight"]
         self.ones = torch.ones(dim, device=dev, dtype=torch.float32)
@@ -58,7 +59,7 @@ class QuantizedWanBlock:
     def _gemm(self, qa, name, M, out, epilogue=EPI_BF16, gate=None):
         t = self.p[name]
         q, asc, lora = qa
-        return ops.gemm_launch(q, asc, lora, t["wcodes"], t["wscales"], t["proj_up"], t["bias"], M, out, epilogue,
+        return ops.gemm_launch(q, asc, lora, t["wcodes"], t["wspairs"], t["proj_up"], t["bias"], M, out, epilogue,
                                gate)
 
     def linear(self, x, name):
@@ -117,7 +118,7 @@ class QuantizedWanBlock:
         # GEMM as int4 codes, scales and low-rank sums)
         q, asc, lora = self._quant(X, "ffn1", ln=dict(shift=sh_f, scale=sc_f, eps=self.eps))
         t1, t2 = self.p["ffn1"], self.p["ffn2"]
-        hq = ops.gelu_quant_launch(q, asc, lora, t1["wcodes"], t1["wscales"], t1["proj_up"], t1["bias"], M,
+        hq = ops.gelu_quant_launch(q, asc, lora, t1["wcodes"], t1["wspairs"], t1["proj_up"], t1["bias"], M,
                                    t2["smooth"], t2["proj_down"])
         self._gemm(hq, "ffn2", M, X, EPI_RESIDUAL, g_f)
         return X

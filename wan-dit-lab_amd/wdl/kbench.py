@@ -102,17 +102,18 @@ def gemm():
                             ("ffn1", 14336, 3072, ops.EPI_GELU), ("ffn2", 3072, 14336, ops.EPI_RESIDUAL)):
         t = w4a4.random_parts(N, K, dev, g)
         wc = ops.as_codes(t["qweight"], K)
+        wsp = ops.scale_pairs(t["wscales"])
         x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
         q, asc, lora = ops.act_quant_launch(x, t["smooth"], t["proj_down"])
         out = torch.randn(M, N, device=dev, generator=g).to(torch.bfloat16)
         gate = torch.rand(N, device=dev) if epi == ops.EPI_RESIDUAL else None
-        us = _replay_us(lambda: ops.gemm_launch(q, asc, lora, wc, t["wscales"], t["proj_up"], t["bias"], M, out, epi,
+        us = _replay_us(lambda: ops.gemm_launch(q, asc, lora, wc, wsp, t["proj_up"], t["bias"], M, out, epi,
                                                 gate))
         print(f"gemm {name} {M}x{N}x{K}: {us:.1f} us ({2 * M * N * K / us / 1e6:.0f} TOP/s)", flush=True)
         if name == "ffn1":  # the fused GELU MLP's first GEMM (epilogue: GELU, second layer's int4 input, low rank)
             s2 = torch.ones(N, device=dev, dtype=torch.bfloat16)
             pd2 = (torch.randn(32, N, device=dev, generator=g) / N ** 0.5).to(torch.bfloat16)
-            us = _replay_us(lambda: ops.gelu_quant_launch(q, asc, lora, wc, t["wscales"], t["proj_up"], t["bias"],
+            us = _replay_us(lambda: ops.gelu_quant_launch(q, asc, lora, wc, wsp, t["proj_up"], t["bias"],
                                                           M, s2, pd2))
             print(f"gemm ffn1 fused {M}x{N}x{K}: {us:.1f} us ({2 * M * N * K / us / 1e6:.0f} TOP/s, with the "
                   f"low-rank sum launch)", flush=True)

@@ -175,6 +175,20 @@ def weight_codes(qweight: torch.Tensor) -> torch.Tensor:
     return codes
 
 
+def scale_pairs(wscales: torch.Tensor) -> torch.Tensor:
+    """Weight scales bf16 or fp16 [K/64, N] -> the GEMM's scale operand, int32 [K/64, N] bf16 pairs hi | lo << 16
+    with hi + lo = the scale exactly (on the GPU). Pairs pass through."""
+    if wscales.dtype == torch.int32:
+        return wscales
+    if wscales.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"weight scales must be bf16 or fp16, got {wscales.dtype}")
+    src = wscales.contiguous()
+    pairs = torch.empty(src.shape, device=src.device, dtype=torch.int32)
+    _lib.call("wdl_w4a4_scale_pairs", ptr(src), int(src.dtype == torch.float16), src.numel(), ptr(pairs),
+              stream_of(src))
+    return pairs
+
+
 def as_codes(qweight: torch.Tensor, K: int) -> torch.Tensor:
     """The weight operand for input width K: tile-blocked fp6 codes [N/128, K/64, 128, 48] pass through, packed
     [N, K/2] nibbles are expanded (once per call)."""
@@ -191,8 +205,10 @@ def as_codes(qweight: torch.Tensor, K: int) -> torch.Tensor:
 
 def gemm_launch(q, ascales, lora, wcodes, wscales, proj_up, bias, M, out, epilogue=EPI_BF16, gate=None,
                 stream_k=True):
-    """W4A4 GEMM on the quantizer's outputs (q, ascales, lora) and tile-blocked fp6 weight codes (weight_codes).
+    """W4A4 GEMM on the quantizer's outputs (q, ascales, lora) and tile-blocked fp6 weight codes (weight_codes);
+    wscales: the scale pairs (scale_pairs), or bf16 / fp16 scales (converted on each call).
     stream_k=False runs the one-pass launch also for the shapes that the library splits in K."""
+    wscales = scale_pairs(wscales)
     if q.dim() != 4 or wcodes.dim() != 4 or q.shape[2:] != (BLOCK, ROW6) or wcodes.shape[2:] != (BLOCK, ROW6):
         raise ValueError("the W4A4 GEMM takes tile-blocked fp6 operands [rows/128, K/64, 128, 48]")
     Mp, K = q.shape[0] * BLOCK, q.shape[1] * 64
@@ -210,7 +226,8 @@ def gelu_quant_launch(q, ascales, lora, wcodes, wscales, proj_up, bias, M, smoot
     """The fused GELU MLP's first GEMM: the quantizer's outputs of x (q, ascales, lora) and the first layer's
     operands -> the second layer's inputs (q2 fp6 codes [Mp/128, N/64, 128, 48], ascales2 bf16 [N/64, Mp], lora2
     fp32 [Mp, 32]) for h = GELU(x W1^T + b1) quantized as (h + 0.171875) / smooth2, unsigned; h stays in
-    registers."""
+    registers. wscales: the scale pairs (scale_pairs), or bf16 / fp16 scales."""
+    wscales = scale_pairs(wscales)
     if q.dim() != 4 or wcodes.dim() != 4 or q.shape[2:] != (BLOCK, ROW6) or wcodes.shape[2:] != (BLOCK, ROW6):
         raise ValueError("the W4A4 GEMM takes tile-blocked fp6 operands [rows/128, K/64, 128, 48]")
     Mp, K = q.shape[0] * BLOCK, q.shape[1] * 64

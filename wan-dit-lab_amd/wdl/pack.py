@@ -10,7 +10,7 @@ FileExistsError; any failure removes what was written.
 The library's rows hold the QuantizedWanBlock parts in its own layouts (the reference's hold Nunchaku's): per W4A4
 layer — fused self_attn.qkv, self_attn.o, cross_attn.q / k / v / o, ffn.0 and ffn.2 (the GELU MLP's second layer,
 quantized for GELU's output + 0.171875) — qweight uint8 [N, K/2] (per 64-group byte j = k_j low nibble, k_{j+32}
-high nibble), wscales bf16 [K/64, N], proj_down bf16 [32, K], proj_up bf16 [N, 32], smooth bf16 [K], bias bf16
+high nibble), wscales bf16 or fp16 [K/64, N], proj_down bf16 [32, K], proj_up bf16 [N, 32], smooth bf16 [K], bias bf16
 [N]; then the Q/K RMSNorm weights (bf16), norm3's affine (fp32) and the modulation (fp32 [6, dim]). The manifest
 names that layout ("layout_notes"), so a reader never guesses it.
 """
@@ -33,9 +33,9 @@ LAYERS = {"qkv": "self_attn.qkv", "o": "self_attn.o", "cq": "cross_attn.q", "ck"
 PARTS = ("qweight", "wscales", "proj_down", "proj_up", "smooth", "bias")
 OTHERS = {"wq": "self_attn.norm_q.weight", "wk": "self_attn.norm_k.weight", "cwq": "cross_attn.norm_q.weight",
           "cwk": "cross_attn.norm_k.weight", "n3w": "norm3.weight", "n3b": "norm3.bias", "modulation": "modulation"}
-DTYPES = {torch.uint8: "uint8", torch.bfloat16: "bfloat16", torch.float32: "float32"}
+DTYPES = {torch.uint8: "uint8", torch.bfloat16: "bfloat16", torch.float16: "float16", torch.float32: "float32"}
 LAYOUT_NOTES = ("qweight uint8 [N, K/2]: per 64-group byte j holds k_j (low nibble) and k_{j+32} (high), int4 in "
-                "two's complement; wscales bf16 [K/64, N] group-major; proj_down bf16 [32, K] (transposed); proj_up "
+                "two's complement; wscales bf16 or fp16 [K/64, N] group-major; proj_down bf16 [32, K] (transposed); proj_up "
                 "bf16 [N, 32]; smooth bf16 [K]; bias bf16 [N]; ffn.2 quantized for the GELU output + 0.171875 "
                 "(unsigned int4 activations); norm weights bf16; norm3 affine and modulation fp32")
 

@@ -6,7 +6,7 @@ Weights are quantized offline (quantize, w4a4.py:140-180) into wdl's own packed 
 into Nunchaku's MMA tile order, which lives outside its tree):
 - qweight uint8 [N, K/2]: per 64-channel group, byte j holds k = j in the low nibble and k = j + 32 in the high
   nibble, two's complement int4 (pack_weight / unpack_weight);
-- wscales bf16 [K/64, N] (group-major); proj_down bf16 [32, K] (the down factor divided by s, transposed);
+- wscales bf16 (or fp16) [K/64, N] (group-major); proj_down bf16 [32, K] (the down factor divided by s, transposed);
   proj_up bf16 [N, 32]; smooth bf16 [K]; bias bf16 [N] (shift-corrected for the second GELU-MLP layer).
 The integer values are those of int4_groups (w4a4.py:80-100) on the quantizer input R; the int4 parity of the
 build is defined on R, since the SVD is not bit-portable between LAPACK and rocSOLVER.
@@ -125,13 +125,15 @@ def unpack_weight(p: torch.Tensor) -> torch.Tensor:
 
 @torch.no_grad()
 def quantize(weight, bias=None, smooth=None, rank: int = 32, shift: float = 0.0, rule: str = "max", R=None,
-             hessian=None):
+             hessian=None, scale_dtype=torch.bfloat16):
     """The tensors of a W4A4 layer for y = x W^T + b (w4a4.py:140-180) in wdl's packed layout.
     weight [N, K]; smooth [K] (ones when None); shift: the second GELU-MLP layer quantizes x + shift unsigned, so
     its bias takes off shift * (Q(R) / s) 1. R: the quantizer input, when given (parity tests). hessian [K, K]:
     X^T X of the inputs the int4 branch multiplies by R (x + shift for the GELU MLP's second layer, before
     smoothing): R is then rounded by gptq in the smoothed space (whose Hessian is diag(1/s) H diag(1/s)) instead
-    of to the nearest."""
+    of to the nearest. scale_dtype: the weight scales' type, bf16 (the reference's) or fp16."""
+    if scale_dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError("weight scales are bf16 or fp16")
     W = weight.float()
     N, K = W.shape
     dev = W.device
@@ -152,7 +154,7 @@ def quantize(weight, bias=None, smooth=None, rank: int = 32, shift: float = 0.0,
         b = b - shift * (deq / s[None, :]).sum(dim=1)
     return dict(
         qweight=pack_weight(q),
-        wscales=scale.to(torch.bfloat16).t().contiguous(),
+        wscales=scale.to(scale_dtype).t().contiguous(),
         proj_down=(down / s[None, :]).to(torch.bfloat16).contiguous(),
         proj_up=up.to(torch.bfloat16).contiguous(),
         smooth=s.to(torch.bfloat16),
@@ -160,7 +162,8 @@ def quantize(weight, bias=None, smooth=None, rank: int = 32, shift: float = 0.0,
     )
 
 
-def random_parts(N: int, K: int, device, generator=None, rank: int = 32, scale: float = 0.02, unsigned_input=False):
+def random_parts(N: int, K: int, device, generator=None, rank: int = 32, scale: float = 0.02, unsigned_input=False,
+                 scale_dtype=torch.bfloat16):
     """A W4A4 layer of the right shapes and value ranges without an SVD (random-init weights of the architecture,
     for the step benchmark): int4 in [-7, 7], group scales of a N(0, scale^2) weight, small low-rank factors."""
     g = generator  # a generator on `device` (or None: the global one of that device)
@@ -169,7 +172,7 @@ def random_parts(N: int, K: int, device, generator=None, rank: int = 32, scale: 
     wsc = (torch.rand(K // GROUP, N, **kw) * 0.5 + 0.75) * (3 * scale / 7)
     return dict(
         qweight=pack_weight(q),
-        wscales=wsc.to(torch.bfloat16),
+        wscales=wsc.to(scale_dtype),
         proj_down=(torch.randn(rank, K, **kw) * (1 / K ** 0.5)).to(torch.bfloat16),
         proj_up=(torch.randn(N, rank, **kw) * scale).to(torch.bfloat16),
         smooth=torch.ones(K, dtype=torch.bfloat16, device=device),
@@ -257,10 +260,11 @@ class FusedQKVAttention(torch.nn.Module):
 
 def pack_parts(logical: dict, device=None) -> dict:
     """Logical parts (q int [N, K], wscales [N, K/64], proj_down [K, r], proj_up [N, r], smooth [K], bias [N]) ->
-    wdl's packed layout, on `device`."""
+    wdl's packed layout, on `device`. fp16 weight scales stay fp16, any other type becomes bf16."""
     return dict(
         qweight=pack_weight(logical["q"]).to(device),
-        wscales=logical["wscales"].to(torch.bfloat16).t().contiguous().to(device),
+        wscales=logical["wscales"].to(logical["wscales"].dtype if logical["wscales"].dtype == torch.float16
+                                      else torch.bfloat16).t().contiguous().to(device),
         proj_down=logical["proj_down"].to(torch.bfloat16).t().contiguous().to(device),
         proj_up=logical["proj_up"].to(torch.bfloat16).contiguous().to(device),
         smooth=logical["smooth"].to(torch.bfloat16).to(device),
