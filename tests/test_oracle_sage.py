@@ -68,3 +68,36 @@ def test_online_softmax_restatement_equals_exact_softmax():
     exact = osage.attention_exact(Q, p["K"], p["V"])
     e_fp8 = osage.rel_err(osage.attention_quantized(p, 128 ** -0.5, p_fp8=True), exact)
     assert osage.rel_err(osage.attention_online(p, 128 ** -0.5), exact) <= 1.2 * e_fp8 + 1e-3
+
+
+def test_exact_attention_and_cross_attention_are_sdpa():
+    """attention_exact (and the block's cross-attention built on it) against torch's scaled_dot_product_attention in
+    float64, an independent library routine; a transposed V or a missing scale would fail."""
+    from oracle import block as oblock
+
+    g = torch.Generator().manual_seed(4)
+    Q = torch.randn(1, 21, 3, 128, generator=g).to(torch.bfloat16)
+    K = torch.randn(1, 37, 3, 128, generator=g).to(torch.bfloat16)
+    V = torch.randn(1, 37, 3, 128, generator=g).to(torch.bfloat16)
+    want = torch.nn.functional.scaled_dot_product_attention(
+        *(t.double().transpose(1, 2) for t in (Q, K, V))).transpose(1, 2)
+    assert (osage.attention_exact(Q, K.float(), V.float()).double() - want).abs().max() < 1e-6
+    got = oblock.cross_attention(Q.reshape(21, 384), K.reshape(37, 384), V.reshape(37, 384), 3)
+    assert torch.equal(got, want.reshape(21, 384).float().to(torch.bfloat16))
+
+
+def test_mapped_gather_is_the_explicit_index_loop():
+    """gather with the heads / tokens maps of sage_kv.attend: output (t, h) is cache row tokens[t], head heads[h],
+    times its scale, for t < at; then the chunk."""
+    g = torch.Generator().manual_seed(5)
+    cache = torch.randn(1, 12, 5, 4, generator=g).to(torch.float8_e4m3fn)
+    scale = torch.rand(1, 12, 5, 1, generator=g)
+    chunk = torch.randn(1, 3, 2, 4, generator=g)
+    heads, tokens = torch.tensor([4, 1], dtype=torch.int32), torch.tensor([7, 0, 11, 2, 9], dtype=torch.int32)
+    got = osage.gather(cache, scale, chunk, 4, heads, tokens)
+    assert got.shape == (1, 7, 2, 4)
+    for t in range(4):
+        for h in range(2):
+            r, c = int(tokens[t]), int(heads[h])
+            assert torch.equal(got[0, t, h], cache[0, r, c].float() * scale[0, r, c, 0])
+    assert torch.equal(got[0, 4:], chunk[0])
