@@ -189,17 +189,18 @@ def entropy_scale(keys: int, head_dim: int, ratio):
     return math.sqrt(math.log(keys) / math.log(keys * ratio) / head_dim)
 
 
-def attention_online(p: dict, sm_scale: float, block: int = 64, round_p: bool = True, splits: int = 2) -> torch.Tensor:
+def attention_online(p: dict, sm_scale: float, block: int = 64, round_p: bool = True, splits: int = 2,
+                     tau: float = 2.0) -> torch.Tensor:
     """The blockwise online-softmax restatement of the HIP kernel's arithmetic (fp32). In log2 units
     y = int dot * k_scale * c with c = q_scale * sm_scale * log2(e). The key blocks are split in `splits`
     contiguous parts (for two: the first ceil(full blocks / 2) blocks, then the rest, a partial final block
-    included), each run as an online softmax:
-    per 64-key block the running max m over y, P448 = 2^(y - m + log2 448) rounded to e4m3 for the PV product,
-    O = O * 2^(m_old - m) + P448_fp8 . V_fp8 (fp32), l = l * 2^(m_old - m) + sum P448 (unrounded). The parts merge
-    as O = sum_i O_i 2^(m_i - m), l = sum_i l_i 2^(m_i - m) with m = max_i m_i, and out = O / l * v_scale. Its exp2
-    is torch's, not the hardware's: P can differ by an ulp before rounding. round_p=False keeps P in fp32: then the
-    result is the exact softmax of attention_quantized up to fp32 rounding (the check that pins the online
-    rescaling and the merge)."""
+    included), each run as an online softmax with a lazy reference max m: per 64-key block with max mb, where
+    mb > m + tau the reference moves, m' = mb, and O, l are rescaled by 2^(m - m'); elsewhere m stays.
+    P448 = 2^(y - m + log2 448 - tau) (<= 448) is rounded to e4m3; O = O + P448_fp8 . V_fp8 and l = l + sum P448_fp8
+    (fp32). The parts merge as O = sum_i O_i 2^(m_i - m), l = sum_i l_i 2^(m_i - m) with m = max_i m_i, and
+    out = O / l * v_scale. Its exp2 is torch's, not the hardware's: P can differ by an ulp before rounding.
+    round_p=False keeps P in fp32 (in O and l): then the result is the exact softmax of attention_quantized up to
+    fp32 rounding, whatever tau (the check that pins the online rescaling and the merge)."""
     q, k = p["q"].float(), p["k"].float()
     B, n, H, D = q.shape
     L = k.shape[1]
@@ -218,13 +219,14 @@ def attention_online(p: dict, sm_scale: float, block: int = 64, round_p: bool = 
             b0, b1 = bi * block, min(L, (bi + 1) * block)
             I = torch.einsum("bnhd,blhd->bhnl", q.double(), k[:, b0:b1].double()).float()
             y = I * ks[:, :, None, b0:b1] * c[..., None]
-            mn = torch.maximum(m, y.amax(-1))
+            mb = y.amax(-1)
+            mn = torch.where(mb > m + tau, mb, m)
             alpha = torch.exp2(m - mn)
-            P = torch.exp2(y - mn[..., None] + log2_448)
+            O, l, m = O * alpha[..., None], l * alpha, mn
+            P = torch.exp2(y - m[..., None] + (log2_448 - tau))
             Pq = P.to(torch.float8_e4m3fn).float() if round_p else P
-            O = O * alpha[..., None] + torch.einsum("bhnl,blhd->bhnd", Pq.double(), vq[:, b0:b1].double()).float()
-            l = l * alpha + P.sum(-1)
-            m = mn
+            O = O + torch.einsum("bhnl,blhd->bhnd", Pq.double(), vq[:, b0:b1].double()).float()
+            l = l + Pq.sum(-1)
         parts.append((O, m, l))
     mt = parts[0][1]
     for _, mi, _ in parts[1:]:

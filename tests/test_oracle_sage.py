@@ -101,3 +101,28 @@ def test_mapped_gather_is_the_explicit_index_loop():
             r, c = int(tokens[t]), int(heads[h])
             assert torch.equal(got[0, t, h], cache[0, r, c].float() * scale[0, r, c, 0])
     assert torch.equal(got[0, 4:], chunk[0])
+
+
+def test_lazy_reference_max_keeps_the_exact_softmax():
+    """attention_online with P unrounded equals the exact softmax for every rescale threshold tau, on keys whose
+    scores grow block after block (so the reference max has to move past the first block: the data is checked for
+    that); with a dropped rescale or a wrong alpha the result would be off by far more than 1e-5."""
+    g = torch.Generator().manual_seed(6)
+    Q = torch.randn(1, 64, 1, 128, generator=g).to(torch.bfloat16)
+    grow = torch.linspace(0.2, 3.0, 320).reshape(1, 320, 1, 1)
+    K = (torch.randn(1, 320, 1, 128, generator=g) * grow + Q.float().mean(1, keepdim=True) * grow * 4)
+    V = torch.randn(1, 320, 1, 128, generator=g).to(torch.bfloat16)
+    z8 = torch.zeros(1, 1, 1, 128, dtype=torch.float8_e4m3fn)
+    z = torch.ones(1, 1, 1, 1)
+    p = osage.prep(Q, z8, z, z8, z, 0, K.to(torch.bfloat16), V)
+    ref = osage.attention_quantized(p, 128 ** -0.5)
+    y = torch.einsum("bnhd,blhd->bnl", Q.double(), K.double()) * 128 ** -0.5 * 1.4426950408889634
+    bmax = y.reshape(1, 64, 5, 64).amax(-1)
+    assert bool((bmax[..., 4] > bmax[..., 0] + 4).all())  # later blocks hold scores larger by more than 2^4
+    for tau in (0.0, 2.0, 8.0):
+        got = osage.attention_online(p, 128 ** -0.5, round_p=False, splits=1, tau=tau)
+        assert osage.rel_err(got, ref) < 1e-5, tau
+    # with P rounded to e4m3 the lazy max costs nothing measurable against exact attention
+    exact = osage.attention_exact(Q, p["K"], p["V"])
+    e0 = osage.rel_err(osage.attention_online(p, 128 ** -0.5, tau=0.0), exact)
+    assert osage.rel_err(osage.attention_online(p, 128 ** -0.5, tau=2.0), exact) <= 1.2 * e0 + 1e-3

@@ -3,9 +3,11 @@
 //
 //   s[q][t]  = q_scale[q] * k_scale[t] * (q_i8 . k_i8)               (exact int32 dot product, then fp32)
 //   O[q][d]  = sum_t softmax_t(s * sm_scale)[q][t] * v_fp8[t][d] * v_scale[d]
-// In log2 units y = s * sm_scale * log2(e); per 64-key block P448 = 2^(y - m + log2 448) (the e4m3 range folded into
-// the exponent: P448 <= 448) is rounded to e4m3 for the PV product, accumulated in fp32; the row sum l uses the
-// unrounded P448 and the output is O / l * v_scale.
+// In log2 units y = s * sm_scale * log2(e); per 64-key block P448 = 2^(y - m + log2 448 - TAU) is rounded to e4m3
+// for the PV product, accumulated in fp32, and the row sum l is the sum of the same rounded values; the output is
+// O / l * v_scale. The reference max m is lazy: it moves to the block's max only where that exceeds m by more than
+// TAU = 2 (then O and l are rescaled by 2^(m_old - m_new)), so P448 <= 448 always and most blocks rescale nothing.
+// (Only the e4m3 underflow threshold moves, by at most TAU bits: values below 2^-9 / 448 of the largest one.)
 //
 // Work split: one workgroup = 128 queries of one head and 8 waves: two groups of 4 waves split the key blocks in
 // halves (so every SIMD runs two waves), each wave owning 32 queries. A group streams its 64-key blocks of K
@@ -17,10 +19,11 @@
 //   S^T = K Q^T with v_mfma_i32_32x32x32_i8 (4 per 32x32 tile over d = 128), and
 //   O^T = V^T P^T with v_mfma_f32_32x32x64_f8f6f4 (one per 32 channels per 64-key block),
 // so a lane owns one query (lane % 32) throughout: the block max needs one exchange with lane ^ 32, and its 32
-// probabilities of a block are exactly the B operand of the PV product. Per score the vector work is an integer
-// max, a conversion, one fma, one exp2, one add and half a pack; the rescale of O by 2^(m_old - m_new) is skipped
-// when no lane's max moved, and key masking runs only in the final partial block. At the end the second group
-// hands (O, m, l) over through LDS and the first merges and writes.
+// probabilities of a block are exactly the B operand of the PV product; l comes from a fifth product of them with
+// an all-ones A operand. Per score the vector work is half an integer max (v_max3), a conversion, one fma, one
+// exp2 and half a pack; the rescale runs only in blocks where some lane's reference max moves, and key masking
+// only in the final partial block. At the end the second group hands (O, m, l) over through LDS and the first
+// merges and writes.
 // Layouts: q_i8 [n, H, 128] (row stride ldq) with q_scale [H, ceil(n/128)*32] (Sage's per-thread groups);
 // k_i8 [H, Lpad, 128] with k_scale [H, Lpad/16]; v_fp8 [H, 128, Lpad]; v_scale [H, 128]; out bf16 [n, H, 128]
 // (row stride ldo).
@@ -45,6 +48,10 @@ constexpr int GSTAGE = KT + VT;           // one group's share of a stage
 constexpr int STAGE = 2 * GSTAGE;
 constexpr int KS_MAX = 2048;              // k scales held in LDS: L <= 32768 keys
 constexpr float LOG2_448 = 8.807354922057604f;
+constexpr float TAU = 2.0f;               // lazy rescale threshold (log2 units)
+constexpr int ONES_E4M3 = 0x38383838;     // four e4m3 1.0
+constexpr int MAGIC_I = 0x4B400000;       // the bits of MAGIC_F = 1.5 * 2^23
+constexpr float MAGIC_F = 12582912.0f;
 constexpr int SLOT_FLOATS = 4 * (64 * 64 + 128);  // one partial: per wave [64 values][64 lanes] of O, m, l
 constexpr int MAX_WG = 2048;                       // workgroups of a split launch (one per CU)
 
@@ -122,7 +129,10 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
     const int kq[2] = {((0 + half) ^ swz) * 16, ((2 + half) ^ swz) * 16};      // chunk parity 0 / 1
     const int vq0 = ((2 * half) ^ swz) * 16, vq1 = ((2 * half + 1) ^ swz) * 16;
     const int rowoff = (lane % 32) * 64;
-    const i32x16 izero = {};
+    // the score accumulators start at the bits of 1.5 * 2^23, so the int32 sum s lands in them as the float
+    // 1.5 * 2^23 + s (exact for |s| < 2^22; |s| <= 127 * 127 * 128): no int-to-float conversion per score
+    const i32x16 imagic = {MAGIC_I, MAGIC_I, MAGIC_I, MAGIC_I, MAGIC_I, MAGIC_I, MAGIC_I, MAGIC_I,
+                           MAGIC_I, MAGIC_I, MAGIC_I, MAGIC_I, MAGIC_I, MAGIC_I, MAGIC_I, MAGIC_I};
     // group 1's hand-over area (stage 0 of the ring): per sub-wave [64 values][64 lanes] floats, then m and l
     float* xo = reinterpret_cast<float*>(smem) + sub * (64 * 64 + 128);
 
@@ -215,7 +225,10 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
         f32x16 o[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = f32x16{};
-        float m = -INFINITY, l = 0.0f;
+        // lv: the row sums of the rounded P448 from a fifth PV product against an all-ones A operand (every row of
+        // it holds the query's sum, so lv[0] is this lane's l over both lane halves)
+        f32x16 lv = {};
+        float m = -INFINITY;
 
         // mask_tag: std::true_type for the final block of a ragged L (keys >= L get P = 0), else std::false_type
         auto compute = [&](int st, int blk, auto mask_tag) {
@@ -232,7 +245,7 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
             i32x16 acc[2];
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                acc[j] = izero;
+                acc[j] = imagic;
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
                     acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
@@ -257,12 +270,26 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
                     if ((r % 4) < 2) mx0 = max(mx0, acc[j][r]);
                     else mx1 = max(mx1, acc[j][r]);
                 }
-            float mb = fmaxf(float(mx0) * kc0, float(mx1) * kc1);
+            float mb = fmaxf((__int_as_float(mx0) - MAGIC_F) * kc0, (__int_as_float(mx1) - MAGIC_F) * kc1);
             mb = fmaxf(mb, __shfl_xor(mb, 32));
-            const float mn = fmaxf(m, mb);
-            const float alpha = __builtin_amdgcn_exp2f(m - mn);
-            const float bias = LOG2_448 - mn;
-            float ls = 0.0f;
+            // lazy rescale: the reference max m moves (to the block max) only where the block max exceeds it by
+            // more than TAU, so P448 = 2^(y - m + log2 448 - TAU) stays <= 448 and O, l are rescaled in few blocks
+            const bool grow = mb > m + TAU;
+            if (__any(grow)) {
+                const float mn = grow ? mb : m;
+                const float alpha = __builtin_amdgcn_exp2f(m - mn);
+#pragma unroll
+                for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) o[ds][e] *= alpha;
+                lv[0] *= alpha;
+                m = mn;
+            }
+            const float bias = LOG2_448 - TAU - m;
+            // y - m + log2 448 - TAU = (1.5 * 2^23 + s) kc + (bias - 1.5 * 2^23 kc): the fma forms the product exactly,
+            // so the one extra rounding is the second term's (at most 0.75 kc, a relative 5e-7 kc/ulp of P: far
+            // below e4m3's steps)
+            const float bias0 = fmaf(-MAGIC_F, kc0, bias), bias1 = fmaf(-MAGIC_F, kc1, bias);
             i32x8 pf;
 #pragma unroll
             for (int wd = 0; wd < 8; ++wd) {
@@ -272,22 +299,14 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
                 for (int e = 0; e < 4; ++e) {
                     const int r = 4 * (wd % 4) + e;
                     // raw v_exp_f32: results below 2^-126 flush to 0 (below e4m3's range and the sum's precision)
-                    p[e] = __builtin_amdgcn_exp2f(fmaf(float(acc[j][r]), (r % 4) < 2 ? kc0 : kc1, bias));
+                    p[e] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(acc[j][r]), (r % 4) < 2 ? kc0 : kc1,
+                                                       (r % 4) < 2 ? bias0 : bias1));
                     if (MASK && acc[j][r] == INT32_MIN) p[e] = 0.0f;
-                    ls = ls + p[e];
                 }
                 // the low pair's conversion keeps the upper half of its old operand, which the high pair's then
                 // replaces: any register serves as the old value (p[0]'s bits: no zero to materialise)
                 const uint32_t word = __builtin_amdgcn_cvt_pk_fp8_f32(p[0], p[1], __float_as_int(p[0]), false);
                 pf[wd] = int(__builtin_amdgcn_cvt_pk_fp8_f32(p[2], p[3], word, true));
-            }
-            l = l * alpha + ls;
-            m = mn;
-            if (__any(alpha != 1.0f)) {
-#pragma unroll
-                for (int ds = 0; ds < 4; ++ds)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) o[ds][e] *= alpha;
             }
 #pragma unroll
             for (int ds = 0; ds < 4; ++ds) {
@@ -296,6 +315,8 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
                 const i32x8 vf = {int(v0.x), int(v0.y), int(v0.z), int(v0.w), int(v1.x), int(v1.y), int(v1.z), int(v1.w)};
                 o[ds] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pf, o[ds], 0, 0, 0, 0, 0, 0);
             }
+            const i32x8 ones = {ONES_E4M3, ONES_E4M3, ONES_E4M3, ONES_E4M3, ONES_E4M3, ONES_E4M3, ONES_E4M3, ONES_E4M3};
+            lv = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ones, pf, lv, 0, 0, 0, 0, 0, 0);
         };
 
 #pragma unroll
@@ -395,18 +416,17 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) xo[(ds * 16 + e) * 64 + lane] = o[ds][e];
             xo[64 * 64 + lane] = m;
-            xo[64 * 64 + 64 + lane] = l;
+            xo[64 * 64 + 64 + lane] = lv[0];
         }
         __syncthreads();
         float lt = 0.0f;
         if (dualwg) {
-            lt = l + __shfl_xor(l, 32);
+            lt = lv[0];
         } else if (grp == 0) {
             const float m1 = xo[64 * 64 + lane], l1 = xo[64 * 64 + 64 + lane];
             const float mt = fmaxf(m, m1);
             const float a0 = __builtin_amdgcn_exp2f(m - mt), a1 = __builtin_amdgcn_exp2f(m1 - mt);
-            const float lh = l * a0 + l1 * a1;
-            lt = lh + __shfl_xor(lh, 32);
+            lt = lv[0] * a0 + l1 * a1;
 #pragma unroll
             for (int ds = 0; ds < 4; ++ds)
 #pragma unroll
