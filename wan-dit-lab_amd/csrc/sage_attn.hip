@@ -271,7 +271,10 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
                     else mx1 = max(mx1, acc[j][r]);
                 }
             float mb = fmaxf((__int_as_float(mx0) - MAGIC_F) * kc0, (__int_as_float(mx1) - MAGIC_F) * kc1);
-            mb = fmaxf(mb, __shfl_xor(mb, 32));
+            {  // the other lane half's block max: v_permlane32_swap (no LDS round trip)
+                const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mb), __float_as_uint(mb), false, false);
+                mb = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+            }
             // lazy rescale: the reference max m moves (to the block max) only where the block max exceeds it by
             // more than TAU, so P448 = 2^(y - m + log2 448 - TAU) stays <= 448 and O, l are rescaled in few blocks
             const bool grow = mb > m + TAU;
