@@ -240,6 +240,16 @@ int wdl_sage_attn_q16(const void* q_bf16, int64_t ldq, const void* k_i8, const f
                       const float* v_scale, int64_t n, int64_t L, int64_t heads, float sm_scale, void* out,
                       int64_t ldo, void* workspace, wdl_stream_t stream);
 
+/* wdl_sage_attn_q16 with a block-causal mask per latent frame: the n queries are the chunk, the last n of the L
+ * keys (after L - n cached ones), and chunk query q sees keys [0, L - n + (q / frame_tokens + 1) frame_tokens), the
+ * cache and the chunk's frames up to its own. No counterpart in the reference, whose chunk attention sees the whole
+ * chunk (native/ops/sage_ops.cpp:15-16; generation/causal.py:269): the benchmark's chunk-causal attention mode.
+ * frame_tokens > 0, n <= L; the workspace is not used (may be NULL): every (query tile, head) runs whole. */
+int wdl_sage_attn_q16_framed(const void* q_bf16, int64_t ldq, const void* k_i8, const float* k_scale,
+                             const void* v_fp8, const float* v_scale, int64_t n, int64_t L, int64_t heads,
+                             float sm_scale, int64_t frame_tokens, void* out, int64_t ldo, void* workspace,
+                             wdl_stream_t stream);
+
 /* Elements (bf16) of each of the two operands wdl_attn_bf16_prep writes for L keys and `heads` heads. */
 int64_t wdl_attn_bf16_prep_elems(int64_t L, int64_t heads);
 

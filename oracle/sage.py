@@ -145,17 +145,28 @@ def prep(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, heads=None, tokens=N
                 K=Kf, V=Vf)
 
 
-def attention_quantized(p: dict, sm_scale: float, p_fp8: bool = False) -> torch.Tensor:
+def frame_mask(n: int, L: int, frame: int) -> torch.Tensor:
+    """bool [n, L]: the keys each of the n chunk queries sees under the block-causal mask per latent frame of
+    `frame` tokens, the chunk being the last n of the L keys: query q sees keys k < L - n + (q // frame + 1) frame
+    (all of them for frame 0)."""
+    q, k = torch.arange(n)[:, None], torch.arange(L)[None, :]
+    if not frame:
+        return torch.ones(n, L, dtype=torch.bool)
+    return k < torch.clamp(L - n + (q // frame + 1) * frame, max=L)
+
+
+def attention_quantized(p: dict, sm_scale: float, p_fp8: bool = False, frame: int = 0) -> torch.Tensor:
     """Softmax (float64) over the quantized operands -> fp32 [B, n, H, D]. p_fp8: P = exp(s - rowmax) rounded to
     e4m3 after scaling by 448 (the PV operand of an fp8 PV kernel), the denominator the unrounded row sum; this
-    is the baseline the reference measures its kernel against (sageattn also rounds P to fp8)."""
+    is the baseline the reference measures its kernel against (sageattn also rounds P to fp8). frame: the
+    block-causal per-frame mask of frame_mask (keys a query does not see get no weight)."""
     q, k = p["q"].double(), p["k"].double()
     B, n, H, D = q.shape
     L = k.shape[1]
     qs = expand_q_scale(p["q_scale"], n).double()  # [B, n, H]
     ks = expand_k_scale(p["k_scale"], L).double()  # [B, L, H]
     S = torch.einsum("bnhd,blhd->bhnl", q, k) * qs.permute(0, 2, 1)[..., None] * ks.permute(0, 2, 1)[:, :, None]
-    S = S * sm_scale
+    S = (S * sm_scale).masked_fill(~frame_mask(n, L, frame), float("-inf"))
     if p_fp8:
         E = torch.exp(S - S.amax(-1, keepdim=True))
         P = (E.float() * 448.0).to(torch.float8_e4m3fn).double() / 448.0 / E.sum(-1, keepdim=True)
@@ -165,11 +176,12 @@ def attention_quantized(p: dict, sm_scale: float, p_fp8: bool = False) -> torch.
     return torch.einsum("bhnl,blhd->bnhd", P, Vd).float()
 
 
-def attention_exact(Q, Kf, Vf, sm_scale=None) -> torch.Tensor:
-    """fp64 softmax(Q K^T * scale) V -> fp32 [B, n, H, D]."""
+def attention_exact(Q, Kf, Vf, sm_scale=None, frame: int = 0) -> torch.Tensor:
+    """fp64 softmax(Q K^T * scale) V -> fp32 [B, n, H, D] (frame: the mask of frame_mask)."""
     D = Q.shape[-1]
     sm_scale = D ** -0.5 if sm_scale is None else sm_scale
     S = torch.einsum("bnhd,blhd->bhnl", Q.double(), Kf.double()) * sm_scale
+    S = S.masked_fill(~frame_mask(Q.shape[1], Kf.shape[1], frame), float("-inf"))
     return torch.einsum("bhnl,blhd->bnhd", torch.softmax(S, -1), Vf.double()).float()
 
 
@@ -192,9 +204,9 @@ def entropy_scale(keys: int, head_dim: int, ratio):
 def attention_online(p: dict, sm_scale: float, block: int = 64, round_p: bool = True, splits: int = 2,
                      tau: float = 2.0) -> torch.Tensor:
     """The blockwise online-softmax restatement of the HIP kernel's arithmetic (fp32). In log2 units
-    y = int dot * k_scale * c with c = q_scale * sm_scale * log2(e). The key blocks are split in `splits`
-    contiguous parts (for two: the first ceil(full blocks / 2) blocks, then the rest, a partial final block
-    included), each run as an online softmax with a lazy reference max m: per 64-key block with max mb, where
+    y = int dot * k_scale * c with c = q_scale * sm_scale * log2(e). The key blocks (a partial final block
+    included) are split in `splits` contiguous parts (for two: the first ceil(blocks / 2), then the rest), each run
+    as an online softmax with a lazy reference max m: per 64-key block with max mb, where
     mb > m + tau the reference moves, m' = mb, and O, l are rescaled by 2^(m - m'); elsewhere m stays.
     P448 = 2^(y - m + log2 448 - tau) (<= 448) is rounded to e4m3; O = O + P448_fp8 . V_fp8 and l = l + sum P448_fp8
     (fp32). The parts merge as O = sum_i O_i 2^(m_i - m), l = sum_i l_i 2^(m_i - m) with m = max_i m_i, and
@@ -208,8 +220,8 @@ def attention_online(p: dict, sm_scale: float, block: int = 64, round_p: bool = 
     ks = expand_k_scale(p["k_scale"], L).float().permute(0, 2, 1)  # [B, H, L]
     vq = p["v"].float()  # fp8 codes as values [B, L, H, D]
     log2_448 = math.log2(448.0)
-    nblk, nfull = -(-L // block), L // block
-    bounds = [0, -(-nfull // 2), nblk] if splits == 2 else [0, nblk]
+    nblk = -(-L // block)
+    bounds = [0, -(-nblk // 2), nblk] if splits == 2 else [0, nblk]
     parts = []
     for s0, s1 in zip(bounds[:-1], bounds[1:]):
         m = torch.full((B, H, n), float("-inf"))

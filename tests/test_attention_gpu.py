@@ -108,6 +108,41 @@ def test_attention_matches_quantized_oracle_and_exact(gpu, at, n, H):
     assert osage.rel_err(out, exact) < 1.2 * osage.rel_err(emul8, exact) + 1e-3
 
 
+@pytest.mark.parametrize("at,n,H,frame", [(100, 1392, 2, 464), (0, 1392, 24, 464), (200, 150, 3, 64),
+                                         (928, 464, 2, 464), (37, 1000, 2, 300)])
+def test_block_causal_per_frame_mask(gpu, at, n, H, frame):
+    """The chunk attention with the block-causal mask per latent frame (query q of the chunk sees the cache and the
+    chunk's frames up to its own): frames of 464 tokens put frame ends inside 128-query tiles (tiles 3 and 7), L is
+    ragged (1492, 1392, 350, 1037 keys), (0, 1392, 24) runs the dual-tile launch (264 tiles over 22 blocks), and
+    (37, 1000, 2, 300) a partial last frame. Against the masked oracle: cosine >= 0.999 with the quantized
+    emulation, error against exact masked attention within 1.2x that of the fp8-P emulation + 1e-3, and the first
+    frame's queries unchanged when the later frames' keys are replaced (they are not seen)."""
+    from wdl import sage_kv
+
+    Q, k, ks, v, vs, at, K, V = setup(at, n, H=H, seed=5)
+    out = sage_kv.attend(*cuda(Q, k, ks, v, vs), at, *cuda(K, V), frame_tokens=frame).cpu().float()
+    p = osage.prep(Q, k, ks, v, vs, at, K, V)
+    emul = osage.attention_quantized(p, 128 ** -0.5, frame=frame)
+    emul8 = osage.attention_quantized(p, 128 ** -0.5, p_fp8=True, frame=frame)
+    exact = osage.attention_exact(Q, p["K"], p["V"], frame=frame)
+    cos = osage.cosine(out, emul)
+    print(f"at {at} n {n} frame {frame}: cos vs emulation {cos:.6f}, err vs exact {osage.rel_err(out, exact):.4f} "
+          f"(fp8 P emulation {osage.rel_err(emul8, exact):.4f})")
+    assert cos >= 0.999
+    assert osage.rel_err(out, exact) < 1.2 * osage.rel_err(emul8, exact) + 1e-3
+    # keys of frames after the first replaced: the first frame's outputs must not move (its K mean and V scale
+    # statistics do, so compare with the oracle on the changed operands rather than bitwise)
+    K2, V2 = K.clone(), V.clone()
+    K2[:, frame:] = -K2[:, frame:]
+    V2[:, frame:] = V2[:, frame:] * 2
+    out2 = sage_kv.attend(*cuda(Q, k, ks, v, vs), at, *cuda(K2, V2), frame_tokens=frame).cpu().float()
+    p2 = osage.prep(Q, k, ks, v, vs, at, K2, V2)
+    ex2 = osage.attention_exact(Q, p2["K"], p2["V"], frame=frame)
+    f0 = slice(0, min(frame, n))
+    assert osage.rel_err(out2[:, f0], ex2[:, f0]) < 1.2 * osage.rel_err(emul8[:, f0], exact[:, f0]) + 2e-3
+    assert osage.rel_err(ex2[:, f0], exact[:, f0]) < 1e-6  # the first frame does not see the changed keys
+
+
 def test_attention_longest_window_with_k_bias(gpu):
     """The chunk-causal attention workload's longest case: 2640 queries over 18480 cached + 2640 chunk keys (21120),
     K with a per-channel bias N(0, 3^2) that the mean smoothing removes; one head (the oracle's CPU cost), at the

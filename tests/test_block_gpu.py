@@ -188,7 +188,32 @@ def test_block_stages_given_identical_inputs(gpu, M, prior, grid, start):
     A = oblock.attention(Q.reshape(-1, D), dict(k=ck, ks=cks, v=ck, vs=cks, at=prior), K.reshape(-1, D),
                          V.reshape(-1, D), heads)
     Ag = sage_kv.attend(*(t.to(dev) for t in (Q, ck, cks, ck, cks)), prior, K.to(dev), V.to(dev)).cpu()
-    assert rel(Ag.reshape(M, D), A) <= 2e-3 and osage.cosine(Ag, A) >= 0.99999
+    # (128-query tile, head) pairs beyond the last whole multiple of the CU count (at 1392 queries, 264 on 256 CUs:
+    # the last head's tiles 3 .. 10) run split over all workgroups in pieces of a few key blocks, each piece with its
+    # own lazy reference max, which the oracle's two-part emulation does not follow: their P roundings differ (~1 %),
+    # so they are held to the Sage bars (cosine 0.9999 with the emulation, error against exact attention within
+    # 1.2x that of the fp8-P emulation + 1e-3), the whole tiles to cosine 0.99999 and 2e-3
+    Ag, A4 = Ag.reshape(M, heads, 128), A.reshape(M, heads, 128)
+    whole = torch.ones(M, heads, dtype=torch.bool)
+    qt, cus = -(-M // 128), torch.cuda.get_device_properties(0).multi_processor_count
+    T = qt * heads
+    if T > cus and (T + cus - 1) // cus * cus * 85 > T * 100 and -(-(prior + M) // 64) >= 32:
+        for tile in range(cus * (T // cus), T):
+            whole[128 * (tile % qt):128 * (tile % qt + 1), tile // qt] = False
+    print(f"attention stage: whole tiles rel {rel(Ag[whole], A4[whole]):.2e}"
+          + (f", split tiles rel {rel(Ag[~whole], A4[~whole]):.2e}" if (~whole).any() else ""))
+    assert rel(Ag[whole], A4[whole]) <= 2e-3 and osage.cosine(Ag[whole], A4[whole]) >= 0.99999
+    if (~whole).any():
+        assert osage.cosine(Ag[~whole], A4[~whole]) >= 0.9999
+        hs = sorted({int(h) for h in (~whole).nonzero()[:, 1]})
+        for h in hs:
+            sl = lambda t: t[:, :, h:h + 1].contiguous()
+            p = osage.prep(sl(Q), sl(ck), sl(cks), sl(ck), sl(cks), prior, sl(K), sl(V))
+            exact = osage.attention_exact(sl(Q), p["K"], p["V"])[0, :, 0]
+            emul8 = osage.attention_quantized(p, 128 ** -0.5, p_fp8=True)[0, :, 0]
+            rows = ~whole[:, h]
+            assert rel(Ag[rows, h], exact[rows]) <= 1.2 * rel(emul8[rows], exact[rows]) + 1e-3
+    Ag = Ag.reshape(M, D)
     assert rel(gpu_lin(A, "o"), oblock._lin(A, P["o"]).to(BF)) <= 1e-4
     xc = onorms.ln_mod(X, None, None, P["n3w"], P["n3b"])
     assert rel(gpu_lin(xc, "cq"), oblock._lin(xc, P["cq"]).to(BF)) <= 1e-4

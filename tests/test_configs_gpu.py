@@ -120,12 +120,13 @@ def test_norm_rope_on_the_704x1280_grid(gpu):
         assert torch.equal(got.cpu().reshape(1, M, 24, 128), want)
 
 
-@pytest.mark.parametrize("at", [0, 6600, 15840])
-def test_chunk_attention_at_24_heads(gpu, at):
+@pytest.mark.parametrize("at,frame", [(0, 0), (6600, 0), (15840, 0), (0, 880), (6600, 880)])
+def test_chunk_attention_at_24_heads(gpu, at, frame):
     """The full 24-head launch (2640 queries: 21 x 24 = 504 query tiles, the scheduling of this shape) over at
     cached FP8 keys + the 2640-token chunk, K with a per-channel bias; RoPE on the chunk's Q and K at start frame
-    at // 880. Heads 0 and 23 against the oracle: cosine >= 0.999 with the quantized emulation, error against exact
-    attention within 1.2x that of the fp8-P emulation + 1e-3."""
+    at // 880; frame 880: the block-causal mask per latent frame of the workload (each of the chunk's 3 frames sees
+    the cache and the frames up to its own). Heads 0 and 23 against the oracle: cosine >= 0.999 with the quantized
+    emulation, error against exact attention within 1.2x that of the fp8-P emulation + 1e-3."""
     from wdl import sage_kv
 
     H, n = 24, 2640
@@ -139,16 +140,17 @@ def test_chunk_attention_at_24_heads(gpu, at):
     cap = max(at, 1)
     kc, ksc = ofp8.quantize_rows(torch.randn(1, cap, H, 128, generator=g) + kbias)
     vc, vsc = ofp8.quantize_rows(torch.randn(1, cap, H, 128, generator=g))
-    out = sage_kv.attend(Q.cuda(), kc.cuda(), ksc.cuda(), vc.cuda(), vsc.cuda(), at, K.cuda(), V.cuda()).cpu().float()
+    out = sage_kv.attend(Q.cuda(), kc.cuda(), ksc.cuda(), vc.cuda(), vsc.cuda(), at, K.cuda(), V.cuda(),
+                         frame_tokens=frame).cpu().float()
     for hh in (0, H - 1):
         sl = lambda t: t[:, :, hh:hh + 1].contiguous()
         p = osage.prep(sl(Q), sl(kc), sl(ksc), sl(vc), sl(vsc), at, sl(K), sl(V))
-        emul = osage.attention_quantized(p, 128 ** -0.5)
-        emul8 = osage.attention_quantized(p, 128 ** -0.5, p_fp8=True)
-        exact = osage.attention_exact(sl(Q), p["K"], p["V"])
+        emul = osage.attention_quantized(p, 128 ** -0.5, frame=frame)
+        emul8 = osage.attention_quantized(p, 128 ** -0.5, p_fp8=True, frame=frame)
+        exact = osage.attention_exact(sl(Q), p["K"], p["V"], frame=frame)
         got = out[:, :, hh:hh + 1]
         cos, err = osage.cosine(got, emul), osage.rel_err(got, exact)
-        print(f"L={at + n} head {hh}: cos {cos:.6f}, err vs exact {err:.4f} (fp8-P emulation "
+        print(f"L={at + n} frame {frame} head {hh}: cos {cos:.6f}, err vs exact {err:.4f} (fp8-P emulation "
               f"{osage.rel_err(emul8, exact):.4f})")
         assert cos >= 0.999
         assert err < 1.2 * osage.rel_err(emul8, exact) + 1e-3

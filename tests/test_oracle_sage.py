@@ -126,3 +126,21 @@ def test_lazy_reference_max_keeps_the_exact_softmax():
     exact = osage.attention_exact(Q, p["K"], p["V"])
     e0 = osage.rel_err(osage.attention_online(p, 128 ** -0.5, tau=0.0), exact)
     assert osage.rel_err(osage.attention_online(p, 128 ** -0.5, tau=2.0), exact) <= 1.2 * e0 + 1e-3
+
+
+def test_frame_mask_is_each_query_over_its_own_keys():
+    """The block-causal per-frame mask: each chunk query's output equals exact attention over the keys it sees
+    (the cache and the chunk's frames up to its own), computed by slicing; frame 0 is no mask."""
+    g = torch.Generator().manual_seed(7)
+    n, at, F = 12, 10, 5  # a chunk of 12 queries in frames of 5 (the last frame partial) over 10 cached keys
+    Q = torch.randn(1, n, 2, 128, generator=g, dtype=torch.float64)
+    K = torch.randn(1, at + n, 2, 128, generator=g, dtype=torch.float64)
+    V = torch.randn(1, at + n, 2, 128, generator=g, dtype=torch.float64)
+    got = osage.attention_exact(Q, K, V, frame=F)
+    for q in range(n):
+        seen = min(at + (q // F + 1) * F, at + n)
+        want = osage.attention_exact(Q[:, q:q + 1], K[:, :seen], V[:, :seen])
+        assert torch.allclose(got[:, q:q + 1], want, atol=1e-6, rtol=0)
+    assert torch.equal(osage.attention_exact(Q, K, V, frame=0), osage.attention_exact(Q, K, V))
+    m = osage.frame_mask(n, at + n, F)
+    assert m.sum(1).tolist() == [15] * 5 + [20] * 5 + [22] * 2

@@ -20,10 +20,13 @@
 //   O^T = V^T P^T with v_mfma_f32_32x32x64_f8f6f4 (one per 32 channels per 64-key block),
 // so a lane owns one query (lane % 32) throughout: the block max needs one exchange with lane ^ 32, and its 32
 // probabilities of a block are exactly the B operand of the PV product; l comes from a fifth product of them with
-// an all-ones A operand. Per score the vector work is half an integer max (v_max3), a conversion, one fma, one
-// exp2 and half a pack; the rescale runs only in blocks where some lane's reference max moves, and key masking
-// only in the final partial block. At the end the second group hands (O, m, l) over through LDS and the first
-// merges and writes.
+// an all-ones A operand. Per score the vector work is half an integer max (v_max3), one fma (the int32 sum lands
+// in an accumulator started at the bits of 1.5 * 2^23, so it is already a float), one exp2 and half a pack; the
+// rescale runs only in blocks where some lane's reference max moves. Key masking runs only in the blocks that
+// hold keys some query of the tile does not see: a ragged final block (L % 64 != 0), and with the block-causal
+// per-frame mode (frame > 0: query q of the chunk, the last n of the L keys, sees the keys before its own frame's
+// end) the blocks between the tile's first and last queries' limits. At the end the second group hands (O, m, l)
+// over through LDS and the first merges and writes.
 // Layouts: q_i8 [n, H, 128] (row stride ldq) with q_scale [H, ceil(n/128)*32] (Sage's per-thread groups);
 // k_i8 [H, Lpad, 128] with k_scale [H, Lpad/16]; v_fp8 [H, 128, Lpad]; v_scale [H, 128]; out bf16 [n, H, 128]
 // (row stride ldo).
@@ -73,7 +76,16 @@ struct AttnArgs {
     int64_t D;            // tiles run whole (the first D of the T = qtiles * H); the other T - D are split
     const uint16_t* qb;   // bf16 Q [n, H, 128] (row stride ldq) quantized in the kernel, or null (q, q_scale given)
     int64_t dual;         // workgroups 0 .. dual - 1 run two whole tiles, one per group (D == T; else 0)
+    int64_t frame;        // > 0: block-causal per latent frame of `frame` tokens (query q sees keys below
+                          // L - n + (q / frame + 1) frame); 0: every query sees all L keys
 };
+
+// Keys [0, limit) that query qq sees.
+__device__ __forceinline__ int64_t key_limit(const AttnArgs& a, int64_t qq) {
+    if (a.frame <= 0) return a.L;
+    const int64_t lim = a.L - a.n + (qq / a.frame + 1) * a.frame;
+    return lim < a.L ? lim : a.L;
+}
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return uint32_t(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
@@ -111,7 +123,6 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
     float* sVs = sVs_[grp];
     const int64_t qblocks8 = (a.n + 127) / 128 * 32;
     const int64_t nblk = a.Lpad / 64, nks = a.Lpad / 16;
-    const bool ragged = (a.L % 64) != 0;
     // Work of workgroup w: the whole tiles w, w + W, .. below D (their output written directly), then its share
     // [s0, s1) of the key blocks of the R = T - D remaining tiles, laid end to end (each piece's partial softmax
     // state goes to the workspace slot 2w for its first piece, 2w + 1 for a second; attn_merge_kernel combines them)
@@ -180,15 +191,26 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
         i32x4 qf[4];
         float cq;
 
-        // full key blocks of the segment [b0, fe), split in halves between the groups; both groups run `iters`
-        // ring steps. A ragged final block (L % 64 != 0) in the segment is group 1's, in a masked step after it.
-        const bool ragged_here = ragged && b1 == nblk;
+        // The tile's keys: query q sees keys [0, key_limit(q)); the tile needs blocks [0, nbt) (its last query's
+        // limit) and blocks from fet on hold keys some of its queries do not see (its first query's limit; with
+        // no frames, only a ragged final block when L % 64 != 0): those run the masked step.
         // (32-bit ring counters: uniform 64-bit compares would run on the vector unit; blocks < 2^9)
-        const int fe = int(ragged_here ? nblk - 1 : b1), ib0 = int(b0);
-        const int nfull = fe - ib0, nb0 = dualwg ? nfull : (nfull + 1) / 2;
-        const int first = grp == 0 || dualwg ? ib0 : ib0 + nb0, count = grp == 0 || dualwg ? nb0 : nfull - nb0;
+        const int64_t qlast = qt * 128 + 127 < a.n ? qt * 128 + 127 : a.n - 1;
+        const int nbt = int((key_limit(a, qlast) + 63) / 64), fet = int(key_limit(a, qt * 128) / 64);
+        const int64_t lim = key_limit(a, qlive ? q : a.n - 1);  // this lane's query
+        // the segment's blocks [b0, bend), split in halves between the groups (both run `iters` ring steps); in a
+        // dual workgroup each group runs all the blocks of its own tile and the steps are the longer tile's
+        const int ib0 = int(b0), bend = int(b1) < nbt ? int(b1) : nbt, nblocks = bend - ib0;
+        int nb0 = (nblocks + 1) / 2, iters = nb0;
+        if (dualwg) {
+            const int64_t other = 2 * w + 1 - grp, oqt = other % a.qtiles;
+            const int64_t olast = oqt * 128 + 127 < a.n ? oqt * 128 + 127 : a.n - 1;
+            const int onbt = int((key_limit(a, olast) + 63) / 64);
+            nb0 = nblocks;
+            iters = nblocks > onbt ? nblocks : onbt;
+        }
+        const int first = grp == 0 || dualwg ? ib0 : ib0 + nb0, count = grp == 0 || dualwg ? nb0 : nblocks - nb0;
         const int last = count > 0 ? first + count - 1 : ib0;
-        const int iters = nb0;
 
         // this lane's load offsets inside a block (block b of the head starts at kbase + 64 D b for K, at
         // vbase + 64 b for V: wave-uniform bases)
@@ -230,7 +252,8 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
         f32x16 lv = {};
         float m = -INFINITY;
 
-        // mask_tag: std::true_type for the final block of a ragged L (keys >= L get P = 0), else std::false_type
+        // mask_tag: std::true_type for blocks at or after fet (keys >= the lane's limit get P = 0), else
+        // std::false_type
         auto compute = [&](int st, int blk, auto mask_tag) {
             constexpr bool MASK = decltype(mask_tag)::value;
             const uint8_t* K = smem + st * STAGE + grp * GSTAGE;
@@ -260,7 +283,7 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
                 for (int j = 0; j < 2; ++j)
 #pragma unroll
                     for (int r = 0; r < 16; ++r)
-                        if (blk * 64 + 32 * j + 8 * (r / 4) + 4 * half + r % 4 >= a.L) acc[j][r] = INT32_MIN;
+                        if (blk * 64 + 32 * j + 8 * (r / 4) + 4 * half + r % 4 >= lim) acc[j][r] = INT32_MIN;
             }
             int mx0 = INT32_MIN, mx1 = INT32_MIN;
 #pragma unroll
@@ -270,7 +293,12 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
                     if ((r % 4) < 2) mx0 = max(mx0, acc[j][r]);
                     else mx1 = max(mx1, acc[j][r]);
                 }
-            float mb = fmaxf((__int_as_float(mx0) - MAGIC_F) * kc0, (__int_as_float(mx1) - MAGIC_F) * kc1);
+            float mb0 = (__int_as_float(mx0) - MAGIC_F) * kc0, mb1 = (__int_as_float(mx1) - MAGIC_F) * kc1;
+            if (MASK) {  // a half with every key masked has no maximum (-inf: the reference max does not move)
+                mb0 = mx0 == INT32_MIN ? -INFINITY : mb0;
+                mb1 = mx1 == INT32_MIN ? -INFINITY : mb1;
+            }
+            float mb = fmaxf(mb0, mb1);
             {  // the other lane half's block max: v_permlane32_swap (no LDS round trip)
                 const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mb), __float_as_uint(mb), false, false);
                 mb = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
@@ -280,7 +308,8 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
             const bool grow = mb > m + TAU;
             if (__any(grow)) {
                 const float mn = grow ? mb : m;
-                const float alpha = __builtin_amdgcn_exp2f(m - mn);
+                // 1 where m stays (m may still be -inf for a lane that has seen only masked keys: no -inf - -inf)
+                const float alpha = grow ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
 #pragma unroll
                 for (int ds = 0; ds < 4; ++ds)
 #pragma unroll
@@ -391,26 +420,20 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
             if (tg < D) sVs[tg] = vsr;
             head_loaded = h;
         }
-        for (int i0 = 0; i0 < iters; i0 += STAGES) {
-#pragma unroll
-            for (int k = 0; k < STAGES; ++k) {
-                const int i = i0 + k;
-                if (i >= iters) break;
-                wait_vmcnt<(STAGES - 2) * LPB>();
-                __syncthreads();
-                issue((k + STAGES - 1) % STAGES, i + STAGES - 1);
-                if (i < count) compute(k, first + i, std::false_type{});
-            }
-        }
+        // ring step i: wait for block i, refill the stage block i - 1 used, compute block i (the group's blocks
+        // before fet unmasked, the rest masked: two loops, so each holds only its own variant's registers)
+        auto step = [&](int i, auto mask_tag) {
+            wait_vmcnt<(STAGES - 2) * LPB>();
+            __syncthreads();
+            const int st = i % STAGES;
+            issue((st + STAGES - 1) % STAGES, i + STAGES - 1);
+            if (i < count) compute(st, first + i, mask_tag);
+        };
+        const int split = fet - first < 0 ? 0 : (fet - first < iters ? fet - first : iters);
+        for (int i = 0; i < split; ++i) step(i, std::false_type{});
+        for (int i = split; i < iters; ++i) step(i, std::true_type{});
         wait_vmcnt<0>();
         __syncthreads();  // all loads landed, every wave is done with the ring, sKs written
-        if (ragged_here) {  // the final, partial block: group 1, keys >= L masked
-            if (grp == 1 || dualwg) load_block(0, nblk - 1);
-            wait_vmcnt<0>();
-            __syncthreads();
-            if (grp == 1 || dualwg) compute(0, nblk - 1, std::true_type{});
-            __syncthreads();  // group 1 is done reading stage 0 before the hand-over overwrites it
-        }
 
         // group 1 hands (O, m, l) to group 0, which merges: O = O0 2^(m0 - m) + O1 2^(m1 - m), l likewise
         if (grp == 1 && !dualwg) {
@@ -549,7 +572,8 @@ extern "C" int64_t wdl_sage_attn_workspace_bytes(int64_t n, int64_t L, int64_t h
 
 static int attn_launch(const void* q_i8, const float* q_scale, const void* q_bf16, int64_t ldq, const void* k_i8,
                        const float* k_scale, const void* v_fp8, const float* v_scale, int64_t n, int64_t L,
-                       int64_t heads, float sm_scale, void* out, int64_t ldo, void* workspace, hipStream_t stream) {
+                       int64_t heads, float sm_scale, void* out, int64_t ldo, void* workspace, hipStream_t stream,
+                       int64_t frame = 0) {
     const void* q = q_bf16 ? q_bf16 : q_i8;
     const int64_t qbytes = q_bf16 ? 2 : 1;
     if (n < 0 || L < 1 || heads <= 0 || ldq < heads * D || ldo < heads * D)
@@ -558,6 +582,9 @@ static int attn_launch(const void* q_i8, const float* q_scale, const void* q_bf1
         return fail(WDL_EINVAL, "sage_attn: null pointer");
     if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) | (ldq * qbytes) | (ldo * 2)) % 16)
         return fail(WDL_EINVAL, "sage_attn: unaligned rows");
+    if (frame < 0 || (frame > 0 && n > L))
+        return fail(WDL_EINVAL, "sage_attn: frame=%lld needs the n=%lld queries' own keys among the L=%lld",
+                    (long long)frame, (long long)n, (long long)L);
     if (n == 0) return WDL_OK;
     const int64_t Lpad = (L + 63) / 64 * 64;
     if (Lpad / 16 > KS_MAX) return fail(WDL_EINVAL, "sage_attn: L=%lld above %d keys", (long long)L, KS_MAX * 16);
@@ -573,11 +600,12 @@ static int attn_launch(const void* q_i8, const float* q_scale, const void* q_bf1
     // blocks between the groups), so the tiles take one round instead of two.
     int64_t W = T, Dw = T, dual = 0;
     const int64_t cus = cu_count();
-    if (cus > 0 && cus <= MAX_WG && T > cus && nblk >= 32) {
+    // (under the per-frame mask tiles differ in key count: none is split)
+    if (frame == 0 && cus > 0 && cus <= MAX_WG && T > cus && nblk >= 32) {
         const int64_t rounds = (T + cus - 1) / cus;
         const int64_t usk = (T % cus) * nblk;  // key blocks of the split tiles
         if (T * 100 < 85 * rounds * cus && (cus + 1) * usk < (int64_t(1) << 31)) W = cus, Dw = cus * (T / cus);
-    } else if (cus > 0 && T > cus && T <= 2 * cus) {
+    } else if (cus > 0 && T > cus && T <= 2 * cus && (nblk < 32 || cus > MAX_WG)) {
         W = cus, dual = T - cus;
     }
     if (Dw < T && (!workspace || reinterpret_cast<uintptr_t>(workspace) % 16))
@@ -585,7 +613,8 @@ static int attn_launch(const void* q_i8, const float* q_scale, const void* q_bf1
     float* part = Dw < T ? static_cast<float*>(workspace) : nullptr;
     AttnArgs a{static_cast<const int8_t*>(q_i8), ldq, q_scale, static_cast<const int8_t*>(k_i8), k_scale,
                static_cast<const uint8_t*>(v_fp8), v_scale, static_cast<uint16_t*>(out), ldo, n, L, Lpad, heads,
-               sm_scale * 1.4426950408889634f, part, W, qtiles, Dw, static_cast<const uint16_t*>(q_bf16), dual};
+               sm_scale * 1.4426950408889634f, part, W, qtiles, Dw, static_cast<const uint16_t*>(q_bf16), dual,
+               frame};
     sage_attn_kernel<<<unsigned(W), 512, 0, stream>>>(a);
     int rc = check_launch("sage_attn");
     if (rc || Dw == T) return rc;
@@ -608,4 +637,14 @@ extern "C" int wdl_sage_attn_q16(const void* q_bf16, int64_t ldq, const void* k_
     if (!q_bf16) return fail(WDL_EINVAL, "sage_attn_q16: null pointer");
     return attn_launch(nullptr, nullptr, q_bf16, ldq, k_i8, k_scale, v_fp8, v_scale, n, L, heads, sm_scale, out, ldo,
                        workspace, stream);
+}
+
+extern "C" int wdl_sage_attn_q16_framed(const void* q_bf16, int64_t ldq, const void* k_i8, const float* k_scale,
+                                        const void* v_fp8, const float* v_scale, int64_t n, int64_t L, int64_t heads,
+                                        float sm_scale, int64_t frame_tokens, void* out, int64_t ldo,
+                                        void* workspace, hipStream_t stream) {
+    if (!q_bf16) return fail(WDL_EINVAL, "sage_attn_q16_framed: null pointer");
+    if (frame_tokens <= 0) return fail(WDL_EINVAL, "sage_attn_q16_framed: frame_tokens must be positive");
+    return attn_launch(nullptr, nullptr, q_bf16, ldq, k_i8, k_scale, v_fp8, v_scale, n, L, heads, sm_scale, out, ldo,
+                       workspace, stream, frame_tokens);
 }

@@ -53,6 +53,8 @@ SIGNATURES: dict[str, list] = {
                       c_ptr, c_ptr],
     "wdl_sage_attn_q16": [c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_f32, c_ptr, c_i64,
                           c_ptr, c_ptr],
+    "wdl_sage_attn_q16_framed": [c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_f32, c_i64, c_ptr,
+                                 c_i64, c_ptr, c_ptr],
     "wdl_rope3d_rotate": [c_ptr, c_int, c_i64p, c_ptr, c_int, c_i64p, c_i64, c_i64, c_i64, c_i64, c_i64, c_i32p,
                           c_i64, c_int, c_ptr, c_int, c_ptr],
     "wdl_attn_bf16_prep_elems": [c_i64, c_i64],

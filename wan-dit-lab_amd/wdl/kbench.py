@@ -53,6 +53,30 @@ def attention():
         print(f"attention n={n} L={L}: {us:.1f} us ({4 * n * L * 128 * H / us / 1e6:.0f} TOP/s)", flush=True)
 
 
+def chunk():
+    """The chunk-causal attention workload at 704x1280: 2640 queries (3 frames of 880) over 6600 / 15840 cached +
+    the chunk's keys, 24 heads, without and with the block-causal mask per latent frame."""
+    import torch
+
+    from wdl import ops
+
+    dev, H, n = "cuda", 24, 2640
+    g = torch.Generator(device=dev).manual_seed(0)
+    for at in (6600, 15840):
+        L = at + n
+        ck = (torch.randn(1, at, H, 128, device=dev, generator=g) * 50).clamp(-448, 448).to(torch.float8_e4m3fn)
+        cks = torch.rand(1, at, H, 1, device=dev, generator=g) * 0.02
+        K, V, Q = (torch.randn(n, H * 128, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+        prep = ops.sage_prep_launch(ck.view(torch.uint8), cks, ck.view(torch.uint8), cks, K, V, at)
+        out = torch.empty(n, H * 128, device=dev, dtype=torch.bfloat16)
+        for frame in (0, 880):
+            us = _replay_us(lambda: ops.sage_attn_q16_launch(Q, prep, L, 128 ** -0.5, out, frame_tokens=frame))
+            # the masked workload: each query's visible keys
+            keys = n * L if not frame else sum(min(L, at + (q // frame + 1) * frame) for q in range(0, n, 16)) * 16
+            print(f"chunk attention n={n} L={L} frame={frame}: {us:.1f} us ({4 * keys * 128 * H / us / 1e6:.0f} "
+                  f"TOP/s over the visible keys)", flush=True)
+
+
 def cross():
     """The cross-attention of the step (1392 queries over 512 prompt keys, 24 x 128 heads): bf16 attention (the
     reference's SDPA semantics) and Sage (int8 QK, fp8 PV), each over K / V laid out once."""
@@ -144,7 +168,7 @@ def main(argv):
         from wdl import _lib
 
         _lib.LIB_PATH = Path(argv[2])
-    {"attention": attention, "cross": cross, "prep": prep, "gemm": gemm, "quant": quant}[argv[1]]()
+    {"attention": attention, "chunk": chunk, "cross": cross, "prep": prep, "gemm": gemm, "quant": quant}[argv[1]]()
 
 
 if __name__ == "__main__":

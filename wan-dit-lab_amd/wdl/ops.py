@@ -434,15 +434,24 @@ def sage_attn_launch(q_i8, q_scale, prep, L, sm_scale, out=None):
     return out
 
 
-def sage_attn_q16_launch(Q, prep, L, sm_scale, out=None):
+def sage_attn_q16_launch(Q, prep, L, sm_scale, out=None, frame_tokens=0):
     """Q bf16 [n, H*128] (row-strided) -> bf16 [n, H*128]: Sage attention with the int8 quantization of Q done in
-    the kernel (bit-identical to quant_q_launch followed by sage_attn_launch)."""
+    the kernel (bit-identical to quant_q_launch followed by sage_attn_launch). frame_tokens > 0: block-causal per
+    latent frame, the n queries being the last n of the L keys (query q sees keys below L - n + (q // frame_tokens
+    + 1) * frame_tokens)."""
     n = Q.shape[0]
     H = Q.shape[1] // 128
     if Q.dtype != torch.bfloat16 or Q.dim() != 2 or Q.shape[1] % 128 or Q.stride(1) != 1:
         raise ValueError("sage_attn_q16: Q must be bf16 [n, H*128] with unit column stride")
     if out is None:
         out = torch.empty(n, H * 128, device=Q.device, dtype=torch.bfloat16)
+    if frame_tokens:
+        if not isinstance(frame_tokens, int) or frame_tokens < 0 or n > L:
+            raise ValueError("sage_attn_q16: frame_tokens must be a positive int and the queries among the keys")
+        _lib.call("wdl_sage_attn_q16_framed", ptr(Q), Q.stride(0), ptr(prep["k"]), ptr(prep["k_scale"]),
+                  ptr(prep["v"]), ptr(prep["v_scale"]), n, L, H, float(sm_scale), frame_tokens, ptr(out),
+                  out.stride(0), 0, stream_of(Q))
+        return out
     ws = workspace(_ATTN_WS, Q.device, _lib.library().wdl_sage_attn_workspace_bytes(n, L, H))
     _lib.call("wdl_sage_attn_q16", ptr(Q), Q.stride(0), ptr(prep["k"]), ptr(prep["k_scale"]), ptr(prep["v"]),
               ptr(prep["v_scale"]), n, L, H, float(sm_scale), ptr(out), out.stride(0), ptr(ws), stream_of(Q))

@@ -49,12 +49,26 @@ def _check(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, heads=None, tokens
         raise ValueError("heads must be contiguous [.., heads, 128] rows")
 
 
-def attend(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, sm_scale=None, heads=None, tokens=None):
+def attend(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, sm_scale=None, heads=None, tokens=None,
+           frame_tokens=0):
     """softmax(Q K^T * sm_scale) V over the cached tokens and the chunk (sage_kv.py:127-134); [1, nq, H, 128] bf16
     (sm_scale defaults to 128^-0.5). heads (int32 [H]): head h of Q, K, V is cache head heads[h], the cache keeping
     all of them; tokens (int32 [at]): cached token i is cache row tokens[i] (KVCache.attend_split's static heads,
-    causal.py:222-241). Neither copies the cache. The maps' ranges are checked on the host (one synchronisation)."""
+    causal.py:222-241). Neither copies the cache. The maps' ranges are checked on the host (one synchronisation).
+    frame_tokens > 0 (not a mode of the reference, whose chunk attention sees the whole chunk): block-causal per
+    latent frame of that many tokens, Q being the chunk (nq == n): chunk query q sees the cache and the chunk's
+    frames up to its own, keys below at + (q // frame_tokens + 1) * frame_tokens."""
     _check(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, heads, tokens)
+    if frame_tokens:
+        if not isinstance(frame_tokens, int) or frame_tokens < 0 or Q.shape[1] != K.shape[1]:
+            raise ValueError("frame_tokens: a positive int, with the chunk's own queries (nq == n)")
+        from wdl import ops
+
+        n, H = K.shape[1], K.shape[2]
+        prep = ops.sage_prep_launch(cache_k.view(torch.uint8), cache_ks, cache_v.view(torch.uint8), cache_vs,
+                                    K[0].flatten(1), V[0].flatten(1), at, heads=heads, tokens=tokens)
+        sm = Q.shape[-1] ** -0.5 if sm_scale is None else float(sm_scale)
+        return ops.sage_attn_q16_launch(Q[0].flatten(1), prep, at + n, sm, frame_tokens=frame_tokens).view(Q.shape)
     return sage_kv_attend(Q, cache_k.view(torch.uint8), cache_ks, cache_v.view(torch.uint8), cache_vs, K, V, at,
                           Q.shape[-1] ** -0.5 if sm_scale is None else float(sm_scale), heads, tokens)
 
