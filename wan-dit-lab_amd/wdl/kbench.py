@@ -162,8 +162,8 @@ def quant():
 
 
 def main(argv):
-    if len(argv) < 2 or argv[1] not in ("attention", "cross", "prep", "gemm", "quant"):
-        raise SystemExit("usage: python -m wdl.kbench attention|cross|prep|gemm|quant [library path]")
+    if len(argv) < 2 or argv[1] not in ("attention", "chunk", "cross", "prep", "gemm", "quant"):
+        raise SystemExit("usage: python -m wdl.kbench attention|chunk|cross|prep|gemm|quant [library path]")
     if len(argv) > 2:
         from wdl import _lib
 
