@@ -159,6 +159,16 @@ int wdl_fp8_quantize(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t
 int wdl_fp8_gemm(const void* xq, const float* x_scale, const void* wq, const float* w_scale, const void* bias,
                  int64_t M, int64_t Mp, int64_t N, int64_t K, int rows, void* out, int64_t ldo, wdl_stream_t stream);
 
+/* FP8 weight-only linear: out = bf16(w_scale[n] * sum_k x[m][k] w[n][k] + bias[n]) (epilogue 0), or the gated
+ * residual out = bf16(out + bf16(y) * gate[n]) in place (epilogue 2). x bf16 [M, ldx] (ldx % 8 == 0), w e4m3 [N, K]
+ * row-major, w_scale fp32 [N] (scale_rows != 0) or [1], bias bf16 [N] or NULL, gate fp32 [N]; out bf16 [M, ldo]
+ * (ldo % 4 == 0). Products of bf16 and e4m3 values are exact; sums in fp32 on the bf16 matrix cores. N % 128 == 0,
+ * K % 64 == 0; x and w 16-byte aligned, out 8-byte. No counterpart in the reference, whose FP8 linears are W8A8
+ * (quantization/fp8.py:1-6): the attention projections of the benchmark's mixed-precision mode. */
+int wdl_fp8wo_gemm(const void* x, int64_t ldx, const void* w, const float* w_scale, int scale_rows, const void* bias,
+                   int64_t M, int64_t N, int64_t K, void* out, int64_t ldo, int epilogue, const float* gate,
+                   wdl_stream_t stream);
+
 /* Q/K RMSNorm over all heads + 3D RoPE, fused. Replaces norm_q / norm_k (src/wan_dit_lab/models/rms_norm.py:10-13,
  * used at src/wan_dit_lab/quantization/w4a4.py:256-257) and rope_apply / wan_dit_lab::rope3d_rotate
  * (src/wan_dit_lab/models/rope.py:12-31; src/wan_dit_lab/kernels/rope_triton.py:66-81, 101-144).

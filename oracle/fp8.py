@@ -4,6 +4,9 @@
 - quantize_rows (fp8.py:37-41): the same per last-dim row; the KV cache's rule (generation/causal.py:177-184).
 - w8a8_linear_rows (fp8.py:58-62): unit-scale fp8 product, then y * (xs ⊗ ws) + b.
 - w8a8_linear_tensor (fp8.py:32-33 / 60): per-tensor scales.
+- w8a16_linear: the weight-only FP8 linear of the mixed-precision mode (no counterpart in the reference, whose FP8
+  linears are W8A8): the weight quantized by quantize_rows (or quantize), the activation kept in bf16,
+  y = bf16(scale * (x . w_fp8) + b) with the product in float64.
 
 The e4m3 rounding is torch's CPU conversion (the reference's own rule). Pinned by:
 - the reference's known answers (tests/test_cache_fp8.py:47-58, 150-158: 84.021 -> 88, never 80 through fp16;
@@ -84,6 +87,17 @@ def w8a8_linear_tensor(x: torch.Tensor, W: torch.Tensor, b: torch.Tensor | None)
     fp32, one bf16 rounding."""
     (xq, xs), (wq, ws) = quantize(x), quantize(W)
     y = (xq.double() @ wq.double().t()).float() * (xs * ws)
+    if b is not None:
+        y = y + b.float()
+    return y.to(torch.bfloat16)
+
+
+def w8a16_linear(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, b: torch.Tensor | None):
+    """The weight-only FP8 linear: x bf16 [M, K], e4m3 weight [N, K] with fp32 scales [N, 1] or a 0-d / [1] one ->
+    bf16 [M, N] = bf16(scale_n * sum_k x_mk w_nk + b_n): the sum in float64 (its products are exact), the scale and
+    the bias in fp32 as the kernel applies them."""
+    y = (x.double() @ wq.double().t()).float()
+    y = y * ws.reshape(1, -1).float()
     if b is not None:
         y = y + b.float()
     return y.to(torch.bfloat16)

@@ -56,3 +56,19 @@ def test_rows_scale_is_amax_over_448_and_values_reconstruct():
     assert torch.equal(q.float().abs().amax(-1), torch.full((5, 7, 3), 448.))  # the row max lands on 448
     rel = ((q.float() * s) - x.float()).abs() / x.float().abs().clamp(min=1e-3)
     assert float(rel[x.float().abs() > s * 2 ** -6 * 448].max()) <= 2 ** -4  # e4m3: 3 mantissa bits, half-ulp
+
+
+def test_weight_only_linear_known_answer():
+    """w8a16_linear with x the identity: row k of the result is column k of the dequantized weight (times its row
+    scale) plus the bias, so a transposed weight or a dropped scale fails."""
+    from oracle import fp8 as ofp8
+
+    g = torch.Generator().manual_seed(2)
+    W = torch.randn(128, 64, generator=g)
+    wq, ws = ofp8.quantize_rows(W)
+    b = torch.randn(128, generator=g).to(torch.bfloat16)
+    y = ofp8.w8a16_linear(torch.eye(64).to(torch.bfloat16), wq, ws, b)
+    want = (wq.float() * ws).t() + b.float()
+    assert torch.equal(y, want.to(torch.bfloat16))
+    # the codes are the nearest e4m3 values of W / scale (the brute-force search)
+    assert np.array_equal(wq.view(torch.uint8).numpy().ravel(), ofp8.e4m3_nearest((W / ws).numpy()))

@@ -40,6 +40,8 @@ SIGNATURES: dict[str, list] = {
     "wdl_fp8_quantize_workspace_floats": [c_i64, c_i64],
     "wdl_fp8_quantize": [c_ptr, c_int, c_i64, c_i64, c_i64, c_i64, c_int, c_ptr, c_ptr, c_ptr, c_ptr],
     "wdl_fp8_gemm": [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_int, c_ptr, c_i64, c_ptr],
+    "wdl_fp8wo_gemm": [c_ptr, c_i64, c_ptr, c_ptr, c_int, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_i64, c_int, c_ptr,
+                       c_ptr],
     "wdl_qk_norm_rope": [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_int, c_i64, c_i64, c_i64, c_int, c_int,
                          c_int, c_int, c_f32, c_ptr, c_ptr, c_i64, c_ptr],
     "wdl_quant_q": [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr],

@@ -19,7 +19,8 @@ FP8_MAX = 448.0
 ROWS_PAD = 128
 
 __all__ = ["FP8", "FP8_MAX", "quantize", "quantize_rows", "Fp8Linear", "DynamicFp8Linear", "PackedFp8Linear",
-           "to_fp8", "to_dynamic_fp8", "quantize_padded", "gemm"]
+           "to_fp8", "to_dynamic_fp8", "quantize_padded", "gemm", "weight_only_gemm", "Fp8WeightOnlyLinear",
+           "to_fp8_weight_only"]
 
 
 def _dtype_code(x):
@@ -73,6 +74,62 @@ def gemm(q: torch.Tensor, x_scale: torch.Tensor, M: int, w_codes: torch.Tensor, 
     _lib.call("wdl_fp8_gemm", ptr(q), ptr(x_scale), ptr(w_codes.view(torch.uint8)), ptr(w_scale), ptr(b), M, Mp, N,
               K, int(rows), ptr(out), out.stride(0), stream_of(q))
     return out
+
+
+def weight_only_gemm(x: torch.Tensor, w_codes: torch.Tensor, w_scale: torch.Tensor, bias: torch.Tensor | None,
+                     out: torch.Tensor | None = None, gate: torch.Tensor | None = None) -> torch.Tensor:
+    """The FP8 weight-only product: x bf16 [M, K] (row-strided, ldx % 8 == 0) times an e4m3 weight [N, K] with fp32
+    scales [N] (per output row) or [1] -> bf16 [M, N] = w_scale * (x . w) + bias. With `gate` (fp32 [N]) the result
+    is added into `out` as the gated residual out = bf16(out + bf16(y) * gate)."""
+    M, K = x.shape
+    N = w_codes.shape[0]
+    if x.dtype != torch.bfloat16 or x.stride(1) != 1 or w_codes.shape[1] != K or N % 128 or K % 64:
+        raise ValueError(f"weight-only FP8 GEMM: bf16 x [M, K] and an [N, K] weight, N % 128 == 0, K % 64 == 0; "
+                         f"got {tuple(x.shape)} and {tuple(w_codes.shape)}")
+    if w_scale.dtype != torch.float32 or w_scale.numel() not in (1, N):
+        raise ValueError("w_scale: fp32 [N] or [1]")
+    b = None if bias is None else bias.to(torch.bfloat16).contiguous()
+    if gate is not None:
+        if out is None or out.shape != (M, N) or out.dtype != torch.bfloat16 or out.stride(1) != 1:
+            raise ValueError("the gated residual needs out bf16 [M, N]")
+        gate = gate.float().contiguous()
+    elif out is None:
+        out = torch.empty(M, N, device=x.device, dtype=torch.bfloat16)
+    _lib.call("wdl_fp8wo_gemm", ptr(x), x.stride(0), ptr(w_codes.view(torch.uint8)), ptr(w_scale),
+              int(w_scale.numel() == N and N > 1), ptr(b), M, N, K, ptr(out), out.stride(0), 0 if gate is None else 2,
+              ptr(gate), stream_of(x))
+    return out
+
+
+class Fp8WeightOnlyLinear(torch.nn.Module):
+    """A linear layer with its weight in FP8 (e4m3, one scale per output row, or per tensor with rows=False) and
+    the activation kept in bf16: y = x (w * scale)^T + b. Not a mode of the reference, whose FP8 linears quantize
+    the activation too (quantization/fp8.py:1-6); the attention projections of the mixed-precision benchmark mode."""
+
+    def __init__(self, linear, rows=True):
+        super().__init__()
+        W = linear.weight.detach()
+        wq, ws = quantize_padded(W.to(torch.bfloat16).contiguous() if W.dtype not in (torch.bfloat16, torch.float32)
+                                 else W.contiguous(), rows=rows, pad=1)
+        self.register_buffer("weight", wq.view(FP8))
+        self.register_buffer("scale", ws)
+        self.register_buffer("bias", None if linear.bias is None else linear.bias.detach().to(torch.bfloat16))
+        self.out_features = linear.out_features
+
+    def forward(self, X):
+        x = X.reshape(-1, X.shape[-1]).to(torch.bfloat16).contiguous()
+        y = weight_only_gemm(x, self.weight, self.scale, self.bias)
+        return y.reshape(*X.shape[:-1], self.out_features)
+
+
+def to_fp8_weight_only(module, rows=True):
+    """Every nn.Linear inside `module` replaced by an Fp8WeightOnlyLinear, in place (weights on the GPU)."""
+    for name, child in module.named_children():
+        if isinstance(child, torch.nn.Linear):
+            setattr(module, name, Fp8WeightOnlyLinear(child, rows))
+        else:
+            to_fp8_weight_only(child, rows)
+    return module
 
 
 class Fp8Linear(torch.nn.Module):

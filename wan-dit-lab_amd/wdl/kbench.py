@@ -143,6 +143,25 @@ def gemm():
                   f"low-rank sum launch)", flush=True)
 
 
+def fp8wo():
+    """The FP8 weight-only attention projections (bf16 activations, e4m3 weights with row scales) at 1392 and 2640
+    tokens: QKV 3072 -> 9216, o 3072 -> 3072."""
+    import torch
+
+    from wdl import fp8
+
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(0)
+    for M in (1392, 2640):
+        for name, N, K in (("qkv", 9216, 3072), ("o", 3072, 3072)):
+            x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+            wq, ws = fp8.quantize_rows(torch.randn(N, K, device=dev, generator=g) * 0.02)
+            out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+            us = _replay_us(lambda: fp8.weight_only_gemm(x, wq, ws.reshape(-1), None, out=out))
+            print(f"fp8 weight-only {name} {M}x{N}x{K}: {us:.1f} us ({2 * M * N * K / us / 1e6:.0f} TFLOP/s)",
+                  flush=True)
+
+
 def quant():
     import torch
 
@@ -162,13 +181,13 @@ def quant():
 
 
 def main(argv):
-    if len(argv) < 2 or argv[1] not in ("attention", "chunk", "cross", "prep", "gemm", "quant"):
-        raise SystemExit("usage: python -m wdl.kbench attention|chunk|cross|prep|gemm|quant [library path]")
+    if len(argv) < 2 or argv[1] not in ("attention", "chunk", "cross", "prep", "gemm", "quant", "fp8wo"):
+        raise SystemExit("usage: python -m wdl.kbench attention|chunk|cross|prep|gemm|quant|fp8wo [library path]")
     if len(argv) > 2:
         from wdl import _lib
 
         _lib.LIB_PATH = Path(argv[2])
-    {"attention": attention, "chunk": chunk, "cross": cross, "prep": prep, "gemm": gemm, "quant": quant}[argv[1]]()
+    {"attention": attention, "chunk": chunk, "cross": cross, "prep": prep, "gemm": gemm, "quant": quant, "fp8wo": fp8wo}[argv[1]]()
 
 
 if __name__ == "__main__":
