@@ -31,6 +31,10 @@ BF = torch.bfloat16
 
 
 def _lin(x: torch.Tensor, t: dict, shift=0.0, unsigned=False) -> torch.Tensor:
+    """A block linear: W4A4 parts (float64 result), or FP8 weight-only parts dict(fp8, fp8_scale, bias) of the
+    mixed-precision mode (the bf16 result of w8a16_linear on the bf16 input)."""
+    if "fp8" in t:
+        return ofp8.w8a16_linear(x.to(BF), t["fp8"], t["fp8_scale"], t["bias"])
     return ow.linear_parts(x, t, shift, unsigned)[0]  # float64
 
 
@@ -141,6 +145,22 @@ def random_logical(N: int, K: int, g: torch.Generator, rank: int = 32, scale: fl
     return dict(q=q, wscales=ws, proj_down=(torch.randn(K, rank, generator=g) / K ** 0.5).to(BF),
                 proj_up=(torch.randn(N, rank, generator=g) * scale).to(BF), smooth=torch.ones(K, dtype=BF),
                 bias=bias.to(BF))
+
+
+def fp8_weight_only(N: int, K: int, g: torch.Generator, scale: float = 0.02) -> dict:
+    """FP8 weight-only parts of a random-init N(0, scale^2) linear: e4m3 rows with their fp32 scales, bf16 bias."""
+    wq, ws = ofp8.quantize_rows(torch.randn(N, K, generator=g) * scale)
+    return dict(fp8=wq, fp8_scale=ws, bias=(torch.randn(N, generator=g) * scale).to(BF))
+
+
+def mixed_precision_block(dim: int, ffn: int, g: torch.Generator) -> dict:
+    """The mixed-precision mode's parts: the attention projections (qkv, o, cq, ck, cv, co) FP8 weight-only, the
+    feed-forward W4A4 (random_logical)."""
+    P = random_logical_block(dim, ffn, g)
+    for name, (n, k) in dict(qkv=(3 * dim, dim), o=(dim, dim), cq=(dim, dim), ck=(dim, dim), cv=(dim, dim),
+                             co=(dim, dim)).items():
+        P[name] = fp8_weight_only(n, k, g)
+    return P
 
 
 def random_logical_block(dim: int, ffn: int, g: torch.Generator) -> dict:

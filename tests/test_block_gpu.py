@@ -93,6 +93,37 @@ def test_small_block_with_fp16_weight_scales_matches_oracle(gpu):
     check("fp16 scales", out, ref)
 
 
+def test_mixed_precision_block_matches_oracle(gpu):
+    """The mixed-precision mode: attention projections FP8 weight-only (e4m3 rows, bf16 activations), the
+    feed-forward W4A4, at dim 256 over an FP8 cache and a prompt, against the oracle block with the same parts: the
+    block bars (max-rel-err 1e-2, relative L2 2^-8)."""
+    from wdl.block import build_block
+    from wdl.kvcache import KVCache
+
+    g = torch.Generator().manual_seed(23)
+    dim, heads, ffn, grid, start, prior, Lc = 256, 2, 1024, (2, 4, 8), 3, 192, 40
+    P = oblock.mixed_precision_block(dim, ffn, g)
+    M = grid[0] * grid[1] * grid[2]
+    X = torch.randn(M, dim, generator=g).to(BF)
+    time_in = torch.randn(6, dim, generator=g) * 0.1
+    C = torch.randn(Lc, dim, generator=g).to(BF)
+    freq = orope.freqs(128, 1024, torch.float64).float()
+    ck = (torch.randn(1, prior + M, heads, 128, generator=g) * 100).clamp(-448, 448).to(torch.float8_e4m3fn)
+    cks = torch.rand(1, prior + M, heads, 1, generator=g) * 0.02
+    ocache = dict(k=ck.clone(), ks=cks.clone(), v=ck.clone(), vs=cks.clone(), at=prior)
+    ref = oblock.block_forward(X, time_in, P, grid, freq, start, ocache, oblock.context_kv(C, P), heads)
+    dev = torch.device("cuda")
+    blk = build_block(P, dim, heads, dev)
+    cache = KVCache(prior, 0, chunk=grid[0])
+    cache.allocate(torch.empty(1, M, heads, 128, device=dev))
+    for dst, src in ((cache.k, ck), (cache.v, ck), (cache.ks, cks), (cache.vs, cks)):
+        dst.copy_(src.to(dev))
+    cache.saved = prior
+    e = (time_in + P["modulation"]).float().to(dev)
+    out = blk.forward(X.to(dev).clone(), e, grid, freq.to(dev), start, cache, blk.prepare_context(C.to(dev))).cpu()
+    check("mixed precision block", out, ref)
+
+
 def test_full_width_block_on_one_frame_matches_oracle(gpu):
     """The full-width block on one frame: dim 3072, 24 x 128 heads, FFN 14336, 464-token frame (16 x 29) at start frame 2 over a
     928-token FP8 cache (two prior frames), 512 context tokens, random-init W4A4 weights."""

@@ -14,13 +14,17 @@ kernel sequence of one block (about 19 launches, all on the current stream, capt
   unsigned, h . proj_down2 partials) -> low-rank sum -> W4A4 ffn.2 (X += gate_f * y, fused)
 
 X is updated in place (a bf16 [M, dim] buffer owned by the caller).
+
+Mixed precision (the benchmark plan's mode; not a mode of the reference, whose FP8 linears are W8A8): attention
+projections given as FP8 weight-only parts dict(fp8, fp8_scale, bias) run on wdl_fp8wo_gemm with bf16 inputs (the
+norm and modulation through the quantizer kernel's bf16 output), the feed-forward stays W4A4.
 """
 
 from __future__ import annotations
 
 import torch
 
-from wdl import ops
+from wdl import fp8, ops
 from wdl.kvcache import KVCache
 from wdl.ops import EPI_BF16, EPI_RESIDUAL
 
@@ -43,13 +47,18 @@ class QuantizedWanBlock:
             raise ValueError(f"cross_attention must be 'sdpa' or 'sage', got {cross_attention!r}")
         self.p, self.dim, self.heads, self.eps = parts, dim, heads, eps
         self.cross_attention = cross_attention
-        dev = parts["qkv"]["qweight"].device
+        dev = parts["ffn1"]["qweight"].device
         for name in LINEARS:  # the GEMM operand: tile-blocked fp6 codes (e3m2 of 2w), expanded once from the nibbles
+            if "fp8" in parts[name]:  # an FP8 weight-only attention projection (mixed precision)
+                if name in ("ffn1", "ffn2"):
+                    raise ValueError("the feed-forward is W4A4 in every mode")
+                continue
             parts[name]["wcodes"] = ops.weight_codes(parts[name]["qweight"])
             parts[name]["wspairs"] = ops.scale_pairs(parts[name]["wscales"])  # bf16 or fp16 scales, exactly
             if not keep_packed:
                 del parts[name]["qweight"]
         self.ones = torch.ones(dim, device=dev, dtype=torch.float32)
+        self.ones_bf16 = torch.ones(dim, device=dev, dtype=torch.bfloat16)
 
     # --------------------------------------------------------------------------------------- pieces
     def _quant(self, x, name, ln=None, shift=0.0, unsigned=False):
@@ -62,9 +71,26 @@ class QuantizedWanBlock:
         return ops.gemm_launch(q, asc, lora, t["wcodes"], t["wspairs"], t["proj_up"], t["bias"], M, out, epilogue,
                                gate)
 
+    def _apply(self, x, name, out, epilogue=EPI_BF16, gate=None, ln=None):
+        """out (or out += gate * y with EPI_RESIDUAL) for the linear `name` of x (normalized and modulated first
+        when ln is given), W4A4 or FP8 weight-only."""
+        t = self.p[name]
+        if "fp8" in t:
+            if ln is not None:  # the quantizer kernel's bf16 copy of the normalized, modulated input
+                v = torch.empty_like(x)
+                ops.act_quant_launch(x, self.ones_bf16, None, ln=ln, v_out=v)
+                x = v
+            return fp8.weight_only_gemm(x, t["fp8"], t["fp8_scale"], t["bias"], out=out,
+                                        gate=gate if epilogue == EPI_RESIDUAL else None)
+        return self._gemm(self._quant(x, name, ln=ln), name, x.shape[0], out, epilogue, gate)
+
+    def out_features(self, name):
+        t = self.p[name]
+        return t["fp8"].shape[0] if "fp8" in t else ops.out_features(t["wcodes"])
+
     def linear(self, x, name):
-        out = torch.empty(x.shape[0], ops.out_features(self.p[name]["wcodes"]), device=x.device, dtype=torch.bfloat16)
-        return self._gemm(self._quant(x, name), name, x.shape[0], out)
+        out = torch.empty(x.shape[0], self.out_features(name), device=x.device, dtype=torch.bfloat16)
+        return self._apply(x, name, out)
 
     def prepare_context(self, C: torch.Tensor) -> dict:
         """Cross-attention keys and values of a prompt, once per prompt (multi_head_attention.py:21-26;
@@ -97,23 +123,23 @@ class QuantizedWanBlock:
         dev = X.device
         # self-attention
         qkv = torch.empty(M, 3 * D, device=dev, dtype=torch.bfloat16)
-        self._gemm(self._quant(X, "qkv", ln=dict(shift=sh_a, scale=sc_a, eps=self.eps)), "qkv", M, qkv)
+        self._apply(X, "qkv", qkv, ln=dict(shift=sh_a, scale=sc_a, eps=self.eps))
         Q, K = ops.qk_norm_rope_launch(qkv[:, :D], qkv[:, D:2 * D], self.p["wq"], self.p["wk"], freq, grid,
                                        start_frame, self.eps)
         V = qkv[:, 2 * D:]
         A = cache.attend(Q.view(1, M, H, 128), K.view(1, M, H, 128), V.view(1, M, H, 128))
-        self._gemm(self._quant(A.view(M, D), "o"), "o", M, X, EPI_RESIDUAL, g_a)
+        self._apply(A.view(M, D), "o", X, EPI_RESIDUAL, g_a)
         # cross-attention over the prompt
         qc = torch.empty(M, D, device=dev, dtype=torch.bfloat16)
         n3 = dict(weight=self.p["n3w"], bias=self.p["n3b"], eps=self.eps)
-        self._gemm(self._quant(X, "cq", ln=n3), "cq", M, qc)
+        self._apply(X, "cq", qc, ln=n3)
         Qc, _ = ops.qk_norm_rope_launch(qc, None, self.p["cwq"], None, self._nofreq(dev), (0, 1, 1), 0,
                                         self.eps)
         if "kp" in ctx:
             Ac = ops.attn_bf16_launch(Qc, ctx, 128 ** -0.5)
         else:
             Ac = ops.sage_attn_q16_launch(Qc, ctx, ctx["L"], 128 ** -0.5)
-        self._gemm(self._quant(Ac, "co"), "co", M, X, EPI_RESIDUAL, self.ones)
+        self._apply(Ac, "co", X, EPI_RESIDUAL, self.ones)
         # feed forward: the fused W4A4 GELU MLP (the hidden layer goes from the first GEMM's epilogue to the second
         # GEMM as int4 codes, scales and low-rank sums)
         q, asc, lora = self._quant(X, "ffn1", ln=dict(shift=sh_f, scale=sc_f, eps=self.eps))
@@ -128,7 +154,9 @@ def build_block(P_logical: dict, dim: int, heads: int, device, cross_attention: 
     """A QuantizedWanBlock from the logical parts of oracle-style quantization (tests) or of quantize_block."""
     from wdl.w4a4 import pack_parts
 
-    parts = {name: pack_parts(P_logical[name], device) for name in LINEARS}
+    parts = {name: (dict(fp8=P_logical[name]["fp8"].to(device), fp8_scale=P_logical[name]["fp8_scale"].reshape(-1)
+                         .float().to(device), bias=P_logical[name]["bias"].to(torch.bfloat16).to(device))
+                    if "fp8" in P_logical[name] else pack_parts(P_logical[name], device)) for name in LINEARS}
     for name in ("wq", "wk", "cwq", "cwk"):
         parts[name] = P_logical[name].to(torch.bfloat16).to(device)
     parts["n3w"] = P_logical["n3w"].float().to(device)

@@ -44,6 +44,9 @@ def _entries(parts: dict):
     """(name, tensor) of a block's parts, in row order. A layer that holds only the GEMM's weight codes (a
     QuantizedWanBlock drops the packed nibbles once it has them) is written as the nibbles those codes decode to."""
     for key, name in LAYERS.items():
+        if "fp8" in parts[key]:
+            raise ValueError(f"{key}: FP8 weight-only layers (the mixed-precision mode) have no place in the "
+                             f"block_w4a4_v2_gfx950 pack, whose layers are all W4A4")
         for p in PARTS:
             if p == "qweight" and p not in parts[key]:
                 from wdl.ops import decode_weights
