@@ -81,6 +81,49 @@ class Step:
         return self.model.forward(self.latent, self.t, self.start_frame)
 
 
+def mixed_stream_ms(chunks: int, device) -> dict:
+    """The mixed-precision streaming workload at 704x1280: 30 blocks with FP8 weight-only attention projections and
+    W4A4 feed-forward, 3-frame chunks of 22 x 40 = 2640 tokens over a full 21-frame window (15840 cached FP8 tokens +
+    the chunk = 18480 keys) and 512 prompt tokens, `chunks` consecutive chunks of the DMD loop (4 levels, write pass,
+    commit with eviction), eager, after one chunk of warm-up. Milliseconds per chunk and latent tokens/s."""
+    import torch
+
+    from wdl.block import random_block
+    from wdl.kvcache import KVCache
+    from wdl.model import ChunkStream, DiTModel, ModelEdges, random_edges
+    from wdl.rope import freqs
+
+    grid = (3, 22, 40)
+    tokens, per_frame = grid[0] * grid[1] * grid[2], grid[1] * grid[2]
+    g = torch.Generator(device=device).manual_seed(5)
+    blocks = [random_block(DIM, FFN, HEADS, device, g, mixed=True) for _ in range(BLOCKS)]
+    caches = []
+    for _ in range(BLOCKS):
+        c = KVCache((WINDOW - grid[0]) * per_frame, 0, chunk=grid[0])
+        c.allocate(torch.empty(1, tokens, HEADS, 128, device=device))
+        c.fill_for_benchmark(g)
+        caches.append(c)
+    context = torch.randn(CONTEXT, DIM, generator=g, device=device).to(torch.bfloat16)
+    model = DiTModel(ModelEdges(random_edges(DIM, LATENT, LATENT, g), device), blocks, caches, context,
+                     freqs(128, 1024, device))
+    stream = ChunkStream(model, (LATENT, grid[0], 2 * grid[1], 2 * grid[2]), g)
+    stream.start = WINDOW - grid[0]
+    stream.next_chunk()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(chunks):
+        stream.next_chunk()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / chunks
+    log(f"bench: 704x1280 mixed precision: {ms:.2f} ms per chunk over {chunks} chunks (DMD loop, eager)")
+    return {"workload": "704x1280, 3-frame chunks of 22x40 = 2640 tokens, 21-frame window (18480 keys, FP8 KV), 512 "
+                        "prompt tokens, attention projections FP8 weight-only, FFN W4A4, DMD loop (4 levels + write "
+                        "pass + commit), eager", "chunks": chunks, "ms_per_chunk": ms,
+            "latent_tokens_per_s": tokens / (ms * 1e-3)}
+
+
 def chunk_ms(step, chunks: int) -> float:
     """Milliseconds per chunk of Stream.next_chunk's DMD loop over the step's model (generation/causal.py:680-740):
     four levels, the write pass and the commit of every block's full FP8 window (the oldest frames evicted), eager;
@@ -325,6 +368,9 @@ def main():
     ap.add_argument("--chunks", type=int, default=0, metavar="C",
                     help="also time C whole chunks of the DMD loop (4 levels + write pass + cache commit, eager) "
                          "after the step measurement, as chunk_ms")
+    ap.add_argument("--mixed-704", type=int, default=0, metavar="C",
+                    help="also stream C chunks of the mixed-precision 704x1280 workload (FP8 weight-only attention "
+                         "projections, W4A4 FFN, 2640-token chunks over an 18480-key window), as mixed_704x1280")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain elementwise copy of MIB MiB (bitwise_not, uint8) three times: the "
                          "known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -418,6 +464,13 @@ def main():
     }
     if args.chunks > 0:
         result["chunk_ms"] = chunk_ms(step, args.chunks)
+    if args.mixed_704 > 0:
+        del step, run
+        if not args.eager:
+            del graph
+        torch.cuda.empty_cache()
+        with torch.no_grad():
+            result["mixed_704x1280"] = mixed_stream_ms(args.mixed_704, dev)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)

@@ -165,15 +165,23 @@ def build_block(P_logical: dict, dim: int, heads: int, device, cross_attention: 
     return QuantizedWanBlock(parts, dim, heads, cross_attention=cross_attention)
 
 
-def random_block(dim: int, ffn: int, heads: int, device, generator=None) -> QuantizedWanBlock:
+def random_block(dim: int, ffn: int, heads: int, device, generator=None, mixed: bool = False) -> QuantizedWanBlock:
     """A block of random-init W4A4 weights of the Wan architecture (no SVD: random int4, group scales of an
-    N(0, 0.02^2) weight, small low-rank factors), for the step benchmark."""
+    N(0, 0.02^2) weight, small low-rank factors), for the step benchmark. mixed: the attention projections FP8
+    weight-only instead (an N(0, 0.02^2) weight quantized to e4m3 rows on the GPU), the feed-forward W4A4."""
     from wdl.w4a4 import random_parts
 
     g = generator
     shapes = dict(qkv=(3 * dim, dim), o=(dim, dim), cq=(dim, dim), ck=(dim, dim), cv=(dim, dim), co=(dim, dim),
                   ffn1=(ffn, dim), ffn2=(dim, ffn))
-    parts = {name: random_parts(n, k, device, g) for name, (n, k) in shapes.items()}
+    parts = {}
+    for name, (n, k) in shapes.items():
+        if mixed and name not in ("ffn1", "ffn2"):
+            wq, ws = fp8.quantize_rows(torch.randn(n, k, generator=g, device=device) * 0.02)
+            parts[name] = dict(fp8=wq, fp8_scale=ws.reshape(-1),
+                               bias=(torch.randn(n, generator=g, device=device) * 0.02).to(torch.bfloat16))
+        else:
+            parts[name] = random_parts(n, k, device, g)
     for name in ("wq", "wk", "cwq", "cwk"):
         parts[name] = torch.ones(dim, device=device, dtype=torch.bfloat16)
     parts["n3w"] = torch.ones(dim, device=device)
