@@ -235,7 +235,7 @@ int64_t wdl_sage_attn_workspace_bytes(int64_t n, int64_t L, int64_t heads);
  * out: bf16 [n, heads, 128] (row stride ldo). workspace: 16-byte aligned, wdl_sage_attn_workspace_bytes(n, L,
  * heads) bytes (no initial contents needed); calls that share a workspace must not overlap. When the (128-query
  * tile, head) pairs just exceed a multiple of the CU count, every CU runs the same number of whole tiles and the
- * key blocks of the remaining tiles are split evenly over the CUs; their partial softmax states go through the
+ * key blocks of the remaining tiles are split evenly over half the CUs; their partial softmax states go through the
  * workspace to a second launch that merges them in a fixed order (deterministic). Otherwise the workspace is not
  * touched and may be NULL. */
 int wdl_sage_attn(const void* q_i8, int64_t ldq, const float* q_scale, const void* k_i8, const float* k_scale,

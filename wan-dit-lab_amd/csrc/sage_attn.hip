@@ -57,6 +57,8 @@ constexpr int MAGIC_I = 0x4B400000;       // the bits of MAGIC_F = 1.5 * 2^23
 constexpr float MAGIC_F = 12582912.0f;
 constexpr int SLOT_FLOATS = 4 * (64 * 64 + 128);  // one partial: per wave [64 values][64 lanes] of O, m, l
 constexpr int MAX_WG = 2048;                       // workgroups of a split launch (one per CU)
+constexpr int TAIL_DIV = 2;  // the split tiles' key blocks go to the first W / TAIL_DIV workgroups (half as many
+                             // pieces to merge, each twice as long: measured 151 -> 148 us at 1392 x 9744, 24 heads)
 
 struct AttnArgs {
     const int8_t* q;
@@ -76,6 +78,7 @@ struct AttnArgs {
     int64_t D;            // tiles run whole (the first D of the T = qtiles * H); the other T - D are split
     const uint16_t* qb;   // bf16 Q [n, H, 128] (row stride ldq) quantized in the kernel, or null (q, q_scale given)
     int64_t dual;         // workgroups 0 .. dual - 1 run two whole tiles, one per group (D == T; else 0)
+    int64_t Wt;           // the first Wt workgroups share the split tiles' key blocks (Wt <= W)
     int64_t frame;        // > 0: block-causal per latent frame of `frame` tokens (query q sees keys below
                           // L - n + (q / frame + 1) frame); 0: every query sees all L keys
 };
@@ -131,7 +134,7 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
     const bool dualwg = w < a.dual;
     const int64_t T = a.qtiles * a.H, R = T - a.D, Usk = R * nblk;
     const int64_t ndp = (a.D - w + a.W - 1) / a.W;
-    const int64_t s0 = w * Usk / a.W, s1 = (w + 1) * Usk / a.W;
+    const int64_t s0 = w < a.Wt ? w * Usk / a.Wt : Usk, s1 = w < a.Wt ? (w + 1) * Usk / a.Wt : Usk;
     int64_t cursor = s0;
 
     // per-lane LDS read offsets: K tile j, chunk c -> (c / 2) * 4096 + (32 j + lane % 32) * 64 + quarter;
@@ -504,12 +507,12 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     const int64_t nblk = a.Lpad / 64, T = a.qtiles * a.H, Usk = (T - a.D) * nblk;
     const int64_t tile = a.D + r, h = tile / a.qtiles, qt = tile % a.qtiles;
     const int64_t q = qt * 128 + sub * 32 + lane % 32;
-    const int64_t cf = wg_of(r * nblk, Usk, a.W), cl = wg_of((r + 1) * nblk - 1, Usk, a.W);
+    const int64_t cf = wg_of(r * nblk, Usk, a.Wt), cl = wg_of((r + 1) * nblk - 1, Usk, a.Wt);
     // the contributors' slots, once per workgroup (one thread each): slot 2c if the tile is c's first piece, 2c + 1
     // if its second, -1 if c's share is empty (fewer split key blocks than workgroups). Share starts in 32-bit
     // arithmetic (the host keeps W * Usk below 2^31).
     __shared__ int cslot[MAX_WG];
-    const uint32_t Uu = uint32_t(Usk), Wu = uint32_t(a.W), tile0 = uint32_t(r * nblk);
+    const uint32_t Uu = uint32_t(Usk), Wu = uint32_t(a.Wt), tile0 = uint32_t(r * nblk);
     const int nc = int(cl - cf + 1);
     for (int i = threadIdx.x; i < nc; i += 256) {
         const uint32_t c = uint32_t(cf) + i, s0 = c * Uu / Wu, s1 = (c + 1) * Uu / Wu;
@@ -614,7 +617,7 @@ static int attn_launch(const void* q_i8, const float* q_scale, const void* q_bf1
     AttnArgs a{static_cast<const int8_t*>(q_i8), ldq, q_scale, static_cast<const int8_t*>(k_i8), k_scale,
                static_cast<const uint8_t*>(v_fp8), v_scale, static_cast<uint16_t*>(out), ldo, n, L, Lpad, heads,
                sm_scale * 1.4426950408889634f, part, W, qtiles, Dw, static_cast<const uint16_t*>(q_bf16), dual,
-               frame};
+               W / TAIL_DIV > 0 ? W / TAIL_DIV : 1, frame};
     sage_attn_kernel<<<unsigned(W), 512, 0, stream>>>(a);
     int rc = check_launch("sage_attn");
     if (rc || Dw == T) return rc;
