@@ -109,8 +109,9 @@ class Fp8WeightOnlyLinear(torch.nn.Module):
     def __init__(self, linear, rows=True):
         super().__init__()
         W = linear.weight.detach()
-        wq, ws = quantize_padded(W.to(torch.bfloat16).contiguous() if W.dtype not in (torch.bfloat16, torch.float32)
-                                 else W.contiguous(), rows=rows, pad=1)
+        if W.dtype not in (torch.bfloat16, torch.float32):  # the quantizer reads bf16 or fp32; fp32 holds any float
+            W = W.float()
+        wq, ws = quantize_padded(W.contiguous(), rows=rows, pad=1)
         self.register_buffer("weight", wq.view(FP8))
         self.register_buffer("scale", ws)
         self.register_buffer("bias", None if linear.bias is None else linear.bias.detach().to(torch.bfloat16))
