@@ -143,6 +143,29 @@ def gemm():
                   f"low-rank sum launch)", flush=True)
 
 
+def fp8():
+    """The FP8 W8A8 linears (fp8.py's DynamicFp8Linear rows / tensor: e4m3 activations quantized per token or per
+    tensor on every call, e4m3 weights) on the W4A4 sweep's shapes at 1392 and 2640 tokens: the activation quantizer
+    and the FP8 GEMM timed together and the GEMM alone."""
+    import torch
+
+    from wdl import fp8
+
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(0)
+    for M in (1392, 2640):
+        for name, N, K in (("qkv", 9216, 3072), ("o", 3072, 3072), ("ffn1", 14336, 3072), ("ffn2", 3072, 14336)):
+            x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+            for rows in (True, False):
+                wq, ws = fp8.quantize_padded(torch.randn(N, K, device=dev, generator=g) * 0.02, rows=rows, pad=1)
+                q, s = fp8.quantize_padded(x, rows=rows)
+                us_g = _replay_us(lambda: fp8.gemm(q, s, M, wq, ws, None, rows=rows))
+                us = _replay_us(lambda: fp8.gemm(*fp8.quantize_padded(x, rows=rows), M, wq, ws, None, rows=rows))
+                print(f"fp8 {'rows' if rows else 'tensor'} {name} {M}x{N}x{K}: GEMM {us_g:.1f} us "
+                      f"({2 * M * N * K / us_g / 1e6:.0f} TOP/s), with the activation quantizer {us:.1f} us",
+                      flush=True)
+
+
 def fp8wo():
     """The FP8 weight-only attention projections (bf16 activations, e4m3 weights with row scales) at 1392 and 2640
     tokens: QKV 3072 -> 9216, o 3072 -> 3072."""
@@ -181,13 +204,14 @@ def quant():
 
 
 def main(argv):
-    if len(argv) < 2 or argv[1] not in ("attention", "chunk", "cross", "prep", "gemm", "quant", "fp8wo"):
-        raise SystemExit("usage: python -m wdl.kbench attention|chunk|cross|prep|gemm|quant|fp8wo [library path]")
+    if len(argv) < 2 or argv[1] not in ("attention", "chunk", "cross", "prep", "gemm", "quant", "fp8", "fp8wo"):
+        raise SystemExit("usage: python -m wdl.kbench attention|chunk|cross|prep|gemm|quant|fp8|fp8wo [library path]")
     if len(argv) > 2:
         from wdl import _lib
 
         _lib.LIB_PATH = Path(argv[2])
-    {"attention": attention, "chunk": chunk, "cross": cross, "prep": prep, "gemm": gemm, "quant": quant, "fp8wo": fp8wo}[argv[1]]()
+    {"attention": attention, "chunk": chunk, "cross": cross, "prep": prep, "gemm": gemm, "quant": quant, "fp8": fp8,
+     "fp8wo": fp8wo}[argv[1]]()
 
 
 if __name__ == "__main__":

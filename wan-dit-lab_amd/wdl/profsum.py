@@ -1,9 +1,12 @@
 """Summaries of rocprofv3 CSV output for the DiT step (kernel time table, calibrated HBM bytes per launch).
 
     python -m wdl.profsum stats  <kernel_stats.csv>  [top]
+    python -m wdl.profsum grids  <kernel_trace.csv>  [name filter]
     python -m wdl.profsum pmc    <fetch counter_collection.csv> <write counter_collection.csv> [copy MiB]
 
 `stats` prints the per-kernel time table of `rocprofv3 --kernel-trace --stats --output-format csv`.
+`grids` prints, from the kernel trace, the launches, average and minimum duration per kernel and grid (one line
+per shape of a benchmark that launches one kernel at several shapes).
 `pmc` averages FETCH_SIZE and WRITE_SIZE (KiB per dispatch) per kernel and grid, and scales each counter by what
 it reads for the plain uint8 bitwise_not copy of `copy MiB` that `bench.py --copy-probe` runs first (known bytes:
 MiB read, MiB written), so that the reported figures are HBM bytes per launch.
@@ -36,6 +39,19 @@ def stats(path: str, top: int = 20) -> str:
         out.append(f"| `{short(r['Name'])}` | {int(r['Calls'])} | {float(r['TotalDurationNs']) / 1e6:.2f} | "
                    f"{float(r['AverageNs']) / 1e3:.1f} | {100 * float(r['TotalDurationNs']) / total:.2f} |")
     out.append(f"| all kernels but the spin | {sum(int(r['Calls']) for r in rows)} | {total / 1e6:.2f} | | 100 |")
+    return "\n".join(out)
+
+
+def grids(path: str, name_filter: str = "") -> str:
+    runs = collections.defaultdict(list)
+    for r in csv.DictReader(open(path)):
+        if "spin_kernel" in r["Kernel_Name"] or name_filter not in r["Kernel_Name"]:
+            continue
+        grid = f"{r['Grid_Size_X']}x{r['Grid_Size_Y']}x{r['Grid_Size_Z']}"
+        runs[(short(r["Kernel_Name"]), grid)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    out = ["| kernel | grid (threads) | launches | avg us | min us |", "|---|---|---:|---:|---:|"]
+    for (k, grid), d in runs.items():
+        out.append(f"| `{k}` | {grid} | {len(d)} | {sum(d) / len(d):.1f} | {min(d):.1f} |")
     return "\n".join(out)
 
 
@@ -78,6 +94,8 @@ def pmc(fetch_path: str, write_path: str, copy_mib: int = 1024) -> str:
 def main(argv):
     if len(argv) >= 2 and argv[0] == "stats":
         print(stats(argv[1], int(argv[2]) if len(argv) > 2 else 20))
+    elif len(argv) >= 2 and argv[0] == "grids":
+        print(grids(argv[1], argv[2] if len(argv) > 2 else ""))
     elif len(argv) >= 3 and argv[0] == "pmc":
         print(pmc(argv[1], argv[2], int(argv[3]) if len(argv) > 3 else 1024))
     else:
