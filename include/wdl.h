@@ -110,9 +110,12 @@ int wdl_w4a4_scale_pairs(const void* scales, int fp16, int64_t n, void* pairs, w
  * Mp % 128 == 0, N % 128 == 0, K % 64 == 0, K <= 2^30; qa, wcodes, out, proj_up, lora, gate and workspace 16-byte
  * aligned, bias 8-byte, scales 4-byte; bf16 outputs: ldo % 8 == 0.
  * workspace: wdl_w4a4_gemm_workspace_bytes(Mp, N, K) bytes (no initial contents), or NULL. When the size is not 0
- * the product runs split in K over one workgroup per CU (stream-K, for shapes whose tiles leave CUs idle) and a
- * second launch adds the pieces in a fixed order: deterministic, rounding not identical to the one-pass launch.
- * With NULL the one-pass launch runs. Calls sharing a workspace must not overlap. */
+ * the product runs split in K over one workgroup per CU, for shapes whose tiles leave CUs idle: either the balanced
+ * form (whole tiles dealt evenly, each summed by two halves of K, the few leftover tiles in 32 x 32 pieces summed
+ * by eighths of K; one launch, the size is then a 256-byte token the kernel does not touch) or stream-K (the
+ * (tile, group) iterations shared evenly, partial sums in the workspace added in a fixed order by a second
+ * launch). Both are deterministic, their rounding not identical to the one-pass launch. With NULL the one-pass
+ * launch runs. Calls sharing a workspace must not overlap. */
 int64_t wdl_w4a4_gemm_workspace_bytes(int64_t Mp, int64_t N, int64_t K);
 int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wcodes, const void* wscales, const float* lora,
                   const void* proj_up, const void* bias, int64_t M, int64_t Mp, int64_t N, int64_t K, int64_t rank,

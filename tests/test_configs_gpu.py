@@ -2,8 +2,8 @@
 
 - the GEMM sweep: every W4A4 shape of a block (QKV 3072 -> 9216, o 3072 -> 3072, FFN-up 3072 -> 14336, FFN-down
   14336 -> 3072) at 1392 and 2640 tokens, weights N(0, 0.02^2) quantized by the max rule, activations N(0, 1) with 1%
-  outlier channels x 20 quantized per token and 64-group, through the launches the library picks (stream-K for
-  FFN-down at 1392 tokens); the same eight shapes as FP8 linears (per-row scales, the reference's rows mode);
+  outlier channels x 20 quantized per token and 64-group, through the launches the library picks (the balanced
+  K split for QKV, o and FFN-down at 1392 tokens); the same eight shapes as FP8 linears (per-row scales, the reference's rows mode);
 - the chunk attention: 24 heads, 2640 queries (3 latent frames of 22 x 40), 2640 / 9240 / 18480 keys (the chunk
   alone, and 6600 / 15840 FP8-cached keys), K with a per-channel bias N(0, 3^2), the chunk's Q and K rotated by the 3D
   RoPE at its start frame; the full 24-head launch, two heads checked against the oracle (its CPU cost);

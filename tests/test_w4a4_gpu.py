@@ -174,11 +174,16 @@ def test_gemm_scaled_lowrank_bias_matches_oracle(gpu, M, N, K, valid, sdt):
     assert torch.all(diff <= ref.abs() * 2 ** -8 + 2 ** -20 * scale * (K // 64))
 
 
-@pytest.mark.parametrize("M,N,K,valid", [(1408, 3072, 8192, 1392), (512, 512, 14336, 464)])
-def test_gemm_stream_k_matches_one_pass_and_oracle(gpu, M, N, K, valid):
-    """Shapes whose tiles leave CUs idle run split in K (stream-K + merge, when the library asks for a workspace):
-    the result is deterministic, within fp32 rounding of the one-pass launch, and meets the oracle bar of the
-    one-pass test; gated residual epilogue in place."""
+@pytest.mark.parametrize("M,N,K,valid", [(1024, 3072, 8192, 1000), (512, 512, 14336, 464), (1408, 3072, 14336, 1392),
+                                         (1408, 3072, 3072, 1392), (1408, 3072, 2048, 1300), (2048, 2048, 1024, 2000),
+                                         (2048, 4096, 3072, 2047)])
+def test_gemm_split_k_matches_one_pass_and_oracle(gpu, M, N, K, valid):
+    """Shapes whose tiles leave CUs idle run split in K when the library asks for a workspace: stream-K + merge
+    (the first three shapes, the last FFN-down at 1392 tokens), or the balanced form on 256 CUs (whole tiles in two
+    K halves; 264 tiles: 8 left over in 128 pieces of 32 x 32, at K = 3072 and 2048; 256 and 512 tiles: none left
+    over, one and two tiles per CU). The result is
+    deterministic, within fp32 rounding of the one-pass launch, and meets the oracle bar of the one-pass test; gated
+    residual epilogue in place, bf16 and GELU outputs one rounding from the fp32 one."""
     from wdl import _lib, ops, w4a4
 
     assert _lib.library().wdl_w4a4_gemm_workspace_bytes(M, N, K) > 0  # the split path is the one under test
@@ -207,7 +212,13 @@ def test_gemm_stream_k_matches_one_pass_and_oracle(gpu, M, N, K, valid):
     assert float((y1.cpu().double() - ref).abs().max()) <= bar
     assert float((y1 - y0).abs().max()) <= bar
     expect = (X.float() + y1.cpu().to(torch.bfloat16).float() * gate).to(torch.bfloat16)
-    assert torch.equal(outs.cpu(), expect)  # the residual epilogue of the merge: bf16(x + bf16(y) gate)
+    assert torch.equal(outs.cpu(), expect)  # the residual epilogue of the split: bf16(x + bf16(y) gate)
+    yb = launch_gemm(qa, asc, wq, wsc, lora, pu, bias, M=valid, epi=0)
+    yg = launch_gemm(qa, asc, wq, wsc, lora, pu, bias, M=valid, epi=3)
+    torch.cuda.synchronize()
+    assert torch.equal(yb, y1.to(torch.bfloat16))
+    hg = torch.nn.functional.gelu(y1.double(), approximate="tanh")
+    assert float((yg.double() - hg).abs().max()) <= 2 ** -7 * float(hg.abs().max()) + 1e-6
 
 
 def test_gemm_residual_and_gelu_epilogues(gpu):

@@ -542,9 +542,77 @@ __device__ __forceinline__ void finish_tile_gelu_quant(const GemmArgs& p, f32x16
 // The main loop of both GEMMs. W4: the W4A4 product (fp6 tile-blocked codes, per-group scale fold, scales
 // streamed with the codes); otherwise the FP8 product (e4m3 row-major codes only, one fp32 accumulation over all
 // of K in the MFMA accumulator).
-template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES, bool W4, bool SK = false>
+// One 32 x 32 piece (features n0 .., tokens m0 ..) summed over all of K by NWT waves: wave v folds the 64-deep
+// groups [v G / NWT, (v + 1) G / NWT) (at most PD) in increasing order with the tiles' arithmetic (the fp6 product,
+// the exact scale product of a bf16 MFMA, one fmaf per element and group). load() reads the wave's operands
+// straight from global memory into registers (the rows as the tiles read them: 16 + 8 bytes of a 48-byte row per
+// lane; lanes 32..63 give the zero k-slots of the scale product); fold() returns the wave's partial sums in the
+// MFMA layout.
+template <int NWT, int PD>
+struct Piece {
+    u32x6 fa[PD], fb[PD];  // the 6 code dwords of each operand row (the MFMA's 8-dword operand gets 2 zeros)
+    uint32_t sa[PD], sb[PD];
+    int n;  // groups of this wave (wave-uniform)
+
+    __device__ __forceinline__ void load(const GemmArgs& p, int64_t n0, int64_t m0, int v, int lane) {
+        const int64_t G = p.K / 64;
+        const int gb = int(int64_t(v) * G / NWT);
+        n = int(int64_t(v + 1) * G / NWT) - gb;
+        const int half = lane / 32;
+        const int64_t nr = n0 + lane % 32, mr = m0 + lane % 32;
+        const uint8_t* arow = p.wc + (nr / BLOCK_ROWS) * G * BLOCK6 + (nr % BLOCK_ROWS) * ROW6;
+        const uint8_t* brow = p.qa + (mr / BLOCK_ROWS) * G * BLOCK6 + (mr % BLOCK_ROWS) * ROW6;
+        const int q0 = 16 * half, q1 = 32 + 8 * half;
+        const bool low = lane < 32;
+#pragma unroll
+        for (int d = 0; d < PD; ++d) {
+            const int64_t gg = n > 0 ? gb + (d < n ? d : n - 1) : 0;  // in range; groups d >= n are not folded
+            const uint4 xa = *reinterpret_cast<const uint4*>(arow + gg * BLOCK6 + q0);
+            const uint2 ya = *reinterpret_cast<const uint2*>(arow + gg * BLOCK6 + q1);
+            const uint4 xb = *reinterpret_cast<const uint4*>(brow + gg * BLOCK6 + q0);
+            const uint2 yb = *reinterpret_cast<const uint2*>(brow + gg * BLOCK6 + q1);
+            fa[d] = u32x6{xa.x, xa.y, xa.z, xa.w, ya.x, ya.y};
+            fb[d] = u32x6{xb.x, xb.y, xb.z, xb.w, yb.x, yb.y};
+            const uint32_t w = p.ws[gg * p.N + nr];
+            const uint32_t a = p.as[gg * p.Mp + mr];
+            sa[d] = low ? w : 0u;
+            sb[d] = low ? a : 0u;
+        }
+    }
+
+    __device__ __forceinline__ f32x16 fold() const {
+        const f32x16 zero = {};
+        f32x16 acc = zero;
+#pragma unroll
+        for (int d = 0; d < PD; ++d) {
+            if (d < n) {
+                const i16x4 oa = __builtin_bit_cast(i16x4, make_uint2(sa[d], 0u));
+                const i16x4 ob = __builtin_bit_cast(i16x4, make_uint2(sb[d] * 0x10001u, 0u));
+                const i32x8 a = {int(fa[d][0]), int(fa[d][1]), int(fa[d][2]), int(fa[d][3]), int(fa[d][4]),
+                                 int(fa[d][5]), 0, 0};
+                const i32x8 b = {int(fb[d][0]), int(fb[d][1]), int(fb[d][2]), int(fb[d][3]), int(fb[d][4]),
+                                 int(fb[d][5]), 0, 0};
+                const f32x16 I = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, zero, 3, 2, 0, 0, 0, 0);
+                const f32x16 P = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(oa, ob, zero, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[e] = fmaf(I[e], P[e], acc[e]);
+            }
+        }
+        return acc;
+    }
+};
+constexpr int PIECE_WAVES = 8, PIECE_GROUPS = 6;  // a piece: K of up to 48 groups, in one batch of loads
+
+// How a launch covers the tiles: one tile per workgroup, stream-K shares, or the balanced form (one workgroup of
+// two K-groups per CU, whole tiles dealt evenly, the leftover tiles in 32 x 32 pieces).
+enum Mode { MODE_TILE = 0, MODE_SK = 1, MODE_BAL = 2 };
+
+template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES, bool W4, int MODE = MODE_TILE>
 __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
     static_assert(!W4 || (BN % BLOCK_ROWS == 0 && BM % BLOCK_ROWS == 0), "blocked operands come in 128-row tiles");
+    // K-groups: MODE_BAL runs 2 x NW waves, each group of NW its own ring over half of a tile's K
+    constexpr int KS = MODE == MODE_BAL ? 2 : 1;
+    static_assert(KS == 1 || (W4 && BN == 128 && BM == 128 && WN == 64 && WM == 64 && NW == 4), "balanced form");
     static_assert((BN / WN) * (BM / WM) == NW, "wave grid");
     static_assert(STAGES >= 4 && STAGES <= 8, "ring depth");
     constexpr int TN = WN / 32, TM = WM / 32;
@@ -562,18 +630,27 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
     static_assert(4 * BN + 2 * BM <= SD, "scale stage");
     __shared__ __attribute__((aligned(1024))) uint8_t sX[W4 ? 1 : STAGES][W4 ? 16 : BM * 64];
     __shared__ __attribute__((aligned(1024))) uint8_t sW[W4 ? 1 : STAGES][W4 ? 16 : BN * 64];
-    __shared__ __attribute__((aligned(1024))) uint8_t sC[W4 ? STAGES : 1][W4 ? CS : 16];
-    __shared__ __attribute__((aligned(256))) uint8_t sS[W4 ? STAGES : 1][W4 ? SB : 256];
+    __shared__ __attribute__((aligned(1024))) uint8_t sC[W4 ? KS * STAGES : 1][W4 ? CS : 16];
+    __shared__ __attribute__((aligned(256))) uint8_t sS[W4 ? KS * STAGES : 1][W4 ? SB : 256];
+    // MODE_BAL: a piece's partial sums, apart from the rings
+    __shared__ __attribute__((aligned(16))) uint8_t sE[KS == 2 ? PIECE_WAVES * 64 * 16 * 4 : 16];
+    static_assert(KS == 1 || (KS * NW == PIECE_WAVES && NW * 64 * 64 * 4 <= KS * STAGES * CS &&
+                              NW * 64 * STG * 2 <= STAGES * CS),
+                  "a K-group's accumulators fit the rings, its staging its own ring");
 
     const int t = threadIdx.x, lane = t % 64;
-    const int wave = __builtin_amdgcn_readfirstlane(t / 64);
+    const int wall = __builtin_amdgcn_readfirstlane(t / 64);
+    const int kg = KS == 1 ? 0 : wall / NW;        // K-group
+    const int wave = KS == 1 ? wall : wall % NW;   // wave within the K-group
     const int wn = wave % (BN / WN), wm = wave / (BN / WN);
     const int64_t ntn = p.N / BN, ntm = p.Mp / BM, total = ntn * ntm;
     const int64_t K = p.K, G = K / 64;
+    uint8_t* const C0 = &sC[0][0] + (W4 ? kg * (STAGES * CS) : 0);  // this K-group's ring
+    uint8_t* const S0 = &sS[0][0] + (W4 ? kg * (STAGES * SB) : 0);
 
     // zero tails of the scale stages (written once; the loads never touch them)
     if constexpr (W4)
-        if (t < STAGES * 32) *reinterpret_cast<uint32_t*>(&sS[t / 32][SD + (t % 32) * 4]) = 0u;
+        if (t < KS * STAGES * 32) *reinterpret_cast<uint32_t*>(&sS[t / 32][SD + (t % 32) * 4]) = 0u;
 
     // per-lane LDS offsets (stage-independent). W4: a lane's 16-byte and 8-byte pieces of its operand row, the
     // scale entries. FP8: operand rows and the two swizzled quarters.
@@ -665,19 +742,15 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         auto issue_one = [&](int st, int g, int u) {
             const int gg = g < GI ? g : GI - 1;
             if constexpr (W4) {
-                if (u < N16) dma16s(cbase[u] + int64_t(gg) * BLOCK6, off16, lds_addr(&sC[st][cdst[u]]));
-                else if (u < N16 + N4) dma4s(cbase[u] + int64_t(gg) * BLOCK6, off4, lds_addr(&sC[st][cdst[u]]));
-                else dma4s(sbase + gg * sstride, off4, lds_addr(&sS[st][wave * 256]));
+                if (u < N16) dma16s(cbase[u] + int64_t(gg) * BLOCK6, off16, lds_addr(C0 + st * CS + cdst[u]));
+                else if (u < N16 + N4) dma4s(cbase[u] + int64_t(gg) * BLOCK6, off4, lds_addr(C0 + st * CS + cdst[u]));
+                else dma4s(sbase + gg * sstride, off4, lds_addr(S0 + st * SB + wave * 256));
             } else {
                 if (u < XI) dma16(xsrc[u] + int64_t(gg) * 64, lds_addr(&sX[st][(wave * XI + u) * 1024]));
                 else dma16(wsrc[u - XI] + int64_t(gg) * 64, lds_addr(&sW[st][(wave * WI + u - XI) * 1024]));
             }
         };
 
-#pragma unroll
-        for (int i = 0; i < TN; ++i)
-#pragma unroll
-            for (int j = 0; j < TM; ++j) acc[i][j] = f32x16{};
         const f32x16 zero = {};
 
         // Two register sets of one group's operands: weight / activation code fragments (W4: 6 dwords of fp6 codes,
@@ -698,16 +771,16 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         };
         auto load_a = [&](int set, int st, int i) {
             if constexpr (W4) {
-                fa[set][i] = load_frag(&sC[st][aoff[i]]);
-                fsa[set][i] = *reinterpret_cast<const uint32_t*>(&sS[st][soa[i]]);
+                fa[set][i] = load_frag(C0 + st * CS + aoff[i]);
+                fsa[set][i] = *reinterpret_cast<const uint32_t*>(S0 + st * SB + soa[i]);
             } else {
                 fa[set][i] = load_frag(&sW[st][aoff[i]]);
             }
         };
         auto load_b = [&](int set, int st, int j) {
             if constexpr (W4) {
-                fb[set][j] = load_frag(&sC[st][boff[j]]);
-                fsb[set][j] = *reinterpret_cast<const uint16_t*>(&sS[st][sob[j]]);
+                fb[set][j] = load_frag(C0 + st * CS + boff[j]);
+                fsb[set][j] = *reinterpret_cast<const uint16_t*>(S0 + st * SB + sob[j]);
             } else {
                 fb[set][j] = load_frag(&sX[st][boff[j]]);
             }
@@ -781,6 +854,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         for (int k = 0; k < STAGES - 1; ++k)
 #pragma unroll
             for (int u = 0; u < LPG; ++u) issue_one(k, k, u);
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j) acc[i][j] = zero;
         wait_vmcnt<(STAGES - 2) * LPG>();
         __syncthreads();
 #pragma unroll
@@ -805,7 +882,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         wait_vmcnt<0>();  // the clamped tail loads land before the workgroup can end
     };
 
-    if constexpr (!SK) {
+    if constexpr (MODE == MODE_TILE) {
         // the whole tile `pid`, ids remapped so that the tiles of one weight slab run on one XCD
         const int64_t pid = blockIdx.x;
         int64_t tile = pid;
@@ -826,7 +903,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         } else {
             finish_tile<TN, TM, EPI>(p, acc, n0 + wn * WN, m0 + wm * WM, lane);
         }
-    } else {
+    } else if constexpr (MODE == MODE_SK) {
         // Stream-K share of this workgroup: the U = total * G (tile, group) iterations in tile-major order split
         // evenly over the W workgroups of the launch, W > total, so a share covers less than one tile: at most two
         // pieces, whose partial sums go to workspace slots 2 c and 2 c + 1 (c: the logical index, workgroup ids
@@ -853,6 +930,95 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
                         dst[((i * TM + j) * 4 + f4) * 64] = make_float4(acc[i][j][4 * f4], acc[i][j][4 * f4 + 1],
                                                                         acc[i][j][4 * f4 + 2], acc[i][j][4 * f4 + 3]);
         }
+    } else {
+        // Balanced form: one workgroup per CU (W = gridDim.x, a multiple of 8). The T = total tiles of 128 x 128 are
+        // dealt out as F = T / W whole tiles per workgroup; the L = T - F W left over are cut into 16 L <= W pieces
+        // of 32 x 32, piece c going to workgroup c. A whole tile is summed by the two K-groups, group 0 over the
+        // first half of the groups and group 1 over the second (G is even), added in that order. A piece is summed
+        // over all of K by the 8 waves first, each folding an eighth of the groups (at most 6, loaded in one
+        // batch); the 8 partial sums wait in LDS, apart from the rings, and wave 0 of K-group 1 adds them in wave
+        // order and finishes the piece while K-group 0 finishes the last tile. Results are deterministic; the sums
+        // are split in K, so their rounding differs from the one-pass fold as the stream-K launch's does. Tile ids
+        // are remapped so that the tiles the workgroups of one XCD (c mod 8) run at the same time are consecutive:
+        // a few weight slabs against all row blocks.
+        const int64_t W = gridDim.x, c = blockIdx.x, Wx = W / 8;
+        const int64_t F = total / W;
+        const bool piece = c < 16 * (total - F * W);  // workgroup-uniform
+        const int64_t ptl = F * W + c / 16;
+        const int64_t pn = (ptl / ntm) * BN + 32 * ((c % 16) / 4), pm = (ptl % ntm) * BM + 32 * (c % 4);
+        float4* const E = reinterpret_cast<float4*>(sE);  // the piece's partial sums, [wave][4][64] float4
+        const int hg = int(G / 2);
+        float4* const R = reinterpret_cast<float4*>(&sC[0][0]) + wave * (TN * TM * 4 * 64) + lane;
+        if (piece) {
+            Piece<PIECE_WAVES, PIECE_GROUPS> pc;
+            pc.load(p, pn, pm, wall, lane);
+            const f32x16 part = pc.fold();
+#pragma unroll
+            for (int f4 = 0; f4 < 4; ++f4)
+                E[(wall * 4 + f4) * 64 + lane] =
+                    make_float4(part[4 * f4], part[4 * f4 + 1], part[4 * f4 + 2], part[4 * f4 + 3]);
+        }
+        for (int64_t k = 0; k < F; ++k) {
+            const int64_t tile = (c % 8) * (F * Wx) + k * Wx + c / 8;
+            const int64_t n0 = (tile / ntm) * BN, m0 = (tile % ntm) * BM;
+            if (k > 0) __syncthreads();  // group 0's staging reads are done before its ring is refilled
+            mainloop(n0, m0, kg * hg, kg * hg + hg);
+            __syncthreads();  // every wave is past its last read of the rings, which now hold group 1's sums
+            if (kg == 1)
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j)
+#pragma unroll
+                        for (int f4 = 0; f4 < 4; ++f4)
+                            R[((i * TM + j) * 4 + f4) * 64] = make_float4(acc[i][j][4 * f4], acc[i][j][4 * f4 + 1],
+                                                                          acc[i][j][4 * f4 + 2], acc[i][j][4 * f4 + 3]);
+            __syncthreads();
+            if (kg == 0)
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j)
+#pragma unroll
+                        for (int f4 = 0; f4 < 4; ++f4) {
+                            const float4 x = R[((i * TM + j) * 4 + f4) * 64];
+                            acc[i][j][4 * f4] += x.x;
+                            acc[i][j][4 * f4 + 1] += x.y;
+                            acc[i][j][4 * f4 + 2] += x.z;
+                            acc[i][j][4 * f4 + 3] += x.w;
+                        }
+            // the sums are read: group 1 may refill its ring, group 0 stages its outputs over its own ring
+            __syncthreads();
+            if (kg == 0) {
+                if constexpr (EPI != EPI_F32)
+                    finish_tile_rows<TN, TM, EPI>(p, acc, n0 + wn * WN, m0 + wm * WM, lane,
+                                                  reinterpret_cast<uint16_t*>(&sC[0][0]) + wave * 64 * STG);
+                else
+                    finish_tile<TN, TM, EPI>(p, acc, n0 + wn * WN, m0 + wm * WM, lane);
+            }
+        }
+        if (wall == NW && piece) {  // while group 0 finishes the last tile
+            f32x16 part[1][1];
+#pragma unroll
+            for (int f4 = 0; f4 < 4; ++f4) {
+                const float4 x = E[f4 * 64 + lane];
+                part[0][0][4 * f4] = x.x;
+                part[0][0][4 * f4 + 1] = x.y;
+                part[0][0][4 * f4 + 2] = x.z;
+                part[0][0][4 * f4 + 3] = x.w;
+            }
+#pragma unroll
+            for (int v = 1; v < PIECE_WAVES; ++v)
+#pragma unroll
+                for (int f4 = 0; f4 < 4; ++f4) {
+                    const float4 x = E[(v * 4 + f4) * 64 + lane];
+                    part[0][0][4 * f4] += x.x;
+                    part[0][0][4 * f4 + 1] += x.y;
+                    part[0][0][4 * f4 + 2] += x.z;
+                    part[0][0][4 * f4 + 3] += x.w;
+                }
+            finish_tile<1, 1, EPI>(p, part, pn, pm, lane);
+        }
     }
 }
 
@@ -861,9 +1027,14 @@ __global__ __launch_bounds__(NW * 64) void w4a4_gemm_kernel(GemmArgs p) {
     gemm_body<BN, BM, WN, WM, NW, EPI, STAGES, true>(p);
 }
 
+template <int EPI, int STAGES>
+__global__ __launch_bounds__(512) void w4a4_gemm_bal_kernel(GemmArgs p) {
+    gemm_body<128, 128, 64, 64, 4, EPI, STAGES, true, MODE_BAL>(p);
+}
+
 template <int BN, int BM, int WN, int WM, int NW, int STAGES>
 __global__ __launch_bounds__(NW * 64) void w4a4_gemm_sk_kernel(GemmArgs p) {
-    gemm_body<BN, BM, WN, WM, NW, EPI_F32, STAGES, true, true>(p);
+    gemm_body<BN, BM, WN, WM, NW, EPI_F32, STAGES, true, MODE_SK>(p);
 }
 
 // The stream-K share c (of W) whose iteration range [c U / W, (c + 1) U / W) contains iteration `it`
@@ -974,16 +1145,43 @@ int launch_fp8(const GemmArgs& a, int epi, hipStream_t stream) {
 constexpr int SK_NW = 8;                                    // the 256 x 128 configuration
 constexpr int64_t SK_SLOT = SK_NW * 64 * 2 * 2 * 16;        // floats per partial: the workgroup's accumulators
 
+// Balanced form (one workgroup of 8 waves per CU: whole 128 x 128 tiles dealt evenly, each summed by two K-groups
+// of 4 waves, the leftover tiles in 32 x 32 pieces): when there is at least one tile per CU, the groups split evenly
+// in two and either no tile is left over or the pieces come to at most one per CU with K of at most 48 groups (a
+// piece's operands in one batch of loads). It takes the shapes whose tile count just exceeds the CU count, where
+// whole-tile launches leave CUs idle: at 1392 tokens, N = 3072, K = 3072 (264 tiles on 256 CUs: o / cross-q /
+// cross-o). Measured there: the K-split tiles alone 24.0 us against 31.7 us for the one-pass 256 x 128 launch; the
+// pieces as a separate phase of three memory round trips cost another 5 us. It needs no memory, but runs (like
+// stream-K) only when the caller passes a workspace: without one every shape takes the one-pass fold.
+constexpr int64_t BAL_TOKEN_BYTES = 256;  // the workspace size reported for it
+bool bal_fits(int64_t Mp, int64_t N, int64_t K) {
+    const int64_t cus = cu_count(), T = (N / 128) * (Mp / 128), G = K / 64;
+    if (cus <= 0 || cus % 8 || G % 2 || T < cus) return false;
+    return T % cus == 0 || (16 * (T % cus) <= cus && G <= PIECE_WAVES * PIECE_GROUPS);
+}
+
 // stream-K workgroups for an M x N x K product (0: plain launch)
 int64_t sk_shares(int64_t Mp, int64_t N, int64_t K) {
     const int64_t cus = cu_count();
-    if (N % 256 || cus <= 0 || K / 64 < WDL_SK_MIN_GROUPS) return 0;
+    if (N % 256 || cus <= 0 || K / 64 < WDL_SK_MIN_GROUPS || bal_fits(Mp, N, K)) return 0;
     const int64_t Tw = (N / 256) * (Mp / 128);
     return 4 * Tw <= 3 * cus ? cus : 0;  // the 256 x 128 launch would leave a quarter of the CUs or more idle
 }
 
 int dispatch(const GemmArgs& a, int epi, hipStream_t stream) {
     const int64_t T = (a.N / 128) * (a.Mp / 128), cus = cu_count();
+    if (a.part && bal_fits(a.Mp, a.N, a.K)) {
+        const unsigned grid = unsigned(cus);
+        constexpr int ST = WDL_GEMM_STAGES;
+        switch (epi) {
+            case EPI_BF16: w4a4_gemm_bal_kernel<EPI_BF16, ST><<<grid, 512, 0, stream>>>(a); break;
+            case EPI_F32: w4a4_gemm_bal_kernel<EPI_F32, ST><<<grid, 512, 0, stream>>>(a); break;
+            case EPI_RESIDUAL: w4a4_gemm_bal_kernel<EPI_RESIDUAL, ST><<<grid, 512, 0, stream>>>(a); break;
+            case EPI_GELU: w4a4_gemm_bal_kernel<EPI_GELU, ST><<<grid, 512, 0, stream>>>(a); break;
+            default: return fail(WDL_EINVAL, "w4a4_gemm: bad epilogue %d", epi);
+        }
+        return check_launch("w4a4_gemm balanced");
+    }
     const int64_t W = a.part ? sk_shares(a.Mp, a.N, a.K) : 0;
     if (W) {
         const int64_t tiles = (a.N / 256) * (a.Mp / 128);
@@ -1071,6 +1269,7 @@ __global__ __launch_bounds__(256) void weight_codes_kernel(const uint4* qw, int6
 // 3 = bf16(GELU_tanh(y)) out
 extern "C" int64_t wdl_w4a4_gemm_workspace_bytes(int64_t Mp, int64_t N, int64_t K) {
     if (Mp <= 0 || Mp % 128 || N <= 0 || K <= 0 || K % 64) return 0;
+    if (bal_fits(Mp, N, K)) return BAL_TOKEN_BYTES;
     return 2 * sk_shares(Mp, N, K) * SK_SLOT * int64_t(sizeof(float));
 }
 
