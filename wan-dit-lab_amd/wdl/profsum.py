@@ -19,7 +19,8 @@ import csv
 import re
 import sys
 
-KERNELS = re.compile(r"(w4a4_gemm_kernel<[^>]*>|w4a4_gemm_sk_kernel<[^>]*>|w4a4_merge_kernel<[^>]*>|attn_merge_kernel|"
+KERNELS = re.compile(r"(w4a4_gemm_kernel<[^>]*>|w4a4_gemm_sk_kernel<[^>]*>|w4a4_gemm_bal_kernel<[^>]*>|"
+                     r"w4a4_merge_kernel<[^>]*>|attn_merge_kernel|"
                      r"sage_attn_kernel|quant_kernel|quant_kv_kernel|colstats_kernel|"
                      r"qk_norm_rope_kernel|quant_q_kernel|row_stats_kernel|lora_sum_kernel|kv_append_kernel<[^>]*>|"
                      r"finalize_kernel|bitwise_not)")
@@ -80,8 +81,8 @@ def pmc(fetch_path: str, write_path: str, copy_mib: int = 1024) -> str:
         f = sum(fetch[k]) / len(fetch[k]) * ff * 1024 / 1e6
         w = (sum(write[k]) / len(write[k]) * fw * 1024 / 1e6) if k in write else float("nan")
         out.append(f"| `{k[0]}` | {k[1]} | {len(fetch[k])} | {f:.1f} | {w:.1f} | {f + w:.1f} |")
-    # the main-loop launches of the W4A4 GEMM (one-pass and stream-K; the stream-K merge is listed above)
-    gemm = [k for k in keys if k[0].startswith(("w4a4_gemm_kernel", "w4a4_gemm_sk_kernel"))]
+    # the main-loop launches of the W4A4 GEMM (one-pass, balanced and stream-K; the stream-K merge is listed above)
+    gemm = [k for k in keys if k[0].startswith(("w4a4_gemm_kernel", "w4a4_gemm_sk_kernel", "w4a4_gemm_bal_kernel"))]
     if gemm:
         n = sum(len(fetch[k]) for k in gemm)
         fb = sum(sum(fetch[k]) for k in gemm) / n * ff * 1024
