@@ -81,11 +81,14 @@ class Step:
         return self.model.forward(self.latent, self.t, self.start_frame)
 
 
-def mixed_stream_ms(chunks: int, device) -> dict:
+def mixed_stream_ms(chunks: int, device, switch: bool = False) -> dict:
     """The mixed-precision streaming workload at 704x1280: 30 blocks with FP8 weight-only attention projections and
     W4A4 feed-forward, 3-frame chunks of 22 x 40 = 2640 tokens over a full 21-frame window (15840 cached FP8 tokens +
     the chunk = 18480 keys) and 512 prompt tokens, `chunks` consecutive chunks of the DMD loop (4 levels, write pass,
-    commit with eviction), eager, after one chunk of warm-up. Milliseconds per chunk and latent tokens/s."""
+    commit with eviction), eager, after one chunk of warm-up. Milliseconds per chunk and latent tokens/s. switch:
+    then the mid-stream switch to 512x928 (the window's 6 chunks resampled and re-encoded, timed) and `chunks` more
+    chunks at 16 x 29 = 1392 tokens over the 9744-key window. The window starts filled with random FP8 rows and
+    random clean latents for its chunks (synthetic)."""
     import torch
 
     from wdl.block import random_block
@@ -108,6 +111,7 @@ def mixed_stream_ms(chunks: int, device) -> dict:
                      freqs(128, 1024, device))
     stream = ChunkStream(model, (LATENT, grid[0], 2 * grid[1], 2 * grid[2]), g)
     stream.start = WINDOW - grid[0]
+    stream.kept = [(f, torch.randn(stream.shape, generator=g, device=device)) for f in range(0, stream.start, grid[0])]
     stream.next_chunk()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -118,10 +122,28 @@ def mixed_stream_ms(chunks: int, device) -> dict:
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / chunks
     log(f"bench: 704x1280 mixed precision: {ms:.2f} ms per chunk over {chunks} chunks (DMD loop, eager)")
-    return {"workload": "704x1280, 3-frame chunks of 22x40 = 2640 tokens, 21-frame window (18480 keys, FP8 KV), 512 "
-                        "prompt tokens, attention projections FP8 weight-only, FFN W4A4, DMD loop (4 levels + write "
-                        "pass + commit), eager", "chunks": chunks, "ms_per_chunk": ms,
-            "latent_tokens_per_s": tokens / (ms * 1e-3)}
+    out = {"workload": "704x1280, 3-frame chunks of 22x40 = 2640 tokens, 21-frame window (18480 keys, FP8 KV), 512 "
+                       "prompt tokens, attention projections FP8 weight-only, FFN W4A4, DMD loop (4 levels + write "
+                       "pass + commit), eager", "chunks": chunks, "ms_per_chunk": ms,
+           "latent_tokens_per_s": tokens / (ms * 1e-3)}
+    if switch:
+        e0.record()
+        stream.switch_resolution(32, 58)
+        e1.record()
+        torch.cuda.synchronize()
+        ms_switch = e0.elapsed_time(e1)
+        stream.next_chunk()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(chunks):
+            stream.next_chunk()
+        e1.record()
+        torch.cuda.synchronize()
+        ms2 = e0.elapsed_time(e1) / chunks
+        log(f"bench: switch to 512x928: {ms_switch:.2f} ms (6 chunks re-encoded); then {ms2:.2f} ms per chunk")
+        out["switch_512x928"] = {"ms_switch": ms_switch, "reencoded_chunks": 6, "ms_per_chunk_after": ms2,
+                                 "latent_tokens_per_s_after": 1392 / (ms2 * 1e-3)}
+    return out
 
 
 def chunk_ms(step, chunks: int) -> float:
@@ -371,6 +393,9 @@ def main():
     ap.add_argument("--mixed-704", type=int, default=0, metavar="C",
                     help="also stream C chunks of the mixed-precision 704x1280 workload (FP8 weight-only attention "
                          "projections, W4A4 FFN, 2640-token chunks over an 18480-key window), as mixed_704x1280")
+    ap.add_argument("--switch", action="store_true",
+                    help="with --mixed-704: then switch to 512x928 mid-stream (window re-encoded) and stream C more "
+                         "chunks")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain elementwise copy of MIB MiB (bitwise_not, uint8) three times: the "
                          "known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -470,7 +495,7 @@ def main():
             del graph
         torch.cuda.empty_cache()
         with torch.no_grad():
-            result["mixed_704x1280"] = mixed_stream_ms(args.mixed_704, dev)
+            result["mixed_704x1280"] = mixed_stream_ms(args.mixed_704, dev, args.switch)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)

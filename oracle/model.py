@@ -10,10 +10,19 @@ Pinned by: the noise levels against the reference's own fixture (tests/test_caus
 [1, 0.9375, 5/6, 0.625]); the patch embedding as torch.nn.functional.conv3d (a textbook routine) of the same
 weights; unpatchify as the exact inverse of the patch order (an index identity); the time features against
 their closed form at t = 0 (cos 1, sin 0) and t with omega_0 = 1.
+
+The mid-stream resolution switch has no reference counterpart (the reference's stream keeps its size,
+causal.py:471-472; its recache, causal.py:662-678, re-encodes the window at the same size): resample() states
+the build's latent resampling, separable, Pillow's antialiased bilinear (the triangle filter max(0, 1 - |t|)
+widened to the scale when shrinking, half-pixel centres, weights normalised over the taps inside the frame), in
+float64; reencode() writes resampled chunks into fresh caches by the write pass at their frame positions. Pinned
+by (tests/test_switch.py): torch's antialiased bilinear interpolation (a library routine) on random frames,
+the identity at the same size, and constant frames staying constant.
 """
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -118,3 +127,35 @@ def next_chunk_unipc(noise: torch.Tensor, E: dict, blocks: list, caches: list, c
     for cache in caches:
         cache["at"] += n
     return x0
+
+
+def _taps(n_in: int, n_out: int):
+    """Weights [n_out, n_in] of one axis of the antialiased bilinear resampling (float64)."""
+    scale = n_in / n_out
+    support = scale if scale >= 1 else 1.0
+    inv = 1 / scale if scale >= 1 else 1.0
+    W = np.zeros((n_out, n_in))
+    for i in range(n_out):
+        centre = scale * (i + 0.5)
+        lo, hi = max(int(centre - support + 0.5), 0), min(int(centre + support + 0.5), n_in)
+        w = np.array([max(0.0, 1 - abs((j - centre + 0.5) * inv)) for j in range(lo, hi)])
+        W[i, lo:hi] = w / w.sum()
+    return W
+
+
+def resample(x: torch.Tensor, height: int, width: int) -> torch.Tensor:
+    """Latent frames [C, f, H, W] -> fp32 [C, f, height, width], each frame through the row and column taps."""
+    C, f, H, W = x.shape
+    rows, cols = _taps(H, height), _taps(W, width)
+    y = np.einsum("ih,cfhw,jw->cfij", rows, x.double().numpy(), cols)
+    return torch.from_numpy(y).float()
+
+
+def reencode(kept: list, E: dict, blocks: list, caches: list, ctx_kvs: list, freq, heads: int) -> None:
+    """The write pass (t = 0) over the chunks `kept` [(first frame, latents at the new size)], oldest first, into
+    `caches` (fresh, sized for the new tokens per frame); each cache's `at` advances by a chunk after each."""
+    for first, x in kept:
+        model_forward(x, torch.zeros(1), E, blocks, caches, ctx_kvs, freq, first, heads)
+        n = x.shape[1] * (x.shape[2] // 2) * (x.shape[3] // 2)
+        for cache in caches:
+            cache["at"] += n

@@ -5,7 +5,8 @@ Small config: dim 256, 2 x 128 heads, FFN 1024, 2 SVD-quantized blocks, 48-chann
 (64 tokens), 16 context tokens. Bars: each edge stage within a few bf16 steps of the oracle on the same input; the
 blocks + Head on the oracle's edge outputs within the block bar (max-rel-err 1e-2, 2^-8 relative L2); end to end
 (one step, and x0 over two chunks of the loop) within 1.5x of the oracle's own change under 50 one-step input
-changes (random-weight W4A4 blocks are chaotic at that level), and so the cached keys of the chunk loop."""
+changes (random-weight W4A4 blocks are chaotic at that level), and so the cached keys of the chunk loop; the
+mid-stream resolution switch (the window re-encoded at a new latent size) at the same bars."""
 
 import pytest
 import torch
@@ -163,3 +164,62 @@ def test_unipc_chunk_loop_matches_oracle(gpu):
         print(f"unipc chunk {chunk}: x0 error / x0 change {rel:.3e} (oracle under 50 one-step changes: {floor:.3e})")
         assert rel <= 1.5 * max(floor, 0.02)
         assert all(c.saved == (chunk + 1) * n for c in model.caches)
+
+
+def test_resolution_switch_reencodes_the_window(gpu):
+    """Two chunks at 8 x 16 latents (64 tokens per chunk), then the switch to 12 x 8 (48 per chunk, grid 2 x 6 x 4):
+    the kept chunks' latents resampled as the oracle resamples them (within fp32 rounding); every block's cache
+    rebuilt for the same 8-frame window at the new tokens per frame and refilled by the write pass, its keys
+    (dequantized) against the oracle's write pass over the same resampled latents, and then one chunk at the new
+    size against the oracle's chunk loop over those caches, both within the chunk-loop bar (1.5x the oracle's own
+    change under 50 one-step input changes, floor 2 %)."""
+    import copy
+
+    from wdl import model as wmodel
+
+    model, (E, Ps, _, octx, freq), g, n = setup(8)
+    gen = torch.Generator(device="cuda").manual_seed(13)
+    stream = wmodel.ChunkStream(model, SHAPE, gen)
+    for _ in range(2):
+        stream.next_chunk(torch.randn(SHAPE, generator=g).cuda())
+    kept = [(f, x.cpu()) for f, x in stream.kept]
+    assert [f for f, _ in kept] == [0, 2]
+    H2, W2 = 12, 8
+    stream.switch_resolution(H2, W2)
+    n2 = SHAPE[1] * (H2 // 2) * (W2 // 2)
+    assert stream.shape == (48, 2, H2, W2) and stream.start == 4
+    assert all(c.max_tokens == 4 * n2 and c.saved == 2 * n2 for c in model.caches)
+    resampled = [(f, x.cpu()) for f, x in stream.kept]
+    for (f, x), (f2, y) in zip(kept, resampled):
+        want = omodel.resample(x, H2, W2)
+        assert f == f2 and float((y - want).abs().max()) <= 2e-5 * float(x.abs().max())
+    cap = 5 * n2
+    fresh_caches = lambda: [dict(k=torch.zeros(1, cap, HEADS, 128, dtype=torch.float8_e4m3fn),
+                                 ks=torch.ones(1, cap, HEADS, 1),
+                                 v=torch.zeros(1, cap, HEADS, 128, dtype=torch.float8_e4m3fn),
+                                 vs=torch.ones(1, cap, HEADS, 1), at=0) for _ in range(NB)]
+    oc, pc = fresh_caches(), fresh_caches()
+    omodel.reencode(resampled, E, Ps, oc, octx, freq, HEADS)
+    omodel.reencode([(f, perturbed(x, 50, 60 + f)) for f, x in resampled], E, Ps, pc, octx, freq, HEADS)
+    deq = lambda k, ks: k[:, :2 * n2].float() * ks[:, :2 * n2]
+    for c, o, p in zip(model.caches, oc, pc):
+        ref_k = deq(o["k"], o["ks"])
+        rel = float((deq(c.k.cpu(), c.ks.cpu()) - ref_k).norm() / ref_k.norm())
+        floor = float((deq(p["k"], p["ks"]) - ref_k).norm() / ref_k.norm())
+        print(f"re-encoded keys: rel-L2 {rel:.3e} (oracle under 50 one-step changes: {floor:.3e})")
+        assert rel <= 1.5 * max(floor, 0.02)
+    # one chunk at the new size from the re-encoded caches (the stream's renoising draws reproduced)
+    ref_gen = torch.Generator(device="cuda").manual_seed(13)
+    for _ in range(6):
+        torch.randn(SHAPE, generator=ref_gen, device="cuda")
+    shape2 = (48, 2, H2, W2)
+    noise = torch.randn(shape2, generator=g)
+    x0 = stream.next_chunk(noise.cuda()).cpu()
+    fresh = [torch.randn(shape2, generator=ref_gen, device="cuda").cpu() for _ in range(3)]
+    pert = omodel.next_chunk(perturbed(noise, 50, 70), fresh, E, Ps, copy.deepcopy(oc), octx, freq, 4, HEADS)
+    ref = omodel.next_chunk(noise, fresh, E, Ps, oc, octx, freq, 4, HEADS)
+    rel = float((x0 - ref).norm() / (ref - noise).norm())
+    floor = float((pert - ref).norm() / (ref - noise).norm())
+    print(f"chunk after the switch: x0 error / x0 change {rel:.3e} (oracle under 50 one-step changes: {floor:.3e})")
+    assert rel <= 1.5 * max(floor, 0.02)
+    assert all(c.saved == 3 * n2 for c in model.caches)

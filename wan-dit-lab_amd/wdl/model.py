@@ -18,6 +18,13 @@ noise; then the write pass at t = 0 puts the final keys and values in the caches
 the chunk is denoised by the UniPC sampler instead (causal.py:620-636, LongLive 2.0's; wdl.unipc): the model at the
 sampler's integer timesteps, each input x_0 - C[k] . flows of the plan, the clean latents its last row. Not restated:
 prompt blending, re-anchoring, shots and context noise.
+
+ChunkStream.switch_resolution changes the latent size mid-stream (a mode of this build; the reference's Stream has a
+fixed size, causal.py:471-472, and its recache, causal.py:662-678, re-encodes the window at the same size): the
+clean latents of the chunks the caches hold are resampled to the new size (resample_latents), every block gets a
+cache of the same window in frames at the new tokens per frame, and the resampled chunks are written into it by
+the write pass (t = 0) at their original frame positions, oldest first, as recache does. The RoPE grid follows
+from each call's latent size.
 """
 
 from __future__ import annotations
@@ -52,6 +59,27 @@ def patch_matrix(x: torch.Tensor) -> torch.Tensor:
     if H % 2 or W % 2:
         raise ValueError(f"latent height and width must be even, got {H} x {W}")
     return x.reshape(C, f, H // 2, 2, W // 2, 2).permute(1, 2, 4, 0, 3, 5).reshape(f * (H // 2) * (W // 2), C * 4)
+
+
+def resample_latents(x: torch.Tensor, height: int, width: int) -> torch.Tensor:
+    """Latent frames [C, f, H, W] -> fp32 [C, f, height, width]: each frame and channel resampled bilinearly with
+    half-pixel centres and, when shrinking, the triangle filter widened to the scale (F.interpolate, bilinear,
+    align_corners=False, antialias=True)."""
+    C, f, H, W = x.shape
+    y = F.interpolate(x.float().permute(1, 0, 2, 3), size=(height, width), mode="bilinear", align_corners=False,
+                      antialias=True)
+    return y.permute(1, 0, 2, 3).contiguous()
+
+
+def window_chunks(kept: list, chunk: int, window_frames: int, sink_frames: int) -> list:
+    """The chunks a cache of `window_frames` frames (the first `sink_frames` never evicted) holds after the chunks
+    of `kept` [(first frame, latents)] were committed in order: the sink's chunks and the newest that fit."""
+    if sink_frames % chunk or (window_frames - sink_frames) % chunk:
+        raise ValueError("the window and its sink must hold whole chunks")
+    nsink, nring = sink_frames // chunk, (window_frames - sink_frames) // chunk
+    if len(kept) <= nsink + nring:
+        return list(kept)
+    return kept[:nsink] + (kept[len(kept) - nring:] if nring else [])
 
 
 def unpatchify(y: torch.Tensor, grid, out_dim: int) -> torch.Tensor:
@@ -145,6 +173,7 @@ class ChunkStream:
         self.model, self.shape, self.generator = model, tuple(shape), generator
         self.levels = sigmas(shift) if levels is None else list(levels)
         self.write_pass, self.start, self.sampler = write_pass, 0, sampler
+        self.kept = []  # (first frame, clean latents) of the chunks the caches hold, oldest first
         if sampler == "unipc":
             timesteps, C = unipc.plan(steps or len(STEPS), shift)
             self.timesteps, self.plan = timesteps, C.tolist()
@@ -168,8 +197,44 @@ class ChunkStream:
             self.model.forward(x0, torch.zeros(1, device=dev), self.start)
         for cache in self.model.caches:
             cache.commit()
+        self._keep(self.start, x0)
         self.start += self.shape[1]
         return x0
+
+    def _window(self):
+        """(frames the caches hold, of which sink) at the current latent size."""
+        c = self.model.caches[0]
+        per_frame = (self.shape[2] // 2) * (self.shape[3] // 2)
+        return c.max_tokens // per_frame, c.sink_tokens // per_frame
+
+    def _keep(self, first_frame: int, x0: torch.Tensor):
+        frames, sink = self._window()
+        self.kept = window_chunks(self.kept + [(first_frame, x0)], self.shape[1], frames, sink)
+
+    @torch.no_grad()
+    def switch_resolution(self, height: int, width: int):
+        """Continue the stream at latents of height x width: the kept chunks resampled, each block's cache rebuilt
+        for the same window in frames at the new tokens per frame and refilled by the write pass over them (t = 0,
+        their original frame positions, oldest first; the caches commit after each, as recache does)."""
+        from wdl.kvcache import KVCache
+
+        if height % 2 or width % 2 or height <= 0 or width <= 0:
+            raise ValueError(f"latent height and width must be positive and even, got {height} x {width}")
+        frames, sink = self._window()
+        chunk = self.shape[1]
+        window_chunks([], chunk, frames, sink)  # the window holds whole chunks
+        per_frame = (height // 2) * (width // 2)
+        self.model.caches[:] = [KVCache(frames * per_frame, sink * per_frame, chunk=chunk,
+                                        entropy_ratio=c.entropy_ratio) for c in self.model.caches]
+        self.shape = (self.shape[0], chunk, height, width)
+        kept, self.kept = self.kept, []
+        dev = self.model.freq.device
+        for first, x0 in kept:
+            x = resample_latents(x0, height, width)
+            self.model.forward(x, torch.zeros(1, device=dev), first)
+            for cache in self.model.caches:
+                cache.commit()
+            self._keep(first, x)
 
     def _unipc(self, noise: torch.Tensor) -> torch.Tensor:
         """The UniPC steps from `noise`: the model at each timestep on x_0 - C[k] . flows; the clean latents."""
