@@ -6,7 +6,9 @@ tokens, random-init W4A4 weights of that architecture (synthetic data; no checkp
 WanModel.forward (src/wan_dit_lab/models/model.py:32-84): patch embedding, time embedding and projection, the 30
 blocks (each writing its chunk into its FP8 cache and attending over the window), head and unpatchify. The
 timed loop replays one HIP graph of the whole step K times; the per-kernel durations (W4A4 GEMM, attention) come
-from an instrumented eager step with HIP events on the launch stream.
+from an instrumented eager step with HIP events on the launch stream. The cache's column statistics (K sums, |V|
+maxima of the cached rows) are refreshed by the commit that changes those rows, not by the step; chunk_ms (the DMD
+loop's 4 levels, write pass and commit) includes them.
 
 Prints one JSON line (rank 0; one GPU).
 """
@@ -387,7 +389,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of the HIP graph")
-    ap.add_argument("--chunks", type=int, default=0, metavar="C",
+    ap.add_argument("--chunks", type=int, default=3, metavar="C",
                     help="also time C whole chunks of the DMD loop (4 levels + write pass + cache commit, eager) "
                          "after the step measurement, as chunk_ms")
     ap.add_argument("--mixed-704", type=int, default=0, metavar="C",
@@ -472,7 +474,11 @@ def main():
                                "14336, 3-frame chunk of 16x29 = 1392 tokens, 21-frame window = 9744 keys (FP8 KV), "
                                "512 cross tokens, all block linears W4A4, HIP-graph replay",
                    "tokens": TOKENS, "keys": CACHED + TOKENS, "context": CONTEXT, "blocks": BLOCKS,
-                   "graph": not args.eager},
+                   "graph": not args.eager,
+                   "cache_statistics": "each block's Sage preparation reads the K column sums and |V| maxima of its "
+                                       "8352 cached rows from the cache, which refreshes them at a commit (outside "
+                                       "the step, as the commit's row copies are; once per chunk of 5 passes, "
+                                       "included in chunk_ms), and sums only the chunk's 1392 tokens"},
         "gemm_tops": g["tops"],
         "gemm_pct_int8_peak": 100 * gemm_frac,
         "gemm_ms_per_step": g["ms"],

@@ -230,6 +230,25 @@ int wdl_sage_prep_mapped(const void* cache_k, const float* cache_ks, const void*
                          int64_t n, int splits, float* workspace, void* k_int8, float* k_scale, void* v_fp8,
                          float* k_mean_out, float* v_scale_out, wdl_stream_t stream);
 
+/* Statistics of the cached tokens [0, at) for wdl_sage_prep_cached: stats fp32 [2, heads, 128] = the K column sums
+ * (`splits` token splits, each summed in a fixed order, then added in split order) and the |V| column maxima, of
+ * cache rows 0 .. at-1 (e4m3 value times the row's scale). No counterpart in the reference, whose _sum_max pass
+ * (src/wan_dit_lab/kernels/sage_kv.py:43-60) re-reads every cached token at every call: the statistics change only
+ * when the cache's rows [0, at) do, so KVCache refreshes them at a commit. workspace: wdl_sage_prep_workspace_floats
+ * floats. Batch 1; at = 0 gives zeros. */
+int wdl_sage_cache_stats(const void* cache_k, const float* cache_ks, const void* cache_v, const float* cache_vs,
+                         int64_t capacity, int64_t heads, int64_t at, int splits, float* workspace, float* stats,
+                         wdl_stream_t stream);
+
+/* wdl_sage_prep with the cached tokens' statistics from wdl_sage_cache_stats (same cache, same at): the statistics
+ * pass reads only the chunk's n tokens, k_mean = (cached K sums + the chunk's, in split order) / (at + n),
+ * v_scale = max(cached |V| maxima, the chunk's, 1e-8) / 2.25; the quantization is wdl_sage_prep's. The K mean
+ * differs from wdl_sage_prep's only in the fp32 summation order. */
+int wdl_sage_prep_cached(const void* cache_k, const float* cache_ks, const void* cache_v, const float* cache_vs,
+                         int64_t capacity, const void* k, int64_t ldk, const void* v, int64_t ldv, int64_t heads,
+                         int64_t at, int64_t n, const float* cache_stats, int splits, float* workspace, void* k_int8,
+                         float* k_scale, void* v_fp8, float* k_mean_out, float* v_scale_out, wdl_stream_t stream);
+
 /* Workspace (bytes) of wdl_sage_attn for n queries, L keys and `heads` heads. */
 int64_t wdl_sage_attn_workspace_bytes(int64_t n, int64_t L, int64_t heads);
 

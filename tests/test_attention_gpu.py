@@ -52,14 +52,20 @@ def test_quant_q_bit_exact(gpu, n, H):
     assert torch.equal(qs.cpu(), rqs)
 
 
-@pytest.mark.parametrize("at,n,H", [(200, 150, 3), (0, 130, 2), (928, 464, 24), (6600, 2640, 2)])
-def test_sage_prep_k_and_v(gpu, at, n, H):
+@pytest.mark.parametrize("cached", [False, True], ids=["whole", "cached-stats"])
+@pytest.mark.parametrize("at,n,H", [(200, 150, 3), (0, 130, 2), (928, 464, 24), (6600, 2640, 2), (8352, 1392, 2),
+                                    (1, 1, 2)])
+def test_sage_prep_k_and_v(gpu, at, n, H, cached):
+    """cached-stats: the preparation from the cached rows' statistics (wdl_sage_cache_stats) plus the chunk's
+    tokens, held to the same bars."""
     from wdl import sage_kv
 
     kbias = torch.randn(1, 1, H, 128, generator=torch.Generator().manual_seed(5)) * 3
     Q, k, ks, v, vs, at, K, V = setup(at, n, H=H, seed=at + n, kbias=kbias)
     ks = ks * 0.5 + torch.rand(ks.shape, generator=torch.Generator().manual_seed(1))  # non-unit cache scales
-    p = sage_kv.prep(*cuda(k, ks, v, vs), at, *cuda(K, V))
+    vs = vs * 0.25 + torch.rand(vs.shape, generator=torch.Generator().manual_seed(2))
+    stats = sage_kv.cache_stats(*cuda(k, ks, v, vs), at) if cached else None
+    p = sage_kv.prep(*cuda(k, ks, v, vs), at, *cuda(K, V), cache_stats=stats)
     torch.cuda.synchronize()
     L = at + n
     Lp = (L + 63) // 64 * 64
@@ -84,6 +90,28 @@ def test_sage_prep_k_and_v(gpu, at, n, H):
     want = osage.wdl_v_layout(vq)[0].view(torch.uint8)  # [H, 128, Lpad]
     assert p["v"].shape == (H, 128, Lp)
     assert torch.equal(p["v"].cpu(), want)
+
+
+@pytest.mark.parametrize("at,H", [(0, 2), (1, 3), (63, 2), (200, 3), (8352, 24)])
+def test_cache_stats_against_float64_sums_and_exact_maxima(gpu, at, H):
+    """wdl_sage_cache_stats: the K column sums within 1e-5 of the sum of |values| (a token dropped or counted twice
+    moves a sum by ~1e-4 of it at 8352 tokens), the |V| maxima exact (fp32 products of e4m3 values and scales)."""
+    from wdl import sage_kv
+
+    g = torch.Generator().manual_seed(at + H)
+    cap = at + 70
+    k = (torch.randn(1, cap, H, 128, generator=g) * 2 + 1).to(torch.float8_e4m3fn)
+    v = torch.randn(1, cap, H, 128, generator=g).to(torch.float8_e4m3fn)
+    ks = torch.rand(1, cap, H, 1, generator=g) + 0.1
+    vs = torch.rand(1, cap, H, 1, generator=g) + 0.1
+    stats = sage_kv.cache_stats(*cuda(k, ks, v, vs), at).cpu()
+    assert stats.shape == (2, H, 128)
+    Kc = k[0, :at].float() * ks[0, :at]
+    Vc = v[0, :at].float() * vs[0, :at]
+    want = Kc.double().sum(0)
+    bound = 1e-5 * Kc.double().abs().sum(0) + 1e-30
+    assert bool(((stats[0].double() - want).abs() <= bound).all())
+    assert torch.equal(stats[1], Vc.abs().amax(0) if at else torch.zeros(H, 128))
 
 
 

@@ -59,3 +59,42 @@ def test_window_holds_sink_and_newest_frames_past_many_commits(gpu, window, sink
         frames += [(K[0, f * T:(f + 1) * T], V[0, f * T:(f + 1) * T]) for f in range(CHUNK)]
     print(f"window {window}, sink {sink}: worst error against exact attention {worst:.4f}")
     assert cache.full()
+
+
+def test_captured_attend_follows_commits_through_the_cached_statistics(gpu):
+    """A HIP graph of KVCache.attend captured on a full window stays correct across commits: each commit rewrites
+    the ring rows and refreshes the cached column statistics in place, so every replay equals an eager attend after
+    the same commits bit for bit, and matches the preparation from all tokens (no cached statistics) to the Sage
+    bar. Replays alternate with eager work and synchronisations."""
+    from wdl import sage_kv
+    from wdl.kvcache import KVCache
+
+    g = torch.Generator().manual_seed(77)
+    window = 9
+    cache = KVCache((window - CHUNK) * T, 0, chunk=CHUNK)
+    new = lambda: [torch.randn(1, CHUNK * T, H, 128, generator=g).to(torch.bfloat16).cuda() for _ in range(3)]
+    for _ in range(4):  # past a full window
+        cache.attend(*new())
+        cache.commit()
+    assert cache.full()
+    Q, K, V = new()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        cache.attend(Q, K, V)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = cache.attend(Q, K, V)
+    for _ in range(3):
+        Qn, Kn, Vn = new()
+        cache.attend(Qn, Kn, Vn)  # the next chunk, eager, then its commit (eviction and statistics)
+        cache.commit()
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out.clone()
+        eager = cache.attend(Q, K, V)
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, eager)
+        whole = sage_kv.attend(Q, cache.k, cache.ks, cache.v, cache.vs, cache.saved, K, V)
+        assert osage.cosine(eager.cpu().float(), whole.cpu().float()) >= 0.9999

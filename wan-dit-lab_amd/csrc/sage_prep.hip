@@ -5,6 +5,9 @@
 //   colstats   (grid H x S): per split s of the tokens, partial sums of K and maxima of |V| per (head, channel),
 //              each in a fixed order (16 token lanes, then the lanes in order);
 //   finalize   (grid H):     k_mean = (sum over splits, in order) / L;  v_scale = max(max |V|, 1e-8) / 2.25;
+//              with cached statistics of tokens [0, at) (wdl_sage_cache_stats: their sums and maxima, formed the
+//              same way over splits of [0, at)) the splits cover only the chunk's tokens and the sum starts from
+//              the cached one;
 //   quant_kv   (grid blocks x H): K - mean to int8 with one scale per group g = 0..3 of each 64-token block (tokens
 //              8i + 2g, 8i + 2g + 1): scale = max|x| / 127 + 1e-7, q = trunc(x / scale +- 0.5);
 //              V / v_scale to e4m3, stored per (head, channel) along the tokens in wdl's order: within a
@@ -101,13 +104,14 @@ __device__ __forceinline__ void colstats_range(const Src& k, const Src& v, int64
     }
 }
 
-__global__ __launch_bounds__(256) void colstats_kernel(Src k, Src v, int64_t H, int64_t at, int64_t L, int S,
-                                                       float* part_k, float* part_v) {
+// the tokens [t0, L) in S splits
+__global__ __launch_bounds__(256) void colstats_kernel(Src k, Src v, int64_t H, int64_t at, int64_t t0, int64_t L,
+                                                       int S, float* part_k, float* part_v) {
     __shared__ float red[2][16][D];
     const int64_t h = blockIdx.x, s = blockIdx.y;
     const int t = threadIdx.x, lane_tok = t / 16, d0 = (t % 16) * 8;
-    const int64_t per = (L + S - 1) / S;
-    const int64_t lo = s * per, hi = min(L, lo + per);
+    const int64_t per = (L - t0 + S - 1) / S;
+    const int64_t lo = t0 + s * per, hi = min(L, lo + per);
     float ks[8] = {}, vm[8] = {};
     // this lane's tokens lo + lane_tok + 16 i: the cached ones first, then the chunk's
     const int64_t first = lo + lane_tok;
@@ -131,14 +135,16 @@ __global__ __launch_bounds__(256) void colstats_kernel(Src k, Src v, int64_t H, 
     }
 }
 
+// base: null, or cached statistics [2][H][D] (K sums, |V| maxima) the splits' values are added to; raw: write the
+// sums and maxima into k_mean (as [2][H][D]) instead of the mean and v_scale
 __global__ void finalize_kernel(const float* part_k, const float* part_v, int S, int64_t H, int64_t L, float* k_mean,
-                                float* v_scale) {
+                                float* v_scale, const float* base, int raw) {
     const int64_t h = blockIdx.x;
     const int d = threadIdx.x;
     // the splits in increasing order; the loads of a batch of 16 are all issued before the first add (one memory
     // round trip per batch, not one per split)
     constexpr int BATCH = 16;
-    float a = 0.0f, m = 0.0f;
+    float a = base ? base[h * D + d] : 0.0f, m = base ? base[(H + h) * D + d] : 0.0f;
     for (int s0 = 0; s0 < S; s0 += BATCH) {
         float pk[BATCH], pv[BATCH];
 #pragma unroll
@@ -153,6 +159,11 @@ __global__ void finalize_kernel(const float* part_k, const float* part_v, int S,
                 a = a + pk[j];
                 m = fmaxf(m, pv[j]);
             }
+    }
+    if (raw) {
+        k_mean[h * D + d] = a;
+        k_mean[(H + h) * D + d] = m;
+        return;
     }
     k_mean[h * D + d] = a / float(L);
     v_scale[h * D + d] = fmaxf(m, 1e-8f) / 2.25f;
@@ -301,7 +312,8 @@ static int sage_prep_launch(const void* cache_k, const float* cache_ks, const vo
                             int64_t capacity, int64_t cache_heads, const int32_t* heads_map,
                             const int32_t* tokens_map, const void* k, int64_t ldk, const void* v, int64_t ldv,
                             int64_t heads, int64_t at, int64_t n, int splits, float* workspace, void* k_int8,
-                            float* k_scale, void* v_fp8, float* k_mean_out, float* v_scale_out, hipStream_t stream) {
+                            float* k_scale, void* v_fp8, float* k_mean_out, float* v_scale_out, hipStream_t stream,
+                            const float* cache_stats = nullptr) {
     const int64_t L = at + n;
     if (at < 0 || n < 0 || heads <= 0 || at > capacity || splits < 1 || ldk < heads * D || ldv < heads * D ||
         cache_heads < heads || (!heads_map && cache_heads != heads))
@@ -323,11 +335,14 @@ static int sage_prep_launch(const void* cache_k, const float* cache_ks, const vo
     float* part_v = workspace + int64_t(splits) * heads * D;
     float* k_mean = k_mean_out ? k_mean_out : workspace + 2 * int64_t(splits) * heads * D;
     float* v_scale = v_scale_out ? v_scale_out : k_mean + heads * D;
-    colstats_kernel<<<dim3(unsigned(heads), unsigned(splits)), 256, 0, stream>>>(sk, sv, heads, at, L, splits, part_k,
-                                                                                 part_v);
+    // with cached statistics of tokens [0, at), only the chunk's tokens are summed here
+    const int64_t t0 = cache_stats ? at : 0;
+    colstats_kernel<<<dim3(unsigned(heads), unsigned(splits)), 256, 0, stream>>>(sk, sv, heads, at, t0, L, splits,
+                                                                                 part_k, part_v);
     int rc = check_launch("sage_prep colstats");
     if (rc) return rc;
-    finalize_kernel<<<unsigned(heads), D, 0, stream>>>(part_k, part_v, splits, heads, L, k_mean, v_scale);
+    finalize_kernel<<<unsigned(heads), D, 0, stream>>>(part_k, part_v, splits, heads, L, k_mean, v_scale, cache_stats,
+                                                       0);
     rc = check_launch("sage_prep finalize");
     if (rc) return rc;
     quant_kv_kernel<<<dim3(unsigned(Lpad / 64), unsigned(heads)), 256, 0, stream>>>(
@@ -353,4 +368,38 @@ extern "C" int wdl_sage_prep_mapped(const void* cache_k, const float* cache_ks, 
     return sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, capacity, cache_heads, heads_map, tokens_map, k,
                             ldk, v, ldv, heads, at, n, splits, workspace, k_int8, k_scale, v_fp8, k_mean_out,
                             v_scale_out, stream);
+}
+
+extern "C" int wdl_sage_cache_stats(const void* cache_k, const float* cache_ks, const void* cache_v,
+                                    const float* cache_vs, int64_t capacity, int64_t heads, int64_t at, int splits,
+                                    float* workspace, float* stats, hipStream_t stream) {
+    if (at < 0 || heads <= 0 || at > capacity || capacity < 1 || splits < 1)
+        return fail(WDL_EINVAL, "sage_cache_stats: bad shape");
+    if (!cache_k || !cache_ks || !cache_v || !cache_vs || !workspace || !stats)
+        return fail(WDL_EINVAL, "sage_cache_stats: null pointer");
+    if ((reinterpret_cast<uintptr_t>(cache_k) | reinterpret_cast<uintptr_t>(cache_v)) % 16)
+        return fail(WDL_EINVAL, "sage_cache_stats: the caches must be 16-byte aligned");
+    // tokens [0, at), all from the cache (no chunk: the chunk source is never read)
+    Src sk{static_cast<const uint8_t*>(cache_k), cache_ks, nullptr, heads * D, heads, capacity, nullptr, nullptr};
+    Src sv{static_cast<const uint8_t*>(cache_v), cache_vs, nullptr, heads * D, heads, capacity, nullptr, nullptr};
+    float* part_k = workspace;
+    float* part_v = workspace + int64_t(splits) * heads * D;
+    colstats_kernel<<<dim3(unsigned(heads), unsigned(splits)), 256, 0, stream>>>(sk, sv, heads, at, 0, at, splits,
+                                                                                 part_k, part_v);
+    const int rc = check_launch("sage_cache_stats colstats");
+    if (rc) return rc;
+    finalize_kernel<<<unsigned(heads), D, 0, stream>>>(part_k, part_v, splits, heads, at, stats, nullptr, nullptr, 1);
+    return check_launch("sage_cache_stats finalize");
+}
+
+extern "C" int wdl_sage_prep_cached(const void* cache_k, const float* cache_ks, const void* cache_v,
+                                    const float* cache_vs, int64_t capacity, const void* k, int64_t ldk,
+                                    const void* v, int64_t ldv, int64_t heads, int64_t at, int64_t n,
+                                    const float* cache_stats, int splits, float* workspace, void* k_int8,
+                                    float* k_scale, void* v_fp8, float* k_mean_out, float* v_scale_out,
+                                    hipStream_t stream) {
+    if (!cache_stats) return fail(WDL_EINVAL, "sage_prep_cached: null cache statistics");
+    return sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, capacity, heads, nullptr, nullptr, k, ldk, v, ldv,
+                            heads, at, n, splits, workspace, k_int8, k_scale, v_fp8, k_mean_out, v_scale_out, stream,
+                            cache_stats);
 }

@@ -114,6 +114,13 @@ def prep():
         L = at + n
         moved = 2 * (2 * at * H * 132 + 2 * n * H * 256) + 2 * L * H * 128  # inputs read twice, outputs written once
         print(f"prep n={n} L={L}: {us:.1f} us ({moved / us / 1e3:.0f} GB/s)", flush=True)
+        stats = ops.sage_cache_stats_launch(ck.view(torch.uint8), cks, ck.view(torch.uint8), cks, at)
+        us_c = _replay_us(lambda: ops.sage_prep_launch(ck.view(torch.uint8), cks, ck.view(torch.uint8), cks, K, V, at,
+                                                       cache_stats=stats))
+        us_s = _replay_us(lambda: ops.sage_cache_stats_launch(ck.view(torch.uint8), cks, ck.view(torch.uint8), cks,
+                                                              at, out=stats))
+        print(f"prep n={n} L={L} from cached statistics: {us_c:.1f} us; the statistics of the {at} cached rows: "
+              f"{us_s:.1f} us", flush=True)
 
 
 def gemm():

@@ -7,6 +7,14 @@ the ring; the last n rows take the chunk once the ring is full. attend() writes 
 row `saved` and attends over rows [0, saved) and the chunk (wdl::sage_kv_attend), the sage + fp8 branch of
 KVCache.attend (causal.py:193-210).
 
+Column statistics. The Sage preparation needs the K column means and |V| column maxima over every key it attends
+to. Those of rows [0, saved) change only when those rows do (a commit, a reset, a new `saved`), while a chunk runs
+its denoising levels and write pass over the same rows; so the cache keeps them (`stats`, fp32 [2, H, 128]: K sums
+and |V| maxima, wdl_sage_cache_stats), refreshes them eagerly at a commit and lazily at the next attend after
+`saved` is set, and attend's preparation reads only the chunk's own tokens beside them. A caller that writes rows
+[0, saved) itself calls invalidate_stats() afterwards. A HIP graph captured over attend reads `stats` in place, so
+its replays stay correct across commits.
+
 Host side. Which ring slot holds which token is bookkeeping on the host (`_FrameQueue`): the ring's frames in the
 order they were committed, each with the slots of its tokens in token order. Attention does not depend on where a
 key sits, only the eviction order does, and the reference defines it as "the oldest unpinned tokens of the video
@@ -77,7 +85,32 @@ class KVCache:
         self.fp8 = True
         self.k = self.v = None
         self.queue = _FrameQueue()
+        self.stats = None
+        self._stats_at = -1  # rows [0, _stats_at) are what `stats` describes; -1: stale
         self.reset()
+
+    @property
+    def saved(self) -> int:
+        """Rows [0, saved) hold the committed tokens."""
+        return self._saved
+
+    @saved.setter
+    def saved(self, value: int):
+        self._saved = value
+        self._stats_at = -1
+
+    def invalidate_stats(self):
+        """To call after writing rows [0, saved) other than through attend / commit."""
+        self._stats_at = -1
+
+    def _refresh_stats(self):
+        from wdl.ops import sage_cache_stats_launch
+
+        if self.k is None or not self.k.is_cuda:  # the statistics live beside device buffers only
+            return
+        self.stats = sage_cache_stats_launch(self.k.view(torch.uint8), self.ks, self.v.view(torch.uint8), self.vs,
+                                             self.saved, out=self.stats)
+        self._stats_at = self.saved
 
     def reset(self):
         """Empties the cache; the buffers stay (causal.py:104-114)."""
@@ -105,6 +138,8 @@ class KVCache:
         self.v = torch.zeros_like(self.k)
         self.ks = torch.ones(B, rows, H, 1, device=dev)
         self.vs = torch.ones_like(self.ks)
+        self.stats = torch.zeros(2, H, D, device=dev) if like.is_cuda else None
+        self._stats_at = -1
         self.last_slots = None
         self.queue.clear()
 
@@ -118,8 +153,11 @@ class KVCache:
         if self.k is None:
             self.allocate(V)
         n, at = K.shape[1], self.saved
+        if self._stats_at != at:
+            self._refresh_stats()
         self.store(at, K, V)
-        return attend(Q, self.k, self.ks, self.v, self.vs, at, K, V, sm_scale=self.scale(at + n, Q.shape[-1]))
+        return attend(Q, self.k, self.ks, self.v, self.vs, at, K, V, sm_scale=self.scale(at + n, Q.shape[-1]),
+                      cache_stats=self.stats)
 
     def commit(self):
         """Keeps the chunk that attend last wrote at row `saved` (causal.py:297-327, without turns, decay or
@@ -144,6 +182,7 @@ class KVCache:
         else:
             self.last_slots = None
         self.frames += self.chunk
+        self._refresh_stats()  # rows [0, saved) changed
 
     def _move_rows(self, at: int, n: int, slots: list[int]):
         """Device rows [at, at + n) of the four buffers into the rows of ring slots `slots`, one row per token in
@@ -177,3 +216,4 @@ class KVCache:
         first = self.sink_tokens // self.per_frame
         self.queue.append(first, self.per_frame, list(range(ring)), list(range(ring)))
         self.frames = rows // self.per_frame
+        self._refresh_stats()

@@ -352,11 +352,32 @@ def quant_q_launch(x, heads):
 SPLITS = 32
 
 
-def sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, k, v, at, want_stats=False, heads=None, tokens=None):
+def sage_cache_stats_launch(cache_k, cache_ks, cache_v, cache_vs, at, out=None):
+    """The statistics of cache rows [0, at) (fp8 as uint8 [1, cap, H, 128] + fp32 scales [1, cap, H, 1]) that
+    sage_prep_launch(cache_stats=...) starts from: fp32 [2, H, 128], the K column sums and the |V| column maxima
+    (written into `out` when given)."""
+    H = cache_k.shape[2]
+    dev = cache_k.device
+    if not isinstance(at, int) or at < 0 or at > cache_k.shape[1]:
+        raise ValueError("at outside the cache")
+    if out is None:
+        out = torch.empty(2, H, 128, device=dev, dtype=torch.float32)
+    elif out.shape != (2, H, 128) or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError(f"cache statistics must be contiguous fp32 [2, {H}, 128]")
+    ws = torch.empty(_lib.library().wdl_sage_prep_workspace_floats(H, SPLITS), device=dev, dtype=torch.float32)
+    _lib.call("wdl_sage_cache_stats", ptr(cache_k), ptr(cache_ks), ptr(cache_v), ptr(cache_vs), cache_k.shape[1], H,
+              at, SPLITS, ptr(ws), ptr(out), stream_of(cache_k))
+    return out
+
+
+def sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, k, v, at, want_stats=False, heads=None, tokens=None,
+                     cache_stats=None):
     """Cache (fp8 [1, cap, Hc, 128] + fp32 scales [1, cap, Hc, 1]) tokens [0, at) and the chunk k, v
     (bf16 [n, H*128] row-strided) -> k_int8 [H, Lpad, 128], k_scale [H, Lpad/16], v_fp8 [H, 128, Lpad],
     v_scale [H, 128] (and k_mean when want_stats). heads (int32 [H], device): head h reads cache head heads[h];
-    tokens (int32 [>= at], device): cached token i is cache row tokens[i]; without them Hc = H and rows 0 .. at-1."""
+    tokens (int32 [>= at], device): cached token i is cache row tokens[i]; without them Hc = H and rows 0 .. at-1.
+    cache_stats: sage_cache_stats_launch of the same cache rows [0, at) (no maps): only the chunk's tokens are then
+    read for the K mean and V scale."""
     n = k.shape[0]
     H = k.shape[1] // 128
     Hc = cache_k.shape[2]
@@ -369,7 +390,15 @@ def sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, k, v, at, want_stats=
     v_f8 = torch.empty(H, 128, Lp, device=dev, dtype=torch.uint8)
     k_mean = torch.empty(H, 128, device=dev, dtype=torch.float32)
     v_sc = torch.empty(H, 128, device=dev, dtype=torch.float32)
-    if heads is None and tokens is None:
+    if cache_stats is not None:
+        if heads is not None or tokens is not None:
+            raise ValueError("cache statistics are for the unmapped cache")
+        if cache_stats.shape != (2, H, 128) or cache_stats.dtype != torch.float32 or not cache_stats.is_contiguous():
+            raise ValueError(f"cache statistics must be contiguous fp32 [2, {H}, 128]")
+        _lib.call("wdl_sage_prep_cached", ptr(cache_k), ptr(cache_ks), ptr(cache_v), ptr(cache_vs), cache_k.shape[1],
+                  ptr(k), k.stride(0), ptr(v), v.stride(0), H, at, n, ptr(cache_stats), SPLITS, ptr(ws), ptr(k_i8),
+                  ptr(k_sc), ptr(v_f8), ptr(k_mean), ptr(v_sc), stream_of(k))
+    elif heads is None and tokens is None:
         _lib.call("wdl_sage_prep", ptr(cache_k), ptr(cache_ks), ptr(cache_v), ptr(cache_vs), cache_k.shape[1],
                   ptr(k), k.stride(0), ptr(v), v.stride(0), H, at, n, SPLITS, ptr(ws), ptr(k_i8), ptr(k_sc),
                   ptr(v_f8), ptr(k_mean), ptr(v_sc), stream_of(k))
@@ -521,6 +550,24 @@ def sage_kv_attend(Q: torch.Tensor, cache_k: torch.Tensor, cache_ks: torch.Tenso
 
 @sage_kv_attend.register_fake
 def _(Q, cache_k, cache_ks, cache_v, cache_vs, K, V, at, sm_scale, heads=None, tokens=None):
+    return Q.new_empty(Q.shape, dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("wdl::sage_kv_attend_cached", mutates_args=())
+def sage_kv_attend_cached(Q: torch.Tensor, cache_k: torch.Tensor, cache_ks: torch.Tensor, cache_v: torch.Tensor,
+                          cache_vs: torch.Tensor, K: torch.Tensor, V: torch.Tensor, at: int, sm_scale: float,
+                          cache_stats: torch.Tensor) -> torch.Tensor:
+    """sage_kv_attend over an unmapped cache whose rows [0, at) have the statistics cache_stats
+    (sage_cache_stats_launch): the preparation reads only the chunk's tokens for the K mean and V scale."""
+    _, nq, H, D = Q.shape
+    n = K.shape[1]
+    prep = sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, K[0].reshape(n, H * D) if K.is_contiguous() else
+                            K[0].flatten(1), V[0].flatten(1), at, cache_stats=cache_stats)
+    return sage_attn_q16_launch(Q[0].flatten(1), prep, at + n, sm_scale).view(1, nq, H, D)
+
+
+@sage_kv_attend_cached.register_fake
+def _(Q, cache_k, cache_ks, cache_v, cache_vs, K, V, at, sm_scale, cache_stats):
     return Q.new_empty(Q.shape, dtype=torch.bfloat16)
 
 

@@ -9,12 +9,12 @@ from __future__ import annotations
 
 import torch
 
-from wdl.ops import quant_q_launch, sage_attn_launch, sage_kv_attend, sage_prep_launch
+from wdl.ops import quant_q_launch, sage_attn_launch, sage_kv_attend, sage_kv_attend_cached, sage_prep_launch
 
 V_MAX = 2.25  # sage_kv.py:24
 BLKQ, WARPQ, BLKK = 128, 32, 64
 
-__all__ = ["V_MAX", "attend", "quant_q", "prep"]
+__all__ = ["V_MAX", "attend", "cache_stats", "quant_q", "prep"]
 
 
 def _check(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, heads=None, tokens=None):
@@ -50,15 +50,19 @@ def _check(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, heads=None, tokens
 
 
 def attend(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, sm_scale=None, heads=None, tokens=None,
-           frame_tokens=0):
+           frame_tokens=0, cache_stats=None):
     """softmax(Q K^T * sm_scale) V over the cached tokens and the chunk (sage_kv.py:127-134); [1, nq, H, 128] bf16
     (sm_scale defaults to 128^-0.5). heads (int32 [H]): head h of Q, K, V is cache head heads[h], the cache keeping
     all of them; tokens (int32 [at]): cached token i is cache row tokens[i] (KVCache.attend_split's static heads,
     causal.py:222-241). Neither copies the cache. The maps' ranges are checked on the host (one synchronisation).
     frame_tokens > 0 (not a mode of the reference, whose chunk attention sees the whole chunk): block-causal per
     latent frame of that many tokens, Q being the chunk (nq == n): chunk query q sees the cache and the chunk's
-    frames up to its own, keys below at + (q // frame_tokens + 1) * frame_tokens."""
+    frames up to its own, keys below at + (q // frame_tokens + 1) * frame_tokens. cache_stats (fp32 [2, H, 128],
+    wdl.ops.sage_cache_stats_launch of rows [0, at), no maps): the K mean and V scale then read only the chunk's
+    tokens beside them."""
     _check(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, heads, tokens)
+    if cache_stats is not None and (heads is not None or tokens is not None):
+        raise ValueError("cache statistics are for the unmapped cache")
     if frame_tokens:
         if not isinstance(frame_tokens, int) or frame_tokens < 0 or Q.shape[1] != K.shape[1]:
             raise ValueError("frame_tokens: a positive int, with the chunk's own queries (nq == n)")
@@ -66,11 +70,16 @@ def attend(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, sm_scale=None, hea
 
         n, H = K.shape[1], K.shape[2]
         prep = ops.sage_prep_launch(cache_k.view(torch.uint8), cache_ks, cache_v.view(torch.uint8), cache_vs,
-                                    K[0].flatten(1), V[0].flatten(1), at, heads=heads, tokens=tokens)
+                                    K[0].flatten(1), V[0].flatten(1), at, heads=heads, tokens=tokens,
+                                    cache_stats=cache_stats)
         sm = Q.shape[-1] ** -0.5 if sm_scale is None else float(sm_scale)
         return ops.sage_attn_q16_launch(Q[0].flatten(1), prep, at + n, sm, frame_tokens=frame_tokens).view(Q.shape)
-    return sage_kv_attend(Q, cache_k.view(torch.uint8), cache_ks, cache_v.view(torch.uint8), cache_vs, K, V, at,
-                          Q.shape[-1] ** -0.5 if sm_scale is None else float(sm_scale), heads, tokens)
+    sm = Q.shape[-1] ** -0.5 if sm_scale is None else float(sm_scale)
+    if cache_stats is not None:
+        return sage_kv_attend_cached(Q, cache_k.view(torch.uint8), cache_ks, cache_v.view(torch.uint8), cache_vs, K, V,
+                                     at, sm, cache_stats)
+    return sage_kv_attend(Q, cache_k.view(torch.uint8), cache_ks, cache_v.view(torch.uint8), cache_vs, K, V, at, sm,
+                          heads, tokens)
 
 
 def quant_q(Q):
@@ -80,7 +89,15 @@ def quant_q(Q):
     return q[None], qs[None]
 
 
-def prep(cache_k, cache_ks, cache_v, cache_vs, at, K, V):
-    """The quantized K/V operands of one call in wdl's layouts (see wdl_sage_prep in include/wdl.h)."""
+def prep(cache_k, cache_ks, cache_v, cache_vs, at, K, V, cache_stats=None):
+    """The quantized K/V operands of one call in wdl's layouts (see wdl_sage_prep in include/wdl.h); cache_stats as
+    in attend."""
     return sage_prep_launch(cache_k.view(torch.uint8), cache_ks, cache_v.view(torch.uint8), cache_vs,
-                            K[0].flatten(1), V[0].flatten(1), at, want_stats=True)
+                            K[0].flatten(1), V[0].flatten(1), at, want_stats=True, cache_stats=cache_stats)
+
+
+def cache_stats(cache_k, cache_ks, cache_v, cache_vs, at):
+    """fp32 [2, H, 128]: the K column sums and |V| column maxima of cache rows [0, at) (wdl_sage_cache_stats)."""
+    from wdl.ops import sage_cache_stats_launch
+
+    return sage_cache_stats_launch(cache_k.view(torch.uint8), cache_ks, cache_v.view(torch.uint8), cache_vs, at)
