@@ -24,7 +24,7 @@
 // slices, which is why V's keys are reordered inside each 16-key group. The block max needs one exchange with
 // lane ^ 32. Group 1 hands (O, m, l) to group 0 through LDS at the end. When the (query tile, head) pairs number
 // between one and two times the CU count, the first T - CUs workgroups run two tiles, one per group over all the
-// key blocks, so the launch takes one round.
+// key blocks, so the launch takes one round. Tiles are dealt so that each XCD runs a contiguous range of them.
 #include "wdl_common.h"
 
 namespace {
@@ -73,7 +73,11 @@ __global__ __launch_bounds__(512) void attn_bf16_kernel(Args a) {
     const int t = threadIdx.x, lane = t % 64, half = lane / 32, tok = lane % 32;
     const int wave = __builtin_amdgcn_readfirstlane(t / 64);
     const int grp = wave / 4, sub = wave % 4;
-    const int64_t w = blockIdx.x;
+    // workgroup ids go round-robin over the 8 XCDs: each XCD takes a contiguous range of the tiles, so the query
+    // tiles of one head (consecutive tiles) read its K / V through one L2 (otherwise every XCD streams every head's
+    // K / V from the memory side)
+    const int64_t W = gridDim.x;
+    const int64_t w = W % 8 == 0 ? (blockIdx.x % 8) * (W / 8) + blockIdx.x / 8 : blockIdx.x;
     const bool dualwg = w < a.dual;
     const int64_t tile = dualwg ? 2 * w + grp : a.dual + w;
     const int64_t h = tile / a.qtiles, qt = tile % a.qtiles;
