@@ -145,6 +145,27 @@ def test_sage_ops_compile_and_capture(gpu):
                                                            128 ** -0.5, 200 + K.shape[1]), _equal)
 
 
+def test_cached_statistics_op_compiles_and_captures(gpu):
+    """wdl::sage_kv_attend_cached (KVCache.attend's op: the cached rows' column statistics beside the chunk's) under
+    torch.compile(fullgraph) and graph capture, bit-equal to its eager form and to sage_kv.attend with the same
+    statistics, and within the Sage bar of the whole-window preparation."""
+    from oracle import sage as osage
+    from wdl import sage_kv
+
+    Q, k, ks, v, vs, K, V = cache_case(H=2)
+    stats = sage_kv.cache_stats(k, ks, v, vs, 200)
+
+    def attend():
+        return torch.ops.wdl.sage_kv_attend_cached(Q, k.view(torch.uint8), ks, v.view(torch.uint8), vs, K, V, 200,
+                                                   128 ** -0.5, stats)
+
+    _compiled_and_captured(attend, _equal)
+    out = attend()
+    assert torch.equal(out, sage_kv.attend(Q, k, ks, v, vs, 200, K, V, cache_stats=stats))
+    whole = sage_kv.attend(Q, k, ks, v, vs, 200, K, V)
+    assert osage.cosine(out.cpu().float(), whole.cpu().float()) >= 0.9999
+
+
 def test_w4a4_ops_compile_and_capture(gpu):
     from wdl import w4a4
 
