@@ -24,6 +24,16 @@ using namespace wdl;
 
 constexpr int MAXCH = 8;
 
+// four consecutive table entries (16 bytes for fp32, 32 for fp64; p0 is a multiple of 4, so both are aligned)
+__device__ __forceinline__ void load4(const float* p, float (&v)[4]) {
+    const float4 r = *reinterpret_cast<const float4*>(p);
+    v[0] = r.x, v[1] = r.y, v[2] = r.z, v[3] = r.w;
+}
+__device__ __forceinline__ void load4(const double* p, double (&v)[4]) {
+    const double2 r0 = reinterpret_cast<const double2*>(p)[0], r1 = reinterpret_cast<const double2*>(p)[1];
+    v[0] = r0.x, v[1] = r0.y, v[2] = r1.x, v[3] = r1.y;
+}
+
 struct NormRopeArgs {
     const uint16_t* q;
     int64_t ldq;
@@ -40,6 +50,7 @@ struct NormRopeArgs {
     uint16_t* ko;
     int64_t ldo;
     int items;           // inputs per row: 2 (q and k) or 1 (q only)
+    int vec;             // the table is 16-byte aligned: 4 entries per vector load
 };
 
 __device__ __forceinline__ void load8(const uint16_t* p, float* f) {
@@ -90,12 +101,23 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs a) {
             xr[k] = *reinterpret_cast<const uint4*>(src + c * 8);
             if (wt) wr[k] = *reinterpret_cast<const uint4*>(wt + c * 8);
             if (rot) {
+                // the chunk's 4 pairs p0 .. p0 + 3: one vector load each of cos and sin when they share an axis
+                // (all but the two groups that straddle an axis boundary)
+                const int p0 = int((c * 8) % 128) / 2;
+                const int ax0 = p0 < tpairs ? 0 : (p0 < tpairs + spairs ? 1 : 2);
+                const int ax3 = p0 + 3 < tpairs ? 0 : (p0 + 3 < tpairs + spairs ? 1 : 2);
+                if (a.vec && ax0 == ax3) {
+                    const int pos = ax0 == 0 ? pos_t : (ax0 == 1 ? pos_h : pos_w);
+                    load4(freq + int64_t(pos) * half + p0, cs[k]);
+                    load4(freq + (a.P + pos) * half + p0, sn[k]);
+                } else {
 #pragma unroll
-                for (int p2 = 0; p2 < 4; ++p2) {
-                    const int p = int((c * 8 + 2 * p2) % 128) / 2;
-                    const int pos = p < tpairs ? pos_t : (p < tpairs + spairs ? pos_h : pos_w);
-                    cs[k][p2] = freq[int64_t(pos) * half + p];
-                    sn[k][p2] = freq[(a.P + pos) * half + p];
+                    for (int p2 = 0; p2 < 4; ++p2) {
+                        const int p = p0 + p2;
+                        const int pos = p < tpairs ? pos_t : (p < tpairs + spairs ? pos_h : pos_w);
+                        cs[k][p2] = freq[int64_t(pos) * half + p];
+                        sn[k][p2] = freq[(a.P + pos) * half + p];
+                    }
                 }
             }
         }
@@ -244,7 +266,7 @@ extern "C" int wdl_qk_norm_rope(const void* q, int64_t ldq, const void* k, int64
     NormRopeArgs a{static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(k), ldk,
                    static_cast<const uint16_t*>(wq), static_cast<const uint16_t*>(wk), freq, positions, M, C,
                    f, h, w, start_frame, eps, static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_out), ldo,
-                   items};
+                   items, reinterpret_cast<uintptr_t>(freq) % 16 == 0};
     const unsigned grid = unsigned((items * M + 1) / 2);
     if (freq_dtype == WDL_F64) qk_norm_rope_kernel<double><<<grid, 256, 0, stream>>>(a);
     else qk_norm_rope_kernel<float><<<grid, 256, 0, stream>>>(a);
