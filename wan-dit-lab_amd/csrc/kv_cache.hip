@@ -93,12 +93,16 @@ __global__ __launch_bounds__(256) void kv_append_vec_kernel(Rows k, Rows v, int6
     const float scale = fmaxf(amax, 1e-12f) / 448.0f;
     if (!live) return;
     const int64_t target = (b * capacity + at + tok) * H + h;
+    // the IEEE quotients val / scale through the reciprocal (div_rn: correctly rounded wherever |quotient| >=
+    // 2^-126; below that every value encodes to a zero of the quotient's sign, which div_rn keeps)
+    const float rs = 1.0f / scale;
     uint32_t c[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
-        c[j] = uint32_t(f32_to_e4m3(val[4 * j] / scale)) | (uint32_t(f32_to_e4m3(val[4 * j + 1] / scale)) << 8) |
-               (uint32_t(f32_to_e4m3(val[4 * j + 2] / scale)) << 16) |
-               (uint32_t(f32_to_e4m3(val[4 * j + 3] / scale)) << 24);
+        c[j] = uint32_t(f32_to_e4m3(div_rn(val[4 * j], scale, rs))) |
+               (uint32_t(f32_to_e4m3(div_rn(val[4 * j + 1], scale, rs))) << 8) |
+               (uint32_t(f32_to_e4m3(div_rn(val[4 * j + 2], scale, rs))) << 16) |
+               (uint32_t(f32_to_e4m3(div_rn(val[4 * j + 3], scale, rs))) << 24);
     *reinterpret_cast<uint2*>(r.cache + target * 128 + 8 * lane) = make_uint2(c[0], c[1]);
     if (lane == 0) r.scale[target] = scale;
 }
