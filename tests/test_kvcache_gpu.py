@@ -98,3 +98,28 @@ def test_captured_attend_follows_commits_through_the_cached_statistics(gpu):
         assert torch.equal(replayed, eager)
         whole = sage_kv.attend(Q, cache.k, cache.ks, cache.v, cache.vs, cache.saved, K, V)
         assert osage.cosine(eager.cpu().float(), whole.cpu().float()) >= 0.9999
+
+
+def test_rows_written_directly_need_invalidate_stats(gpu):
+    """Rows [0, saved) written around commit (as a caller restoring a cache would) are seen once invalidate_stats()
+    is called: the attention then equals the whole-window preparation's within the Sage bar; assigning `saved`
+    invalidates by itself."""
+    from wdl import sage_kv
+    from wdl.kvcache import KVCache
+
+    g = torch.Generator().manual_seed(5)
+    cache = KVCache(6 * T, 0, chunk=CHUNK)
+    Q, K, V = (torch.randn(1, CHUNK * T, H, 128, generator=g).to(torch.bfloat16).cuda() for _ in range(3))
+    cache.attend(Q, K, V)
+    cache.commit()
+    rows = torch.randn(1, cache.saved, H, 128, generator=g).mul(50).clamp(-448, 448).to(torch.float8_e4m3fn)
+    cache.k[:, :cache.saved] = rows.cuda()
+    cache.invalidate_stats()
+    out = cache.attend(Q, K, V)
+    whole = sage_kv.attend(Q, cache.k, cache.ks, cache.v, cache.vs, cache.saved, K, V)
+    assert osage.cosine(out.cpu().float(), whole.cpu().float()) >= 0.9999
+    cache.v[:, :cache.saved] = rows.cuda()
+    cache.saved = cache.saved  # assigning saved invalidates too
+    out = cache.attend(Q, K, V)
+    whole = sage_kv.attend(Q, cache.k, cache.ks, cache.v, cache.vs, cache.saved, K, V)
+    assert osage.cosine(out.cpu().float(), whole.cpu().float()) >= 0.9999
