@@ -49,63 +49,100 @@ def linear_bf16(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None) -> tor
     return y.to(BF)
 
 
-def patch_embed(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+def linear_f32(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None) -> torch.Tensor:
+    """An fp32 linear: the sum in fp64 of the fp32 operands, one rounding to fp32."""
+    y = x.float().double() @ w.float().double().t()
+    if b is not None:
+        y = y + b.float().double()
+    return y.float()
+
+
+def _linear(dtype):
+    return linear_bf16 if dtype == BF else linear_f32
+
+
+def patch_embed(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor, dtype=BF) -> torch.Tensor:
     """Conv3d(in_dim, dim, (1, 2, 2), (1, 2, 2)) of the latent [C, f, H, W] (model.py:13, 36), through
-    torch's conv3d in fp64 on bf16-rounded operands, rounded to bf16: tokens [f h w, dim] in (f, i, j) order."""
-    y = F.conv3d(x.to(BF).double()[None], w.to(BF).double(), b.to(BF).double(), stride=(1, 2, 2))[0]
-    return y.flatten(1).t().contiguous().to(BF)
+    torch's conv3d in fp64 on operands rounded to `dtype`, rounded to `dtype`: tokens [f h w, dim] in (f, i, j)
+    order."""
+    y = F.conv3d(x.to(dtype).double()[None], w.to(dtype).double(), b.to(dtype).double(), stride=(1, 2, 2))[0]
+    return y.flatten(1).t().contiguous().to(dtype)
 
 
-def time_embed(t: torch.Tensor, P: dict):
-    """model.py:38-41: (t_emb bf16 [dim], e0 bf16 [6, dim])."""
+def time_embed(t: torch.Tensor, P: dict, dtype=BF):
+    """model.py:38-41: (t_emb [dim], e0 [6, dim]) in `dtype` (bf16: the autocast step; fp32: the float model)."""
+    lin = _linear(dtype)
     omega = 10000 ** (-torch.arange(128, dtype=torch.float64) / 128)
     theta = t.double()[:, None] * omega[None, :]
     feats = torch.cat([torch.cos(theta), torch.sin(theta)], dim=1).float()
-    h = linear_bf16(feats, P["t1_w"], P["t1_b"])
-    t_emb = linear_bf16(F.silu(h.float()).to(BF), P["t2_w"], P["t2_b"])
-    e0 = linear_bf16(F.silu(t_emb.float()).to(BF), P["proj_w"], P["proj_b"])
+    h = lin(feats, P["t1_w"], P["t1_b"])
+    t_emb = lin(F.silu(h.float()).to(dtype), P["t2_w"], P["t2_b"])
+    e0 = lin(F.silu(t_emb.float()).to(dtype), P["proj_w"], P["proj_b"])
     return t_emb[0], e0.reshape(6, -1)
 
 
-def head(X: torch.Tensor, t_emb: torch.Tensor, P: dict, grid, eps: float = 1e-6) -> torch.Tensor:
-    """Head.forward (head.py:13-18) and unpatchify (model.py:82-84): tokens [f h w, dim] -> bf16 [out, f, 2h, 2w]."""
+def head(X: torch.Tensor, t_emb: torch.Tensor, P: dict, grid, eps: float = 1e-6, dtype=BF) -> torch.Tensor:
+    """Head.forward (head.py:13-18) and unpatchify (model.py:82-84): tokens [f h w, dim] -> [out, f, 2h, 2w] in
+    `dtype`."""
     dim = X.shape[1]
     shift, scale = P["head_mod"].float().reshape(2, dim) + t_emb.float()[None, :]
     y = F.layer_norm(X.float(), (dim,), eps=eps) * (1 + scale) + shift
-    o = linear_bf16(y, P["head_w"], P["head_b"])
+    o = _linear(dtype)(y, P["head_w"], P["head_b"])
     out_dim = P["head_w"].shape[0] // 4
     f, h, w = grid
     return o.view(f, h, w, 1, 2, 2, out_dim).permute(6, 0, 3, 1, 4, 2, 5).reshape(out_dim, f, 2 * h, 2 * w)
+
+
+def _model(x: torch.Tensor, t: torch.Tensor, E: dict, blocks, dtype) -> torch.Tensor:
+    """WanModel.forward (model.py:32-84) on one chunk: patch embedding, time embedding, blocks(X, e0, grid), head
+    and unpatchify."""
+    _, f, H, W = x.shape
+    grid = (f, H // 2, W // 2)
+    X = patch_embed(x, E["patch_w"], E["patch_b"], dtype)
+    t_emb, e0 = time_embed(t, E, dtype)
+    return head(blocks(X, e0, grid), t_emb, E, grid, dtype=dtype)
 
 
 def model_forward(x: torch.Tensor, t: torch.Tensor, E: dict, blocks: list, caches: list, ctx_kvs: list, freq,
                   start_frame: int, heads: int) -> torch.Tensor:
     """WanModel.forward on one chunk (model.py:32-84) with oracle blocks: latent [C, f, H, W] -> flow bf16. Each
     block's cache dict (k, ks, v, vs, at) receives the chunk's keys and values at `at`."""
-    _, f, H, W = x.shape
-    grid = (f, H // 2, W // 2)
-    X = patch_embed(x, E["patch_w"], E["patch_b"])
-    t_emb, e0 = time_embed(t, E)
-    for P, cache, kv in zip(blocks, caches, ctx_kvs):
-        X = oblock.block_forward(X, e0.float(), P, grid, freq, start_frame, cache, kv, heads)
-    return head(X, t_emb, E, grid)
+    def run(X, e0, grid):
+        for P, cache, kv in zip(blocks, caches, ctx_kvs):
+            X = oblock.block_forward(X, e0.float(), P, grid, freq, start_frame, cache, kv, heads)
+        return X
+
+    return _model(x, t, E, run, BF)
+
+
+def float_model_forward(x: torch.Tensor, t: torch.Tensor, E: dict, blocks: list, cache_kvs: list, ctxs: list, freq,
+                        start_frame: int, heads: int) -> torch.Tensor:
+    """The same model in fp32 with unquantized blocks (oracle.block.float_block_forward): latent -> flow fp32;
+    cache_kvs[i] = (K, V) fp32 [Lc, D] the cached keys / values of block i, ctxs[i] its context fp32."""
+    def run(X, e0, grid):
+        for B, ckv, ctx in zip(blocks, cache_kvs, ctxs):
+            X = oblock.float_block_forward(X, e0, B, grid, freq, start_frame, ckv, ctx, heads)
+        return X
+
+    return _model(x, t, E, run, torch.float32)
 
 
 def next_chunk(noise: torch.Tensor, fresh: list, E: dict, blocks: list, caches: list, ctx_kvs: list, freq,
-               start_frame: int, heads: int, levels=None) -> torch.Tensor:
+               start_frame: int, heads: int, levels=None, flow=None) -> torch.Tensor:
     """Stream.next_chunk's DMD loop (causal.py:680-740): x0 of one chunk from `noise`, renoising with the given
     `fresh` noises (one per level after the first), then the write pass at t = 0; the caches' write offsets `at`
-    advance by the chunk's tokens (the commit of a cache that is not full)."""
+    advance by the chunk's tokens (the commit of a cache that is not full). flow(x, t) replaces the oracle model
+    (a model with a known exact flow, in the tests)."""
     levels = sigmas() if levels is None else levels
+    run = flow if flow is not None else (
+        lambda x, t: model_forward(x, t, E, blocks, caches, ctx_kvs, freq, start_frame, heads))
     x = noise.float()
     x0 = x
     for i, sigma in enumerate(levels):
-        flow = model_forward(x, torch.full((1,), 1000 * sigma), E, blocks, caches, ctx_kvs, freq, start_frame,
-                             heads).float()
-        x0 = x - sigma * flow
+        x0 = x - sigma * run(x, torch.full((1,), 1000 * sigma)).float()  # flow = noise - x0 (causal.py:716)
         if i + 1 < len(levels):
             x = (1 - levels[i + 1]) * x0 + levels[i + 1] * fresh[i]
-    model_forward(x0, torch.zeros(1), E, blocks, caches, ctx_kvs, freq, start_frame, heads)
+    run(x0, torch.zeros(1))
     n = x0.shape[1] * (x0.shape[2] // 2) * (x0.shape[3] // 2)
     for cache in caches:
         cache["at"] += n

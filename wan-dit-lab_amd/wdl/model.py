@@ -29,6 +29,8 @@ from each call's latent size.
 
 from __future__ import annotations
 
+from collections import deque
+
 import torch
 import torch.nn.functional as F
 
@@ -71,15 +73,34 @@ def resample_latents(x: torch.Tensor, height: int, width: int) -> torch.Tensor:
     return y.permute(1, 0, 2, 3).contiguous()
 
 
-def window_chunks(kept: list, chunk: int, window_frames: int, sink_frames: int) -> list:
-    """The chunks a cache of `window_frames` frames (the first `sink_frames` never evicted) holds after the chunks
-    of `kept` [(first frame, latents)] were committed in order: the sink's chunks and the newest that fit."""
-    if sink_frames % chunk or (window_frames - sink_frames) % chunk:
-        raise ValueError("the window and its sink must hold whole chunks")
-    nsink, nring = sink_frames // chunk, (window_frames - sink_frames) // chunk
-    if len(kept) <= nsink + nring:
-        return list(kept)
-    return kept[:nsink] + (kept[len(kept) - nring:] if nring else [])
+class FrameHistory:
+    """The clean latent frames the caches hold, as Stream.next_chunk keeps them (sink_latents / recent_latents,
+    causal.py:535-536, 744-746): the first `sink` frames of the video stay; of the others the newest `ring` follow.
+    Frames are (frame number, latents [C, H, W])."""
+
+    def __init__(self, sink: int, ring: int):
+        self.sink_frames, self.sink, self.recent = sink, [], deque(maxlen=max(ring, 0))
+
+    def add(self, first_frame: int, x0: torch.Tensor):
+        """The frames of a chunk x0 [C, f, H, W] starting at frame `first_frame`."""
+        for f in range(x0.shape[1]):
+            n = first_frame + f
+            (self.sink if n < self.sink_frames else self.recent).append((n, x0[:, f]))
+
+    def chunks(self, chunk: int) -> list:
+        """[(first frame, latents [C, chunk, H, W])] of the kept frames, oldest first; ValueError unless they are
+        whole chunks of consecutive frames (the reference's recache asserts the same, causal.py:672)."""
+        frames = self.sink + list(self.recent)
+        if len(frames) % chunk:
+            raise ValueError(f"{len(frames)} kept frames are not whole chunks of {chunk}")
+        out = []
+        for g in range(0, len(frames), chunk):
+            group = frames[g:g + chunk]
+            first = group[0][0]
+            if [n for n, _ in group] != list(range(first, first + chunk)):
+                raise ValueError("the kept frames do not form whole chunks of consecutive frames")
+            out.append((first, torch.stack([x for _, x in group], dim=1)))
+        return out
 
 
 def unpatchify(y: torch.Tensor, grid, out_dim: int) -> torch.Tensor:
@@ -173,7 +194,7 @@ class ChunkStream:
         self.model, self.shape, self.generator = model, tuple(shape), generator
         self.levels = sigmas(shift) if levels is None else list(levels)
         self.write_pass, self.start, self.sampler = write_pass, 0, sampler
-        self.kept = []  # (first frame, clean latents) of the chunks the caches hold, oldest first
+        self.history = None  # FrameHistory of the clean frames the caches hold (made at the first chunk)
         if sampler == "unipc":
             timesteps, C = unipc.plan(steps or len(STEPS), shift)
             self.timesteps, self.plan = timesteps, C.tolist()
@@ -207,9 +228,25 @@ class ChunkStream:
         per_frame = (self.shape[2] // 2) * (self.shape[3] // 2)
         return c.max_tokens // per_frame, c.sink_tokens // per_frame
 
-    def _keep(self, first_frame: int, x0: torch.Tensor):
+    def _window_split(self):
         frames, sink = self._window()
-        self.kept = window_chunks(self.kept + [(first_frame, x0)], self.shape[1], frames, sink)
+        return sink, frames - sink
+
+    def _keep(self, first_frame: int, x0: torch.Tensor):
+        if self.history is None:
+            self.history = FrameHistory(*self._window_split())
+        self.history.add(first_frame, x0)
+
+    @property
+    def kept(self) -> list:
+        """(first frame, clean latents [C, chunk, H, W]) of the chunks the caches hold, oldest first."""
+        return [] if self.history is None else self.history.chunks(self.shape[1])
+
+    @kept.setter
+    def kept(self, chunks):
+        self.history = FrameHistory(*self._window_split())
+        for first, x0 in chunks:
+            self.history.add(first, x0)
 
     @torch.no_grad()
     def switch_resolution(self, height: int, width: int):
@@ -222,12 +259,15 @@ class ChunkStream:
             raise ValueError(f"latent height and width must be positive and even, got {height} x {width}")
         frames, sink = self._window()
         chunk = self.shape[1]
-        window_chunks([], chunk, frames, sink)  # the window holds whole chunks
+        if sink % chunk or (frames - sink) % chunk:
+            raise ValueError("the resolution switch re-encodes whole chunks: the window and its sink must hold "
+                             f"whole chunks of {chunk} frames (window {frames}, sink {sink})")
+        kept = self.kept  # raises before anything changes if the kept frames are not whole chunks
         per_frame = (height // 2) * (width // 2)
         self.model.caches[:] = [KVCache(frames * per_frame, sink * per_frame, chunk=chunk,
                                         entropy_ratio=c.entropy_ratio) for c in self.model.caches]
         self.shape = (self.shape[0], chunk, height, width)
-        kept, self.kept = self.kept, []
+        self.history = FrameHistory(*self._window_split())
         dev = self.model.freq.device
         for first, x0 in kept:
             x = resample_latents(x0, height, width)
