@@ -249,6 +249,15 @@ int wdl_sage_prep_cached(const void* cache_k, const float* cache_ks, const void*
                          int64_t at, int64_t n, const float* cache_stats, int splits, float* workspace, void* k_int8,
                          float* k_scale, void* v_fp8, float* k_mean_out, float* v_scale_out, wdl_stream_t stream);
 
+/* The operands live::sage_sm89 receives from the reference's sage_kv._attend (kernels/sage_kv.py:141-176; schema
+ * native/ops/sage_ops.cpp:12-19, 28-31) in wdl_sage_attn's layouts: k_i8 int8 [L, heads, 128] (row stride ldk
+ * bytes) -> k_out int8 [heads, Lpad, 128], tokens L..Lpad-1 zero; v_fp8 e4m3 [128, heads, Lpad] (element strides
+ * v_stride_d, v_stride_h, tokens contiguous) in Sage's 16-token order (sage_kv.py:101-103) -> v_out [heads, 128,
+ * Lpad] in wdl's 64-token order. Lpad = 64 ceil(L / 64). q_scale, k_scale and v_scale already have wdl's layouts.
+ * Pointers and strides 16-byte aligned. */
+int wdl_sage_sm89_relayout(const void* k_i8, int64_t ldk, const void* v_fp8, int64_t v_stride_d, int64_t v_stride_h,
+                           int64_t L, int64_t heads, void* k_out, void* v_out, wdl_stream_t stream);
+
 /* Workspace (bytes) of wdl_sage_attn for n queries, L keys and `heads` heads. */
 int64_t wdl_sage_attn_workspace_bytes(int64_t n, int64_t L, int64_t heads);
 

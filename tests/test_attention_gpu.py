@@ -319,13 +319,17 @@ def test_rope_apply_bit_exact_with_padding_and_batch(gpu, table):
 def test_fused_qkv_attention_module_matches_oracle(gpu, cached):
     """FusedQKVAttention (w4a4.py:246-262) on the HIP path, dim 256, 2 heads, grid (2, 4, 6), with and without an
     FP8 cache of 96 prior tokens:
-    - wiring: bit-equal to the forward of the reference written out with the same wdl ops;
-    - the attention stage, fed the oracle's own Q, K, V: cosine >= 0.99999 and relative L2 <= 2e-3 against the
-      oracle's blockwise attention (the config-1 stage bar);
+    - wiring: bit-equal to the forward of the reference written out with the same wdl ops (with a cache, the
+      KVCache's Sage attention, causal.py:193-210; without, the bf16 attention of the chunk over itself, the
+      reference's scaled_dot_product_attention branch, w4a4.py:259-261);
+    - the attention stage, fed the oracle's own Q, K, V: with a cache, cosine >= 0.99999 and relative L2 <= 2e-3
+      against the oracle's blockwise Sage attention (the config-1 stage bar); without, relative L2 <= 2 * 2^-9 and
+      cosine >= 0.99999 against the exact softmax on the bf16 operands (P's bf16 rounding, the bf16 attention's
+      bar);
     - end to end against the oracle composition: relative L2 <= 2e-2 (the W4A4 o projection re-quantizes the
       attention output to int4, so its ~1e-3 differences flip codes: measured ~7e-3)."""
     from oracle import block as oblock
-    from wdl import rope, sage_kv, w4a4
+    from wdl import ops, rope, w4a4
     from wdl.kvcache import KVCache
 
     g = torch.Generator().manual_seed(5)
@@ -361,9 +365,7 @@ def test_fused_qkv_attention_module_matches_oracle(gpu, cached):
     if c is not None:
         Aw = c.attend(Qw.view(shape), Kw.view(shape), v[0].reshape(shape))
     else:
-        z8 = torch.zeros(1, 1, H, 128, device=dev, dtype=torch.float8_e4m3fn)
-        one = torch.ones(1, 1, H, 1, device=dev)
-        Aw = sage_kv.attend(Qw.view(shape), z8, one, z8, one, 0, Kw.view(shape), v[0].reshape(shape))
+        Aw = ops.attn_bf16_launch(Qw, ops.attn_bf16_prep_launch(Kw, v[0]), 128 ** -0.5)
     assert torch.equal(got, m.o(Aw.reshape(1, M, dim)))
     # the oracle
     qkv = oblock._lin(X[0], P["qkv"]).to(torch.bfloat16)
@@ -378,12 +380,11 @@ def test_fused_qkv_attention_module_matches_oracle(gpu, cached):
     if c is not None:
         Ag = c.attend(Qd, Kd, Vd)
     else:
-        z8 = torch.zeros(1, 1, H, 128, device=dev, dtype=torch.float8_e4m3fn)
-        one = torch.ones(1, 1, H, 1, device=dev)
-        Ag = sage_kv.attend(Qd, z8, one, z8, one, 0, Kd, Vd)
+        Ag = ops.attn_bf16_launch(Qd.reshape(M, dim), ops.attn_bf16_prep_launch(Kd.reshape(M, dim),
+                                                                                Vd.reshape(M, dim)), 128 ** -0.5)
     Ag = Ag.cpu().reshape(M, dim)
     rel = lambda a, b: float((a.float() - b.float()).norm() / b.float().norm())
-    assert rel(Ag, A) <= 2e-3 and osage.cosine(Ag, A) >= 0.99999
+    assert rel(Ag, A) <= (2e-3 if cached else 2 * 2 ** -9) and osage.cosine(Ag, A) >= 0.99999
     want = oblock._lin(A, P["o"]).to(torch.bfloat16)
     e2e = rel(got.cpu().reshape(M, dim), want)
     print(f"cached={cached}: attention stage rel {rel(Ag, A):.2e}, end to end rel-L2 {e2e:.2e}")

@@ -22,13 +22,13 @@ pytestmark = pytest.mark.gpu
 BF = torch.bfloat16
 
 
-def run_pair(dim, heads, ffn, grid, start, prior, Lc, seed, svd=False, scale_dtype=None):
+def run_pair(dim, heads, ffn, grid, start, prior, Lc, seed, svd=False, scale_dtype=None, weight_scale=0.02):
     from wdl.block import LINEARS, build_block
     from wdl.kvcache import KVCache
 
     g = torch.Generator().manual_seed(seed)
     P = (oblock.quantize_block(oblock.random_block(dim, ffn, g)) if svd
-         else oblock.random_logical_block(dim, ffn, g))
+         else oblock.random_logical_block(dim, ffn, g, scale=weight_scale))
     if scale_dtype is not None:  # both sides take the weight scales in this type
         for name in LINEARS:
             P[name]["wscales"] = P[name]["wscales"].to(scale_dtype)

@@ -79,6 +79,55 @@ def test_sage_attn_operator_is_the_kernel_of_sage_kv_attend(gpu):
     assert torch.equal(sm, out)
 
 
+@pytest.mark.parametrize("at,n,H", [(200, 150, 2), (128, 37, 3), (0, 64, 1)])
+def test_sage_sm89_takes_the_reference_operands(gpu, at, n, H):
+    """live::sage_sm89 on the operands the reference's sage_kv._attend hands it (kernels/sage_kv.py:141-176): int8 K
+    [1, L, H, 128], k_scale [1, H, 4 ceil(L/64)], fp8 V [1, 128, H, Lpad] in Sage's 16-token order, q int8 [1, n, H,
+    128] with q_scale [1, H, 32 ceil(n/128)], v_scale [1, H, 128], built by the oracle's restatement of those
+    quantizers and layouts (sage_v_layout). The device relayout gives exactly wdl's layouts of the same operands
+    (k [H, Lpad, 128], wdl_v_layout), the result is bit-equal to wdl::sage_attn on them, meets the Sage bars
+    (cosine >= 0.999 against the exact-P emulation, error against exact attention within 1.2x + 1e-3 of the fp8-P
+    emulation), and is bit-equal to eager under torch.compile and HIP-graph capture. L = 350 and 165 end in a
+    partial 64-key block."""
+    import wdl.live  # noqa: F401
+    from oracle import sage as osage
+    from wdl import ops
+
+    Q, k, ks, v, vs, K, V = cache_case(H=H, n=n, seed=at + n)
+    Qc, Kc, Vc = Q.cpu(), K.cpu(), V.cpu()
+    p = osage.prep(Qc, k.cpu(), ks.cpu(), v.cpu(), vs.cpu(), at, Kc, Vc)
+    L = at + n
+    Lpad = (L + 63) // 64 * 64
+    ref_ops = [t.cuda() for t in (p["q"], p["k"], osage.sage_v_layout(p["v"]), p["q_scale"], p["k_scale"],
+                                  p["v_scale"])]
+    assert ref_ops[1].shape == (1, L, H, 128) and ref_ops[2].shape == (1, 128, H, Lpad)
+    # the relayout alone: wdl's layouts of the same operands
+    kw = torch.empty(H, Lpad, 128, device="cuda", dtype=torch.int8)
+    vw = torch.empty(H, 128, Lpad, device="cuda", dtype=torch.uint8)
+    from wdl import _lib
+    _lib.call("wdl_sage_sm89_relayout", ref_ops[1].data_ptr(), ref_ops[1].stride(1), ref_ops[2].data_ptr(),
+              ref_ops[2].stride(1), ref_ops[2].stride(2), L, H, kw.data_ptr(), vw.data_ptr(),
+              torch.cuda.current_stream().cuda_stream)
+    want_k = torch.zeros(H, Lpad, 128, dtype=torch.int8)
+    want_k[:, :L] = p["k"][0].permute(1, 0, 2)
+    assert torch.equal(kw.cpu(), want_k)
+    assert torch.equal(vw.cpu(), osage.wdl_v_layout(p["v"])[0].view(torch.uint8))
+    sm = 128 ** -0.5
+    out = torch.ops.live.sage_sm89(*ref_ops, sm)
+    direct = torch.ops.wdl.sage_attn(ref_ops[0], kw, vw, ref_ops[3], ref_ops[4][0], ref_ops[5][0], sm, L)
+    assert torch.equal(out, direct)
+    emul = osage.attention_quantized(p, sm)
+    emul8 = osage.attention_quantized(p, sm, p_fp8=True)
+    exact = osage.attention_exact(Qc, p["K"], p["V"], sm)
+    cos, err = osage.cosine(out.cpu(), emul), osage.rel_err(out.cpu(), exact)
+    print(f"sage_sm89 reference operands at={at} n={n} H={H}: cos {cos:.6f}, err {err:.4f} "
+          f"(fp8-P emulation {osage.rel_err(emul8, exact):.4f})")
+    assert cos >= 0.999 and err < 1.2 * osage.rel_err(emul8, exact) + 1e-3
+    _compiled_and_captured(lambda: torch.ops.live.sage_sm89(*ref_ops, sm), _equal)
+    with pytest.raises(ValueError):  # V not padded to whole 64-key blocks
+        torch.ops.live.sage_sm89(ref_ops[0], ref_ops[1], ref_ops[2][..., :Lpad - 16].contiguous(), *ref_ops[3:], sm)
+
+
 def _compiled_and_captured(fn, check):
     """fn() eager, compiled (fullgraph) and replayed from a captured graph: `check` compares each to the eager
     result."""

@@ -31,3 +31,27 @@ def test_sage_attend_rejects_strided_or_misshaped_caches():
         _check(Q, ck, torch.ones(1, 64, 2, 2)[..., :1], cv, cvs, 8, K, V)
     with pytest.raises(ValueError, match="at outside"):
         _check(Q, ck, cks, cv, cvs, 65, K, V)
+
+
+def test_weight_only_gemm_refuses_views_and_mismatched_parts():
+    """fp8.weight_only_gemm reads the weight as dense [N, K] rows: a transposed or sliced e4m3 weight, a bias or
+    gate of the wrong length, a misshaped out and tensors on different devices are refused before any launch."""
+    from wdl.fp8 import weight_only_gemm
+
+    M, N, K = 16, 128, 64
+    x = torch.zeros(M, K, dtype=torch.bfloat16)
+    w = torch.zeros(N, K, dtype=FP8)
+    s = torch.ones(N)
+    b = torch.zeros(N, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="contiguous e4m3"):
+        weight_only_gemm(x, torch.zeros(K, N, dtype=FP8).t(), s, b)
+    with pytest.raises(ValueError, match="contiguous e4m3"):
+        weight_only_gemm(x, torch.zeros(N, 2 * K, dtype=FP8)[:, :K], s, b)
+    with pytest.raises(ValueError, match="bias"):
+        weight_only_gemm(x, w, s, torch.zeros(N - 1, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="out must be"):
+        weight_only_gemm(x, w, s, b, out=torch.zeros(M, N + 1, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="gate"):
+        weight_only_gemm(x, w, s, b, out=torch.zeros(M, N, dtype=torch.bfloat16), gate=torch.ones(N - 1))
+    with pytest.raises(ValueError, match="device"):
+        weight_only_gemm(x, w, s.to("meta"), b)

@@ -50,3 +50,19 @@ def test_commit_copies_rows_into_evicted_slots():
     # window of 4 frames: chunks 3..6 survive (values 3, 4, 5, 6 at some rows)
     kept = sorted(set(cache.k[0, :8, 0, 0].float().tolist()))
     assert kept == [3.0, 4.0, 5.0, 6.0]
+
+
+def test_a_pinned_chunk_larger_than_the_free_ring_is_evicted_last():
+    """A ring of 6 slots (3 frames of 2 tokens) whose two oldest frames are a pinned shot chunk: a 4-token commit
+    takes the one unpinned frame and then the oldest pinned slots (the reference ranks pinned tokens after all
+    others, causal.py:329-337) instead of failing."""
+    from wdl.kvcache import _FrameQueue
+
+    q = _FrameQueue()
+    q.append(0, 2, [0, 1, 2, 3], [0, 1, 2, 3])      # frames 0, 1 in slots 0..3
+    q.append(2, 2, [0, 1], [4, 5])                  # frame 2 in slots 4, 5
+    q.pinned = frozenset([0, 1, 2, 3])              # the shot's first chunk
+    assert q.take_oldest(4) == [4, 5, 0, 1]         # the unpinned frame first, then the oldest pinned
+    assert q.frames == [[1, [2, 3]]]
+    q.append(3, 2, [0, 1, 2, 3], [4, 5, 0, 1])
+    assert q.take_oldest(2) == [4, 5]               # slot 0 and 1 stay pinned with their new tokens

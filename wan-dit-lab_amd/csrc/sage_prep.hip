@@ -303,6 +303,63 @@ __global__ __launch_bounds__(256) void quant_kv_kernel(Src k, Src v, int64_t H, 
     }
 }
 
+// ---------------------------------------------------------------- the reference's Sage operand layouts
+// live::sage_sm89 (native/ops/sage_ops.cpp:12-19) takes the operands kernels/sage_kv.py:141-176 builds: int8 K
+// [L, H, 128] (token-major, heads interleaved) and fp8 V [128, H, Lpad] whose 16-token groups are stored in Sage's
+// order (token j of a group at 4 (p % 4) + 2 (p / 4) + j % 2, p = j / 2; sage_kv.py:101-103). The scales have
+// wdl's layouts already (q_scale [H, blocks * 8], k_scale [H, Lpad / 64 * 4], v_scale [H, 128]).
+
+// K: one thread per 16 bytes of the output [H, Lpad, 128]; tokens L .. Lpad - 1 zero.
+__global__ __launch_bounds__(256) void sm89_k_kernel(const int8_t* __restrict__ k, int64_t ldk, int64_t H,
+                                                    int64_t L, int64_t Lpad, int8_t* __restrict__ out) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;  // 16-byte chunk of the output
+    if (i >= H * Lpad * 8) return;
+    const int64_t c = i % 8, t = (i / 8) % Lpad, h = i / (8 * Lpad);
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (t < L) v = *reinterpret_cast<const uint4*>(k + t * ldk + h * D + c * 16);
+    *reinterpret_cast<uint4*>(out + (h * Lpad + t) * D + c * 16) = v;
+}
+
+// position of token j (0..15) of a 16-token group in Sage's order
+__device__ __forceinline__ int sage16_pos(int j) {
+    const int p = j / 2;
+    return (p % 4) * 4 + (p / 4) * 2 + j % 2;
+}
+
+// V: one thread per (head, channel, 64-token block): the block's 64 bytes in Sage's order in, wdl's order out
+// (output position 32 a + 4 b + c holds token 8 b + 4 a + c).
+__global__ __launch_bounds__(256) void sm89_v_kernel(const uint8_t* __restrict__ v, int64_t sd, int64_t sh,
+                                                    int64_t H, int64_t Lpad, uint8_t* __restrict__ out) {
+    const int64_t nb = Lpad / 64;
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= H * D * nb) return;
+    const int64_t blk = i % nb, d = (i / nb) % D, h = i / (nb * D);
+    const uint8_t* src = v + d * sd + h * sh + blk * 64;
+    uint32_t in[16];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint4 w = *reinterpret_cast<const uint4*>(src + 16 * c);
+        in[4 * c] = w.x, in[4 * c + 1] = w.y, in[4 * c + 2] = w.z, in[4 * c + 3] = w.w;
+    }
+    uint32_t o[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int pos = 4 * q + b;                                     // output position in the block
+            const int t = 8 * ((pos % 32) / 4) + 4 * (pos / 32) + pos % 4;  // its token
+            const int s = (t & ~15) + sage16_pos(t & 15);                   // where Sage's order keeps it
+            word |= ((in[s / 4] >> (8 * (s % 4))) & 0xffu) << (8 * b);
+        }
+        o[q] = word;
+    }
+    uint8_t* dst = out + (h * D + d) * Lpad + blk * 64;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        *reinterpret_cast<uint4*>(dst + 16 * c) = make_uint4(o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]);
+}
+
 }  // namespace
 
 // workspace floats: 2 * S * H * 128 (partials) + 2 * H * 128 (k_mean, v_scale)
@@ -402,4 +459,25 @@ extern "C" int wdl_sage_prep_cached(const void* cache_k, const float* cache_ks, 
     return sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, capacity, heads, nullptr, nullptr, k, ldk, v, ldv,
                             heads, at, n, splits, workspace, k_int8, k_scale, v_fp8, k_mean_out, v_scale_out, stream,
                             cache_stats);
+}
+
+extern "C" int wdl_sage_sm89_relayout(const void* k_i8, int64_t ldk, const void* v_fp8, int64_t v_stride_d,
+                                      int64_t v_stride_h, int64_t L, int64_t heads, void* k_out, void* v_out,
+                                      hipStream_t stream) {
+    if (L <= 0 || heads <= 0 || ldk < heads * D || v_stride_h < (L + 63) / 64 * 64 || v_stride_d < heads * v_stride_h)
+        return fail(WDL_EINVAL, "sage_sm89_relayout: bad shape");
+    if (!k_i8 || !v_fp8 || !k_out || !v_out) return fail(WDL_EINVAL, "sage_sm89_relayout: null pointer");
+    if ((reinterpret_cast<uintptr_t>(k_i8) | reinterpret_cast<uintptr_t>(v_fp8) | reinterpret_cast<uintptr_t>(k_out) |
+         reinterpret_cast<uintptr_t>(v_out) | ldk | v_stride_d | v_stride_h) % 16)
+        return fail(WDL_EINVAL, "sage_sm89_relayout: buffers and strides must be 16-byte aligned");
+    const int64_t Lpad = (L + 63) / 64 * 64;
+    const int64_t nk = heads * Lpad * 8, nv = heads * D * (Lpad / 64);
+    sm89_k_kernel<<<unsigned((nk + 255) / 256), 256, 0, stream>>>(static_cast<const int8_t*>(k_i8), ldk, heads, L,
+                                                                  Lpad, static_cast<int8_t*>(k_out));
+    const int rc = check_launch("sage_sm89_relayout k");
+    if (rc) return rc;
+    sm89_v_kernel<<<unsigned((nv + 255) / 256), 256, 0, stream>>>(static_cast<const uint8_t*>(v_fp8), v_stride_d,
+                                                                  v_stride_h, heads, Lpad,
+                                                                  static_cast<uint8_t*>(v_out));
+    return check_launch("sage_sm89_relayout v");
 }

@@ -33,10 +33,11 @@ LINEARS = ("qkv", "o", "cq", "ck", "cv", "co", "ffn1", "ffn2")
 
 class QuantizedWanBlock:
     """parts: {linear: packed W4A4 parts (w4a4.quantize / pack_parts)} for LINEARS, plus wq, wk, cwq, cwk (bf16
-    RMSNorm weights [dim]), n3w, n3b (fp32 LayerNorm-3 affine [dim]) and modulation (fp32 [6, dim]). The block owns
-    `parts`: each linear's packed nibbles ([N, K/2], 0.5 B per weight) are replaced by the GEMM's tile-blocked fp6
-    codes (0.75 B per weight), so the weights are held once (3.7 GB of fp6 codes for the 30 blocks of Wan 5B
-    instead of that plus 2.45 GB of nibbles); keep_packed keeps both."""
+    RMSNorm weights [dim]), n3w, n3b (fp32 LayerNorm-3 affine [dim]) and modulation (fp32 [6, dim]). The caller's
+    dicts are not changed: the block keeps shallow copies in which each linear's packed nibbles ([N, K/2], 0.5 B
+    per weight) are replaced by the GEMM's tile-blocked fp6 codes (0.75 B per weight), so once the caller drops
+    its parts the weights are held once (3.7 GB of fp6 codes for the 30 blocks of Wan 5B instead of that plus
+    2.45 GB of nibbles); keep_packed keeps both."""
 
     def __init__(self, parts: dict, dim: int, heads: int, eps: float = 1e-6, cross_attention: str = "sdpa",
                  keep_packed: bool = False):
@@ -45,6 +46,7 @@ class QuantizedWanBlock:
         the context too (an opt-in deviation: faster on long prompts, within Sage's error bars)."""
         if cross_attention not in ("sdpa", "sage"):
             raise ValueError(f"cross_attention must be 'sdpa' or 'sage', got {cross_attention!r}")
+        parts = {name: dict(t) if name in LINEARS else t for name, t in parts.items()}
         self.p, self.dim, self.heads, self.eps = parts, dim, heads, eps
         self.cross_attention = cross_attention
         dev = parts["ffn1"]["qweight"].device

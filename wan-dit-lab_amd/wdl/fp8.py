@@ -86,12 +86,24 @@ def weight_only_gemm(x: torch.Tensor, w_codes: torch.Tensor, w_scale: torch.Tens
     if x.dtype != torch.bfloat16 or x.stride(1) != 1 or w_codes.shape[1] != K or N % 128 or K % 64:
         raise ValueError(f"weight-only FP8 GEMM: bf16 x [M, K] and an [N, K] weight, N % 128 == 0, K % 64 == 0; "
                          f"got {tuple(x.shape)} and {tuple(w_codes.shape)}")
-    if w_scale.dtype != torch.float32 or w_scale.numel() not in (1, N):
-        raise ValueError("w_scale: fp32 [N] or [1]")
+    # the kernel reads the weight as dense rows of K codes: a transposed or sliced view would be read wrongly
+    if w_codes.element_size() != 1 or not w_codes.is_contiguous():
+        raise ValueError("weight-only FP8 GEMM: the weight must be a contiguous e4m3 [N, K] tensor")
+    if w_scale.dtype != torch.float32 or w_scale.numel() not in (1, N) or not w_scale.is_contiguous():
+        raise ValueError("w_scale: contiguous fp32 [N] or [1]")
+    if bias is not None and bias.numel() != N:
+        raise ValueError(f"bias: {N} values, got {bias.numel()}")
+    tensors = [t for t in (x, w_codes, w_scale, bias, out, gate) if t is not None]
+    if any(t.device != x.device for t in tensors):
+        raise ValueError("weight-only FP8 GEMM: every tensor must be on x's device")
     b = None if bias is None else bias.to(torch.bfloat16).contiguous()
+    if out is not None and (out.shape != (M, N) or out.dtype != torch.bfloat16 or out.stride(1) != 1):
+        raise ValueError(f"out must be bf16 [{M}, {N}] with unit column stride")
     if gate is not None:
-        if out is None or out.shape != (M, N) or out.dtype != torch.bfloat16 or out.stride(1) != 1:
+        if out is None:
             raise ValueError("the gated residual needs out bf16 [M, N]")
+        if gate.numel() != N:
+            raise ValueError(f"gate: {N} values, got {gate.numel()}")
         gate = gate.float().contiguous()
     elif out is None:
         out = torch.empty(M, N, device=x.device, dtype=torch.bfloat16)

@@ -60,12 +60,24 @@ class _FrameQueue:
             self.frames[-1][1].append(s)
 
     def take_oldest(self, n: int) -> list[int]:
-        """Removes and returns the n oldest unpinned slots (in token order of the video)."""
+        """Removes and returns the n oldest unpinned slots (in token order of the video). When fewer than n are
+        unpinned, the oldest pinned slots follow: the reference ranks pinned tokens after every other one
+        (causal.py:329-337, the pinned order masked to the largest value) and leaves the order among them to
+        torch.topk; here it is the video's. A slot stays pinned when a new token takes it, as the reference's
+        per-slot mask does."""
+        out = self._take(n, lambda s: s not in self.pinned)
+        if len(out) < n:
+            out += self._take(n - len(out), lambda s: True)
+        if len(out) < n:
+            raise RuntimeError(f"the ring has {len(out)} tokens, the chunk needs {n}")
+        return out
+
+    def _take(self, n: int, eligible) -> list[int]:
         out: list[int] = []
         for entry in self.frames:
             keep = []
             for s in entry[1]:
-                if len(out) < n and s not in self.pinned:
+                if len(out) < n and eligible(s):
                     out.append(s)
                 else:
                     keep.append(s)
@@ -73,8 +85,6 @@ class _FrameQueue:
             if len(out) == n:
                 break
         self.frames = [e for e in self.frames if e[1]]
-        if len(out) < n:
-            raise RuntimeError(f"the ring has {len(out)} evictable tokens, the chunk needs {n}")
         return out
 
 

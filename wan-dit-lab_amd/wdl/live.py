@@ -6,10 +6,11 @@ The reference registers `live::w4a4_linear` and `live::w4a4_gelu_mlp` from Nunch
 names and schemas over wdl's HIP kernels, so those call sites run unchanged on MI355X, given weights packed
 by wdl.w4a4.quantize (wdl's layout; Nunchaku's tile order is not reproduced).
 
-`live::sage_sm89` takes the reference's argument list over wdl's operand layouts (wdl.sage_kv.quant_q / prep, the
-keys and values as [H, L, 128] / [H, 128, L] views of the padded buffers); SageAttention's own sm89 layouts are not
-reproduced. The usual attention swap point is one level up, `sage_kv.attend` / `KVCache.attend`
-(kernels/sage_kv.py:127-134; generation/causal.py:193-220), replaced by wdl.sage_kv.attend / wdl.kvcache.KVCache.
+`live::sage_sm89` takes the reference's argument list over the operands the reference's sage_kv._attend builds
+(kernels/sage_kv.py:141-176: int8 K [1, L, H, 128], fp8 V [1, 128, H, Lpad] in Sage's 16-token order, the scales),
+copied into wdl's layouts on the device, or over wdl's own layouts (wdl.sage_kv.quant_q / prep). The faster swap
+point is one level up, `sage_kv.attend` / `KVCache.attend` (kernels/sage_kv.py:127-134; generation/causal.py:193-220),
+replaced by wdl.sage_kv.attend / wdl.kvcache.KVCache, whose preparation writes wdl's layouts directly.
 """
 
 from __future__ import annotations
@@ -52,7 +53,7 @@ def _(x, qweight1, wscales1, proj_down1, proj_up1, smooth1, bias1, qweight2, wsc
 @torch.library.custom_op("live::sage_sm89", mutates_args=())
 def sage_sm89(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_scale: torch.Tensor, k_scale: torch.Tensor,
               v_scale: torch.Tensor, sm_scale: float) -> torch.Tensor:
-    """live::sage_sm89 (sage_ops.cpp:12-19, 28-31) on libwdl (wdl's layouts, see the module docstring)."""
+    """live::sage_sm89 (sage_ops.cpp:12-19, 28-31) on libwdl (either layout, see the module docstring)."""
     return ops.sage_sm89(q, k, v, q_scale, k_scale, v_scale, sm_scale)
 
 

@@ -9,6 +9,8 @@ torch, on the current stream; the library allocates nothing.
 
 from __future__ import annotations
 
+import weakref
+
 import torch
 
 from wdl import _lib
@@ -189,6 +191,25 @@ def scale_pairs(wscales: torch.Tensor) -> torch.Tensor:
     return pairs
 
 
+# scale pairs made for bf16 / fp16 weight-scale tensors passed to the bare ops, per tensor object and version:
+# the reference-schema ops (w4a4_linear, w4a4_gelu_mlp) take the module's scales on every call, and converting them
+# each time would cost an allocation and a launch per call
+_PAIRS: dict[int, tuple] = {}
+
+
+def cached_scale_pairs(wscales: torch.Tensor) -> torch.Tensor:
+    """scale_pairs(wscales), made once per tensor (and again after an in-place change of it)."""
+    if wscales.dtype == torch.int32:
+        return wscales
+    key = id(wscales)
+    hit = _PAIRS.get(key)
+    if hit is not None and hit[0]() is wscales and hit[1] == wscales._version:
+        return hit[2]
+    pairs = scale_pairs(wscales)
+    _PAIRS[key] = (weakref.ref(wscales, lambda _, k=key: _PAIRS.pop(k, None)), wscales._version, pairs)
+    return pairs
+
+
 def as_codes(qweight: torch.Tensor, K: int) -> torch.Tensor:
     """The weight operand for input width K: tile-blocked fp6 codes [N/128, K/64, 128, 48] pass through, packed
     [N, K/2] nibbles are expanded (once per call)."""
@@ -206,9 +227,9 @@ def as_codes(qweight: torch.Tensor, K: int) -> torch.Tensor:
 def gemm_launch(q, ascales, lora, wcodes, wscales, proj_up, bias, M, out, epilogue=EPI_BF16, gate=None,
                 stream_k=True):
     """W4A4 GEMM on the quantizer's outputs (q, ascales, lora) and tile-blocked fp6 weight codes (weight_codes);
-    wscales: the scale pairs (scale_pairs), or bf16 / fp16 scales (converted on each call).
+    wscales: the scale pairs (scale_pairs), or bf16 / fp16 scales (converted once per tensor, cached_scale_pairs).
     stream_k=False runs the one-pass launch also for the shapes that the library splits in K."""
-    wscales = scale_pairs(wscales)
+    wscales = cached_scale_pairs(wscales)
     if q.dim() != 4 or wcodes.dim() != 4 or q.shape[2:] != (BLOCK, ROW6) or wcodes.shape[2:] != (BLOCK, ROW6):
         raise ValueError("the W4A4 GEMM takes tile-blocked fp6 operands [rows/128, K/64, 128, 48]")
     Mp, K = q.shape[0] * BLOCK, q.shape[1] * 64
@@ -226,8 +247,8 @@ def gelu_quant_launch(q, ascales, lora, wcodes, wscales, proj_up, bias, M, smoot
     """The fused GELU MLP's first GEMM: the quantizer's outputs of x (q, ascales, lora) and the first layer's
     operands -> the second layer's inputs (q2 fp6 codes [Mp/128, N/64, 128, 48], ascales2 bf16 [N/64, Mp], lora2
     fp32 [Mp, 32]) for h = GELU(x W1^T + b1) quantized as (h + 0.171875) / smooth2, unsigned; h stays in
-    registers. wscales: the scale pairs (scale_pairs), or bf16 / fp16 scales."""
-    wscales = scale_pairs(wscales)
+    registers. wscales: the scale pairs (scale_pairs), or bf16 / fp16 scales (cached_scale_pairs)."""
+    wscales = cached_scale_pairs(wscales)
     if q.dim() != 4 or wcodes.dim() != 4 or q.shape[2:] != (BLOCK, ROW6) or wcodes.shape[2:] != (BLOCK, ROW6):
         raise ValueError("the W4A4 GEMM takes tile-blocked fp6 operands [rows/128, K/64, 128, 48]")
     Mp, K = q.shape[0] * BLOCK, q.shape[1] * 64
@@ -592,16 +613,34 @@ def _(q, k, v, q_scale, k_scale, v_scale, sm_scale, keys):
 @torch.library.custom_op("wdl::sage_sm89", mutates_args=())
 def sage_sm89(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_scale: torch.Tensor, k_scale: torch.Tensor,
               v_scale: torch.Tensor, sm_scale: float) -> torch.Tensor:
-    """live::sage_sm89's schema (native/ops/sage_ops.cpp:28-31) on wdl's layouts, the key count in the shapes: k the
-    [H, L, 128] view of the padded int8 keys (k_int8[:, :L]), v the [H, 128, L] view of the fp8 values
-    (v_fp8[:, :, :L]); q, q_scale, k_scale, v_scale as wdl::sage_attn takes them."""
+    """live::sage_sm89 (native/ops/sage_ops.cpp:12-19, 28-31): q int8 [1, n, H, 128], q_scale fp32 [1, H,
+    ceil(n/128)*32], v_scale fp32 [1, H, 128] -> bf16 [1, n, H, 128]. k and v in either of two layouts:
+    - the reference's, as kernels/sage_kv.py:141-176 builds them: k int8 [1, L, H, 128], k_scale [1, H,
+      ceil(L/64)*4], v fp8 [1, 128, H, Lpad] in Sage's 16-token order (Lpad = 64 ceil(L/64)); the op copies k and
+      v into wdl's layouts on the device (wdl_sage_sm89_relayout: one pass over them) and runs wdl's kernel;
+    - wdl's own: k the [H, L, 128] view of the padded int8 keys (k_int8[:, :L]) with k_scale [H, Lpad/16], v the
+      [H, 128, L] view of the fp8 values (v_fp8[:, :, :L]), as wdl.sage_kv.prep makes them."""
+    _, n, H, D = q.shape
+    if k.dim() == 4:
+        _, L, Hk, Dk = k.shape
+        Lpad = (L + 63) // 64 * 64
+        if (k.shape[0] != 1 or Hk != H or Dk != D or D != 128 or k.dtype != torch.int8 or k.stride(3) != 1
+                or k.stride(2) != D or v.shape != (1, D, H, Lpad) or v.stride(3) != 1 or v.element_size() != 1
+                or k_scale.shape[-1] != Lpad // 16 or v_scale.shape[-2:] != (H, D)):
+            raise ValueError(f"sage_sm89: k must be int8 [1, L, {H}, 128] and v fp8 [1, 128, {H}, 64 ceil(L / 64)] "
+                             "(the layouts of kernels/sage_kv.py:160-170)")
+        kw = torch.empty(H, Lpad, D, device=k.device, dtype=torch.int8)
+        vw = torch.empty(H, D, Lpad, device=k.device, dtype=torch.uint8)
+        _lib.call("wdl_sage_sm89_relayout", ptr(k), k.stride(1), ptr(v), v.stride(1), v.stride(2), L, H, ptr(kw),
+                  ptr(vw), stream_of(k))
+        prep = dict(k=kw, k_scale=k_scale.reshape(H, -1), v=vw, v_scale=v_scale.reshape(H, D))
+        return sage_attn_launch(q[0], q_scale.reshape(H, -1), prep, L, sm_scale).view(1, n, H, D)
     H, L, D = k.shape
     Lpad = (L + 63) // 64 * 64  # the kernel's row pitch for L keys: the views must come from buffers of that pitch
     if k.stride(1) != D or k.stride(2) != 1 or k.stride(0) != Lpad * D or v.stride(2) != 1 or v.stride(1) != Lpad \
             or v.shape != (H, D, L):
         raise ValueError("sage_sm89: k must be a [H, L, 128] view of wdl's [H, Lpad, 128] keys and v the matching "
                          "[H, 128, L] view of the [H, 128, Lpad] values")
-    _, n, _, _ = q.shape
     prep = dict(k=k, k_scale=k_scale, v=v, v_scale=v_scale)
     return sage_attn_launch(q[0], q_scale[0], prep, L, sm_scale).view(1, n, H, D)
 

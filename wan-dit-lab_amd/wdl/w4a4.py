@@ -225,8 +225,9 @@ class PackedW4A4GeluMLP(torch.nn.Module):
 class FusedQKVAttention(torch.nn.Module):
     """Self-attention with q, k, v as one W4A4 layer qkv [3 dim, dim] (w4a4.py:246-262): X quantized once, one GEMM,
     then the fused Q/K RMSNorm + 3D RoPE kernel, the KVCache's Sage attention over the FP8 window (or, with no
-    cache, Sage attention over the chunk alone) and the W4A4 o projection. qkv / o: PackedW4A4Linear; norm_q /
-    norm_k: bf16 RMSNorm weights [dim]."""
+    cache, the chunk attending to itself in bf16 with an exact fp32 softmax, as the reference's
+    scaled_dot_product_attention does, w4a4.py:259-261) and the W4A4 o projection. qkv / o: PackedW4A4Linear;
+    norm_q / norm_k: bf16 RMSNorm weights [dim]."""
 
     def __init__(self, dim, num_heads, eps=1e-6):
         super().__init__()
@@ -235,7 +236,7 @@ class FusedQKVAttention(torch.nn.Module):
         self.norm_q = self.norm_k = None
 
     def forward(self, X, grid_sizes=None, freq=None, context=None, start_frame=0, cache=None, context_kv=None):
-        from wdl import rope, sage_kv
+        from wdl import rope
 
         assert context is None and context_kv is None, "q, k and v of one input: self-attention only"
         if self.head_dim != 128:
@@ -251,10 +252,8 @@ class FusedQKVAttention(torch.nn.Module):
         V = qkv[:, 2 * self.dim:]
         if cache is not None:
             A = cache.attend(Q.view(shape), K.view(shape), V.reshape(shape))
-        else:
-            z8 = torch.zeros(1, 1, self.num_heads, 128, device=X.device, dtype=torch.float8_e4m3fn)
-            one = torch.ones(1, 1, self.num_heads, 1, device=X.device)
-            A = sage_kv.attend(Q.view(shape), z8, one, z8, one, 0, K.view(shape), V.reshape(shape))
+        else:  # SDPA over the chunk alone (w4a4.py:259-261): bf16 operands, exact softmax
+            A = ops.attn_bf16_launch(Q, ops.attn_bf16_prep_launch(K, V), self.head_dim ** -0.5)
         return self.o(A.reshape(1, L, self.dim))
 
 
