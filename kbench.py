@@ -1,4 +1,4 @@
-"""Kernel timings at the step's shapes, for profiling runs: `python -m wdl.kbench attention|cross|prep|gemm|quant
+"""Kernel timings at the step's shapes, for profiling runs: `python kbench.py attention|cross|prep|gemm|quant
 [lib]`.
 
 attention: Sage prep + attention of 1280 and 1392 queries over a full 9744-key window (8352 cached FP8 tokens + the
@@ -15,6 +15,11 @@ from __future__ import annotations
 
 import sys
 from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "wan-dit-lab_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
 
 
 def _replay_us(fn, reps: int = 10) -> float:
@@ -219,7 +224,7 @@ def quant():
 
 def main(argv):
     if len(argv) < 2 or argv[1] not in ("attention", "chunk", "cross", "prep", "gemm", "quant", "fp8", "fp8wo"):
-        raise SystemExit("usage: python -m wdl.kbench attention|chunk|cross|prep|gemm|quant|fp8|fp8wo [library path]")
+        raise SystemExit("usage: python kbench.py attention|chunk|cross|prep|gemm|quant|fp8|fp8wo [library path]")
     if len(argv) > 2:
         from wdl import _lib
 

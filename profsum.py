@@ -1,8 +1,8 @@
 """Summaries of rocprofv3 CSV output for the DiT step (kernel time table, calibrated HBM bytes per launch).
 
-    python -m wdl.profsum stats  <kernel_stats.csv>  [top]
-    python -m wdl.profsum grids  <kernel_trace.csv>  [name filter]
-    python -m wdl.profsum pmc    <fetch counter_collection.csv> <write counter_collection.csv> [copy MiB]
+    python profsum.py stats  <kernel_stats.csv>  [top]
+    python profsum.py grids  <kernel_trace.csv>  [name filter]
+    python profsum.py pmc    <fetch counter_collection.csv> <write counter_collection.csv> [copy MiB]
 
 `stats` prints the per-kernel time table of `rocprofv3 --kernel-trace --stats --output-format csv`.
 `grids` prints, from the kernel trace, the launches, average and minimum duration per kernel and grid (one line

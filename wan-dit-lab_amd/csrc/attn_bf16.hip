@@ -15,16 +15,18 @@
 // keys >= L are zero. Both swizzles make the 16-byte reads of 16 consecutive rows (one LDS read phase) hit 16
 // distinct bank groups, and both layouts make one 64-key block a straight copy into LDS.
 //
-// Work split: a workgroup of 8 waves takes 128 queries of one head; its two groups of 4 waves take the key blocks in
-// halves, each wave 32 queries, and stream K / V blocks through a 2-stage LDS ring per group (global_load_lds, 16
-// bytes per lane). Products are computed transposed so that a lane owns one query:
+// Work split: a workgroup of 2 WPG waves takes 32 WPG queries of one head; its two groups of WPG waves take the key
+// blocks in halves, each wave 32 queries, and stream K / V blocks through a 2-stage LDS ring per group
+// (global_load_lds, 16 bytes per lane, issued by the group's first 4 waves). WPG is 4, or 5 / 6 when that fits
+// every (query tile, head) pair into one round of workgroups (1392 queries x 24 heads: 9 tiles of 160 queries,
+// 216 workgroups, where 128-query tiles would need 264). Products are computed transposed so that a lane owns one query:
 //   S^T = K Q^T   with v_mfma_f32_32x32x16_bf16 (8 per 32 x 32 tile over d = 128);
 //   O^T = V^T P^T with v_mfma_f32_32x32x16_bf16 (4 per 16 keys, one per 32 channels);
 // the lane's 32 scores of a block (keys 32 j + 8 g + 4 half + e) are the B operand of the P V product in 16-key
 // slices, which is why V's keys are reordered inside each 16-key group. The block max needs one exchange with
 // lane ^ 32. Group 1 hands (O, m, l) to group 0 through LDS at the end. When the (query tile, head) pairs number
-// between one and two times the CU count, the first T - CUs workgroups run two tiles, one per group over all the
-// key blocks, so the launch takes one round. Tiles are dealt so that each XCD runs a contiguous range of them.
+// between one and two times the CU count and no wider tile fits one round, the first T - CUs workgroups run two
+// tiles, one per group over all the key blocks, so the launch takes one round. Tiles are dealt so that each XCD runs a contiguous range of them.
 #include "wdl_common.h"
 
 namespace {
@@ -39,7 +41,7 @@ constexpr int RING = 2;                        // stages per group
 constexpr int BLK_BYTES = 64 * D * 2;          // one 64-key block of K (or of V), bf16
 constexpr int GSTAGE = 2 * BLK_BYTES;          // K then V
 constexpr int STAGE = 2 * GSTAGE;              // both groups
-constexpr int LPB = 2 * BLK_BYTES / (256 * 16);  // 16-byte loads per lane per block (K and V): 8
+constexpr int LPB = 2 * BLK_BYTES / (256 * 16);  // 16-byte loads per loading lane per block (K and V): 8
 
 struct Args {
     const uint16_t* q;
@@ -67,12 +69,15 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-__global__ __launch_bounds__(512) void attn_bf16_kernel(Args a) {
+template <int WPG>
+__global__ __launch_bounds__(128 * WPG) void attn_bf16_kernel(Args a) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[RING * STAGE];
+    static_assert(WPG >= 4 && WPG * (64 * 64 + 128) * 4 <= RING * STAGE, "the hand-over fits the ring's LDS");
 
     const int t = threadIdx.x, lane = t % 64, half = lane / 32, tok = lane % 32;
     const int wave = __builtin_amdgcn_readfirstlane(t / 64);
-    const int grp = wave / 4, sub = wave % 4;
+    const int grp = wave / WPG, sub = wave % WPG;
+    const bool loader = sub < 4;  // the group's first 4 waves copy its K / V blocks (uniform per wave)
     // workgroup ids go round-robin over the 8 XCDs: each XCD takes a contiguous range of the tiles, so the query
     // tiles of one head (consecutive tiles) read its K / V through one L2 (otherwise every XCD streams every head's
     // K / V from the memory side)
@@ -81,7 +86,7 @@ __global__ __launch_bounds__(512) void attn_bf16_kernel(Args a) {
     const bool dualwg = w < a.dual;
     const int64_t tile = dualwg ? 2 * w + grp : a.dual + w;
     const int64_t h = tile / a.qtiles, qt = tile % a.qtiles;
-    const int64_t q = qt * 128 + sub * 32 + tok;
+    const int64_t q = qt * (32 * WPG) + sub * 32 + tok;
     const bool qlive = q < a.n;
     const int nblk = int(a.Lpad / 64), L32 = int(a.L);  // Lpad < 2^23 (checked by the launcher)
     const bool ragged = L32 % 64 != 0;
@@ -103,6 +108,7 @@ __global__ __launch_bounds__(512) void attn_bf16_kernel(Args a) {
         voff[j] = uint32_t((slot / 8) * (2 * a.Lpad) + (slot % 8) * 16);
     }
     auto load_block = [&](int st, int blk) {
+        if (!loader) return;
         uint8_t* base = smem + st * STAGE + grp * GSTAGE;
         const uint8_t* kb = kbase + int64_t(blk) * BLK_BYTES;
         const uint8_t* vb = vbase + int64_t(blk) * 128;  // 64 keys x 2 bytes into each channel row
@@ -314,12 +320,21 @@ extern "C" int wdl_attn_bf16(const void* q, int64_t ldq, const void* kp, const v
     const int64_t Lpad = (L + 63) / 64 * 64;
     if (2 * Lpad * 128 >= (int64_t(1) << 31)) return fail(WDL_EINVAL, "attn_bf16: L=%lld too long", (long long)L);
     if (n == 0) return WDL_OK;
-    const int64_t qtiles = (n + 127) / 128, T = qtiles * heads;
+    // the narrowest query tile (32 WPG queries) whose (tile, head) pairs fit one round of workgroups; else 128
     const int64_t cus = cu_count();
+    int wpg = 4;
+    for (int w = 4; w <= 6; ++w)
+        if (cus > 0 && (n + 32 * w - 1) / (32 * w) * heads <= cus) {
+            wpg = w;
+            break;
+        }
+    const int64_t qtiles = (n + 32 * wpg - 1) / (32 * wpg), T = qtiles * heads;
     const int64_t dual = cus > 0 && T > cus && T <= 2 * cus ? T - cus : 0;
     const int64_t W = T - dual;
     Args a{static_cast<const uint16_t*>(q), ldq, static_cast<const uint16_t*>(kp), static_cast<const uint16_t*>(vp),
            static_cast<uint16_t*>(out), ldo, n, L, Lpad, heads, qtiles, sm_scale * 1.4426950408889634f, dual};
-    attn_bf16_kernel<<<unsigned(W), 512, 0, stream>>>(a);
+    if (wpg == 5) attn_bf16_kernel<5><<<unsigned(W), 640, 0, stream>>>(a);
+    else if (wpg == 6) attn_bf16_kernel<6><<<unsigned(W), 768, 0, stream>>>(a);
+    else attn_bf16_kernel<4><<<unsigned(W), 512, 0, stream>>>(a);
     return check_launch("attn_bf16");
 }
