@@ -273,23 +273,27 @@ class CpuBlock:
     RMSNorm, 3D RoPE (fp32 table) and torch's scaled_dot_product_attention over the window and over the prompt.
     Random-init parts of the Wan2.2-TI2V-5B block shapes (int4 in [-7, 7], N(0, 0.02^2)-sized group scales)."""
 
-    def __init__(self, dtype, seed=0):
+    def __init__(self, dtype, seed=0, dim=DIM, ffn=FFN, heads=HEADS):
         import torch
 
         g = torch.Generator().manual_seed(seed)
-        self.dt = dtype
-        shapes = dict(qkv=(3 * DIM, DIM), o=(DIM, DIM), cq=(DIM, DIM), ck=(DIM, DIM), cv=(DIM, DIM), co=(DIM, DIM),
-                      ffn1=(FFN, DIM), ffn2=(DIM, FFN))
-        self.lin = {}
+        self.dt, self.dim, self.heads = dtype, dim, heads
+        shapes = dict(qkv=(3 * dim, dim), o=(dim, dim), cq=(dim, dim), ck=(dim, dim), cv=(dim, dim), co=(dim, dim),
+                      ffn1=(ffn, dim), ffn2=(dim, ffn))
+        self.lin, self.logical = {}, {}
         for name, (n, k) in shapes.items():
-            q = torch.randint(-7, 8, (n, k), generator=g).float()
-            ws = (torch.rand(n, k // 64, generator=g) * 0.5 + 0.75) * (3 * 0.02 / 7)
+            q = torch.randint(-7, 8, (n, k), generator=g)
+            ws = ((torch.rand(n, k // 64, generator=g) * 0.5 + 0.75) * (3 * 0.02 / 7)).to(torch.bfloat16)
+            pd = (torch.randn(k, 32, generator=g) / k ** 0.5).to(torch.bfloat16)
+            pu = (torch.randn(n, 32, generator=g) * 0.02).to(torch.bfloat16)
+            b = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16)
             self.lin[name] = dict(
-                W=(q.view(n, k // 64, 64) * ws.to(torch.bfloat16).float()[..., None]).view(n, k).to(dtype),
-                pd=(torch.randn(k, 32, generator=g) / k ** 0.5).to(dtype),
-                pu=(torch.randn(n, 32, generator=g) * 0.02).to(dtype),
-                b=(torch.randn(n, generator=g) * 0.02).to(dtype))
-        self.mod = torch.randn(6, DIM, generator=g) / DIM ** 0.5
+                W=(q.float().view(n, k // 64, 64) * ws.float()[..., None]).view(n, k).to(dtype),
+                pd=pd.to(dtype), pu=pu.to(dtype), b=b.to(dtype))
+            # the same layer as the oracle's logical W4A4 parts (unit smoothing)
+            self.logical[name] = dict(q=q.to(torch.int32), wscales=ws, proj_down=pd, proj_up=pu,
+                                      smooth=torch.ones(k, dtype=torch.bfloat16), bias=b)
+        self.mod = torch.randn(6, dim, generator=g) / dim ** 0.5
         from oracle import rope as orope
 
         self.freq = orope.freqs(128, 1024, torch.float64).float()
@@ -313,19 +317,31 @@ class CpuBlock:
                                                              V.transpose(0, 1)[None])
         return o[0].transpose(0, 1).reshape(Q.shape[0], -1)
 
+    def oracle_parts(self) -> dict:
+        """The block as the oracle's logical parts (oracle.block.block_forward): the linears, unit RMSNorm weights,
+        no affine on norm3, the modulation."""
+        import torch
+
+        P = dict(self.logical)
+        for name in ("wq", "wk", "cwq", "cwk"):
+            P[name] = torch.ones(self.dim, dtype=torch.bfloat16)
+        P["n3w"], P["n3b"] = torch.ones(self.dim), torch.zeros(self.dim)
+        P["modulation"] = self.mod.float()
+        return P
+
     def forward(self, X, time_in, cache_k, cache_v, ctx_k, ctx_v, grid, start):
         import torch
         from oracle import rope as orope
 
-        dt, H = self.dt, HEADS
+        dt, H, D = self.dt, self.heads, self.dim
         e = (time_in + self.mod).to(dt)
         M = X.shape[0]
-        ln = lambda x: torch.nn.functional.layer_norm(x.float(), (DIM,), eps=1e-6).to(dt)
+        ln = lambda x: torch.nn.functional.layer_norm(x.float(), (D,), eps=1e-6).to(dt)
         rms = lambda x: (x.float() * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + 1e-6)).to(dt)
         qkv = self.linear(ln(X) * (1 + e[1]) + e[0], "qkv")
-        Q = orope.rope_apply(rms(qkv[:, :DIM]).view(1, M, H, 128).float(), grid, self.freq, start)[0].to(dt)
-        K = orope.rope_apply(rms(qkv[:, DIM:2 * DIM]).view(1, M, H, 128).float(), grid, self.freq, start)[0].to(dt)
-        V = qkv[:, 2 * DIM:].reshape(M, H, 128)
+        Q = orope.rope_apply(rms(qkv[:, :D]).view(1, M, H, 128).float(), grid, self.freq, start)[0].to(dt)
+        K = orope.rope_apply(rms(qkv[:, D:2 * D]).view(1, M, H, 128).float(), grid, self.freq, start)[0].to(dt)
+        V = qkv[:, 2 * D:].reshape(M, H, 128)
         A = self.attention(Q, torch.cat([cache_k, K]), torch.cat([cache_v, V]))
         X = X + self.linear(A, "o") * e[2]
         qc = rms(self.linear(ln(X), "cq")).view(M, H, 128)
