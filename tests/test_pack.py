@@ -103,3 +103,43 @@ def test_fp16_weight_scales_round_trip(tmp_path):
         if isinstance(v, dict):
             assert back[k]["wscales"].dtype == torch.float16
             same(back[k]["wscales"], v["wscales"])
+
+
+def mixed_parts_of(dim, ffn, seed):
+    """Mixed-precision parts: the attention projections FP8 weight-only (e4m3 rows, fp32 scale per row, bf16 bias),
+    the feed-forward W4A4."""
+    g = torch.Generator().manual_seed(seed)
+    P = parts_of(dim, ffn, seed)
+    for k, (n, kk) in dict(qkv=(3 * dim, dim), o=(dim, dim), cq=(dim, dim), ck=(dim, dim), cv=(dim, dim),
+                           co=(dim, dim)).items():
+        w = torch.randn(n, kk, generator=g) * 0.02
+        s = w.abs().amax(1) / 448
+        P[k] = dict(fp8=(w / s[:, None]).to(torch.float8_e4m3fn), fp8_scale=s.float(),
+                    bias=(torch.randn(n, generator=g) * 0.02).to(torch.bfloat16))
+    return P
+
+
+def test_mixed_precision_round_trip(tmp_path):
+    """Blocks with FP8 weight-only attention projections pack under block_mixed_v1_gfx950: every entry (e4m3 codes,
+    per-row scales, biases, the W4A4 feed-forward, norms) round-trips bit-exactly, 16-byte aligned, digest checked;
+    an all-W4A4 pack keeps block_w4a4_v2_gfx950; an FP8 feed-forward is refused before anything is written."""
+    blocks = [mixed_parts_of(256, 1024, s) for s in (5, 6)]
+    path = tmp_path / "m.pack"
+    info = pack.build_pack(blocks, path, source="mixed")
+    assert info["format"] == pack.FORMAT_MIXED and "FP8" in info["quantization"]
+    rows, layout, meta = pack.mapped_pack(path, source="mixed", verify=True)
+    assert all(e["offset"] % 16 == 0 for e in layout)
+    assert [e["name"] for e in layout][:3] == ["self_attn.qkv.fp8", "self_attn.qkv.fp8_scale", "self_attn.qkv.bias"]
+    for i, parts in enumerate(blocks):
+        got = pack.slot(rows[i], layout)
+        for k in pack.LAYERS:
+            for p in (pack.FP8_PARTS if "fp8" in parts[k] else pack.PARTS):
+                same(got[k][p], parts[k][p])
+        for k in pack.OTHERS:
+            same(got[k], parts[k])
+    assert pack.build_pack([parts_of(128, 256, 1)], tmp_path / "w.pack")["format"] == pack.FORMAT
+    bad = mixed_parts_of(128, 256, 7)
+    bad["ffn1"] = dict(bad["qkv"])
+    with pytest.raises(ValueError, match="feed-forward"):
+        pack.build_pack([bad], tmp_path / "bad.pack")
+    assert not (tmp_path / "bad.pack").exists() and not (tmp_path / "bad.pack.json").exists()

@@ -1,4 +1,5 @@
-"""On-disk weight pack of quantized blocks in wdl's physical layout (block_w4a4_v2_gfx950).
+"""On-disk weight pack of quantized blocks in wdl's physical layout (block_w4a4_v2_gfx950; block_mixed_v1_gfx950 with FP8
+weight-only attention projections).
 
 The reference's block_w4a4_v2 pack (quantization/w4a4.py:279-313 pack_layout, 360-436 build_pack / mapped_pack;
 weight_pack.py:84-171 for the FP8 sibling): one uint8 row per block, each tensor of the block at a 16-byte aligned
@@ -13,6 +14,12 @@ quantized for GELU's output + 0.171875) — qweight uint8 [N, K/2] (per 64-group
 high nibble), wscales bf16 or fp16 [K/64, N], proj_down bf16 [32, K], proj_up bf16 [N, 32], smooth bf16 [K], bias bf16
 [N]; then the Q/K RMSNorm weights (bf16), norm3's affine (fp32) and the modulation (fp32 [6, dim]). The manifest
 names that layout ("layout_notes"), so a reader never guesses it.
+
+Blocks of the mixed-precision mode (attention projections FP8 weight-only, feed-forward W4A4) are packed the same
+way under the format block_mixed_v1_gfx950: an FP8 layer's entries are fp8 (e4m3 codes [N, K]), fp8_scale (fp32 [N],
+one per output row, or [1]) and bias (bf16 [N]), in the place of the W4A4 layer's six — the FP8 sibling of the
+reference's block_fp8_v1 rows (weight_pack.py:84-171: e4m3 weights with fp32 scales, 16-byte aligned entries), with
+this build's per-row scales.
 """
 
 from __future__ import annotations
@@ -26,6 +33,9 @@ import numpy as np
 import torch
 
 FORMAT = "block_w4a4_v2_gfx950"
+FORMAT_MIXED = "block_mixed_v1_gfx950"
+FORMATS = (FORMAT, FORMAT_MIXED)
+FP8_PARTS = ("fp8", "fp8_scale", "bias")
 ALIGN = 16
 # wdl's part names -> the reference block's module names (models/block.py, multi_head_attention.py)
 LAYERS = {"qkv": "self_attn.qkv", "o": "self_attn.o", "cq": "cross_attn.q", "ck": "cross_attn.k",
@@ -33,20 +43,28 @@ LAYERS = {"qkv": "self_attn.qkv", "o": "self_attn.o", "cq": "cross_attn.q", "ck"
 PARTS = ("qweight", "wscales", "proj_down", "proj_up", "smooth", "bias")
 OTHERS = {"wq": "self_attn.norm_q.weight", "wk": "self_attn.norm_k.weight", "cwq": "cross_attn.norm_q.weight",
           "cwk": "cross_attn.norm_k.weight", "n3w": "norm3.weight", "n3b": "norm3.bias", "modulation": "modulation"}
-DTYPES = {torch.uint8: "uint8", torch.bfloat16: "bfloat16", torch.float16: "float16", torch.float32: "float32"}
+DTYPES = {torch.uint8: "uint8", torch.bfloat16: "bfloat16", torch.float16: "float16", torch.float32: "float32",
+          torch.float8_e4m3fn: "float8_e4m3fn"}
 LAYOUT_NOTES = ("qweight uint8 [N, K/2]: per 64-group byte j holds k_j (low nibble) and k_{j+32} (high), int4 in "
                 "two's complement; wscales bf16 or fp16 [K/64, N] group-major; proj_down bf16 [32, K] (transposed); proj_up "
                 "bf16 [N, 32]; smooth bf16 [K]; bias bf16 [N]; ffn.2 quantized for the GELU output + 0.171875 "
                 "(unsigned int4 activations); norm weights bf16; norm3 affine and modulation fp32")
+LAYOUT_NOTES_MIXED = LAYOUT_NOTES + ("; FP8 weight-only layers: fp8 e4m3 [N, K] row-major, fp8_scale fp32 [N] (per "
+                                     "output row) or [1], bias bf16 [N]; y = fp8_scale * (x . w) + bias with bf16 x")
 
 
 def _entries(parts: dict):
     """(name, tensor) of a block's parts, in row order. A layer that holds only the GEMM's weight codes (a
     QuantizedWanBlock drops the packed nibbles once it has them) is written as the nibbles those codes decode to."""
     for key, name in LAYERS.items():
-        if "fp8" in parts[key]:
-            raise ValueError(f"{key}: FP8 weight-only layers (the mixed-precision mode) have no place in the "
-                             f"block_w4a4_v2_gfx950 pack, whose layers are all W4A4")
+        if "fp8" in parts[key]:  # an FP8 weight-only layer (the mixed-precision mode)
+            if key in ("ffn1", "ffn2"):
+                raise ValueError(f"{key}: the feed-forward is W4A4 in every mode")
+            t = parts[key]
+            yield f"{name}.fp8", t["fp8"].contiguous()
+            yield f"{name}.fp8_scale", t["fp8_scale"].reshape(-1).float()
+            yield f"{name}.bias", t["bias"].to(torch.bfloat16)
+            continue
         for p in PARTS:
             if p == "qweight" and p not in parts[key]:
                 from wdl.ops import decode_weights
@@ -131,14 +149,19 @@ def build_pack(blocks: list, path, source: str = "", **metadata) -> dict:
     if any(lay != layouts[0] for lay in layouts[1:]):
         raise ValueError("packed blocks must share one layout")
     layout, size = layouts[0]
+    mixed = any(e["name"].endswith(".fp8") for e in layout)
     manifest = path.with_name(path.name + ".json")
     with _StagedFile(path, manifest) as out:
         for parts in blocks:
             out.write(_row_bytes(parts, layout, size))
-        meta = dict(format=FORMAT, blocks=len(blocks), layout=layout, bytes_per_block=size, bytes=out.written,
-                    sha256=out.sha.hexdigest(), source=source, layout_notes=LAYOUT_NOTES,
-                    quantization="SVDQuant W4A4: int4 groups of 64, rank-32 low-rank branch in bf16, smoothing; "
-                                 "q, k, v of self-attention as one layer, the feed forward as the fused GELU MLP",
+        quantization = ("SVDQuant W4A4: int4 groups of 64, rank-32 low-rank branch in bf16, smoothing; q, k, v of "
+                        "self-attention as one layer, the feed forward as the fused GELU MLP")
+        if mixed:
+            quantization += ("; the attention projections FP8 e4m3 weight-only (one fp32 scale per output row, bf16 "
+                             "activations)")
+        meta = dict(format=FORMAT_MIXED if mixed else FORMAT, blocks=len(blocks), layout=layout,
+                    bytes_per_block=size, bytes=out.written, sha256=out.sha.hexdigest(), source=source,
+                    layout_notes=LAYOUT_NOTES_MIXED if mixed else LAYOUT_NOTES, quantization=quantization,
                     **metadata)
         manifest.write_text(json.dumps(meta, indent=1), encoding="utf-8")
     return {k: v for k, v in meta.items() if k != "layout"}
@@ -167,8 +190,8 @@ def mapped_pack(path, source: str | None = None, verify: bool = False):
     path = Path(path)
     meta = read_manifest(path)
     problems = []
-    if meta.get("format") != FORMAT:
-        problems.append(f"format {meta.get('format')!r} is not {FORMAT}")
+    if meta.get("format") not in FORMATS:
+        problems.append(f"format {meta.get('format')!r} is not one of {FORMATS}")
     if source is not None and meta.get("source") != source:
         problems.append(f"made from {meta.get('source')!r}, not {source!r}")
     rows, size = meta["blocks"], meta["bytes_per_block"]
@@ -194,7 +217,7 @@ def slot(row: torch.Tensor, layout: list, device=None) -> dict:
         t = t.to(device) if device is not None else t
         name = e["name"]
         layer, _, part = name.rpartition(".")
-        if layer in inv_layers and part in PARTS:
+        if layer in inv_layers and (part in PARTS or part in FP8_PARTS):
             parts[inv_layers[layer]][part] = t
         elif name in inv_others:
             parts[inv_others[name]] = t
