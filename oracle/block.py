@@ -268,10 +268,10 @@ def fp8_weight_only(N: int, K: int, g: torch.Generator, scale: float = 0.02) -> 
     return dict(fp8=wq, fp8_scale=ws, bias=(torch.randn(N, generator=g) * scale).to(BF))
 
 
-def mixed_precision_block(dim: int, ffn: int, g: torch.Generator) -> dict:
-    """The mixed-precision mode's parts: the attention projections (qkv, o, cq, ck, cv, co) FP8 weight-only, the
-    feed-forward W4A4 (random_logical)."""
-    P = random_logical_block(dim, ffn, g)
+def mixed_precision_block(dim: int, ffn: int, g: torch.Generator, scale: float = 0.02) -> dict:
+    """The mixed-precision mode's parts: the attention projections (qkv, o, cq, ck, cv, co) FP8 weight-only
+    (N(0, 0.02^2) weights), the feed-forward W4A4 (random_logical at `scale`)."""
+    P = random_logical_block(dim, ffn, g, scale=scale)
     for name, (n, k) in dict(qkv=(3 * dim, dim), o=(dim, dim), cq=(dim, dim), ck=(dim, dim), cv=(dim, dim),
                              co=(dim, dim)).items():
         P[name] = fp8_weight_only(n, k, g)
