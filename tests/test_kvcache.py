@@ -66,3 +66,30 @@ def test_a_pinned_chunk_larger_than_the_free_ring_is_evicted_last():
     assert q.frames == [[1, [2, 3]]]
     q.append(3, 2, [0, 1, 2, 3], [4, 5, 0, 1])
     assert q.take_oldest(2) == [4, 5]               # slot 0 and 1 stay pinned with their new tokens
+
+
+def test_anchor_rows_are_the_newest_frame_in_topk_order():
+    """Forcing-KV's anchor (causal.py:243-248): the ring tokens with the largest (frame, place) order, as torch.topk
+    ranks them (largest first), after the sink. Checked against an independent per-slot bookkeeping of the frame and
+    place of every ring token over 9 commits (the window fills, then evicts the oldest frames)."""
+    from wdl.kvcache import KVCache
+
+    per, chunk, window, sink = 3, 2, 10, 2
+    n = chunk * per
+    cache = KVCache((window - chunk) * per, sink * per, chunk=chunk)
+    cache.allocate(torch.zeros(1, n, 1, 4))
+    ring = (window - chunk - sink) * per
+    frame_of = torch.full((ring,), -1, dtype=torch.long)  # -1: no token yet (never the newest)
+    place = torch.zeros(ring, dtype=torch.long)
+    for c in range(9):
+        frames_before = cache.frames
+        cache.commit()
+        if cache.last_slots is not None:
+            # the chunk's tokens past the sink, in token order (the tail of the chunk when part of it is sink)
+            i = torch.arange(n - len(cache.last_slots), n)
+            frame_of[cache.last_slots] = frames_before + i // per
+            place[cache.last_slots] = i % per
+        order = torch.where(frame_of >= 0, frame_of * per + place, torch.full_like(frame_of, -1))
+        if int((frame_of >= 0).sum()) >= per:
+            want = (sink * per + torch.topk(order, per).indices).tolist()
+            assert cache.anchor_rows() == want, (c, cache.anchor_rows(), want)

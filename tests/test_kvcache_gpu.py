@@ -123,3 +123,53 @@ def test_rows_written_directly_need_invalidate_stats(gpu):
     out = cache.attend(Q, K, V)
     whole = sage_kv.attend(Q, cache.k, cache.ks, cache.v, cache.vs, cache.saved, K, V)
     assert osage.cosine(out.cpu().float(), whole.cpu().float()) >= 0.9999
+
+
+@pytest.mark.parametrize("static", [(1, 3), (0,), (0, 1, 2, 3)])
+def test_forcing_kv_head_split_on_a_full_window(gpu, static):
+    """KVCache.set_heads (causal.py:98-104, 222-248): on a full window the static heads attend over the sink, the
+    newest finished frame and the chunk only, the dynamic heads over the whole window. Each group's output equals a
+    direct sage_kv.attend of its heads through the head and row maps bit for bit, and meets the Sage bars against
+    the oracle emulation over the same rows and against exact attention over the unquantized keys and values of
+    those frames. The anchor follows each commit (the rows of the frame just finished)."""
+    from wdl import sage_kv
+    from wdl.kvcache import KVCache
+
+    heads, window, sink = 4, 12, 3
+    g = torch.Generator().manual_seed(sum(static) + 10 * len(static))
+    cache = KVCache((window - CHUNK) * T, sink * T, chunk=CHUNK)
+    cache.set_heads(list(static), heads)
+    dynamic = [h for h in range(heads) if h not in static]
+    frames = []
+    new = lambda: [torch.randn(1, CHUNK * T, heads, 128, generator=g).to(torch.bfloat16) for _ in range(3)]
+    for c in range(7):
+        Q, K, V = new()
+        full = cache.full()
+        out = cache.attend(Q.cuda(), K.cuda(), V.cuda())
+        at = cache.saved
+        if full:
+            ring = window - CHUNK - sink
+            seen = frames[:sink] + frames[len(frames) - ring:]
+            rows = torch.tensor(list(range(sink * T)) + cache.anchor_rows(), dtype=torch.int32)
+            assert torch.equal(cache.anchor_tokens.cpu(), rows)
+            for group, tokens, length, keep in ((dynamic, None, at, seen), (list(static), rows, rows.numel(),
+                                                                           frames[:sink] + frames[-1:])):
+                if not group:
+                    continue
+                idx = torch.tensor(group, dtype=torch.int32)
+                q, k, v = (t[:, :, idx.long()].contiguous() for t in (Q, K, V))
+                direct = sage_kv.attend(q.cuda(), cache.k, cache.ks, cache.v, cache.vs, length, k.cuda(), v.cuda(),
+                                        heads=idx.cuda(), tokens=None if tokens is None else tokens.cuda())
+                mine = out[:, :, idx.long()].cpu()
+                assert torch.equal(mine, direct.cpu()), f"heads {group}"
+                p = osage.prep(q, cache.k.cpu(), cache.ks.cpu(), cache.v.cpu(), cache.vs.cpu(), length, k, v,
+                               heads=idx, tokens=tokens)
+                assert osage.cosine(mine, osage.attention_quantized(p, 128 ** -0.5)) >= 0.999, f"heads {group}"
+                Kw = torch.cat([f[0][:, idx.long()] for f in keep] + [k[0]]).float()[None]
+                Vw = torch.cat([f[1][:, idx.long()] for f in keep] + [v[0]]).float()[None]
+                exact = osage.attention_exact(q, Kw, Vw)
+                base = osage.rel_err(osage.attention_quantized(p, 128 ** -0.5, p_fp8=True), exact)
+                assert osage.rel_err(mine, exact) < 1.2 * base + 1e-3, f"heads {group}"
+        cache.commit()
+        frames += [(K[0, f * T:(f + 1) * T], V[0, f * T:(f + 1) * T]) for f in range(CHUNK)]
+    assert cache.full()

@@ -22,8 +22,13 @@ first" (causal.py:329-337); walking the queue from its head, skipping pinned slo
 without sorting. The slot numbers a commit produces are pinned by the reference's own fixture
 (native/live/tests/fixtures/ring.json, in tests/golden/).
 
-Positions-in-window turns, Echo-Forcing decay, Participative Compression and Forcing-KV head splits are not on
-this hot path and are not implemented here.
+Forcing-KV head split (set_heads, causal.py:98-104, 222-248): once the window is full, the dynamic heads attend over
+the whole window and the static heads over the sink and the newest finished frame only (anchor_tokens: the sink's
+rows, then the newest frame's rows in decreasing token order, as the reference's topk gives them, refreshed at every
+commit); both read the one cache through the heads / tokens maps of the Sage preparation, nothing copied.
+
+Positions-in-window turns, Echo-Forcing decay and Participative Compression are not on this hot path and are not
+implemented here.
 """
 
 from __future__ import annotations
@@ -95,6 +100,8 @@ class KVCache:
         self.fp8 = True
         self.k = self.v = None
         self.queue = _FrameQueue()
+        self.static_heads = None  # Forcing-KV: the heads that see only the sink and the newest frame (set_heads)
+        self._groups = None
         self.stats = None
         self._stats_at = -1  # rows [0, _stats_at) are what `stats` describes; -1: stale
         self.reset()
@@ -128,6 +135,14 @@ class KVCache:
         self.frames = 0
         self.last_slots = None
         self.queue.clear()
+
+    def set_heads(self, static, heads: int):
+        """static: the head numbers (of `heads`) that attend to the sink, the newest finished frame and the chunk
+        once the cache is full; None or empty: every head sees the whole window (causal.py:98-104)."""
+        self.static_heads = sorted(static) if static else None
+        self.dynamic_heads = [h for h in range(heads) if h not in (static or ())]
+        self._groups = None
+        self.__dict__.pop("anchor_tokens", None)
 
     def full(self) -> bool:
         return self.k is not None and self.saved == self.max_tokens
@@ -163,11 +178,58 @@ class KVCache:
         if self.k is None:
             self.allocate(V)
         n, at = K.shape[1], self.saved
+        if self.static_heads is not None and self.full():
+            self.store(at, K, V)
+            return self.attend_split(Q, K, V, at, n)
         if self._stats_at != at:
             self._refresh_stats()
         self.store(at, K, V)
         return attend(Q, self.k, self.ks, self.v, self.vs, at, K, V, sm_scale=self.scale(at + n, Q.shape[-1]),
                       cache_stats=self.stats)
+
+    def _head_groups(self, dev):
+        """[(cache heads int32, as index, cache rows int32 or None)] of the two Forcing-KV groups, made once per
+        set_heads: the dynamic heads read rows [0, at), the static ones anchor_tokens (the sink's rows, then the
+        newest finished frame's, which commit rewrites in place)."""
+        if self._groups is None:
+            self.anchor_tokens = torch.zeros(self.sink_tokens + self.per_frame, device=dev, dtype=torch.int32)
+            self.anchor_tokens[:self.sink_tokens] = torch.arange(self.sink_tokens, device=dev, dtype=torch.int32)
+            self.place_anchor()
+            groups = []
+            for heads, rows in ((self.dynamic_heads, None), (self.static_heads, self.anchor_tokens)):
+                if heads:
+                    idx = torch.tensor(heads, device=dev, dtype=torch.int32)
+                    groups.append((idx, idx.long(), rows))
+            self._groups = groups
+        return self._groups
+
+    def attend_split(self, Q, K, V, at: int, n: int):
+        """Forcing-KV over the FP8 cache (causal.py:222-241): each head group attends with its own heads' columns
+        of Q, K, V over the one cache, read through the head map and, for the static heads, the row map (nothing
+        of the cache copied); [1, n, H, D] bf16."""
+        from wdl.sage_kv import attend
+
+        A = torch.empty(Q.shape, device=Q.device, dtype=torch.bfloat16)
+        for idx, cols, rows in self._head_groups(Q.device):
+            length = at if rows is None else rows.numel()
+            A[:, :, cols] = attend(Q[:, :, cols].contiguous(), self.k, self.ks, self.v, self.vs, length,
+                                   K[:, :, cols].contiguous(), V[:, :, cols].contiguous(),
+                                   sm_scale=self.scale(length + n, Q.shape[-1]), heads=idx, tokens=rows)
+        return A
+
+    def anchor_rows(self) -> list[int]:
+        """The cache rows of the newest finished frame, in decreasing token order (the largest frame and place of
+        the ring first, as torch.topk ranks them in the reference, causal.py:243-248)."""
+        newest = self.queue.frames[-1][1] if self.queue.frames else []
+        return [self.sink_tokens + s for s in reversed(newest)]
+
+    def place_anchor(self):
+        """The newest finished frame's rows into anchor_tokens after the sink, in place (a captured graph reads
+        them)."""
+        rows = self.anchor_rows()
+        if len(rows) != self.per_frame:
+            raise RuntimeError(f"the newest frame holds {len(rows)} ring tokens, a frame has {self.per_frame}")
+        self.anchor_tokens[self.sink_tokens:] = torch.tensor(rows, dtype=torch.int32).to(self.anchor_tokens.device)
 
     def commit(self):
         """Keeps the chunk that attend last wrote at row `saved` (causal.py:297-327, without turns, decay or
@@ -192,6 +254,8 @@ class KVCache:
         else:
             self.last_slots = None
         self.frames += self.chunk
+        if self._groups is not None and self.max_tokens > sink and self.full():  # anchors are read when full
+            self.place_anchor()
         self._refresh_stats()  # rows [0, saved) changed
 
     def _move_rows(self, at: int, n: int, slots: list[int]):
