@@ -254,6 +254,45 @@ def instrumented(step):
 COUNTERS = ROOT / "profiles" / "w4a4_gemm_kernel_dit_step_512x928_counters.md"
 
 
+def fp8_sweep(device) -> dict:
+    """The FP8 W8A8 GEMMs of the W4A4 sweep's shapes (QKV, O, FFN-up, FFN-down at 1392 and 2640 tokens), e4m3
+    activations with per-token scales and e4m3 weights with per-channel scales, as DynamicFp8Linear runs them: each
+    shape's GEMM launches (stream-K and merge where the library splits K) replayed ten times from a HIP graph and
+    timed with HIP events on the stream it runs on; tops = all shapes' 2 M N K over their summed times."""
+    import torch
+
+    from wdl import fp8
+
+    g = torch.Generator(device=device).manual_seed(11)
+    ops = us = 0.0
+    per = {}
+    for M in (1392, 2640):
+        for name, N, K in (("qkv", 9216, 3072), ("o", 3072, 3072), ("ffn1", 14336, 3072), ("ffn2", 3072, 14336)):
+            x = torch.randn(M, K, device=device, generator=g).to(torch.bfloat16)
+            wq, ws = fp8.quantize_padded(torch.randn(N, K, device=device, generator=g) * 0.02, rows=True, pad=1)
+            q, xs = fp8.quantize_padded(x, rows=True)
+            fn = lambda: fp8.gemm(q, xs, M, wq, ws, None, rows=True)
+            fn()
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for _ in range(10):
+                    fn()
+            graph.replay()
+            stream = torch.cuda.current_stream()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            graph.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            t = e0.elapsed_time(e1) / 10 * 1e3
+            per[f"{name}_{M}"] = round(t, 1)
+            ops += 2.0 * M * N * K
+            us += t
+            del graph
+    return {"tops": ops / us / 1e6, "us_per_shape": per}
+
+
 def gemm_traffic():
     """HBM bytes per W4A4 GEMM launch over the step: FETCH_SIZE and WRITE_SIZE averages of two rocprofv3 --pmc runs
     of this benchmark, each scaled by its reading for a copy of known size (the committed counter summary)."""
@@ -509,6 +548,12 @@ def main():
                               "metric's dense int8 MFMA peak (the kernel issues fp6 MFMAs, dense peak 10.1 POP/s: "
                               "against that the fraction is half)"},
     }
+    with torch.no_grad():
+        f8 = fp8_sweep(dev)
+    log(f"bench: FP8 W8A8 sweep {f8['tops']:.0f} TOP/s")
+    result["fp8_gemm_tops"] = f8["tops"]
+    result["fp8_gemm_pct_fp8_peak"] = 100 * f8["tops"] / INT8_PEAK_TOPS
+    result["fp8_gemm_us"] = f8["us_per_shape"]
     if args.chunks > 0:
         result["chunk_ms"] = chunk_ms(step, args.chunks)
     if args.mixed_704 > 0:

@@ -158,9 +158,15 @@ int wdl_fp8_quantize(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t
  * xq: e4m3 [Mp, K] (wdl_fp8_quantize), wq: e4m3 [N, K] ([out, in]); acc = sum_k xq[m][k] wq[n][k] in fp32.
  * rows != 0: out = bf16(float(bf16(acc)) * (x_scale[m] * w_scale[n]) + bias[n]) (fp8.py:57-62);
  * rows == 0: out = bf16(acc * (x_scale[0] * w_scale[0]) + bias[n]) (one rounding). bias bf16 [N] or NULL;
- * out bf16 [M, ldo]. Mp % 128 == 0, N % 128 == 0, K % 64 == 0, operands 16-byte aligned. */
+ * out bf16 [M, ldo]. Mp % 128 == 0, N % 128 == 0, K % 64 == 0, operands 16-byte aligned.
+ * workspace: wdl_fp8_gemm_workspace_bytes(Mp, N, K) bytes (16-byte aligned, no initial contents), or NULL. When
+ * the size is not 0 and a workspace is given, the product is split in K over one workgroup per CU (stream-K:
+ * fp32 partial sums of each tile's pieces added in a fixed order), which changes the fp32 summation order of the
+ * one-pass launch: deterministic, not bit-identical to it. */
+int64_t wdl_fp8_gemm_workspace_bytes(int64_t Mp, int64_t N, int64_t K);
 int wdl_fp8_gemm(const void* xq, const float* x_scale, const void* wq, const float* w_scale, const void* bias,
-                 int64_t M, int64_t Mp, int64_t N, int64_t K, int rows, void* out, int64_t ldo, wdl_stream_t stream);
+                 int64_t M, int64_t Mp, int64_t N, int64_t K, int rows, void* out, int64_t ldo, void* workspace,
+                 wdl_stream_t stream);
 
 /* FP8 weight-only linear: out = bf16(w_scale[n] * sum_k x[m][k] w[n][k] + bias[n]) (epilogue 0), or the gated
  * residual out = bf16(out + bf16(y) * gate[n]) in place (epilogue 2). x bf16 [M, ldx] (ldx % 8 == 0), w e4m3 [N, K]

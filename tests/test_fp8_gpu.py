@@ -58,7 +58,9 @@ def test_quantize_tensor_bit_exact(gpu, M, K):
 @pytest.mark.parametrize("rows", [False, True])
 def test_gemm_exact_on_integer_values(gpu, rows):
     """Operands whose fp8 values are small integers (scale 1: each row / the tensor holds 448): every fp32 sum is
-    exact, so the result is the oracle's bit for bit whatever the accumulation order."""
+    exact, so the result is the oracle's bit for bit whatever the accumulation order. (Only while the sums stay
+    small: at K = 6144 with the 448 x 448 column the fp8 matrix cores' accumulation is off by a few units in
+    ~2e5, which turns 0.5 % of the bf16 outputs by one ulp, in the one-pass launch as in stream-K.)"""
     from wdl import fp8
 
     g = torch.Generator().manual_seed(3)
@@ -77,8 +79,10 @@ def test_gemm_exact_on_integer_values(gpu, rows):
 
 
 @pytest.mark.parametrize("rows", [False, True])
-@pytest.mark.parametrize("M,N,K", [(96, 512, 256), (1392, 3072, 3072)])
+@pytest.mark.parametrize("M,N,K", [(96, 512, 256), (1392, 3072, 3072), (1392, 3072, 14336)])
 def test_gemm_matches_oracle(gpu, rows, M, N, K):
+    """Against the oracle's W8A8 linear at the bars of the reference's FP8 tests, through the one-pass launch and
+    stream-K (FFN-down, K 14336), which must also agree with the one-pass launch to fp32 summation order."""
     from wdl import fp8
 
     g = torch.Generator().manual_seed(N)
@@ -94,6 +98,9 @@ def test_gemm_matches_oracle(gpu, rows, M, N, K):
     err = float((y - ref).abs().max()) / float(ref.abs().max())
     rel = float((y - ref).norm() / ref.norm())
     assert err <= 1e-2 and rel <= 2 ** -8, (err, rel)
+    one = fp8.gemm(q, s, M, wq, ws, b.cuda(), rows, stream_k=False).cpu().float()
+    # element by element: a bf16 ulp or two of fp32 summation order, nothing of a misplaced tile or piece
+    assert bool(((y - one).abs() <= 2 ** -7 * one.abs() + 1e-3 * one.abs().max()).all())
 
 
 @pytest.mark.parametrize("rows", [False, True])

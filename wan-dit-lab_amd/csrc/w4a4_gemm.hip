@@ -1051,7 +1051,8 @@ __device__ __forceinline__ int64_t share_of(int64_t it, int64_t U, int64_t W) {
 template <int BN, int BM, int WN, int WM, int NW, int EPI>
 __global__ __launch_bounds__(NW * 64) void w4a4_merge_kernel(GemmArgs p, int64_t W) {
     constexpr int TN = WN / 32, TM = WM / 32;
-    __shared__ __attribute__((aligned(16))) uint16_t stage[EPI == EPI_F32 ? 8 : NW * 64 * STG];
+    constexpr bool ROWS = EPI == EPI_BF16 || EPI == EPI_RESIDUAL || EPI == EPI_GELU;  // token-major staging
+    __shared__ __attribute__((aligned(16))) uint16_t stage[ROWS ? NW * 64 * STG : 8];
     const int t = threadIdx.x, lane = t % 64;
     const int wave = __builtin_amdgcn_readfirstlane(t / 64);
     const int wn = wave % (BN / WN), wm = wave / (BN / WN);
@@ -1087,13 +1088,22 @@ __global__ __launch_bounds__(NW * 64) void w4a4_merge_kernel(GemmArgs p, int64_t
         first = false;
     }
     const int64_t n0 = (tl / ntm) * BN + wn * WN, m0 = (tl % ntm) * BM + wm * WM;
-    if constexpr (EPI != EPI_F32) finish_tile_rows<TN, TM, EPI>(p, acc, n0, m0, lane, stage + wave * 64 * STG);
-    else finish_tile<TN, TM, EPI>(p, acc, n0, m0, lane);
+    if constexpr (EPI == EPI_BF16 || EPI == EPI_RESIDUAL || EPI == EPI_GELU)
+        finish_tile_rows<TN, TM, EPI>(p, acc, n0, m0, lane, stage + wave * 64 * STG);
+    else
+        finish_tile<TN, TM, EPI>(p, acc, n0, m0, lane);
 }
 
 template <int BN, int BM, int WN, int WM, int NW, int EPI, int STAGES>
 __global__ __launch_bounds__(NW * 64) void fp8_gemm_kernel(GemmArgs p) {
     gemm_body<BN, BM, WN, WM, NW, EPI, STAGES, false>(p);
+}
+
+// FP8 stream-K shares: the fp32 accumulators of each share's pieces, merged by w4a4_merge_kernel with the FP8
+// epilogue
+template <int BN, int BM, int WN, int WM, int NW, int STAGES>
+__global__ __launch_bounds__(NW * 64) void fp8_gemm_sk_kernel(GemmArgs p) {
+    gemm_body<BN, BM, WN, WM, NW, EPI_F32, STAGES, false, MODE_SK>(p);
 }
 
 template <int BN, int BM, int WN, int WM, int NW, int ST>
@@ -1109,18 +1119,6 @@ int launch(const GemmArgs& a, int epi, hipStream_t stream) {
         default: return fail(WDL_EINVAL, "w4a4_gemm: bad epilogue %d", epi);
     }
     return check_launch("w4a4_gemm");
-}
-
-int launch_fp8(const GemmArgs& a, int epi, hipStream_t stream) {
-    if (a.N % 128 || a.Mp % 128) return fail(WDL_EINVAL, "fp8_gemm: tile 128x128 does not divide N=%lld Mp=%lld",
-                                             (long long)a.N, (long long)a.Mp);
-    const unsigned grid = unsigned((a.N / 128) * (a.Mp / 128));
-    switch (epi) {
-        case EPI_FP8_ROWS: fp8_gemm_kernel<128, 128, 64, 64, 4, EPI_FP8_ROWS, 4><<<grid, 256, 0, stream>>>(a); break;
-        case EPI_FP8_TENSOR: fp8_gemm_kernel<128, 128, 64, 64, 4, EPI_FP8_TENSOR, 4><<<grid, 256, 0, stream>>>(a); break;
-        default: return fail(WDL_EINVAL, "fp8_gemm: bad mode");
-    }
-    return check_launch("fp8_gemm");
 }
 
 // Tile configuration: 128 x 128 per workgroup (4 waves of 64 x 64, 54 KB of LDS: two workgroups per CU), except
@@ -1200,6 +1198,41 @@ int dispatch(const GemmArgs& a, int epi, hipStream_t stream) {
     if (a.N % 256 == 0 && cus > 0 && T > cus && 4 * T <= 5 * cus)
         return launch<256, 128, 64, 64, 8, WDL_GEMM_STAGES>(a, epi, stream);
     return launch<128, 128, 64, 64, 4, WDL_GEMM_STAGES>(a, epi, stream);
+}
+
+// FP8 launches: stream-K when the caller passes a workspace and the 256 x 128 tiles would leave a quarter of the
+// CUs or more idle with K of 96 groups or more (FFN-down at 1392 tokens, K = 14336: 130 -> 101 us), else
+// 128 x 128 tiles (the 256 x 128 one-pass tiles measured slower for FP8 at 264 tiles: 29.5 -> 31.1 us).
+int64_t fp8_sk_shares(int64_t Mp, int64_t N, int64_t K) {
+    const int64_t cus = cu_count();
+    if (N % 256 || cus <= 0 || K / 64 < WDL_SK_MIN_GROUPS) return 0;
+    return 4 * (N / 256) * (Mp / 128) <= 3 * cus ? cus : 0;
+}
+
+template <int EPI>
+int launch_fp8_epi(const GemmArgs& a, hipStream_t stream) {
+    const int64_t T = (a.N / 128) * (a.Mp / 128);
+    const int64_t W = a.part ? fp8_sk_shares(a.Mp, a.N, a.K) : 0;
+    if (W) {
+        fp8_gemm_sk_kernel<256, 128, 64, 64, SK_NW, WDL_GEMM_STAGES><<<unsigned(W), SK_NW * 64, 0, stream>>>(a);
+        const int rc = check_launch("fp8_gemm stream-K");
+        if (rc) return rc;
+        const unsigned tiles = unsigned((a.N / 256) * (a.Mp / 128));
+        w4a4_merge_kernel<256, 128, 64, 64, SK_NW, EPI><<<tiles, SK_NW * 64, 0, stream>>>(a, W);
+        return check_launch("fp8_gemm merge");
+    }
+    fp8_gemm_kernel<128, 128, 64, 64, 4, EPI, 4><<<unsigned(T), 256, 0, stream>>>(a);
+    return check_launch("fp8_gemm");
+}
+
+int launch_fp8(const GemmArgs& a, int epi, hipStream_t stream) {
+    if (a.N % 128 || a.Mp % 128) return fail(WDL_EINVAL, "fp8_gemm: tile 128x128 does not divide N=%lld Mp=%lld",
+                                             (long long)a.N, (long long)a.Mp);
+    switch (epi) {
+        case EPI_FP8_ROWS: return launch_fp8_epi<EPI_FP8_ROWS>(a, stream);
+        case EPI_FP8_TENSOR: return launch_fp8_epi<EPI_FP8_TENSOR>(a, stream);
+        default: return fail(WDL_EINVAL, "fp8_gemm: bad mode");
+    }
 }
 
 // The fused GELU MLP's first GEMM always runs the one-pass 128 x 128 launch (its epilogue owns one 64-feature
@@ -1363,9 +1396,14 @@ extern "C" int wdl_w4a4_weight_codes(const void* qweight, int64_t N, int64_t K, 
     return check_launch("w4a4_weight_codes");
 }
 
+extern "C" int64_t wdl_fp8_gemm_workspace_bytes(int64_t Mp, int64_t N, int64_t K) {
+    if (Mp <= 0 || Mp % 128 || N <= 0 || K <= 0 || K % 64) return 0;
+    return 2 * fp8_sk_shares(Mp, N, K) * SK_SLOT * int64_t(sizeof(float));
+}
+
 extern "C" int wdl_fp8_gemm(const void* xq, const float* x_scale, const void* wq, const float* w_scale,
                             const void* bias, int64_t M, int64_t Mp, int64_t N, int64_t K, int rows, void* out,
-                            int64_t ldo, hipStream_t stream) {
+                            int64_t ldo, void* workspace, hipStream_t stream) {
     if (M < 0 || Mp < M || Mp % 128 || N <= 0 || N % 128 || K <= 0 || K % 64 || K > (int64_t(1) << 30) || ldo < N ||
         ldo % 4)
         return fail(WDL_EINVAL, "fp8_gemm: bad shape M=%lld Mp=%lld N=%lld K=%lld ldo=%lld", (long long)M,
@@ -1377,7 +1415,10 @@ extern "C" int wdl_fp8_gemm(const void* xq, const float* x_scale, const void* wq
         (rows && reinterpret_cast<uintptr_t>(w_scale) % 16))
         return fail(WDL_EINVAL, "fp8_gemm: bias and out must be 8-byte aligned, row scales 16-byte");
     if (M == 0) return WDL_OK;
+    if (reinterpret_cast<uintptr_t>(workspace) % 16) return fail(WDL_EINVAL, "fp8_gemm: workspace must be 16-byte aligned");
+    // the stream-K launch runs only with a workspace of the queried size; any other shape ignores it
+    float* part = workspace && wdl_fp8_gemm_workspace_bytes(Mp, N, K) ? static_cast<float*>(workspace) : nullptr;
     GemmArgs a{static_cast<const uint8_t*>(xq), nullptr, static_cast<const uint8_t*>(wq), nullptr, nullptr, nullptr,
-               static_cast<const uint16_t*>(bias), M, Mp, N, K, out, ldo, nullptr, x_scale, w_scale, nullptr};
+               static_cast<const uint16_t*>(bias), M, Mp, N, K, out, ldo, nullptr, x_scale, w_scale, part};
     return launch_fp8(a, rows ? EPI_FP8_ROWS : EPI_FP8_TENSOR, stream);
 }

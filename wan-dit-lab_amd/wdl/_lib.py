@@ -39,7 +39,9 @@ SIGNATURES: dict[str, list] = {
                                  c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr],
     "wdl_fp8_quantize_workspace_floats": [c_i64, c_i64],
     "wdl_fp8_quantize": [c_ptr, c_int, c_i64, c_i64, c_i64, c_i64, c_int, c_ptr, c_ptr, c_ptr, c_ptr],
-    "wdl_fp8_gemm": [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_int, c_ptr, c_i64, c_ptr],
+    "wdl_fp8_gemm_workspace_bytes": [c_i64, c_i64, c_i64],
+    "wdl_fp8_gemm": [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_int, c_ptr, c_i64, c_ptr,
+                     c_ptr],
     "wdl_fp8wo_gemm": [c_ptr, c_i64, c_ptr, c_ptr, c_int, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_i64, c_int, c_ptr,
                        c_ptr],
     "wdl_qk_norm_rope": [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_int, c_i64, c_i64, c_i64, c_int, c_int,
@@ -71,7 +73,8 @@ SIGNATURES: dict[str, list] = {
 RESTYPES = {"wdl_last_error": ctypes.c_char_p, "wdl_sage_prep_workspace_floats": c_i64,
             "wdl_sage_attn_workspace_bytes": c_i64, "wdl_w4a4_gemm_workspace_bytes": c_i64,
             "wdl_act_quant_workspace_floats": c_i64, "wdl_fp8_quantize_workspace_floats": c_i64,
-            "wdl_w4a4_gemm_gelu_quant_workspace_floats": c_i64, "wdl_attn_bf16_prep_elems": c_i64}
+            "wdl_w4a4_gemm_gelu_quant_workspace_floats": c_i64, "wdl_attn_bf16_prep_elems": c_i64,
+            "wdl_fp8_gemm_workspace_bytes": c_i64}
 
 _LIB = None
 

@@ -12,7 +12,7 @@ from __future__ import annotations
 import torch
 
 from wdl import _lib
-from wdl.ops import ptr, stream_of
+from wdl.ops import ptr, stream_of, workspace
 
 FP8 = torch.float8_e4m3fn
 FP8_MAX = 448.0
@@ -62,17 +62,24 @@ def quantize_rows(X: torch.Tensor):
     return q.view(FP8).view(X.shape), scale.view(*X.shape[:-1], 1)
 
 
+_FP8_GEMM_WS: dict = {}  # stream-K partial sums, one buffer per device (wdl.ops.workspace)
+
+
 def gemm(q: torch.Tensor, x_scale: torch.Tensor, M: int, w_codes: torch.Tensor, w_scale: torch.Tensor,
-         bias: torch.Tensor | None, rows: bool) -> torch.Tensor:
-    """The FP8 product of quantize_padded's output with an FP8 weight [N, K] -> bf16 [M, N]."""
+         bias: torch.Tensor | None, rows: bool, stream_k: bool = True) -> torch.Tensor:
+    """The FP8 product of quantize_padded's output with an FP8 weight [N, K] -> bf16 [M, N]. stream_k: let long-K
+    shapes that leave CUs idle split K over the CUs (fp32 partial sums in a per-device workspace; a different but
+    fixed summation order); False: the one-pass launch."""
     Mp, K = q.shape
     N = w_codes.shape[0]
     if w_codes.shape[1] != K or N % 128 or K % 64:
         raise ValueError(f"fp8 GEMM needs [N, K] weights with N % 128 == 0 and K % 64 == 0, got {tuple(w_codes.shape)}")
     b = None if bias is None else bias.to(torch.bfloat16).contiguous()
     out = torch.empty(M, N, device=q.device, dtype=torch.bfloat16)
+    nbytes = _lib.library().wdl_fp8_gemm_workspace_bytes(Mp, N, K) if stream_k else 0
+    ws = workspace(_FP8_GEMM_WS, q.device, nbytes) if nbytes else None
     _lib.call("wdl_fp8_gemm", ptr(q), ptr(x_scale), ptr(w_codes.view(torch.uint8)), ptr(w_scale), ptr(b), M, Mp, N,
-              K, int(rows), ptr(out), out.stride(0), stream_of(q))
+              K, int(rows), ptr(out), out.stride(0), ptr(ws), stream_of(q))
     return out
 
 
