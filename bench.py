@@ -453,6 +453,8 @@ def main():
     ap.add_argument("--switch", action="store_true",
                     help="with --mixed-704: then switch to 512x928 mid-stream (window re-encoded) and stream C more "
                          "chunks")
+    ap.add_argument("--no-fp8-sweep", action="store_true",
+                    help="skip the FP8 W8A8 GEMM sweep (fp8_gemm_tops), e.g. for a kernel trace of the step alone")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain elementwise copy of MIB MiB (bitwise_not, uint8) three times: the "
                          "known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -548,12 +550,13 @@ def main():
                               "metric's dense int8 MFMA peak (the kernel issues fp6 MFMAs, dense peak 10.1 POP/s: "
                               "against that the fraction is half)"},
     }
-    with torch.no_grad():
-        f8 = fp8_sweep(dev)
-    log(f"bench: FP8 W8A8 sweep {f8['tops']:.0f} TOP/s")
-    result["fp8_gemm_tops"] = f8["tops"]
-    result["fp8_gemm_pct_fp8_peak"] = 100 * f8["tops"] / INT8_PEAK_TOPS
-    result["fp8_gemm_us"] = f8["us_per_shape"]
+    if not args.no_fp8_sweep:
+        with torch.no_grad():
+            f8 = fp8_sweep(dev)
+        log(f"bench: FP8 W8A8 sweep {f8['tops']:.0f} TOP/s")
+        result["fp8_gemm_tops"] = f8["tops"]
+        result["fp8_gemm_pct_fp8_peak"] = 100 * f8["tops"] / INT8_PEAK_TOPS
+        result["fp8_gemm_us"] = f8["us_per_shape"]
     if args.chunks > 0:
         result["chunk_ms"] = chunk_ms(step, args.chunks)
     if args.mixed_704 > 0:
