@@ -56,15 +56,17 @@ def test_quantize_tensor_bit_exact(gpu, M, K):
 
 
 @pytest.mark.parametrize("rows", [False, True])
-def test_gemm_exact_on_integer_values(gpu, rows):
+@pytest.mark.parametrize("M,N", [(200, 256), (1392, 9216)])
+def test_gemm_exact_on_integer_values(gpu, rows, M, N):
     """Operands whose fp8 values are small integers (scale 1: each row / the tensor holds 448): every fp32 sum is
     exact, so the result is the oracle's bit for bit whatever the accumulation order. (Only while the sums stay
     small: at K = 6144 with the 448 x 448 column the fp8 matrix cores' accumulation is off by a few units in
-    ~2e5, which turns 0.5 % of the bf16 outputs by one ulp, in the one-pass launch as in stream-K.)"""
+    ~2e5, which turns 0.5 % of the bf16 outputs by one ulp, in the one-pass launch as in stream-K.) 1392 x 9216
+    runs the wide 256 x 128 tiles (396 of them), 200 x 256 the 128 x 128 ones."""
     from wdl import fp8
 
     g = torch.Generator().manual_seed(3)
-    M, N, K = 200, 256, 512
+    K = 512
     x = torch.randint(-3, 4, (M, K), generator=g).float()
     w = torch.randint(-3, 4, (N, K), generator=g).float()
     x[:, 0] = 448.0
@@ -79,10 +81,11 @@ def test_gemm_exact_on_integer_values(gpu, rows):
 
 
 @pytest.mark.parametrize("rows", [False, True])
-@pytest.mark.parametrize("M,N,K", [(96, 512, 256), (1392, 3072, 3072), (1392, 3072, 14336)])
+@pytest.mark.parametrize("M,N,K", [(96, 512, 256), (1392, 3072, 3072), (1392, 9216, 1024), (1392, 3072, 14336)])
 def test_gemm_matches_oracle(gpu, rows, M, N, K):
-    """Against the oracle's W8A8 linear at the bars of the reference's FP8 tests, through the one-pass launch and
-    stream-K (FFN-down, K 14336), which must also agree with the one-pass launch to fp32 summation order."""
+    """Against the oracle's W8A8 linear at the bars of the reference's FP8 tests, through the 128 x 128 tiles, the
+    wide 256 x 128 tiles (1392 x 9216) and stream-K (FFN-down, K 14336), which must also agree with the one-pass
+    launch to fp32 summation order."""
     from wdl import fp8
 
     g = torch.Generator().manual_seed(N)

@@ -627,7 +627,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
     constexpr int LPG = W4 ? N16 + N4 + 1 : XI + WI;  // loads per wave per group (W4: + one 4-byte load of scales)
     constexpr int SD = NW * 256;           // scale bytes loaded per stage (ws[BN] pairs, as[BM], then padding)
     constexpr int SB = SD + 256;           // + 128 zero bytes (rounded up) read by lanes 32..63
-    static_assert(4 * BN + 2 * BM <= SD, "scale stage");
+    static_assert(!W4 || 4 * BN + 2 * BM <= SD, "scale stage");
     __shared__ __attribute__((aligned(1024))) uint8_t sX[W4 ? 1 : STAGES][W4 ? 16 : BM * 64];
     __shared__ __attribute__((aligned(1024))) uint8_t sW[W4 ? 1 : STAGES][W4 ? 16 : BN * 64];
     __shared__ __attribute__((aligned(1024))) uint8_t sC[W4 ? KS * STAGES : 1][W4 ? CS : 16];
@@ -1200,9 +1200,16 @@ int dispatch(const GemmArgs& a, int epi, hipStream_t stream) {
     return launch<128, 128, 64, 64, 4, WDL_GEMM_STAGES>(a, epi, stream);
 }
 
-// FP8 launches: stream-K when the caller passes a workspace and the 256 x 128 tiles would leave a quarter of the
-// CUs or more idle with K of 96 groups or more (FFN-down at 1392 tokens, K = 14336: 130 -> 101 us), else
-// 128 x 128 tiles (the 256 x 128 one-pass tiles measured slower for FP8 at 264 tiles: 29.5 -> 31.1 us).
+// FP8 launches. The fp8 products carry no per-group fold, so the accumulators can take a wave tile of 128 x 64
+// (8 subtiles, 128 accumulator registers; the compiler keeps part of the set in AGPRs) with one workgroup of 4 waves
+// per CU on a 256 x
+// 128 tile, which halves the LDS fragment reads per MFMA of the 64 x 64 wave tile (6 fragments for 8 MFMAs
+// against 4 for 4). That wide tile runs whenever N % 256 == 0 and its tiles fill at least 15/16 of the CUs
+// (A/B on one box, two runs each, 2640 tokens: QKV 114 -> 106 us, o 39.9 -> 36.9, FFN-up 191 -> 167, FFN-down
+// 162 -> 143 us; 1392 tokens: QKV 70.7 -> 67.8 us, FFN-up unchanged); below that (o at 1392 tokens: 132 wide tiles)
+// the 128 x 128 tiles of two workgroups per CU keep every CU busy and are faster (29.0 against 31.3 us). Stream-K
+// when the caller passes a workspace and the 256 x 128 tiles would leave a quarter of the CUs or more idle with K
+// of 96 groups or more (FFN-down at 1392 tokens, K = 14336: 130 -> 101 us).
 int64_t fp8_sk_shares(int64_t Mp, int64_t N, int64_t K) {
     const int64_t cus = cu_count();
     if (N % 256 || cus <= 0 || K / 64 < WDL_SK_MIN_GROUPS) return 0;
@@ -1212,14 +1219,18 @@ int64_t fp8_sk_shares(int64_t Mp, int64_t N, int64_t K) {
 template <int EPI>
 int launch_fp8_epi(const GemmArgs& a, hipStream_t stream) {
     const int64_t T = (a.N / 128) * (a.Mp / 128);
-    const int64_t W = a.part ? fp8_sk_shares(a.Mp, a.N, a.K) : 0;
-    if (W) {
+    const int64_t W = a.part ? fp8_sk_shares(a.Mp, a.N, a.K) : 0, cus = cu_count();
+    if (W) {  // the 8-wave shares of the W4A4 stream-K (the wide tile's shares measured slower: 100 -> 104 us)
         fp8_gemm_sk_kernel<256, 128, 64, 64, SK_NW, WDL_GEMM_STAGES><<<unsigned(W), SK_NW * 64, 0, stream>>>(a);
         const int rc = check_launch("fp8_gemm stream-K");
         if (rc) return rc;
         const unsigned tiles = unsigned((a.N / 256) * (a.Mp / 128));
         w4a4_merge_kernel<256, 128, 64, 64, SK_NW, EPI><<<tiles, SK_NW * 64, 0, stream>>>(a, W);
         return check_launch("fp8_gemm merge");
+    }
+    if (a.N % 256 == 0 && cus > 0 && 16 * (T / 2) >= 15 * cus) {
+        fp8_gemm_kernel<256, 128, 128, 64, 4, EPI, 4><<<unsigned(T / 2), 256, 0, stream>>>(a);
+        return check_launch("fp8_gemm");
     }
     fp8_gemm_kernel<128, 128, 64, 64, 4, EPI, 4><<<unsigned(T), 256, 0, stream>>>(a);
     return check_launch("fp8_gemm");
