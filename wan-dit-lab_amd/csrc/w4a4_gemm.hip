@@ -624,8 +624,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
     constexpr int CS = (BN + BM) * ROW6, CB = CS / NW;
     constexpr int N16 = W4 ? CB / 1024 : 0, N4 = W4 ? CB % 1024 / 256 : 0;
     static_assert(!W4 || (CS % NW == 0 && CB % 256 == 0), "fp6 stage vs waves");
-    constexpr int LPG = W4 ? N16 + N4 + 1 : XI + WI;  // loads per wave per group (W4: + one 4-byte load of scales)
-    constexpr int SD = NW * 256;           // scale bytes loaded per stage (ws[BN] pairs, as[BM], then padding)
+    // W4: SL 4-byte loads of scales per wave (256 bytes each): ws[BN] pairs, as[BM], then padding
+    constexpr int SL = W4 ? (4 * BN + 2 * BM + NW * 256 - 1) / (NW * 256) : 0;
+    constexpr int LPG = W4 ? N16 + N4 + SL : XI + WI;  // loads per wave per group
+    constexpr int SD = NW * 256 * (SL > 1 ? SL : 1);   // scale bytes loaded per stage
     constexpr int SB = SD + 256;           // + 128 zero bytes (rounded up) read by lanes 32..63
     static_assert(!W4 || 4 * BN + 2 * BM <= SD, "scale stage");
     __shared__ __attribute__((aligned(1024))) uint8_t sX[W4 ? 1 : STAGES][W4 ? 16 : BM * 64];
@@ -721,19 +723,22 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
                 wsrc[j] = p.wc + (n0 + row) * K + quarter * 16 + int64_t(g0) * 64;
             }
         }
-        const uint8_t* sbase;   // the wave's 256 scale bytes of group g0: ws, as or (padding waves) a valid dummy
-        int64_t sstride;
-        {
-            const int b = 256 * wave;
+        // the wave's SL chunks of 256 scale bytes of group g0 (chunk c = wave SL + u at byte 256 c of the stage): ws,
+        // as or (padding) a valid dummy
+        const uint8_t* sbase[SL > 0 ? SL : 1];
+        int64_t sstride[SL > 0 ? SL : 1];
+#pragma unroll
+        for (int u = 0; u < SL; ++u) {
+            const int b = 256 * (wave * SL + u);
             if (b < 4 * BN) {
-                sstride = 4 * p.N;
-                sbase = reinterpret_cast<const uint8_t*>(p.ws + n0) + b + g0 * sstride;
+                sstride[u] = 4 * p.N;
+                sbase[u] = reinterpret_cast<const uint8_t*>(p.ws + n0) + b + g0 * sstride[u];
             } else if (b < 4 * BN + 2 * BM) {
-                sstride = 2 * p.Mp;
-                sbase = reinterpret_cast<const uint8_t*>(p.as + m0) + (b - 4 * BN) + g0 * sstride;
+                sstride[u] = 2 * p.Mp;
+                sbase[u] = reinterpret_cast<const uint8_t*>(p.as + m0) + (b - 4 * BN) + g0 * sstride[u];
             } else {
-                sbase = reinterpret_cast<const uint8_t*>(p.ws + n0);
-                sstride = 0;
+                sbase[u] = reinterpret_cast<const uint8_t*>(p.ws + n0);
+                sstride[u] = 0;
             }
         }
         const uint32_t off16 = uint32_t(lane) * 16, off4 = uint32_t(lane) * 4;
@@ -744,7 +749,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
             if constexpr (W4) {
                 if (u < N16) dma16s(cbase[u] + int64_t(gg) * BLOCK6, off16, lds_addr(C0 + st * CS + cdst[u]));
                 else if (u < N16 + N4) dma4s(cbase[u] + int64_t(gg) * BLOCK6, off4, lds_addr(C0 + st * CS + cdst[u]));
-                else dma4s(sbase + gg * sstride, off4, lds_addr(S0 + st * SB + wave * 256));
+                else dma4s(sbase[u - N16 - N4] + gg * sstride[u - N16 - N4], off4,
+                           lds_addr(S0 + st * SB + (wave * SL + u - N16 - N4) * 256));
             } else {
                 if (u < XI) dma16(xsrc[u] + int64_t(gg) * 64, lds_addr(&sX[st][(wave * XI + u) * 1024]));
                 else dma16(wsrc[u - XI] + int64_t(gg) * 64, lds_addr(&sW[st][(wave * WI + u - XI) * 1024]));
@@ -895,7 +901,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
             static_assert(4 * 2 * 16 * 64 * 4 <= STAGES * CS, "exchange fits in the ring");
             finish_tile_gelu_quant<TN, TM>(p, acc, n0 + wn * WN, m0 + wm * WM, wn, wm, lane,
                                            reinterpret_cast<float*>(&sC[0][0]));
-        } else if constexpr (W4 && EPI != EPI_F32) {
+        } else if constexpr (W4 && EPI != EPI_F32 && TN == 2 && TM == 2) {
             __syncthreads();  // every wave is past its last read of the ring, whose LDS the staging reuses
             static_assert(NW * 64 * STG * 2 <= STAGES * CS, "staging fits in the ring");
             finish_tile_rows<TN, TM, EPI>(p, acc, n0 + wn * WN, m0 + wm * WM, lane,
