@@ -1,7 +1,8 @@
 """The benchmark workloads at their exact shapes, on the HIP path against the oracle:
 
 - the GEMM sweep: every W4A4 shape of a block (QKV 3072 -> 9216, o 3072 -> 3072, FFN-up 3072 -> 14336, FFN-down
-  14336 -> 3072) at 1392 and 2640 tokens, weights N(0, 0.02^2) quantized by the max rule, activations N(0, 1) with 1%
+  14336 -> 3072) at 1392 and 2640 tokens, weights N(0, 0.02^2) quantized by the max rule with fp16 (the sweep's) and
+  bf16 (the reference's) group scales, activations N(0, 1) with 1%
   outlier channels x 20 quantized per token and 64-group, through the launches the library picks (the balanced
   K split for QKV, o and FFN-down at 1392 tokens); the same eight shapes as FP8 linears (per-row scales, the reference's rows mode);
 - the chunk attention: 24 heads, 2640 queries (3 latent frames of 22 x 40), 2640 / 9240 / 18480 keys (the chunk
@@ -33,10 +34,12 @@ def activations(M, K, g):
     return x.to(BF)
 
 
+@pytest.mark.parametrize("sdt", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("M", [1392, 2640])
 @pytest.mark.parametrize("name,N,K", SHAPES)
-def test_w4a4_linear_sweep(gpu, name, N, K, M):
-    """Quantizer + GEMM (low-rank branch, bias) as the product runs them against the oracle's linear: the int4
+def test_w4a4_linear_sweep(gpu, name, N, K, M, sdt):
+    """Quantizer + GEMM (low-rank branch, bias) as the product runs them against the oracle's linear, with the
+    sweep's fp16 weight scales and with the reference's bf16 ones (both reach the GEMM as exact bf16 pairs): the int4
     activations and their scales bit-exact; the fp32 result within the fold's rounding bound, element by element:
     each of the K/64 group steps rounds once (the scale product is exact), by at most 2^-24 of a partial sum that
     is bounded by the absolute sum A = sum_g |as ws I_g| + |low-rank| + |bias| (computed by the oracle from |q|):
@@ -46,7 +49,7 @@ def test_w4a4_linear_sweep(gpu, name, N, K, M):
     g = torch.Generator().manual_seed(M + N + K)
     W = torch.randn(N, K, generator=g) * 0.02
     q, scale = ow.int4_groups(W)
-    t = dict(q=q, wscales=scale.to(BF), proj_down=(torch.randn(K, 32, generator=g) / K ** 0.5).to(BF),
+    t = dict(q=q, wscales=scale.to(sdt), proj_down=(torch.randn(K, 32, generator=g) / K ** 0.5).to(BF),
              proj_up=(torch.randn(N, 32, generator=g) * 0.02).to(BF), smooth=torch.ones(K, dtype=BF),
              bias=(torch.randn(N, generator=g) * 0.02).to(BF))
     x = activations(M, K, g)
