@@ -93,3 +93,40 @@ def test_anchor_rows_are_the_newest_frame_in_topk_order():
         if int((frame_of >= 0).sum()) >= per:
             want = (sink * per + torch.topk(order, per).indices).tolist()
             assert cache.anchor_rows() == want, (c, cache.anchor_rows(), want)
+
+
+def test_evicted_and_copy_have_the_reference_signatures():
+    """KVCache.evicted(n) names the ring slots the next commit takes (oldest frames first, causal.py:329-337) without
+    changing the cache, and KVCache.copy(to, at, n) moves rows [at, at + n) of all four buffers, FP8 as bytes
+    (causal.py:339-343): a full-window commit equals copy(sink + evicted(n), at, n) by hand."""
+    from wdl.kvcache import KVCache
+
+    per, chunk, window, sink = 2, 2, 8, 2
+    n = chunk * per
+    g = torch.Generator().manual_seed(4)
+    a = KVCache((window - chunk) * per, sink * per, chunk=chunk)
+    b = KVCache((window - chunk) * per, sink * per, chunk=chunk)
+    for c in (a, b):
+        c.allocate(torch.zeros(1, n, 1, 4))
+    for _ in range(5):  # past a full window
+        at = a.saved
+        rows = torch.randn(1, n, 1, 4, generator=g) * 50
+        for c in (a, b):
+            c.k[:, at:at + n] = rows.clamp(-448, 448).to(torch.float8_e4m3fn)
+            c.v[:, at:at + n] = (-rows).clamp(-448, 448).to(torch.float8_e4m3fn)
+            c.ks[:, at:at + n] = rows.abs().amax(-1, keepdim=True)
+            c.vs[:, at:at + n] = rows.abs().amin(-1, keepdim=True)
+        if a.full():
+            slots = a.evicted(n)
+            assert torch.equal(a.evicted(n), slots)  # asking twice changes nothing
+            b.copy(sink * per + slots, at, n)
+            a.commit()
+            assert a.last_slots.tolist() == slots.tolist()
+            for x, y in ((a.k, b.k), (a.v, b.v)):
+                assert torch.equal(x[:, :at].view(torch.uint8), y[:, :at].view(torch.uint8))
+            assert torch.equal(a.ks[:, :at], b.ks[:, :at]) and torch.equal(a.vs[:, :at], b.vs[:, :at])
+            b.saved, b.frames = a.saved, a.frames
+            b.queue.frames = [[f, list(s)] for f, s in a.queue.frames]
+        else:
+            a.commit()
+            b.commit()

@@ -245,7 +245,7 @@ class KVCache:
         elif self.max_tokens > sink:
             tokens = list(range(n))
             slots = self.queue.take_oldest(n)
-            self._move_rows(at, n, slots)
+            self.copy([sink + s for s in slots], at, n)
         else:
             tokens = slots = None
         if slots is not None:
@@ -258,11 +258,21 @@ class KVCache:
             self.place_anchor()
         self._refresh_stats()  # rows [0, saved) changed
 
-    def _move_rows(self, at: int, n: int, slots: list[int]):
-        """Device rows [at, at + n) of the four buffers into the rows of ring slots `slots`, one row per token in
-        order; FP8 rows move as bytes."""
+    def evicted(self, n: int) -> torch.Tensor:
+        """Ring indices (long) of the n tokens the next chunk replaces once the window is full, oldest first: the
+        oldest unpinned tokens in video order, then pinned ones (causal.py:329-337). The cache is not changed."""
+        probe = _FrameQueue()
+        probe.frames = [[f, list(slots)] for f, slots in self.queue.frames]
+        probe.pinned = self.queue.pinned
+        return torch.tensor(probe.take_oldest(n), dtype=torch.long)
+
+    def copy(self, to, at: int, n: int):
+        """Rows [at, at + n) of the four buffers to the buffer rows `to` (n indices), one row per token in order;
+        FP8 rows move as bytes (causal.py:339-343)."""
         dev = self.k.device
-        dst = torch.tensor(slots, dtype=torch.long, device=dev) + self.sink_tokens
+        dst = torch.as_tensor(to, dtype=torch.long).to(dev)
+        if dst.numel() != n:
+            raise ValueError(f"copy: {dst.numel()} destination rows for {n} tokens")
         for buf in (self.k, self.v, self.ks, self.vs):
             rows = buf[0].view(torch.uint8) if buf.dtype == FP8 else buf[0]
             rows.index_copy_(0, dst, rows[at:at + n].clone())
