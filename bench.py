@@ -173,57 +173,45 @@ def chunk_ms(step, chunks: int) -> float:
 
 
 def instrumented(step):
-    """One eager step with HIP events around every W4A4 GEMM and attention launch (on the launch stream)."""
+    """The step's W4A4 GEMM and attention launches, timed two ways on the launch stream: HIP events around every
+    launch of one eager step (`events`), and each kind's launches of that step (the same calls on the same
+    buffers) captured into a HIP graph of their own whose replays are timed as a whole (`ms`, kernel time without
+    per-launch event records; the roofline's basis)."""
     import torch
 
     from wdl import ops
 
     rec = {"gemm": [], "attn": []}
+    calls = {"gemm": [], "attn": []}
     orig_gemm, orig_attn, orig_attn16 = ops.gemm_launch, ops.sage_attn_launch, ops.sage_attn_q16_launch
     orig_gq, orig_bf16 = ops.gelu_quant_launch, ops.attn_bf16_launch
 
-    def gemm(q, ascales, lora, qweight, *a, **k):
-        M = a[3]
+    def timed(kind, fn, flops, *a, **k):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        out = orig_gemm(q, ascales, lora, qweight, *a, **k)
+        out = fn(*a, **k)
         e1.record()
-        rec["gemm"].append((e0, e1, 2.0 * M * ops.out_features(qweight) * q.shape[1] * 64))
+        rec[kind].append((e0, e1, flops))
+        calls[kind].append((fn, a, k))
         return out
 
-    def gelu_quant(q, ascales, lora, wcodes, *a, **k):
-        M = a[3]  # (wscales, proj_up, bias, M, smooth2, proj_down2_t)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        out = orig_gq(q, ascales, lora, wcodes, *a, **k)
-        e1.record()
-        rec["gemm"].append((e0, e1, 2.0 * M * ops.out_features(wcodes) * q.shape[1] * 64))
-        return out
+    def gemm(q, ascales, lora, qweight, *a, **k):
+        return timed("gemm", orig_gemm, 2.0 * a[3] * ops.out_features(qweight) * q.shape[1] * 64,
+                     q, ascales, lora, qweight, *a, **k)
+
+    def gelu_quant(q, ascales, lora, wcodes, *a, **k):  # (wscales, proj_up, bias, M, smooth2, proj_down2_t)
+        return timed("gemm", orig_gq, 2.0 * a[3] * ops.out_features(wcodes) * q.shape[1] * 64,
+                     q, ascales, lora, wcodes, *a, **k)
 
     def attn(q_i8, q_scale, prep, L, sm_scale, out=None):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        r = orig_attn(q_i8, q_scale, prep, L, sm_scale, out)
-        e1.record()
         n, H, d = q_i8.shape
-        rec["attn"].append((e0, e1, 4.0 * n * L * d * H))
-        return r
+        return timed("attn", orig_attn, 4.0 * n * L * d * H, q_i8, q_scale, prep, L, sm_scale, out)
 
     def attn_bf16(Q, prep, sm_scale, out=None):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        r = orig_bf16(Q, prep, sm_scale, out)
-        e1.record()
-        rec["attn"].append((e0, e1, 4.0 * Q.shape[0] * prep["L"] * Q.shape[1]))
-        return r
+        return timed("attn", orig_bf16, 4.0 * Q.shape[0] * prep["L"] * Q.shape[1], Q, prep, sm_scale, out)
 
     def attn16(Q, prep, L, sm_scale, out=None):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        r = orig_attn16(Q, prep, L, sm_scale, out)
-        e1.record()
-        rec["attn"].append((e0, e1, 4.0 * Q.shape[0] * L * Q.shape[1]))
-        return r
+        return timed("attn", orig_attn16, 4.0 * Q.shape[0] * L * Q.shape[1], Q, prep, L, sm_scale, out)
 
     ops.gemm_launch, ops.sage_attn_launch, ops.sage_attn_q16_launch = gemm, attn, attn16
     ops.gelu_quant_launch, ops.attn_bf16_launch = gelu_quant, attn_bf16
@@ -245,9 +233,34 @@ def instrumented(step):
         ops.gelu_quant_launch, ops.attn_bf16_launch = orig_gq, orig_bf16
     out = {}
     for name, items in rec.items():
-        ms = sum(a.elapsed_time(b) for a, b, _ in items)
+        ev = sum(a.elapsed_time(b) for a, b, _ in items)
         flops = sum(f for _, _, f in items)
-        out[name] = dict(launches=len(items), ms=ms, tops=flops / (ms * 1e-3) / 1e12 if ms else 0.0)
+        # the same launches as one graph, replayed: kernel time back to back (the launches rewrite their outputs,
+        # the residual GEMMs their residual in place: the values change, the work does not)
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for fn, a, k in calls[name]:
+                fn(*a, **k)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph):
+            for fn, a, k in calls[name]:
+                fn(*a, **k)
+        graph.replay()
+        torch.cuda.synchronize()
+        reps = 5
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        del graph
+        out[name] = dict(launches=len(items), ms=ms, tops=flops / (ms * 1e-3) / 1e12 if ms else 0.0,
+                         events_ms=ev, events_tops=flops / (ev * 1e-3) / 1e12 if ev else 0.0)
     return out
 
 
@@ -539,13 +552,16 @@ def main():
         "gemm_tops": g["tops"],
         "gemm_pct_int8_peak": 100 * gemm_frac,
         "gemm_ms_per_step": g["ms"],
+        "gemm_tops_eager_events": g["events_tops"],
         "attention_tops": a["tops"],
         "attention_pct_int8_peak": 100 * a["tops"] / INT8_PEAK_TOPS,
         "attention_ms_per_step": a["ms"],
         "roofline": {"bound": "mfma", "kernel": "w4a4_gemm_kernel", "achieved": g["tops"], "peak": INT8_PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": gemm_frac, "traffic": gemm_traffic(),
                      "basis": "2*M*N*K int ops per launch (M = 1392 tokens) summed over the step's "
-                              f"{g['launches']} W4A4 GEMM launches / their summed HIP-event durations; traffic = "
+                              f"{g['launches']} W4A4 GEMM launches / the HIP-event time of those launches replayed "
+                              "back to back from a graph of their own (per-launch events around an eager step: "
+                              "gemm_tops_eager_events); traffic = "
                               "calibrated HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE; peak = the "
                               "metric's dense int8 MFMA peak (the kernel issues fp6 MFMAs, dense peak 10.1 POP/s: "
                               "against that the fraction is half)"},
