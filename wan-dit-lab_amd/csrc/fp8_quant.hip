@@ -7,8 +7,8 @@
 // x, the reference's X / scale divides by a 0-d fp32 tensor, which does not promote the bf16 result: the quotient
 // is rounded to bf16 before the e4m3 conversion (the per-row scale [..., 1] does promote: fp32 quotient there).
 //
-// rows:   one wave per row, two passes over it (the maximum, then the codes; the second pass reads the row back
-//         from cache).
+// rows:   one workgroup per row (4 waves from K = 2048 on, else 1), two passes over it (the maximum, then the codes;
+//         the second pass reads the row back from cache), 16 bytes of bf16 per lane and load.
 // tensor: pass 1 writes one partial maximum per workgroup to the workspace; pass 2 has every workgroup reduce
 //         the partials (the same order in each: deterministic) and quantize its share. No atomics, no memory that
 //         has to start zeroed.
@@ -41,51 +41,98 @@ __device__ __forceinline__ uint32_t e4m3x4(const float* y) {
     return __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], w, true);
 }
 
+// 8 consecutive values of a row as floats (one 16-byte load of bf16, two of fp32)
 template <typename T>
-__global__ __launch_bounds__(256) void rows_kernel(const T* x, int64_t ldx, int64_t M, int64_t Mp, int64_t K,
-                                                   uint8_t* q, float* scale) {
-    const int lane = threadIdx.x % 64;
-    const int64_t row = int64_t(blockIdx.x) * 4 + threadIdx.x / 64;
-    if (row >= Mp) return;
-    uint32_t* qr = reinterpret_cast<uint32_t*>(q + row * K);
-    if (row >= M) {
-        for (int64_t c = lane; c < K / 4; c += 64) qr[c] = 0u;
-        if (lane == 0) scale[row] = 0.0f;
+__device__ __forceinline__ void ld8(const T* p, float* f) {
+    ld4<T>(p, f);
+    ld4<T>(p + 4, f + 4);
+}
+template <>
+__device__ __forceinline__ void ld8<uint16_t>(const uint16_t* p, float* f) {
+    const uint4 r = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) f[2 * e] = __uint_as_float(w[e] << 16), f[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+}
+
+// One workgroup of WPR waves per row, 8 values per lane and step, two steps in flight: the row's maximum (lanes,
+// then waves through LDS), then the codes from a second read of the row (from cache). The maximum is
+// order-independent, so the result is the same for any WPR.
+template <typename T, int WPR>
+__global__ __launch_bounds__(64 * WPR) void rows_kernel(const T* x, int64_t ldx, int64_t M, int64_t K, uint8_t* q,
+                                                        float* scale) {
+    __shared__ float red[WPR];
+    const int t = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    constexpr int NT = 64 * WPR;
+    uint2* qr = reinterpret_cast<uint2*>(q + row * K);
+    const int64_t chunks = K / 8;
+    if (row >= M) {  // padding rows of the GEMM tiles: zero codes, zero scale
+        for (int64_t c = t; c < chunks; c += NT) qr[c] = make_uint2(0u, 0u);
+        if (t == 0) scale[row] = 0.0f;
         return;
     }
     const T* xr = x + row * ldx;
     float amax = 0.0f;
-    for (int64_t c = lane; c < K / 4; c += 64) {
-        float f[4];
-        ld4<T>(xr + 4 * c, f);
+    int64_t c = t;
+    for (; c + NT < chunks; c += 2 * NT) {
+        float f[8], g[8];
+        ld8<T>(xr + 8 * c, f);
+        ld8<T>(xr + 8 * (c + NT), g);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(f[e]));
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fmaxf(fabsf(f[e]), fabsf(g[e])));
+    }
+    if (c < chunks) {
+        float f[8];
+        ld8<T>(xr + 8 * c, f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[e]));
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-    const float s = fmaxf(amax, 1e-12f) / FP8_MAX;
-    if (lane == 0) scale[row] = s;
-    for (int64_t c = lane; c < K / 4; c += 64) {
-        float f[4];
-        ld4<T>(xr + 4 * c, f);
+    if (WPR > 1) {
+        if (t % 64 == 0) red[t / 64] = amax;
+        __syncthreads();
+        amax = red[0];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) f[e] = f[e] / s;
-        qr[c] = e4m3x4(f);
+        for (int w = 1; w < WPR; ++w) amax = fmaxf(amax, red[w]);
     }
+    const float s = fmaxf(amax, 1e-12f) / FP8_MAX;
+    if (t == 0) scale[row] = s;
+    auto codes = [&](int64_t cc) {
+        float f[8];
+        ld8<T>(xr + 8 * cc, f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = f[e] / s;
+        qr[cc] = make_uint2(e4m3x4(f), e4m3x4(f + 4));
+    };
+    c = t;
+    for (; c + NT < chunks; c += 2 * NT) {
+        codes(c);
+        codes(c + NT);
+    }
+    if (c < chunks) codes(c);
 }
 
 template <typename T>
 __global__ __launch_bounds__(256) void tensor_max_kernel(const T* x, int64_t ldx, int64_t M, int64_t K,
                                                          float* partial) {
     __shared__ float red[4];
-    const int64_t n4 = M * (K / 4);
+    const int64_t k8 = K / 8, n8 = M * k8, stride = int64_t(gridDim.x) * 256;
     float amax = 0.0f;
-    for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n4; i += int64_t(gridDim.x) * 256) {
-        const int64_t m = i / (K / 4), c = i % (K / 4);
-        float f[4];
-        ld4<T>(x + m * ldx + 4 * c, f);
+    int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    for (; i + stride < n8; i += 2 * stride) {  // two 16-byte loads of bf16 in flight
+        float f[8], g[8];
+        ld8<T>(x + (i / k8) * ldx + 8 * (i % k8), f);
+        ld8<T>(x + ((i + stride) / k8) * ldx + 8 * ((i + stride) % k8), g);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(f[e]));
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fmaxf(fabsf(f[e]), fabsf(g[e])));
+    }
+    if (i < n8) {
+        float f[8];
+        ld8<T>(x + (i / k8) * ldx + 8 * (i % k8), f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[e]));
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
@@ -106,27 +153,33 @@ __global__ __launch_bounds__(256) void tensor_quant_kernel(const T* x, int64_t l
     __syncthreads();
     const float s = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), 1e-12f) / FP8_MAX;
     if (blockIdx.x == 0 && threadIdx.x == 0) scale[0] = s;
-    const int64_t n4 = Mp * (K / 4);
-    for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n4; i += int64_t(gridDim.x) * 256) {
-        const int64_t m = i / (K / 4), c = i % (K / 4);
-        uint32_t w = 0u;
+    const int64_t k8 = K / 8, n8 = Mp * k8, stride = int64_t(gridDim.x) * 256;
+    auto codes = [&](int64_t i) {
+        const int64_t m = i / k8, c = i % k8;
+        uint2 w = make_uint2(0u, 0u);
         if (m < M) {
-            float f[4];
-            ld4<T>(x + m * ldx + 4 * c, f);
+            float f[8];
+            ld8<T>(x + m * ldx + 8 * c, f);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
+            for (int e = 0; e < 8; ++e) {
                 f[e] = f[e] / s;
                 if constexpr (sizeof(T) == 2) f[e] = bf16_to_f32(f32_to_bf16(f[e]));
             }
-            w = e4m3x4(f);
+            w = make_uint2(e4m3x4(f), e4m3x4(f + 4));
         }
-        reinterpret_cast<uint32_t*>(q + m * K)[c] = w;
+        reinterpret_cast<uint2*>(q + m * K)[c] = w;
+    };
+    int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    for (; i + stride < n8; i += 2 * stride) {
+        codes(i);
+        codes(i + stride);
     }
+    if (i < n8) codes(i);
 }
 
 int tensor_blocks(int64_t M, int64_t K) {
-    const int64_t n4 = M * (K / 4);
-    const int64_t b = (n4 + 256 * 8 - 1) / (256 * 8);
+    const int64_t n8 = M * (K / 8);
+    const int64_t b = (n8 + 256 * 4 - 1) / (256 * 4);
     return int(b < 1 ? 1 : (b > TBLOCKS ? TBLOCKS : b));
 }
 
@@ -136,7 +189,8 @@ int quantize(const void* xv, int64_t ldx, int64_t M, int64_t K, int64_t Mp, int 
     const T* x = static_cast<const T*>(xv);
     uint8_t* qb = static_cast<uint8_t*>(q);
     if (rows) {
-        rows_kernel<T><<<unsigned((Mp + 3) / 4), 256, 0, stream>>>(x, ldx, M, Mp, K, qb, scale);
+        if (K >= 2048) rows_kernel<T, 4><<<unsigned(Mp), 256, 0, stream>>>(x, ldx, M, K, qb, scale);
+        else rows_kernel<T, 1><<<unsigned(Mp), 64, 0, stream>>>(x, ldx, M, K, qb, scale);
         return check_launch("fp8_quantize rows");
     }
     const int nb = tensor_blocks(M, K);
