@@ -175,13 +175,14 @@ def test_gemm_scaled_lowrank_bias_matches_oracle(gpu, M, N, K, valid, sdt):
 
 
 @pytest.mark.parametrize("M,N,K,valid", [(1024, 3072, 8192, 1000), (512, 512, 14336, 464), (1408, 3072, 14336, 1392),
-                                         (1408, 3072, 3072, 1392), (1408, 3072, 2048, 1300), (2048, 2048, 1024, 2000),
-                                         (2048, 4096, 3072, 2047)])
+                                         (1408, 3072, 6144, 1392), (1408, 3072, 3072, 1392), (1408, 3072, 2048, 1300),
+                                         (2048, 2048, 1024, 2000), (2048, 4096, 3072, 2047)])
 def test_gemm_split_k_matches_one_pass_and_oracle(gpu, M, N, K, valid):
     """Shapes whose tiles leave CUs idle run split in K when the library asks for a workspace: stream-K + merge
-    (the first three shapes, the last FFN-down at 1392 tokens), or the balanced form on 256 CUs (whole tiles in two
-    K halves; 264 tiles: 8 left over in 128 pieces of 32 x 32, at K = 3072 and 2048; 256 and 512 tiles: none left
-    over, one and two tiles per CU). The result is
+    (the first two shapes), or the balanced form on 256 CUs (whole tiles in two K halves; 264 tiles: 8 left over in
+    128 pieces of 32 x 32, at K = 14336 (FFN-down at 1392 tokens: each wave's 28 groups of a piece in 5 batches),
+    6144 (2 batches), 3072 and 2048 (one batch); 256 and 512 tiles: none left over, one and two tiles per CU). The
+    result is
     deterministic, within fp32 rounding of the one-pass launch, and meets the oracle bar of the one-pass test; gated
     residual epilogue in place, bf16 and GELU outputs one rounding from the fp32 one."""
     from wdl import _lib, ops, w4a4

@@ -543,21 +543,21 @@ __device__ __forceinline__ void finish_tile_gelu_quant(const GemmArgs& p, f32x16
 // streamed with the codes); otherwise the FP8 product (e4m3 row-major codes only, one fp32 accumulation over all
 // of K in the MFMA accumulator).
 // One 32 x 32 piece (features n0 .., tokens m0 ..) summed over all of K by NWT waves: wave v folds the 64-deep
-// groups [v G / NWT, (v + 1) G / NWT) (at most PD) in increasing order with the tiles' arithmetic (the fp6 product,
-// the exact scale product of a bf16 MFMA, one fmaf per element and group). load() reads the wave's operands
-// straight from global memory into registers (the rows as the tiles read them: 16 + 8 bytes of a 48-byte row per
-// lane; lanes 32..63 give the zero k-slots of the scale product); fold() returns the wave's partial sums in the
-// MFMA layout.
+// groups [v G / NWT, (v + 1) G / NWT) in increasing order with the tiles' arithmetic (the fp6 product, the exact
+// scale product of a bf16 MFMA, one fmaf per element and group), in batches of at most PD groups. load() reads a
+// batch's operands straight from global memory into registers (the rows as the tiles read them: 16 + 8 bytes of
+// a 48-byte row per lane; lanes 32..63 give the zero k-slots of the scale product); fold() continues the wave's
+// partial sums in the MFMA layout with the batch's groups.
 template <int NWT, int PD>
 struct Piece {
     u32x6 fa[PD], fb[PD];  // the 6 code dwords of each operand row (the MFMA's 8-dword operand gets 2 zeros)
     uint32_t sa[PD], sb[PD];
-    int n;  // groups of this wave (wave-uniform)
+    int n;  // groups of this batch (wave-uniform)
 
-    __device__ __forceinline__ void load(const GemmArgs& p, int64_t n0, int64_t m0, int v, int lane) {
+    // the groups [gb, gb + cnt) of wave v's range (cnt <= PD; cnt = 0 loads a valid dummy and folds nothing)
+    __device__ __forceinline__ void load(const GemmArgs& p, int64_t n0, int64_t m0, int gb, int cnt, int lane) {
         const int64_t G = p.K / 64;
-        const int gb = int(int64_t(v) * G / NWT);
-        n = int(int64_t(v + 1) * G / NWT) - gb;
+        n = cnt;
         const int half = lane / 32;
         const int64_t nr = n0 + lane % 32, mr = m0 + lane % 32;
         const uint8_t* arow = p.wc + (nr / BLOCK_ROWS) * G * BLOCK6 + (nr % BLOCK_ROWS) * ROW6;
@@ -580,9 +580,8 @@ struct Piece {
         }
     }
 
-    __device__ __forceinline__ f32x16 fold() const {
+    __device__ __forceinline__ f32x16 fold(f32x16 acc) const {
         const f32x16 zero = {};
-        f32x16 acc = zero;
 #pragma unroll
         for (int d = 0; d < PD; ++d) {
             if (d < n) {
@@ -601,7 +600,9 @@ struct Piece {
         return acc;
     }
 };
-constexpr int PIECE_WAVES = 8, PIECE_GROUPS = 6;  // a piece: K of up to 48 groups, in one batch of loads
+// a piece: 8 waves, each folding its share of K in batches of 6 groups (one batch up to K = 48 groups), at most
+// 5 batches (K up to 240 groups)
+constexpr int PIECE_WAVES = 8, PIECE_GROUPS = 6, PIECE_BATCHES = 5;
 
 // How a launch covers the tiles: one tile per workgroup, stream-K shares, or the balanced form (one workgroup of
 // two K-groups per CU, whole tiles dealt evenly, the leftover tiles in 32 x 32 pieces).
@@ -956,9 +957,23 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         const int hg = int(G / 2);
         float4* const R = reinterpret_cast<float4*>(&sC[0][0]) + wave * (TN * TM * 4 * 64) + lane;
         if (piece) {
-            Piece<PIECE_WAVES, PIECE_GROUPS> pc;
-            pc.load(p, pn, pm, wall, lane);
-            const f32x16 part = pc.fold();
+            // wave `wall` folds the groups [gb, ge) in batches, the next batch's loads issued before the current
+            // batch is folded (two register sets)
+            const int gb = int(G * wall / PIECE_WAVES), ge = int(G * (wall + 1) / PIECE_WAVES), ng = ge - gb;
+            auto count = [&](int b) {
+                const int r = ng - b * PIECE_GROUPS;
+                return r < 0 ? 0 : (r < PIECE_GROUPS ? r : PIECE_GROUPS);
+            };
+            Piece<PIECE_WAVES, PIECE_GROUPS> pa, pb;
+            f32x16 part = {};
+            pa.load(p, pn, pm, gb, count(0), lane);
+            for (int b = 0; b * PIECE_GROUPS < ng; b += 2) {
+                const bool more = (b + 1) * PIECE_GROUPS < ng;
+                if (more) pb.load(p, pn, pm, gb + (b + 1) * PIECE_GROUPS, count(b + 1), lane);
+                part = pa.fold(part);
+                if ((b + 2) * PIECE_GROUPS < ng) pa.load(p, pn, pm, gb + (b + 2) * PIECE_GROUPS, count(b + 2), lane);
+                if (more) part = pb.fold(part);
+            }
 #pragma unroll
             for (int f4 = 0; f4 < 4; ++f4)
                 E[(wall * 4 + f4) * 64 + lane] =
@@ -1151,17 +1166,22 @@ constexpr int64_t SK_SLOT = SK_NW * 64 * 2 * 2 * 16;        // floats per partia
 
 // Balanced form (one workgroup of 8 waves per CU: whole 128 x 128 tiles dealt evenly, each summed by two K-groups
 // of 4 waves, the leftover tiles in 32 x 32 pieces): when there is at least one tile per CU, the groups split evenly
-// in two and either no tile is left over or the pieces come to at most one per CU with K of at most 48 groups (a
-// piece's operands in one batch of loads). It takes the shapes whose tile count just exceeds the CU count, where
-// whole-tile launches leave CUs idle: at 1392 tokens, N = 3072, K = 3072 (264 tiles on 256 CUs: o / cross-q /
-// cross-o). Measured there: the K-split tiles alone 24.0 us against 31.7 us for the one-pass 256 x 128 launch; the
-// pieces as a separate phase of three memory round trips cost another 5 us. It needs no memory, but runs (like
-// stream-K) only when the caller passes a workspace: without one every shape takes the one-pass fold.
+// in two and either no tile is left over or the pieces come to at most one per CU with K of at most 240 groups (a
+// wave's share of a piece in at most 5 batches of loads). It takes the shapes whose tile count just exceeds the CU
+// count, where whole-tile launches leave CUs idle: at 1392 tokens, N = 3072 (264 tiles on 256 CUs: o / cross-q /
+// cross-o at K = 3072, FFN-down at K = 14336). Measured at K = 3072: the K-split tiles alone 24.0 us against 31.7
+// us for the one-pass 256 x 128 launch; the pieces as a separate phase of three memory round trips cost another 5
+// us. At K = 14336 it replaces stream-K, whose partial sums and merge launch cost more than the pieces' five
+// batches. It needs no memory, but runs (like stream-K) only when the caller passes a workspace: without one every
+// shape takes the one-pass fold.
+#ifndef WDL_BAL_BATCHES
+#define WDL_BAL_BATCHES PIECE_BATCHES
+#endif
 constexpr int64_t BAL_TOKEN_BYTES = 256;  // the workspace size reported for it
 bool bal_fits(int64_t Mp, int64_t N, int64_t K) {
     const int64_t cus = cu_count(), T = (N / 128) * (Mp / 128), G = K / 64;
     if (cus <= 0 || cus % 8 || G % 2 || T < cus) return false;
-    return T % cus == 0 || (16 * (T % cus) <= cus && G <= PIECE_WAVES * PIECE_GROUPS);
+    return T % cus == 0 || (16 * (T % cus) <= cus && G <= PIECE_WAVES * PIECE_GROUPS * WDL_BAL_BATCHES);
 }
 
 // stream-K workgroups for an M x N x K product (0: plain launch)
