@@ -950,9 +950,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         // a few weight slabs against all row blocks.
         const int64_t W = gridDim.x, c = blockIdx.x, Wx = W / 8;
         const int64_t F = total / W;
-        const bool piece = c < 16 * (total - F * W);  // workgroup-uniform
-        const int64_t ptl = F * W + c / 16;
-        const int64_t pn = (ptl / ntm) * BN + 32 * ((c % 16) / 4), pm = (ptl % ntm) * BM + 32 * (c % 4);
+        // pieces: P = 16 L of them on workgroups c < P; workgroup c runs on XCD c % 8, so piece pc = (c % 8) P / 8 +
+        // c / 8 puts consecutive pieces (the 16 of a leftover tile) on one XCD, whose L2 then holds the tile's
+        // operand rows for all of them
+        const int64_t P = 16 * (total - F * W);
+        const bool piece = c < P;  // workgroup-uniform
+        const int64_t pc = (c % 8) * (P / 8) + c / 8;
+        const int64_t ptl = F * W + pc / 16;
+        const int64_t pn = (ptl / ntm) * BN + 32 * ((pc % 16) / 4), pm = (ptl % ntm) * BM + 32 * (pc % 4);
         float4* const E = reinterpret_cast<float4*>(sE);  // the piece's partial sums, [wave][4][64] float4
         const int hg = int(G / 2);
         float4* const R = reinterpret_cast<float4*>(&sC[0][0]) + wave * (TN * TM * 4 * 64) + lane;
