@@ -235,9 +235,14 @@ __global__ __launch_bounds__(128 * WPG) void attn_bf16_kernel(Args a) {
             for (int e = 0; e < 16; ++e) o[ds][e] = o[ds][e] * a0 + xo[(ds * 16 + e) * 64 + lane] * a1;
     }
     const float lt = l + __shfl_xor(l, 32);  // the two lane halves summed different keys
-    if (!qlive) return;
     const float inv = 1.0f / lt;
-    uint16_t* dst = a.out + q * a.ldo + h * D;
+    // The wave's 32 x 128 bf16 outputs go through its own LDS area (the hand-over slot it has just read, or for a
+    // dual workgroup a slot per wave), rows of 272 bytes, and leave as whole 256-byte query rows: 16 bytes per lane,
+    // four rows per store instead of 32 rows in 8-byte pieces.
+    constexpr int SROW = 136;  // staged row, in bf16 elements (128 + 8 pad)
+    static_assert(32 * SROW * 2 <= (64 * 64 + 128) * 4 && 2 * WPG * 32 * SROW * 2 <= RING * STAGE, "staging fits");
+    uint16_t* stg = dualwg ? reinterpret_cast<uint16_t*>(smem) + (grp * WPG + sub) * 32 * SROW
+                           : reinterpret_cast<uint16_t*>(xo);
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds)
 #pragma unroll
@@ -246,8 +251,16 @@ __global__ __launch_bounds__(128 * WPG) void attn_bf16_kernel(Args a) {
             uint16_t r[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) r[e] = f32_to_bf16(o[ds][4 * g + e] * inv);
-            *reinterpret_cast<uint2*>(dst + d) = make_uint2(r[0] | (uint32_t(r[1]) << 16), r[2] | (uint32_t(r[3]) << 16));
+            *reinterpret_cast<uint2*>(stg + tok * SROW + d) =
+                make_uint2(r[0] | (uint32_t(r[1]) << 16), r[2] | (uint32_t(r[3]) << 16));
         }
+    const int64_t q0 = qt * (32 * WPG) + sub * 32;  // the wave's first query
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int row = 4 * i + lane / 16, c = lane % 16;
+        const uint4 v = *reinterpret_cast<const uint4*>(stg + row * SROW + 8 * c);
+        if (q0 + row < a.n) *reinterpret_cast<uint4*>(a.out + (q0 + row) * a.ldo + h * D + 8 * c) = v;
+    }
 }
 
 // K, V bf16 [L, H, 128] (token strides ldk, ldv) -> Kp, Vp (layouts above). One thread per 16-byte chunk of Kp and
