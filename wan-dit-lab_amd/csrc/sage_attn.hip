@@ -464,10 +464,15 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
         }
 
         // out = O / l * v_scale, bf16; lane half h holds channels 32 ds + 8 g + 4 h + e
+        // The wave's 32 x 128 bf16 outputs go through its own LDS area (the hand-over slot it has just read, or for a
+        // dual workgroup a slot per wave of the ring, which every wave is done with), rows of 272 bytes, and leave as
+        // whole 256-byte query rows: 16 bytes per lane, four rows per store instead of 32 rows in 8-byte pieces.
         auto write_out = [&](const f32x16 (&ov)[4], float lsum) {
-            if (!qlive) return;
             const float inv = 1.0f / lsum;
-            uint16_t* dst = a.out + q * a.ldo + h * D;
+            constexpr int SROW = 136;  // staged row, in bf16 elements (128 + 8 pad)
+            static_assert(32 * SROW * 2 <= (64 * 64 + 128) * 4 && 8 * 32 * SROW * 2 <= STAGES * STAGE, "staging");
+            uint16_t* stg = dualwg ? reinterpret_cast<uint16_t*>(smem) + (grp * 4 + sub) * 32 * SROW
+                                   : reinterpret_cast<uint16_t*>(xo);
 #pragma unroll
             for (int ds = 0; ds < 4; ++ds) {
 #pragma unroll
@@ -476,9 +481,16 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
                     uint16_t r[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) r[e] = f32_to_bf16(ov[ds][4 * g + e] * inv * sVs[d + e]);
-                    *reinterpret_cast<uint2*>(dst + d) =
+                    *reinterpret_cast<uint2*>(stg + (lane % 32) * SROW + d) =
                         make_uint2(r[0] | (uint32_t(r[1]) << 16), r[2] | (uint32_t(r[3]) << 16));
                 }
+            }
+            const int64_t q0 = qt * 128 + sub * 32;  // the wave's first query
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int row = 4 * i + lane / 16, c = lane % 16;
+                const uint4 v = *reinterpret_cast<const uint4*>(stg + row * SROW + 8 * c);
+                if (q0 + row < a.n) *reinterpret_cast<uint4*>(a.out + (q0 + row) * a.ldo + h * D + 8 * c) = v;
             }
         };
 
