@@ -8,8 +8,10 @@
 // e4m3 value is exact in fp32 (8 + 4 significant bits), sums accumulate in fp32, and the per-row scale multiplies
 // the sum once in the epilogue (scale * sum, then + bias, then bf16).
 //
-// Tiles. A workgroup of 4 waves computes a 128 (features) x 128 (tokens) tile, each wave 64 x 64 (2 x 2 subtiles of
-// 32 x 32), so a lane owns one token and 16 features per subtile. K advances 64 per stage through a 3-stage LDS ring
+// Tiles. A workgroup of 4 waves computes a 128 (features) x 128 (tokens) tile, each wave 32 features x 128 tokens
+// (4 subtiles of 32 x 32), so a lane owns one token and 16 features per subtile, and every weight row of the tile is
+// widened by one wave only, once per 16-deep step for four MFMAs (64 x 64 wave tiles widened each row twice, for two
+// MFMAs: 7-11 % slower). K advances 64 per stage through a 3-stage LDS ring
 // fed by direct global->LDS loads (16 bytes per lane, 6 per wave per stage, waited for with an explicit vmcnt):
 //   W stage: [128 rows][64 B] of e4m3, each row's four 16-byte quarters XOR-swizzled by (row / 4) % 4;
 //   X stage: [128 rows][128 B] of bf16, each row's eight 16-byte chunks XOR-swizzled by row % 8,
@@ -75,7 +77,7 @@ __global__ __launch_bounds__(256) void fp8wo_gemm_kernel(Args a) {
 
     const int t = threadIdx.x, lane = t % 64, half = lane / 32, tok = lane % 32;
     const int wave = __builtin_amdgcn_readfirstlane(t / 64);
-    const int wn = wave / 2, wm = wave % 2;
+    const int wn = wave;  // the wave's 32 feature rows of the tile, against all 128 tokens
     const int64_t total = gridDim.x, pid = blockIdx.x;
     const int64_t tile = total % 8 == 0 ? (pid % 8) * (total / 8) + pid / 8 : pid;
     const int64_t n0 = (tile / a.ntm) * BN, m0 = (tile % a.ntm) * BM;
@@ -107,14 +109,12 @@ __global__ __launch_bounds__(256) void fp8wo_gemm_kernel(Args a) {
         for (int i = 0; i < 4; ++i) dma16s(xb, xoff[i], lds_addr(&sX[slot][1024 * (4 * i + wave)]));
     };
 
-    f32x16 acc[2][2];
+    f32x16 acc[4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+    for (int j = 0; j < 4; ++j) acc[j] = f32x16{};
 
-    // fragment rows of this lane: W rows 64 wn + 32 i + tok, X rows 64 wm + 32 j + tok
-    const int wsw = ((tok / 4) % 4), xsw = tok % 8;  // (32 i and 64 wn, 32 j and 64 wm leave both unchanged)
+    // fragment rows of this lane: W row 32 wn + tok, X rows 32 j + tok
+    const int wsw = ((tok / 4) % 4), xsw = tok % 8;  // (32 wn and 32 j leave both unchanged)
     issue(0, 0);
     issue(1, 1);
     for (int g = 0; g < G; ++g) {
@@ -125,43 +125,37 @@ __global__ __launch_bounds__(256) void fp8wo_gemm_kernel(Args a) {
         const uint8_t* X = sX[g % STAGES];
 #pragma unroll
         for (int s = 0; s < 4; ++s) {  // 16-deep steps: quarter s of the rows, k = 16 s + 8 half .. + 7
-            bf16x8 af[2], bf[2];
+            bf16x8 bf[4];
+            const bf16x8 af = widen(*reinterpret_cast<const uint2*>(W + (32 * wn + tok) * 64 + 16 * (s ^ wsw) + 8 * half));
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const uint8_t* row = W + (64 * wn + 32 * i + tok) * 64;
-                af[i] = widen(*reinterpret_cast<const uint2*>(row + 16 * (s ^ wsw) + 8 * half));
-            }
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const uint8_t* row = X + (64 * wm + 32 * j + tok) * 128;
+            for (int j = 0; j < 4; ++j) {
+                const uint8_t* row = X + (32 * j + tok) * 128;
                 bf[j] = *reinterpret_cast<const bf16x8*>(row + 16 * ((2 * s + half) ^ xsw));
             }
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf[j], acc[j], 0, 0, 0);
         }
     }
     wait_vmcnt<0>();  // the clamped tail loads land before the workgroup ends
 
-    // epilogue: element e of subtile (i, j) is feature n0 + 64 wn + 32 i + 8 (e / 4) + 4 half + e % 4 of token
-    // m0 + 64 wm + 32 j + tok; four consecutive features per 8-byte store
+    // epilogue: element e of subtile j is feature n0 + 32 wn + 8 (e / 4) + 4 half + e % 4 of token m0 + 32 j + tok;
+    // four consecutive features per 8-byte store
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int64_t m = m0 + 64 * wm + 32 * j + tok;
+    for (int j = 0; j < 4; ++j) {
+        const int64_t m = m0 + 32 * j + tok;
         if (m >= a.M) continue;
         uint16_t* orow = a.out + m * a.ldo;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 1; ++i)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int64_t n = n0 + 64 * wn + 32 * i + 8 * q + 4 * half;
+                const int64_t n = n0 + 32 * wn + 8 * q + 4 * half;
                 uint16_t r[4];
                 uint2 old = make_uint2(0u, 0u);
                 if (EPI == EPI_RESIDUAL) old = *reinterpret_cast<const uint2*>(orow + n);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    float y = acc[i][j][4 * q + e] * a.ws[(n + e) * a.ws_step];
+                    float y = acc[j][4 * q + e] * a.ws[(n + e) * a.ws_step];
                     if (a.bias) y = y + bf16_to_f32(a.bias[n + e]);
                     if (EPI == EPI_RESIDUAL) {
                         const uint16_t o = uint16_t(((e < 2 ? old.x : old.y) >> (16 * (e % 2))) & 0xffffu);
