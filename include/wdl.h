@@ -53,18 +53,25 @@ int64_t wdl_act_quant_workspace_floats(int64_t Mp, int64_t K);
  * q = clamp(rint(u / scale)). Outputs: q as fp6 codes of the integers [Mp, K] in the operand format (below);
  * ascales bf16 [K/64, Mp]; lora fp32 [Mp, 32] = v . proj_down; rows M..Mp-1 zero. Mp % 128 == 0. v_out (bf16
  * [M, K]) optional copy of v.
- * LayerNorm statistics: lane l of a wave owns the 8-value chunks l, l+64, ..., summed value by value, the 64 lane
- * sums combined by an xor butterfly 32..1 (the oracle's order). workspace: wdl_act_quant_workspace_floats(Mp, K). */
+ * LayerNorm statistics (K <= 4096) from chunk partials of x: ln_partials fp32 [M][K / 32][2] (8-byte aligned) as
+ * the residual epilogue of wdl_w4a4_gemm writes them for the rows it produces, or NULL (then the call forms them
+ * from x first, one more launch). Per row and 32-value chunk: (S, M2) = the chunk's sum and its sum of squared
+ * deviations from S / 32, each as 8 quads of 4 values summed in order, the quads combined as
+ * ((t0 + t1) + (t2 + t3)) + ((t4 + t5) + (t6 + t7)); the row's C chunks merged by 8 slots (slot j: chunks
+ * [j C / 8, (j + 1) C / 8) in order from +0, the slots combined as the same tree): mean = sum S / K, M2 = sum of
+ * M2_c + 32 (S_c / 32 - mean)^2, rstd = 1 / sqrt(M2 / K + eps) (the oracle's order).
+ * workspace: wdl_act_quant_workspace_floats(Mp, K). */
 int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K, const void* smooth, float qshift,
                      int unsigned_q, const void* proj_down_t, int64_t rank, void* q, void* ascales, float* lora,
                      int64_t Mp, const float* mod_shift, const float* mod_scale, const float* ln_w,
-                     const float* ln_b, int ln, float eps, void* v_out, float* workspace, wdl_stream_t stream);
+                     const float* ln_b, int ln, float eps, const float* ln_partials, void* v_out, float* workspace,
+                     wdl_stream_t stream);
 
 /* wdl_act_quant_w4 without the workspace argument, for callers that cannot allocate device memory (code under HIP
  * graph capture that must not allocate, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
  * reference. The scratch is a static device array of WDL_ACT_QUANT_STATIC_FLOATS floats (16 MiB) per GPU, held
  * until the process ends; a shape with wdl_act_quant_workspace_floats(Mp, K) above that is rejected (WDL_EINVAL)
- * before any launch (Mp <= 4608 at K = 14336, Mp <= 10752 at K = 3072). Nothing is allocated or freed. The first
+ * before any launch (Mp <= 4608 at K = 14336, Mp <= 7168 at K = 3072). Nothing is allocated or freed. The first
  * call on a device looks up that device's copy of the array; the stream must belong to the current device. All
  * calls on one GPU share its array: calls that overlap in time on one GPU (different streams, or threads) race,
  * as calls sharing one workspace of wdl_act_quant_w4 do. Outputs are bit-identical to wdl_act_quant_w4's. */
@@ -72,8 +79,8 @@ int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K, const voi
 int wdl_act_quant_w4_static(const void* x, int64_t ldx, int64_t M, int64_t K, const void* smooth, float qshift,
                             int unsigned_q, const void* proj_down_t, int64_t rank, void* q, void* ascales,
                             float* lora, int64_t Mp, const float* mod_shift, const float* mod_scale,
-                            const float* ln_w, const float* ln_b, int ln, float eps, void* v_out,
-                            wdl_stream_t stream);
+                            const float* ln_w, const float* ln_b, int ln, float eps, const float* ln_partials,
+                            void* v_out, wdl_stream_t stream);
 
 /* Operand format of the W4A4 GEMM (both sides; R % 128 == 0, K % 64 == 0), R * K * 3/4 bytes:
  * - values: weights w in [-8, 7] as the fp6 e3m2 code of 2w (sign, 3 exponent bits of bias 3, 2 mantissa bits);
@@ -115,11 +122,16 @@ int wdl_w4a4_scale_pairs(const void* scales, int fp16, int64_t n, void* pairs, w
  * by eighths of K; one launch, the size is then a 256-byte token the kernel does not touch) or stream-K (the
  * (tile, group) iterations shared evenly, partial sums in the workspace added in a fixed order by a second
  * launch). Both are deterministic, their rounding not identical to the one-pass launch. With NULL the one-pass
- * launch runs. Calls sharing a workspace must not overlap. */
+ * launch runs. Calls sharing a workspace must not overlap.
+ * ln_partials (epilogue 2 only, else NULL): fp32 [M][N / 32][2], 8-byte aligned, receives the LayerNorm chunk
+ * partials of the rows written (the N columns being whole rows), in wdl_act_quant_w4's order, so the next
+ * LayerNorm-fused quantization of out skips its statistics pass. No counterpart in the reference (its LayerNorm
+ * is a separate torch op). */
 int64_t wdl_w4a4_gemm_workspace_bytes(int64_t Mp, int64_t N, int64_t K);
 int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wcodes, const void* wscales, const float* lora,
                   const void* proj_up, const void* bias, int64_t M, int64_t Mp, int64_t N, int64_t K, int64_t rank,
-                  void* out, int64_t ldo, int epilogue, const float* gate, void* workspace, wdl_stream_t stream);
+                  void* out, int64_t ldo, int epilogue, const float* gate, float* ln_partials, void* workspace,
+                  wdl_stream_t stream);
 
 /* Workspace (in floats) of wdl_w4a4_gemm_gelu_quant for Mp tokens and a hidden layer of N features. */
 int64_t wdl_w4a4_gemm_gelu_quant_workspace_floats(int64_t Mp, int64_t N);

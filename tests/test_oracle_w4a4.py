@@ -121,6 +121,60 @@ def test_ordered_row_sum_equals_scalar_loop():
         assert got[r] == lanes[0]
 
 
+@pytest.mark.parametrize("K", [3072, 224])
+def test_layernorm_chunk_statistics_equal_scalar_loops(K):
+    """The LayerNorm statistics' order (chunk partials, then the 8-slot merge), restated as scalar loops, one fp32
+    operation at a time; K = 224 leaves slots with no chunk (7 chunks over 8 slots)."""
+    g = torch.Generator().manual_seed(8)
+    x = (torch.randn(2, K, generator=g) * 3 + 1.5).to(torch.bfloat16)
+    a = x.float().numpy().astype(np.float32)
+    f = np.float32
+    S, M2 = onorms.ln_chunk_partials(x)
+    mean, rstd = onorms.ln_stats(x, 1e-6)
+    C = K // 32
+    for r in range(2):
+        sums, m2s = [], []
+        for c in range(C):
+            v = [a[r, 32 * c + i] for i in range(32)]
+
+            def chunk(vals):
+                t = []
+                for k in range(8):
+                    s = f(vals[4 * k])
+                    for e in range(1, 4):
+                        s = f(s + vals[4 * k + e])
+                    t.append(s)
+                return f(f(f(t[0] + t[1]) + f(t[2] + t[3])) + f(f(t[4] + t[5]) + f(t[6] + t[7])))
+
+            s = chunk(v)
+            mc = f(s * f(1 / 32))
+            sq = [f(f(vi - mc) * f(vi - mc)) for vi in v]
+            sums.append(s)
+            m2s.append(chunk(sq))
+        assert S[r].tolist() == sums and M2[r].tolist() == m2s
+
+        def merge(vals):
+            lanes = []
+            for j in range(8):
+                acc = f(0)
+                for c in range(j * C // 8, (j + 1) * C // 8):
+                    acc = f(acc + vals[c])
+                lanes.append(acc)
+            for o in (1, 2, 4):  # the butterfly of 8 lanes; lane 0's value
+                lanes = [f(lanes[i] + lanes[i ^ o]) for i in range(8)]
+            return lanes[0]
+
+        mu = f(merge(sums) / f(K))
+        terms = [f(m2s[c] + f(f(32) * f(f(f(sums[c] * f(1 / 32)) - mu) * f(f(sums[c] * f(1 / 32)) - mu))))
+                 for c in range(C)]
+        var = f(merge(terms) / f(K))
+        assert mean[r] == mu and rstd[r] == f(f(1) / np.sqrt(f(var + f(1e-6))))
+        # the closed form in float64
+        xd = a[r].astype(np.float64)
+        assert abs(float(mean[r]) - xd.mean()) <= 1e-6 * max(1.0, abs(xd.mean()))
+        assert abs(float(rstd[r]) - 1 / np.sqrt(xd.var() + 1e-6)) <= 1e-5 / np.sqrt(xd.var())
+
+
 def test_ln_mod_and_rms_close_to_torch():
     g = torch.Generator().manual_seed(7)
     x = (torch.randn(5, 3072, generator=g) * 2 + 0.3).to(torch.bfloat16)

@@ -80,6 +80,47 @@ def test_fused_layernorm_modulation_quant_bit_exact(gpu, affine):
     assert torch.equal(asc.cpu()[:, :M].t(), rs)
 
 
+@pytest.mark.parametrize("Mp,M,N,K,stream_k", [(1408, 1392, 3072, 3072, True), (384, 300, 384, 256, False),
+                                               (512, 464, 512, 14336, True)])
+def test_layernorm_partials_of_the_residual_epilogue(gpu, Mp, M, N, K, stream_k):
+    """The gated-residual epilogue's LayerNorm chunk partials of the rows it writes, bit-exact to the oracle's
+    partials of those rows, through each launch that runs the residual: the balanced form with its 32 x 32 pieces
+    (1392 x 3072, K 3072), the one-pass tile, stream-K + merge (K 14336). Then the LayerNorm-fused quantizer of the
+    new rows from those partials equals the quantizer forming them itself (and the oracle), bit for bit."""
+    from wdl import ops, w4a4
+
+    g = torch.Generator().manual_seed(M + N)
+    qa = torch.randint(-7, 8, (Mp, K), generator=g, dtype=torch.int32)
+    qw = torch.randint(-8, 8, (N, K), generator=g, dtype=torch.int32)
+    asc = (torch.rand(K // 64, Mp, generator=g) * 0.3 + 0.01).to(torch.bfloat16)
+    wsc = (torch.rand(K // 64, N, generator=g) * 0.01 + 1e-4).to(torch.bfloat16)
+    lora = torch.randn(Mp, 32, generator=g)
+    pu = (torch.randn(N, 32, generator=g) * 0.05).to(torch.bfloat16)
+    bias = (torch.randn(N, generator=g) * 0.1).to(torch.bfloat16)
+    X = (torch.randn(M, N, generator=g) * 2 + 0.5).to(torch.bfloat16)
+    gate = torch.randn(N, generator=g)
+    out = X.cuda().clone()
+    part = torch.full((M, N // 32, 2), float("nan"), device="cuda")
+    codes = ops.encode_acts(qa).cuda()
+    ops.gemm_launch(codes, asc.cuda(), lora.cuda(), ops.as_codes(w4a4.pack_weight(qw).cuda(), K), wsc.cuda(),
+                    pu.cuda(), bias.cuda(), M, out, ops.EPI_RESIDUAL, gate.cuda(), stream_k, ln_out=part)
+    torch.cuda.synchronize()
+    S, M2 = onorms.ln_chunk_partials(out.cpu())
+    got = part.cpu().numpy()
+    assert (got[..., 0] == S).all() and (got[..., 1] == M2).all()
+    if N % 64 == 0 and N <= 4096:
+        shift, scale = torch.randn(N, generator=g) * 0.1, torch.randn(N, generator=g) * 0.1
+        smooth = (torch.rand(N, generator=g) + 0.5).to(torch.bfloat16)
+        pdt = (torch.randn(32, N, generator=g) / N ** 0.5).to(torch.bfloat16)
+        ln = dict(shift=shift.cuda(), scale=scale.cuda(), eps=1e-6)
+        v1, v2 = (torch.empty(M, N, device="cuda", dtype=torch.bfloat16) for _ in range(2))
+        a = ops.act_quant_launch(out, smooth.cuda(), pdt.cuda(), ln=dict(ln, partials=part), v_out=v1)
+        b = ops.act_quant_launch(out, smooth.cuda(), pdt.cuda(), ln=ln, v_out=v2)
+        torch.cuda.synchronize()
+        assert torch.equal(v1, v2) and all(torch.equal(x, y) for x, y in zip(a, b))
+        assert torch.equal(v1.cpu(), onorms.ln_mod(out.cpu(), shift, scale, eps=1e-6))
+
+
 def launch_gemm(qa_int, asc, qweight, wsc, lora=None, pu=None, bias=None, M=None, epi=1, out=None, gate=None,
                 stream_k=True):
     from wdl import ops

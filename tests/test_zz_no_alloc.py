@@ -24,7 +24,7 @@ def _call(static, x, smooth, pdt, M, Mp, unsigned, ln):
     common = [x.data_ptr(), x.stride(0), M, K, smooth.data_ptr(), ctypes.c_float(0.171875 if unsigned else 0.0),
               int(unsigned), pdt.data_ptr(), 32, q.data_ptr(), asc.data_ptr(), lora.data_ptr(), Mp,
               ops.ptr(ln.get("shift")), ops.ptr(ln.get("scale")), ops.ptr(ln.get("weight")), ops.ptr(ln.get("bias")),
-              int(bool(ln)), ctypes.c_float(1e-6), None]
+              int(bool(ln)), ctypes.c_float(1e-6), None, None]  # eps, no LN partials (formed here), no v_out
     stream = torch.cuda.current_stream().cuda_stream
     if static:
         _lib.call("wdl_act_quant_w4_static", *common, stream)
@@ -68,5 +68,5 @@ def test_static_scratch_refuses_shapes_above_its_maximum(gpu):
     x = torch.zeros(1, K, device="cuda", dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="static maximum"):
         _lib.call("wdl_act_quant_w4_static", x.data_ptr(), K, 1, K, x.data_ptr(), ctypes.c_float(0.0), 0, None, 32,
-                  x.data_ptr(), x.data_ptr(), None, Mp, None, None, None, None, 0, ctypes.c_float(1e-6), None,
+                  x.data_ptr(), x.data_ptr(), None, Mp, None, None, None, None, 0, ctypes.c_float(1e-6), None, None,
                   torch.cuda.current_stream().cuda_stream)

@@ -12,10 +12,16 @@
 // ([Mp / 128][K / 64][128][48 bytes], Mp a multiple of 128; see blocked6_offset); ascales bf16 [K/64, Mp]; lora
 // fp32 [Mp, 32].
 //
+// LayerNorm statistics come from per-chunk partials of x: for each row and 32-value chunk c, (S_c, M2_c) = the
+// chunk's sum and its sum of squared deviations from its own mean, each as 8 quads summed sequentially and the
+// quads combined as ((t0 + t1) + (t2 + t3)) + ((t4 + t5) + (t6 + t7)). The W4A4 GEMM's gated-residual epilogue
+// writes them for the rows it produces (wdl_w4a4_gemm's ln_partials), in the same order; otherwise ln_partials
+// runs here. The quant launch merges a row's C = K / 32 chunks over 8 lanes (lane j: chunks [j C / 8, (j + 1) C / 8)
+// in order from +0, the lanes combined by an xor butterfly 1, 2, 4): mean = sum S_c / K, M2 = sum of
+// M2_c + 32 (S_c / 32 - mean)^2, var = M2 / K, rstd = 1 / sqrt(var + eps).
+//
 // Launches (all parallel over rows and column blocks, nothing serial over K):
-//   row_stats  (LN only): one wave per row; LN statistics in a fixed order — lane l owns the 8-value chunks
-//              c = l, l + 64, ... and sums them value by value; the 64 lane sums meet in an xor butterfly
-//              (32, 16, 8, 4, 2, 1); mean = sum / K, var = sum((x - mean)^2) / K, rstd = 1 / sqrt(var + eps).
+//   ln_partials (LN only, when the caller passes no partials): one thread per (row, chunk).
 //   quant      grid (Mp / 32, ceil(K / 64 / S)): 32 rows x S 64-groups per workgroup of S waves (S = 4 up to
 //              K = 4096, 8 above), each wave one group of the 32 rows; lane l owns row l % 32 and half
 //              l / 32 of a group (64 bytes of x, loaded up front with the matching 64 bytes of proj_down^T); the
@@ -42,7 +48,8 @@ constexpr int RANK = 32;
 // 4 x 2 and 16 x 1 take 10.8 - 12.6 us), 8 x 1 at K = 14336 (22.1 us; 8 x 2, 4 x 2 and 16 x 1 take 25 - 33 us).
 constexpr int SMALL_WAVES = 4, SMALL_G = 1, BIG_WAVES = 8, BIG_G = 1;
 constexpr int groups_per_block(int64_t K) { return K <= 4096 ? SMALL_WAVES * SMALL_G : BIG_WAVES * BIG_G; }
-constexpr int MAXCH = 8; // row_stats keeps up to 8 chunks per lane in registers (K <= 4096)
+constexpr int MAXCH = 8; // LN rows: K <= 64 * 8 * MAXCH = 4096 (the merge holds up to 16 chunks per lane)
+constexpr int LN_CHUNK = 32;
 
 __device__ __forceinline__ void load8(const uint16_t* p, float* f) {
     uint4 raw = *reinterpret_cast<const uint4*>(p);
@@ -60,39 +67,35 @@ __device__ __forceinline__ float butterfly64(float s) {
     return s;
 }
 
-__global__ __launch_bounds__(256) void row_stats_kernel(const uint16_t* x, int64_t ldx, int64_t M, int64_t K,
-                                                        float eps, float2* stats) {
-    const int lane = threadIdx.x % 64;
-    const int64_t row = int64_t(blockIdx.x) * 4 + threadIdx.x / 64;
-    if (row >= M) return;
-    const uint16_t* xr = x + row * ldx;
-    const int64_t chunks = K / 8;
-    float v[MAXCH][8];
+// ((t0 + t1) + (t2 + t3)) + ((t4 + t5) + (t6 + t7)) of the 8 quad sums of a chunk
+__device__ __forceinline__ float tree8(const float* t) {
+    return ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+}
+
+// (S_c, M2_c) of one 32-value chunk held in registers
+__device__ __forceinline__ float2 chunk_partial(const float* v) {
+    float t[8];
 #pragma unroll
-    for (int i = 0; i < MAXCH; ++i) {
-        const int64_t c = lane + 64 * i;
-        if (c < chunks) load8(xr + c * 8, v[i]);
-        else
-            for (int j = 0; j < 8; ++j) v[i][j] = 0.0f;
+    for (int k = 0; k < 8; ++k) t[k] = ((v[4 * k] + v[4 * k + 1]) + v[4 * k + 2]) + v[4 * k + 3];
+    const float S = tree8(t), mc = S * (1.0f / LN_CHUNK);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float d0 = v[4 * k] - mc, d1 = v[4 * k + 1] - mc, d2 = v[4 * k + 2] - mc, d3 = v[4 * k + 3] - mc;
+        t[k] = ((d0 * d0 + d1 * d1) + d2 * d2) + d3 * d3;
     }
-    float s = 0.0f;
+    return make_float2(S, tree8(t));
+}
+
+// LayerNorm chunk partials of x [M, K]: thread = (row, chunk), part [M][K / 32]
+__global__ __launch_bounds__(256) void ln_partials_kernel(const uint16_t* x, int64_t ldx, int64_t M, int64_t K,
+                                                          float2* part) {
+    const int64_t C = K / LN_CHUNK, i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= M * C) return;
+    const int64_t row = i / C, c = i % C;
+    float v[LN_CHUNK];
 #pragma unroll
-    for (int i = 0; i < MAXCH; ++i)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) s = s + v[i][j];
-    const float mean = butterfly64(s) / float(K);
-    float ss = 0.0f;
-#pragma unroll
-    for (int i = 0; i < MAXCH; ++i) {
-        const bool real = lane + 64 * i < chunks;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float d = v[i][j] - mean;
-            ss = ss + (real ? d * d : 0.0f);
-        }
-    }
-    const float var = butterfly64(ss) / float(K);
-    if (lane == 0) stats[row] = make_float2(mean, 1.0f / sqrtf(var + eps));
+    for (int j = 0; j < 4; ++j) load8(x + row * ldx + c * LN_CHUNK + 8 * j, v + 8 * j);
+    part[i] = chunk_partial(v);
 }
 
 struct QuantArgs {
@@ -106,12 +109,13 @@ struct QuantArgs {
     uint8_t* q;                // [Mp, K], tile-blocked
     uint16_t* ascales;         // [K/64, Mp]
     float* lora;               // [nblocks, Mp, RANK] partials (or [Mp, RANK] when nblocks == 1)
-    const float2* stats;       // LN (mean, rstd) per row, or null (no LN)
+    const float2* lnp;         // LN chunk partials [M][K / 32] (LN rows), or null (no LN)
     const float* mod_shift;    // fp32 [K] or null
     const float* mod_scale;    // fp32 [K] or null (used as 1 + scale)
     const float* ln_w;         // fp32 [K] or null
     const float* ln_b;         // fp32 [K] or null
     uint16_t* v_out;           // bf16 [M, K] copy of v, or null
+    float eps;                 // LN
 };
 
 // Workgroups of WAVES waves on the same 32 rows; wave w takes the 64-groups w, w + WAVES, ... (G of them) of the
@@ -129,6 +133,7 @@ __global__ __launch_bounds__(64 * WAVES) void quant_kernel(QuantArgs a) {
     // 1 / smooth
     __shared__ __attribute__((aligned(16))) float sp[6][SC];
     __shared__ float part[WAVES][ROWS * RANK];
+    __shared__ float2 sst[LN ? ROWS : 1];  // LN (mean, rstd) of the workgroup's rows
 
     const int t = threadIdx.x, lane = t % 64, wave = t / 64;
     const int r = lane % 32, h = lane / 32;
@@ -157,7 +162,20 @@ __global__ __launch_bounds__(64 * WAVES) void quant_kernel(QuantArgs a) {
             for (int i = 0; i < 4; ++i) pd[j][i] = *reinterpret_cast<const uint4*>(pr + 8 * i);
         }
     }
-    const float2 st = (LN && live) ? a.stats[row] : make_float2(0.0f, 0.0f);
+    // LN: this lane's merge slot — row 8 wave + lane / 8 of the workgroup, chunks [j C / 8, (j + 1) C / 8) of it
+    // (j = lane % 8), loaded with the row data
+    constexpr int MAXCP = 64 * 8 * MAXCH / LN_CHUNK / 8;  // chunks per slot at K = 4096
+    float2 cp[LN ? MAXCP : 1];
+    int ncp = 0;
+    if constexpr (LN) {
+        static_assert(WAVES * 8 == ROWS, "the merge maps the workgroup's rows to its waves, 8 rows x 8 slots each");
+        const int64_t C = K / LN_CHUNK, mrow = int64_t(blockIdx.x) * ROWS + 8 * wave + lane / 8;
+        const int64_t c0 = (lane % 8) * C / 8;
+        ncp = int((lane % 8 + 1) * C / 8 - c0);
+#pragma unroll
+        for (int i = 0; i < MAXCP; ++i)
+            cp[i] = i < ncp && mrow < a.M ? a.lnp[mrow * C + c0 + i] : make_float2(0.0f, 0.0f);
+    }
 #pragma unroll
     for (int i = 0; i < G; ++i) {
         const int c = t + NT * i;
@@ -180,7 +198,29 @@ __global__ __launch_bounds__(64 * WAVES) void quant_kernel(QuantArgs a) {
         sp[4][c] = p4;
         sp[5][c] = 1.0f / sm;
     }
+    if constexpr (LN) {  // the row's (mean, rstd) from its chunk partials, into sst
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < MAXCP; ++i)
+            if (i < ncp) sum = sum + cp[i].x;
+        sum = sum + __shfl_xor(sum, 1);
+        sum = sum + __shfl_xor(sum, 2);
+        sum = sum + __shfl_xor(sum, 4);
+        const float mean = sum / float(K);
+        float m2 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < MAXCP; ++i)
+            if (i < ncp) {
+                const float d = cp[i].x * (1.0f / LN_CHUNK) - mean;
+                m2 = m2 + (cp[i].y + float(LN_CHUNK) * (d * d));
+            }
+        m2 = m2 + __shfl_xor(m2, 1);
+        m2 = m2 + __shfl_xor(m2, 2);
+        m2 = m2 + __shfl_xor(m2, 4);
+        if (lane % 8 == 0) sst[8 * wave + lane / 8] = make_float2(mean, 1.0f / sqrtf(m2 / float(K) + a.eps));
+    }
     __syncthreads();
+    const float2 st = (LN && live) ? sst[r] : make_float2(0.0f, 0.0f);
 
     const float qmax = a.unsigned_q ? 15.0f : 7.0f;
     const float qlo = a.unsigned_q ? 0.0f : -8.0f;
@@ -326,7 +366,8 @@ int lora_sum(const float* part, int nb, int64_t n, float* out, hipStream_t strea
 
 extern "C" int64_t wdl_act_quant_workspace_floats(int64_t Mp, int64_t K) {
     const int64_t S = groups_per_block(K), nb = (K / 64 + S - 1) / S;
-    return (nb > 1 ? nb * Mp * RANK : 0) + 2 * Mp;
+    // the low-rank column-block partials, then (LN-capable widths) the LayerNorm chunk partials
+    return (nb > 1 ? nb * Mp * RANK : 0) + (K <= 64 * 8 * MAXCH ? Mp * (K / LN_CHUNK) * 2 : 0);
 }
 
 namespace {
@@ -334,7 +375,8 @@ namespace {
 int act_quant_launch(const void* x, int64_t ldx, int64_t M, int64_t K, const void* smooth, float qshift,
                      int unsigned_q, const void* proj_down_t, int64_t rank, void* q, void* ascales, float* lora,
                      int64_t Mp, const float* mod_shift, const float* mod_scale, const float* ln_w, const float* ln_b,
-                     int ln, float eps, void* v_out, float* workspace, hipStream_t stream) {
+                     int ln, float eps, const float* ln_partials, void* v_out, float* workspace,
+                     hipStream_t stream) {
     if (M < 0 || K <= 0 || K % 64 || Mp < M || Mp % BLOCK_ROWS || ldx < K)
         return fail(WDL_EINVAL, "act_quant_w4: bad shape M=%lld K=%lld Mp=%lld ldx=%lld", (long long)M,
                     (long long)K, (long long)Mp, (long long)ldx);
@@ -344,26 +386,33 @@ int act_quant_launch(const void* x, int64_t ldx, int64_t M, int64_t K, const voi
         return fail(WDL_EINVAL, "act_quant_w4: null pointer");
     if ((reinterpret_cast<uintptr_t>(x) | (ldx * 2)) % 16)
         return fail(WDL_EINVAL, "act_quant_w4: x rows must be 16-byte aligned");
+    if (ln_partials && reinterpret_cast<uintptr_t>(ln_partials) % 8)
+        return fail(WDL_EINVAL, "act_quant_w4: LayerNorm partials must be 8-byte aligned");
     if (Mp == 0) return WDL_OK;
     const int S = groups_per_block(K), nb = int((K / 64 + S - 1) / S);
-    float2* stats = reinterpret_cast<float2*>(workspace + (nb > 1 ? int64_t(nb) * Mp * RANK : 0));
-    if (ln && M > 0) {
-        row_stats_kernel<<<unsigned((M + 3) / 4), 256, 0, stream>>>(static_cast<const uint16_t*>(x), ldx, M, K, eps,
-                                                                    stats);
-        int rc = check_launch("act_quant_w4 row_stats");
-        if (rc) return rc;
+    // LayerNorm chunk partials: the caller's (written by the GEMM epilogue that produced x), or made here
+    const float2* lnp = reinterpret_cast<const float2*>(ln_partials);
+    if (ln && !ln_partials) {
+        float2* wp = reinterpret_cast<float2*>(workspace + (nb > 1 ? int64_t(nb) * Mp * RANK : 0));
+        if (M > 0) {
+            const int64_t n = M * (K / LN_CHUNK);
+            ln_partials_kernel<<<unsigned((n + 255) / 256), 256, 0, stream>>>(static_cast<const uint16_t*>(x), ldx,
+                                                                               M, K, wp);
+            int rc = check_launch("act_quant_w4 ln_partials");
+            if (rc) return rc;
+        }
+        lnp = wp;
     }
     QuantArgs a{static_cast<const uint16_t*>(x), ldx, M, Mp, K, static_cast<const uint16_t*>(smooth), qshift,
                 unsigned_q, static_cast<const uint16_t*>(proj_down_t), static_cast<uint8_t*>(q),
-                static_cast<uint16_t*>(ascales), nb > 1 ? workspace : lora, ln ? stats : nullptr, mod_shift,
-                mod_scale, ln_w, ln_b, static_cast<uint16_t*>(v_out)};
+                static_cast<uint16_t*>(ascales), nb > 1 ? workspace : lora, ln ? lnp : nullptr, mod_shift,
+                mod_scale, ln_w, ln_b, static_cast<uint16_t*>(v_out), eps};
     const dim3 grid(unsigned(Mp / ROWS), unsigned(nb));
     if (K <= 4096) {
         if (ln) quant_kernel<SMALL_WAVES, SMALL_G, true><<<grid, 64 * SMALL_WAVES, 0, stream>>>(a);
         else quant_kernel<SMALL_WAVES, SMALL_G, false><<<grid, 64 * SMALL_WAVES, 0, stream>>>(a);
-    } else {
-        if (ln) quant_kernel<BIG_WAVES, BIG_G, true><<<grid, 64 * BIG_WAVES, 0, stream>>>(a);
-        else quant_kernel<BIG_WAVES, BIG_G, false><<<grid, 64 * BIG_WAVES, 0, stream>>>(a);
+    } else {  // no LayerNorm at these widths (checked above)
+        quant_kernel<BIG_WAVES, BIG_G, false><<<grid, 64 * BIG_WAVES, 0, stream>>>(a);
     }
     int rc = check_launch("act_quant_w4 quant");
     if (rc || !proj_down_t || nb == 1) return rc;
@@ -375,7 +424,7 @@ int act_quant_launch(const void* x, int64_t ldx, int64_t M, int64_t K, const voi
 // taken once per device with that device current (hipGetSymbolAddress) and kept in scratch_ptr; in host code the
 // array's name is not a device address and is never passed to a kernel. Every kernel writes the parts of it that
 // a later kernel of the same call reads before that kernel runs (the partials of every column block and row, the
-// statistics of every row < M), so nothing needs clearing between calls.
+// LayerNorm chunk partials of every row < M), so nothing needs clearing between calls.
 static __device__ __align__(256) float scratch[WDL_ACT_QUANT_STATIC_FLOATS];
 
 constexpr int MAX_DEVICES = 64;
@@ -409,17 +458,17 @@ int static_scratch(hipStream_t stream, float** out) {
 extern "C" int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K, const void* smooth, float qshift,
                                 int unsigned_q, const void* proj_down_t, int64_t rank, void* q, void* ascales,
                                 float* lora, int64_t Mp, const float* mod_shift, const float* mod_scale,
-                                const float* ln_w, const float* ln_b, int ln, float eps, void* v_out,
-                                float* workspace, hipStream_t stream) {
+                                const float* ln_w, const float* ln_b, int ln, float eps, const float* ln_partials,
+                                void* v_out, float* workspace, hipStream_t stream) {
     return act_quant_launch(x, ldx, M, K, smooth, qshift, unsigned_q, proj_down_t, rank, q, ascales, lora, Mp,
-                            mod_shift, mod_scale, ln_w, ln_b, ln, eps, v_out, workspace, stream);
+                            mod_shift, mod_scale, ln_w, ln_b, ln, eps, ln_partials, v_out, workspace, stream);
 }
 
 extern "C" int wdl_act_quant_w4_static(const void* x, int64_t ldx, int64_t M, int64_t K, const void* smooth,
                                        float qshift, int unsigned_q, const void* proj_down_t, int64_t rank, void* q,
                                        void* ascales, float* lora, int64_t Mp, const float* mod_shift,
                                        const float* mod_scale, const float* ln_w, const float* ln_b, int ln,
-                                       float eps, void* v_out, hipStream_t stream) {
+                                       float eps, const float* ln_partials, void* v_out, hipStream_t stream) {
     if (Mp < 0 || K <= 0 || K % 64)
         return fail(WDL_EINVAL, "act_quant_w4_static: bad shape K=%lld Mp=%lld", (long long)K, (long long)Mp);
     const int64_t need = wdl_act_quant_workspace_floats(Mp, K);
@@ -431,5 +480,5 @@ extern "C" int wdl_act_quant_w4_static(const void* x, int64_t ldx, int64_t M, in
     const int rc = static_scratch(stream, &ws);
     if (rc) return rc;
     return act_quant_launch(x, ldx, M, K, smooth, qshift, unsigned_q, proj_down_t, rank, q, ascales, lora, Mp,
-                            mod_shift, mod_scale, ln_w, ln_b, ln, eps, v_out, ws, stream);
+                            mod_shift, mod_scale, ln_w, ln_b, ln, eps, ln_partials, v_out, ws, stream);
 }

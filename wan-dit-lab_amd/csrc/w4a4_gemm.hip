@@ -71,7 +71,19 @@ struct GemmArgs {
     const uint16_t* sm2;      // smooth2, bf16 [N]
     const uint16_t* pd2t;     // proj_down2^T, bf16 [32, N]
     float* lpart;             // low-rank partials fp32 [N/128][Mp][32]
+    float2* lnp;              // EPI_RESIDUAL: LayerNorm chunk partials of the output rows [M][N / 32], or null
 };
+
+// LayerNorm chunk partials of the rows a residual epilogue writes (the activation quantizer's LN input): for a row's
+// 32-value chunk, (S, M2) = its sum and its sum of squared deviations from its mean S / 32, each as 8 quads of 4
+// values summed in order and the quads combined as ((t0 + t1) + (t2 + t3)) + ((t4 + t5) + (t6 + t7)), on the bf16
+// values written. The staged epilogue holds 8 consecutive values per lane (quads 2a, 2a + 1 of a chunk, a = lane
+// % 4 of a 4-lane group), the MFMA layout 4 per lane half (quad 2q + half of quarter q).
+__device__ __forceinline__ float quad_sum(float a, float b, float c, float d) { return ((a + b) + c) + d; }
+__device__ __forceinline__ float quad_sq(float a, float b, float c, float d, float m) {
+    const float da = a - m, db = b - m, dc = c - m, dd = d - m;
+    return ((da * da + db * db) + dc * dc) + dd * dd;
+}
 
 // Tile BN (features) x BM (tokens), NW waves in a (BN / WN) x (BM / WM) grid. Every operand byte streams from
 // global memory straight into a STAGES-deep LDS ring with global_load_lds (lane-linear in LDS: 16 or 4 bytes per
@@ -165,6 +177,8 @@ __device__ __forceinline__ void finish_tile(const GemmArgs& p, f32x16 (&acc)[TN]
                                                                    nb0 + i * 32 + 8 * q + 4 * half);
     }
     const float xs0 = EPI == EPI_FP8_TENSOR ? p.xs[0] * p.wsf[0] : 0.0f;
+    static_assert(EPI != EPI_RESIDUAL || (TN == 1 && TM == 1), "the gated residual runs here on 32 x 32 pieces only");
+    float nx[EPI == EPI_RESIDUAL ? 16 : 1] = {};  // the piece's new values of the lane (LayerNorm partials)
 
     // ---- low-rank branch: acc += pu[n] . bf16(lora[m]) over r = 0..31, two 32x32x16 bf16 MFMAs per subtile
     if (p.lora) {
@@ -218,6 +232,7 @@ __device__ __forceinline__ void finish_tile(const GemmArgs& p, f32x16 (&acc)[TN]
                         for (int e = 0; e < 4; ++e) {
                             const float yb = bf16_to_f32(f32_to_bf16(y[e]));
                             r[e] = f32_to_bf16(bf16_to_f32(ov[e]) + yb * gate[i][q][e]);
+                            if constexpr (EPI == EPI_RESIDUAL) nx[4 * q + e] = bf16_to_f32(r[e]);
                         }
                     } else if (EPI == EPI_GELU) {
 #pragma unroll
@@ -230,6 +245,25 @@ __device__ __forceinline__ void finish_tile(const GemmArgs& p, f32x16 (&acc)[TN]
                 }
             }
         }
+    if constexpr (EPI == EPI_RESIDUAL) {
+        if (p.lnp) {  // the piece's 32 features are one chunk; quarter q of a lane half holds quad 2 q + half
+            float t[4], u[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                t[q] = quad_sum(nx[4 * q], nx[4 * q + 1], nx[4 * q + 2], nx[4 * q + 3]);
+                t[q] = t[q] + __shfl_xor(t[q], 32);  // quads 2 q + 2 q + 1
+            }
+            const float S = (t[0] + t[1]) + (t[2] + t[3]), mc = S * (1.0f / 32);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                u[q] = quad_sq(nx[4 * q], nx[4 * q + 1], nx[4 * q + 2], nx[4 * q + 3], mc);
+                u[q] = u[q] + __shfl_xor(u[q], 32);
+            }
+            const float M2 = (u[0] + u[1]) + (u[2] + u[3]);
+            const int64_t m = mb0 + lane % 32;
+            if (half == 0 && m < p.M) p.lnp[m * (p.N / 32) + nb0 / 32] = make_float2(S, M2);
+        }
+    }
 }
 
 // Staged epilogue of the W4A4 GEMM's bf16 outputs (bf16, GELU, gated residual) for a wave's 64 x 64 subtiles.
@@ -342,6 +376,23 @@ __device__ __forceinline__ void finish_tile_rows(const GemmArgs& p, f32x16 (&acc
                 rw[d] = f32_to_bf16(o0 + y0 * g[2 * d]) | (uint32_t(f32_to_bf16(o1 + y1 * g[2 * d + 1])) << 16);
             }
             w = make_uint4(rw[0], rw[1], rw[2], rw[3]);
+            if (p.lnp) {  // this token's chunk (nb0 + 8 rc) / 32: lanes rc % 4 = 0..3 hold its quads 0-1 .. 6-7
+                const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+                float v[8];
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    v[2 * d] = bf16_to_f32(uint16_t(ww[d]));
+                    v[2 * d + 1] = bf16_to_f32(uint16_t(ww[d] >> 16));
+                }
+                float S = quad_sum(v[0], v[1], v[2], v[3]) + quad_sum(v[4], v[5], v[6], v[7]);
+                S = S + __shfl_xor(S, 1);
+                S = S + __shfl_xor(S, 2);
+                const float mc = S * (1.0f / 32);
+                float M2 = quad_sq(v[0], v[1], v[2], v[3], mc) + quad_sq(v[4], v[5], v[6], v[7], mc);
+                M2 = M2 + __shfl_xor(M2, 1);
+                M2 = M2 + __shfl_xor(M2, 2);
+                if (rc % 4 == 0 && m < p.M) p.lnp[m * (p.N / 32) + (nb0 + 8 * rc) / 32] = make_float2(S, M2);
+            }
         }
         if (m < p.M) *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.out) + m * p.ldo + nb0 + 8 * rc) = w;
     }
@@ -1351,7 +1402,7 @@ extern "C" int64_t wdl_w4a4_gemm_workspace_bytes(int64_t Mp, int64_t N, int64_t 
 extern "C" int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wcodes, const void* wscales,
                              const float* lora, const void* proj_up, const void* bias, int64_t M, int64_t Mp,
                              int64_t N, int64_t K, int64_t rank, void* out, int64_t ldo, int epilogue,
-                             const float* gate, void* workspace, hipStream_t stream) {
+                             const float* gate, float* ln_partials, void* workspace, hipStream_t stream) {
     if (M < 0 || Mp < M || Mp % 128 || N <= 0 || N % 128 || K <= 0 || K % 64 || K > (int64_t(1) << 30) || ldo < N ||
         ldo % 4)
         return fail(WDL_EINVAL, "w4a4_gemm: bad shape M=%lld Mp=%lld N=%lld K=%lld ldo=%lld", (long long)M,
@@ -1367,11 +1418,14 @@ extern "C" int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wc
         reinterpret_cast<uintptr_t>(lora) % 16 || (epilogue != EPI_F32 && ldo % 8))
         return fail(WDL_EINVAL, "w4a4_gemm: out, gate, lora and proj_up must be 16-byte aligned, bias 8-byte, and "
                                 "bf16 output rows a multiple of 8 elements");
+    if (ln_partials && (epilogue != EPI_RESIDUAL || reinterpret_cast<uintptr_t>(ln_partials) % 8))
+        return fail(WDL_EINVAL, "w4a4_gemm: LayerNorm partials come with the residual epilogue, 8-byte aligned");
     if (M == 0) return WDL_OK;
     GemmArgs a{static_cast<const uint8_t*>(qa), static_cast<const uint16_t*>(ascales),
                static_cast<const uint8_t*>(wcodes), static_cast<const uint32_t*>(wscales), lora,
                static_cast<const uint16_t*>(proj_up), static_cast<const uint16_t*>(bias), M, Mp, N, K, out, ldo,
                gate, nullptr, nullptr, static_cast<float*>(workspace)};
+    a.lnp = reinterpret_cast<float2*>(ln_partials);
     if (reinterpret_cast<uintptr_t>(workspace) % 16)
         return fail(WDL_EINVAL, "w4a4_gemm: workspace must be 16-byte aligned");
     return dispatch(a, epilogue, stream);

@@ -26,14 +26,14 @@ SIGNATURES: dict[str, list] = {
                           c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_ptr],
     "wdl_act_quant_workspace_floats": [c_i64, c_i64],
     "wdl_act_quant_w4": [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_f32, c_int, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_i64,
-                         c_ptr, c_ptr, c_ptr, c_ptr, c_int, c_f32, c_ptr, c_ptr, c_ptr],
+                         c_ptr, c_ptr, c_ptr, c_ptr, c_int, c_f32, c_ptr, c_ptr, c_ptr, c_ptr],
     "wdl_act_quant_w4_static": [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_f32, c_int, c_ptr, c_i64, c_ptr, c_ptr, c_ptr,
-                                c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_int, c_f32, c_ptr, c_ptr],
+                                c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_int, c_f32, c_ptr, c_ptr, c_ptr],
     "wdl_w4a4_weight_codes": [c_ptr, c_i64, c_i64, c_ptr, c_ptr],
     "wdl_w4a4_scale_pairs": [c_ptr, c_int, c_i64, c_ptr, c_ptr],
     "wdl_w4a4_gemm_workspace_bytes": [c_i64, c_i64, c_i64],
     "wdl_w4a4_gemm": [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_ptr,
-                      c_i64, c_int, c_ptr, c_ptr, c_ptr],
+                      c_i64, c_int, c_ptr, c_ptr, c_ptr, c_ptr],
     "wdl_w4a4_gemm_gelu_quant_workspace_floats": [c_i64, c_i64],
     "wdl_w4a4_gemm_gelu_quant": [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64,
                                  c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr],

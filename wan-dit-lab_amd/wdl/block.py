@@ -67,24 +67,28 @@ class QuantizedWanBlock:
         t = self.p[name]
         return ops.act_quant_launch(x, t["smooth"], t["proj_down"], shift, unsigned, ln=ln)
 
-    def _gemm(self, qa, name, M, out, epilogue=EPI_BF16, gate=None):
+    def _gemm(self, qa, name, M, out, epilogue=EPI_BF16, gate=None, ln_out=None):
         t = self.p[name]
         q, asc, lora = qa
         return ops.gemm_launch(q, asc, lora, t["wcodes"], t["wspairs"], t["proj_up"], t["bias"], M, out, epilogue,
-                               gate)
+                               gate, ln_out=ln_out)
 
-    def _apply(self, x, name, out, epilogue=EPI_BF16, gate=None, ln=None):
+    def _apply(self, x, name, out, epilogue=EPI_BF16, gate=None, ln=None, ln_out=None):
         """out (or out += gate * y with EPI_RESIDUAL) for the linear `name` of x (normalized and modulated first
-        when ln is given), W4A4 or FP8 weight-only."""
+        when ln is given), W4A4 or FP8 weight-only. ln_out (residual): a buffer for the LayerNorm chunk partials of
+        the updated rows; returns it when the W4A4 epilogue filled it, else None (the FP8 weight-only GEMM forms
+        none)."""
         t = self.p[name]
         if "fp8" in t:
             if ln is not None:  # the quantizer kernel's bf16 copy of the normalized, modulated input
                 v = torch.empty_like(x)
                 ops.act_quant_launch(x, self.ones_bf16, None, ln=ln, v_out=v)
                 x = v
-            return fp8.weight_only_gemm(x, t["fp8"], t["fp8_scale"], t["bias"], out=out,
-                                        gate=gate if epilogue == EPI_RESIDUAL else None)
-        return self._gemm(self._quant(x, name, ln=ln), name, x.shape[0], out, epilogue, gate)
+            fp8.weight_only_gemm(x, t["fp8"], t["fp8_scale"], t["bias"], out=out,
+                                 gate=gate if epilogue == EPI_RESIDUAL else None)
+            return None
+        self._gemm(self._quant(x, name, ln=ln), name, x.shape[0], out, epilogue, gate, ln_out=ln_out)
+        return ln_out
 
     def out_features(self, name):
         t = self.p[name]
@@ -92,7 +96,8 @@ class QuantizedWanBlock:
 
     def linear(self, x, name):
         out = torch.empty(x.shape[0], self.out_features(name), device=x.device, dtype=torch.bfloat16)
-        return self._apply(x, name, out)
+        self._apply(x, name, out)
+        return out
 
     def prepare_context(self, C: torch.Tensor) -> dict:
         """Cross-attention keys and values of a prompt, once per prompt (multi_head_attention.py:21-26;
@@ -117,23 +122,29 @@ class QuantizedWanBlock:
         return self._zero_freq
 
     # --------------------------------------------------------------------------------------- forward
-    def forward(self, X: torch.Tensor, e: torch.Tensor, grid, freq, start_frame: int, cache: KVCache, ctx: dict):
-        """X bf16 [M, dim] (updated in place and returned); e fp32 [6, dim] = time_in + modulation."""
+    def forward(self, X: torch.Tensor, e: torch.Tensor, grid, freq, start_frame: int, cache: KVCache, ctx: dict,
+                ln_in=None, ln_out=None):
+        """X bf16 [M, dim] (updated in place and returned); e fp32 [6, dim] = time_in + modulation.
+        ln_in: the LayerNorm chunk partials of X (fp32 [M, dim / 32, 2], as the previous block's ln_out), or None;
+        ln_out: a buffer of that shape that receives them for the returned X (the feed-forward's residual GEMM
+        writes them), or None. Each LayerNorm-fused quantization of the block takes its partials from the residual
+        GEMM that wrote X before it where that GEMM is W4A4, and forms them itself otherwise."""
         M, D = X.shape
         H = self.heads
         sh_a, sc_a, g_a, sh_f, sc_f, g_f = e
         dev = X.device
+        lnp = torch.empty(2, M, D // 32, 2, device=dev, dtype=torch.float32)  # after o, after cross-o
         # self-attention
         qkv = torch.empty(M, 3 * D, device=dev, dtype=torch.bfloat16)
-        self._apply(X, "qkv", qkv, ln=dict(shift=sh_a, scale=sc_a, eps=self.eps))
+        self._apply(X, "qkv", qkv, ln=dict(shift=sh_a, scale=sc_a, eps=self.eps, partials=ln_in))
         Q, K = ops.qk_norm_rope_launch(qkv[:, :D], qkv[:, D:2 * D], self.p["wq"], self.p["wk"], freq, grid,
                                        start_frame, self.eps)
         V = qkv[:, 2 * D:]
         A = cache.attend(Q.view(1, M, H, 128), K.view(1, M, H, 128), V.view(1, M, H, 128))
-        self._apply(A.view(M, D), "o", X, EPI_RESIDUAL, g_a)
+        p_o = self._apply(A.view(M, D), "o", X, EPI_RESIDUAL, g_a, ln_out=lnp[0])
         # cross-attention over the prompt
         qc = torch.empty(M, D, device=dev, dtype=torch.bfloat16)
-        n3 = dict(weight=self.p["n3w"], bias=self.p["n3b"], eps=self.eps)
+        n3 = dict(weight=self.p["n3w"], bias=self.p["n3b"], eps=self.eps, partials=p_o)
         self._apply(X, "cq", qc, ln=n3)
         Qc, _ = ops.qk_norm_rope_launch(qc, None, self.p["cwq"], None, self._nofreq(dev), (0, 1, 1), 0,
                                         self.eps)
@@ -141,14 +152,14 @@ class QuantizedWanBlock:
             Ac = ops.attn_bf16_launch(Qc, ctx, 128 ** -0.5)
         else:
             Ac = ops.sage_attn_q16_launch(Qc, ctx, ctx["L"], 128 ** -0.5)
-        self._apply(Ac, "co", X, EPI_RESIDUAL, self.ones)
+        p_co = self._apply(Ac, "co", X, EPI_RESIDUAL, self.ones, ln_out=lnp[1])
         # feed forward: the fused W4A4 GELU MLP (the hidden layer goes from the first GEMM's epilogue to the second
         # GEMM as int4 codes, scales and low-rank sums)
-        q, asc, lora = self._quant(X, "ffn1", ln=dict(shift=sh_f, scale=sc_f, eps=self.eps))
+        q, asc, lora = self._quant(X, "ffn1", ln=dict(shift=sh_f, scale=sc_f, eps=self.eps, partials=p_co))
         t1, t2 = self.p["ffn1"], self.p["ffn2"]
         hq = ops.gelu_quant_launch(q, asc, lora, t1["wcodes"], t1["wspairs"], t1["proj_up"], t1["bias"], M,
                                    t2["smooth"], t2["proj_down"])
-        self._gemm(hq, "ffn2", M, X, EPI_RESIDUAL, g_f)
+        self._gemm(hq, "ffn2", M, X, EPI_RESIDUAL, g_f, ln_out=ln_out)
         return X
 
 

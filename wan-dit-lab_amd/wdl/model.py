@@ -174,8 +174,13 @@ class DiTModel:
         X = self.edges.patchify(x)
         t_emb, e0 = self.edges.time(t)
         e_all = e0 + self.modulation
-        for blk, cache, ctx, e in zip(self.blocks, self.caches, self.ctx, e_all):
-            blk.forward(X, e, grid, self.freq, start_frame, cache, ctx)
+        # each block's feed-forward residual GEMM writes the LayerNorm chunk partials of X for the next block's first
+        # LayerNorm (two buffers in turn); block 0 forms its own
+        lnb = torch.empty(2, X.shape[0], X.shape[1] // 32, 2, device=X.device, dtype=torch.float32)
+        ln_in = None
+        for i, (blk, cache, ctx, e) in enumerate(zip(self.blocks, self.caches, self.ctx, e_all)):
+            blk.forward(X, e, grid, self.freq, start_frame, cache, ctx, ln_in=ln_in, ln_out=lnb[i % 2])
+            ln_in = lnb[i % 2]
         return self.edges.head(X, t_emb, grid)
 
 

@@ -65,7 +65,8 @@ def act_quant_launch(x, smooth, proj_down_t, qshift=0.0, unsigned=False, *, ln=N
     """x bf16 [M, K] (rows 16-byte aligned) -> (q fp6 codes of the int4 values, tile-blocked uint8
     [Mp/128, K/64, 128, 48] (decode_acts gives the [Mp, K] integers), ascales bf16 [K/64, Mp], lora fp32 [Mp, 32]
     or None).
-    ln: dict(shift, scale, weight, bias, eps) fuses LayerNorm + modulation."""
+    ln: dict(shift, scale, weight, bias, eps, partials) fuses LayerNorm + modulation; partials: the LayerNorm chunk
+    partials of x (fp32 [M, K / 32, 2], as gemm_launch's ln_out writes them), or None to form them here."""
     M, K = x.shape
     Mp = padded_rows(M)
     q = torch.empty(Mp // BLOCK, K // 64, BLOCK, ROW6, device=x.device, dtype=torch.uint8)
@@ -75,8 +76,8 @@ def act_quant_launch(x, smooth, proj_down_t, qshift=0.0, unsigned=False, *, ln=N
     ws = torch.empty(_lib.library().wdl_act_quant_workspace_floats(Mp, K), device=x.device, dtype=torch.float32)
     _lib.call("wdl_act_quant_w4", ptr(x), x.stride(0), M, K, ptr(smooth), float(qshift), int(unsigned),
               ptr(proj_down_t), RANK, ptr(q), ptr(ascales), ptr(lora), Mp, ptr(ln.get("shift")), ptr(ln.get("scale")),
-              ptr(ln.get("weight")), ptr(ln.get("bias")), int(bool(ln)), float(ln.get("eps", 1e-6)), ptr(v_out),
-              ptr(ws), stream_of(x))
+              ptr(ln.get("weight")), ptr(ln.get("bias")), int(bool(ln)), float(ln.get("eps", 1e-6)),
+              ptr(ln.get("partials")), ptr(v_out), ptr(ws), stream_of(x))
     return q, ascales, lora
 
 
@@ -225,10 +226,11 @@ def as_codes(qweight: torch.Tensor, K: int) -> torch.Tensor:
 
 
 def gemm_launch(q, ascales, lora, wcodes, wscales, proj_up, bias, M, out, epilogue=EPI_BF16, gate=None,
-                stream_k=True):
+                stream_k=True, ln_out=None):
     """W4A4 GEMM on the quantizer's outputs (q, ascales, lora) and tile-blocked fp6 weight codes (weight_codes);
     wscales: the scale pairs (scale_pairs), or bf16 / fp16 scales (converted once per tensor, cached_scale_pairs).
-    stream_k=False runs the one-pass launch also for the shapes that the library splits in K."""
+    stream_k=False runs the one-pass launch also for the shapes that the library splits in K. ln_out (with the
+    gated residual): fp32 [M, N / 32, 2] receiving the LayerNorm chunk partials of the updated rows of out."""
     wscales = cached_scale_pairs(wscales)
     if q.dim() != 4 or wcodes.dim() != 4 or q.shape[2:] != (BLOCK, ROW6) or wcodes.shape[2:] != (BLOCK, ROW6):
         raise ValueError("the W4A4 GEMM takes tile-blocked fp6 operands [rows/128, K/64, 128, 48]")
@@ -238,8 +240,11 @@ def gemm_launch(q, ascales, lora, wcodes, wscales, proj_up, bias, M, out, epilog
         raise ValueError(f"weight codes {tuple(wcodes.shape)} do not match activations of width {K}")
     nbytes = _lib.library().wdl_w4a4_gemm_workspace_bytes(Mp, N, K) if stream_k else 0
     ws = workspace(_GEMM_WS, q.device, nbytes) if nbytes else None
+    if ln_out is not None and (ln_out.dtype != torch.float32 or not ln_out.is_contiguous() or
+                               ln_out.numel() < M * (N // 32) * 2 or out.shape[-1] != N):
+        raise ValueError(f"ln_out: a contiguous fp32 [{M}, {N // 32}, 2] buffer for whole output rows of {N}")
     _lib.call("wdl_w4a4_gemm", ptr(q), ptr(ascales), ptr(wcodes), ptr(wscales), ptr(lora), ptr(proj_up), ptr(bias),
-              M, Mp, N, K, RANK, ptr(out), out.stride(0), epilogue, ptr(gate), ptr(ws), stream_of(q))
+              M, Mp, N, K, RANK, ptr(out), out.stride(0), epilogue, ptr(gate), ptr(ln_out), ptr(ws), stream_of(q))
     return out
 
 
