@@ -61,12 +61,6 @@ __device__ __forceinline__ void load8(const uint16_t* p, float* f) {
     }
 }
 
-__device__ __forceinline__ float butterfly64(float s) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s = s + __shfl_xor(s, o);
-    return s;
-}
-
 // ((t0 + t1) + (t2 + t3)) + ((t4 + t5) + (t6 + t7)) of the 8 quad sums of a chunk
 __device__ __forceinline__ float tree8(const float* t) {
     return ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
@@ -203,9 +197,7 @@ __global__ __launch_bounds__(64 * WAVES) void quant_kernel(QuantArgs a) {
 #pragma unroll
         for (int i = 0; i < MAXCP; ++i)
             if (i < ncp) sum = sum + cp[i].x;
-        sum = sum + __shfl_xor(sum, 1);
-        sum = sum + __shfl_xor(sum, 2);
-        sum = sum + __shfl_xor(sum, 4);
+        sum = xor_sum<4>(xor_sum<2>(xor_sum<1>(sum)));
         const float mean = sum / float(K);
         float m2 = 0.0f;
 #pragma unroll
@@ -214,9 +206,7 @@ __global__ __launch_bounds__(64 * WAVES) void quant_kernel(QuantArgs a) {
                 const float d = cp[i].x * (1.0f / LN_CHUNK) - mean;
                 m2 = m2 + (cp[i].y + float(LN_CHUNK) * (d * d));
             }
-        m2 = m2 + __shfl_xor(m2, 1);
-        m2 = m2 + __shfl_xor(m2, 2);
-        m2 = m2 + __shfl_xor(m2, 4);
+        m2 = xor_sum<4>(xor_sum<2>(xor_sum<1>(m2)));
         if (lane % 8 == 0) sst[8 * wave + lane / 8] = make_float2(mean, 1.0f / sqrtf(m2 / float(K) + a.eps));
     }
     __syncthreads();
@@ -296,7 +286,7 @@ __global__ __launch_bounds__(64 * WAVES) void quant_kernel(QuantArgs a) {
                 amax = fmaxf(amax, fabsf(u[k]));
             }
         }
-        amax = fmaxf(amax, __shfl_xor(amax, 32));  // the group's other half
+        amax = xor_max<32>(amax);  // the group's other half
         const uint16_t sb = f32_to_bf16(amax / qmax);
         const float sc = bf16_to_f32(sb);
         const float rsc = sc > 0.0f ? 1.0f / sc : 0.0f;

@@ -165,11 +165,7 @@ __global__ __launch_bounds__(128 * WPG) void attn_bf16_kernel(Args a) {
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[j][r]);
-        {  // the other lane half's maximum: v_permlane32_swap gives each lane its own and the other value (no LDS
-           // round trip)
-            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-            mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-        }
+        mx = xor_max<32>(mx);  // the other lane half's maximum
         const float mn = fmaxf(m, mx * a.scale_log2);
         const float alpha = __builtin_amdgcn_exp2f(m - mn);  // m = -inf on the first block: 0
         float ls = 0.0f;
@@ -238,9 +234,7 @@ __global__ __launch_bounds__(128 * WPG) void attn_bf16_kernel(Args a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) o[ds][e] = o[ds][e] * a0 + xo[(ds * 16 + e) * 64 + lane] * a1;
     }
-    // the two lane halves summed different keys (own + other, in an order that depends on the half: the same sum)
-    const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
-    const float lt = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
+    const float lt = xor_sum<32>(l);  // the two lane halves summed different keys
     const float inv = 1.0f / lt;
     // The wave's 32 x 128 bf16 outputs go through its own LDS area (the hand-over slot it has just read, or for a
     // dual workgroup a slot per wave), rows of 272 bytes, and leave as whole 256-byte query rows: 16 bytes per lane,

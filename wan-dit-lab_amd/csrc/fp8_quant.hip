@@ -88,8 +88,7 @@ __global__ __launch_bounds__(64 * WPR) void rows_kernel(const T* x, int64_t ldx,
 #pragma unroll
         for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[e]));
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    amax = group_max<64>(amax);
     if (WPR > 1) {
         if (t % 64 == 0) red[t / 64] = amax;
         __syncthreads();
@@ -134,8 +133,7 @@ __global__ __launch_bounds__(256) void tensor_max_kernel(const T* x, int64_t ldx
 #pragma unroll
         for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[e]));
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    amax = group_max<64>(amax);
     if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = amax;
     __syncthreads();
     if (threadIdx.x == 0) partial[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -147,8 +145,7 @@ __global__ __launch_bounds__(256) void tensor_quant_kernel(const T* x, int64_t l
     __shared__ float red[4];
     float amax = 0.0f;
     for (int i = threadIdx.x; i < nparts; i += 256) amax = fmaxf(amax, partial[i]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    amax = group_max<64>(amax);
     if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = amax;
     __syncthreads();
     const float s = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), 1e-12f) / FP8_MAX;

@@ -149,8 +149,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs a) {
                 if (i0 + k < i1) t = t + v * v;
             }
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) t = t + __shfl_xor(t, o);
+        t = group_sum<64>(t);
         if (lane == 0) srstd[slot] = 1.0f / sqrtf(t / float(a.C) + a.eps);
     }
     __syncthreads();
@@ -218,9 +217,7 @@ __global__ __launch_bounds__(256) void quant_q_kernel(const uint16_t* x, int64_t
         }
     }
     // group of lane l8 = tok % 8: tokens l8 + 8k -> lanes 2 * l8 + 16 k + dh: xor over lane bits 0, 4, 5
-    amax = fmaxf(amax, __shfl_xor(amax, 1));
-    amax = fmaxf(amax, __shfl_xor(amax, 16));
-    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    amax = xor_max<32>(xor_max<16>(xor_max<1>(amax)));
     const float scale = amax / 127.0f + 1e-7f;
     if (lane < 16 && (lane % 2) == 0) q_scale[h * blocks * 8 + blk * 8 + lane / 2] = scale;
     if (!live) return;

@@ -379,9 +379,7 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
                     amax = fmaxf(amax, fmaxf(fabsf(x[c][2 * e]), fabsf(x[c][2 * e + 1])));
                 }
             }
-            amax = fmaxf(amax, __shfl_xor(amax, 8));
-            amax = fmaxf(amax, __shfl_xor(amax, 16));
-            amax = fmaxf(amax, __shfl_xor(amax, 32));
+            amax = xor_max<32>(xor_max<16>(xor_max<8>(amax)));
             const float scale = amax / 127.0f + 1e-7f;
             // x / scale through the reciprocal (div_rn: the IEEE quotient wherever |x / scale| >= 2^-126, and below
             // that both round to a zero code)

@@ -80,19 +80,6 @@ struct GemmArgs {
 // values written. The staged epilogue holds 8 consecutive values per lane (quads 2a, 2a + 1 of a chunk, a = lane
 // % 4 of a 4-lane group), the MFMA layout 4 per lane half (quad 2q + half of quarter q).
 __device__ __forceinline__ float quad_sum(float a, float b, float c, float d) { return ((a + b) + c) + d; }
-// x + x of lane ^ 1 (^ 2): a DPP quad permutation, a register exchange with no LDS round trip (ds_bpermute)
-__device__ __forceinline__ float add_xor1(float x) {
-    return x + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, true));  // [1, 0, 3, 2]
-}
-__device__ __forceinline__ float add_xor2(float x) {
-    return x + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, true));  // [2, 3, 0, 1]
-}
-// x + x of lane ^ 32 (the same sum in both lanes: v_permlane32_swap of x with itself gives each lane its own value
-// and the other half's, in an order that depends on the half, and the sum of two floats does not)
-__device__ __forceinline__ float add_xor32(float x) {
-    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
-}
 __device__ __forceinline__ float quad_sq(float a, float b, float c, float d, float m) {
     const float da = a - m, db = b - m, dc = c - m, dd = d - m;
     return ((da * da + db * db) + dc * dc) + dd * dd;
@@ -264,13 +251,13 @@ __device__ __forceinline__ void finish_tile(const GemmArgs& p, f32x16 (&acc)[TN]
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 t[q] = quad_sum(nx[4 * q], nx[4 * q + 1], nx[4 * q + 2], nx[4 * q + 3]);
-                t[q] = add_xor32(t[q]);  // quads 2 q + 2 q + 1
+                t[q] = xor_sum<32>(t[q]);  // quads 2 q + 2 q + 1
             }
             const float S = (t[0] + t[1]) + (t[2] + t[3]), mc = S * (1.0f / 32);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 u[q] = quad_sq(nx[4 * q], nx[4 * q + 1], nx[4 * q + 2], nx[4 * q + 3], mc);
-                u[q] = add_xor32(u[q]);
+                u[q] = xor_sum<32>(u[q]);
             }
             const float M2 = (u[0] + u[1]) + (u[2] + u[3]);
             const int64_t m = mb0 + lane % 32;
@@ -398,10 +385,10 @@ __device__ __forceinline__ void finish_tile_rows(const GemmArgs& p, f32x16 (&acc
                     v[2 * d + 1] = bf16_to_f32(uint16_t(ww[d] >> 16));
                 }
                 float S = quad_sum(v[0], v[1], v[2], v[3]) + quad_sum(v[4], v[5], v[6], v[7]);
-                S = add_xor2(add_xor1(S));
+                S = xor_sum<2>(xor_sum<1>(S));
                 const float mc = S * (1.0f / 32);
                 float M2 = quad_sq(v[0], v[1], v[2], v[3], mc) + quad_sq(v[4], v[5], v[6], v[7], mc);
-                M2 = add_xor2(add_xor1(M2));
+                M2 = xor_sum<2>(xor_sum<1>(M2));
                 if (rc % 4 == 0 && m < p.M) p.lnp[m * (p.N / 32) + (nb0 + 8 * rc) / 32] = make_float2(S, M2);
             }
         }
@@ -544,10 +531,7 @@ __device__ __forceinline__ void finish_tile_gelu_quant(const GemmArgs& p, f32x16
                 u[i][k] = div_rn(acc[i][j][k] + GELU_SHIFT, smooth_at(smv[i][k / 4], k % 4), rsm[i][k]);
                 amax = fmaxf(amax, fabsf(u[i][k]));
             }
-        {  // the group's other 32 features (v_permlane32_swap: own and other value, in either order)
-            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(amax), __float_as_uint(amax), false, false);
-            amax = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-        }
+        amax = xor_max<32>(amax);  // the group's other 32 features
         const uint16_t sb = f32_to_bf16(amax / 15.0f);
         const float sc = bf16_to_f32(sb);
         const float rsc = sc > 0.0f ? 1.0f / sc : 0.0f;

@@ -151,17 +151,65 @@ __device__ __forceinline__ float load_as_f32<half_tag>(const void* p, int64_t i)
 
 // ---------------------------------------------------------------- wavefront reductions (64 lanes)
 
+// Lane exchanges in registers, not through the LDS crossbar (ds_bpermute, a round trip of the LDS pipeline):
+// lane_xor<O> (O = 1, 2, 4, 8) is the value of lane ^ O by DPP within rows of 16 lanes; across rows (O = 16, 32)
+// v_permlane16_swap / v_permlane32_swap of a value with itself give each lane its own value and that of lane ^ O,
+// in an order that depends on the lane, so they serve commutative combinations only (xor_sum, xor_max: for every
+// O the result equals v op (v of lane ^ O), bit for bit).
+template <int O>
+__device__ __forceinline__ float lane_xor(float v) {
+    static_assert(O == 1 || O == 2 || O == 4 || O == 8, "within a row of 16 lanes");
+    const int x = __float_as_int(v);
+    if constexpr (O == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, true));  // [1,0,3,2]
+    if constexpr (O == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, true));  // [2,3,0,1]
+    if constexpr (O == 4)  // half-row mirror (i -> i ^ 7), then quad [3,2,1,0] (i -> i ^ 3)
+        return __int_as_float(
+            __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, true), 0x1B, 0xF, 0xF, true));
+    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, true));  // row rotate by 8: i -> i ^ 8
+}
+
+template <int O>
+__device__ __forceinline__ float xor_sum(float v) {
+    if constexpr (O == 16 || O == 32) {
+        const auto s = O == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false)
+                               : __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+    } else {
+        return v + lane_xor<O>(v);
+    }
+}
+
+template <int O>
+__device__ __forceinline__ float xor_max(float v) {
+    if constexpr (O == 16 || O == 32) {
+        const auto s = O == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false)
+                               : __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+    } else {
+        return fmaxf(v, lane_xor<O>(v));
+    }
+}
+
+// butterfly over groups of WIDTH lanes (WIDTH / 2 first, down to 1)
 template <int WIDTH>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int o = WIDTH / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WIDTH));
+    if constexpr (WIDTH >= 64) v = xor_max<32>(v);
+    if constexpr (WIDTH >= 32) v = xor_max<16>(v);
+    if constexpr (WIDTH >= 16) v = xor_max<8>(v);
+    if constexpr (WIDTH >= 8) v = xor_max<4>(v);
+    if constexpr (WIDTH >= 4) v = xor_max<2>(v);
+    if constexpr (WIDTH >= 2) v = xor_max<1>(v);
     return v;
 }
 
 template <int WIDTH>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int o = WIDTH / 2; o > 0; o >>= 1) v = v + __shfl_xor(v, o, WIDTH);
+    if constexpr (WIDTH >= 64) v = xor_sum<32>(v);
+    if constexpr (WIDTH >= 32) v = xor_sum<16>(v);
+    if constexpr (WIDTH >= 16) v = xor_sum<8>(v);
+    if constexpr (WIDTH >= 8) v = xor_sum<4>(v);
+    if constexpr (WIDTH >= 4) v = xor_sum<2>(v);
+    if constexpr (WIDTH >= 2) v = xor_sum<1>(v);
     return v;
 }
 
