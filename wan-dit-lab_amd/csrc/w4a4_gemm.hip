@@ -41,13 +41,15 @@ enum Epilogue {
 };
 constexpr float GELU_SHIFT = 0.171875f;  // quantization/w4a4.py:195: GELU(x) > -0.17, so GELU(x) + shift >= 0
 
-// GELU, tanh form: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), tanh(u) = 1 - 2 / (exp(2u) + 1) with the
-// hardware exp2 and reciprocal (about 1 ulp each; exp(2u) -> inf gives tanh 1, -> 0 gives -1)
+// GELU, tanh form: 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3), computed as the identical
+// x / (1 + exp(-2u)) with exp(-2u) = 2^(x (C1 + C2 x^2)) on the hardware exp2 and reciprocal (about 1 ulp each).
+// Unlike 1 + tanh(u) it does not cancel for negative x. Large negative x: exp -> inf, x * 0 = -0; large positive
+// x: exp -> 0, x.
 __device__ __forceinline__ float gelu_tanh(float x) {
-    const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-    const float e = __builtin_amdgcn_exp2f(u * 2.8853900817779268f);  // exp(2u) = 2^(2u log2 e)
-    const float th = fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
-    return 0.5f * x * (1.0f + th);
+    constexpr float C1 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;  // -2 sqrt(2/pi) log2(e)
+    constexpr float C2 = C1 * 0.044715f;
+    const float e = __builtin_amdgcn_exp2f(x * fmaf(C2, x * x, C1));
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 struct GemmArgs {
@@ -474,7 +476,23 @@ __device__ __forceinline__ void finish_tile_gelu_quant(const GemmArgs& p, f32x16
                 for (int i = 0; i < TN; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[i][h], lb, acc[i][j], 0, 0, 0);
             }
     }
-    float rsm[TN][16];  // IEEE reciprocals of smooth2 at the lane's features
+    // IEEE reciprocals of smooth2 at the lane's 32 features: lane l divides once, for the wave's feature nb0 + l,
+    // into the wave's 256-byte LDS slot past the exchange area, and reads back the 32 it needs (the 32 lanes of a
+    // half need the same ones; one wave's LDS accesses complete in order)
+    float* const rslot = xch + 4 * TM * 16 * 64 + (wm * 2 + wn) * 64;
+    rslot[lane] = 1.0f / bf16_to_f32(p.sm2[nb0 + lane]);
+    asm volatile("" ::: "memory");
+    float rsm[TN][16];
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 r4 = *reinterpret_cast<const float4*>(rslot + i * 32 + 8 * q + 4 * half);
+            rsm[i][4 * q] = r4.x;
+            rsm[i][4 * q + 1] = r4.y;
+            rsm[i][4 * q + 2] = r4.z;
+            rsm[i][4 * q + 3] = r4.w;
+        }
 #pragma unroll
     for (int i = 0; i < TN; ++i)
 #pragma unroll
@@ -483,7 +501,6 @@ __device__ __forceinline__ void finish_tile_gelu_quant(const GemmArgs& p, f32x16
                                     uint16_t(bias[i][q].y >> 16)};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                rsm[i][4 * q + e] = 1.0f / smooth_at(smv[i][q], e);
 #pragma unroll
                 for (int j = 0; j < TM; ++j) {
                     float y = acc[i][j][4 * q + e];
@@ -948,7 +965,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         if constexpr (EPI == EPI_GELU_QUANT) {
             static_assert(W4 && BN == 128 && BM == 128 && NW == 4, "the fused GELU epilogue runs on 128 x 128 tiles");
             __syncthreads();  // every wave is past its last read of the ring, whose LDS the exchange reuses
-            static_assert(4 * 2 * 16 * 64 * 4 <= STAGES * CS, "exchange fits in the ring");
+            static_assert((4 * 2 * 16 * 64 + 4 * 64) * 4 <= STAGES * CS, "exchange and reciprocals fit in the ring");
             finish_tile_gelu_quant<TN, TM>(p, acc, n0 + wn * WN, m0 + wm * WM, wn, wm, lane,
                                            reinterpret_cast<float*>(&sC[0][0]));
         } else if constexpr (W4 && EPI != EPI_F32 && TN == 2 && TM == 2) {
