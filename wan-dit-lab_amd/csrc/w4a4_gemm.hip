@@ -413,9 +413,11 @@ __device__ __forceinline__ void finish_tile_rows(const GemmArgs& p, f32x16 (&acc
 // h split exactly into bf16 hi + lo parts (two MFMAs per 16 features, about 16 significant bits of h) with the
 // k-slots of both operands mapped to the features the lane already holds. Rows m >= M get zero codes, scales and
 // partials.
-// element e (0..3) of four packed bf16 values, as fp32
-__device__ __forceinline__ float smooth_at(uint2 v, int e) {
-    return bf16_to_f32(uint16_t(e < 2 ? (e ? v.x >> 16 : v.x) : (e == 3 ? v.y >> 16 : v.y)));
+// div_rn for w > 0 or w = +0, whose quotient needs no sign fix-up: here u = (GELU(y) + 0.171875) / s with GELU
+// above -0.1700, and u / scale with u > 0 (with r = 0 the result is +0)
+__device__ __forceinline__ float div_rn_pos(float w, float d, float r) {
+    const float q0 = w * r;
+    return fmaf(fmaf(-q0, d, w), r, q0);
 }
 
 template <int TN, int TM>
@@ -442,7 +444,7 @@ __device__ __forceinline__ void finish_tile_gelu_quant(const GemmArgs& p, f32x16
                 lr[j][h][1] = *reinterpret_cast<const float4*>(l + 4);
             }
     }
-    uint2 bias[TN][4], smv[TN][4];
+    uint2 bias[TN][4];
     uint2 pdv[TN][2][2];  // proj_down2^T row tok: features 32 ti + 16 qp + 8 part + 4 half .. + 3
 #pragma unroll
     for (int i = 0; i < TN; ++i) {
@@ -450,7 +452,6 @@ __device__ __forceinline__ void finish_tile_gelu_quant(const GemmArgs& p, f32x16
         for (int q = 0; q < 4; ++q) {
             const int64_t nb = nb0 + i * 32 + 8 * q + 4 * half;
             bias[i][q] = p.bias ? *reinterpret_cast<const uint2*>(p.bias + nb) : make_uint2(0u, 0u);
-            smv[i][q] = *reinterpret_cast<const uint2*>(p.sm2 + nb);
         }
 #pragma unroll
         for (int qp = 0; qp < 2; ++qp)
@@ -476,22 +477,32 @@ __device__ __forceinline__ void finish_tile_gelu_quant(const GemmArgs& p, f32x16
                 for (int i = 0; i < TN; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[i][h], lb, acc[i][j], 0, 0, 0);
             }
     }
-    // IEEE reciprocals of smooth2 at the lane's 32 features: lane l divides once, for the wave's feature nb0 + l,
-    // into the wave's 256-byte LDS slot past the exchange area, and reads back the 32 it needs (the 32 lanes of a
-    // half need the same ones; one wave's LDS accesses complete in order)
-    float* const rslot = xch + 4 * TM * 16 * 64 + (wm * 2 + wn) * 64;
-    rslot[lane] = 1.0f / bf16_to_f32(p.sm2[nb0 + lane]);
+    // smooth2 and its IEEE reciprocal at the lane's 32 features: lane l loads and divides once, for the wave's
+    // feature nb0 + l, into the wave's 512-byte LDS slot past the exchange area ([64 reciprocals][64 values]), and
+    // reads back the 32 it needs (the 32 lanes of a half need the same ones; one wave's LDS accesses complete in
+    // order)
+    float* const rslot = xch + 4 * TM * 16 * 64 + (wm * 2 + wn) * 128;
+    {
+        const float sv = bf16_to_f32(p.sm2[nb0 + lane]);
+        rslot[lane] = 1.0f / sv;
+        rslot[64 + lane] = sv;
+    }
     asm volatile("" ::: "memory");
-    float rsm[TN][16];
+    float rsm[TN][16], smf[TN][16];
 #pragma unroll
     for (int i = 0; i < TN; ++i)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const float4 r4 = *reinterpret_cast<const float4*>(rslot + i * 32 + 8 * q + 4 * half);
+            const float4 s4 = *reinterpret_cast<const float4*>(rslot + 64 + i * 32 + 8 * q + 4 * half);
             rsm[i][4 * q] = r4.x;
             rsm[i][4 * q + 1] = r4.y;
             rsm[i][4 * q + 2] = r4.z;
             rsm[i][4 * q + 3] = r4.w;
+            smf[i][4 * q] = s4.x;
+            smf[i][4 * q + 1] = s4.y;
+            smf[i][4 * q + 2] = s4.z;
+            smf[i][4 * q + 3] = s4.w;
         }
 #pragma unroll
     for (int i = 0; i < TN; ++i)
@@ -545,20 +556,19 @@ __device__ __forceinline__ void finish_tile_gelu_quant(const GemmArgs& p, f32x16
         for (int i = 0; i < TN; ++i)
 #pragma unroll
             for (int k = 0; k < 16; ++k) {
-                u[i][k] = div_rn(acc[i][j][k] + GELU_SHIFT, smooth_at(smv[i][k / 4], k % 4), rsm[i][k]);
+                u[i][k] = div_rn_pos(acc[i][j][k] + GELU_SHIFT, smf[i][k], rsm[i][k]);
                 amax = fmaxf(amax, fabsf(u[i][k]));
             }
         amax = xor_max<32>(amax);  // the group's other 32 features
         const uint16_t sb = f32_to_bf16(amax / 15.0f);
         const float sc = bf16_to_f32(sb);
-        const float rsc = sc > 0.0f ? 1.0f / sc : 0.0f;
+        // a row past M (or a group of zeros) takes a zero reciprocal: every quotient below is then +0, code 0
+        const float rsc = live && sc > 0.0f ? 1.0f / sc : 0.0f;
 #pragma unroll
         for (int i = 0; i < TN; ++i)
 #pragma unroll
-            for (int k = 0; k < 16; ++k) {  // u becomes q / 2 (an fp6 e2m3 value) of feature 32 i + 8 (k / 4) + 4 half + k % 4
-                const float rq = sc > 0.0f ? __builtin_rintf(div_rn(u[i][k], sc, rsc)) : 0.0f;
-                u[i][k] = live ? fminf(fmaxf(rq, 0.0f), 15.0f) * 0.5f : 0.0f;
-            }
+            for (int k = 0; k < 16; ++k)  // u becomes q / 2 (an fp6 e2m3 value) of feature 32 i + 8 (k / 4) + 4 half + k % 4
+                u[i][k] = fminf(__builtin_rintf(div_rn_pos(u[i][k], sc, rsc)), 15.0f) * 0.5f;
         // lanes l and l + 32 trade: afterwards the first result holds feature 32 half + 8 q + e of the group and
         // the second 32 half + 8 q + 4 + e (the swap exchanges the upper 32 lanes of its first operand with the
         // lower 32 lanes of its second)
@@ -965,7 +975,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         if constexpr (EPI == EPI_GELU_QUANT) {
             static_assert(W4 && BN == 128 && BM == 128 && NW == 4, "the fused GELU epilogue runs on 128 x 128 tiles");
             __syncthreads();  // every wave is past its last read of the ring, whose LDS the exchange reuses
-            static_assert((4 * 2 * 16 * 64 + 4 * 64) * 4 <= STAGES * CS, "exchange and reciprocals fit in the ring");
+            static_assert((4 * 2 * 16 * 64 + 4 * 128) * 4 <= STAGES * CS, "exchange and smooth2 slots fit in the ring");
             finish_tile_gelu_quant<TN, TM>(p, acc, n0 + wn * WN, m0 + wm * WM, wn, wm, lane,
                                            reinterpret_cast<float*>(&sC[0][0]));
         } else if constexpr (W4 && EPI != EPI_F32 && TN == 2 && TM == 2) {
