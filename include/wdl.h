@@ -267,6 +267,18 @@ int wdl_sage_prep_cached(const void* cache_k, const float* cache_ks, const void*
                          int64_t at, int64_t n, const float* cache_stats, int splits, float* workspace, void* k_int8,
                          float* k_scale, void* v_fp8, float* k_mean_out, float* v_scale_out, wdl_stream_t stream);
 
+/* wdl_sage_prep_cached that also appends the chunk to the caches: rows at .. at + n - 1 of cache_k / cache_v (fp8
+ * [capacity, heads, 128]) and cache_ks / cache_vs (fp32 [capacity, heads]) receive k, v as wdl_kv_append_fp8 writes
+ * them (the same bytes and scales), from the values the quantization pass already holds, so the chunk is read once
+ * and the append needs no launch of its own. Replaces KVCache.store followed by KVCache.attend's preparation
+ * (src/wan_dit_lab/generation/causal.py:177-181, 193-220; kernels/cache_fp8.py:59-72 and sage_kv.py:127-134).
+ * Requires at + n <= capacity; rows [0, at) are only read, rows [at, at + n) only written. */
+int wdl_sage_prep_cached_append(void* cache_k, float* cache_ks, void* cache_v, float* cache_vs, int64_t capacity,
+                                const void* k, int64_t ldk, const void* v, int64_t ldv, int64_t heads, int64_t at,
+                                int64_t n, const float* cache_stats, int splits, float* workspace, void* k_int8,
+                                float* k_scale, void* v_fp8, float* k_mean_out, float* v_scale_out,
+                                wdl_stream_t stream);
+
 /* The operands live::sage_sm89 receives from the reference's sage_kv._attend (kernels/sage_kv.py:141-176; schema
  * native/ops/sage_ops.cpp:12-19, 28-31) in wdl_sage_attn's layouts: k_i8 int8 [L, heads, 128] (row stride ldk
  * bytes) -> k_out int8 [heads, Lpad, 128], tokens L..Lpad-1 zero; v_fp8 e4m3 [128, heads, Lpad] (element strides

@@ -5,7 +5,8 @@ attention: Sage prep + attention of 1280 and 1392 queries over a full 9744-key w
 chunk), 24 x 128 heads; prep: the Sage preparation (K mean and V maxima, int8 K and fp8 V of the whole window) of
 the same two shapes; gemm: the W4A4 GEMMs of one block at 1392 tokens (QKV 3072 -> 9216, o 3072 -> 3072 with the
 gated residual, FFN-up 3072 -> 14336 with GELU (bf16 out) and fused with the second layer's quantization, FFN-down 14336 -> 3072 with the gated residual), random weights; quant: the activation quantizer with its low-rank down projection at 1392 tokens
-(K 3072 with the fused LayerNorm and modulation, K 3072 plain, K 14336 unsigned).
+(K 3072 with the fused LayerNorm and modulation, its statistics formed in the launch or from chunk partials given,
+K 3072 plain, K 14336 unsigned).
 Each shape is captured into a HIP graph of 10 launches and replayed; one line per shape with microseconds per
 launch (gemm: the launch the library picks and the one-pass launch, alternated three times, the best of each).
 An optional library path replaces lib/libwdl.so (for comparing builds).
@@ -211,12 +212,16 @@ def quant():
 
     dev, M = "cuda", 1392
     g = torch.Generator(device=dev).manual_seed(0)
-    for name, K, ln, unsigned in (("ln", 3072, True, False), ("plain", 3072, False, False),
-                                  ("unsigned", 14336, False, True)):
+    for name, K, ln, unsigned in (("ln", 3072, True, False), ("ln from partials", 3072, True, False),
+                                  ("plain", 3072, False, False), ("unsigned", 14336, False, True)):
         t = w4a4.random_parts(64, K, dev, g)
         x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
         lnd = dict(shift=torch.randn(K, device=dev, generator=g) * 0.1, scale=torch.randn(K, device=dev,
                    generator=g) * 0.1, weight=None, bias=None, eps=1e-6) if ln else None
+        if name == "ln from partials":  # the chunk partials a residual GEMM epilogue would have written
+            xs = x.float().view(M, K // 32, 32)
+            s = xs.sum(-1)
+            lnd["partials"] = torch.stack((s, ((xs - (s / 32)[..., None]) ** 2).sum(-1)), -1).contiguous()
         us = _replay_us(lambda: ops.act_quant_launch(x, t["smooth"], t["proj_down"], 0.171875 if unsigned else 0.0,
                                                      unsigned, ln=lnd))
         print(f"quant {name} {M}x{K}: {us:.1f} us ({M * K * 2 / us / 1e3:.0f} GB/s of x)", flush=True)

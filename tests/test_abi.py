@@ -25,7 +25,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     for name in declared():
         assert hasattr(lib, name), name
     assert set(declared()) == set(_lib.SIGNATURES)
-    assert lib.wdl_abi_version() == 13
+    assert lib.wdl_abi_version() == 14
     assert lib.wdl_last_error() == b""
 
 

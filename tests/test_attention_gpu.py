@@ -92,6 +92,49 @@ def test_sage_prep_k_and_v(gpu, at, n, H, cached):
     assert torch.equal(p["v"].cpu(), want)
 
 
+@pytest.mark.parametrize("at,n,H", [(200, 150, 3), (0, 130, 2), (64, 64, 2), (63, 1, 2), (8352, 1392, 24)])
+def test_prep_with_append_is_store_then_prep(gpu, at, n, H):
+    """wdl_sage_prep_cached_append (the chunk's cache store inside the preparation pass) against store_kv_fp8
+    (wdl_kv_append_fp8) followed by the unfused preparation: every byte of the caches and their scales equal (rows
+    at .. at + n written, the others untouched), and the Sage operands, K mean and V scales bit-equal."""
+    from wdl import ops, sage_kv
+    from wdl.cache_fp8 import store_kv_fp8
+
+    Q, k, ks, v, vs, at, K, V = setup(at, n, H=H, seed=at + n + 7)
+    ks = ks * 0.5 + torch.rand(ks.shape, generator=torch.Generator().manual_seed(3))
+    vs = vs * 0.25 + torch.rand(vs.shape, generator=torch.Generator().manual_seed(4))
+    k, ks, v, vs, K, V = cuda(k, ks, v, vs, K, V)
+    stats = sage_kv.cache_stats(k, ks, v, vs, at)
+    ka, ksa, va, vsa = (t.clone() for t in (k, ks, v, vs))
+    store_kv_fp8(K, V, ka, ksa, va, vsa, at)
+    pa = ops.sage_prep_launch(ka.view(torch.uint8), ksa, va.view(torch.uint8), vsa, K[0].flatten(1), V[0].flatten(1),
+                              at, want_stats=True, cache_stats=stats)
+    kb, ksb, vb, vsb = (t.clone() for t in (k, ks, v, vs))
+    pb = ops.sage_prep_launch(kb.view(torch.uint8), ksb, vb.view(torch.uint8), vsb, K[0].flatten(1), V[0].flatten(1),
+                              at, want_stats=True, cache_stats=stats, append=True)
+    torch.cuda.synchronize()
+    assert torch.equal(ka.view(torch.uint8), kb.view(torch.uint8)) and torch.equal(va.view(torch.uint8),
+                                                                                      vb.view(torch.uint8))
+    assert torch.equal(ksa, ksb) and torch.equal(vsa, vsb)
+    assert not torch.equal(kb.view(torch.uint8)[:, at:at + n], k.view(torch.uint8)[:, at:at + n])
+    for key in ("k", "k_scale", "v", "v_scale", "k_mean"):
+        assert torch.equal(pa[key], pb[key]), key
+
+
+def test_attend_with_append_refuses_before_writing(gpu):
+    """sage_kv.attend(append=True) checks the store's requirements (rows past the cache here) before any launch."""
+    from wdl import sage_kv
+
+    Q, k, ks, v, vs, at, K, V = setup(100, 64, H=2, seed=11)
+    Q, k, ks, v, vs, K, V = cuda(Q, k, ks, v, vs, K, V)
+    stats = sage_kv.cache_stats(k, ks, v, vs, at)
+    before = k.view(torch.uint8).clone()
+    with pytest.raises(ValueError):
+        sage_kv.attend(Q, k, ks, v, vs, k.shape[1] - 10, K, V, cache_stats=stats, append=True)
+    torch.cuda.synchronize()
+    assert torch.equal(k.view(torch.uint8), before)
+
+
 @pytest.mark.parametrize("at,H", [(0, 2), (1, 3), (63, 2), (200, 3), (8352, 24)])
 def test_cache_stats_against_float64_sums_and_exact_maxima(gpu, at, H):
     """wdl_sage_cache_stats: the K column sums within 1e-5 of the sum of |values| (a token dropped or counted twice

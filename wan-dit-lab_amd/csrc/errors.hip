@@ -42,4 +42,4 @@ int cu_count() {
 
 extern "C" const char* wdl_last_error(void) { return g_message; }
 
-extern "C" int wdl_abi_version(void) { return 13; }
+extern "C" int wdl_abi_version(void) { return 14; }

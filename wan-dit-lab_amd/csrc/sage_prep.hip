@@ -204,9 +204,46 @@ __device__ __forceinline__ void quant_block(const Src& k, const Src& v, int64_t 
     }
 }
 
+// Row `row` of an FP8 cache from 32 channels (dq .. dq + 31) per thread, the 4 threads of a token in consecutive
+// lanes: the arithmetic of wdl_kv_append_fp8 (kv_cache.hip), scale = max(max |x| over the 128 channels, 1e-12) /
+// 448, codes e4m3 of the IEEE quotients x / scale (div_rn on the reciprocal), so the bytes and scales are the
+// same. Every thread takes part in the row maximum; only `on` threads store.
+__device__ __forceinline__ void append_row(const float (&f)[4][8], uint8_t* cache, float* scales, int64_t row, int dq,
+                                           bool on) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(f[c][j]));
+    amax = xor_max<2>(xor_max<1>(amax));  // the token's 4 threads
+    const float scale = fmaxf(amax, 1e-12f) / 448.0f;
+    if (!on) return;
+    const float rs = 1.0f / scale;
+    uint32_t w[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const float* x = f[b / 2] + 4 * (b % 2);
+        w[b] = uint32_t(f32_to_e4m3(div_rn(x[0], scale, rs))) | (uint32_t(f32_to_e4m3(div_rn(x[1], scale, rs))) << 8) |
+               (uint32_t(f32_to_e4m3(div_rn(x[2], scale, rs))) << 16) |
+               (uint32_t(f32_to_e4m3(div_rn(x[3], scale, rs))) << 24);
+    }
+    uint4* dst = reinterpret_cast<uint4*>(cache + row * D + dq);
+    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    if (dq == 0) scales[row] = scale;
+}
+
+// Where the chunk's rows also go into the FP8 caches (Append::k non-null): rows token * H + head, unmapped caches.
+struct Append {
+    uint8_t* k;
+    float* ks;
+    uint8_t* v;
+    float* vs;
+};
+
 __global__ __launch_bounds__(256) void quant_kv_kernel(Src k, Src v, int64_t H, int64_t at, int64_t L, int64_t Lpad,
                                                        const float* k_mean, const float* v_scale, int8_t* k_out,
-                                                       float* k_scale, uint8_t* v_out) {
+                                                       float* k_scale, uint8_t* v_out, Append app) {
     __shared__ float gmax[64][4];
     __shared__ uint8_t vt[D][64 + 4];  // codes [channel][position]
     __shared__ __attribute__((aligned(16))) float stat[3][D];  // k_mean, v_scale, 1 / v_scale of the head
@@ -225,6 +262,11 @@ __global__ __launch_bounds__(256) void quant_kv_kernel(Src k, Src v, int64_t H, 
     if (b1 <= at) quant_block<CACHE>(k, v, h, H, at, L, tok, dq, fk, fv);
     else if (b0 >= at && b1 <= L) quant_block<CHUNK>(k, v, h, H, at, L, tok, dq, fk, fv);
     else quant_block<MIXED>(k, v, h, H, at, L, tok, dq, fk, fv);
+    if (app.k && b1 > at) {  // the block holds chunk tokens (uniform)
+        const bool on = tok >= at && tok < L;
+        append_row(fk, app.k, app.ks, tok * H + h, dq, on);
+        append_row(fv, app.v, app.vs, tok * H + h, dq, on);
+    }
     __syncthreads();
     // K - mean: 32 channels of one token per thread. Tokens >= L loaded as +0 (load_token8), so with live = 0 the
     // fma gives +0 and with live = 1 it is the one rounding of fk - mean; their V quotients are +0, code 0.
@@ -370,7 +412,7 @@ static int sage_prep_launch(const void* cache_k, const float* cache_ks, const vo
                             const int32_t* tokens_map, const void* k, int64_t ldk, const void* v, int64_t ldv,
                             int64_t heads, int64_t at, int64_t n, int splits, float* workspace, void* k_int8,
                             float* k_scale, void* v_fp8, float* k_mean_out, float* v_scale_out, hipStream_t stream,
-                            const float* cache_stats = nullptr) {
+                            const float* cache_stats = nullptr, Append app = Append{}) {
     const int64_t L = at + n;
     if (at < 0 || n < 0 || heads <= 0 || at > capacity || splits < 1 || ldk < heads * D || ldv < heads * D ||
         cache_heads < heads || (!heads_map && cache_heads != heads))
@@ -404,7 +446,7 @@ static int sage_prep_launch(const void* cache_k, const float* cache_ks, const vo
     if (rc) return rc;
     quant_kv_kernel<<<dim3(unsigned(Lpad / 64), unsigned(heads)), 256, 0, stream>>>(
         sk, sv, heads, at, L, Lpad, k_mean, v_scale, static_cast<int8_t*>(k_int8), k_scale,
-        static_cast<uint8_t*>(v_fp8));
+        static_cast<uint8_t*>(v_fp8), app);
     return check_launch("sage_prep quant_kv");
 }
 
@@ -459,6 +501,21 @@ extern "C" int wdl_sage_prep_cached(const void* cache_k, const float* cache_ks, 
     return sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, capacity, heads, nullptr, nullptr, k, ldk, v, ldv,
                             heads, at, n, splits, workspace, k_int8, k_scale, v_fp8, k_mean_out, v_scale_out, stream,
                             cache_stats);
+}
+
+extern "C" int wdl_sage_prep_cached_append(void* cache_k, float* cache_ks, void* cache_v, float* cache_vs,
+                                           int64_t capacity, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                                           int64_t heads, int64_t at, int64_t n, const float* cache_stats, int splits,
+                                           float* workspace, void* k_int8, float* k_scale, void* v_fp8,
+                                           float* k_mean_out, float* v_scale_out, hipStream_t stream) {
+    if (!cache_stats) return fail(WDL_EINVAL, "sage_prep_cached_append: null cache statistics");
+    if (at < 0 || n < 0 || at + n > capacity)
+        return fail(WDL_EINVAL, "sage_prep_cached_append: rows %lld .. %lld outside the cache of %lld", (long long)at,
+                    (long long)(at + n), (long long)capacity);
+    return sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, capacity, heads, nullptr, nullptr, k, ldk, v, ldv,
+                            heads, at, n, splits, workspace, k_int8, k_scale, v_fp8, k_mean_out, v_scale_out, stream,
+                            cache_stats,
+                            Append{static_cast<uint8_t*>(cache_k), cache_ks, static_cast<uint8_t*>(cache_v), cache_vs});
 }
 
 extern "C" int wdl_sage_sm89_relayout(const void* k_i8, int64_t ldk, const void* v_fp8, int64_t v_stride_d,

@@ -183,9 +183,10 @@ class KVCache:
             return self.attend_split(Q, K, V, at, n)
         if self._stats_at != at:
             self._refresh_stats()
-        self.store(at, K, V)
+        # the store of the chunk (rows at .. at + n, the bytes and scales store() writes) runs inside the
+        # preparation pass of the attention, which reads the chunk anyway
         return attend(Q, self.k, self.ks, self.v, self.vs, at, K, V, sm_scale=self.scale(at + n, Q.shape[-1]),
-                      cache_stats=self.stats)
+                      cache_stats=self.stats, append=True)
 
     def _head_groups(self, dev):
         """[(cache heads int32, as index, cache rows int32 or None)] of the two Forcing-KV groups, made once per

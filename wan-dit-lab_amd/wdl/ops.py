@@ -397,13 +397,14 @@ def sage_cache_stats_launch(cache_k, cache_ks, cache_v, cache_vs, at, out=None):
 
 
 def sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, k, v, at, want_stats=False, heads=None, tokens=None,
-                     cache_stats=None):
+                     cache_stats=None, append=False):
     """Cache (fp8 [1, cap, Hc, 128] + fp32 scales [1, cap, Hc, 1]) tokens [0, at) and the chunk k, v
     (bf16 [n, H*128] row-strided) -> k_int8 [H, Lpad, 128], k_scale [H, Lpad/16], v_fp8 [H, 128, Lpad],
     v_scale [H, 128] (and k_mean when want_stats). heads (int32 [H], device): head h reads cache head heads[h];
     tokens (int32 [>= at], device): cached token i is cache row tokens[i]; without them Hc = H and rows 0 .. at-1.
     cache_stats: sage_cache_stats_launch of the same cache rows [0, at) (no maps): only the chunk's tokens are then
-    read for the K mean and V scale."""
+    read for the K mean and V scale. append (with cache_stats): the pass also writes k, v into cache rows at .. at + n
+    (wdl_sage_prep_cached_append: the bytes and scales of wdl_kv_append_fp8)."""
     n = k.shape[0]
     H = k.shape[1] // 128
     Hc = cache_k.shape[2]
@@ -421,9 +422,12 @@ def sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, k, v, at, want_stats=
             raise ValueError("cache statistics are for the unmapped cache")
         if cache_stats.shape != (2, H, 128) or cache_stats.dtype != torch.float32 or not cache_stats.is_contiguous():
             raise ValueError(f"cache statistics must be contiguous fp32 [2, {H}, 128]")
-        _lib.call("wdl_sage_prep_cached", ptr(cache_k), ptr(cache_ks), ptr(cache_v), ptr(cache_vs), cache_k.shape[1],
-                  ptr(k), k.stride(0), ptr(v), v.stride(0), H, at, n, ptr(cache_stats), SPLITS, ptr(ws), ptr(k_i8),
-                  ptr(k_sc), ptr(v_f8), ptr(k_mean), ptr(v_sc), stream_of(k))
+        _lib.call("wdl_sage_prep_cached_append" if append else "wdl_sage_prep_cached", ptr(cache_k), ptr(cache_ks),
+                  ptr(cache_v), ptr(cache_vs), cache_k.shape[1], ptr(k), k.stride(0), ptr(v), v.stride(0), H, at, n,
+                  ptr(cache_stats), SPLITS, ptr(ws), ptr(k_i8), ptr(k_sc), ptr(v_f8), ptr(k_mean), ptr(v_sc),
+                  stream_of(k))
+    elif append:
+        raise ValueError("append runs with the cache statistics")
     elif heads is None and tokens is None:
         _lib.call("wdl_sage_prep", ptr(cache_k), ptr(cache_ks), ptr(cache_v), ptr(cache_vs), cache_k.shape[1],
                   ptr(k), k.stride(0), ptr(v), v.stride(0), H, at, n, SPLITS, ptr(ws), ptr(k_i8), ptr(k_sc),
@@ -593,6 +597,25 @@ def sage_kv_attend_cached(Q: torch.Tensor, cache_k: torch.Tensor, cache_ks: torc
 
 
 @sage_kv_attend_cached.register_fake
+def _(Q, cache_k, cache_ks, cache_v, cache_vs, K, V, at, sm_scale, cache_stats):
+    return Q.new_empty(Q.shape, dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("wdl::sage_kv_append_attend_cached", mutates_args=("cache_k", "cache_ks", "cache_v", "cache_vs"))
+def sage_kv_append_attend_cached(Q: torch.Tensor, cache_k: torch.Tensor, cache_ks: torch.Tensor, cache_v: torch.Tensor,
+                                 cache_vs: torch.Tensor, K: torch.Tensor, V: torch.Tensor, at: int, sm_scale: float,
+                                 cache_stats: torch.Tensor) -> torch.Tensor:
+    """The cache store of the chunk (KVCache.store, causal.py:177-181: store_kv_fp8 into rows at .. at + n) and
+    sage_kv_attend_cached over the cache and the chunk, with the store inside the preparation's quantization pass
+    (one read of the chunk, no launch of its own): the cache receives the bytes and scales store_kv_fp8 writes."""
+    _, nq, H, D = Q.shape
+    n = K.shape[1]
+    prep = sage_prep_launch(cache_k, cache_ks, cache_v, cache_vs, K[0].reshape(n, H * D) if K.is_contiguous() else
+                            K[0].flatten(1), V[0].flatten(1), at, cache_stats=cache_stats, append=True)
+    return sage_attn_q16_launch(Q[0].flatten(1), prep, at + n, sm_scale).view(1, nq, H, D)
+
+
+@sage_kv_append_attend_cached.register_fake
 def _(Q, cache_k, cache_ks, cache_v, cache_vs, K, V, at, sm_scale, cache_stats):
     return Q.new_empty(Q.shape, dtype=torch.bfloat16)
 

@@ -9,7 +9,8 @@ from __future__ import annotations
 
 import torch
 
-from wdl.ops import quant_q_launch, sage_attn_launch, sage_kv_attend, sage_kv_attend_cached, sage_prep_launch
+from wdl.ops import (quant_q_launch, sage_attn_launch, sage_kv_append_attend_cached, sage_kv_attend,
+                     sage_kv_attend_cached, sage_prep_launch)
 
 V_MAX = 2.25  # sage_kv.py:24
 BLKQ, WARPQ, BLKK = 128, 32, 64
@@ -50,7 +51,7 @@ def _check(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, heads=None, tokens
 
 
 def attend(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, sm_scale=None, heads=None, tokens=None,
-           frame_tokens=0, cache_stats=None):
+           frame_tokens=0, cache_stats=None, append=False):
     """softmax(Q K^T * sm_scale) V over the cached tokens and the chunk (sage_kv.py:127-134); [1, nq, H, 128] bf16
     (sm_scale defaults to 128^-0.5). heads (int32 [H]): head h of Q, K, V is cache head heads[h], the cache keeping
     all of them; tokens (int32 [at]): cached token i is cache row tokens[i] (KVCache.attend_split's static heads,
@@ -59,8 +60,19 @@ def attend(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, sm_scale=None, hea
     latent frame of that many tokens, Q being the chunk (nq == n): chunk query q sees the cache and the chunk's
     frames up to its own, keys below at + (q // frame_tokens + 1) * frame_tokens. cache_stats (fp32 [2, H, 128],
     wdl.ops.sage_cache_stats_launch of rows [0, at), no maps): the K mean and V scale then read only the chunk's
-    tokens beside them."""
+    tokens beside them. append (with cache_stats, not with frame_tokens): K, V also go into cache rows at .. at + n
+    (KVCache.store's store_kv_fp8, causal.py:177-181) inside the preparation pass; its requirements are checked
+    first, and a broken one raises before anything is written."""
     _check(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, heads, tokens)
+    if append:
+        from wdl.cache_fp8 import _refusal
+
+        if cache_stats is None or frame_tokens:
+            raise ValueError("append runs with the cache statistics and without frame_tokens")
+        refused = _refusal(K, V, cache_k, cache_ks, cache_v, cache_vs, at)
+        if refused is not None:
+            kind, message = refused
+            raise kind(message)
     if cache_stats is not None and (heads is not None or tokens is not None):
         raise ValueError("cache statistics are for the unmapped cache")
     if frame_tokens:
@@ -76,8 +88,9 @@ def attend(Q, cache_k, cache_ks, cache_v, cache_vs, at, K, V, sm_scale=None, hea
         return ops.sage_attn_q16_launch(Q[0].flatten(1), prep, at + n, sm, frame_tokens=frame_tokens).view(Q.shape)
     sm = Q.shape[-1] ** -0.5 if sm_scale is None else float(sm_scale)
     if cache_stats is not None:
-        return sage_kv_attend_cached(Q, cache_k.view(torch.uint8), cache_ks, cache_v.view(torch.uint8), cache_vs, K, V,
-                                     at, sm, cache_stats)
+        op = sage_kv_append_attend_cached if append else sage_kv_attend_cached
+        return op(Q, cache_k.view(torch.uint8), cache_ks, cache_v.view(torch.uint8), cache_vs, K, V, at, sm,
+                  cache_stats)
     return sage_kv_attend(Q, cache_k.view(torch.uint8), cache_ks, cache_v.view(torch.uint8), cache_vs, K, V, at, sm,
                           heads, tokens)
 
