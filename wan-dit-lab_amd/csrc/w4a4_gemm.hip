@@ -159,7 +159,8 @@ __device__ __forceinline__ void finish_tile(const GemmArgs& p, f32x16 (&acc)[TN]
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int64_t nb = nb0 + i * 32 + 8 * q + 4 * half;
-            bias[i][q] = p.bias ? *reinterpret_cast<const uint2*>(p.bias + nb) : make_uint2(0u, 0u);
+            bias[i][q] = p.bias ? *reinterpret_cast<const uint2*>(p.bias + nb)
+                                : make_uint2(0x80008000u, 0x80008000u);  // -0: an exact identity of the sum
             if (EPI == EPI_RESIDUAL) gate[i][q] = *reinterpret_cast<const float4*>(p.gate + nb);
             if (EPI == EPI_FP8_ROWS) wsf[i][q] = *reinterpret_cast<const float4*>(p.wsf + nb);
         }
@@ -219,7 +220,7 @@ __device__ __forceinline__ void finish_tile(const GemmArgs& p, f32x16 (&acc)[TN]
                         y[e] = bf16_to_f32(f32_to_bf16(y[e])) * (xsm[j] * wsf[i][q][e]);
                     else if (EPI == EPI_FP8_TENSOR)  // _scaled_mm: acc * (xs ws) + b, one rounding
                         y[e] = y[e] * xs0;
-                    if (p.bias) y[e] = y[e] + bf16_to_f32(bv[e]);
+                    y[e] = y[e] + bf16_to_f32(bv[e]);  // -0 without a bias
                 }
                 if (EPI == EPI_F32) {
                     float* o = static_cast<float*>(p.out) + m * p.ldo + nb;
@@ -307,7 +308,7 @@ __device__ __forceinline__ void finish_tile_rows(const GemmArgs& p, f32x16 (&acc
 #pragma unroll
         for (int q = 0; q < 4; ++q)
             bias[i][q] = p.bias ? *reinterpret_cast<const uint2*>(p.bias + nb0 + i * 32 + 8 * q + 4 * half)
-                                : make_uint2(0u, 0u);
+                                : make_uint2(0x80008000u, 0x80008000u);  // -0: an exact identity of the sum
     float4 gate[2];
     uint4 old[8];
     if (EPI == EPI_RESIDUAL) {
@@ -351,7 +352,7 @@ __device__ __forceinline__ void finish_tile_rows(const GemmArgs& p, f32x16 (&acc
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     float y = acc[i][j][4 * q + e];
-                    if (p.bias) y = y + bf16_to_f32(bv[e]);
+                    y = y + bf16_to_f32(bv[e]);  // -0 without a bias
                     r[e] = f32_to_bf16(EPI == EPI_GELU ? gelu_tanh(y) : y);
                 }
                 *reinterpret_cast<uint2*>(stage + (j * 32 + lane % 32) * STG + i * 32 + 8 * q + 4 * half) =
@@ -444,15 +445,9 @@ __device__ __forceinline__ void finish_tile_gelu_quant(const GemmArgs& p, f32x16
                 lr[j][h][1] = *reinterpret_cast<const float4*>(l + 4);
             }
     }
-    uint2 bias[TN][4];
     uint2 pdv[TN][2][2];  // proj_down2^T row tok: features 32 ti + 16 qp + 8 part + 4 half .. + 3
 #pragma unroll
     for (int i = 0; i < TN; ++i) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int64_t nb = nb0 + i * 32 + 8 * q + 4 * half;
-            bias[i][q] = p.bias ? *reinterpret_cast<const uint2*>(p.bias + nb) : make_uint2(0u, 0u);
-        }
 #pragma unroll
         for (int qp = 0; qp < 2; ++qp)
 #pragma unroll
@@ -477,24 +472,26 @@ __device__ __forceinline__ void finish_tile_gelu_quant(const GemmArgs& p, f32x16
                 for (int i = 0; i < TN; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[i][h], lb, acc[i][j], 0, 0, 0);
             }
     }
-    // smooth2 and its IEEE reciprocal at the lane's 32 features: lane l loads and divides once, for the wave's
-    // feature nb0 + l, into the wave's 512-byte LDS slot past the exchange area ([64 reciprocals][64 values]), and
-    // reads back the 32 it needs (the 32 lanes of a half need the same ones; one wave's LDS accesses complete in
-    // order)
-    float* const rslot = xch + 4 * TM * 16 * 64 + (wm * 2 + wn) * 128;
+    // smooth2, its IEEE reciprocal and the bias (fp32; -0 when absent, an exact identity of the sum) at the lane's
+    // 32 features: lane l loads and divides once, for the wave's feature nb0 + l, into the wave's 768-byte LDS slot
+    // past the exchange area ([64 reciprocals][64 smooth2][64 bias]), and reads back the 32 it needs (the 32 lanes
+    // of a half need the same ones; one wave's LDS accesses complete in order)
+    float* const rslot = xch + 4 * TM * 16 * 64 + (wm * 2 + wn) * 192;
     {
         const float sv = bf16_to_f32(p.sm2[nb0 + lane]);
         rslot[lane] = 1.0f / sv;
         rslot[64 + lane] = sv;
+        rslot[128 + lane] = p.bias ? bf16_to_f32(p.bias[nb0 + lane]) : -0.0f;
     }
     asm volatile("" ::: "memory");
-    float rsm[TN][16], smf[TN][16];
+    float rsm[TN][16], smf[TN][16], bsf[TN][16];
 #pragma unroll
     for (int i = 0; i < TN; ++i)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const float4 r4 = *reinterpret_cast<const float4*>(rslot + i * 32 + 8 * q + 4 * half);
             const float4 s4 = *reinterpret_cast<const float4*>(rslot + 64 + i * 32 + 8 * q + 4 * half);
+            const float4 b4 = *reinterpret_cast<const float4*>(rslot + 128 + i * 32 + 8 * q + 4 * half);
             rsm[i][4 * q] = r4.x;
             rsm[i][4 * q + 1] = r4.y;
             rsm[i][4 * q + 2] = r4.z;
@@ -503,23 +500,17 @@ __device__ __forceinline__ void finish_tile_gelu_quant(const GemmArgs& p, f32x16
             smf[i][4 * q + 1] = s4.y;
             smf[i][4 * q + 2] = s4.z;
             smf[i][4 * q + 3] = s4.w;
+            bsf[i][4 * q] = b4.x;
+            bsf[i][4 * q + 1] = b4.y;
+            bsf[i][4 * q + 2] = b4.z;
+            bsf[i][4 * q + 3] = b4.w;
         }
 #pragma unroll
     for (int i = 0; i < TN; ++i)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint16_t bv[4] = {uint16_t(bias[i][q].x), uint16_t(bias[i][q].x >> 16), uint16_t(bias[i][q].y),
-                                    uint16_t(bias[i][q].y >> 16)};
+        for (int k = 0; k < 16; ++k)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-#pragma unroll
-                for (int j = 0; j < TM; ++j) {
-                    float y = acc[i][j][4 * q + e];
-                    if (p.bias) y = y + bf16_to_f32(bv[e]);
-                    acc[i][j][4 * q + e] = gelu_tanh(y);
-                }
-            }
-        }
+            for (int j = 0; j < TM; ++j) acc[i][j][k] = gelu_tanh(acc[i][j][k] + bsf[i][k]);
 
     const int64_t g = nb0 / 64;  // the group of the second layer's input
     float* mine = xch + (wm * 2 + wn) * TM * 16 * 64;  // this wave's low-rank partials, lane-linear
@@ -975,7 +966,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         if constexpr (EPI == EPI_GELU_QUANT) {
             static_assert(W4 && BN == 128 && BM == 128 && NW == 4, "the fused GELU epilogue runs on 128 x 128 tiles");
             __syncthreads();  // every wave is past its last read of the ring, whose LDS the exchange reuses
-            static_assert((4 * 2 * 16 * 64 + 4 * 128) * 4 <= STAGES * CS, "exchange and smooth2 slots fit in the ring");
+            static_assert((4 * 2 * 16 * 64 + 4 * 192) * 4 <= STAGES * CS, "exchange and per-feature slots fit in the ring");
             finish_tile_gelu_quant<TN, TM>(p, acc, n0 + wn * WN, m0 + wm * WM, wn, wm, lane,
                                            reinterpret_cast<float*>(&sC[0][0]));
         } else if constexpr (W4 && EPI != EPI_F32 && TN == 2 && TM == 2) {
