@@ -36,10 +36,7 @@ __device__ __forceinline__ void ld4<float>(const float* p, float* f) {
     f[0] = r.x, f[1] = r.y, f[2] = r.z, f[3] = r.w;
 }
 
-__device__ __forceinline__ uint32_t e4m3x4(const float* y) {
-    uint32_t w = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
-    return __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], w, true);
-}
+__device__ __forceinline__ uint32_t e4m3x4(const float* y) { return wdl::e4m3x4(y[0], y[1], y[2], y[3]); }
 
 // 8 consecutive values of a row as floats (one 16-byte load of bf16, two of fp32)
 template <typename T>

@@ -99,10 +99,8 @@ __global__ __launch_bounds__(256) void kv_append_vec_kernel(Rows k, Rows v, int6
     uint32_t c[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
-        c[j] = uint32_t(f32_to_e4m3(div_rn(val[4 * j], scale, rs))) |
-               (uint32_t(f32_to_e4m3(div_rn(val[4 * j + 1], scale, rs))) << 8) |
-               (uint32_t(f32_to_e4m3(div_rn(val[4 * j + 2], scale, rs))) << 16) |
-               (uint32_t(f32_to_e4m3(div_rn(val[4 * j + 3], scale, rs))) << 24);
+        c[j] = e4m3x4(div_rn(val[4 * j], scale, rs), div_rn(val[4 * j + 1], scale, rs),
+                      div_rn(val[4 * j + 2], scale, rs), div_rn(val[4 * j + 3], scale, rs));
     *reinterpret_cast<uint2*>(r.cache + target * 128 + 8 * lane) = make_uint2(c[0], c[1]);
     if (lane == 0) r.scale[target] = scale;
 }

@@ -207,7 +207,7 @@ __device__ __forceinline__ void quant_block(const Src& k, const Src& v, int64_t 
 // Row `row` of an FP8 cache from 32 channels (dq .. dq + 31) per thread, the 4 threads of a token in consecutive
 // lanes: the arithmetic of wdl_kv_append_fp8 (kv_cache.hip), scale = max(max |x| over the 128 channels, 1e-12) /
 // 448, codes e4m3 of the IEEE quotients x / scale (div_rn on the reciprocal), so the bytes and scales are the
-// same. Every thread takes part in the row maximum; only `on` threads store.
+// same (the hardware conversion, e4m3x4). Every thread takes part in the row maximum; only `on` threads store.
 __device__ __forceinline__ void append_row(const float (&f)[4][8], uint8_t* cache, float* scales, int64_t row, int dq,
                                            bool on) {
     float amax = 0.0f;
@@ -223,9 +223,8 @@ __device__ __forceinline__ void append_row(const float (&f)[4][8], uint8_t* cach
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
         const float* x = f[b / 2] + 4 * (b % 2);
-        w[b] = uint32_t(f32_to_e4m3(div_rn(x[0], scale, rs))) | (uint32_t(f32_to_e4m3(div_rn(x[1], scale, rs))) << 8) |
-               (uint32_t(f32_to_e4m3(div_rn(x[2], scale, rs))) << 16) |
-               (uint32_t(f32_to_e4m3(div_rn(x[3], scale, rs))) << 24);
+        w[b] = e4m3x4(div_rn(x[0], scale, rs), div_rn(x[1], scale, rs), div_rn(x[2], scale, rs),
+                      div_rn(x[3], scale, rs));
     }
     uint4* dst = reinterpret_cast<uint4*>(cache + row * D + dq);
     dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
