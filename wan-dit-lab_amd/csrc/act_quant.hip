@@ -137,7 +137,8 @@ __global__ __launch_bounds__(64 * WAVES) void quant_kernel(QuantArgs a) {
     const int64_t gb = int64_t(blockIdx.y) * S;             // first group of the workgroup
     const int nsg = int(min(int64_t(S), K / 64 - gb));     // its groups present in the matrix
 
-    // loads first: each present group's 64 bytes of the row (absent rows read row 0; zeroed below) and of
+    // loads first: each present group's 64 bytes of the row (absent rows read row 0: every output of theirs is
+    // masked below, the codes and scales by their store, the low-rank sums by the partial store) and of
     // proj_down^T row r, the row's LN statistics, the workgroup's per-column vectors (thread t: columns t + NT i)
     uint4 raw[G][4], pd[G][4];
 #pragma unroll
@@ -149,6 +150,9 @@ __global__ __launch_bounds__(64 * WAVES) void quant_kernel(QuantArgs a) {
             const uint16_t* xr = a.x + (live ? row : 0) * a.ldx + col;
 #pragma unroll
             for (int i = 0; i < 4; ++i) raw[j][i] = *reinterpret_cast<const uint4*>(xr + 8 * i);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) raw[j][i] = make_uint4(0u, 0u, 0u, 0u);
         }
         if (a.pdt) {
             const uint16_t* pr = a.pdt + int64_t(r) * K + col;
@@ -214,7 +218,6 @@ __global__ __launch_bounds__(64 * WAVES) void quant_kernel(QuantArgs a) {
 
     const float qmax = a.unsigned_q ? 15.0f : 7.0f;
     const float qlo = a.unsigned_q ? 0.0f : -8.0f;
-    const bool present = live && a.M > 0;
     f32x16 acc = {};
 #pragma unroll
     for (int j = 0; j < G; ++j) {
@@ -227,11 +230,11 @@ __global__ __launch_bounds__(64 * WAVES) void quant_kernel(QuantArgs a) {
             const uint32_t w[4] = {raw[j][i].x, raw[j][i].y, raw[j][i].z, raw[j][i].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                v[8 * i + 2 * e] = present ? __uint_as_float(w[e] << 16) : 0.0f;
-                v[8 * i + 2 * e + 1] = present ? __uint_as_float(w[e] & 0xffff0000u) : 0.0f;
+                v[8 * i + 2 * e] = __uint_as_float(w[e] << 16);
+                v[8 * i + 2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
             }
         }
-        if (LN && present) {
+        if (LN) {  // rows past M compute with (0, 0) statistics; their outputs are masked
 #pragma unroll
             for (int j4 = 0; j4 < 8; ++j4) {
                 const float4 w4 = *reinterpret_cast<const float4*>(&sp[1][cl + 4 * j4]);
@@ -296,7 +299,7 @@ __global__ __launch_bounds__(64 * WAVES) void quant_kernel(QuantArgs a) {
 #pragma unroll
         for (int k = 0; k < 32; ++k) {
             const float rq = sc > 0.0f ? __builtin_rintf(div_rn(u[k], sc, rsc)) : 0.0f;
-            const float qv = live ? fminf(fmaxf(rq, qlo), qmax) + 0.0f : 0.0f;  // + 0 turns -0 into +0
+            const float qv = fminf(fmaxf(rq, qlo), qmax) + 0.0f;  // + 0 turns -0 into +0
             if (k % 2 == 0) ea[k / 2] = qv * 0.5f;
             else eb[k / 2] = qv * 0.5f;
         }
@@ -305,6 +308,8 @@ __global__ __launch_bounds__(64 * WAVES) void quant_kernel(QuantArgs a) {
         // field 4, measured); scale 1.0 (the values are exact fp6 values)
         u32x6 w;
         asm volatile("v_cvt_scalef32_2xpk16_fp6_f32 %0, %1, %2, 1.0" : "=&v"(w) : "v"(ea), "v"(eb));
+#pragma unroll
+        for (int d = 0; d < 6; ++d) w[d] = live ? w[d] : 0u;  // rows past M: code 0 (+0) everywhere
         uint8_t* dst = a.q + blocked6_offset(row, g, K);
         *reinterpret_cast<uint4*>(dst + 16 * h) = make_uint4(w[0], w[1], w[2], w[3]);
         *reinterpret_cast<uint2*>(dst + 32 + 8 * h) = make_uint2(w[4], w[5]);
