@@ -129,7 +129,7 @@ __global__ __launch_bounds__(64 * WAVES) void quant_kernel(QuantArgs a) {
     __shared__ float part[WAVES][ROWS * RANK];
     __shared__ float2 sst[LN ? ROWS : 1];  // LN (mean, rstd) of the workgroup's rows
 
-    const int t = threadIdx.x, lane = t % 64, wave = t / 64;
+    const int t = threadIdx.x, lane = t % 64, wave = __builtin_amdgcn_readfirstlane(t / 64);  // uniform: scalar
     const int r = lane % 32, h = lane / 32;
     const int64_t row = int64_t(blockIdx.x) * ROWS + r;
     const bool live = row < a.M;

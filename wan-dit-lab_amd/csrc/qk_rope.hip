@@ -73,7 +73,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs a) {
     constexpr int CW = MAXCH / 2;  // chunks per lane and wave
     __shared__ float part[2][64];  // the first wave's lane sums, per row slot
     __shared__ float srstd[2];
-    const int lane = threadIdx.x % 64, wv = threadIdx.x / 64, slot = wv / 2, hw = wv % 2;
+    // the wave index through readfirstlane: the row, its pointers and the branches on them are then wave-uniform
+    // (scalar registers and branches) instead of per-lane values
+    const int lane = threadIdx.x % 64, wv = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), slot = wv / 2,
+              hw = wv % 2;
     const int64_t item = int64_t(blockIdx.x) * 2 + slot;  // (row, which)
     const bool valid = item < a.items * a.M;
     const int64_t row = valid ? item / a.items : 0;
@@ -195,7 +198,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs a) {
 // one wave per (32-token block, head); lane = 2 * token_in_block + (d half); values of 64 d per lane
 __global__ __launch_bounds__(256) void quant_q_kernel(const uint16_t* x, int64_t ldx, int64_t n, int64_t H,
                                                       int64_t blocks, int8_t* q, float* q_scale) {
-    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
     const int64_t item = int64_t(blockIdx.x) * 4 + wave;  // (block, head)
     if (item >= blocks * H) return;
     const int64_t blk = item / H, h = item % H;

@@ -512,7 +512,7 @@ __global__ __launch_bounds__(512) void sage_attn_kernel(AttnArgs a) {
 // Grid (R, 4 query waves, 4 channel subtiles) x 256 threads: lane = query (and channel half), thread / 64 = one
 // group of 4 channels, in the partial layout of the main kernel.
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
-    const int lane = threadIdx.x % 64, half = lane / 32, g = threadIdx.x / 64;
+    const int lane = threadIdx.x % 64, half = lane / 32, g = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const int64_t r = blockIdx.x, sub = blockIdx.y, ds = blockIdx.z;
     const int64_t nblk = a.Lpad / 64, T = a.qtiles * a.H, Usk = (T - a.D) * nblk;
     const int64_t tile = a.D + r, h = tile / a.qtiles, qt = tile % a.qtiles;
