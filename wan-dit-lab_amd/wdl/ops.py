@@ -375,7 +375,9 @@ def quant_q_launch(x, heads):
     return q, qs
 
 
-SPLITS = 32
+# token splits of the Sage preparation's column statistics per head (workgroups of colstats_kernel, partials summed in
+# order by finalize_kernel): 16 measured 0.02 ms per step faster than 8 or 32 and 0.14 ms faster than 64
+SPLITS = 16
 
 
 def sage_cache_stats_launch(cache_k, cache_ks, cache_v, cache_vs, at, out=None):
