@@ -348,11 +348,37 @@ __global__ void lora_sum_kernel(const float* part, int nb, int64_t n, float* out
     out[i] = s;
 }
 
+// The same sum over many partials (the fused MLP's 112 tile partials): 4 lanes per output, lane j adding the
+// partials [j nb / 4, (j + 1) nb / 4) in increasing order, the four sums combined as (s0 + s1) + (s2 + s3) (DPP
+// exchanges): a quarter of the dependent load batches per output.
+__global__ __launch_bounds__(256) void lora_sum4_kernel(const float* part, int nb, int64_t n, float* out) {
+    const int64_t i = int64_t(blockIdx.x) * 64 + threadIdx.x / 4;
+    const int j = threadIdx.x % 4;
+    const bool live = i < n;  // every lane takes part in the exchanges
+    const int b0 = j * nb / 4, b1 = (j + 1) * nb / 4;
+    constexpr int BATCH = 16;
+    float s = 0.0f;
+    for (int c0 = b0; c0 < b1; c0 += BATCH) {
+        float v[BATCH];
+#pragma unroll
+        for (int k = 0; k < BATCH; ++k) v[k] = live && c0 + k < b1 ? part[int64_t(c0 + k) * n + i] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < BATCH; ++k)
+            if (c0 + k < b1) s = c0 + k == b0 ? v[k] : s + v[k];
+    }
+    s = xor_sum<2>(xor_sum<1>(s));
+    if (live && j == 0) out[i] = s;
+}
+
 }  // namespace
 
 namespace wdl {
 
 int lora_sum(const float* part, int nb, int64_t n, float* out, hipStream_t stream) {
+    if (nb >= 32) {
+        lora_sum4_kernel<<<unsigned((n + 63) / 64), 256, 0, stream>>>(part, nb, n, out);
+        return check_launch("lora_sum");
+    }
     lora_sum_kernel<<<unsigned((n + 255) / 256), 256, 0, stream>>>(part, nb, n, out);
     return check_launch("lora_sum");
 }
