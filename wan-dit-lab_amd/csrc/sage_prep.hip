@@ -244,7 +244,7 @@ __global__ __launch_bounds__(256) void quant_kv_kernel(Src k, Src v, int64_t H, 
                                                        const float* k_mean, const float* v_scale, int8_t* k_out,
                                                        float* k_scale, uint8_t* v_out, Append app) {
     __shared__ float gmax[64][4];
-    __shared__ uint8_t vt[D][64 + 4];  // codes [channel][position]
+    __shared__ __attribute__((aligned(16))) uint8_t vt[D][64 + 4];  // codes [channel][position], 4-byte rows
     __shared__ __attribute__((aligned(16))) float stat[3][D];  // k_mean, v_scale, 1 / v_scale of the head
     const int64_t blk = blockIdx.x, h = blockIdx.y;
     const int t = threadIdx.x, tt = t / 4, dq = (t % 4) * 32;
@@ -281,18 +281,29 @@ __global__ __launch_bounds__(256) void quant_kv_kernel(Src k, Src v, int64_t H, 
             amax = fmaxf(amax, fabsf(y));
         }
     gmax[tt][t % 4] = amax;
-    // V codes into the transposed tile (V / v_scale is below 2.25 in magnitude: the conversion never saturates)
+    // V codes into the transposed tile (V / v_scale is below 2.25 in magnitude: the conversion never saturates).
+    // A dword holds 4 channels of the thread's token; a 4 x 4 byte transpose between the 4 lanes that hold tokens
+    // 4k .. 4k + 3 of the same channel quarter (lanes 4 apart in a row of 16: DPP, then v_perm) leaves each lane 4
+    // consecutive positions of one channel (v_position keeps 4 consecutive tokens at consecutive positions), so
+    // one 4-byte LDS store replaces four byte stores.
+    {
+        const int ti = tt % 4;  // the token's place in its group of 4; the lane ends with channel d + ti
+        const uint32_t sel1 = (ti & 2) ? 0x03020706u : 0x05040100u;  // exchange halves with the token ti ^ 2
+        const uint32_t sel2 = (ti & 1) ? 0x03070105u : 0x06020400u;  // exchange bytes with the token ti ^ 1
+        const int pos = v_position(tt - ti);
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+        for (int c4 = 0; c4 < 8; ++c4) {
+            const int d = dq + 4 * c4, c = c4 / 2, j = 4 * (c4 % 2);
+            float y[4];
 #pragma unroll
-        for (int j = 0; j < 8; j += 2) {
-            const int d = dq + c * 8 + j;
-            const float y0 = div_rn(fv[c][j], stat[1][d], stat[2][d]);
-            const float y1 = div_rn(fv[c][j + 1], stat[1][d + 1], stat[2][d + 1]);
-            const uint32_t w = __builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false);
-            vt[d][v_position(tt)] = uint8_t(w);
-            vt[d + 1][v_position(tt)] = uint8_t(w >> 8);
+            for (int e = 0; e < 4; ++e) y[e] = div_rn(fv[c][j + e], stat[1][d + e], stat[2][d + e]);
+            uint32_t w = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+            w = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], w, true);
+            w = __builtin_amdgcn_perm(__float_as_uint(lane_xor<8>(__uint_as_float(w))), w, sel1);
+            w = __builtin_amdgcn_perm(__float_as_uint(lane_xor<4>(__uint_as_float(w))), w, sel2);
+            *reinterpret_cast<uint32_t*>(&vt[d + ti][pos]) = w;
         }
+    }
     __syncthreads();
     const int g = (tt % 8) / 2;
     float m = 0.0f;
@@ -337,9 +348,7 @@ __global__ __launch_bounds__(256) void quant_kv_kernel(Src k, Src v, int64_t H, 
     for (int c = 0; c < 2; ++c) {
         uint32_t w[4];
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
-            w[b] = uint32_t(vt[d][p0 + c * 16 + b * 4]) | (uint32_t(vt[d][p0 + c * 16 + b * 4 + 1]) << 8) |
-                   (uint32_t(vt[d][p0 + c * 16 + b * 4 + 2]) << 16) | (uint32_t(vt[d][p0 + c * 16 + b * 4 + 3]) << 24);
+        for (int b = 0; b < 4; ++b) w[b] = *reinterpret_cast<const uint32_t*>(&vt[d][p0 + c * 16 + b * 4]);
         *reinterpret_cast<uint4*>(vd + c * 16) = make_uint4(w[0], w[1], w[2], w[3]);
     }
 }
