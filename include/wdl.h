@@ -53,12 +53,13 @@ int64_t wdl_act_quant_workspace_floats(int64_t Mp, int64_t K);
  * q = clamp(rint(u / scale)). Outputs: q as fp6 codes of the integers [Mp, K] in the operand format (below);
  * ascales bf16 [K/64, Mp]; lora fp32 [Mp, 32] = v . proj_down; rows M..Mp-1 zero. Mp % 128 == 0. v_out (bf16
  * [M, K]) optional copy of v.
- * LayerNorm statistics (K <= 4096) from chunk partials of x: ln_partials fp32 [M][K / 32][2] (8-byte aligned) as
+ * LayerNorm statistics (K <= 4096) from chunk partials of x: ln_partials fp32 [M][K / 32][2] (16-byte aligned) as
  * the residual epilogue of wdl_w4a4_gemm writes them for the rows it produces, or NULL (then the call forms them
  * from x first, one more launch). Per row and 32-value chunk: (S, M2) = the chunk's sum and its sum of squared
  * deviations from S / 32, each as 8 quads of 4 values summed in order, the quads combined as
- * ((t0 + t1) + (t2 + t3)) + ((t4 + t5) + (t6 + t7)); the row's C chunks merged by 8 slots (slot j: chunks
- * [j C / 8, (j + 1) C / 8) in order from +0, the slots combined as the same tree): mean = sum S / K, M2 = sum of
+ * ((t0 + t1) + (t2 + t3)) + ((t4 + t5) + (t6 + t7)); the row's C chunks merged by 8 slots (slot j: the chunk
+ * pairs j, j + 8, ... = chunks 2p, 2p + 1, in chunk order from +0, the slots combined as the same tree): mean =
+ * sum S / K, M2 = sum of
  * M2_c + 32 (S_c / 32 - mean)^2, rstd = 1 / sqrt(M2 / K + eps) (the oracle's order).
  * workspace: wdl_act_quant_workspace_floats(Mp, K). */
 int wdl_act_quant_w4(const void* x, int64_t ldx, int64_t M, int64_t K, const void* smooth, float qshift,
@@ -123,7 +124,7 @@ int wdl_w4a4_scale_pairs(const void* scales, int fp16, int64_t n, void* pairs, w
  * (tile, group) iterations shared evenly, partial sums in the workspace added in a fixed order by a second
  * launch). Both are deterministic, their rounding not identical to the one-pass launch. With NULL the one-pass
  * launch runs. Calls sharing a workspace must not overlap.
- * ln_partials (epilogue 2 only, else NULL): fp32 [M][N / 32][2], 8-byte aligned, receives the LayerNorm chunk
+ * ln_partials (epilogue 2 only, else NULL): fp32 [M][N / 32][2], 16-byte aligned, receives the LayerNorm chunk
  * partials of the rows written (the N columns being whole rows), in wdl_act_quant_w4's order, so the next
  * LayerNorm-fused quantization of out skips its statistics pass. No counterpart in the reference (its LayerNorm
  * is a separate torch op). */

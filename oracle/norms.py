@@ -10,8 +10,9 @@ residual GEMM epilogues that write the row, or a statistics kernel) can produce 
   t_k = ((x0 + x1) + x2) + x3; the chunk sum S_c = ((t0 + t1) + (t2 + t3)) + ((t4 + t5) + (t6 + t7)); its mean
   m_c = S_c / 32 (exact); M2_c = the same quad and tree sums of (x - m_c)^2 (each difference and square one fp32
   rounding);
-- the C = K / 32 chunks are merged by 8 slots: slot j takes chunks [j C / 8, (j + 1) C / 8) (integer division) and
-  adds them into a running sum started at +0, in increasing order; the 8 slot sums are combined as
+- the C = K / 32 chunks are merged by 8 slots: slot j takes the chunk pairs p = j, j + 8, j + 16, ... (pair p =
+  chunks 2p and 2p + 1, those below C; a lane loads a pair with one 16-byte load) and adds them into a running sum
+  started at +0, in increasing chunk order; the 8 slot sums are combined as
   ((L0 + L1) + (L2 + L3)) + ((L4 + L5) + (L6 + L7)) (a butterfly over 8 lanes gives every lane this value);
 - mean = sum over the chunks of S_c / K; M2 = the same merge of T_c = M2_c + 32 (m_c - mean)^2 (difference,
   square, the exact product by 32, then the sum, each one fp32 rounding); var = M2 / K; rstd = 1 / sqrt(var + eps)
@@ -108,13 +109,16 @@ def ln_chunk_partials(x) -> tuple[np.ndarray, np.ndarray]:
 
 
 def _slot_merge(v: np.ndarray) -> np.ndarray:
-    """v float32 [M, C] -> float32 [M]: 8 slots of consecutive chunks, each a running sum from +0, then the tree."""
+    """v float32 [M, C] -> float32 [M]: 8 slots, slot j the chunk pairs j, j + 8, j + 16, ... (pair p = chunks 2p
+    and 2p + 1 below C) in increasing chunk order as a running sum from +0, then the tree."""
     M, C = v.shape
     slots = []
     for j in range(SLOTS):
         acc = np.zeros(M, dtype=np.float32)
-        for c in range(j * C // SLOTS, (j + 1) * C // SLOTS):
-            acc = (acc + v[:, c]).astype(np.float32)
+        for p in range(j, (C + 1) // 2, SLOTS):
+            for c in (2 * p, 2 * p + 1):
+                if c < C:
+                    acc = (acc + v[:, c]).astype(np.float32)
         slots.append(acc)
     return _tree8(np.stack(slots, axis=-1))
 

@@ -155,10 +155,14 @@ def test_layernorm_chunk_statistics_equal_scalar_loops(K):
 
         def merge(vals):
             lanes = []
-            for j in range(8):
+            for j in range(8):  # slot j: chunk pairs j, j + 8, ... (chunks 2p, 2p + 1 below C), in chunk order
                 acc = f(0)
-                for c in range(j * C // 8, (j + 1) * C // 8):
-                    acc = f(acc + vals[c])
+                p = j
+                while 2 * p < C:
+                    for c in (2 * p, 2 * p + 1):
+                        if c < C:
+                            acc = f(acc + vals[c])
+                    p += 8
                 lanes.append(acc)
             for o in (1, 2, 4):  # the butterfly of 8 lanes; lane 0's value
                 lanes = [f(lanes[i] + lanes[i ^ o]) for i in range(8)]

@@ -16,8 +16,9 @@
 // chunk's sum and its sum of squared deviations from its own mean, each as 8 quads summed sequentially and the
 // quads combined as ((t0 + t1) + (t2 + t3)) + ((t4 + t5) + (t6 + t7)). The W4A4 GEMM's gated-residual epilogue
 // writes them for the rows it produces (wdl_w4a4_gemm's ln_partials), in the same order; otherwise ln_partials
-// runs here. The quant launch merges a row's C = K / 32 chunks over 8 lanes (lane j: chunks [j C / 8, (j + 1) C / 8)
-// in order from +0, the lanes combined by an xor butterfly 1, 2, 4): mean = sum S_c / K, M2 = sum of
+// runs here. The quant launch merges a row's C = K / 32 chunks over 8 lanes (lane j: the chunk pairs j, j + 8, ...
+// — chunks 2p, 2p + 1, one 16-byte load each — in chunk order from +0, the lanes combined by an xor butterfly 1, 2,
+// 4): mean = sum S_c / K, M2 = sum of
 // M2_c + 32 (S_c / 32 - mean)^2, var = M2 / K, rstd = 1 / sqrt(var + eps).
 //
 // Launches (all parallel over rows and column blocks, nothing serial over K):
@@ -160,19 +161,24 @@ __global__ __launch_bounds__(64 * WAVES) void quant_kernel(QuantArgs a) {
             for (int i = 0; i < 4; ++i) pd[j][i] = *reinterpret_cast<const uint4*>(pr + 8 * i);
         }
     }
-    // LN: this lane's merge slot — row 8 wave + lane / 8 of the workgroup, chunks [j C / 8, (j + 1) C / 8) of it
-    // (j = lane % 8), loaded with the row data
+    // LN: this lane's merge slot — row 8 wave + lane / 8 of the workgroup, the chunk pairs j, j + 8, ... of it
+    // (j = lane % 8; C is even since K % 64 == 0), loaded with the row data
     constexpr int MAXCP = 64 * 8 * MAXCH / LN_CHUNK / 8;  // chunks per slot at K = 4096
     float2 cp[LN ? MAXCP : 1];
     int ncp = 0;
     if constexpr (LN) {
         static_assert(WAVES * 8 == ROWS, "the merge maps the workgroup's rows to its waves, 8 rows x 8 slots each");
         const int64_t C = K / LN_CHUNK, mrow = int64_t(blockIdx.x) * ROWS + 8 * wave + lane / 8;
-        const int64_t c0 = (lane % 8) * C / 8;
-        ncp = int((lane % 8 + 1) * C / 8 - c0);
+        const int j = lane % 8;
+        ncp = 2 * int((C / 2 - j + 7) / 8);
 #pragma unroll
-        for (int i = 0; i < MAXCP; ++i)
-            cp[i] = i < ncp && mrow < a.M ? a.lnp[mrow * C + c0 + i] : make_float2(0.0f, 0.0f);
+        for (int i = 0; i < MAXCP / 2; ++i) {
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (2 * i < ncp && mrow < a.M)
+                v = *reinterpret_cast<const float4*>(a.lnp + mrow * C + 2 * (j + 8 * i));
+            cp[2 * i] = make_float2(v.x, v.y);
+            cp[2 * i + 1] = make_float2(v.z, v.w);
+        }
     }
 #pragma unroll
     for (int i = 0; i < G; ++i) {
@@ -407,8 +413,8 @@ int act_quant_launch(const void* x, int64_t ldx, int64_t M, int64_t K, const voi
         return fail(WDL_EINVAL, "act_quant_w4: null pointer");
     if ((reinterpret_cast<uintptr_t>(x) | (ldx * 2)) % 16)
         return fail(WDL_EINVAL, "act_quant_w4: x rows must be 16-byte aligned");
-    if (ln_partials && reinterpret_cast<uintptr_t>(ln_partials) % 8)
-        return fail(WDL_EINVAL, "act_quant_w4: LayerNorm partials must be 8-byte aligned");
+    if (ln_partials && reinterpret_cast<uintptr_t>(ln_partials) % 16)
+        return fail(WDL_EINVAL, "act_quant_w4: LayerNorm partials must be 16-byte aligned");
     if (Mp == 0) return WDL_OK;
     const int S = groups_per_block(K), nb = int((K / 64 + S - 1) / S);
     // LayerNorm chunk partials: the caller's (written by the GEMM epilogue that produced x), or made here

@@ -1434,8 +1434,8 @@ extern "C" int wdl_w4a4_gemm(const void* qa, const void* ascales, const void* wc
         reinterpret_cast<uintptr_t>(lora) % 16 || (epilogue != EPI_F32 && ldo % 8))
         return fail(WDL_EINVAL, "w4a4_gemm: out, gate, lora and proj_up must be 16-byte aligned, bias 8-byte, and "
                                 "bf16 output rows a multiple of 8 elements");
-    if (ln_partials && (epilogue != EPI_RESIDUAL || reinterpret_cast<uintptr_t>(ln_partials) % 8))
-        return fail(WDL_EINVAL, "w4a4_gemm: LayerNorm partials come with the residual epilogue, 8-byte aligned");
+    if (ln_partials && (epilogue != EPI_RESIDUAL || reinterpret_cast<uintptr_t>(ln_partials) % 16))
+        return fail(WDL_EINVAL, "w4a4_gemm: LayerNorm partials come with the residual epilogue, 16-byte aligned");
     if (M == 0) return WDL_OK;
     GemmArgs a{static_cast<const uint8_t*>(qa), static_cast<const uint16_t*>(ascales),
                static_cast<const uint8_t*>(wcodes), static_cast<const uint32_t*>(wscales), lora,
