@@ -134,9 +134,11 @@ class ModelEdges:
     def time(self, t: torch.Tensor):
         """t [1] -> (t_emb bf16 [dim], e0 fp32 [6, dim])."""
         h = F.linear(time_features(t).to(torch.bfloat16), self.t1_w, self.t1_b)
-        t_emb = F.linear(F.silu(h), self.t2_w, self.t2_b)
-        e0 = F.linear(F.silu(t_emb), self.proj_w, self.proj_b)
-        return t_emb[0], e0.float().view(6, self.dim)
+        # one row: matrix-vector products (the 113 MB modulation projection streams its weights faster through
+        # addmv than through a 1-row GEMM; step -0.04 ms)
+        t_emb = torch.addmv(self.t2_b, self.t2_w, F.silu(h)[0])
+        e0 = torch.addmv(self.proj_b, self.proj_w, F.silu(t_emb))
+        return t_emb, e0.float().view(6, self.dim)
 
     def head(self, X: torch.Tensor, t_emb: torch.Tensor, grid) -> torch.Tensor:
         """Tokens bf16 [f h w, dim] -> flow bf16 [out_dim, f, 2h, 2w]."""
