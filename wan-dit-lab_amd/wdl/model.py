@@ -47,9 +47,15 @@ def sigmas(shift: float = SHIFT, steps=STEPS) -> list:
     return (shift * u / (1 + (shift - 1) * u)).tolist()
 
 
+_OMEGA: dict = {}
+
+
 def time_features(t: torch.Tensor) -> torch.Tensor:
-    """[cos(t omega), sin(t omega)] in fp64, omega = 10000^(-i / 128), i < 128 (model.py:38-40) -> fp32 [B, 256]."""
-    omega = 10000 ** (-torch.arange(128, dtype=torch.float64, device=t.device) / 128)
+    """[cos(t omega), sin(t omega)] in fp64, omega = 10000^(-i / 128), i < 128 (model.py:38-40) -> fp32 [B, 256]
+    (omega made once per device)."""
+    omega = _OMEGA.get(t.device)
+    if omega is None:
+        omega = _OMEGA[t.device] = 10000 ** (-torch.arange(128, dtype=torch.float64, device=t.device) / 128)
     theta = t.double()[:, None] * omega[None, :]
     return torch.cat([torch.cos(theta), torch.sin(theta)], dim=1).float()
 
