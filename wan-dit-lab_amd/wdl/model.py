@@ -146,11 +146,24 @@ class ModelEdges:
         e0 = torch.addmv(self.proj_b, self.proj_w, F.silu(t_emb))
         return t_emb, e0.float().view(6, self.dim)
 
-    def head(self, X: torch.Tensor, t_emb: torch.Tensor, grid) -> torch.Tensor:
-        """Tokens bf16 [f h w, dim] -> flow bf16 [out_dim, f, 2h, 2w]."""
+    def head(self, X: torch.Tensor, t_emb: torch.Tensor, grid, ln_partials=None) -> torch.Tensor:
+        """Tokens bf16 [f h w, dim] -> flow bf16 [out_dim, f, 2h, 2w]. ln_partials: the LayerNorm chunk partials of X
+        (as the last block's residual GEMM wrote them); with them the LayerNorm and modulation run as one launch of
+        the activation quantizer's LayerNorm path (its bf16 copy of the modulated rows), the statistics in the
+        partials' order; without them, through torch."""
         shift, scale = self.head_mod + t_emb.float()[None, :]
-        y = F.layer_norm(X.float(), (self.dim,), eps=self.eps) * (1 + scale) + shift
-        return unpatchify(F.linear(y.to(torch.bfloat16), self.head_w, self.head_b), grid, self.out_dim)
+        if ln_partials is not None:
+            from wdl import ops
+
+            if not hasattr(self, "_ones"):
+                self._ones = torch.ones(self.dim, device=X.device, dtype=torch.bfloat16)
+            y = torch.empty_like(X)
+            ops.act_quant_launch(X, self._ones, None, ln=dict(shift=shift.contiguous(), scale=scale.contiguous(),
+                                                             weight=None, bias=None, eps=self.eps,
+                                                             partials=ln_partials), v_out=y)
+        else:
+            y = (F.layer_norm(X.float(), (self.dim,), eps=self.eps) * (1 + scale) + shift).to(torch.bfloat16)
+        return unpatchify(F.linear(y, self.head_w, self.head_b), grid, self.out_dim)
 
 
 def random_edges(dim: int, in_dim: int, out_dim: int, generator: torch.Generator, std: float = 0.02) -> dict:
@@ -189,7 +202,7 @@ class DiTModel:
         for i, (blk, cache, ctx, e) in enumerate(zip(self.blocks, self.caches, self.ctx, e_all)):
             blk.forward(X, e, grid, self.freq, start_frame, cache, ctx, ln_in=ln_in, ln_out=lnb[i % 2])
             ln_in = lnb[i % 2]
-        return self.edges.head(X, t_emb, grid)
+        return self.edges.head(X, t_emb, grid, ln_partials=ln_in)
 
 
 class ChunkStream:
